@@ -1,0 +1,138 @@
+"""Batch-1 greedy decode benchmark of the Qwen3.6-27B-shaped hybrid model on
+one MI355X (64 layers = 48 gated-DeltaNet + 16
+attention, Q4_K_M-style mix, 4096-token context).
+
+A step is one decode pass (one token).  Weights are synthetic random-init
+(generated on the device); the 4096-token context is a seeded synthetic KV
+cache / recurrent state.  W warmup tokens, then K tokens
+timed as one multi-pass launch of the cooperative interpreter, bracketed by
+torch.cuda.synchronize().  Prints one JSON line.
+
+The roofline object prices the algorithmic bytes per token (weights read
+once, KV rows read once, recurrent state read+written, logits written)
+against 8 TB/s, using the interpreter kernel's own duration measured with HIP
+events recorded on its launch stream.  cpu_baseline times the CPU oracle
+(the repository's restatement of ggml's CPU semantics, OpenMP over rows) on
+a bounded sample of the same decode.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+METRIC = "batch-1 decode tok/s, 27B-shaped Q4_K @4k ctx; achieved HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+
+
+def bytes_per_token(cfg, m, n_attended):
+    """Algorithmic HBM bytes of one decode pass at n_attended KV positions."""
+    import sinter
+    n_attn = sum(1 for il in range(cfg.n_layer) if il % cfg.attn_every == cfg.attn_every - 1)
+    n_gdn = cfg.n_layer - n_attn
+    wb = m.info()["weight_bytes"]
+    _, emb_bytes, emb_type = m.tensor(cfg.n_layer, 0)
+    weights = wb - emb_bytes + sinter.row_bytes(emb_type, cfg.n_embd)      # one embedding row
+    D = cfg.gdn_d
+    C = (2 * cfg.gdn_hk + cfg.gdn_hv) * D
+    gdn_state = n_gdn * cfg.gdn_hv * D * D * 4 * 2                         # read + write
+    conv_state = n_gdn * C * (cfg.conv_k - 1) * 4 * 2
+    rw = cfg.attn_nkv * cfg.head_dim
+    kv_row = n_attn * 2 * rw * 2                                             # K and V, f16
+    logits = cfg.n_vocab * 4
+    return {"weights": weights, "gdn_state": gdn_state, "conv_state": conv_state,
+            "kv_read": kv_row * n_attended, "kv_append": kv_row, "logits": logits,
+            "total": weights + gdn_state + conv_state + kv_row * n_attended + kv_row + logits}
+
+
+def cpu_baseline(m, ctx, seconds):
+    """Time the CPU oracle decoding from the same synthetic context."""
+    import numpy as np
+    import oracle
+    t0 = time.perf_counter()
+    mirror = oracle.ModelMirror(m)
+    copy_s = time.perf_counter() - t0
+    n, t = 0, 0.0
+    tok = 1
+    while t < seconds or n == 0:
+        s = time.perf_counter()
+        tok, _ = mirror.step(tok, ctx + n)
+        t += time.perf_counter() - s
+        n += 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": n / t, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps of the same model from position {ctx} "
+                      f"(CPU oracle, OpenMP over rows, {threads} threads; weights copied to host in {copy_s:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--quant", default="q4_k_m", choices=["q4_k_m", "bf16"])
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=2026)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the decode path on one GPU "
+              "(the 27B model fits one MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import sinter
+
+    torch.cuda.set_device(0)
+    n_ctx = args.ctx + args.warmup + args.steps + 8
+    cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
+    t0 = time.perf_counter()
+    m = sinter.Model(cfg, seed=args.seed)
+    m.synth_context(args.ctx, seed=args.seed + 1)
+    setup_s = time.perf_counter() - t0
+    print(f"# model ready in {setup_s:.1f} s: {m.info()}", file=sys.stderr, flush=True)
+
+    tok = 1
+    if args.warmup:
+        toks = m.greedy(tok, args.ctx, args.warmup)
+        tok = toks[-1]
+    pos0 = args.ctx + args.warmup
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = m.greedy(tok, pos0, args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = sinter.lib().sinter_host_last_launch_ms(m.host())
+    print(f"# timed {args.steps} tokens: wall {wall * 1e3:.2f} ms, interpreter kernel {kernel_ms:.2f} ms; "
+          f"tokens[:8] {toks[:8]}", file=sys.stderr, flush=True)
+
+    mean_attended = pos0 + (args.steps + 1) / 2.0
+    bpt = bytes_per_token(cfg, m, mean_attended)
+    tok_s = args.steps / wall
+    achieved = bpt["total"] * args.steps / (kernel_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8" if args.quant == "q4_k_m" else "bf16",
+        "data": "synthetic (seeded random-init weights and 4096-token synthetic KV/recurrent state)",
+        "config": {"workload": f"e2e greedy decode, Qwen3.6-27B-shaped hybrid (48 GDN + 16 attention), "
+                               f"{args.quant} weights, {args.ctx}-token context",
+                   "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
+                   "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "sinter_interp", "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(m, args.ctx, args.cpu_seconds)
+    m.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

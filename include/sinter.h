@@ -1,0 +1,299 @@
+/*
+ * sinter-mi355x C ABI.
+ *
+ * The drop-in boundary for the batch-1 decode hot path of a Qwen3.6-27B-shaped
+ * hybrid (gated-DeltaNet + full-attention) model on one MI355X (gfx950).  Every
+ * entry point is extern "C" with plain pointers and sizes; device pointers are
+ * hipMalloc'd memory on the handle's device; no exception crosses the ABI.
+ * Functions return SINTER_OK (0) or a negative sinter_status; the message of
+ * the last failure on the calling thread is sinter_last_error().
+ *
+ * Layers (each cites the reference interface it replaces):
+ *   1. ISA: sinter_instr and the op payloads -- core/isa.cuh:32-88 and the
+ *      per-op Args structs of k0/ops/{gemv,gdn,attn,glue}.cuh.
+ *   2. Host control plane: sinter_host_* -- mk::host_* in core/host.h:62-80.
+ *   3. Op entry points: sinter_op_* -- one interpreter instruction run as a
+ *      standalone launch, the role of the mk_run test wrappers
+ *      (tests/test_gemv.cu:57-78, test_gdn.cu:52-83, test_attn.cu:68-98).
+ *   4. Model: sinter_model_* -- the harness residency/packer/driver
+ *      (k0/harness.cpp:315-566, 1019-1060, 1197-1275) with the schedule
+ *      compiler (k0/compile_schedule.py) re-derived for this layout.
+ */
+#ifndef SINTER_H
+#define SINTER_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SINTER_ABI_VERSION 1
+
+/* ------------------------------------------------------------------ status */
+enum sinter_status {
+    SINTER_OK = 0,
+    SINTER_ERR_ARG = -1,     /* bad argument / shape the kernels do not support */
+    SINTER_ERR_HIP = -2,     /* HIP runtime call failed */
+    SINTER_ERR_DEVICE = -3,  /* device error cell set (see sinter_host_error) */
+    SINTER_ERR_TIMEOUT = -4, /* watchdog fired */
+    SINTER_ERR_STATE = -5,   /* call out of lifecycle order */
+    SINTER_ERR_NOMEM = -6
+};
+/* core/host.h:31-35 RunStatus */
+enum sinter_run_status { SINTER_RUN_OK = 0, SINTER_RUN_ERR = 1, SINTER_RUN_TIMEOUT = 2 };
+/* core/interp.cuh:49-56 ErrCode (+ codes of the fused ops) */
+enum sinter_err_code {
+    SINTER_E_NONE = 0,
+    SINTER_E_BAD_KIND = 1,        /* kind >= SINTER_OP_KIND_COUNT */
+    SINTER_E_UNWIRED_KIND = 2,    /* valid kind without an implementation */
+    SINTER_E_BAD_SHAPE = 3,       /* an op found its payload inconsistent */
+    SINTER_E_ATTN_SENTINEL = 4,   /* a split-K partial was never written */
+    SINTER_E_TIMEOUT_BARRIER = 5  /* a grid-barrier wait exceeded the spin limit */
+};
+
+const char *sinter_last_error(void);
+int sinter_abi_version(void);
+
+/* ------------------------------------------------------------------ types */
+/* ggml_type numbering */
+enum sinter_type {
+    SINTER_F32 = 0, SINTER_F16 = 1, SINTER_Q8_0 = 8, SINTER_Q4_K = 12,
+    SINTER_Q6_K = 14, SINTER_Q8_K = 15, SINTER_BF16 = 30
+};
+size_t sinter_row_bytes(int type, int64_t k);
+
+/* ------------------------------------------------------------------ ISA */
+/* core/isa.cuh:32-81, re-sized: 256-byte instructions (payload 240 B) so the
+ * fused ops carry their operands inline; block ranges cover up to 65535
+ * workgroups.  Instructions between two BOUNDARY instructions run
+ * concurrently on disjoint [block_lo, block_hi) ranges. */
+enum sinter_op_kind {
+    SINTER_OP_NOP = 0,
+    SINTER_OP_BOUNDARY = 1,    /* grid barrier */
+    SINTER_OP_GEMV = 2,        /* prologue (norm/embed) + act. quant + GEMV + epilogue */
+    SINTER_OP_GDN_STEP = 3,    /* conv+silu, l2norm, gates, delta rule */
+    SINTER_OP_ATTN_DECODE = 4, /* qk norm+rope, KV append, split-K, merge, gate */
+    SINTER_OP_KIND_COUNT = 5
+};
+
+typedef struct sinter_instr {
+    uint16_t kind;
+    uint16_t block_lo;
+    uint16_t block_hi;
+    uint16_t flags;
+    uint32_t dbg_node;
+    uint32_t _pad;
+    unsigned char payload[240];
+} sinter_instr;
+
+/* SINTER_OP_GEMV prologue modes: how the activation vector a[K] is formed
+ * before it is quantised to the weights' vec_dot type (Q8_K for K-quants,
+ * Q8_0 for Q8_0, BF16 for BF16, F32 for F32). */
+enum sinter_gemv_pro {
+    SINTER_PRO_PLAIN = 0,   /* a = x */
+    SINTER_PRO_RMSNORM = 1, /* a = rmsnorm(x) * norm_w          (glue.cuh:56-152) */
+    SINTER_PRO_GATED = 2,   /* per head of 2^gn_log2d: rmsnorm(x_h)*norm_w*silu(z_h) (gdn.cuh:339-383) */
+    SINTER_PRO_EMBED = 3    /* x = dequant(embd[token]); block_lo writes x_out; a = rmsnorm(x)*norm_w (glue.cuh:202-227) */
+};
+/* SINTER_OP_GEMV epilogue modes, per segment */
+enum sinter_gemv_epi {
+    SINTER_EPI_STORE = 0,  /* y[r] = dot */
+    SINTER_EPI_RESID = 1,  /* y[r] = res[r] + dot (residual add fused) */
+    SINTER_EPI_SWIGLU = 2, /* y[r] = silu(w.a) * (w2.a)   (gemv.cuh:327-347) */
+    SINTER_EPI_ARGMAX = 3, /* y[r] = dot, plus greedy argmax over all rows (harness.cpp:1187-1195) */
+    SINTER_EPI_CONV = 4    /* causal conv + silu per row (channel):          (gdn.cuh:106-171)
+                              y[r] = silu(sum_j win_j * w2[r*dconv+j]), win = {aux[r*(dconv-1)..], dot};
+                              aux (conv state) <- win[1..] */
+};
+
+typedef struct sinter_gemv_seg {
+    const void *w;   /* weight rows (gate rows for SWIGLU) */
+    const void *w2;  /* SWIGLU: up rows; CONV: f32 conv weights [rows][dconv]; else NULL */
+    float *y;        /* output rows */
+    float *aux;      /* RESID: residual rows (read); CONV: conv state [rows][dconv-1] (updated) */
+    uint32_t rows;
+    uint8_t type;    /* sinter_type of w (and w2) */
+    uint8_t epi;     /* sinter_gemv_epi */
+    uint8_t dconv;   /* CONV: taps */
+    uint8_t _pad;
+} sinter_gemv_seg;
+
+#define SINTER_GEMV_MAX_SEG 4
+typedef struct sinter_gemv_args {
+    const float *x;        /* PLAIN/RMSNORM/GATED input, K floats */
+    const float *norm_w;   /* RMSNORM/EMBED: K floats; GATED: 2^gn_log2d floats */
+    const void *aux;       /* GATED: z (K floats); EMBED: embedding rows */
+    const int32_t *token;  /* EMBED: token id cell */
+    float *x_out;          /* EMBED: dequantised row (K floats), written by block_lo */
+    void *epi_ws;          /* ARGMAX: sinter_argmax_ws in device memory */
+    uint32_t K;
+    float eps;
+    uint8_t pro;           /* sinter_gemv_pro */
+    uint8_t n_seg;
+    uint8_t aux_type;      /* EMBED: sinter_type of the embedding rows */
+    uint8_t gn_log2d;      /* GATED: log2 of the head width */
+    uint32_t aux_rows;     /* EMBED: rows of the embedding (tokens >= aux_rows raise BAD_SHAPE) */
+    sinter_gemv_seg seg[SINTER_GEMV_MAX_SEG];
+} sinter_gemv_args;
+
+/* Greedy argmax workspace (device memory).  count must be 0 before the first
+ * use; the last-arriving block resets it. */
+typedef struct sinter_argmax_ws {
+    float *part_val;      /* [nblocks] */
+    int32_t *part_idx;    /* [nblocks] */
+    uint32_t *count;      /* arrival counter */
+    int32_t *pass_cell;   /* sinter_pass_cell: token <- argmax, pos += 1, history */
+    int32_t *history;     /* tokens produced, indexed by pass_cell->steps */
+    uint32_t history_cap;
+    uint32_t capacity;    /* partial slots (blocks the workspace was created for) */
+} sinter_argmax_ws;
+
+/* Per-pass inputs the kernel reads (harness.cpp:549-566 set_pass_inputs):
+ * token and position; the argmax epilogue advances them on device so several
+ * greedy passes can run in one launch. */
+typedef struct sinter_pass_cell {
+    int32_t token;
+    int32_t pos;
+    int32_t steps;
+    int32_t _pad;
+} sinter_pass_cell;
+
+/* The causal conv + silu runs in the qkv GEMV epilogue (SINTER_EPI_CONV);
+ * this op takes its output. */
+typedef struct sinter_gdn_args {
+    const float *qkv;       /* [C] conv outputs: q[HK*D] | k[HK*D] | v[HV*D] */
+    const float *alpha;     /* [HV] raw ssm_alpha projection */
+    const float *beta;      /* [HV] raw ssm_beta projection (pre-sigmoid) */
+    const float *dt_bias;   /* [HV] */
+    const float *ssm_a;     /* [HV] (= -exp(A_log)) */
+    float *state;           /* [HV][D][D] transposed: M[h][col][i] = S[i][col], updated */
+    float *o;               /* [HV*D] output, before the gated norm */
+    uint32_t hk, hv, d;
+    uint32_t cols;          /* columns per work item (divides D; 256 % (D/..) see op) */
+    float eps;              /* l2-norm eps */
+    float scale;            /* output scale 1/sqrt(D) */
+} sinter_gdn_args;
+
+typedef struct sinter_attn_args {
+    const float *qg;        /* [NQ][2*HD]: q | gate per head */
+    const float *k;         /* [NKV*HD] raw k projection */
+    const float *v;         /* [NKV*HD] raw v projection */
+    const float *q_norm;    /* [HD] */
+    const float *k_norm;    /* [HD] */
+    uint16_t *kc;           /* K cache f16 [n_ctx][NKV*HD] */
+    uint16_t *vc;           /* V cache f16 [n_ctx][NKV*HD] */
+    double *part;           /* partials [NKV][n_chunks][NQ/NKV][HD+2] fp64 */
+    uint32_t *count;        /* [NKV] arrival counters, 0 before first use (self-resetting) */
+    float *out;             /* [NQ*HD] gated attention output */
+    const int32_t *pass_cell; /* sinter_pass_cell (pos) */
+    uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;
+    float theta_scale, eps, scale;
+    uint32_t _pad;
+} sinter_attn_args;
+
+/* ------------------------------------------------------------------ host control plane */
+/* core/host.h:62-80.  Lifecycle: init -> upload -> launch -> run_pass* ->
+ * shutdown -> destroy.  On MI355X a pass is one cooperative launch of the
+ * interpreter (optionally several greedy passes per launch); launch()
+ * validates the program and the cooperative envelope. */
+typedef struct sinter_host sinter_host;
+
+int  sinter_host_init(sinter_host **out, int device, unsigned pass_cycles_cap);
+int  sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_instr,
+                        uint32_t epoch_stride);
+int  sinter_host_launch(sinter_host *h);
+/* returns sinter_run_status */
+int  sinter_host_run_pass(sinter_host *h, int32_t token, double timeout_ms);
+/* n greedy passes in one launch: tokens_out[i] is the argmax of pass i */
+int  sinter_host_run_passes(sinter_host *h, int32_t token, uint32_t n_passes,
+                            int32_t *tokens_out, double timeout_ms);
+int  sinter_host_shutdown(sinter_host *h, double timeout_ms);
+void sinter_host_destroy(sinter_host *h);
+int  sinter_host_read_pass_cycles(sinter_host *h, long long *out, unsigned count);
+int  sinter_host_reset_op_cycles(sinter_host *h);
+int  sinter_host_read_op_cycles(sinter_host *h, long long *out, unsigned count);
+/* device pointers the program payloads reference */
+sinter_pass_cell *sinter_host_pass_cell(sinter_host *h);
+int32_t *sinter_host_history(sinter_host *h, uint32_t *cap);
+int  sinter_host_error(sinter_host *h, uint32_t *code, uint32_t *aux);
+int  sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32_t *lds_bytes);
+int  sinter_host_set_pos(sinter_host *h, int32_t pos);
+/* cooperative grid size (default: one workgroup per CU); before launch() */
+int  sinter_host_set_grid(sinter_host *h, uint32_t blocks);
+/* device time of the last interpreter launch: HIP events recorded on the
+ * launch stream immediately before and after the kernel */
+float sinter_host_last_launch_ms(sinter_host *h);
+
+/* ------------------------------------------------------------------ op entry points */
+/* Each runs one instruction of the given kind over `blocks` workgroups on
+ * `stream` (0 = the legacy stream is never used; pass a real hipStream_t).
+ * All pointers are device pointers. */
+int sinter_op_gemv(const sinter_gemv_args *a, uint32_t blocks, void *stream);
+int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream);
+int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream);
+/* synchronise the device and read/clear the op error cell of the current device */
+int sinter_op_error(uint32_t *code, uint32_t *aux);
+/* argmax workspace for `blocks` workgroups (allocated on the current device) */
+int sinter_argmax_ws_create(uint32_t blocks, int32_t *pass_cell, int32_t *history,
+                            uint32_t history_cap, sinter_argmax_ws **out_dev);
+void sinter_argmax_ws_destroy(sinter_argmax_ws *dev);
+
+/* ------------------------------------------------------------------ synthetic data */
+/* Deterministic synthetic tensors (integer hashing plus exactly rounded fp32
+ * arithmetic, so host and device produce identical bytes).  kind selects the
+ * distribution; see sinter_synth_kind. */
+enum sinter_synth_kind {
+    SINTER_SYN_WEIGHT = 0,  /* quantised weight rows of `type`, ~N(0, 0.02) scale */
+    SINTER_SYN_Q8_0_CFG1 = 1,/* Q8_0: codes U[-127,127], d = f16(|N(0, 0.02)|) */
+    SINTER_SYN_NORMAL = 2,  /* f32 ~ mean + std * N(0,1) (Irwin-Hall(4) approximation) */
+    SINTER_SYN_UNIFORM = 3, /* f32 ~ U[lo, hi) */
+    SINTER_SYN_NORMAL_F16 = 4 /* f16 ~ std * N(0,1) */
+};
+/* Fill n elements (rows*k for weights) at dst.  dev != 0: dst is device
+ * memory and the fill runs on `stream`; dev == 0: host memory. */
+int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k,
+                 uint64_t seed, float a, float b, void *stream);
+uint64_t sinter_seed(uint64_t config_id, const char *tensor_name, int64_t layer);
+
+/* ------------------------------------------------------------------ model */
+typedef struct sinter_model_config {
+    int32_t n_layer, attn_every, n_embd, n_ff, n_vocab;
+    int32_t gdn_hk, gdn_hv, gdn_d, conv_k;
+    int32_t attn_nq, attn_nkv, head_dim, rope_dims;
+    float rope_base, eps;
+    int32_t n_ctx;
+    int32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
+} sinter_model_config;
+
+typedef struct sinter_model sinter_model;
+
+/* Allocates weights (synthesised on device from seed), state and buffers,
+ * compiles and uploads the pass program. */
+int  sinter_model_create(const sinter_model_config *cfg, int device, uint64_t seed,
+                         uint32_t blocks, sinter_model **out);
+void sinter_model_destroy(sinter_model *m);
+/* one pass: writes logits (host, n_vocab floats, nullable) and the greedy id */
+int  sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logits_host,
+                         int32_t *next_token);
+/* n greedy passes from (token, pos) in one launch */
+int  sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
+                         int32_t *tokens_out);
+/* fill KV caches / recurrent states with seeded synthetic values, as if a
+ * context of n_past tokens had been prefilled */
+int  sinter_model_synth_context(sinter_model *m, int32_t n_past, uint64_t seed);
+/* host access to the tensors the oracle needs (slot numbering as
+ * oracle/oracle.h: layer*16 + slot; globals at n_layer*16 + {0,1,2}) */
+int  sinter_model_tensor_info(sinter_model *m, int64_t layer, int slot, void **dev_ptr,
+                              size_t *bytes, int *type);
+int  sinter_model_state_info(sinter_model *m, int64_t layer, int slot, void **dev_ptr,
+                             size_t *bytes);
+int  sinter_model_copy(sinter_model *m, void *dst, const void *src, size_t bytes, int dir);
+int  sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr,
+                       uint32_t *n_boundaries, uint32_t *blocks);
+sinter_host *sinter_model_host(sinter_model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

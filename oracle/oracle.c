@@ -1,0 +1,725 @@
+/*
+ * CPU ORACLE -- test infrastructure only (see oracle.h).  Nothing in the
+ * product links or loads this file.
+ *
+ * Reference anchors (paths relative to the reference checkout):
+ *   - op list and decode order: docs/BLOCKS.md, k0/compile_schedule.py:358-703
+ *   - GDN math: k0/ops/gdn.cuh:66-383, docs/SEMANTICS.md:280-304
+ *   - attention math: k0/ops/attn.cuh:109-488, tests/test_attn.cu:388-424
+ *   - RMSNorm / glue: k0/ops/glue.cuh:25-152
+ *   - argmax: k0/harness.cpp:1187-1195
+ * The quantised block formats (Q8_0, Q4_K, Q6_K, Q8_K) and the activation
+ * quantisers are ggml's public GGUF formats; ggml itself is not in the
+ * reference (it is the un-vendored llama.cpp fork autoround @546eca8dc,
+ * ggml 0.12.0), so these are restated from the published layouts.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------ conversions */
+
+float or_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f, man = h & 0x3ff, bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal: value = man * 2^-24 */
+            float v = (float)man * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even (what F16C/`__float2half`
+ * compute). */
+uint16_t or_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) /* inf / nan */
+        return sign | 0x7c00 | (ax > 0x7f800000u ? 0x200 : 0);
+    if (ax >= 0x477ff000u) /* rounds to >= 65520 -> inf */
+        return sign | 0x7c00;
+    if (ax < 0x38800000u) { /* result is subnormal or zero: value/2^-24 */
+        float a;
+        memcpy(&a, &ax, 4);
+        /* a * 2^24 is exact in fp32 range; nearbyintf rounds half-even */
+        const float m = nearbyintf(a * 16777216.0f);
+        return sign | (uint16_t)m;
+    }
+    /* normal: keep 10 mantissa bits, round half to even on the dropped 13 */
+    uint32_t mant = ax + 0xfffu + ((ax >> 13) & 1u);
+    return sign | (uint16_t)((mant - 0x38000000u) >> 13);
+}
+
+float or_bf16_to_f32(uint16_t h) {
+    uint32_t b = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+/* ggml GGML_FP32_TO_BF16: nan -> quiet nan, otherwise round half to even */
+uint16_t or_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((u >> 16) | 64);
+    return (uint16_t)((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+}
+
+/* ggml nearest_int: the 1.5*2^23 magic-number round (half to even) */
+int or_nearest_int(float fval) {
+    float val = fval + 12582912.f;
+    int i;
+    memcpy(&i, &val, sizeof(int));
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* ------------------------------------------------------------ formats */
+
+typedef struct { uint16_t d; int8_t qs[32]; } blk_q8_0;                          /* 34 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } blk_q4_K; /* 144 B */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } blk_q6_K; /* 210 B */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } blk_q8_K;          /* 292 B */
+
+size_t or_type_block_elems(int t) {
+    switch (t) {
+    case OR_Q8_0: return 32;
+    case OR_Q4_K: case OR_Q6_K: case OR_Q8_K: return 256;
+    default: return 1;
+    }
+}
+
+size_t or_type_block_bytes(int t) {
+    switch (t) {
+    case OR_F32: return 4;
+    case OR_F16: case OR_BF16: return 2;
+    case OR_Q8_0: return 34;
+    case OR_Q4_K: return 144;
+    case OR_Q6_K: return 210;
+    case OR_Q8_K: return 292;
+    default: return 0;
+    }
+}
+
+size_t or_row_bytes(int t, int64_t k) {
+    return (size_t)(k / (int64_t)or_type_block_elems(t)) * or_type_block_bytes(t);
+}
+
+/* Q4_K packed 6-bit scale/min pair j of 8 (ggml get_scale_min_k4) */
+static void q4k_scale_min(int j, const uint8_t *q, int *sc, int *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Q4_K element e (0..255) code, 0..15: sub-block pair p = e/64 shares bytes
+ * qs[32p .. 32p+32), low nibble for e%64 < 32, high nibble otherwise. */
+static inline int q4k_code(const blk_q4_K *b, int e) {
+    const int p = e >> 6, l = e & 31;
+    const uint8_t byte = b->qs[32 * p + l];
+    return (e & 32) ? (byte >> 4) : (byte & 0xF);
+}
+
+/* Q6_K element e code, -32..31: half n = e/128 uses ql[64n..], qh[32n..];
+ * within a half, quarter t = (e%128)/32 selects {ql low, ql+32 low, ql high,
+ * ql+32 high} and qh bit pair 2t. */
+static inline int q6k_code(const blk_q6_K *b, int e) {
+    const int n = e >> 7, r = e & 127, t = r >> 5, l = r & 31;
+    const uint8_t *ql = b->ql + 64 * n, *qh = b->qh + 32 * n;
+    const uint8_t lo = (t & 1) ? ql[l + 32] : ql[l];
+    const int nib = (t & 2) ? (lo >> 4) : (lo & 0xF);
+    const int hi = (qh[l] >> (2 * t)) & 3;
+    return (nib | (hi << 4)) - 32;
+}
+
+void or_dequant_row(int t, const void *row, float *out, int64_t k) {
+    if (t == OR_F32) { memcpy(out, row, (size_t)k * 4); return; }
+    if (t == OR_F16) { for (int64_t i = 0; i < k; i++) out[i] = or_f16_to_f32(((const uint16_t *)row)[i]); return; }
+    if (t == OR_BF16) { for (int64_t i = 0; i < k; i++) out[i] = or_bf16_to_f32(((const uint16_t *)row)[i]); return; }
+    const int64_t nb = k / (int64_t)or_type_block_elems(t);
+    for (int64_t ib = 0; ib < nb; ib++) {
+        if (t == OR_Q8_0) {
+            const blk_q8_0 *b = (const blk_q8_0 *)row + ib;
+            const float d = or_f16_to_f32(b->d);
+            for (int l = 0; l < 32; l++) out[ib * 32 + l] = d * (float)b->qs[l];
+        } else if (t == OR_Q4_K) {
+            /* ggml dequantize_row_q4_K: y = (d*sc)*q - (dmin*m), fp32 */
+            const blk_q4_K *b = (const blk_q4_K *)row + ib;
+            const float d = or_f16_to_f32(b->d), dmin = or_f16_to_f32(b->dmin);
+            for (int s = 0; s < 8; s++) {
+                int sc, m;
+                q4k_scale_min(s, b->scales, &sc, &m);
+                const float d1 = d * (float)sc, m1 = dmin * (float)m;
+                for (int l = 0; l < 32; l++)
+                    out[ib * 256 + 32 * s + l] = d1 * (float)q4k_code(b, 32 * s + l) - m1;
+            }
+        } else if (t == OR_Q6_K) {
+            /* ggml dequantize_row_q6_K: y = d * sc * q, fp32 left to right */
+            const blk_q6_K *b = (const blk_q6_K *)row + ib;
+            const float d = or_f16_to_f32(b->d);
+            for (int e = 0; e < 256; e++)
+                out[ib * 256 + e] = d * (float)b->scales[e / 16] * (float)q6k_code(b, e);
+        } else if (t == OR_Q8_K) {
+            const blk_q8_K *b = (const blk_q8_K *)row + ib;
+            for (int e = 0; e < 256; e++) out[ib * 256 + e] = b->d * (float)b->qs[e];
+        }
+    }
+}
+
+/* ------------------------------------------------------------ activation quant */
+
+/* ggml-cpu x86 quantize_row_q8_0 (AVX2 branch): d = amax/127 stored as f16;
+ * id = 127/amax (0 if amax == 0); q = round-half-even(x*id). */
+void or_quant_q8_0(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    for (int64_t ib = 0; ib < k / 32; ib++) {
+        const float *xb = x + ib * 32;
+        float amax = 0.0f;
+        for (int l = 0; l < 32; l++) amax = fmaxf(amax, fabsf(xb[l]));
+        const float d = amax / 127.f;
+        y[ib].d = or_f32_to_f16(d);
+        const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+        for (int l = 0; l < 32; l++) y[ib].qs[l] = (int8_t)or_nearest_int(xb[l] * id);
+    }
+}
+
+/* ggml quantize_row_q8_K_ref: max = signed element of largest |x| (first
+ * wins); iscale = -127/max; q = min(127, nearest_int(iscale*x)); bsums over
+ * 16; d = 1/iscale. */
+void or_quant_q8_K(const float *x, void *vy, int64_t k) {
+    blk_q8_K *y = (blk_q8_K *)vy;
+    for (int64_t ib = 0; ib < k / 256; ib++) {
+        const float *xb = x + ib * 256;
+        float max = 0, amax = 0;
+        for (int j = 0; j < 256; j++) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) { amax = ax; max = xb[j]; }
+        }
+        if (amax == 0.0f) {
+            y[ib].d = 0;
+            memset(y[ib].qs, 0, 256);
+            memset(y[ib].bsums, 0, sizeof(y[ib].bsums));
+            continue;
+        }
+        const float iscale = -127.f / max;
+        for (int j = 0; j < 256; j++) {
+            const int v = or_nearest_int(iscale * xb[j]);
+            y[ib].qs[j] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; j++) {
+            int s = 0;
+            for (int i = 0; i < 16; i++) s += y[ib].qs[16 * j + i];
+            y[ib].bsums[j] = (int16_t)s;
+        }
+        y[ib].d = 1 / iscale;
+    }
+}
+
+void or_quant_bf16(const float *x, uint16_t *y, int64_t k) {
+    for (int64_t i = 0; i < k; i++) y[i] = or_f32_to_bf16(x[i]);
+}
+
+/* ------------------------------------------------------------ block terms */
+
+double or_block_term(int t, const void *wb, const void *xb) {
+    if (t == OR_Q8_0) {
+        const blk_q8_0 *w = (const blk_q8_0 *)wb, *x = (const blk_q8_0 *)xb;
+        int32_t isum = 0;
+        for (int l = 0; l < 32; l++) isum += (int32_t)w->qs[l] * (int32_t)x->qs[l];
+        return ((double)or_f16_to_f32(w->d) * (double)or_f16_to_f32(x->d)) * (double)isum;
+    }
+    if (t == OR_Q4_K) {
+        const blk_q4_K *w = (const blk_q4_K *)wb;
+        const blk_q8_K *x = (const blk_q8_K *)xb;
+        int64_t isum = 0, imin = 0;
+        for (int s = 0; s < 8; s++) {
+            int sc, m;
+            q4k_scale_min(s, w->scales, &sc, &m);
+            int32_t dot = 0;
+            for (int l = 0; l < 32; l++) dot += q4k_code(w, 32 * s + l) * (int32_t)x->qs[32 * s + l];
+            isum += (int64_t)sc * dot;
+            imin += (int64_t)m * ((int32_t)x->bsums[2 * s] + (int32_t)x->bsums[2 * s + 1]);
+        }
+        const double dx = (double)x->d;
+        return ((double)or_f16_to_f32(w->d) * dx) * (double)isum -
+               ((double)or_f16_to_f32(w->dmin) * dx) * (double)imin;
+    }
+    if (t == OR_Q6_K) {
+        const blk_q6_K *w = (const blk_q6_K *)wb;
+        const blk_q8_K *x = (const blk_q8_K *)xb;
+        int64_t isum = 0;
+        for (int j = 0; j < 16; j++) {
+            int32_t dot = 0;
+            for (int l = 0; l < 16; l++) dot += q6k_code(w, 16 * j + l) * (int32_t)x->qs[16 * j + l];
+            isum += (int64_t)w->scales[j] * dot;
+        }
+        return ((double)or_f16_to_f32(w->d) * (double)x->d) * (double)isum;
+    }
+    return 0.0;
+}
+
+static int vec_dot_type(int t) {
+    switch (t) {
+    case OR_Q8_0: return OR_Q8_0;
+    case OR_Q4_K: case OR_Q6_K: return OR_Q8_K;
+    case OR_BF16: return OR_BF16;
+    default: return OR_F32;
+    }
+}
+
+/* fast per-row kernels (same arithmetic as or_block_term, unrolled so the
+ * full-model oracle runs in reasonable time) */
+static double row_q4k(const blk_q4_K *w, const blk_q8_K *x, int64_t nb) {
+    double acc = 0.0;
+    int8_t codes[256];
+    for (int64_t ib = 0; ib < nb; ib++) {
+        const blk_q4_K *b = w + ib;
+        for (int p = 0; p < 4; p++)
+            for (int l = 0; l < 32; l++) {
+                codes[64 * p + l] = (int8_t)(b->qs[32 * p + l] & 0xF);
+                codes[64 * p + 32 + l] = (int8_t)(b->qs[32 * p + l] >> 4);
+            }
+        int64_t isum = 0, imin = 0;
+        for (int s = 0; s < 8; s++) {
+            int sc, m;
+            q4k_scale_min(s, b->scales, &sc, &m);
+            int32_t dot = 0;
+            const int8_t *cq = codes + 32 * s, *xq = x[ib].qs + 32 * s;
+            for (int l = 0; l < 32; l++) dot += (int32_t)cq[l] * (int32_t)xq[l];
+            isum += (int64_t)sc * dot;
+            imin += (int64_t)m * ((int32_t)x[ib].bsums[2 * s] + (int32_t)x[ib].bsums[2 * s + 1]);
+        }
+        const double dx = (double)x[ib].d;
+        acc += ((double)or_f16_to_f32(b->d) * dx) * (double)isum -
+               ((double)or_f16_to_f32(b->dmin) * dx) * (double)imin;
+    }
+    return acc;
+}
+
+static double row_q6k(const blk_q6_K *w, const blk_q8_K *x, int64_t nb) {
+    double acc = 0.0;
+    int8_t codes[256];
+    for (int64_t ib = 0; ib < nb; ib++) {
+        const blk_q6_K *b = w + ib;
+        for (int n = 0; n < 2; n++) {
+            const uint8_t *ql = b->ql + 64 * n, *qh = b->qh + 32 * n;
+            int8_t *c = codes + 128 * n;
+            for (int l = 0; l < 32; l++) {
+                c[l] = (int8_t)(((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+                c[l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                c[l + 64] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                c[l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+            }
+        }
+        int64_t isum = 0;
+        for (int j = 0; j < 16; j++) {
+            int32_t dot = 0;
+            const int8_t *cq = codes + 16 * j, *xq = x[ib].qs + 16 * j;
+            for (int l = 0; l < 16; l++) dot += (int32_t)cq[l] * (int32_t)xq[l];
+            isum += (int64_t)b->scales[j] * dot;
+        }
+        acc += ((double)or_f16_to_f32(b->d) * (double)x[ib].d) * (double)isum;
+    }
+    return acc;
+}
+
+static double row_q8_0(const blk_q8_0 *w, const blk_q8_0 *x, int64_t nb) {
+    /* declared fold: groups of 8 blocks (256 elements) summed ascending
+     * inside the group, then the group terms ascending */
+    double acc = 0.0;
+    for (int64_t g = 0; g < nb / 8; g++) {
+        double part = 0.0;
+        for (int64_t ib = 8 * g; ib < 8 * g + 8; ib++) {
+            int32_t isum = 0;
+            for (int l = 0; l < 32; l++) isum += (int32_t)w[ib].qs[l] * (int32_t)x[ib].qs[l];
+            part += ((double)or_f16_to_f32(w[ib].d) * (double)or_f16_to_f32(x[ib].d)) * (double)isum;
+        }
+        acc += part;
+    }
+    return acc;
+}
+
+static double row_bf16(const uint16_t *w, const uint16_t *x, int64_t k) {
+    /* declared fold: 256-element groups, exact products, fp64 */
+    double acc = 0.0;
+    for (int64_t g = 0; g < k / 256; g++) {
+        double part = 0.0;
+        for (int64_t i = 256 * g; i < 256 * g + 256; i++)
+            part += (double)or_bf16_to_f32(w[i]) * (double)or_bf16_to_f32(x[i]);
+        acc += part;
+    }
+    return acc;
+}
+
+void or_gemv_q(int t, const void *w, int64_t rows, int64_t k, const void *xq, float *y) {
+    const size_t rb = or_row_bytes(t, k);
+    const int64_t nb = k / (int64_t)or_type_block_elems(t);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const void *row = (const char *)w + (size_t)r * rb;
+        double acc = 0.0;
+        switch (t) {
+        case OR_Q4_K: acc = row_q4k((const blk_q4_K *)row, (const blk_q8_K *)xq, nb); break;
+        case OR_Q6_K: acc = row_q6k((const blk_q6_K *)row, (const blk_q8_K *)xq, nb); break;
+        case OR_Q8_0: acc = row_q8_0((const blk_q8_0 *)row, (const blk_q8_0 *)xq, nb); break;
+        case OR_BF16: acc = row_bf16((const uint16_t *)row, (const uint16_t *)xq, k); break;
+        case OR_F32: {
+            const float *wf = (const float *)row, *xf = (const float *)xq;
+            for (int64_t g = 0; g < k / 256; g++) {
+                double part = 0.0;
+                for (int64_t i = 256 * g; i < 256 * g + 256; i++) part += (double)wf[i] * (double)xf[i];
+                acc += part;
+            }
+        } break;
+        default: break;
+        }
+        y[r] = (float)acc;
+    }
+}
+
+void or_gemv(int t, const void *w, int64_t rows, int64_t k, const float *x, float *y) {
+    const int vt = vec_dot_type(t);
+    void *xq = malloc(or_row_bytes(vt, k) + 64);
+    switch (vt) {
+    case OR_Q8_0: or_quant_q8_0(x, xq, k); break;
+    case OR_Q8_K: or_quant_q8_K(x, xq, k); break;
+    case OR_BF16: or_quant_bf16(x, (uint16_t *)xq, k); break;
+    default: memcpy(xq, x, (size_t)k * 4); break;
+    }
+    or_gemv_q(t, w, rows, k, xq, y);
+    free(xq);
+}
+
+/* ------------------------------------------------------------ norms, unary */
+
+/* ggml CPU rms_norm: sum of fp32 squares in double; mean -> float;
+ * scale = 1/sqrtf(mean+eps); y = x*scale; then the separate MUL by w
+ * (reference k0/ops/glue.cuh:56-152 is the same operator). */
+void or_rmsnorm(const float *x, const float *w, float *y, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = 0; i < n; i++) {
+        const float t = x[i] * scale;
+        y[i] = w ? t * w[i] : t;
+    }
+}
+
+/* ggml CPU l2_norm: scale = 1/fmaxf(sqrtf(sum), eps) over fp32 squares summed
+ * in double (the CUDA form rsqrtf(fmaxf(sum, eps^2)) in k0/ops/gdn.cuh:187-212
+ * is the same operator up to rounding). */
+void or_l2norm(const float *x, float *y, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) sum += (double)(x[i] * x[i]);
+    const float scale = 1.0f / fmaxf(sqrtf((float)sum), eps);
+    for (int64_t i = 0; i < n; i++) y[i] = x[i] * scale;
+}
+
+float or_silu(float x) { return x / (1.0f + (float)exp(-(double)x)); }
+float or_sigmoid(float x) { return 1.0f / (1.0f + (float)exp(-(double)x)); }
+float or_softplus(float x) {
+    if (x > 20.0f) return x;
+    const float e = (float)exp((double)x);
+    return (float)log((double)(1.0f + e));
+}
+
+/* ------------------------------------------------------------ gated DeltaNet */
+
+/* k0/ops/gdn.cuh:106-171: window {h0,h1,h2,x}, tap-contiguous weights
+ * w[c*dconv + j]; history <- {h1,h2,x}; y = silu(sum_j win_j*w_j) with the
+ * sum in fp64 rounded once. */
+void or_conv_silu(const float *xnew, float *st, const float *cw, float *out,
+                  int64_t channels, int dconv) {
+    const int nh = dconv - 1;
+    for (int64_t c = 0; c < channels; c++) {
+        float win[8];
+        for (int j = 0; j < nh; j++) win[j] = st[c * nh + j];
+        win[nh] = xnew[c];
+        double acc = 0.0;
+        for (int j = 0; j < dconv; j++) acc += (double)win[j] * (double)cw[c * dconv + j];
+        out[c] = or_silu((float)acc);
+        for (int j = 0; j < nh; j++) st[c * nh + j] = win[j + 1];
+    }
+}
+
+/* k0/ops/gdn.cuh:215-245: g = exp(softplus(alpha + dt_bias) * a);
+ * beta = sigmoid(beta_raw). */
+void or_gdn_gates(const float *alpha, const float *beta_raw, const float *dt_bias,
+                  const float *ssm_a, float *g, float *beta, int nh) {
+    for (int h = 0; h < nh; h++) {
+        const float sp = or_softplus(alpha[h] + dt_bias[h]);
+        g[h] = (float)exp((double)(sp * ssm_a[h]));
+        beta[h] = or_sigmoid(beta_raw[h]);
+    }
+}
+
+/* k0/ops/gdn.cuh:248-337 (delta rule, modulo head map hk = h % HK):
+ *   kv    = sum_i S[i][col] k[i]                       (fp64, rounded once)
+ *   delta = (v[col] - g*kv) * beta                     (fp32 ops)
+ *   S'    = g*S + k*delta                              (fp32: mul, mul, add)
+ *   o     = (sum_i S'[i][col] q[i]) * scale            (fp64 sum, then fp32 mul) */
+void or_gdn_step(const float *q, const float *k, const float *v, const float *g,
+                 const float *beta, float *state, float *o, int hv, int hk, int d,
+                 float scale) {
+    for (int h = 0; h < hv; h++) {
+        const int kh = h % hk;
+        const float *qh = q + (size_t)kh * d, *kk = k + (size_t)kh * d;
+        const float gv = g[h], bv = beta[h];
+        for (int col = 0; col < d; col++) {
+            float *s = state + ((size_t)h * d + col) * d;
+            double kv = 0.0;
+            for (int i = 0; i < d; i++) kv += (double)s[i] * (double)kk[i];
+            const float kvf = (float)kv;
+            const float delta = (v[(size_t)h * d + col] - gv * kvf) * bv;
+            double acc = 0.0;
+            for (int i = 0; i < d; i++) {
+                const float a = gv * s[i];
+                const float b = kk[i] * delta;
+                s[i] = a + b;
+                acc += (double)s[i] * (double)qh[i];
+            }
+            o[(size_t)h * d + col] = (float)acc * scale;
+        }
+    }
+}
+
+/* k0/ops/gdn.cuh:339-383: per head rms_norm(x)*w, then * silu(z). */
+void or_gated_rmsnorm(const float *x, const float *z, const float *w, float *y,
+                      int nh, int d, float eps) {
+    for (int h = 0; h < nh; h++) {
+        or_rmsnorm(x + (size_t)h * d, w, y + (size_t)h * d, d, eps);
+        for (int i = 0; i < d; i++) y[(size_t)h * d + i] *= or_silu(z[(size_t)h * d + i]);
+    }
+}
+
+/* ------------------------------------------------------------ attention */
+
+/* theta_scale = powf(base, -2/n_dims), correctly rounded (k0/ops/attn.cuh:63
+ * pins 1e7 -> 0x1.356656p-1). */
+float or_rope_theta_scale(float base, int n_dims) {
+    return (float)pow((double)base, -2.0 / (double)n_dims);
+}
+
+/* ggml rope cache: theta_0 = pos, theta_{i+1} = theta_i * theta_scale (fp32);
+ * NEOX pairs (i, i + n_dims/2) for i < n_dims/2; dims >= n_dims pass through.
+ * IMROPE with sections [11,11,10,0] and four equal position ids is this same
+ * operator (k0/ops/attn.cuh:135-175, docs/SEMANTICS.md:500-523). */
+void or_rope_neox(float *x, int hd, int n_dims, int pos, float theta_scale) {
+    (void)hd;
+    float theta = (float)pos;
+    const int half = n_dims / 2;
+    for (int i = 0; i < half; i++) {
+        const float c = (float)cos((double)theta), s = (float)sin((double)theta);
+        const float x0 = x[i], x1 = x[i + half];
+        x[i] = x0 * c - x1 * s;
+        x[i + half] = x0 * s + x1 * c;
+        theta *= theta_scale;
+    }
+}
+
+/* Exact-arithmetic decode attention (tests/test_attn.cu:388-424 computes the
+ * same thing in double): scores s_j = scale * q.k_j with exact fp64 products,
+ * softmax and the V sum in fp64, rounded to fp32 once.  GQA: q head h reads
+ * kv head h / (nq/nkv).  Caches are rows of row_width f16 (all kv heads of a
+ * position contiguous). */
+void or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc, int n_kv,
+                    int nq, int nkv, int hd, int row_width, float scale, float *out) {
+    const int gqa = nq / nkv;
+    double *s = (double *)malloc(sizeof(double) * (size_t)(n_kv > 0 ? n_kv : 1));
+    double *acc = (double *)malloc(sizeof(double) * (size_t)hd);
+    for (int h = 0; h < nq; h++) {
+        const int g = h / gqa;
+        const float *qh = q + (size_t)h * hd;
+        double m = -INFINITY;
+        for (int j = 0; j < n_kv; j++) {
+            const uint16_t *kr = kc + (size_t)j * row_width + (size_t)g * hd;
+            double dot = 0.0;
+            for (int d = 0; d < hd; d++) dot += (double)qh[d] * (double)or_f16_to_f32(kr[d]);
+            s[j] = dot * (double)scale;
+            if (s[j] > m) m = s[j];
+        }
+        double sum = 0.0;
+        for (int d = 0; d < hd; d++) acc[d] = 0.0;
+        for (int j = 0; j < n_kv; j++) {
+            const double p = exp(s[j] - m);
+            sum += p;
+            const uint16_t *vr = vc + (size_t)j * row_width + (size_t)g * hd;
+            for (int d = 0; d < hd; d++) acc[d] += p * (double)or_f16_to_f32(vr[d]);
+        }
+        for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(acc[d] / sum);
+    }
+    free(s);
+    free(acc);
+}
+
+/* ------------------------------------------------------------ layers */
+
+int or_is_attn_layer(const or_cfg *c, int il) {
+    return c->attn_every > 0 && (il % c->attn_every) == c->attn_every - 1;
+}
+
+/* dbg (nullable) receives the GDN intermediates in this order:
+ * qkv[C] | z[HV*D] | alpha[HV] | beta_raw[HV] | conv_out[C] | g[HV] | beta[HV]
+ * | o[HV*D] | on[HV*D] */
+void or_gdn_mixer(const or_cfg *c, const void *const *w, void *const *st,
+                  const float *xn, float *out, float *dbg) {
+    const int E = c->n_embd, HK = c->gdn_hk, HV = c->gdn_hv, D = c->gdn_d;
+    const int C = (2 * HK + HV) * D, VD = HV * D;
+    float *qkv = (float *)malloc(sizeof(float) * (size_t)C);
+    float *z = (float *)malloc(sizeof(float) * (size_t)VD);
+    float *al = (float *)malloc(sizeof(float) * (size_t)HV);
+    float *br = (float *)malloc(sizeof(float) * (size_t)HV);
+    float *cv = (float *)malloc(sizeof(float) * (size_t)C);
+    float *g = (float *)malloc(sizeof(float) * (size_t)HV);
+    float *be = (float *)malloc(sizeof(float) * (size_t)HV);
+    float *o = (float *)malloc(sizeof(float) * (size_t)VD);
+    float *on = (float *)malloc(sizeof(float) * (size_t)VD);
+    const int t = c->t_default;
+    or_gemv(t, w[OR_SLOT_QKV], C, E, xn, qkv);
+    or_gemv(t, w[OR_SLOT_Z], VD, E, xn, z);
+    or_gemv(t, w[OR_SLOT_ALPHA], HV, E, xn, al);
+    or_gemv(t, w[OR_SLOT_BETA], HV, E, xn, br);
+    or_conv_silu(qkv, (float *)st[OR_ST_CONV], (const float *)w[OR_SLOT_CONV_W], cv, C, c->conv_k);
+    for (int h = 0; h < 2 * HK; h++) or_l2norm(cv + (size_t)h * D, cv + (size_t)h * D, D, c->eps);
+    or_gdn_gates(al, br, (const float *)w[OR_SLOT_DT_BIAS], (const float *)w[OR_SLOT_SSM_A], g, be, HV);
+    const float scale = 1.0f / sqrtf((float)D);
+    or_gdn_step(cv, cv + (size_t)HK * D, cv + (size_t)2 * HK * D, g, be, (float *)st[OR_ST_SSM], o,
+                HV, HK, D, scale);
+    or_gated_rmsnorm(o, z, (const float *)w[OR_SLOT_SSM_NORM], on, HV, D, c->eps);
+    or_gemv(t, w[OR_SLOT_SSM_OUT], E, VD, on, out);
+    if (dbg) {
+        float *p = dbg;
+        memcpy(p, qkv, sizeof(float) * C); p += C;
+        memcpy(p, z, sizeof(float) * VD); p += VD;
+        memcpy(p, al, sizeof(float) * HV); p += HV;
+        memcpy(p, br, sizeof(float) * HV); p += HV;
+        memcpy(p, cv, sizeof(float) * C); p += C;
+        memcpy(p, g, sizeof(float) * HV); p += HV;
+        memcpy(p, be, sizeof(float) * HV); p += HV;
+        memcpy(p, o, sizeof(float) * VD); p += VD;
+        memcpy(p, on, sizeof(float) * VD);
+    }
+    free(qkv); free(z); free(al); free(br); free(cv); free(g); free(be); free(o); free(on);
+}
+
+/* dbg (nullable): qg[NQ*2*HD] | k[NKV*HD] | v[NKV*HD] | qr[NQ*HD] | kr[NKV*HD]
+ * | att[NQ*HD] | gated[NQ*HD] */
+void or_attn_mixer(const or_cfg *c, const void *const *w, void *const *st,
+                   const float *xn, int pos, float *out, float *dbg) {
+    const int E = c->n_embd, NQ = c->attn_nq, NKV = c->attn_nkv, HD = c->head_dim;
+    const int RW = NKV * HD;
+    float *qg = (float *)malloc(sizeof(float) * (size_t)NQ * 2 * HD);
+    float *kk = (float *)malloc(sizeof(float) * (size_t)RW);
+    float *vv = (float *)malloc(sizeof(float) * (size_t)RW);
+    float *qr = (float *)malloc(sizeof(float) * (size_t)NQ * HD);
+    float *kr = (float *)malloc(sizeof(float) * (size_t)RW);
+    float *att = (float *)malloc(sizeof(float) * (size_t)NQ * HD);
+    float *gt = (float *)malloc(sizeof(float) * (size_t)NQ * HD);
+    or_gemv(c->t_default, w[OR_SLOT_WQ], (int64_t)NQ * 2 * HD, E, xn, qg);
+    or_gemv(c->t_default, w[OR_SLOT_WK], RW, E, xn, kk);
+    or_gemv(c->t_attn_v, w[OR_SLOT_WV], RW, E, xn, vv);
+    const float ts = or_rope_theta_scale(c->rope_base, c->rope_dims);
+    for (int h = 0; h < NQ; h++) {
+        or_rmsnorm(qg + (size_t)h * 2 * HD, (const float *)w[OR_SLOT_Q_NORM], qr + (size_t)h * HD, HD, c->eps);
+        or_rope_neox(qr + (size_t)h * HD, HD, c->rope_dims, pos, ts);
+    }
+    for (int g = 0; g < NKV; g++) {
+        or_rmsnorm(kk + (size_t)g * HD, (const float *)w[OR_SLOT_K_NORM], kr + (size_t)g * HD, HD, c->eps);
+        or_rope_neox(kr + (size_t)g * HD, HD, c->rope_dims, pos, ts);
+    }
+    uint16_t *K = (uint16_t *)st[OR_ST_K], *V = (uint16_t *)st[OR_ST_V];
+    for (int i = 0; i < RW; i++) {
+        K[(size_t)pos * RW + i] = or_f32_to_f16(kr[i]);
+        V[(size_t)pos * RW + i] = or_f32_to_f16(vv[i]);
+    }
+    or_attn_decode(qr, K, V, pos + 1, NQ, NKV, HD, RW, 1.0f / sqrtf((float)HD), att);
+    for (int h = 0; h < NQ; h++)
+        for (int d = 0; d < HD; d++) {
+            const float gv = qg[(size_t)h * 2 * HD + HD + d];
+            gt[(size_t)h * HD + d] = att[(size_t)h * HD + d] * or_sigmoid(gv);
+        }
+    or_gemv(c->t_default, w[OR_SLOT_WO], E, (int64_t)NQ * HD, gt, out);
+    if (dbg) {
+        float *p = dbg;
+        memcpy(p, qg, sizeof(float) * NQ * 2 * HD); p += NQ * 2 * HD;
+        memcpy(p, kk, sizeof(float) * RW); p += RW;
+        memcpy(p, vv, sizeof(float) * RW); p += RW;
+        memcpy(p, qr, sizeof(float) * NQ * HD); p += NQ * HD;
+        memcpy(p, kr, sizeof(float) * RW); p += RW;
+        memcpy(p, att, sizeof(float) * NQ * HD); p += NQ * HD;
+        memcpy(p, gt, sizeof(float) * NQ * HD);
+    }
+    free(qg); free(kk); free(vv); free(qr); free(kr); free(att); free(gt);
+}
+
+/* SwiGLU FFN: silu(gate.x) * (up.x), then down (k0/ops/gemv.cuh:327-347) */
+void or_ffn(const or_cfg *c, const void *const *w, const float *xn, float *out) {
+    const int E = c->n_embd, F = c->n_ff;
+    float *gg = (float *)malloc(sizeof(float) * (size_t)F);
+    float *uu = (float *)malloc(sizeof(float) * (size_t)F);
+    or_gemv(c->t_default, w[OR_SLOT_FFN_GATE], F, E, xn, gg);
+    or_gemv(c->t_default, w[OR_SLOT_FFN_UP], F, E, xn, uu);
+    for (int i = 0; i < F; i++) gg[i] = or_silu(gg[i]) * uu[i];
+    or_gemv(c->t_ffn_down, w[OR_SLOT_FFN_DOWN], E, F, gg, out);
+    free(gg);
+    free(uu);
+}
+
+int64_t or_argmax_first(const float *x, int64_t n) {
+    int64_t best = 0;
+    for (int64_t i = 1; i < n; i++)
+        if (x[i] > x[best]) best = i;
+    return best;
+}
+
+int or_decode_step(const or_cfg *c, const void *const *weights, void *const *state,
+                   int token, int pos, float *logits, float *resid) {
+    const int E = c->n_embd;
+    const void *embd = weights[(size_t)c->n_layer * OR_NSLOT + 0];
+    const float *onorm = (const float *)weights[(size_t)c->n_layer * OR_NSLOT + 1];
+    const void *outw = weights[(size_t)c->n_layer * OR_NSLOT + 2];
+    float *x = (float *)malloc(sizeof(float) * (size_t)E);
+    float *xn = (float *)malloc(sizeof(float) * (size_t)E);
+    float *a = (float *)malloc(sizeof(float) * (size_t)E);
+    or_dequant_row(c->t_embd, (const char *)embd + (size_t)token * or_row_bytes(c->t_embd, E), x, E);
+    for (int il = 0; il < c->n_layer; il++) {
+        const void *const *w = weights + (size_t)il * OR_NSLOT;
+        void *const *st = state + (size_t)il * OR_NST;
+        or_rmsnorm(x, (const float *)w[OR_SLOT_ATTN_NORM], xn, E, c->eps);
+        if (or_is_attn_layer(c, il))
+            or_attn_mixer(c, w, st, xn, pos, a, NULL);
+        else
+            or_gdn_mixer(c, w, st, xn, a, NULL);
+        for (int i = 0; i < E; i++) x[i] = x[i] + a[i];
+        or_rmsnorm(x, (const float *)w[OR_SLOT_POST_NORM], xn, E, c->eps);
+        or_ffn(c, w, xn, a);
+        for (int i = 0; i < E; i++) x[i] = x[i] + a[i];
+        if (resid) memcpy(resid + (size_t)il * E, x, sizeof(float) * E);
+    }
+    or_rmsnorm(x, onorm, xn, E, c->eps);
+    or_gemv(c->t_output, outw, c->n_vocab, E, xn, logits);
+    free(x);
+    free(xn);
+    free(a);
+    return (int)or_argmax_first(logits, c->n_vocab);
+}

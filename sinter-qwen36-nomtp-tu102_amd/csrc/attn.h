@@ -1,0 +1,225 @@
+// SINTER_OP_ATTN_DECODE: one full-attention layer's decode step after the
+// q|gate / k / v projections, fused:
+//   per-head RMSNorm * weight + NEOX RoPE on the first rope_dims dims
+//                                              (k0/ops/attn.cuh:109-182)
+//   f16 KV append at row pos                   (attn.cuh:184-211)
+//   split-K online-softmax partials            (attn.cuh:244-401)
+//   max/LSE merge by the last-arriving block   (attn.cuh:403-458)
+//   sigmoid output gate                        (attn.cuh:460-488)
+// Work item = (kv head g, chunk c).  An item serves all NQ/NKV q heads of
+// its group from one read of its K/V rows (GQA sharing).  The item whose
+// chunk holds `pos` also appends the new K/V row and uses it directly.  Each
+// item publishes an fp64 partial {acc[HD], max, sum} per q head; the block
+// that arrives last for kv head g merges that head group and applies the
+// gate, so the reference's separate FATTN_REDUCE / ATTN_GATE windows (and
+// their barriers) disappear.
+//
+// Declared numerics (oracle/oracle.c or_attn_decode): q/k norms and RoPE in
+// fp32 as ggml; scores are fp64 sums of exact products times the fp32 scale;
+// softmax and the V sum in fp64; the merged output rounded to fp32 once.
+#pragma once
+#include "dev_common.h"
+
+namespace sinter {
+
+constexpr int ATT_TILE = 32;   // KV positions per LDS tile
+constexpr int ATT_MAXG = 8;    // max q heads per kv head
+
+// y = rmsnorm(x) * w then NEOX RoPE, for one 256-wide head held one element
+// per thread; result in dst (LDS).  Every thread of the block calls this.
+__device__ __forceinline__ void att_norm_rope(float x, const float *w, float eps, int pos, float theta_scale,
+                                              uint32_t rope_dims, float *dst, double *red) {
+    const uint32_t t = threadIdx.x;
+    const double ss = block_sum_f64((double)(x * x), red);
+    const float mean = (float)(ss / 256.0);
+    const float sc = 1.0f / sqrtf(mean + eps);
+    const float nrm = x * sc;
+    dst[t] = nrm * w[t];
+    __syncthreads();
+    const uint32_t half = rope_dims / 2;
+    float y0 = 0.0f, y1 = 0.0f;
+    if (t < half) {
+        float theta = (float)pos;
+        for (uint32_t i = 0; i < t; i++) theta *= theta_scale;
+        const float c = (float)cos((double)theta), s = (float)sin((double)theta);
+        const float x0 = dst[t], x1 = dst[t + half];
+        const float a0 = x0 * c, a1 = x1 * s;
+        const float b0 = x0 * s, b1 = x1 * c;
+        y0 = a0 - a1;
+        y1 = b0 + b1;
+    }
+    __syncthreads();
+    if (t < half) {
+        dst[t] = y0;
+        dst[t + half] = y1;
+    }
+    __syncthreads();
+}
+
+__device__ void op_attn_decode(const sinter_instr &ins, char *lds, unsigned *err) {
+    const sinter_attn_args &a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
+    const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
+    const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
+    const int pos = reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos;
+    const uint32_t gqa = NKV ? NQ / NKV : 0;
+    const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 &&
+                    a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 && (uint32_t)pos < a.n_ctx;
+    if (!ok) {
+        if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
+        return;
+    }
+    const uint32_t t = threadIdx.x;
+    const uint32_t RW = NKV * HD;
+    const uint32_t n_kv = (uint32_t)pos + 1;
+    uint32_t clen = (n_kv + C - 1) / C;
+    clen = (clen + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
+
+    // LDS map
+    float *qf = reinterpret_cast<float *>(lds);                          // [gqa][256]
+    uint16_t *kt = reinterpret_cast<uint16_t *>(qf + ATT_MAXG * 256);    // [32][256]
+    uint16_t *vt = kt + ATT_TILE * 256;                                  // [32][256]
+    uint16_t *knew = vt + ATT_TILE * 256;                                // [256]
+    uint16_t *vnew = knew + 256;                                         // [256]
+    double *sc = reinterpret_cast<double *>(vnew + 256);                 // [gqa][32] scores -> weights
+    double *mrun = sc + ATT_MAXG * ATT_TILE;                             // [gqa]
+    double *lrun = mrun + ATT_MAXG;                                      // [gqa]
+    double *corr = lrun + ATT_MAXG;                                      // [gqa]
+    double *red = corr + ATT_MAXG;                                       // 16
+    float *knf = reinterpret_cast<float *>(red + 16);                    // [256] k scratch
+    unsigned *flag = reinterpret_cast<unsigned *>(knf + 256);
+
+    for (uint32_t item = rel; item < NKV * C; item += nblk) {
+        const uint32_t g = item / C, c = item % C;
+        const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
+        const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
+
+        for (uint32_t hh = 0; hh < gqa; hh++) {
+            const uint32_t h = g * gqa + hh;
+            att_norm_rope(a.qg[(size_t)h * 2 * HD + t], a.q_norm, a.eps, pos, a.theta_scale, a.rope_dims,
+                          qf + hh * 256, red);
+        }
+        if (owner) {
+            att_norm_rope(a.k[(size_t)g * HD + t], a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, knf, red);
+            const uint16_t kh = f2h(knf[t]), vh = f2h(a.v[(size_t)g * HD + t]);
+            knew[t] = kh;
+            vnew[t] = vh;
+            a.kc[(size_t)pos * RW + (size_t)g * HD + t] = kh;
+            a.vc[(size_t)pos * RW + (size_t)g * HD + t] = vh;
+        }
+        if (t < gqa) { mrun[t] = -INFINITY; lrun[t] = 0.0; }
+        double acc[ATT_MAXG];
+#pragma unroll
+        for (int hh = 0; hh < ATT_MAXG; hh++) acc[hh] = 0.0;
+        __syncthreads();
+
+        for (uint32_t t0 = kv0; t0 < kv1; t0 += ATT_TILE) {
+            // K and V tiles of this kv head: 32 rows x 512 B each
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t idx = t + k * 256, r = idx >> 5, ch = idx & 31, j = t0 + r;
+                uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
+                if (j < kv1) {
+                    if (owner && j == (uint32_t)pos) {
+                        kv4 = reinterpret_cast<const uint4 *>(knew)[ch];
+                        vv4 = reinterpret_cast<const uint4 *>(vnew)[ch];
+                    } else {
+                        const size_t o = (size_t)j * RW + (size_t)g * HD;
+                        kv4 = reinterpret_cast<const uint4 *>(a.kc + o)[ch];
+                        vv4 = reinterpret_cast<const uint4 *>(a.vc + o)[ch];
+                    }
+                }
+                reinterpret_cast<uint4 *>(kt)[idx] = kv4;
+                reinterpret_cast<uint4 *>(vt)[idx] = vv4;
+            }
+            __syncthreads();
+            // scores: thread (r = t/8, part = t%8) covers dims [32 part, 32 part + 32)
+            {
+                const uint32_t r = t >> 3, part = t & 7;
+                const uint16_t *kr = kt + r * 256 + part * 32;
+                for (uint32_t hh = 0; hh < gqa; hh++) {
+                    const float *q = qf + hh * 256 + part * 32;
+                    double d = 0.0;
+#pragma unroll
+                    for (int i = 0; i < 32; i++) d = fma((double)q[i], (double)h2f(kr[i]), d);
+                    d += __shfl_xor(d, 1, 64);
+                    d += __shfl_xor(d, 2, 64);
+                    d += __shfl_xor(d, 4, 64);
+                    if (part == 0) sc[hh * ATT_TILE + r] = (t0 + r < kv1) ? d * (double)a.scale : -INFINITY;
+                }
+            }
+            __syncthreads();
+            // online softmax per head: 32 lanes per head
+            if (t < gqa * ATT_TILE) {
+                const uint32_t hh = t / ATT_TILE, r = t % ATT_TILE;
+                const double s = sc[hh * ATT_TILE + r];
+                double mt = s;
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) mt = fmax(mt, __shfl_xor(mt, o, 64));
+                const double mo = mrun[hh];
+                const double mn = fmax(mo, mt);
+                const double w = (s == -INFINITY) ? 0.0 : exp(s - mn);
+                double ws = w;
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) ws += __shfl_xor(ws, o, 64);
+                sc[hh * ATT_TILE + r] = w;
+                if (r == 0) {
+                    const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
+                    corr[hh] = cf;
+                    lrun[hh] = lrun[hh] * cf + ws;
+                    mrun[hh] = mn;
+                }
+            }
+            __syncthreads();
+            // V accumulation: thread t owns dim t
+            for (uint32_t hh = 0; hh < gqa; hh++) {
+                double v = acc[hh] * corr[hh];
+                const double *w = sc + hh * ATT_TILE;
+#pragma unroll 8
+                for (int r = 0; r < ATT_TILE; r++) v = fma(w[r], (double)h2f(vt[r * 256 + t]), v);
+                acc[hh] = v;
+            }
+            __syncthreads();
+        }
+
+        // publish the partial, count in; the last block of kv head g merges
+        double *pbase = a.part + ((size_t)g * C + c) * gqa * (HD + 2);
+        for (uint32_t hh = 0; hh < gqa; hh++) {
+            double *p = pbase + hh * (HD + 2);
+            p[t] = acc[hh];
+            if (t == 0) { p[HD] = mrun[hh]; p[HD + 1] = lrun[hh]; }
+        }
+        __syncthreads();
+        if (t == 0) {
+            fence_release_agent();
+            const unsigned old = __hip_atomic_fetch_add(a.count + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned last = (old == C - 1) ? 1u : 0u;
+            if (last) fence_acquire_agent();
+            *flag = last;
+        }
+        __syncthreads();
+        if (*flag) {
+            const double *gbase = a.part + (size_t)g * C * gqa * (HD + 2);
+            for (uint32_t hh = 0; hh < gqa; hh++) {
+                double M = -INFINITY;
+                for (uint32_t cc = 0; cc < C; cc++) M = fmax(M, gbase[(cc * gqa + hh) * (HD + 2) + HD]);
+                double O = 0.0, L = 0.0;
+                for (uint32_t cc = 0; cc < C; cc++) {
+                    const double *p = gbase + (cc * gqa + hh) * (HD + 2);
+                    const double m = p[HD];
+                    if (m == -INFINITY) continue;
+                    const double e = exp(m - M);
+                    O = fma(e, p[t], O);
+                    L = fma(e, p[HD + 1], L);
+                }
+                const uint32_t h = g * gqa + hh;
+                const float att = (float)(O / L);
+                const float gate = a.qg[(size_t)h * 2 * HD + HD + t];
+                a.out[(size_t)h * HD + t] = att * dev_sigmoid(gate);
+            }
+            if (t == 0) __hip_atomic_store(a.count + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace sinter

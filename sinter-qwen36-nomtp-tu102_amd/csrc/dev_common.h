@@ -1,0 +1,116 @@
+// Device-side building blocks shared by every op family: wave64 reductions,
+// agent-scope (cross-XCD) loads/stores and fences, f16/bf16 conversions and
+// the activation-quantiser arithmetic.
+//
+// Coherence on gfx950: each of the 8 XCDs has its own L2.  Data written in
+// one phase and read by another workgroup in a later phase is ordered by the
+// grid barrier (sync.h), whose release/acquire fences at agent scope write
+// back and invalidate the L2/L1 of the participating XCDs; after the barrier
+// ordinary loads see the producer's stores.  Weights are immutable and use
+// plain loads throughout.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "isa.h"
+
+namespace sinter {
+
+// ---------------------------------------------------------------- wave64
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Block-wide fp64 sum (blockDim.x a multiple of 64, <= 1024); every thread
+// gets the total.  `red` is LDS scratch of >= 16 doubles.  The result is
+// order-dependent only at fp64 rounding level (callers round to fp32).
+__device__ __forceinline__ double block_sum_f64(double v, double *red) {
+    v = wave_sum_f64(v);
+    const int nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; i++) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
+    return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float bf2f(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+// ggml FP32->BF16: quiet NaN, otherwise round half to even
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 64);
+    return (uint16_t)((u + (0x7fffu + ((u >> 16) & 1u))) >> 16);
+}
+
+// ggml silu/sigmoid/softplus in fp32 with the exponential evaluated in fp64
+// and rounded once (the declared transcendental rule).
+__device__ __forceinline__ float dev_silu(float x) { return x / (1.0f + (float)exp(-(double)x)); }
+__device__ __forceinline__ float dev_sigmoid(float x) { return 1.0f / (1.0f + (float)exp(-(double)x)); }
+__device__ __forceinline__ float dev_softplus(float x) {
+    if (x > 20.0f) return x;
+    const float e = (float)exp((double)x);
+    return (float)log((double)(1.0f + e));
+}
+
+// ---------------------------------------------------------------- memory scope
+
+__device__ __forceinline__ unsigned atomic_load_relaxed_agent(const unsigned *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fence_release_agent() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+__device__ __forceinline__ void fence_acquire_agent() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Record the first error: err[0] = code (first writer wins), err[1] = aux.
+// Ops call this and return normally so every block still reaches the next
+// grid barrier (core/interp.cuh error protocol).
+__device__ __forceinline__ void raise_error(unsigned *err, unsigned code, unsigned aux) {
+    if (!err) return;
+    if (atomicCAS(err, 0u, code) == 0u)
+        __hip_atomic_store(err + 1, aux, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- block formats
+
+struct blk_q8_0 { uint16_t d; int8_t qs[32]; };                                  // 34 B
+struct blk_q4_K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; };      // 144 B
+struct blk_q6_K { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; }; // 210 B
+static_assert(sizeof(blk_q8_0) == 34, "q8_0");
+static_assert(sizeof(blk_q4_K) == 144, "q4_K");
+static_assert(sizeof(blk_q6_K) == 210, "q6_K");
+
+}  // namespace sinter

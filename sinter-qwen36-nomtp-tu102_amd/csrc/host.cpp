@@ -1,0 +1,528 @@
+// C ABI: status/error plumbing, standalone op entry points, synthetic data,
+// and the host control plane (core/host.cpp:19-245 in the reference).
+//
+// Control-plane design on MI355X: the reference keeps one cooperative kernel
+// resident and rings a host-mapped doorbell per pass.  Here a pass (or a run
+// of greedy passes) is one cooperative launch of the interpreter: a launch
+// costs microseconds against a ~2.5 ms pass, needs no PCIe polling from the
+// device, and a faulty program ends with its kernel instead of leaving a
+// resident grid behind.  The lifecycle and status semantics of host_init /
+// upload / launch / run_pass / shutdown / destroy are kept.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "internal.h"
+#include "synth.h"
+
+namespace sinter {
+
+static thread_local std::string g_last_error;
+
+int set_error(int status, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_error(SINTER_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+unsigned *op_err_cell() {
+    static std::mutex mu;
+    static std::map<int, unsigned *> cells;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cells.find(dev);
+    if (it != cells.end()) return it->second;
+    unsigned *p = nullptr;
+    if (hipMalloc(&p, 256) != hipSuccess) return nullptr;
+    if (hipMemset(p, 0, 256) != hipSuccess) return nullptr;
+    cells[dev] = p;
+    return p;
+}
+
+static bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int vdot(int t) {
+    return (t == SINTER_Q4_K || t == SINTER_Q6_K) ? SINTER_Q8_K
+         : (t == SINTER_Q8_0) ? SINTER_Q8_0
+         : (t == SINTER_BF16) ? SINTER_BF16
+         : (t == SINTER_F32) ? SINTER_F32 : -1;
+}
+
+int validate_gemv(const sinter_gemv_args &a, const char **why) {
+    auto bad = [&](const char *w) { *why = w; return SINTER_ERR_ARG; };
+    if (a.n_seg < 1 || a.n_seg > SINTER_GEMV_MAX_SEG) return bad("n_seg out of range");
+    if (a.K == 0 || a.K % 256) return bad("K must be a positive multiple of 256");
+    const int vt = vdot(a.seg[0].type);
+    if (vt < 0) return bad("unsupported weight type");
+    const uint64_t need = vt == SINTER_Q8_K ? a.K + (a.K / 256) * 4 + (a.K / 16) * 2
+                        : vt == SINTER_Q8_0 ? a.K + (a.K / 32) * 4
+                        : vt == SINTER_BF16 ? (uint64_t)a.K * 2 : (uint64_t)a.K * 4;
+    if (need > QBUF_BYTES) return bad("K too large for the activation buffer");
+    switch (a.pro) {
+    case SINTER_PRO_PLAIN:
+        if (!a.x || !al16(a.x)) return bad("x must be a 16-byte aligned device pointer");
+        break;
+    case SINTER_PRO_RMSNORM:
+        if (!a.x || !al16(a.x) || !a.norm_w || !al16(a.norm_w)) return bad("x / norm_w missing or unaligned");
+        break;
+    case SINTER_PRO_GATED:
+        if (!a.x || !al16(a.x) || !a.norm_w || !a.aux || !al16(a.aux)) return bad("gated: x / norm_w / z");
+        if (a.gn_log2d < 2 || a.gn_log2d > 8) return bad("gated: head width must be 4..256");
+        break;
+    case SINTER_PRO_EMBED:
+        if (!a.aux || !a.token || !a.norm_w || !al16(a.norm_w) || a.aux_rows == 0)
+            return bad("embed: rows / token / norm_w / aux_rows");
+        if (sinter_row_bytes_dev(a.aux_type, a.K) == 0) return bad("embed: type");
+        if (a.x_out && !al16(a.x_out)) return bad("embed: x_out unaligned");
+        break;
+    default: return bad("unknown prologue");
+    }
+    for (int s = 0; s < a.n_seg; s++) {
+        const sinter_gemv_seg &g = a.seg[s];
+        if (vdot(g.type) != vt) return bad("segments must share one vec_dot type");
+        if (!g.w || !al16(g.w) || !g.y) return bad("segment weights must be 16-byte aligned; y required");
+        const bool sw = g.epi == SINTER_EPI_SWIGLU;
+        const uint64_t rbe = sinter_row_bytes_dev(g.type, a.K) * (sw ? 2 : 1);
+        if (rbe > TILE_BYTES - 64) return bad("row too long for one LDS tile");
+        if ((a.K / 256) * (sw ? 2u : 1u) > BLOCK_THREADS) return bad("too many groups per row");
+        switch (g.epi) {
+        case SINTER_EPI_STORE: break;
+        case SINTER_EPI_RESID: if (!g.aux) return bad("resid: aux"); break;
+        case SINTER_EPI_SWIGLU: if (!g.w2 || !al16(g.w2)) return bad("swiglu: w2"); break;
+        case SINTER_EPI_ARGMAX: if (!a.epi_ws) return bad("argmax: epi_ws"); break;
+        case SINTER_EPI_CONV:
+            if (!g.w2 || !g.aux || g.dconv < 2 || g.dconv > 8) return bad("conv: w2 / aux / dconv");
+            break;
+        default: return bad("unknown epilogue");
+        }
+    }
+    return SINTER_OK;
+}
+
+template <class T>
+static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
+    if (blocks == 0 || blocks > 65535) return set_error(SINTER_ERR_ARG, "blocks must be 1..65535");
+    unsigned *err = op_err_cell();
+    if (!err) return set_error(SINTER_ERR_HIP, "cannot allocate the op error cell");
+    sinter_instr ins;
+    std::memset(&ins, 0, sizeof ins);
+    ins.kind = (uint16_t)kind;
+    ins.block_lo = 0;
+    ins.block_hi = (uint16_t)blocks;
+    std::memcpy(ins.payload, &args, sizeof args);
+    if (!hip_ok(launch_op(ins, blocks, err, (hipStream_t)stream), "op launch")) return SINTER_ERR_HIP;
+    return SINTER_OK;
+}
+
+}  // namespace sinter
+
+using namespace sinter;
+
+extern "C" {
+
+const char *sinter_last_error(void) { return g_last_error.c_str(); }
+int sinter_abi_version(void) { return SINTER_ABI_VERSION; }
+size_t sinter_row_bytes(int type, int64_t k) { return sinter_row_bytes_dev(type, k); }
+
+int sinter_op_gemv(const sinter_gemv_args *a, uint32_t blocks, void *stream) {
+    if (!a) return set_error(SINTER_ERR_ARG, "null args");
+    const char *why = "";
+    if (validate_gemv(*a, &why) != SINTER_OK) return set_error(SINTER_ERR_ARG, "gemv: %s", why);
+    return run_one(SINTER_OP_GEMV, *a, blocks, stream);
+}
+
+int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream) {
+    if (!a || !a->qkv || !a->alpha || !a->beta || !a->dt_bias || !a->ssm_a || !a->state || !a->o)
+        return set_error(SINTER_ERR_ARG, "gdn: null pointer");
+    const uint32_t D = a->d, cols = a->cols;
+    const uint32_t tpc = cols ? BLOCK_THREADS / cols : 0;
+    if (!(D == 64 || D == 128 || D == 256) || !cols || D % cols || BLOCK_THREADS % cols || !tpc || tpc > 64 ||
+        D % tpc || (D / tpc) % 4 || D / tpc > 32 || !a->hk || a->hv % a->hk || !al16(a->state))
+        return set_error(SINTER_ERR_ARG, "gdn: unsupported shape (D=%u cols=%u hk=%u hv=%u)", D, cols, a->hk, a->hv);
+    return run_one(SINTER_OP_GDN_STEP, *a, blocks, stream);
+}
+
+int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream) {
+    if (!a || !a->qg || !a->k || !a->v || !a->q_norm || !a->k_norm || !a->kc || !a->vc || !a->part || !a->count ||
+        !a->out || !a->pass_cell)
+        return set_error(SINTER_ERR_ARG, "attn: null pointer");
+    if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->rope_dims > a->hd ||
+        a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
+        return set_error(SINTER_ERR_ARG, "attn: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
+    return run_one(SINTER_OP_ATTN_DECODE, *a, blocks, stream);
+}
+
+int sinter_op_error(uint32_t *code, uint32_t *aux) {
+    unsigned *err = op_err_cell();
+    if (!err) return set_error(SINTER_ERR_HIP, "no error cell");
+    if (!hip_ok(hipDeviceSynchronize(), "synchronize")) return SINTER_ERR_HIP;
+    unsigned h[2] = {0, 0};
+    if (!hip_ok(hipMemcpy(h, err, 8, hipMemcpyDeviceToHost), "error cell read")) return SINTER_ERR_HIP;
+    if (!hip_ok(hipMemset(err, 0, 8), "error cell clear")) return SINTER_ERR_HIP;
+    if (code) *code = h[0];
+    if (aux) *aux = h[1];
+    return SINTER_OK;
+}
+
+int sinter_argmax_ws_create(uint32_t blocks, int32_t *pass_cell, int32_t *history, uint32_t history_cap,
+                            sinter_argmax_ws **out_dev) {
+    if (!out_dev || !pass_cell || blocks == 0) return set_error(SINTER_ERR_ARG, "argmax ws: args");
+    char *mem = nullptr;
+    const size_t bytes = 256 + (size_t)blocks * 8 + 256;
+    if (!hip_ok(hipMalloc(&mem, bytes), "argmax ws alloc")) return SINTER_ERR_HIP;
+    if (!hip_ok(hipMemset(mem, 0, bytes), "argmax ws clear")) return SINTER_ERR_HIP;
+    sinter_argmax_ws h;
+    std::memset(&h, 0, sizeof h);
+    h.count = reinterpret_cast<uint32_t *>(mem + 128);
+    h.part_val = reinterpret_cast<float *>(mem + 256);
+    h.part_idx = reinterpret_cast<int32_t *>(mem + 256 + (size_t)blocks * 4);
+    h.pass_cell = pass_cell;
+    h.history = history;
+    h.history_cap = history_cap;
+    h.capacity = blocks;
+    if (!hip_ok(hipMemcpy(mem, &h, sizeof h, hipMemcpyHostToDevice), "argmax ws upload")) return SINTER_ERR_HIP;
+    *out_dev = reinterpret_cast<sinter_argmax_ws *>(mem);
+    return SINTER_OK;
+}
+
+void sinter_argmax_ws_destroy(sinter_argmax_ws *dev) {
+    if (dev) (void)hipFree(dev);
+}
+
+uint64_t sinter_seed(uint64_t config_id, const char *name, int64_t layer) {
+    uint64_t h = 1469598103934665603ull;  // FNV-1a over the name
+    for (const char *p = name ? name : ""; *p; p++) { h ^= (uint8_t)*p; h *= 1099511628211ull; }
+    return sx_mix(sx_mix(config_id) ^ h ^ sx_mix((uint64_t)layer + 0x5151));
+}
+
+int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k, uint64_t seed, float a, float b,
+                 void *stream) {
+    if (!dst || rows < 0 || k < 0) return set_error(SINTER_ERR_ARG, "synth: args");
+    const bool weight = kind == SINTER_SYN_WEIGHT || kind == SINTER_SYN_Q8_0_CFG1;
+    if (weight) {
+        if (k % 256) return set_error(SINTER_ERR_ARG, "synth: k must be a multiple of 256");
+        if (kind == SINTER_SYN_Q8_0_CFG1 && type != SINTER_Q8_0) return set_error(SINTER_ERR_ARG, "synth: cfg1 is Q8_0");
+        if (!(type == SINTER_Q4_K || type == SINTER_Q6_K || type == SINTER_Q8_0 || type == SINTER_BF16 ||
+              type == SINTER_F16 || type == SINTER_F32))
+            return set_error(SINTER_ERR_ARG, "synth: type");
+    } else if (kind != SINTER_SYN_NORMAL && kind != SINTER_SYN_UNIFORM && kind != SINTER_SYN_NORMAL_F16) {
+        return set_error(SINTER_ERR_ARG, "synth: kind");
+    }
+    const uint64_t n_units = weight ? (uint64_t)rows * (uint64_t)(k / 256) : (uint64_t)rows * (uint64_t)k;
+    if (dev) {
+        if (!hip_ok(launch_synth(dst, kind, type, n_units, seed, a, b, (hipStream_t)stream), "synth launch"))
+            return SINTER_ERR_HIP;
+        return SINTER_OK;
+    }
+    const unsigned nt = std::max(1u, std::min(64u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> th;
+    for (unsigned w = 0; w < nt; w++) {
+        th.emplace_back([=]() {
+            const uint64_t lo = n_units * w / nt, hi = n_units * (w + 1) / nt;
+            uint8_t *d = static_cast<uint8_t *>(dst);
+            for (uint64_t i = lo; i < hi; i++) {
+                if (weight) {
+                    const uint32_t gb = sx_group_bytes(type);
+                    sx_weight_group(seed, i, type, kind == SINTER_SYN_Q8_0_CFG1, d + i * gb);
+                } else if (kind == SINTER_SYN_NORMAL) {
+                    reinterpret_cast<float *>(d)[i] = a + b * sx_normal(seed, i);
+                } else if (kind == SINTER_SYN_UNIFORM) {
+                    reinterpret_cast<float *>(d)[i] = a + (b - a) * sx_unit(seed, i);
+                } else {
+                    reinterpret_cast<uint16_t *>(d)[i] = sx_f2h(b * sx_normal(seed, i));
+                }
+            }
+        });
+    }
+    for (auto &t : th) t.join();
+    return SINTER_OK;
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------- host control plane
+
+struct sinter_host {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    sinter_instr *d_prog = nullptr;
+    uint32_t n_instr = 0, epoch_stride = 0;
+    unsigned *d_cells = nullptr;          // [0] barrier counter | [32] err[2]
+    sinter_pass_cell *d_pass = nullptr;
+    int32_t *d_history = nullptr;
+    uint32_t history_cap = 0;
+    long long *d_pass_cycles = nullptr;
+    unsigned pass_cycles_cap = 0;
+    uint32_t passes_done = 0;
+    long long *d_op_cycles = nullptr;
+    uint32_t blocks = 0;
+    uint64_t spin_limit = 0;
+    uint64_t clock_khz = 0;
+    bool launched = false;
+    bool profile_ops = false;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;  // bracket every interpreter launch
+    float last_ms = 0.0f;
+};
+
+static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
+    InterpCtl ctl;
+    std::memset(&ctl, 0, sizeof ctl);
+    ctl.bar = h->d_cells;
+    ctl.err = h->d_cells + 32;
+    ctl.pass_cycles = h->d_pass_cycles;
+    ctl.pass_cycles_cap = h->pass_cycles_cap;
+    ctl.pass_base = h->passes_done;
+    ctl.op_cycles = h->profile_ops ? h->d_op_cycles : nullptr;
+    ctl.spin_limit = h->spin_limit;
+    ctl.n_instr = h->n_instr;
+    ctl.n_passes = n_passes;
+    if (!hip_ok(hipMemsetAsync(h->d_cells, 0, 4, h->stream), "barrier reset")) return SINTER_RUN_ERR;
+    if (!hip_ok(hipEventRecord(h->ev0, h->stream), "event")) return SINTER_RUN_ERR;
+    if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream), "cooperative launch")) return SINTER_RUN_ERR;
+    if (!hip_ok(hipEventRecord(h->ev1, h->stream), "event")) return SINTER_RUN_ERR;
+    h->passes_done += n_passes;
+    // wait with a watchdog; the kernel's own barrier spin limit bounds it too
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double, std::milli>(timeout_ms);
+    for (;;) {
+        const hipError_t q = hipStreamQuery(h->stream);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) {
+            hip_ok(q, "interpreter");
+            return SINTER_RUN_ERR;
+        }
+        if (std::chrono::steady_clock::now() > deadline) {
+            set_error(SINTER_ERR_TIMEOUT, "watchdog: pass did not finish in %.1f ms", timeout_ms);
+            return SINTER_RUN_TIMEOUT;
+        }
+        std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+    (void)hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1);
+    unsigned e[2] = {0, 0};
+    if (!hip_ok(hipMemcpy(e, h->d_cells + 32, 8, hipMemcpyDeviceToHost), "error cell")) return SINTER_RUN_ERR;
+    if (e[0]) {
+        set_error(SINTER_ERR_DEVICE, "device error %u (aux %u)", e[0], e[1]);
+        return SINTER_RUN_ERR;
+    }
+    return SINTER_RUN_OK;
+}
+
+extern "C" {
+
+int sinter_host_init(sinter_host **out, int device, unsigned pass_cycles_cap) {
+    if (!out) return set_error(SINTER_ERR_ARG, "null out");
+    *out = nullptr;
+    if (!hip_ok(hipSetDevice(device), "hipSetDevice")) return SINTER_ERR_HIP;
+    hipDeviceProp_t p;
+    if (!hip_ok(hipGetDeviceProperties(&p, device), "device properties")) return SINTER_ERR_HIP;
+    int coop = 0;
+    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
+    int per_cu = 0;
+    if (!hip_ok(interp_max_blocks(&per_cu), "occupancy")) return SINTER_ERR_HIP;
+    if (!coop || per_cu < 1)
+        return set_error(SINTER_ERR_DEVICE, "device %d cannot run the interpreter envelope (coop %d, blocks/CU %d)",
+                         device, coop, per_cu);
+    sinter_host *h = new sinter_host();
+    h->device = device;
+    h->blocks = (uint32_t)p.multiProcessorCount;  // one workgroup per CU
+    int khz = 0;
+    (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device);
+    h->clock_khz = khz > 0 ? (uint64_t)khz : 100000;
+    h->spin_limit = h->clock_khz * 1000ull * 10ull;  // 10 s
+    bool ok = hip_ok(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "stream") &&
+              hip_ok(hipEventCreate(&h->ev0), "event") && hip_ok(hipEventCreate(&h->ev1), "event") &&
+              hip_ok(hipMalloc(&h->d_cells, 4096), "cells") && hip_ok(hipMemset(h->d_cells, 0, 4096), "cells clear");
+    if (ok) h->d_pass = reinterpret_cast<sinter_pass_cell *>(reinterpret_cast<char *>(h->d_cells) + 1024);
+    h->pass_cycles_cap = pass_cycles_cap;
+    if (ok && pass_cycles_cap) {
+        ok = hip_ok(hipMalloc(&h->d_pass_cycles, (size_t)pass_cycles_cap * 8), "pass cycles") &&
+             hip_ok(hipMemset(h->d_pass_cycles, 0, (size_t)pass_cycles_cap * 8), "pass cycles clear");
+    }
+    if (ok)
+        ok = hip_ok(hipMalloc(&h->d_op_cycles, SINTER_OP_KIND_COUNT * 8), "op cycles") &&
+             hip_ok(hipMemset(h->d_op_cycles, 0, SINTER_OP_KIND_COUNT * 8), "op cycles clear");
+    if (!ok) {
+        sinter_host_destroy(h);
+        return SINTER_ERR_HIP;
+    }
+    // token history of greedy runs (the argmax epilogue appends to it)
+    if (!hip_ok(hipMalloc(&h->d_history, 65536 * 4), "history")) { sinter_host_destroy(h); return SINTER_ERR_HIP; }
+    h->history_cap = 65536;
+    *out = h;
+    return SINTER_OK;
+}
+
+int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_instr, uint32_t epoch_stride) {
+    if (!h || !prog || n_instr == 0) return set_error(SINTER_ERR_ARG, "upload: args");
+    if (h->launched) return set_error(SINTER_ERR_STATE, "upload after launch");
+    for (uint32_t i = 0; i < n_instr; i++) {
+        const sinter_instr &in = prog[i];
+        if (in.kind != SINTER_OP_BOUNDARY && in.kind != SINTER_OP_NOP && in.kind < SINTER_OP_KIND_COUNT &&
+            (in.block_lo >= in.block_hi || in.block_hi > h->blocks))
+            return set_error(SINTER_ERR_ARG, "instruction %u: block range [%u,%u) outside the %u-block grid", i,
+                             in.block_lo, in.block_hi, h->blocks);
+        if (in.kind == SINTER_OP_GEMV) {
+            sinter_gemv_args a;
+            std::memcpy(&a, in.payload, sizeof a);
+            const char *why = "";
+            if (validate_gemv(a, &why) != SINTER_OK)
+                return set_error(SINTER_ERR_ARG, "instruction %u (gemv): %s", i, why);
+        }
+    }
+    if (h->d_prog) (void)hipFree(h->d_prog);
+    h->d_prog = nullptr;
+    if (!hip_ok(hipMalloc(&h->d_prog, (size_t)n_instr * sizeof(sinter_instr)), "program alloc")) return SINTER_ERR_HIP;
+    if (!hip_ok(hipMemcpy(h->d_prog, prog, (size_t)n_instr * sizeof(sinter_instr), hipMemcpyHostToDevice),
+                "program upload"))
+        return SINTER_ERR_HIP;
+    h->n_instr = n_instr;
+    h->epoch_stride = epoch_stride;
+    return SINTER_OK;
+}
+
+int sinter_host_launch(sinter_host *h) {
+    if (!h || !h->d_prog) return set_error(SINTER_ERR_STATE, "launch before upload");
+    h->launched = true;
+    return SINTER_OK;
+}
+
+int sinter_host_run_pass(sinter_host *h, int32_t token, double timeout_ms) {
+    if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_pass before launch"), SINTER_RUN_ERR;
+    if (!hip_ok(hipMemcpyAsync(&h->d_pass->token, &token, 4, hipMemcpyHostToDevice, h->stream), "token write"))
+        return SINTER_RUN_ERR;
+    return run_launch(h, 1, timeout_ms);
+}
+
+int sinter_host_run_passes(sinter_host *h, int32_t token, uint32_t n_passes, int32_t *tokens_out, double timeout_ms) {
+    if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_passes before launch"), SINTER_RUN_ERR;
+    if (n_passes == 0 || n_passes > h->history_cap) return set_error(SINTER_ERR_ARG, "n_passes"), SINTER_RUN_ERR;
+    int32_t cell[2] = {token, 0};
+    if (!hip_ok(hipMemcpyAsync(&h->d_pass->token, &cell[0], 4, hipMemcpyHostToDevice, h->stream), "token write") ||
+        !hip_ok(hipMemcpyAsync(&h->d_pass->steps, &cell[1], 4, hipMemcpyHostToDevice, h->stream), "steps reset"))
+        return SINTER_RUN_ERR;
+    const int rs = run_launch(h, n_passes, timeout_ms);
+    if (rs != SINTER_RUN_OK) return rs;
+    if (tokens_out &&
+        !hip_ok(hipMemcpy(tokens_out, h->d_history, (size_t)n_passes * 4, hipMemcpyDeviceToHost), "history read"))
+        return SINTER_RUN_ERR;
+    return SINTER_RUN_OK;
+}
+
+int sinter_host_shutdown(sinter_host *h, double timeout_ms) {
+    if (!h) return set_error(SINTER_ERR_ARG, "null host");
+    if (!h->launched) return SINTER_OK;
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double, std::milli>(timeout_ms);
+    for (;;) {
+        const hipError_t q = hipStreamQuery(h->stream);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) return hip_ok(q, "shutdown") ? SINTER_OK : SINTER_ERR_HIP;
+        if (std::chrono::steady_clock::now() > deadline) return set_error(SINTER_ERR_TIMEOUT, "shutdown watchdog");
+        std::this_thread::sleep_for(std::chrono::microseconds(100));
+    }
+    h->launched = false;
+    return SINTER_OK;
+}
+
+void sinter_host_destroy(sinter_host *h) {
+    if (!h) return;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->d_prog) (void)hipFree(h->d_prog);
+    if (h->d_cells) (void)hipFree(h->d_cells);
+    if (h->d_pass_cycles) (void)hipFree(h->d_pass_cycles);
+    if (h->d_op_cycles) (void)hipFree(h->d_op_cycles);
+    if (h->d_history) (void)hipFree(h->d_history);
+    if (h->ev0) (void)hipEventDestroy(h->ev0);
+    if (h->ev1) (void)hipEventDestroy(h->ev1);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+int sinter_host_read_pass_cycles(sinter_host *h, long long *out, unsigned count) {
+    if (!h || !out || !h->d_pass_cycles || count > h->pass_cycles_cap) return set_error(SINTER_ERR_ARG, "pass cycles");
+    if (!hip_ok(hipMemcpy(out, h->d_pass_cycles, (size_t)count * 8, hipMemcpyDeviceToHost), "pass cycles read"))
+        return SINTER_ERR_HIP;
+    return SINTER_OK;
+}
+
+int sinter_host_reset_op_cycles(sinter_host *h) {
+    if (!h) return set_error(SINTER_ERR_ARG, "null host");
+    h->profile_ops = true;
+    return hip_ok(hipMemset(h->d_op_cycles, 0, SINTER_OP_KIND_COUNT * 8), "op cycles reset") ? SINTER_OK
+                                                                                              : SINTER_ERR_HIP;
+}
+
+int sinter_host_read_op_cycles(sinter_host *h, long long *out, unsigned count) {
+    if (!h || !out || count > SINTER_OP_KIND_COUNT) return set_error(SINTER_ERR_ARG, "op cycles");
+    return hip_ok(hipMemcpy(out, h->d_op_cycles, (size_t)count * 8, hipMemcpyDeviceToHost), "op cycles read")
+               ? SINTER_OK
+               : SINTER_ERR_HIP;
+}
+
+sinter_pass_cell *sinter_host_pass_cell(sinter_host *h) { return h ? h->d_pass : nullptr; }
+
+float sinter_host_last_launch_ms(sinter_host *h) { return h ? h->last_ms : 0.0f; }
+
+int32_t *sinter_host_history(sinter_host *h, uint32_t *cap) {
+    if (!h) return nullptr;
+    if (cap) *cap = h->history_cap;
+    return h->d_history;
+}
+
+int sinter_host_error(sinter_host *h, uint32_t *code, uint32_t *aux) {
+    if (!h) return set_error(SINTER_ERR_ARG, "null host");
+    unsigned e[2] = {0, 0};
+    if (!hip_ok(hipMemcpy(e, h->d_cells + 32, 8, hipMemcpyDeviceToHost), "error cell")) return SINTER_ERR_HIP;
+    if (code) *code = e[0];
+    if (aux) *aux = e[1];
+    return SINTER_OK;
+}
+
+int sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32_t *lds_bytes) {
+    if (!h) return set_error(SINTER_ERR_ARG, "null host");
+    if (blocks) *blocks = h->blocks;
+    if (threads) *threads = BLOCK_THREADS;
+    if (lds_bytes) *lds_bytes = LDS_BYTES;
+    return SINTER_OK;
+}
+
+int sinter_host_set_grid(sinter_host *h, uint32_t blocks) {
+    if (!h || blocks == 0) return set_error(SINTER_ERR_ARG, "set_grid: args");
+    if (h->launched) return set_error(SINTER_ERR_STATE, "set_grid after launch");
+    hipDeviceProp_t p;
+    if (!hip_ok(hipGetDeviceProperties(&p, h->device), "device properties")) return SINTER_ERR_HIP;
+    int per_cu = 0;
+    if (!hip_ok(interp_max_blocks(&per_cu), "occupancy")) return SINTER_ERR_HIP;
+    if (blocks > (uint32_t)(per_cu * p.multiProcessorCount))
+        return set_error(SINTER_ERR_ARG, "set_grid: %u blocks exceed the co-resident limit %d", blocks,
+                         per_cu * p.multiProcessorCount);
+    h->blocks = blocks;
+    return SINTER_OK;
+}
+
+int sinter_host_set_pos(sinter_host *h, int32_t pos) {
+    if (!h) return set_error(SINTER_ERR_ARG, "null host");
+    return hip_ok(hipMemcpyAsync(&h->d_pass->pos, &pos, 4, hipMemcpyHostToDevice, h->stream), "pos write") &&
+                   hip_ok(hipStreamSynchronize(h->stream), "pos sync")
+               ? SINTER_OK
+               : SINTER_ERR_HIP;
+}
+
+}  // extern "C"

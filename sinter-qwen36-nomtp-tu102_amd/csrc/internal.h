@@ -1,0 +1,36 @@
+// Declarations shared by the kernel TU (interp.hip) and the host TUs
+// (host.cpp, model.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "isa.h"
+
+namespace sinter {
+
+// Kernel-side control block of one interpreter launch (core/interp.cuh:60-75)
+struct InterpCtl {
+    unsigned *bar;            // grid barrier counter, zeroed before the launch
+    unsigned *err;            // [0] code, [1] aux
+    long long *pass_cycles;   // ring of per-pass durations (wall clock ticks), or null
+    long long *op_cycles;     // per-kind durations on block 0, or null
+    uint64_t spin_limit;      // barrier spin limit in wall clock ticks
+    uint32_t n_instr;
+    uint32_t n_passes;
+    uint32_t pass_cycles_cap;
+    uint32_t pass_base;
+};
+
+hipError_t launch_op(const sinter_instr &ins, uint32_t blocks, unsigned *err, hipStream_t s);
+hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s);
+hipError_t interp_max_blocks(int *blocks_per_cu);
+hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
+                        hipStream_t s);
+
+// host-side helpers (host.cpp)
+int set_error(int status, const char *fmt, ...);
+bool hip_ok(hipError_t e, const char *what);
+unsigned *op_err_cell();  // per-device error cell of the standalone op launches
+int validate_gemv(const sinter_gemv_args &a, const char **why);
+
+}  // namespace sinter

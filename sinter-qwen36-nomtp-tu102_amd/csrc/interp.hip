@@ -1,0 +1,198 @@
+// The interpreter spine for gfx950 and the standalone op / synthesis kernels.
+//
+// sinter_interp is one cooperative grid (one 256-thread workgroup per CU)
+// that walks the instruction array once per pass, crossing a grid barrier at
+// every BOUNDARY and dispatching every other instruction whose
+// [block_lo, block_hi) range holds the workgroup (core/interp.cu:39-146).
+// A launch runs n_passes passes back to back; the greedy-argmax epilogue of
+// the head GEMV advances the pass cell (token, pos) on device, so a greedy
+// decode of many tokens needs no host round trip between tokens.
+//
+// Error protocol (core/interp.cuh:36-56): an unknown kind is seen by every
+// workgroup at the same instruction, all return, no barrier is left half
+// arrived.  Ops raise into the error cell and return normally; the cell is
+// sampled after the pass-end barrier, uniformly.  A barrier wait that exceeds
+// the spin limit raises SINTER_E_BAD_KIND+16 (timeout) and returns, so a
+// broken program ends the kernel instead of hanging the device.
+#include <hip/hip_runtime.h>
+
+#include "internal.h"
+#include "gemv.h"
+#include "gdn.h"
+#include "attn.h"
+#include "synth.h"
+
+namespace sinter {
+
+__device__ __forceinline__ bool kind_wired(unsigned k) {
+    return k == SINTER_OP_NOP || k == SINTER_OP_BOUNDARY || k == SINTER_OP_GEMV ||
+           k == SINTER_OP_GDN_STEP || k == SINTER_OP_ATTN_DECODE;
+}
+
+__device__ __forceinline__ void dispatch(const sinter_instr &ins, char *lds, unsigned *err) {
+    switch (ins.kind) {
+    case SINTER_OP_GEMV: op_gemv(ins, lds, err); break;
+    case SINTER_OP_GDN_STEP: op_gdn_step(ins, lds, err); break;
+    case SINTER_OP_ATTN_DECODE: op_attn_decode(ins, lds, err); break;
+    default: break;
+    }
+}
+
+// Grid barrier over a monotonic counter (zeroed before the launch): every
+// workgroup release-arrives, one thread spins until epoch*gridDim arrivals,
+// then acquires.  The agent-scope release writes back this XCD's L2 and the
+// acquire invalidates L1/L2, so plain loads after the barrier observe every
+// store made before any workgroup's arrival.  Returns false on timeout.
+__device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned &epoch, uint64_t spin_limit_ticks,
+                                             unsigned *err) {
+    __syncthreads();
+    epoch += 1;
+    __shared__ unsigned timed_out;
+    if (threadIdx.x == 0) {
+        timed_out = 0;
+        fence_release_agent();
+        __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned target = epoch * gridDim.x;
+        const uint64_t t0 = wall_clock64();
+        while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (wall_clock64() - t0 > spin_limit_ticks) {
+                raise_error(err, SINTER_E_TIMEOUT_BARRIER, epoch);
+                timed_out = 1;
+                break;
+            }
+        }
+        fence_acquire_agent();
+    }
+    __syncthreads();
+    return timed_out == 0;
+}
+
+}  // namespace sinter
+
+using namespace sinter;
+
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    unsigned epoch = 0;
+    for (uint32_t pass = 0; pass < ctl.n_passes; ++pass) {
+        const uint64_t t0 = wall_clock64();
+        for (uint32_t i = 0; i < ctl.n_instr; ++i) {
+            const sinter_instr &ins = prog[i];
+            const unsigned kind = ins.kind;
+            if (kind == SINTER_OP_BOUNDARY) {
+                if (!grid_barrier(ctl.bar, epoch, ctl.spin_limit, ctl.err)) return;
+                continue;
+            }
+            if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
+                if (blockIdx.x == 0 && threadIdx.x == 0)
+                    raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
+                return;
+            }
+            if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
+                if (ctl.op_cycles && blockIdx.x == 0) {
+                    const uint64_t s = wall_clock64();
+                    dispatch(ins, lds, ctl.err);
+                    if (threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
+                } else {
+                    dispatch(ins, lds, ctl.err);
+                }
+            }
+        }
+        // pass epilogue: everyone finished, then a uniform error sample
+        if (!grid_barrier(ctl.bar, epoch, ctl.spin_limit, ctl.err)) return;
+        __shared__ unsigned e;
+        if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (blockIdx.x == 0 && threadIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
+            ctl.pass_cycles[(ctl.pass_base + pass) % ctl.pass_cycles_cap] = (long long)(wall_clock64() - t0);
+        if (e) return;
+    }
+}
+
+// One instruction over the whole (non-cooperative) grid: the standalone op
+// entry points.  Ops that need cross-block results use last-arriver counters,
+// never a grid barrier, so co-residency is not required here.
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_op_kernel(sinter_instr ins, unsigned *err) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    ins.block_lo = 0;
+    ins.block_hi = (uint16_t)gridDim.x;
+    dispatch(ins, lds, err);
+}
+
+// Synthetic tensor fill: one thread per 256-element group (weights) or per
+// element (f32 / f16 tensors).
+extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type, uint64_t n_units,
+                                               uint64_t seed, float a, float b) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_units) return;
+    if (kind == SINTER_SYN_WEIGHT || kind == SINTER_SYN_Q8_0_CFG1) {
+        const uint32_t gb = sx_group_bytes(type);
+        uint8_t tmp[1024];
+        sx_weight_group(seed, i, type, kind == SINTER_SYN_Q8_0_CFG1, tmp);
+        for (uint32_t k = 0; k < gb; k++) dst[i * gb + k] = tmp[k];
+    } else if (kind == SINTER_SYN_NORMAL) {
+        reinterpret_cast<float *>(dst)[i] = a + b * sx_normal(seed, i);
+    } else if (kind == SINTER_SYN_UNIFORM) {
+        reinterpret_cast<float *>(dst)[i] = a + (b - a) * sx_unit(seed, i);
+    } else if (kind == SINTER_SYN_NORMAL_F16) {
+        reinterpret_cast<uint16_t *>(dst)[i] = sx_f2h(b * sx_normal(seed, i));
+    }
+}
+
+// ----------------------------------------------------------------- launchers
+
+namespace sinter {
+
+hipError_t launch_op(const sinter_instr &ins, uint32_t blocks, unsigned *err, hipStream_t s) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)sinter_op_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), LDS_BYTES, s, ins, err);
+    return hipGetLastError();
+}
+
+hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)sinter_interp,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    InterpCtl c = ctl;
+    const sinter_instr *p = prog;
+    void *args[] = {(void *)&p, (void *)&c};
+    return hipLaunchCooperativeKernel((const void *)sinter_interp, dim3(blocks), dim3(BLOCK_THREADS), args,
+                                      LDS_BYTES, s);
+}
+
+hipError_t interp_max_blocks(int *blocks_per_cu) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)sinter_interp,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void *)sinter_interp,
+                                                        BLOCK_THREADS, LDS_BYTES);
+}
+
+hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
+                        hipStream_t s) {
+    if (n_units == 0) return hipSuccess;
+    const uint32_t tpb = 256;
+    const uint64_t nb = (n_units + tpb - 1) / tpb;
+    hipLaunchKernelGGL(sinter_synth_kernel, dim3((uint32_t)nb), dim3(tpb), 0, s, (uint8_t *)dst, kind, type,
+                       n_units, seed, a, b);
+    return hipGetLastError();
+}
+
+}  // namespace sinter

@@ -1,0 +1,501 @@
+// Model residency, state, and the pass program for one MI355X.
+//
+// Replaces, for this layout, the reference's harness residency/runtime
+// (k0/harness.cpp:402-566), its packer (harness.cpp:668-1060) and the offline
+// schedule compiler (k0/compile_schedule.py:358-703).  The whole model lives
+// on one GPU (15.5 GB Q4_K_M-mix or ~54 GB bf16 of 288 GB HBM3E); the dual-GPU
+// split and its exchange are gone.
+//
+// Pass program (per layer; B = grid barrier):
+//   GEMV  pro=RMSNORM(attn_norm) [EMBED on layer 0]
+//         GDN : qkv (EPI_CONV: conv+silu, conv state update) | z | alpha | beta
+//         ATTN: q|gate | k | v
+//   B
+//   GDN_STEP (l2norm, gates, delta rule)  |  ATTN_DECODE (norm+rope, KV append,
+//                                             split-K, merge, gate)
+//   B
+//   GEMV  pro=GATED(ssm_norm, z) for GDN / PLAIN for ATTN; ssm_out|attn_output, EPI_RESID -> H
+//   B
+//   GEMV  pro=RMSNORM(post_attention_norm); ffn_gate,ffn_up EPI_SWIGLU -> F
+//   B
+//   GEMV  pro=PLAIN; ffn_down EPI_RESID -> X
+//   B
+// then GEMV pro=RMSNORM(output_norm); output EPI_ARGMAX -> logits, token.
+// 5 barriers per layer (the reference schedule has 15) plus the pass-end one.
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+#include "synth.h"
+
+using namespace sinter;
+
+namespace {
+
+struct Tensor {
+    void *d = nullptr;
+    size_t bytes = 0;
+    int type = 0;
+    int64_t rows = 0, k = 0;
+};
+
+// slot numbering shared with oracle/oracle.h
+enum {
+    S_ATTN_NORM = 0, S_POST_NORM, S_FFN_GATE, S_FFN_UP, S_FFN_DOWN,
+    S_QKV = 5, S_Z, S_ALPHA, S_BETA, S_SSM_OUT, S_CONV_W, S_DT_BIAS, S_SSM_A, S_SSM_NORM,
+    S_WQ = 5, S_WK, S_WV, S_WO, S_Q_NORM, S_K_NORM,
+    NSLOT = 16
+};
+
+bool is_attn(const sinter_model_config &c, int il) {
+    return c.attn_every > 0 && (il % c.attn_every) == c.attn_every - 1;
+}
+
+}  // namespace
+
+struct sinter_model {
+    sinter_model_config cfg{};
+    int device = 0;
+    uint32_t blocks = 0;
+    sinter_host *host = nullptr;
+    hipStream_t stream = nullptr;
+    std::vector<std::array<Tensor, NSLOT>> W;
+    Tensor embd, onorm, output;
+    std::vector<std::array<Tensor, 2>> S;
+    float *X = nullptr, *H = nullptr, *qkv = nullptr, *z = nullptr, *al = nullptr, *be = nullptr, *o = nullptr;
+    float *ffn = nullptr, *qg = nullptr, *kk = nullptr, *vv = nullptr, *att = nullptr, *logits = nullptr;
+    double *part = nullptr;
+    unsigned *count = nullptr;
+    sinter_argmax_ws *ws = nullptr;
+    std::vector<sinter_instr> prog;
+    uint32_t n_boundaries = 0;
+    uint64_t weight_bytes = 0;
+    std::vector<void *> allocs;
+    uint64_t seed = 0;
+};
+
+namespace {
+
+void *dalloc(sinter_model *m, size_t bytes) {
+    void *p = nullptr;
+    // 256 B of slack: tile loads round the last row up to 16 bytes
+    const size_t sz = (bytes + 256 + 255) & ~(size_t)255;
+    if (hipMalloc(&p, sz) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, sz, m->stream) != hipSuccess) return nullptr;
+    m->allocs.push_back(p);
+    return p;
+}
+
+bool make_weight(sinter_model *m, Tensor &t, const char *name, int il, int type, int64_t rows, int64_t k) {
+    t.type = type;
+    t.rows = rows;
+    t.k = k;
+    t.bytes = sinter_row_bytes_dev(type, k) * (size_t)rows;
+    t.d = dalloc(m, t.bytes);
+    if (!t.d) return false;
+    m->weight_bytes += t.bytes;
+    return launch_synth(t.d, SINTER_SYN_WEIGHT, type, (uint64_t)rows * (uint64_t)(k / 256),
+                        sinter_seed(m->seed, name, il), 0.f, 0.f, m->stream) == hipSuccess;
+}
+
+bool make_vec(sinter_model *m, Tensor &t, const char *name, int il, int64_t n, int kind, float a, float b) {
+    t.type = SINTER_F32;
+    t.rows = 1;
+    t.k = n;
+    t.bytes = (size_t)n * 4;
+    t.d = dalloc(m, t.bytes);
+    if (!t.d) return false;
+    m->weight_bytes += t.bytes;
+    return launch_synth(t.d, kind, SINTER_F32, (uint64_t)n, sinter_seed(m->seed, name, il), a, b, m->stream) ==
+           hipSuccess;
+}
+
+sinter_instr mk_instr(uint16_t kind, uint32_t blocks, uint32_t dbg) {
+    sinter_instr in;
+    std::memset(&in, 0, sizeof in);
+    in.kind = kind;
+    in.block_lo = 0;
+    in.block_hi = (uint16_t)blocks;
+    in.dbg_node = dbg;
+    return in;
+}
+
+template <class T>
+void push(sinter_model *m, uint16_t kind, const T &args, uint32_t dbg) {
+    sinter_instr in = mk_instr(kind, m->blocks, dbg);
+    static_assert(sizeof(T) <= sizeof(in.payload), "payload");
+    std::memcpy(in.payload, &args, sizeof args);
+    m->prog.push_back(in);
+}
+
+void boundary(sinter_model *m) {
+    m->prog.push_back(mk_instr(SINTER_OP_BOUNDARY, m->blocks, 0));
+    m->n_boundaries++;
+}
+
+sinter_gemv_seg seg(const Tensor &w, float *y, int epi, const void *w2 = nullptr, float *aux = nullptr,
+                    int dconv = 0) {
+    sinter_gemv_seg s;
+    std::memset(&s, 0, sizeof s);
+    s.w = w.d;
+    s.w2 = w2;
+    s.y = y;
+    s.aux = aux;
+    s.rows = (uint32_t)w.rows;
+    s.type = (uint8_t)w.type;
+    s.epi = (uint8_t)epi;
+    s.dconv = (uint8_t)dconv;
+    return s;
+}
+
+void build_program(sinter_model *m) {
+    const sinter_model_config &c = m->cfg;
+    const int E = c.n_embd, D = c.gdn_d, HD = c.head_dim;
+    const sinter_pass_cell *pc = sinter_host_pass_cell(m->host);
+    m->prog.clear();
+    m->n_boundaries = 0;
+    int log2d = 0;
+    while ((1 << log2d) < D) log2d++;
+    for (int il = 0; il < c.n_layer; il++) {
+        const auto &w = m->W[il];
+        const bool at = is_attn(c, il);
+        const uint32_t dbg = (uint32_t)il * 8;
+        // 1. mixer input projections
+        sinter_gemv_args g1;
+        std::memset(&g1, 0, sizeof g1);
+        g1.K = (uint32_t)E;
+        g1.eps = c.eps;
+        g1.norm_w = (const float *)w[S_ATTN_NORM].d;
+        if (il == 0) {
+            g1.pro = SINTER_PRO_EMBED;
+            g1.aux = m->embd.d;
+            g1.aux_type = (uint8_t)m->embd.type;
+            g1.aux_rows = (uint32_t)m->embd.rows;
+            g1.token = &pc->token;
+            g1.x_out = m->X;
+        } else {
+            g1.pro = SINTER_PRO_RMSNORM;
+            g1.x = m->X;
+        }
+        if (at) {
+            g1.n_seg = 3;
+            g1.seg[0] = seg(w[S_WQ], m->qg, SINTER_EPI_STORE);
+            g1.seg[1] = seg(w[S_WK], m->kk, SINTER_EPI_STORE);
+            g1.seg[2] = seg(w[S_WV], m->vv, SINTER_EPI_STORE);
+        } else {
+            g1.n_seg = 4;
+            g1.seg[0] = seg(w[S_QKV], m->qkv, SINTER_EPI_CONV, w[S_CONV_W].d, (float *)m->S[il][0].d, c.conv_k);
+            g1.seg[1] = seg(w[S_Z], m->z, SINTER_EPI_STORE);
+            g1.seg[2] = seg(w[S_ALPHA], m->al, SINTER_EPI_STORE);
+            g1.seg[3] = seg(w[S_BETA], m->be, SINTER_EPI_STORE);
+        }
+        push(m, SINTER_OP_GEMV, g1, dbg + 0);
+        boundary(m);
+        // 2. recurrent / attention core
+        if (at) {
+            sinter_attn_args a;
+            std::memset(&a, 0, sizeof a);
+            a.qg = m->qg;
+            a.k = m->kk;
+            a.v = m->vv;
+            a.q_norm = (const float *)w[S_Q_NORM].d;
+            a.k_norm = (const float *)w[S_K_NORM].d;
+            a.kc = (uint16_t *)m->S[il][0].d;
+            a.vc = (uint16_t *)m->S[il][1].d;
+            a.part = m->part;
+            a.count = m->count;
+            a.out = m->att;
+            a.pass_cell = &pc->token;
+            a.nq = (uint32_t)c.attn_nq;
+            a.nkv = (uint32_t)c.attn_nkv;
+            a.hd = (uint32_t)HD;
+            a.rope_dims = (uint32_t)c.rope_dims;
+            a.n_ctx = (uint32_t)c.n_ctx;
+            a.n_chunks = std::max(1u, m->blocks / (uint32_t)c.attn_nkv);
+            a.theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
+            a.eps = c.eps;
+            a.scale = 1.0f / std::sqrt((float)HD);
+            push(m, SINTER_OP_ATTN_DECODE, a, dbg + 1);
+        } else {
+            sinter_gdn_args a;
+            std::memset(&a, 0, sizeof a);
+            a.qkv = m->qkv;
+            a.alpha = m->al;
+            a.beta = m->be;
+            a.dt_bias = (const float *)w[S_DT_BIAS].d;
+            a.ssm_a = (const float *)w[S_SSM_A].d;
+            a.state = (float *)m->S[il][1].d;
+            a.o = m->o;
+            a.hk = (uint32_t)c.gdn_hk;
+            a.hv = (uint32_t)c.gdn_hv;
+            a.d = (uint32_t)D;
+            a.cols = D >= 128 ? 16u : 8u;
+            a.eps = c.eps;
+            a.scale = 1.0f / std::sqrt((float)D);
+            push(m, SINTER_OP_GDN_STEP, a, dbg + 1);
+        }
+        boundary(m);
+        // 3. mixer output projection + residual: H = X + W_out . a
+        sinter_gemv_args g3;
+        std::memset(&g3, 0, sizeof g3);
+        g3.eps = c.eps;
+        g3.n_seg = 1;
+        if (at) {
+            g3.K = (uint32_t)(c.attn_nq * HD);
+            g3.pro = SINTER_PRO_PLAIN;
+            g3.x = m->att;
+            g3.seg[0] = seg(w[S_WO], m->H, SINTER_EPI_RESID, nullptr, m->X);
+        } else {
+            g3.K = (uint32_t)(c.gdn_hv * D);
+            g3.pro = SINTER_PRO_GATED;
+            g3.x = m->o;
+            g3.norm_w = (const float *)w[S_SSM_NORM].d;
+            g3.aux = m->z;
+            g3.gn_log2d = (uint8_t)log2d;
+            g3.seg[0] = seg(w[S_SSM_OUT], m->H, SINTER_EPI_RESID, nullptr, m->X);
+        }
+        push(m, SINTER_OP_GEMV, g3, dbg + 2);
+        boundary(m);
+        // 4. FFN gate/up with SwiGLU
+        sinter_gemv_args g4;
+        std::memset(&g4, 0, sizeof g4);
+        g4.K = (uint32_t)E;
+        g4.eps = c.eps;
+        g4.pro = SINTER_PRO_RMSNORM;
+        g4.x = m->H;
+        g4.norm_w = (const float *)w[S_POST_NORM].d;
+        g4.n_seg = 1;
+        g4.seg[0] = seg(w[S_FFN_GATE], m->ffn, SINTER_EPI_SWIGLU, w[S_FFN_UP].d);
+        push(m, SINTER_OP_GEMV, g4, dbg + 3);
+        boundary(m);
+        // 5. FFN down + residual: X = H + W_down . f
+        sinter_gemv_args g5;
+        std::memset(&g5, 0, sizeof g5);
+        g5.K = (uint32_t)c.n_ff;
+        g5.eps = c.eps;
+        g5.pro = SINTER_PRO_PLAIN;
+        g5.x = m->ffn;
+        g5.n_seg = 1;
+        g5.seg[0] = seg(w[S_FFN_DOWN], m->X, SINTER_EPI_RESID, nullptr, m->H);
+        push(m, SINTER_OP_GEMV, g5, dbg + 4);
+        boundary(m);
+    }
+    // head: final norm, logits, greedy argmax
+    sinter_gemv_args gh;
+    std::memset(&gh, 0, sizeof gh);
+    gh.K = (uint32_t)E;
+    gh.eps = c.eps;
+    gh.pro = SINTER_PRO_RMSNORM;
+    gh.x = m->X;
+    gh.norm_w = (const float *)m->onorm.d;
+    gh.epi_ws = m->ws;
+    gh.n_seg = 1;
+    gh.seg[0] = seg(m->output, m->logits, SINTER_EPI_ARGMAX);
+    push(m, SINTER_OP_GEMV, gh, (uint32_t)c.n_layer * 8);
+}
+
+int check_config(const sinter_model_config &c) {
+    if (c.n_layer < 1 || c.n_embd <= 0 || c.n_embd % 256 || c.n_ff % 256 || c.n_vocab < 1)
+        return set_error(SINTER_ERR_ARG, "config: n_layer/n_embd/n_ff/n_vocab");
+    if (c.gdn_hk < 1 || c.gdn_hv % c.gdn_hk || !(c.gdn_d == 64 || c.gdn_d == 128 || c.gdn_d == 256) || c.conv_k < 2 ||
+        c.conv_k > 8 || ((2 * c.gdn_hk + c.gdn_hv) * c.gdn_d) % 256 || (c.gdn_hv * c.gdn_d) % 256)
+        return set_error(SINTER_ERR_ARG, "config: gated-DeltaNet shape");
+    if (c.head_dim != 256 || c.attn_nkv < 1 || c.attn_nq % c.attn_nkv || c.attn_nq / c.attn_nkv > 8 ||
+        c.rope_dims > c.head_dim || c.rope_dims % 2 || c.n_ctx < 1)
+        return set_error(SINTER_ERR_ARG, "config: attention shape");
+    return SINTER_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void sinter_model_destroy(sinter_model *m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->host) sinter_host_destroy(m->host);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->ws) sinter_argmax_ws_destroy(m->ws);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks,
+                        sinter_model **out) {
+    if (!cfg || !out) return set_error(SINTER_ERR_ARG, "model: null argument");
+    *out = nullptr;
+    int rc = check_config(*cfg);
+    if (rc) return rc;
+    sinter_model *m = new sinter_model();
+    m->cfg = *cfg;
+    m->device = device;
+    m->seed = seed;
+    auto fail = [&](int st) { sinter_model_destroy(m); return st; };
+    if ((rc = sinter_host_init(&m->host, device, 1024)) != SINTER_OK) return fail(rc);
+    uint32_t hb = 0;
+    sinter_host_grid(m->host, &hb, nullptr, nullptr);
+    m->blocks = blocks ? std::min(blocks, hb) : hb;
+    if ((rc = sinter_host_set_grid(m->host, m->blocks)) != SINTER_OK) return fail(rc);
+    if (!hip_ok(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "model stream")) return fail(SINTER_ERR_HIP);
+    const sinter_model_config &c = m->cfg;
+    const int E = c.n_embd, F = c.n_ff, D = c.gdn_d, HK = c.gdn_hk, HV = c.gdn_hv;
+    const int C = (2 * HK + HV) * D, VD = HV * D;
+    const int NQ = c.attn_nq, NKV = c.attn_nkv, HD = c.head_dim, RW = NKV * HD;
+    m->W.resize(c.n_layer);
+    m->S.resize(c.n_layer);
+    bool ok = true;
+    for (int il = 0; il < c.n_layer && ok; il++) {
+        auto &w = m->W[il];
+        ok = ok && make_vec(m, w[S_ATTN_NORM], "attn_norm", il, E, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+        ok = ok && make_vec(m, w[S_POST_NORM], "post_attention_norm", il, E, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+        ok = ok && make_weight(m, w[S_FFN_GATE], "ffn_gate", il, c.t_default, F, E);
+        ok = ok && make_weight(m, w[S_FFN_UP], "ffn_up", il, c.t_default, F, E);
+        ok = ok && make_weight(m, w[S_FFN_DOWN], "ffn_down", il, c.t_ffn_down, E, F);
+        if (is_attn(c, il)) {
+            ok = ok && make_weight(m, w[S_WQ], "attn_q", il, c.t_default, (int64_t)NQ * 2 * HD, E);
+            ok = ok && make_weight(m, w[S_WK], "attn_k", il, c.t_default, RW, E);
+            ok = ok && make_weight(m, w[S_WV], "attn_v", il, c.t_attn_v, RW, E);
+            ok = ok && make_weight(m, w[S_WO], "attn_output", il, c.t_default, E, (int64_t)NQ * HD);
+            ok = ok && make_vec(m, w[S_Q_NORM], "attn_q_norm", il, HD, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+            ok = ok && make_vec(m, w[S_K_NORM], "attn_k_norm", il, HD, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+            Tensor &K = m->S[il][0], &V = m->S[il][1];
+            K.bytes = V.bytes = (size_t)c.n_ctx * RW * 2;
+            K.type = V.type = SINTER_F16;
+            ok = ok && (K.d = dalloc(m, K.bytes)) && (V.d = dalloc(m, V.bytes));
+        } else {
+            ok = ok && make_weight(m, w[S_QKV], "attn_qkv", il, c.t_default, C, E);
+            ok = ok && make_weight(m, w[S_Z], "attn_gate", il, c.t_default, VD, E);
+            ok = ok && make_weight(m, w[S_ALPHA], "ssm_alpha", il, c.t_default, HV, E);
+            ok = ok && make_weight(m, w[S_BETA], "ssm_beta", il, c.t_default, HV, E);
+            ok = ok && make_weight(m, w[S_SSM_OUT], "ssm_out", il, c.t_default, E, VD);
+            ok = ok && make_vec(m, w[S_CONV_W], "ssm_conv1d", il, (int64_t)C * c.conv_k, SINTER_SYN_UNIFORM, -0.5f, 0.5f);
+            ok = ok && make_vec(m, w[S_DT_BIAS], "ssm_dt_bias", il, HV, SINTER_SYN_UNIFORM, -6.9f, -2.3f);
+            ok = ok && make_vec(m, w[S_SSM_A], "ssm_a", il, HV, SINTER_SYN_UNIFORM, -16.0f, -1.0f);
+            ok = ok && make_vec(m, w[S_SSM_NORM], "ssm_norm", il, D, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+            Tensor &cs = m->S[il][0], &ss = m->S[il][1];
+            cs.bytes = (size_t)C * (c.conv_k - 1) * 4;
+            ss.bytes = (size_t)HV * D * D * 4;
+            cs.type = ss.type = SINTER_F32;
+            ok = ok && (cs.d = dalloc(m, cs.bytes)) && (ss.d = dalloc(m, ss.bytes));
+        }
+    }
+    ok = ok && make_weight(m, m->embd, "token_embd", -1, c.t_embd, c.n_vocab, E);
+    ok = ok && make_vec(m, m->onorm, "output_norm", -1, E, SINTER_SYN_NORMAL, 1.0f, 0.02f);
+    ok = ok && make_weight(m, m->output, "output", -1, c.t_output, c.n_vocab, E);
+    auto fa = [&](size_t n) { return (float *)dalloc(m, n * 4); };
+    ok = ok && (m->X = fa(E)) && (m->H = fa(E)) && (m->qkv = fa(C)) && (m->z = fa(VD)) && (m->al = fa(HV)) &&
+         (m->be = fa(HV)) && (m->o = fa(VD)) && (m->ffn = fa(F)) && (m->qg = fa((size_t)NQ * 2 * HD)) &&
+         (m->kk = fa(RW)) && (m->vv = fa(RW)) && (m->att = fa((size_t)NQ * HD)) && (m->logits = fa(c.n_vocab));
+    const uint32_t chunks = std::max(1u, m->blocks / (uint32_t)NKV);
+    ok = ok && (m->part = (double *)dalloc(m, (size_t)NKV * chunks * (NQ / NKV) * (HD + 2) * 8));
+    ok = ok && (m->count = (unsigned *)dalloc(m, 256));
+    if (!ok) return fail(set_error(SINTER_ERR_NOMEM, "model: device allocation or synthesis failed"));
+    if (!hip_ok(hipStreamSynchronize(m->stream), "model synthesis")) return fail(SINTER_ERR_HIP);
+    uint32_t hcap = 0;
+    int32_t *hist = sinter_host_history(m->host, &hcap);
+    if ((rc = sinter_argmax_ws_create(m->blocks, &sinter_host_pass_cell(m->host)->token, hist, hcap, &m->ws)))
+        return fail(rc);
+    build_program(m);
+    if ((rc = sinter_host_upload(m->host, m->prog.data(), (uint32_t)m->prog.size(), m->n_boundaries + 1)))
+        return fail(rc);
+    if ((rc = sinter_host_launch(m->host))) return fail(rc);
+    *out = m;
+    return SINTER_OK;
+}
+
+int sinter_model_synth_context(sinter_model *m, int32_t n_past, uint64_t seed) {
+    if (!m || n_past < 0 || n_past > m->cfg.n_ctx) return set_error(SINTER_ERR_ARG, "synth_context: args");
+    const sinter_model_config &c = m->cfg;
+    const int RW = c.attn_nkv * c.head_dim;
+    for (int il = 0; il < c.n_layer; il++) {
+        hipError_t e = hipSuccess;
+        if (is_attn(c, il)) {
+            e = launch_synth(m->S[il][0].d, SINTER_SYN_NORMAL_F16, 0, (uint64_t)n_past * RW,
+                             sinter_seed(seed, "cache_k", il), 0.f, 1.0f, m->stream);
+            if (e == hipSuccess)
+                e = launch_synth(m->S[il][1].d, SINTER_SYN_NORMAL_F16, 0, (uint64_t)n_past * RW,
+                                 sinter_seed(seed, "cache_v", il), 0.f, 1.0f, m->stream);
+        } else {
+            e = launch_synth(m->S[il][0].d, SINTER_SYN_NORMAL, 0, m->S[il][0].bytes / 4,
+                             sinter_seed(seed, "conv_state", il), 0.f, 1.0f, m->stream);
+            if (e == hipSuccess)
+                e = launch_synth(m->S[il][1].d, SINTER_SYN_NORMAL, 0, m->S[il][1].bytes / 4,
+                                 sinter_seed(seed, "ssm_state", il), 0.f, 0.1f, m->stream);
+        }
+        if (!hip_ok(e, "context synthesis")) return SINTER_ERR_HIP;
+    }
+    return hip_ok(hipStreamSynchronize(m->stream), "context synthesis") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+int sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logits_host, int32_t *next_token) {
+    if (!m || pos < 0 || pos >= m->cfg.n_ctx || token < 0 || token >= m->cfg.n_vocab)
+        return set_error(SINTER_ERR_ARG, "decode: token/pos out of range");
+    int rc = sinter_host_set_pos(m->host, pos);
+    if (rc) return rc;
+    const int rs = sinter_host_run_pass(m->host, token, 120000.0);
+    if (rs != SINTER_RUN_OK) return rs == SINTER_RUN_TIMEOUT ? SINTER_ERR_TIMEOUT : SINTER_ERR_DEVICE;
+    if (logits_host &&
+        !hip_ok(hipMemcpy(logits_host, m->logits, (size_t)m->cfg.n_vocab * 4, hipMemcpyDeviceToHost), "logits"))
+        return SINTER_ERR_HIP;
+    if (next_token &&
+        !hip_ok(hipMemcpy(next_token, &sinter_host_pass_cell(m->host)->token, 4, hipMemcpyDeviceToHost), "token"))
+        return SINTER_ERR_HIP;
+    return SINTER_OK;
+}
+
+int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n, int32_t *tokens_out) {
+    if (!m || pos < 0 || (int64_t)pos + n > m->cfg.n_ctx || token < 0 || token >= m->cfg.n_vocab)
+        return set_error(SINTER_ERR_ARG, "greedy: token/pos/n out of range");
+    int rc = sinter_host_set_pos(m->host, pos);
+    if (rc) return rc;
+    const int rs = sinter_host_run_passes(m->host, token, n, tokens_out, 600000.0);
+    if (rs != SINTER_RUN_OK) return rs == SINTER_RUN_TIMEOUT ? SINTER_ERR_TIMEOUT : SINTER_ERR_DEVICE;
+    return SINTER_OK;
+}
+
+int sinter_model_tensor_info(sinter_model *m, int64_t layer, int slot, void **dev_ptr, size_t *bytes, int *type) {
+    if (!m || slot < 0 || slot >= NSLOT || layer < 0 || layer > m->cfg.n_layer) return set_error(SINTER_ERR_ARG, "slot");
+    const Tensor *t = nullptr;
+    if (layer == m->cfg.n_layer) {
+        t = slot == 0 ? &m->embd : slot == 1 ? &m->onorm : slot == 2 ? &m->output : nullptr;
+    } else {
+        t = &m->W[layer][slot];
+    }
+    if (!t) return set_error(SINTER_ERR_ARG, "slot");
+    if (dev_ptr) *dev_ptr = t->d;
+    if (bytes) *bytes = t->d ? t->bytes : 0;
+    if (type) *type = t->type;
+    return SINTER_OK;
+}
+
+int sinter_model_state_info(sinter_model *m, int64_t layer, int slot, void **dev_ptr, size_t *bytes) {
+    if (!m || layer < 0 || layer >= m->cfg.n_layer || slot < 0 || slot > 1) return set_error(SINTER_ERR_ARG, "state");
+    if (dev_ptr) *dev_ptr = m->S[layer][slot].d;
+    if (bytes) *bytes = m->S[layer][slot].bytes;
+    return SINTER_OK;
+}
+
+int sinter_model_copy(sinter_model *m, void *dst, const void *src, size_t bytes, int dir) {
+    if (!m || !dst || !src) return set_error(SINTER_ERR_ARG, "copy");
+    const hipMemcpyKind k = dir == 0 ? hipMemcpyDeviceToHost : dir == 1 ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+    return hip_ok(hipMemcpy(dst, src, bytes, k), "copy") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+int sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr, uint32_t *n_boundaries,
+                      uint32_t *blocks) {
+    if (!m) return set_error(SINTER_ERR_ARG, "null model");
+    if (weight_bytes) *weight_bytes = m->weight_bytes;
+    if (n_instr) *n_instr = (uint32_t)m->prog.size();
+    if (n_boundaries) *n_boundaries = m->n_boundaries + 1;
+    if (blocks) *blocks = m->blocks;
+    return SINTER_OK;
+}
+
+sinter_host *sinter_model_host(sinter_model *m) { return m ? m->host : nullptr; }
+
+}  // extern "C"

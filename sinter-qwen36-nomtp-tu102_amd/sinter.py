@@ -1,0 +1,232 @@
+"""ctypes binding of libsinter.so (include/sinter.h).
+
+Host-side mirror of the C ABI for tests, smoke() and bench.py.  The HIP
+library is the product: loading fails loudly when libsinter.so is missing,
+and nothing here falls back to a CPU path.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsinter.so")
+
+# sinter_type
+F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 8, 12, 14, 15, 30
+# ops
+OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range(6)
+PRO_PLAIN, PRO_RMSNORM, PRO_GATED, PRO_EMBED = range(4)
+EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV = range(5)
+SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16 = range(5)
+OK, ERR_ARG, ERR_HIP, ERR_DEVICE, ERR_TIMEOUT, ERR_STATE, ERR_NOMEM = 0, -1, -2, -3, -4, -5, -6
+RUN_OK, RUN_ERR, RUN_TIMEOUT = 0, 1, 2
+E_NONE, E_BAD_KIND, E_UNWIRED_KIND, E_BAD_SHAPE, E_ATTN_SENTINEL, E_TIMEOUT_BARRIER = range(6)
+
+BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+BLOCK_ELEMS = {F32: 1, F16: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+
+
+def row_bytes(t, k):
+    return (k // BLOCK_ELEMS[t]) * BLOCK_BYTES[t]
+
+
+vp = C.c_void_p
+
+
+class Instr(C.Structure):
+    _fields_ = [("kind", C.c_uint16), ("block_lo", C.c_uint16), ("block_hi", C.c_uint16),
+                ("flags", C.c_uint16), ("dbg_node", C.c_uint32), ("_pad", C.c_uint32),
+                ("payload", C.c_ubyte * 240)]
+
+
+class GemvSeg(C.Structure):
+    _fields_ = [("w", vp), ("w2", vp), ("y", vp), ("aux", vp), ("rows", C.c_uint32),
+                ("type", C.c_uint8), ("epi", C.c_uint8), ("dconv", C.c_uint8), ("_pad", C.c_uint8)]
+
+
+class GemvArgs(C.Structure):
+    _fields_ = [("x", vp), ("norm_w", vp), ("aux", vp), ("token", vp), ("x_out", vp), ("epi_ws", vp),
+                ("K", C.c_uint32), ("eps", C.c_float), ("pro", C.c_uint8), ("n_seg", C.c_uint8),
+                ("aux_type", C.c_uint8), ("gn_log2d", C.c_uint8), ("aux_rows", C.c_uint32),
+                ("seg", GemvSeg * 4)]
+
+
+class GdnArgs(C.Structure):
+    _fields_ = [("qkv", vp), ("alpha", vp), ("beta", vp), ("dt_bias", vp), ("ssm_a", vp), ("state", vp),
+                ("o", vp), ("hk", C.c_uint32), ("hv", C.c_uint32), ("d", C.c_uint32), ("cols", C.c_uint32),
+                ("eps", C.c_float), ("scale", C.c_float)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [("qg", vp), ("k", vp), ("v", vp), ("q_norm", vp), ("k_norm", vp), ("kc", vp), ("vc", vp),
+                ("part", vp), ("count", vp), ("out", vp), ("pass_cell", vp),
+                ("nq", C.c_uint32), ("nkv", C.c_uint32), ("hd", C.c_uint32), ("rope_dims", C.c_uint32),
+                ("n_ctx", C.c_uint32), ("n_chunks", C.c_uint32), ("theta_scale", C.c_float),
+                ("eps", C.c_float), ("scale", C.c_float), ("_pad", C.c_uint32)]
+
+
+class PassCell(C.Structure):
+    _fields_ = [("token", C.c_int32), ("pos", C.c_int32), ("steps", C.c_int32), ("_pad", C.c_int32)]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("n_layer", C.c_int32), ("attn_every", C.c_int32), ("n_embd", C.c_int32), ("n_ff", C.c_int32),
+                ("n_vocab", C.c_int32), ("gdn_hk", C.c_int32), ("gdn_hv", C.c_int32), ("gdn_d", C.c_int32),
+                ("conv_k", C.c_int32), ("attn_nq", C.c_int32), ("attn_nkv", C.c_int32),
+                ("head_dim", C.c_int32), ("rope_dims", C.c_int32), ("rope_base", C.c_float),
+                ("eps", C.c_float), ("n_ctx", C.c_int32), ("t_default", C.c_int32), ("t_attn_v", C.c_int32),
+                ("t_ffn_down", C.c_int32), ("t_output", C.c_int32), ("t_embd", C.c_int32)]
+
+
+assert C.sizeof(Instr) == 256 and C.sizeof(GemvSeg) == 40
+assert C.sizeof(GemvArgs) == 224 and C.sizeof(GdnArgs) == 80 and C.sizeof(AttnArgs) == 128
+
+
+def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64):
+    """The 27B-shaped hybrid: 48 gated-DeltaNet + 16 attention layers."""
+    if quant == "q4_k_m":
+        td, tv, tdown, tout, temb = Q4_K, Q6_K, Q6_K, Q6_K, Q4_K
+    elif quant == "bf16":
+        td = tv = tdown = tout = temb = BF16
+    else:
+        raise ValueError(quant)
+    return ModelConfig(n_layer=n_layer, attn_every=4, n_embd=5120, n_ff=17408, n_vocab=151936,
+                       gdn_hk=16, gdn_hv=32, gdn_d=128, conv_k=4, attn_nq=24, attn_nkv=4, head_dim=256,
+                       rope_dims=64, rope_base=1e7, eps=1e-6, n_ctx=n_ctx, t_default=td, t_attn_v=tv,
+                       t_ffn_down=tdown, t_output=tout, t_embd=temb)
+
+
+_lib = None
+
+
+def lib():
+    """Load libsinter.so; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError("libsinter.so is not built (run __graft_entry__.build()); "
+                           "there is no CPU fallback")
+    L = C.CDLL(LIB_PATH)
+    I, U32, I64, U64 = C.c_int, C.c_uint32, C.c_int64, C.c_uint64
+    sig = {
+        "sinter_last_error": (C.c_char_p, []),
+        "sinter_abi_version": (I, []),
+        "sinter_row_bytes": (C.c_size_t, [I, I64]),
+        "sinter_op_gemv": (I, [C.POINTER(GemvArgs), U32, vp]),
+        "sinter_op_gdn_step": (I, [C.POINTER(GdnArgs), U32, vp]),
+        "sinter_op_attn_decode": (I, [C.POINTER(AttnArgs), U32, vp]),
+        "sinter_op_error": (I, [C.POINTER(U32), C.POINTER(U32)]),
+        "sinter_argmax_ws_create": (I, [U32, vp, vp, U32, C.POINTER(vp)]),
+        "sinter_argmax_ws_destroy": (None, [vp]),
+        "sinter_synth": (I, [I, vp, I, I, I64, I64, U64, C.c_float, C.c_float, vp]),
+        "sinter_seed": (U64, [U64, C.c_char_p, I64]),
+        "sinter_host_init": (I, [C.POINTER(vp), I, C.c_uint]),
+        "sinter_host_upload": (I, [vp, C.POINTER(Instr), U32, U32]),
+        "sinter_host_launch": (I, [vp]),
+        "sinter_host_run_pass": (I, [vp, C.c_int32, C.c_double]),
+        "sinter_host_run_passes": (I, [vp, C.c_int32, U32, C.POINTER(C.c_int32), C.c_double]),
+        "sinter_host_shutdown": (I, [vp, C.c_double]),
+        "sinter_host_destroy": (None, [vp]),
+        "sinter_host_read_pass_cycles": (I, [vp, C.POINTER(C.c_longlong), C.c_uint]),
+        "sinter_host_reset_op_cycles": (I, [vp]),
+        "sinter_host_read_op_cycles": (I, [vp, C.POINTER(C.c_longlong), C.c_uint]),
+        "sinter_host_pass_cell": (vp, [vp]),
+        "sinter_host_history": (vp, [vp, C.POINTER(U32)]),
+        "sinter_host_error": (I, [vp, C.POINTER(U32), C.POINTER(U32)]),
+        "sinter_host_grid": (I, [vp, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
+        "sinter_host_set_pos": (I, [vp, C.c_int32]),
+        "sinter_host_set_grid": (I, [vp, U32]),
+        "sinter_host_last_launch_ms": (C.c_float, [vp]),
+        "sinter_model_create": (I, [C.POINTER(ModelConfig), I, U64, U32, C.POINTER(vp)]),
+        "sinter_model_destroy": (None, [vp]),
+        "sinter_model_decode": (I, [vp, C.c_int32, C.c_int32, vp, C.POINTER(C.c_int32)]),
+        "sinter_model_greedy": (I, [vp, C.c_int32, C.c_int32, U32, C.POINTER(C.c_int32)]),
+        "sinter_model_synth_context": (I, [vp, C.c_int32, U64]),
+        "sinter_model_tensor_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t), C.POINTER(I)]),
+        "sinter_model_state_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t)]),
+        "sinter_model_copy": (I, [vp, vp, vp, C.c_size_t, I]),
+        "sinter_model_info": (I, [vp, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
+        "sinter_model_host": (vp, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+class SinterError(RuntimeError):
+    pass
+
+
+def check(rc, what=""):
+    if rc != 0:
+        msg = lib().sinter_last_error()
+        raise SinterError(f"{what}: status {rc}: {msg.decode() if msg else ''}")
+    return rc
+
+
+def op_error():
+    code, aux = C.c_uint32(0), C.c_uint32(0)
+    check(lib().sinter_op_error(C.byref(code), C.byref(aux)), "op_error")
+    return code.value, aux.value
+
+
+class Model:
+    """Owner of a sinter_model handle."""
+
+    def __init__(self, cfg, seed=1, device=0, blocks=0):
+        self.cfg = cfg
+        h = vp()
+        check(lib().sinter_model_create(C.byref(cfg), device, seed, blocks, C.byref(h)), "model_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().sinter_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self):
+        wb, ni, nb, bl = C.c_uint64(), C.c_uint32(), C.c_uint32(), C.c_uint32()
+        check(lib().sinter_model_info(self.h, C.byref(wb), C.byref(ni), C.byref(nb), C.byref(bl)), "info")
+        return {"weight_bytes": wb.value, "n_instr": ni.value, "n_boundaries": nb.value, "blocks": bl.value}
+
+    def synth_context(self, n_past, seed):
+        check(lib().sinter_model_synth_context(self.h, n_past, seed), "synth_context")
+
+    def decode(self, token, pos, logits=None):
+        nt = C.c_int32()
+        ptr = logits.ctypes.data if logits is not None else None
+        check(lib().sinter_model_decode(self.h, token, pos, ptr, C.byref(nt)), "decode")
+        return nt.value
+
+    def greedy(self, token, pos, n):
+        out = (C.c_int32 * n)()
+        check(lib().sinter_model_greedy(self.h, token, pos, n, out), "greedy")
+        return list(out)
+
+    def tensor(self, layer, slot):
+        p, nb, t = vp(), C.c_size_t(), C.c_int()
+        check(lib().sinter_model_tensor_info(self.h, layer, slot, C.byref(p), C.byref(nb), C.byref(t)), "tensor")
+        return p.value, nb.value, t.value
+
+    def state(self, layer, slot):
+        p, nb = vp(), C.c_size_t()
+        check(lib().sinter_model_state_info(self.h, layer, slot, C.byref(p), C.byref(nb)), "state")
+        return p.value, nb.value
+
+    def d2h(self, dst_np, src_dev, nbytes):
+        check(lib().sinter_model_copy(self.h, dst_np.ctypes.data, src_dev, nbytes, 0), "copy d2h")
+
+    def h2d(self, dst_dev, src_np, nbytes):
+        check(lib().sinter_model_copy(self.h, dst_dev, src_np.ctypes.data, nbytes, 1), "copy h2d")
+
+    def host(self):
+        return lib().sinter_model_host(self.h)

@@ -1,0 +1,129 @@
+"""The C-ABI library loads and exports every declared entry point; host-side
+logic that runs without a GPU (argument validation, synthetic data)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sinter.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"\b(sinter_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_every_declared_symbol_is_exported(sn):
+    lib = sn.lib()
+    names = declared_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", sn.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (sinter_[a-z0-9_]+)", out))
+    assert set(names) <= exported
+
+
+def test_abi_version_and_struct_layout(sn, tmp_path):
+    assert sn.lib().sinter_abi_version() == 1
+    src = tmp_path / "sz.c"
+    src.write_text('#include "sinter.h"\n#include <stdio.h>\n#include <stddef.h>\nint main(void){printf("%zu %zu %zu %zu %zu %zu %zu\\n",'
+                   'sizeof(sinter_instr),sizeof(sinter_gemv_seg),sizeof(sinter_gemv_args),sizeof(sinter_gdn_args),'
+                   'sizeof(sinter_attn_args),sizeof(sinter_model_config),offsetof(sinter_gemv_args,seg));return 0;}\n')
+    exe = tmp_path / "sz"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
+    assert got == [C.sizeof(sn.Instr), C.sizeof(sn.GemvSeg), C.sizeof(sn.GemvArgs), C.sizeof(sn.GdnArgs),
+                   C.sizeof(sn.AttnArgs), C.sizeof(sn.ModelConfig), sn.GemvArgs.seg.offset]
+
+
+def test_row_bytes(sn):
+    L = sn.lib()
+    assert L.sinter_row_bytes(sn.Q4_K, 5120) == 2880
+    assert L.sinter_row_bytes(sn.Q6_K, 5120) == 4200
+    assert L.sinter_row_bytes(sn.Q6_K, 17408) == 14280
+    assert L.sinter_row_bytes(sn.Q8_0, 5120) == 5440
+    assert L.sinter_row_bytes(sn.BF16, 5120) == 10240
+
+
+def test_gemv_argument_validation_rejects_before_launch(sn):
+    """Shapes the kernel does not support are refused on the host with
+    SINTER_ERR_ARG and a message; no device call is made."""
+    L = sn.lib()
+    a = sn.GemvArgs()
+    a.K = 5000                       # not a multiple of 256
+    a.n_seg = 1
+    a.pro = sn.PRO_PLAIN
+    a.x = 16
+    a.seg[0].w = 256
+    a.seg[0].y = 512
+    a.seg[0].rows = 4
+    a.seg[0].type = sn.Q4_K
+    assert L.sinter_op_gemv(C.byref(a), 4, None) == sn.ERR_ARG
+    assert b"multiple of 256" in L.sinter_last_error()
+    a.K = 5120
+    a.seg[0].w = 258                 # unaligned weights
+    assert L.sinter_op_gemv(C.byref(a), 4, None) == sn.ERR_ARG
+    a.seg[0].w = 256
+    a.seg[1].type = sn.Q8_0          # mixed vec_dot types
+    a.seg[1].w = 256
+    a.seg[1].y = 512
+    a.n_seg = 2
+    assert L.sinter_op_gemv(C.byref(a), 4, None) == sn.ERR_ARG
+    assert b"vec_dot" in L.sinter_last_error()
+    a.n_seg = 1
+    a.K = 65536                      # activation does not fit the LDS buffer
+    assert L.sinter_op_gemv(C.byref(a), 4, None) == sn.ERR_ARG
+    g = sn.GdnArgs()
+    assert L.sinter_op_gdn_step(C.byref(g), 4, None) == sn.ERR_ARG
+    t = sn.AttnArgs()
+    assert L.sinter_op_attn_decode(C.byref(t), 4, None) == sn.ERR_ARG
+
+
+def test_model_config_validation(sn):
+    L = sn.lib()
+    cfg = sn.qwen36_27b_config()
+    cfg.head_dim = 128               # attention op supports head_dim 256
+    h = C.c_void_p()
+    assert L.sinter_model_create(C.byref(cfg), 0, 1, 0, C.byref(h)) == sn.ERR_ARG
+
+
+def test_host_synth_is_deterministic_and_scaled(sn, orc):
+    L = sn.lib()
+    for t, std in ((sn.Q4_K, 0.02), (sn.Q6_K, 0.02), (sn.Q8_0, 0.02), (sn.BF16, 0.02)):
+        n = sn.row_bytes(t, 5120) * 64
+        a = np.zeros(n, np.uint8)
+        b = np.zeros(n, np.uint8)
+        assert L.sinter_synth(0, a.ctypes.data, sn.SYN_WEIGHT, t, 64, 5120, 77, 0, 0, None) == 0
+        assert L.sinter_synth(0, b.ctypes.data, sn.SYN_WEIGHT, t, 64, 5120, 77, 0, 0, None) == 0
+        assert np.array_equal(a, b)
+        rb = sn.row_bytes(t, 5120)
+        vals = np.concatenate([orc.dequant(t, a[r * rb:(r + 1) * rb], 5120) for r in range(64)])
+        assert abs(vals.mean()) < 0.15 * std and 0.6 * std < vals.std() < 1.6 * std, (t, vals.mean(), vals.std())
+    x = np.zeros(100000, np.float32)
+    assert L.sinter_synth(0, x.ctypes.data, sn.SYN_NORMAL, 0, 1, x.size, 5, 1.0, 0.5, None) == 0
+    assert abs(x.mean() - 1.0) < 0.01 and abs(x.std() - 0.5) < 0.01
+    assert L.sinter_synth(0, x.ctypes.data, sn.SYN_UNIFORM, 0, 1, x.size, 5, -2.0, 3.0, None) == 0
+    assert x.min() >= -2.0 and x.max() < 3.0 and abs(x.mean() - 0.5) < 0.05
+    s1 = L.sinter_seed(1, b"ffn_up", 3)
+    assert s1 != L.sinter_seed(1, b"ffn_up", 4) and s1 != L.sinter_seed(1, b"ffn_gate", 3)
+    assert s1 == L.sinter_seed(1, b"ffn_up", 3)
+
+
+def test_cfg1_q8_0_synth_matches_config(sn, orc):
+    """config 1: int8 codes uniform in [-127,127], f16 scale |N(0,0.02)|"""
+    L = sn.lib()
+    rows, k = 64, 5120
+    w = np.zeros(sn.row_bytes(sn.Q8_0, k) * rows, np.uint8)
+    assert L.sinter_synth(0, w.ctypes.data, sn.SYN_Q8_0_CFG1, sn.Q8_0, rows, k, 9, 0, 0, None) == 0
+    blk = w.reshape(-1, 34)
+    d = blk[:, :2].copy().view(np.float16)[:, 0].astype(np.float64)
+    q = blk[:, 2:].view(np.int8).astype(np.int64)
+    assert d.min() >= 0 and abs(d.mean() - 0.02 * np.sqrt(2 / np.pi)) < 0.002
+    assert q.min() == -127 and q.max() == 127 and abs(q.mean()) < 0.5

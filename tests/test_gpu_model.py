@@ -1,0 +1,93 @@
+"""End-to-end decode on the GPU interpreter vs the CPU oracle.
+
+The model is created through the C ABI (weights synthesised on device),
+then mirrored to host memory for the oracle, so both sides run the same
+pass on the same bytes.  Greedy token ids must be identical; logits are
+compared element-wise (bit-exact except for fp64 fold-order effects).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def small_config(sn, n_layer=4, n_ctx=512, quant="q4_k_m"):
+    c = sn.qwen36_27b_config(n_ctx=n_ctx, quant=quant, n_layer=n_layer)
+    c.n_embd, c.n_ff, c.n_vocab = 1024, 2048, 3000
+    c.gdn_hk, c.gdn_hv = 2, 4
+    c.attn_nq, c.attn_nkv = 8, 2
+    return c
+
+
+def compare_logits(got, ref):
+    ulp = np.abs(np.spacing(ref))
+    bad = np.abs(got - ref) > 4 * ulp
+    assert bad.mean() < 1e-3, (bad.mean(), np.abs(got - ref).max())
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel < 1e-5, rel
+
+
+@pytest.mark.parametrize("quant", ["q4_k_m", "bf16"])
+def test_small_model_decode_matches_oracle(sn, orc, torch_gpu, quant):
+    cfg = small_config(sn, quant=quant)
+    print(f"small model {quant}: create", flush=True)
+    m = sn.Model(cfg, seed=11)
+    try:
+        m.synth_context(40, seed=12)
+        mirror = orc.ModelMirror(m)
+        info = m.info()
+        assert info["n_boundaries"] == 5 * cfg.n_layer + 1
+        tok, pos = 17, 40
+        for step in range(6):
+            logits = np.zeros(cfg.n_vocab, np.float32)
+            nxt = m.decode(tok, pos, logits)
+            rtok, rlog = mirror.step(tok, pos)
+            print(f"step {step}: gpu {nxt} oracle {rtok}", flush=True)
+            compare_logits(logits, rlog)
+            assert nxt == rtok == int(np.argmax(rlog))
+            tok, pos = nxt, pos + 1
+    finally:
+        m.close()
+
+
+def test_greedy_multi_pass_equals_single_passes(sn, orc, torch_gpu):
+    cfg = small_config(sn, n_layer=8)
+    m = sn.Model(cfg, seed=21)
+    try:
+        m.synth_context(100, seed=22)
+        mirror = orc.ModelMirror(m)
+        toks = m.greedy(5, 100, 12)        # one launch, 12 passes
+        ref = []
+        tok = 5
+        for i in range(12):
+            tok, _ = mirror.step(tok, 100 + i)
+            ref.append(tok)
+        assert toks == ref
+    finally:
+        m.close()
+
+
+def test_error_cell_path_bad_kind(sn, torch_gpu):
+    """An unknown instruction kind ends the pass with RUN_ERR and the
+    instruction index in the error cell (core/interp.cuh error protocol)."""
+    L = sn.lib()
+    h = C.c_void_p()
+    sn.check(L.sinter_host_init(C.byref(h), 0, 0), "init")
+    try:
+        prog = (sn.Instr * 3)()
+        blocks = C.c_uint32()
+        L.sinter_host_grid(h, C.byref(blocks), None, None)
+        prog[0].kind, prog[0].block_hi = sn.OP_NOP, blocks.value
+        prog[1].kind = sn.OP_BOUNDARY
+        prog[2].kind, prog[2].block_hi = 77, blocks.value
+        sn.check(L.sinter_host_upload(h, prog, 3, 1), "upload")
+        sn.check(L.sinter_host_launch(h), "launch")
+        assert L.sinter_host_run_pass(h, 0, 20000.0) == sn.RUN_ERR
+        code, aux = C.c_uint32(), C.c_uint32()
+        L.sinter_host_error(h, C.byref(code), C.byref(aux))
+        assert code.value == sn.E_BAD_KIND and aux.value == 2
+        assert L.sinter_host_shutdown(h, 1000.0) == 0
+    finally:
+        L.sinter_host_destroy(h)

@@ -1,0 +1,334 @@
+"""GPU parity of each interpreter op, called through the C ABI
+(sinter_op_*), against the CPU oracle on identical seeded inputs.
+
+The declared numerics make integer/byte work and the fp64-folded float work
+reproducible, so outputs are compared bit for bit (np.array_equal) unless a
+test states a tolerance.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K, Q6_K, BF16, F32 = 8, 12, 14, 30, 0
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def empty_f32(torch, n):
+    return torch.zeros(n, dtype=torch.float32, device="cuda")
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def run_gemv(sn, torch, a, blocks):
+    print(f"gemv K={a.K} pro={a.pro} segs={a.n_seg} types={[a.seg[i].type for i in range(a.n_seg)]} "
+          f"blocks={blocks}", flush=True)
+    sn.check(sn.lib().sinter_op_gemv(C.byref(a), blocks, C.c_void_p(stream(torch))), "op_gemv")
+    torch.cuda.synchronize()
+    code, aux = sn.op_error()
+    assert code == 0, (code, aux)
+
+
+def synth_w(sn, t, rows, k, seed, cfg1=False):
+    w = np.zeros(sn.row_bytes(t, k) * rows, np.uint8)
+    kind = sn.SYN_Q8_0_CFG1 if cfg1 else sn.SYN_WEIGHT
+    sn.check(sn.lib().sinter_synth(0, w.ctypes.data, kind, t, rows, k, seed, 0, 0, None), "synth")
+    return w
+
+
+def xvec(k, seed, zero_block=True):
+    x = np.random.default_rng(seed).standard_normal(k).astype(np.float32)
+    if zero_block and k >= 512:
+        x[256:512] = 0.0          # exercises the amax == 0 quantiser branch
+    return x
+
+
+@pytest.mark.parametrize("t,k,rows,blocks", [
+    (Q4_K, 5120, 1000, 256), (Q6_K, 5120, 1000, 256), (Q6_K, 17408, 300, 256), (Q8_0, 5120, 1000, 256),
+    (BF16, 5120, 300, 128), (F32, 1024, 100, 32), (Q4_K, 4096, 513, 100), (Q4_K, 6144, 200, 256),
+    (Q6_K, 5120, 7, 256), (Q4_K, 5120, 1, 3)])
+def test_gemv_plain_matches_oracle(sn, orc, torch_gpu, t, k, rows, blocks):
+    torch = torch_gpu
+    w = synth_w(sn, t, rows, k, 100 + t + k, cfg1=(t == Q8_0))
+    x = xvec(k, 7)
+    dw, dx, dy = dev(torch, w), dev(torch, x), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    a.x = dx.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=t, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, blocks)
+    ref = orc.gemv(t, w, rows, k, x)
+    got = host(dy)
+    assert np.array_equal(got, ref), np.abs(got - ref).max()
+
+
+def test_gemv_rmsnorm_resid_and_multiseg(sn, orc, torch_gpu):
+    """attention-style phase: RMSNORM prologue, three segments (Q4_K, Q4_K,
+    Q6_K) sharing one Q8_K activation; then an EPI_RESID segment."""
+    torch = torch_gpu
+    k = 5120
+    x = xvec(k, 8) * 3
+    nw = (1 + 0.02 * np.random.default_rng(9).standard_normal(k)).astype(np.float32)
+    specs = [(Q4_K, 1536), (Q4_K, 256), (Q6_K, 256)]
+    ws = [synth_w(sn, t, r, k, 200 + i) for i, (t, r) in enumerate(specs)]
+    dws = [dev(torch, w) for w in ws]
+    dys = [empty_f32(torch, r) for _, r in specs]
+    dx, dn = dev(torch, x), dev(torch, nw)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_RMSNORM, n_seg=3, eps=1e-6)
+    a.x, a.norm_w = dx.data_ptr(), dn.data_ptr()
+    for i, (t, r) in enumerate(specs):
+        a.seg[i] = sn.GemvSeg(w=dws[i].data_ptr(), y=dys[i].data_ptr(), rows=r, type=t, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 256)
+    xn = orc.rmsnorm(x, nw, 1e-6)
+    for i, (t, r) in enumerate(specs):
+        assert np.array_equal(host(dys[i]), orc.gemv(t, ws[i], r, k, xn)), i
+    # residual epilogue
+    res = np.random.default_rng(10).standard_normal(r).astype(np.float32)
+    dres = dev(torch, res)
+    b = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    b.x = dx.data_ptr()
+    b.seg[0] = sn.GemvSeg(w=dws[2].data_ptr(), y=dys[2].data_ptr(), aux=dres.data_ptr(), rows=256, type=Q6_K,
+                          epi=sn.EPI_RESID)
+    run_gemv(sn, torch, b, 64)
+    assert np.array_equal(host(dys[2]), res + orc.gemv(Q6_K, ws[2], 256, k, x))
+
+
+def test_gemv_gated_prologue(sn, orc, torch_gpu):
+    """ssm_out phase: gated RMSNorm over 32 heads of 128, then Q4_K 4096->E."""
+    torch = torch_gpu
+    hv, d, rows = 32, 128, 640
+    k = hv * d
+    o = xvec(k, 11, zero_block=False)
+    z = xvec(k, 12, zero_block=False) * 2
+    nw = (1 + 0.02 * np.random.default_rng(13).standard_normal(d)).astype(np.float32)
+    w = synth_w(sn, Q4_K, rows, k, 300)
+    do, dz, dn, dw, dy = dev(torch, o), dev(torch, z), dev(torch, nw), dev(torch, w), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_GATED, n_seg=1, eps=1e-6, gn_log2d=7)
+    a.x, a.norm_w, a.aux = do.data_ptr(), dn.data_ptr(), dz.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=Q4_K, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 256)
+    on = np.zeros(k, np.float32)
+    orc.lib().or_gated_rmsnorm(o.ctypes.data, z.ctypes.data, nw.ctypes.data, on.ctypes.data, hv, d, 1e-6)
+    assert np.array_equal(host(dy), orc.gemv(Q4_K, w, rows, k, on))
+
+
+@pytest.mark.parametrize("et", [Q4_K, BF16])
+def test_gemv_embed_prologue(sn, orc, torch_gpu, et):
+    torch = torch_gpu
+    k, vocab, rows, tok = 5120, 300, 200, 217
+    emb = synth_w(sn, et, vocab, k, 400)
+    w = synth_w(sn, et if et == BF16 else Q4_K, rows, k, 401)
+    nw = (1 + 0.02 * np.random.default_rng(14).standard_normal(k)).astype(np.float32)
+    de, dw, dn, dy, dxo = dev(torch, emb), dev(torch, w), dev(torch, nw), empty_f32(torch, rows), empty_f32(torch, k)
+    cell = dev(torch, np.array([tok, 0, 0, 0], np.int32))
+    a = sn.GemvArgs(K=k, pro=sn.PRO_EMBED, n_seg=1, eps=1e-6, aux_type=et, aux_rows=vocab)
+    a.aux, a.token, a.norm_w, a.x_out = de.data_ptr(), cell.data_ptr(), dn.data_ptr(), dxo.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=et if et == BF16 else Q4_K,
+                          epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 64)
+    rb = sn.row_bytes(et, k)
+    x0 = orc.dequant(et, emb[tok * rb:(tok + 1) * rb], k)
+    assert np.array_equal(host(dxo), x0)
+    assert np.array_equal(host(dy), orc.gemv(et if et == BF16 else Q4_K, w, rows, k, orc.rmsnorm(x0, nw)))
+
+
+def test_gemv_swiglu_epilogue(sn, orc, torch_gpu):
+    torch = torch_gpu
+    k, rows = 5120, 1741
+    g = synth_w(sn, Q4_K, rows, k, 500)
+    u = synth_w(sn, Q4_K, rows, k, 501)
+    x = xvec(k, 15)
+    dg, du, dx, dy = dev(torch, g), dev(torch, u), dev(torch, x), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    a.x = dx.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dg.data_ptr(), w2=du.data_ptr(), y=dy.data_ptr(), rows=rows, type=Q4_K,
+                          epi=sn.EPI_SWIGLU)
+    run_gemv(sn, torch, a, 256)
+    yg, yu = orc.gemv(Q4_K, g, rows, k, x), orc.gemv(Q4_K, u, rows, k, x)
+    L = orc.lib()
+    ref = np.array([np.float32(L.or_silu(float(a_))) * b_ for a_, b_ in zip(yg, yu)], np.float32)
+    assert np.array_equal(host(dy), ref)
+
+
+def test_gemv_conv_epilogue(sn, orc, torch_gpu):
+    torch = torch_gpu
+    k, rows, dc = 5120, 1024, 4
+    w = synth_w(sn, Q4_K, rows, k, 600)
+    x = xvec(k, 16)
+    rng = np.random.default_rng(17)
+    cw = rng.uniform(-0.5, 0.5, rows * dc).astype(np.float32)
+    st = rng.standard_normal(rows * (dc - 1)).astype(np.float32)
+    dw, dx, dy, dcw, dst = dev(torch, w), dev(torch, x), empty_f32(torch, rows), dev(torch, cw), dev(torch, st)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    a.x = dx.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), w2=dcw.data_ptr(), y=dy.data_ptr(), aux=dst.data_ptr(), rows=rows,
+                          type=Q4_K, epi=sn.EPI_CONV, dconv=dc)
+    run_gemv(sn, torch, a, 256)
+    dot = orc.gemv(Q4_K, w, rows, k, x)
+    out = np.zeros(rows, np.float32)
+    st2 = st.copy()
+    orc.lib().or_conv_silu(dot.ctypes.data, st2.ctypes.data, cw.ctypes.data, out.ctypes.data, rows, dc)
+    assert np.array_equal(host(dy), out)
+    assert np.array_equal(host(dst), st2)
+
+
+def test_gemv_argmax_epilogue(sn, orc, torch_gpu):
+    torch = torch_gpu
+    k, vocab, blocks = 5120, 151936, 256
+    w = synth_w(sn, Q6_K, vocab, k, 700)
+    x = xvec(k, 18)
+    dw, dx, dy = dev(torch, w), dev(torch, x), empty_f32(torch, vocab)
+    cell = dev(torch, np.array([5, 41, 0, 0], np.int32))
+    hist = dev(torch, np.full(16, -1, np.int32))
+    ws = C.c_void_p()
+    sn.check(sn.lib().sinter_argmax_ws_create(blocks, C.c_void_p(cell.data_ptr()), C.c_void_p(hist.data_ptr()),
+                                              16, C.byref(ws)), "ws")
+    try:
+        a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+        a.x, a.epi_ws = dx.data_ptr(), ws.value
+        a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=vocab, type=Q6_K, epi=sn.EPI_ARGMAX)
+        run_gemv(sn, torch, a, blocks)
+        ref = orc.gemv(Q6_K, w, vocab, k, x)
+        assert np.array_equal(host(dy), ref)
+        best = int(np.argmax(ref))
+        c = host(cell)
+        assert c[0] == best and c[1] == 42 and c[2] == 1 and host(hist)[0] == best
+        # all-equal logits (x = 0): the first index wins; second call reuses
+        # the self-reset arrival counter
+        dx.zero_()
+        run_gemv(sn, torch, a, blocks)
+        c = host(cell)
+        assert c[0] == 0 and c[1] == 43 and c[2] == 2 and host(hist)[1] == 0
+    finally:
+        sn.lib().sinter_argmax_ws_destroy(ws)
+
+
+def test_gdn_step_matches_oracle(sn, orc, torch_gpu):
+    torch = torch_gpu
+    HK, HV, D = 16, 32, 128
+    rng = np.random.default_rng(19)
+    qkv = rng.standard_normal((2 * HK + HV) * D).astype(np.float32)
+    qkv[5 * D:6 * D] = 1e-9                   # a near-zero q head: l2 eps floor
+    al = (rng.standard_normal(HV) * 1.4).astype(np.float32)
+    be = rng.standard_normal(HV).astype(np.float32)
+    al[3] = 40.0                              # softplus linear branch
+    dt = rng.uniform(-6.9, -2.3, HV).astype(np.float32)
+    A = rng.uniform(-16, -1, HV).astype(np.float32)
+    M = (rng.standard_normal((HV, D, D)) * 0.1).astype(np.float32)
+    d = {n: dev(torch, v) for n, v in dict(qkv=qkv, al=al, be=be, dt=dt, A=A, M=M).items()}
+    do = empty_f32(torch, HV * D)
+    a = sn.GdnArgs(hk=HK, hv=HV, d=D, cols=16, eps=1e-6, scale=np.float32(1) / np.sqrt(np.float32(D)))
+    a.qkv, a.alpha, a.beta, a.dt_bias, a.ssm_a = (d["qkv"].data_ptr(), d["al"].data_ptr(), d["be"].data_ptr(),
+                                                  d["dt"].data_ptr(), d["A"].data_ptr())
+    a.state, a.o = d["M"].data_ptr(), do.data_ptr()
+    print("gdn_step HK=16 HV=32 D=128 cols=16 blocks=256", flush=True)
+    sn.check(sn.lib().sinter_op_gdn_step(C.byref(a), 256, C.c_void_p(stream(torch))), "gdn")
+    torch.cuda.synchronize()
+    assert sn.op_error()[0] == 0
+    L = orc.lib()
+    q = qkv[:HK * D].copy()
+    k = qkv[HK * D:2 * HK * D].copy()
+    for h in range(HK):
+        L.or_l2norm(q[h * D:].ctypes.data, q[h * D:].ctypes.data, D, 1e-6)
+        L.or_l2norm(k[h * D:].ctypes.data, k[h * D:].ctypes.data, D, 1e-6)
+    g = np.zeros(HV, np.float32)
+    bt = np.zeros(HV, np.float32)
+    L.or_gdn_gates(al.ctypes.data, be.ctypes.data, dt.ctypes.data, A.ctypes.data, g.ctypes.data, bt.ctypes.data, HV)
+    o = np.zeros(HV * D, np.float32)
+    st = M.copy()
+    v = qkv[2 * HK * D:].copy()
+    L.or_gdn_step(q.ctypes.data, k.ctypes.data, v.ctypes.data, g.ctypes.data, bt.ctypes.data, st.ctypes.data,
+                  o.ctypes.data, HV, HK, D, a.scale)
+    assert np.array_equal(host(d["M"]), st)
+    assert np.array_equal(host(do), o)
+
+
+@pytest.mark.parametrize("pos,n_ctx,chunks", [(0, 64, 64), (5, 4096, 64), (1000, 4096, 64), (4095, 4096, 64),
+                                              (4095, 4096, 7), (40000, 40960, 64)])
+def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
+    torch = torch_gpu
+    NQ, NKV, HD = 24, 4, 256
+    RW = NKV * HD
+    rng = np.random.default_rng(20 + pos)
+    qg = (rng.standard_normal(NQ * 2 * HD) * 2).astype(np.float32)
+    k = rng.standard_normal(RW).astype(np.float32)
+    v = rng.standard_normal(RW).astype(np.float32)
+    qn = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+    kn = (1 + 0.02 * rng.standard_normal(HD)).astype(np.float32)
+    K = np.zeros((n_ctx, RW), np.float16)
+    V = np.zeros((n_ctx, RW), np.float16)
+    K[:pos] = rng.standard_normal((pos, RW))
+    V[:pos] = rng.standard_normal((pos, RW))
+    ts = orc.lib().or_rope_theta_scale(1e7, 64)
+    dK, dV = dev(torch, K.view(np.uint16)), dev(torch, V.view(np.uint16))
+    dqg, dk, dv_, dqn, dkn = dev(torch, qg), dev(torch, k), dev(torch, v), dev(torch, qn), dev(torch, kn)
+    part = torch.zeros(NKV * chunks * (NQ // NKV) * (HD + 2), dtype=torch.float64, device="cuda")
+    cnt = torch.zeros(64, dtype=torch.int32, device="cuda")
+    out = empty_f32(torch, NQ * HD)
+    cell = dev(torch, np.array([0, pos, 0, 0], np.int32))
+    a = sn.AttnArgs(nq=NQ, nkv=NKV, hd=HD, rope_dims=64, n_ctx=n_ctx, n_chunks=chunks, theta_scale=ts, eps=1e-6,
+                    scale=0.0625)
+    a.qg, a.k, a.v, a.q_norm, a.k_norm = dqg.data_ptr(), dk.data_ptr(), dv_.data_ptr(), dqn.data_ptr(), dkn.data_ptr()
+    a.kc, a.vc, a.part, a.count, a.out, a.pass_cell = (dK.data_ptr(), dV.data_ptr(), part.data_ptr(),
+                                                       cnt.data_ptr(), out.data_ptr(), cell.data_ptr())
+    print(f"attn_decode pos={pos} n_ctx={n_ctx} chunks={chunks} blocks=256", flush=True)
+    sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), 256, C.c_void_p(stream(torch))), "attn")
+    torch.cuda.synchronize()
+    assert sn.op_error()[0] == 0
+    assert np.all(host(cnt) == 0)            # counters self-reset
+    # oracle: norms + rope, append, attention, gate
+    L = orc.lib()
+    qr = np.zeros((NQ, HD), np.float32)
+    for h in range(NQ):
+        L.or_rmsnorm(qg[h * 2 * HD:].ctypes.data, qn.ctypes.data, qr[h].ctypes.data, HD, 1e-6)
+        L.or_rope_neox(qr[h].ctypes.data, HD, 64, pos, ts)
+    kr = np.zeros((NKV, HD), np.float32)
+    for g in range(NKV):
+        L.or_rmsnorm(k[g * HD:].ctypes.data, kn.ctypes.data, kr[g].ctypes.data, HD, 1e-6)
+        L.or_rope_neox(kr[g].ctypes.data, HD, 64, pos, ts)
+    K[pos] = kr.reshape(-1).astype(np.float16)
+    V[pos] = v.astype(np.float16)
+    assert np.array_equal(host(dK)[pos], K[pos].view(np.uint16))
+    assert np.array_equal(host(dV)[pos], V[pos].view(np.uint16))
+    att = np.zeros((NQ, HD), np.float32)
+    L.or_attn_decode(qr.ctypes.data, K.ctypes.data, V.ctypes.data, pos + 1, NQ, NKV, HD, RW, 0.0625, att.ctypes.data)
+    gate = qg.reshape(NQ, 2, HD)[:, 1]
+    ref = np.array([[np.float32(att[h, i]) * np.float32(L.or_sigmoid(float(gate[h, i]))) for i in range(HD)]
+                    for h in range(NQ)], np.float32)
+    got = host(out).reshape(NQ, HD)
+    # fp64 softmax folded in a different (split) order: equal after the fp32
+    # rounding except with ~1e-8 probability per element; allow 1 ulp
+    ulp = np.abs(np.spacing(ref))
+    assert np.all(np.abs(got - ref) <= ulp), np.abs(got - ref).max()
+    assert np.mean(got == ref) > 0.999
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, BF16])
+def test_device_synth_equals_host(sn, torch_gpu, t):
+    torch = torch_gpu
+    rows, k = 97, 5120
+    h = synth_w(sn, t, rows, k, 800 + t, cfg1=(t == Q8_0))
+    d = torch.zeros(h.size, dtype=torch.uint8, device="cuda")
+    kind = sn.SYN_Q8_0_CFG1 if t == Q8_0 else sn.SYN_WEIGHT
+    sn.check(sn.lib().sinter_synth(1, C.c_void_p(d.data_ptr()), kind, t, rows, k, 800 + t, 0, 0,
+                                   C.c_void_p(stream(torch))), "synth")
+    torch.cuda.synchronize()
+    assert np.array_equal(host(d), h)
+    x = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    xh = np.zeros(4096, np.float32)
+    for kind, a_, b_ in ((sn.SYN_NORMAL, 1.0, 0.02), (sn.SYN_UNIFORM, -6.9, -2.3)):
+        sn.check(sn.lib().sinter_synth(1, C.c_void_p(x.data_ptr()), kind, 0, 1, 4096, 5, a_, b_,
+                                       C.c_void_p(stream(torch))), "synth")
+        sn.check(sn.lib().sinter_synth(0, xh.ctypes.data, kind, 0, 1, 4096, 5, a_, b_, None), "synth")
+        torch.cuda.synchronize()
+        assert np.array_equal(host(x), xh)
