@@ -54,6 +54,9 @@ enum sinter_err_code {
 
 const char *sinter_last_error(void);
 int sinter_abi_version(void);
+/* rig precheck (tests/devinfo.cu): a one-line report of runtime, device and
+ * interpreter envelope into buf; non-zero if the device cannot run it */
+int sinter_device_info(int device, char *buf, size_t n);
 
 /* ------------------------------------------------------------------ types */
 /* ggml_type numbering */

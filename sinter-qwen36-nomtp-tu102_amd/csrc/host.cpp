@@ -47,13 +47,13 @@ unsigned *op_err_cell() {
     static std::mutex mu;
     static std::map<int, unsigned *> cells;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    if (!hip_ok(hipGetDevice(&dev), "op error cell: hipGetDevice")) return nullptr;
     std::lock_guard<std::mutex> lk(mu);
     auto it = cells.find(dev);
     if (it != cells.end()) return it->second;
     unsigned *p = nullptr;
-    if (hipMalloc(&p, 256) != hipSuccess) return nullptr;
-    if (hipMemset(p, 0, 256) != hipSuccess) return nullptr;
+    if (!hip_ok(hipMalloc(&p, 256), "op error cell: hipMalloc")) return nullptr;
+    if (!hip_ok(hipMemset(p, 0, 256), "op error cell: hipMemset")) return nullptr;
     cells[dev] = p;
     return p;
 }
@@ -122,7 +122,7 @@ template <class T>
 static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
     if (blocks == 0 || blocks > 65535) return set_error(SINTER_ERR_ARG, "blocks must be 1..65535");
     unsigned *err = op_err_cell();
-    if (!err) return set_error(SINTER_ERR_HIP, "cannot allocate the op error cell");
+    if (!err) return SINTER_ERR_HIP;
     sinter_instr ins;
     std::memset(&ins, 0, sizeof ins);
     ins.kind = (uint16_t)kind;
@@ -140,6 +140,31 @@ using namespace sinter;
 extern "C" {
 
 const char *sinter_last_error(void) { return g_last_error.c_str(); }
+
+// Rig precheck (tests/devinfo.cu in the reference): runtime version, device
+// name, CU count, LDS, cooperative support, interpreter occupancy.
+int sinter_device_info(int device, char *buf, size_t n) {
+    if (!buf || n == 0) return set_error(SINTER_ERR_ARG, "device_info: buffer");
+    int rt = 0, drv = 0, coop = 0, per_cu = -1;
+    hipError_t e1 = hipRuntimeGetVersion(&rt);
+    hipError_t e2 = hipDriverGetVersion(&drv);
+    hipDeviceProp_t p;
+    std::memset(&p, 0, sizeof p);
+    hipError_t e3 = hipGetDeviceProperties(&p, device);
+    hipError_t e4 = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
+    hipError_t e5 = hipSetDevice(device);
+    void *probe = nullptr;
+    hipError_t e6 = hipMalloc(&probe, 4096);
+    if (e6 == hipSuccess) (void)hipFree(probe);
+    hipError_t e7 = interp_max_blocks(&per_cu);
+    std::snprintf(buf, n,
+                  "runtime %d driver %d | %s (%s) CUs %d LDS/block %zu coop %d | interp blocks/CU %d | "
+                  "errors: version %s, props %s, attr %s, setdev %s, malloc %s, occupancy %s",
+                  rt, drv, p.name, p.gcnArchName, p.multiProcessorCount, (size_t)p.sharedMemPerBlock, coop, per_cu,
+                  hipGetErrorString(e1 ? e1 : e2), hipGetErrorString(e3), hipGetErrorString(e4),
+                  hipGetErrorString(e5), hipGetErrorString(e6), hipGetErrorString(e7));
+    return (e3 || e5 || e6 || e7) ? set_error(SINTER_ERR_HIP, "%s", buf) : SINTER_OK;
+}
 int sinter_abi_version(void) { return SINTER_ABI_VERSION; }
 size_t sinter_row_bytes(int type, int64_t k) { return sinter_row_bytes_dev(type, k); }
 

@@ -106,11 +106,20 @@ def lib():
     if not os.path.exists(LIB_PATH):
         raise RuntimeError("libsinter.so is not built (run __graft_entry__.build()); "
                            "there is no CPU fallback")
+    # One HIP runtime per process: torch ships its own libamdhip64.so.7, and
+    # whichever copy is loaded first satisfies the other's dependency.  torch
+    # does not run on the system copy, while libsinter runs on either, so
+    # let torch (when installed) load its runtime first.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     I, U32, I64, U64 = C.c_int, C.c_uint32, C.c_int64, C.c_uint64
     sig = {
         "sinter_last_error": (C.c_char_p, []),
         "sinter_abi_version": (I, []),
+        "sinter_device_info": (I, [I, C.c_char_p, C.c_size_t]),
         "sinter_row_bytes": (C.c_size_t, [I, I64]),
         "sinter_op_gemv": (I, [C.POINTER(GemvArgs), U32, vp]),
         "sinter_op_gdn_step": (I, [C.POINTER(GdnArgs), U32, vp]),
@@ -165,6 +174,12 @@ def check(rc, what=""):
         msg = lib().sinter_last_error()
         raise SinterError(f"{what}: status {rc}: {msg.decode() if msg else ''}")
     return rc
+
+
+def device_info(device=0):
+    buf = C.create_string_buffer(1024)
+    rc = lib().sinter_device_info(device, buf, 1024)
+    return rc, buf.value.decode()
 
 
 def op_error():
