@@ -79,6 +79,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--profile-ops", type=int, default=0,
+                    help="after the timed run, N more tokens with block-0 per-kind timers (stderr)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the decode path on one GPU "
@@ -111,6 +113,18 @@ def main():
     print(f"# timed {args.steps} tokens: wall {wall * 1e3:.2f} ms, interpreter kernel {kernel_ms:.2f} ms; "
           f"tokens[:8] {toks[:8]}", file=sys.stderr, flush=True)
 
+    if args.profile_ops:
+        import ctypes as C
+        L = sinter.lib()
+        h = m.host()
+        L.sinter_host_reset_op_cycles(h)
+        m.greedy(toks[-1], pos0 + args.steps, args.profile_ops)
+        cyc = (C.c_longlong * 5)()
+        L.sinter_host_read_op_cycles(h, cyc, 5)
+        names = ["nop", "boundary", "gemv", "gdn_step", "attn_decode"]
+        # wall clock ticks: 100 MHz on MI355X
+        rep = {n: round(c / 1e5 / args.profile_ops, 4) for n, c in zip(names, cyc)}
+        print(f"# block-0 ms per token by kind: {rep}", file=sys.stderr, flush=True)
     mean_attended = pos0 + (args.steps + 1) / 2.0
     bpt = bytes_per_token(cfg, m, mean_attended)
     tok_s = args.steps / wall

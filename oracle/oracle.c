@@ -359,11 +359,11 @@ static double row_q8_0(const blk_q8_0 *w, const blk_q8_0 *x, int64_t nb) {
 }
 
 static double row_bf16(const uint16_t *w, const uint16_t *x, int64_t k) {
-    /* declared fold: 256-element groups, exact products, fp64 */
+    /* declared fold: 64-element items, exact products, fp64 */
     double acc = 0.0;
-    for (int64_t g = 0; g < k / 256; g++) {
+    for (int64_t g = 0; g < k / 64; g++) {
         double part = 0.0;
-        for (int64_t i = 256 * g; i < 256 * g + 256; i++)
+        for (int64_t i = 64 * g; i < 64 * g + 64; i++)
             part += (double)or_bf16_to_f32(w[i]) * (double)or_bf16_to_f32(x[i]);
         acc += part;
     }
@@ -384,9 +384,9 @@ void or_gemv_q(int t, const void *w, int64_t rows, int64_t k, const void *xq, fl
         case OR_BF16: acc = row_bf16((const uint16_t *)row, (const uint16_t *)xq, k); break;
         case OR_F32: {
             const float *wf = (const float *)row, *xf = (const float *)xq;
-            for (int64_t g = 0; g < k / 256; g++) {
+            for (int64_t g = 0; g < k / 64; g++) {
                 double part = 0.0;
-                for (int64_t i = 256 * g; i < 256 * g + 256; i++) part += (double)wf[i] * (double)xf[i];
+                for (int64_t i = 64 * g; i < 64 * g + 64; i++) part += (double)wf[i] * (double)xf[i];
                 acc += part;
             }
         } break;

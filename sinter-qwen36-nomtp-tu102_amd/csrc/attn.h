@@ -56,7 +56,7 @@ __device__ __forceinline__ void att_norm_rope(float x, const float *w, float eps
     __syncthreads();
 }
 
-__device__ void op_attn_decode(const sinter_instr &ins, char *lds, unsigned *err) {
+__device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
     const sinter_attn_args &a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
@@ -74,13 +74,14 @@ __device__ void op_attn_decode(const sinter_instr &ins, char *lds, unsigned *err
     uint32_t clen = (n_kv + C - 1) / C;
     clen = (clen + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
 
-    // LDS map
-    float *qf = reinterpret_cast<float *>(lds);                          // [gqa][256]
+    // LDS map (two of the GEMV tile buffers): q heads, K tile, new K/V row |
+    // V tile, scores, softmax state, scratch
+    float *qf = reinterpret_cast<float *>(g_tiles);                      // [gqa][256]
     uint16_t *kt = reinterpret_cast<uint16_t *>(qf + ATT_MAXG * 256);    // [32][256]
-    uint16_t *vt = kt + ATT_TILE * 256;                                  // [32][256]
-    uint16_t *knew = vt + ATT_TILE * 256;                                // [256]
+    uint16_t *knew = kt + ATT_TILE * 256;                                // [256]
     uint16_t *vnew = knew + 256;                                         // [256]
-    double *sc = reinterpret_cast<double *>(vnew + 256);                 // [gqa][32] scores -> weights
+    uint16_t *vt = reinterpret_cast<uint16_t *>(g_tiles + TILE_BYTES);                // [32][256]
+    double *sc = reinterpret_cast<double *>(vt + ATT_TILE * 256);        // [gqa][32] scores -> weights
     double *mrun = sc + ATT_MAXG * ATT_TILE;                             // [gqa]
     double *lrun = mrun + ATT_MAXG;                                      // [gqa]
     double *corr = lrun + ATT_MAXG;                                      // [gqa]

@@ -17,6 +17,21 @@
 
 namespace sinter {
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ---------------------------------------------------------------- static LDS
+// g_tiles: the GEMV's three LDS-DMA tile buffers (other ops use the space as
+// scratch); g_qbuf: the quantised activation.
+__shared__ __attribute__((aligned(16))) char g_tiles[3 * TILE_BYTES];
+__shared__ __attribute__((aligned(16))) char g_qbuf[QBUF_BYTES];
+__shared__ float g_res[2 * RES_CAP];
+__shared__ double g_red[16];
+__shared__ double g_part[16];
+__shared__ double g_cb[CB_CAP];           // GEMV item terms of the current tile
+// the running op's payload, copied out of the program once per op so that
+// reading it never waits behind tile LDS-DMA (lgkmcnt, not vmcnt)
+__shared__ __attribute__((aligned(16))) unsigned char g_args[240];
+
 // ---------------------------------------------------------------- wave64
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

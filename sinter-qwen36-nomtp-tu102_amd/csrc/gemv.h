@@ -11,21 +11,23 @@
 //
 // Work split: the rows of all segments form one byte-weighted row space; the
 // participating workgroups take contiguous, byte-balanced row ranges.  A
-// workgroup streams its rows in tiles: 16-byte coalesced global loads into
-// registers, one tile ahead, stored into a double-buffered LDS tile; compute
-// then reads the (arbitrarily aligned) ggml blocks from LDS.  One lane owns one
-// (row, 256-element group) item and produces that group's exact term.
+// workgroup streams its rows through three 36 KiB LDS tiles with gfx950
+// LDS-DMA (global_load_lds_dwordx4: 16 B per lane straight into LDS, no
+// VGPRs), two tiles in flight while one is computed; compute reads the
+// (arbitrarily aligned) ggml blocks from LDS, one wave per row, lanes over
+// 32-element units, and a wave-wide fp64 sum per row.  Row results stay in
+// LDS; the epilogues run once over the block's rows at the end.
 //
-// Declared fold (identical in oracle/oracle.c): integer block dots are exact;
-// each 256-element group contributes one fp64 term (for Q8_0 the sum of its
-// 8 block terms in ascending order); the row is the ascending fp64 sum of its
-// group terms, rounded to fp32 once.
+// Declared numerics (oracle/oracle.c): integer block dots are exact; each
+// unit's term is an fp64 expression of exact integers and the f16/f32
+// scales; a row is the fp64 sum of its terms rounded to fp32 once.  The
+// oracle sums in ascending order, the kernel in wave order; both round the
+// same ~1e-16-accurate fp64 value, so outputs agree to the last bit except
+// with probability ~1e-8 per row (1 ulp then).
 #pragma once
 #include "dev_common.h"
 
 namespace sinter {
-
-constexpr int MAX_LD = (int)(TILE_BYTES / 16 / BLOCK_THREADS);  // uint4 per thread per tile
 
 __device__ __forceinline__ int vec_dot_type(int t) {
     return (t == SINTER_Q4_K || t == SINTER_Q6_K) ? SINTER_Q8_K
@@ -57,29 +59,36 @@ __device__ __forceinline__ uint16_t lds_u16(const char *lds, uint32_t off) {
 }
 
 // ------------------------------------------------------------ activation layout in LDS
-// Q8_K: qs int8[K] | d f32[K/256] | bsums i16[K/16]
-// Q8_0: qs int8[K] | d f32[K/32]  (d is the f16-rounded scale, as float)
-// BF16: u16[K];  F32: f32[K]
+// Padded so that lanes working on different groups/chunks start on
+// different LDS banks (an unpadded 256-byte group stride puts every group on
+// bank 0 and serialises the activation reads):
+//   Q8_K: int8 codes, group g at g*ACT_GSTRIDE | d f32[G] | bsums i16[16G]
+//   Q8_0: int8 codes, group g at g*ACT_GSTRIDE | d f32[K/32] (f16-rounded)
+//   BF16: 64-element chunk c at c*ACT_BF_CSTRIDE (u16)
+//   F32:  64-element chunk c at c*ACT_F_CSTRIDE
+constexpr uint32_t ACT_GSTRIDE = 272;
+constexpr uint32_t ACT_BF_CSTRIDE = 144;
+constexpr uint32_t ACT_F_CSTRIDE = 272;
+__host__ __device__ inline uint32_t act_bytes(int vt, uint32_t K) {
+    if (vt == SINTER_Q8_K) return (K / 256) * ACT_GSTRIDE + (K / 256) * 4 + (K / 16) * 2;
+    if (vt == SINTER_Q8_0) return (K / 256) * ACT_GSTRIDE + (K / 32) * 4;
+    if (vt == SINTER_BF16) return (K / 64) * ACT_BF_CSTRIDE;
+    return (K / 64) * ACT_F_CSTRIDE;
+}
 struct ActView {
-    const int8_t *qs;
+    const char *q;       // codes / bf16 / f32 chunks
     const float *d;
     const int16_t *bs;
-    const uint16_t *bf;
-    const float *f;
 };
 __device__ __forceinline__ ActView act_view(char *q, uint32_t K, int vt) {
     ActView v{};
-    v.qs = reinterpret_cast<const int8_t *>(q);
-    if (vt == SINTER_Q8_K) {
-        v.d = reinterpret_cast<const float *>(q + K);
-        v.bs = reinterpret_cast<const int16_t *>(q + K + (K / 256) * 4);
-    } else if (vt == SINTER_Q8_0) {
-        v.d = reinterpret_cast<const float *>(q + K);
-    }
-    v.bf = reinterpret_cast<const uint16_t *>(q);
-    v.f = reinterpret_cast<const float *>(q);
+    v.q = q;
+    v.d = reinterpret_cast<const float *>(q + (K / 256) * ACT_GSTRIDE);
+    v.bs = reinterpret_cast<const int16_t *>(q + (K / 256) * ACT_GSTRIDE + (K / 256) * 4);
+    (void)vt;
     return v;
 }
+__device__ __forceinline__ uint32_t act_qoff(uint32_t e) { return (e >> 8) * ACT_GSTRIDE + (e & 255); }
 
 // ------------------------------------------------------------ embedding dequant (4 elements)
 
@@ -173,9 +182,8 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
     const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (64..256)
     const int lane = lane_id();
     const int nw = blockDim.x >> 6;
-    int8_t *qs = reinterpret_cast<int8_t *>(q);
-    float *qd = reinterpret_cast<float *>(q + K);
-    int16_t *qb = reinterpret_cast<int16_t *>(q + K + (K / 256) * 4);
+    float *qd = reinterpret_cast<float *>(q + (K / 256) * ACT_GSTRIDE);
+    int16_t *qb = reinterpret_cast<int16_t *>(q + (K / 256) * ACT_GSTRIDE + (K / 256) * 4);
     // one wave per 256-element chunk, 4 consecutive elements per lane
     for (uint32_t c = wave_id(); c < K / 256; c += nw) {
         const uint32_t e = c * 256 + lane * 4;
@@ -239,7 +247,7 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
             }
             const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
                                     ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-            *reinterpret_cast<uint32_t *>(qs + e) = packed;
+            *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
             int bsum = qv[0] + qv[1] + qv[2] + qv[3];
             bsum += __shfl_xor(bsum, 1, 64);
             bsum += __shfl_xor(bsum, 2, 64);
@@ -258,44 +266,75 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
             for (int i = 0; i < 4; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
             const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
                                     ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-            *reinterpret_cast<uint32_t *>(qs + e) = packed;
+            *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
             if ((lane & 7) == 0) qd[e / 32] = h2f(f2h(d));
         } else if (vt == SINTER_BF16) {
-            uint16_t *bf = reinterpret_cast<uint16_t *>(q);
+            uint16_t *bf = reinterpret_cast<uint16_t *>(q + (e >> 6) * ACT_BF_CSTRIDE) + (e & 63);
 #pragma unroll
-            for (int i = 0; i < 4; i++) bf[e + i] = f2bf(t[i]);
+            for (int i = 0; i < 4; i++) bf[i] = f2bf(t[i]);
         } else {
-            float *f = reinterpret_cast<float *>(q);
+            float *f = reinterpret_cast<float *>(q + (e >> 6) * ACT_F_CSTRIDE) + (e & 63);
 #pragma unroll
-            for (int i = 0; i < 4; i++) f[e + i] = t[i];
+            for (int i = 0; i < 4; i++) f[i] = t[i];
         }
     }
     __syncthreads();
 }
 
-// ------------------------------------------------------------ group terms
+// ------------------------------------------------------------ item terms
+// A weight row is a sequence of items: one 256-element group for the
+// quantised types (one Q4_K / Q6_K block, eight Q8_0 blocks), 64 elements
+// for BF16 / F32.  One lane computes one item's term: an fp64 expression of
+// exact integer block dots and the f16/f32 scales (a float sum of exact
+// products for BF16/F32).  A row is the ascending fp64 sum of its item terms,
+// rounded to fp32 once -- the fold oracle/oracle.c declares.
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// n words (4 bytes each) at a 2-aligned LDS byte offset
+template <int N>
+__device__ __forceinline__ void lds_words(const char *lds, uint32_t off, uint32_t w[N]) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(lds + (off & ~3u));
+    const uint32_t sh = off & 3u;
+    uint32_t d[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) d[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+}
+
+__device__ __forceinline__ uint32_t item_elems(int t) { return (t == SINTER_BF16 || t == SINTER_F32) ? 64u : 256u; }
+__device__ __forceinline__ uint32_t item_bytes(int t) {
+    switch (t) {
+    case SINTER_Q4_K: return 144;
+    case SINTER_Q6_K: return 210;
+    case SINTER_Q8_0: return 272;
+    case SINTER_BF16: return 128;
+    default: return 256;
+    }
+}
+
 // Q4_K block (16-aligned in LDS) against Q8_K group g
 __device__ __forceinline__ double term_q4k(const char *blk, const ActView &x, uint32_t g) {
     const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
-    const uint8_t *scb = reinterpret_cast<const uint8_t *>(blk) + 4;
-    int sc[8], mn[8];
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        sc[s] = scb[s] & 63;
-        mn[s] = scb[s + 4] & 63;
-        sc[s + 4] = (scb[s + 8] & 0xF) | ((scb[s] >> 6) << 4);
-        mn[s + 4] = (scb[s + 8] >> 4) | ((scb[s + 4] >> 6) << 4);
-    }
-    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.qs + g * 256);
+    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};   // scales[0..11]
+    auto byte = [&](uint32_t i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xff); };
+    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE);
     const int16_t *bs = x.bs + g * 16;
     int isum = 0, imin = 0;
 #pragma unroll
     for (int p = 0; p < 4; p++) {
+        const int s0 = 2 * p, s1 = 2 * p + 1;
+        int sc0, m0, sc1, m1;
+        if (p < 2) {
+            sc0 = byte(s0) & 63; m0 = byte(s0 + 4) & 63;
+            sc1 = byte(s1) & 63; m1 = byte(s1 + 4) & 63;
+        } else {
+            sc0 = (byte(s0 + 4) & 0xF) | ((byte(s0 - 4) >> 6) << 4); m0 = (byte(s0 + 4) >> 4) | ((byte(s0) >> 6) << 4);
+            sc1 = (byte(s1 + 4) & 0xF) | ((byte(s1 - 4) >> 6) << 4); m1 = (byte(s1 + 4) >> 4) | ((byte(s1) >> 6) << 4);
+        }
         const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
         const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * p);
         const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
@@ -305,9 +344,8 @@ __device__ __forceinline__ double term_q4k(const char *blk, const ActView &x, ui
             dlo = sdot4(w[i] & 0x0F0F0F0Fu, xq[16 * p + i], dlo);
             dhi = sdot4((w[i] >> 4) & 0x0F0F0F0Fu, xq[16 * p + 8 + i], dhi);
         }
-        isum += sc[2 * p] * dlo + sc[2 * p + 1] * dhi;
-        imin += mn[2 * p] * ((int)bs[4 * p] + (int)bs[4 * p + 1]) +
-                mn[2 * p + 1] * ((int)bs[4 * p + 2] + (int)bs[4 * p + 3]);
+        isum += sc0 * dlo + sc1 * dhi;
+        imin += m0 * ((int)bs[4 * p] + (int)bs[4 * p + 1]) + m1 * ((int)bs[4 * p + 2] + (int)bs[4 * p + 3]);
     }
     const double dx = (double)x.d[g];
     const double dw = (double)h2f((uint16_t)(hdr.x & 0xffff));
@@ -316,37 +354,40 @@ __device__ __forceinline__ double term_q4k(const char *blk, const ActView &x, ui
 }
 
 // Q6_K block at a 2-aligned LDS offset against Q8_K group g.  Codes are
-// taken unsigned (0..63) and the -32 offset is folded through the bsums:
+// taken unsigned (0..63) and the -32 offset folds through the bsums:
 // sum((c-32)*x) = sum(c*x) - 32*bsum, exact in integers.
 __device__ __forceinline__ double term_q6k(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
-    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.qs + g * 256);
+    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE);
     const int16_t *bs = x.bs + g * 16;
+    uint32_t scw[4];
+    lds_words<4>(lds, off + 192, scw);                 // int8 scales[16]
     int isum = 0;
 #pragma unroll
     for (int n = 0; n < 2; n++) {
+        uint32_t qa[8], qb[8], qh[8];
+        lds_words<8>(lds, off + 64 * n, qa);           // ql[64n .. 64n+32)
+        lds_words<8>(lds, off + 64 * n + 32, qb);      // ql[64n+32 .. 64n+64)
+        lds_words<8>(lds, off + 128 + 32 * n, qh);     // qh[32n .. 32n+32)
+        int dot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // [quarter][16-element half]
 #pragma unroll
-        for (int h = 0; h < 2; h++) {          // lbase = 16h
-            int dot[4] = {0, 0, 0, 0};          // quarters t = 0..3
+        for (int i = 0; i < 8; i++) {
+            const uint32_t c0 = (qa[i] & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u);
+            const uint32_t c1 = (qb[i] & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u);
+            const uint32_t c2 = ((qa[i] >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u);
+            const uint32_t c3 = ((qb[i] >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u);
+            const int hf = i >> 2;                     // l = 4i.. : half hf of each quarter
+            dot[0][hf] = sdot4(c0, xq[(128 * n + 0) / 4 + i], dot[0][hf]);
+            dot[1][hf] = sdot4(c1, xq[(128 * n + 32) / 4 + i], dot[1][hf]);
+            dot[2][hf] = sdot4(c2, xq[(128 * n + 64) / 4 + i], dot[2][hf]);
+            dot[3][hf] = sdot4(c3, xq[(128 * n + 96) / 4 + i], dot[3][hf]);
+        }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t qla = lds_u32(lds, off + 64 * n + 16 * h + 4 * i);
-                const uint32_t qlb = lds_u32(lds, off + 64 * n + 32 + 16 * h + 4 * i);
-                const uint32_t qh = lds_u32(lds, off + 128 + 32 * n + 16 * h + 4 * i);
-                const uint32_t c0 = (qla & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
-                const uint32_t c1 = (qlb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
-                const uint32_t c2 = ((qla >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
-                const uint32_t c3 = ((qlb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
-                // element base of quarter t: 128n + 32t + 16h + 4i
-                dot[0] = sdot4(c0, xq[(128 * n + 0 + 16 * h) / 4 + i], dot[0]);
-                dot[1] = sdot4(c1, xq[(128 * n + 32 + 16 * h) / 4 + i], dot[1]);
-                dot[2] = sdot4(c2, xq[(128 * n + 64 + 16 * h) / 4 + i], dot[2]);
-                dot[3] = sdot4(c3, xq[(128 * n + 96 + 16 * h) / 4 + i], dot[3]);
-            }
+        for (int t = 0; t < 4; t++) {
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int j = 8 * n + 2 * t + h;  // 16-element sub-block
-                const int sc = (int)(int8_t)(lds_u16(lds, off + 192 + (j & ~1)) >> (8 * (j & 1)));
-                isum += sc * (dot[t] - 32 * (int)bs[j]);
+            for (int hf = 0; hf < 2; hf++) {
+                const int j = 8 * n + 2 * t + hf;      // 16-element sub-block
+                const int sc = (int)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xff);
+                isum += sc * (dot[t][hf] - 32 * (int)bs[j]);
             }
         }
     }
@@ -354,53 +395,70 @@ __device__ __forceinline__ double term_q6k(const char *lds, uint32_t off, const 
     return (dw * (double)x.d[g]) * (double)isum;
 }
 
-// 8 Q8_0 blocks (272 B, 16-aligned item) against Q8_0 activation blocks 8g..8g+7
+// 8 Q8_0 blocks (272 B group) against Q8_0 activation blocks 8g..8g+7,
+// block terms summed in ascending order inside the group
 __device__ __forceinline__ double term_q80(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
     double acc = 0.0;
 #pragma unroll
     for (int b = 0; b < 8; b++) {
         const uint32_t bo = off + 34 * b;
-        const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.qs + (8 * g + b) * 32);
+        uint32_t w[8];
+        lds_words<8>(lds, bo + 2, w);
+        const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE + 32 * b);
         int isum = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) isum = sdot4(lds_u32(lds, bo + 2 + 4 * i), xq[i], isum);
+        for (int i = 0; i < 8; i++) isum = sdot4(w[i], xq[i], isum);
         const double dw = (double)h2f(lds_u16(lds, bo));
         acc += (dw * (double)x.d[8 * g + b]) * (double)isum;
     }
     return acc;
 }
 
-__device__ __forceinline__ double term_bf16(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(lds + off);
-    const uint32_t *xx = reinterpret_cast<const uint32_t *>(x.bf + g * 256);
+// 64 bf16 elements (128 B, 16-aligned), products exact in fp64, ascending
+__device__ __forceinline__ double term_bf16(const char *lds, uint32_t off, const ActView &x, uint32_t k) {
+    const uint4 *w = reinterpret_cast<const uint4 *>(lds + off);
+    const uint4 *xx = reinterpret_cast<const uint4 *>(x.q + k * ACT_BF_CSTRIDE);
     double acc = 0.0;
-    for (int i = 0; i < 128; i++) {
-        const uint32_t ww = w[i], xv = xx[i];
-        acc = fma((double)__uint_as_float(ww << 16), (double)__uint_as_float(xv << 16), acc);
-        acc = fma((double)__uint_as_float(ww & 0xffff0000u), (double)__uint_as_float(xv & 0xffff0000u), acc);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint4 a = w[i], b = xx[i];
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            acc += (double)__uint_as_float(aw[j] << 16) * (double)__uint_as_float(bw[j] << 16);
+            acc += (double)__uint_as_float(aw[j] & 0xffff0000u) * (double)__uint_as_float(bw[j] & 0xffff0000u);
+        }
     }
     return acc;
 }
 
-__device__ __forceinline__ double term_f32(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
-    const float *w = reinterpret_cast<const float *>(lds + off);
-    const float *xx = x.f + g * 256;
+// 64 f32 elements (256 B, 16-aligned), products exact in fp64, ascending
+__device__ __forceinline__ double term_f32(const char *lds, uint32_t off, const ActView &x, uint32_t k) {
+    const float4 *w = reinterpret_cast<const float4 *>(lds + off);
+    const float4 *xx = reinterpret_cast<const float4 *>(x.q + k * ACT_F_CSTRIDE);
     double acc = 0.0;
-    for (int i = 0; i < 256; i++) acc = fma((double)w[i], (double)xx[i], acc);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float4 a = w[i], b = xx[i];
+        acc += (double)a.x * (double)b.x;
+        acc += (double)a.y * (double)b.y;
+        acc += (double)a.z * (double)b.z;
+        acc += (double)a.w * (double)b.w;
+    }
     return acc;
 }
 
-__device__ __forceinline__ double group_term(int type, const char *lds, uint32_t off, const ActView &x, uint32_t g) {
+__device__ __forceinline__ double item_term(int type, const char *tile, uint32_t off, const ActView &x, uint32_t k) {
     switch (type) {
-    case SINTER_Q4_K: return term_q4k(lds + off, x, g);
-    case SINTER_Q6_K: return term_q6k(lds, off, x, g);
-    case SINTER_Q8_0: return term_q80(lds, off, x, g);
-    case SINTER_BF16: return term_bf16(lds, off, x, g);
-    default: return term_f32(lds, off, x, g);
+    case SINTER_Q4_K: return term_q4k(tile + off, x, k);
+    case SINTER_Q6_K: return term_q6k(tile, off, x, k);
+    case SINTER_Q8_0: return term_q80(tile, off, x, k);
+    case SINTER_BF16: return term_bf16(tile, off, x, k);
+    default: return term_f32(tile, off, x, k);
     }
 }
 
-// ------------------------------------------------------------ row ranges
+// ------------------------------------------------------------ row ranges and tiles
 
 // Row cut for workgroup w of n: the global row nearest to byte w*T/n of the
 // concatenated (byte-weighted) row space.
@@ -414,22 +472,116 @@ __device__ __forceinline__ uint32_t row_cut(const sinter_gemv_args &a, const uin
     const uint64_t target = total * w / n;
     uint64_t acc = 0;
     uint32_t rows = 0;
-    for (int s = 0; s < a.n_seg; s++) {
-        const uint64_t sb = (uint64_t)a.seg[s].rows * rb_eff[s];
-        if (target < acc + sb) return rows + (uint32_t)((target - acc + rb_eff[s] / 2) / rb_eff[s]);
-        acc += sb;
-        rows += a.seg[s].rows;
+#pragma unroll
+    for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
+        if (s < a.n_seg) {
+            const uint64_t sb = (uint64_t)a.seg[s].rows * rb_eff[s];
+            if (target < acc + sb) return rows + (uint32_t)((target - acc + rb_eff[s] / 2) / rb_eff[s]);
+            acc += sb;
+            rows += a.seg[s].rows;
+        }
     }
     return rows;
 }
 
 struct Tile {
-    int seg;
+    uint32_t seg;
     uint32_t r0, nr;           // output rows [r0, r0+nr) of segment seg
     uint32_t skew_a, n16_a;    // range A (w): byte skew in its first uint4, uint4 count
     uint32_t skew_b, n16_b;    // range B (w2, SwiGLU only)
     const uint4 *src_a, *src_b;
 };
+
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// per-segment geometry, read from the payload (scalar loads; no private arrays)
+__device__ __forceinline__ uint32_t seg_rb(const sinter_gemv_args &a, uint32_t s) {
+    return (uint32_t)sinter_row_bytes_dev(a.seg[s].type, a.K);
+}
+__device__ __forceinline__ uint32_t seg_rb_eff(const sinter_gemv_args &a, uint32_t s) {
+    return seg_rb(a, s) * (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
+}
+// segment holding global row grow, and its first global row
+__device__ __forceinline__ uint32_t seg_of(const sinter_gemv_args &a, uint32_t grow, uint32_t &base) {
+    uint32_t s = 0, b = 0;
+    while (s + 1 < a.n_seg && grow >= b + a.seg[s].rows) { b += a.seg[s].rows; s++; }
+    base = b;
+    return s;
+}
+
+// Tile starting at global row grow (caller checks grow < row_hi).
+__device__ __forceinline__ Tile tile_at(const sinter_gemv_args &a, uint32_t grow, uint32_t row_hi) {
+    Tile t;
+    uint32_t base;
+    t.seg = uni(seg_of(a, grow, base));
+    base = uni(base);
+    const sinter_gemv_seg &sg = a.seg[t.seg];
+    const uint32_t rb = seg_rb(a, t.seg);
+    uint32_t nr = (TILE_BYTES - 64) / seg_rb_eff(a, t.seg);
+    // one lane per item: at most BLOCK_THREADS items per tile (a longer row
+    // still gets a tile of its own and is looped over)
+    const uint32_t ipr = a.K / item_elems(sg.type) * (sg.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
+    nr = min(nr, max(1u, BLOCK_THREADS / ipr));
+    const uint32_t seg_end = min(base + sg.rows, row_hi);
+    if (nr > RES_CAP) nr = RES_CAP;
+    if (grow + nr > seg_end) nr = seg_end - grow;
+    nr = uni(nr);
+    t.r0 = grow - base;
+    t.nr = nr;
+    const uintptr_t A = reinterpret_cast<uintptr_t>(sg.w) + (uintptr_t)t.r0 * rb;
+    t.src_a = reinterpret_cast<const uint4 *>(A & ~(uintptr_t)15);
+    t.skew_a = (uint32_t)(A & 15);
+    t.n16_a = (t.skew_a + nr * rb + 15) / 16;
+    if (sg.epi == SINTER_EPI_SWIGLU) {
+        const uintptr_t B = reinterpret_cast<uintptr_t>(sg.w2) + (uintptr_t)t.r0 * rb;
+        t.src_b = reinterpret_cast<const uint4 *>(B & ~(uintptr_t)15);
+        t.skew_b = (uint32_t)(B & 15);
+        t.n16_b = (t.skew_b + nr * rb + 15) / 16;
+    } else {
+        t.src_b = nullptr; t.skew_b = 0; t.n16_b = 0;
+    }
+    return t;
+}
+
+// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at src land at
+// lds_base + 16*l.  Issued from inline asm so the compiler does not treat the
+// pending DMA as aliasing every later LDS read (it would insert vmcnt(0)
+// before them and serialise the pipeline); the tile loop below waits for it
+// explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds_base), "v"(src)
+        : "memory");
+}
+
+// LDS-DMA one tile into a 36 KiB buffer: every wave issues exactly
+// TILE_CPW 1-KiB chunks (lanes past the tile re-read its first 16 bytes into
+// the unused tail of the buffer), so the number of outstanding loads per wave
+// is a compile-time constant and the tile waits below can be partial.
+__device__ __forceinline__ void tile_issue(const Tile &t, char *buf) {
+    const uint32_t w = uni(wave_id()), lane = lane_id();
+    const uint32_t n16 = t.n16_a + t.n16_b;
+    const uint32_t base = (uint32_t)(uintptr_t)(lds_void *)buf;
+#pragma unroll
+    for (uint32_t k = 0; k < TILE_CPW; k++) {
+        const uint32_t j = w + 4 * k;
+        const uint32_t idx = j * 64 + lane;
+        const uint4 *src = idx < t.n16_a ? t.src_a + idx : (idx < n16 ? t.src_b + (idx - t.n16_a) : t.src_a);
+        lds_dma16(src, uni(base + j * 1024));
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------ the op
 
@@ -439,199 +591,205 @@ __device__ __forceinline__ bool gemv_args_ok(const sinter_gemv_args &a) {
     if (a.n_seg < 1 || a.n_seg > SINTER_GEMV_MAX_SEG) return false;
     if (a.K == 0 || (a.K & 255u) != 0) return false;
     const int vt = vec_dot_type(a.seg[0].type);
-    const uint32_t need = vt == SINTER_Q8_K ? a.K + (a.K / 256) * 4 + (a.K / 16) * 2
-                        : vt == SINTER_Q8_0 ? a.K + (a.K / 32) * 4
-                        : vt == SINTER_BF16 ? a.K * 2 : a.K * 4;
-    if (need > QBUF_BYTES) return false;
+    if (act_bytes(vt, a.K) > QBUF_BYTES) return false;
     if (a.pro == SINTER_PRO_GATED && (a.gn_log2d < 2 || a.gn_log2d > 8)) return false;
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
         if (vec_dot_type(g.type) != vt) return false;
         const uint32_t rbe = (uint32_t)sinter_row_bytes_dev(g.type, a.K) * (g.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
         if (rbe == 0 || rbe > TILE_BYTES - 64) return false;
-        if ((a.K / 256) * (g.epi == SINTER_EPI_SWIGLU ? 2u : 1u) > BLOCK_THREADS) return false;
+        if ((a.K / item_elems(g.type)) * (g.epi == SINTER_EPI_SWIGLU ? 2u : 1u) > CB_CAP) return false;
         if (g.epi == SINTER_EPI_CONV && (g.dconv < 2 || g.dconv > 8)) return false;
     }
     return true;
 }
 
-__device__ void op_gemv(const sinter_instr &ins, char *lds, unsigned *err) {
-    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(ins.payload);
-    const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
+// Apply the epilogues to the buffered rows [row0, row0 + n) and store them;
+// greedy-argmax candidates fold into (bv, bi).  All threads.
+__device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
+    for (uint32_t i = threadIdx.x; i < n; i += BLOCK_THREADS) {
+        const uint32_t grow = row0 + i;
+        uint32_t base;
+        const uint32_t s = seg_of(a, grow, base);
+        const sinter_gemv_seg &sg = a.seg[s];
+        const uint32_t r = grow - base;
+        const float dot = g_res[2 * i];
+        float y = dot;
+        if (sg.epi == SINTER_EPI_SWIGLU) {
+            y = dev_silu(dot) * g_res[2 * i + 1];
+        } else if (sg.epi == SINTER_EPI_RESID) {
+            y = sg.aux[r] + dot;
+        } else if (sg.epi == SINTER_EPI_CONV) {
+            // causal conv over {state[0..dc-2], dot}, fp64 sum rounded once,
+            // then silu; the state shifts by one tap (this block owns row r)
+            const uint32_t dc = sg.dconv;
+            float *st = sg.aux + (size_t)r * (dc - 1);
+            const float *cw = static_cast<const float *>(sg.w2) + (size_t)r * dc;
+            float win[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) win[j] = (j + 1 < dc) ? st[j] : 0.0f;
+            double cacc = 0.0;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) {
+                const float wv = (j + 1 < dc) ? win[j] : (j + 1 == dc ? dot : 0.0f);
+                if (j < dc) cacc += (double)wv * (double)cw[j];
+            }
+            y = dev_silu((float)cacc);
+#pragma unroll
+            for (uint32_t j = 0; j < 7; j++)
+                if (j + 1 < dc) st[j] = (j + 2 < dc) ? win[j + 1] : dot;
+        } else if (sg.epi == SINTER_EPI_ARGMAX) {
+            if (y > bv || (y == bv && (int32_t)r < bi)) { bv = y; bi = (int32_t)r; }
+        }
+        sg.y[r] = y;
+    }
+}
+
+// Compute one landed tile: one lane per (virtual row, item) writes the item
+// term to LDS, then one lane per virtual row sums its terms in ascending
+// order.  A SwiGLU tile has nr gate rows then nr up rows.  Row results go to
+// g_res[2*(slot0 + row) + {0: gate/plain, 1: up}].
+template <int TYPE>
+__device__ __forceinline__ void tile_compute_t(const Tile &t, const char *buf, uint32_t ipr, uint32_t nv,
+                                               uint32_t rb, uint32_t slot0, const ActView &x) {
+    const uint32_t ib = item_bytes(TYPE);
+    const uint32_t n_items = nv * ipr;
+    for (uint32_t it = threadIdx.x; it < n_items; it += BLOCK_THREADS) {
+        const uint32_t v = it / ipr, k = it - v * ipr;
+        const uint32_t roff = v < t.nr ? t.skew_a + v * rb : t.n16_a * 16 + t.skew_b + (v - t.nr) * rb;
+        g_cb[it] = item_term(TYPE, buf, roff + k * ib, x, k);
+    }
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    for (uint32_t v = threadIdx.x; v < nv; v += BLOCK_THREADS) {
+        double s = 0.0;
+        for (uint32_t k = 0; k < ipr; k++) s += g_cb[v * ipr + k];
+        const uint32_t row = v < t.nr ? v : v - t.nr;
+        g_res[2 * (slot0 + row) + (v < t.nr ? 0 : 1)] = (float)s;
+    }
+}
+
+__device__ __forceinline__ void tile_compute(const sinter_gemv_args &a, const Tile &t, const char *buf,
+                                          uint32_t slot0, const ActView &x) {
+    const sinter_gemv_seg &sg = a.seg[t.seg];
+    const int type = (int)uni(sg.type);
+    const uint32_t ipr = a.K / item_elems(type);
+    const uint32_t nv = t.nr * (sg.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
+    const uint32_t rb = uni(seg_rb(a, t.seg));
+    switch (type) {
+    case SINTER_Q4_K: tile_compute_t<SINTER_Q4_K>(t, buf, ipr, nv, rb, slot0, x); break;
+    case SINTER_Q6_K: tile_compute_t<SINTER_Q6_K>(t, buf, ipr, nv, rb, slot0, x); break;
+    case SINTER_Q8_0: tile_compute_t<SINTER_Q8_0>(t, buf, ipr, nv, rb, slot0, x); break;
+    case SINTER_BF16: tile_compute_t<SINTER_BF16>(t, buf, ipr, nv, rb, slot0, x); break;
+    default: tile_compute_t<SINTER_F32>(t, buf, ipr, nv, rb, slot0, x); break;
+    }
+}
+
+__device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
+    if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
+        reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
+    __syncthreads();
+    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
+    const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
     if (!gemv_args_ok(a)) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
         return;
     }
-    const uint32_t K = a.K, G = K / 256;
-    double *red = reinterpret_cast<double *>(lds);
-    char *qbuf = lds + RED_BYTES;
-    char *tbuf0 = qbuf + QBUF_BYTES;
-    char *tbuf1 = tbuf0 + TILE_BYTES;
-    double *cb = reinterpret_cast<double *>(tbuf1 + TILE_BYTES);
-    float *rowv = reinterpret_cast<float *>(cb + 256);      // per-tile row results
+    const uint32_t K = a.K;
     const int vt = vec_dot_type(a.seg[0].type);
-
-    // byte-weighted row space
-    uint32_t rb[SINTER_GEMV_MAX_SEG], rb_eff[SINTER_GEMV_MAX_SEG];
+    uint32_t rb_eff[SINTER_GEMV_MAX_SEG];
     uint64_t total = 0;
-    for (int s = 0; s < a.n_seg; s++) {
-        rb[s] = (uint32_t)sinter_row_bytes_dev(a.seg[s].type, K);
-        rb_eff[s] = rb[s] * (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
-        total += (uint64_t)a.seg[s].rows * rb_eff[s];
+#pragma unroll
+    for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
+        rb_eff[s] = s < a.n_seg ? seg_rb_eff(a, s) : 0u;
+        total += s < a.n_seg ? (uint64_t)a.seg[s].rows * rb_eff[s] : 0ull;
     }
-    const uint32_t row_lo = row_cut(a, rb_eff, total, rel, nblk);
-    const uint32_t row_hi = row_cut(a, rb_eff, total, rel + 1, nblk);
+    const uint32_t row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
+    const uint32_t row_hi = uni(row_cut(a, rb_eff, total, rel + 1, nblk));
 
-    // tile iterator over [row_lo, row_hi) of the concatenated row space
-    auto make_tile = [&](uint32_t grow, Tile &t) -> bool {
-        if (grow >= row_hi) return false;
-        uint32_t base = 0;
-        int s = 0;
-        while (s < a.n_seg && grow >= base + a.seg[s].rows) { base += a.seg[s].rows; s++; }
-        const sinter_gemv_seg &sg = a.seg[s];
-        const bool sw = sg.epi == SINTER_EPI_SWIGLU;
-        const uint32_t items_per_row = G * (sw ? 2u : 1u);
-        uint32_t nr = BLOCK_THREADS / items_per_row;
-        const uint32_t by_bytes = (TILE_BYTES - 64) / rb_eff[s];
-        if (by_bytes < nr) nr = by_bytes;
-        const uint32_t seg_end = base + sg.rows < row_hi ? base + sg.rows : row_hi;
-        if (grow + nr > seg_end) nr = seg_end - grow;
-        t.seg = s;
-        t.r0 = grow - base;
-        t.nr = nr;
-        const uintptr_t A = reinterpret_cast<uintptr_t>(sg.w) + (uintptr_t)t.r0 * rb[s];
-        t.src_a = reinterpret_cast<const uint4 *>(A & ~(uintptr_t)15);
-        t.skew_a = (uint32_t)(A & 15);
-        t.n16_a = (t.skew_a + nr * rb[s] + 15) / 16;
-        if (sw) {
-            const uintptr_t B = reinterpret_cast<uintptr_t>(sg.w2) + (uintptr_t)t.r0 * rb[s];
-            t.src_b = reinterpret_cast<const uint4 *>(B & ~(uintptr_t)15);
-            t.skew_b = (uint32_t)(B & 15);
-            t.n16_b = (t.skew_b + nr * rb[s] + 15) / 16;
-        } else {
-            t.src_b = nullptr; t.skew_b = 0; t.n16_b = 0;
-        }
-        return true;
-    };
-
-    uint4 stage[MAX_LD];
-    auto issue = [&](const Tile &t) {
-#pragma unroll
-        for (int k = 0; k < MAX_LD; k++) {
-            const uint32_t i = threadIdx.x + k * BLOCK_THREADS;
-            if (i < t.n16_a) stage[k] = t.src_a[i];
-            else if (i < t.n16_a + t.n16_b) stage[k] = t.src_b[i - t.n16_a];
-        }
-    };
-    auto commit = [&](const Tile &t, char *buf) {
-#pragma unroll
-        for (int k = 0; k < MAX_LD; k++) {
-            const uint32_t i = threadIdx.x + k * BLOCK_THREADS;
-            if (i < t.n16_a + t.n16_b) reinterpret_cast<uint4 *>(buf)[i] = stage[k];
-        }
-    };
-
-    Tile cur{}, nxt{};
-    bool have = make_tile(row_lo, cur);
-    if (have) issue(cur);   // first weight loads overlap the prologue
+    // Three-buffer rotation over tiles identified by their first row (the
+    // geometry is recomputed).  X = tile being computed (buffer bx), Y = the
+    // next tile, already in flight.  Before computing X each wave waits for
+    // its own DMA into X -- Y's TILE_CPW loads may stay outstanding -- and a
+    // barrier makes every wave's chunks visible; after the compute a barrier
+    // frees buffer bx+2 (computed last step) for the tile after Y.
+    uint32_t gx = row_lo, gy = 0, next = row_lo, bx = 0;
+    bool hx = gx < row_hi, hy = false;
+    if (hx) { const Tile t = tile_at(a, gx, row_hi); next += t.nr; tile_issue(t, g_tiles); }
+    if (hx && next < row_hi) {
+        gy = next; hy = true;
+        const Tile t = tile_at(a, gy, row_hi); next += t.nr; tile_issue(t, g_tiles + TILE_BYTES);
+    }
 
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
-    gemv_prologue(a, vt, write_x, qbuf, red, err);
-    const ActView xv = act_view(qbuf, K, vt);
+    gemv_prologue(a, vt, write_x, g_qbuf, g_red, err);   // ends with __syncthreads()
+    const ActView x = act_view(g_qbuf, K, vt);
 
-    // greedy argmax state (thread 0 of the block)
-    float best_v = -INFINITY;
-    int32_t best_i = 0x7fffffff;
-
-    if (have) commit(cur, tbuf0);
-    __syncthreads();
-    int bi = 0;
-    uint32_t grow = row_lo;
-    while (have) {
-        char *buf = bi ? tbuf1 : tbuf0;
-        const bool more = make_tile(grow + cur.nr, nxt);
-        if (more) issue(nxt);
-        const sinter_gemv_seg &sg = a.seg[cur.seg];
-        const bool sw = sg.epi == SINTER_EPI_SWIGLU;
-        const uint32_t per = G * (sw ? 2u : 1u);
-        const uint32_t n_items = cur.nr * per;
-        const uint32_t gb = group_bytes(sg.type);
-        const uint32_t rbs = rb[cur.seg];
-        for (uint32_t it = threadIdx.x; it < n_items; it += BLOCK_THREADS) {
-            const uint32_t rr = it / per, k = it - rr * per;
-            const bool up = k >= G;
-            const uint32_t g = up ? k - G : k;
-            const uint32_t off = up ? (cur.n16_a * 16 + cur.skew_b + rr * rbs + g * gb)
-                                    : (cur.skew_a + rr * rbs + g * gb);
-            cb[it] = group_term(sg.type, buf, off, xv, g);
-        }
-        __syncthreads();
-        // row results: ascending fp64 sum of the group terms
-        if (threadIdx.x < cur.nr) {
-            const uint32_t rr = threadIdx.x, r = cur.r0 + rr;
-            double acc = 0.0;
-            for (uint32_t g = 0; g < G; g++) acc += cb[rr * per + g];
-            const float dot = (float)acc;
-            float y = dot;
-            if (sw) {
-                double acc2 = 0.0;
-                for (uint32_t g = 0; g < G; g++) acc2 += cb[rr * per + G + g];
-                y = dev_silu(dot) * (float)acc2;
-            } else if (sg.epi == SINTER_EPI_RESID) {
-                y = sg.aux[r] + dot;
-            } else if (sg.epi == SINTER_EPI_CONV) {
-                // causal conv over {state[0..dc-2], dot}, fp64 sum rounded once,
-                // then silu; the state shifts by one tap (this block owns row r)
-                const uint32_t dc = sg.dconv;
-                float *st = sg.aux + (size_t)r * (dc - 1);
-                const float *cw = static_cast<const float *>(sg.w2) + (size_t)r * dc;
-                float win[8];
-                for (uint32_t j = 0; j + 1 < dc; j++) win[j] = st[j];
-                win[dc - 1] = dot;
-                double cacc = 0.0;
-                for (uint32_t j = 0; j < dc; j++) cacc += (double)win[j] * (double)cw[j];
-                y = dev_silu((float)cacc);
-                for (uint32_t j = 0; j + 1 < dc; j++) st[j] = win[j + 1];
-            }
-            sg.y[r] = y;
-            rowv[rr] = y;
-        }
-        if (sg.epi == SINTER_EPI_ARGMAX) {
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+    uint32_t res_row0 = row_lo, res_n = 0;
+    while (hx) {
+        const Tile t = tile_at(a, gx, row_hi);
+        if (res_n + t.nr > RES_CAP) {
             __syncthreads();
-            if (threadIdx.x == 0) {
-                for (uint32_t rr = 0; rr < cur.nr; rr++) {
-                    const float v = rowv[rr];
-                    if (v > best_v) { best_v = v; best_i = (int32_t)(cur.r0 + rr); }
-                }
-            }
+            gemv_flush(a, res_row0, res_n, bv, bi);
+            res_row0 += res_n;
+            res_n = 0;
+            __syncthreads();
         }
-        if (more) commit(nxt, bi ? tbuf0 : tbuf1);
-        __syncthreads();
-        grow += cur.nr;
-        cur = nxt;
-        have = more;
-        bi ^= 1;
+        if (hy) wait_vmcnt<TILE_CPW>(); else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        tile_compute(a, t, g_tiles + bx * TILE_BYTES, res_n, x);
+        res_n += t.nr;
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+        const uint32_t bz = bx == 0 ? 2u : bx - 1;
+        bool hz = hy && next < row_hi;
+        uint32_t gz = 0;
+        if (hz) { gz = next; const Tile tz = tile_at(a, gz, row_hi); next += tz.nr; tile_issue(tz, g_tiles + bz * TILE_BYTES); }
+        gx = gy; hx = hy; gy = gz; hy = hz;
+        bx = bx == 2 ? 0u : bx + 1;
     }
+    __syncthreads();
+    gemv_flush(a, res_row0, res_n, bv, bi);
 
-    // greedy argmax: last-arriving block reduces the per-block partials
+    // greedy argmax: block-local best, then the last-arriving block reduces
     bool any_argmax = false;
     for (int s = 0; s < a.n_seg; s++) any_argmax |= a.seg[s].epi == SINTER_EPI_ARGMAX;
+    if (any_argmax) {
+        // block reduction of (value, index): larger value, then smaller index
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int32_t oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        float *rv = reinterpret_cast<float *>(g_part);
+        int32_t *ri = reinterpret_cast<int32_t *>(g_part + 4);
+        __syncthreads();
+        if (lane_id() == 0) { rv[wave_id()] = bv; ri[wave_id()] = bi; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < (int)(BLOCK_THREADS / 64); w++)
+                if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) { bv = rv[w]; bi = ri[w]; }
+        }
+    }
     if (any_argmax && threadIdx.x == 0 && rel >= static_cast<sinter_argmax_ws *>(a.epi_ws)->capacity) {
         raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
     } else if (any_argmax && threadIdx.x == 0) {
         sinter_argmax_ws *ws = static_cast<sinter_argmax_ws *>(a.epi_ws);
-        ws->part_val[rel] = best_v;
-        ws->part_idx[rel] = best_i;
+        ws->part_val[rel] = bv;
+        ws->part_idx[rel] = bi;
         fence_release_agent();
         const unsigned old = __hip_atomic_fetch_add(ws->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == nblk - 1) {
             fence_acquire_agent();
-            float bv = -INFINITY;
+            float best = -INFINITY;
             int32_t bidx = 0x7fffffff;
             for (uint32_t w = 0; w < nblk; w++) {
                 const float v = __hip_atomic_load(ws->part_val + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const int32_t i = __hip_atomic_load(ws->part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (v > bv || (v == bv && i < bidx)) { bv = v; bidx = i; }
+                if (v > best || (v == best && i < bidx)) { best = v; bidx = i; }
             }
             sinter_pass_cell *pc = reinterpret_cast<sinter_pass_cell *>(ws->pass_cell);
             if (ws->history && (uint32_t)pc->steps < ws->history_cap) ws->history[pc->steps] = bidx;

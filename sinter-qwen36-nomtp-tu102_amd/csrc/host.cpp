@@ -43,19 +43,45 @@ bool hip_ok(hipError_t e, const char *what) {
     return false;
 }
 
-unsigned *op_err_cell() {
+// Per-device state of the standalone op entry points: the error cell and a
+// ring of instruction slots (an op reads its instruction from device memory,
+// as the interpreter does).  A slot is reused after OP_RING launches; the
+// copy into it is ordered on the caller's stream.
+constexpr unsigned OP_RING = 256;
+struct OpDev {
+    unsigned *err = nullptr;
+    sinter_instr *ring = nullptr;
+    unsigned next = 0;
+};
+
+static OpDev *op_dev() {
     static std::mutex mu;
-    static std::map<int, unsigned *> cells;
+    static std::map<int, OpDev> devs;
     int dev = 0;
-    if (!hip_ok(hipGetDevice(&dev), "op error cell: hipGetDevice")) return nullptr;
+    if (!hip_ok(hipGetDevice(&dev), "op state: hipGetDevice")) return nullptr;
     std::lock_guard<std::mutex> lk(mu);
-    auto it = cells.find(dev);
-    if (it != cells.end()) return it->second;
-    unsigned *p = nullptr;
-    if (!hip_ok(hipMalloc(&p, 256), "op error cell: hipMalloc")) return nullptr;
-    if (!hip_ok(hipMemset(p, 0, 256), "op error cell: hipMemset")) return nullptr;
-    cells[dev] = p;
-    return p;
+    OpDev &d = devs[dev];
+    if (!d.err) {
+        char *p = nullptr;
+        if (!hip_ok(hipMalloc(&p, 256 + OP_RING * sizeof(sinter_instr)), "op state: hipMalloc")) return nullptr;
+        if (!hip_ok(hipMemset(p, 0, 256), "op state: hipMemset")) return nullptr;
+        d.err = reinterpret_cast<unsigned *>(p);
+        d.ring = reinterpret_cast<sinter_instr *>(p + 256);
+    }
+    return &d;
+}
+
+unsigned *op_err_cell() {
+    OpDev *d = op_dev();
+    return d ? d->err : nullptr;
+}
+
+sinter_instr *op_instr_slot() {
+    OpDev *d = op_dev();
+    if (!d) return nullptr;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lk(mu);
+    return d->ring + (d->next++ % OP_RING);
 }
 
 static bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -73,9 +99,9 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
     if (a.K == 0 || a.K % 256) return bad("K must be a positive multiple of 256");
     const int vt = vdot(a.seg[0].type);
     if (vt < 0) return bad("unsupported weight type");
-    const uint64_t need = vt == SINTER_Q8_K ? a.K + (a.K / 256) * 4 + (a.K / 16) * 2
-                        : vt == SINTER_Q8_0 ? a.K + (a.K / 32) * 4
-                        : vt == SINTER_BF16 ? (uint64_t)a.K * 2 : (uint64_t)a.K * 4;
+    const uint64_t need = vt == SINTER_Q8_K ? (uint64_t)(a.K / 256) * 276 + (a.K / 16) * 2
+                        : vt == SINTER_Q8_0 ? (uint64_t)(a.K / 256) * 272 + (a.K / 32) * 4
+                        : vt == SINTER_BF16 ? (uint64_t)(a.K / 64) * 144 : (uint64_t)(a.K / 64) * 272;
     if (need > QBUF_BYTES) return bad("K too large for the activation buffer");
     switch (a.pro) {
     case SINTER_PRO_PLAIN:
@@ -103,7 +129,8 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
         const bool sw = g.epi == SINTER_EPI_SWIGLU;
         const uint64_t rbe = sinter_row_bytes_dev(g.type, a.K) * (sw ? 2 : 1);
         if (rbe > TILE_BYTES - 64) return bad("row too long for one LDS tile");
-        if ((a.K / 256) * (sw ? 2u : 1u) > BLOCK_THREADS) return bad("too many groups per row");
+        const uint32_t ie = (g.type == SINTER_BF16 || g.type == SINTER_F32) ? 64u : 256u;
+        if ((a.K / ie) * (sw ? 2u : 1u) > CB_CAP) return bad("row has too many items for one tile");
         switch (g.epi) {
         case SINTER_EPI_STORE: break;
         case SINTER_EPI_RESID: if (!g.aux) return bad("resid: aux"); break;
@@ -129,7 +156,11 @@ static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
     ins.block_lo = 0;
     ins.block_hi = (uint16_t)blocks;
     std::memcpy(ins.payload, &args, sizeof args);
-    if (!hip_ok(launch_op(ins, blocks, err, (hipStream_t)stream), "op launch")) return SINTER_ERR_HIP;
+    sinter_instr *slot = op_instr_slot();
+    if (!slot) return SINTER_ERR_HIP;
+    if (!hip_ok(hipMemcpyAsync(slot, &ins, sizeof ins, hipMemcpyHostToDevice, (hipStream_t)stream), "op upload"))
+        return SINTER_ERR_HIP;
+    if (!hip_ok(launch_op(slot, blocks, err, (hipStream_t)stream), "op launch")) return SINTER_ERR_HIP;
     return SINTER_OK;
 }
 
@@ -524,7 +555,7 @@ int sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
     if (blocks) *blocks = h->blocks;
     if (threads) *threads = BLOCK_THREADS;
-    if (lds_bytes) *lds_bytes = LDS_BYTES;
+    if (lds_bytes) *lds_bytes = 3 * TILE_BYTES + QBUF_BYTES + 2 * RES_CAP * 4 + 256;
     return SINTER_OK;
 }
 

@@ -21,7 +21,7 @@ struct InterpCtl {
     uint32_t pass_base;
 };
 
-hipError_t launch_op(const sinter_instr &ins, uint32_t blocks, unsigned *err, hipStream_t s);
+hipError_t launch_op(const sinter_instr *ins_dev, uint32_t blocks, unsigned *err, hipStream_t s);
 hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s);
 hipError_t interp_max_blocks(int *blocks_per_cu);
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
@@ -31,6 +31,8 @@ hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_
 int set_error(int status, const char *fmt, ...);
 bool hip_ok(hipError_t e, const char *what);
 unsigned *op_err_cell();  // per-device error cell of the standalone op launches
+// next slot of the per-device ring of standalone-op instructions (device memory)
+sinter_instr *op_instr_slot();
 int validate_gemv(const sinter_gemv_args &a, const char **why);
 
 }  // namespace sinter

@@ -29,11 +29,11 @@ __device__ __forceinline__ bool kind_wired(unsigned k) {
            k == SINTER_OP_GDN_STEP || k == SINTER_OP_ATTN_DECODE;
 }
 
-__device__ __forceinline__ void dispatch(const sinter_instr &ins, char *lds, unsigned *err) {
+__device__ __forceinline__ void dispatch(const sinter_instr &ins, unsigned *err) {
     switch (ins.kind) {
-    case SINTER_OP_GEMV: op_gemv(ins, lds, err); break;
-    case SINTER_OP_GDN_STEP: op_gdn_step(ins, lds, err); break;
-    case SINTER_OP_ATTN_DECODE: op_attn_decode(ins, lds, err); break;
+    case SINTER_OP_GEMV: op_gemv(ins, err); break;
+    case SINTER_OP_GDN_STEP: op_gdn_step(ins, err); break;
+    case SINTER_OP_ATTN_DECODE: op_attn_decode(ins, err); break;
     default: break;
     }
 }
@@ -74,7 +74,6 @@ using namespace sinter;
 
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
 sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
-    extern __shared__ __attribute__((aligned(16))) char lds[];
     unsigned epoch = 0;
     for (uint32_t pass = 0; pass < ctl.n_passes; ++pass) {
         const uint64_t t0 = wall_clock64();
@@ -82,7 +81,10 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             const sinter_instr &ins = prog[i];
             const unsigned kind = ins.kind;
             if (kind == SINTER_OP_BOUNDARY) {
+                const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
                 if (!grid_barrier(ctl.bar, epoch, ctl.spin_limit, ctl.err)) return;
+                if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
+                    ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(wall_clock64() - s);
                 continue;
             }
             if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
@@ -93,10 +95,10 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
                 if (ctl.op_cycles && blockIdx.x == 0) {
                     const uint64_t s = wall_clock64();
-                    dispatch(ins, lds, ctl.err);
+                    dispatch(ins, ctl.err);
                     if (threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
                 } else {
-                    dispatch(ins, lds, ctl.err);
+                    dispatch(ins, ctl.err);
                 }
             }
         }
@@ -112,14 +114,13 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
 }
 
 // One instruction over the whole (non-cooperative) grid: the standalone op
-// entry points.  Ops that need cross-block results use last-arriver counters,
+// entry points.  The instruction sits in device memory like a program entry,
+// so ops index its payload with ordinary loads.  Ops that need cross-block results use last-arriver counters,
 // never a grid barrier, so co-residency is not required here.
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
-sinter_op_kernel(sinter_instr ins, unsigned *err) {
-    extern __shared__ __attribute__((aligned(16))) char lds[];
-    ins.block_lo = 0;
-    ins.block_hi = (uint16_t)gridDim.x;
-    dispatch(ins, lds, err);
+sinter_op_kernel(const sinter_instr *__restrict__ ins, unsigned *err) {
+    // the host sets block_lo = 0, block_hi = gridDim.x
+    dispatch(*ins, err);
 }
 
 // Synthetic tensor fill: one thread per 256-element group (weights) or per
@@ -146,43 +147,21 @@ extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type,
 
 namespace sinter {
 
-hipError_t launch_op(const sinter_instr &ins, uint32_t blocks, unsigned *err, hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)sinter_op_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), LDS_BYTES, s, ins, err);
+hipError_t launch_op(const sinter_instr *ins_dev, uint32_t blocks, unsigned *err, hipStream_t s) {
+    hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), 0, s, ins_dev, err);
     return hipGetLastError();
 }
 
 hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)sinter_interp,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
     InterpCtl c = ctl;
     const sinter_instr *p = prog;
     void *args[] = {(void *)&p, (void *)&c};
-    return hipLaunchCooperativeKernel((const void *)sinter_interp, dim3(blocks), dim3(BLOCK_THREADS), args,
-                                      LDS_BYTES, s);
+    return hipLaunchCooperativeKernel((const void *)sinter_interp, dim3(blocks), dim3(BLOCK_THREADS), args, 0, s);
 }
 
 hipError_t interp_max_blocks(int *blocks_per_cu) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)sinter_interp,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void *)sinter_interp,
-                                                        BLOCK_THREADS, LDS_BYTES);
+                                                        BLOCK_THREADS, 0);
 }
 
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,

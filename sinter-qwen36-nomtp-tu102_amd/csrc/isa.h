@@ -16,20 +16,18 @@ static_assert(sizeof(sinter_gemv_seg) == 40, "gemv segment");
 namespace sinter {
 
 // Launch envelope of the cooperative interpreter: one 256-thread workgroup
-// (4 wave64) per CU, the whole 160 KiB LDS of the CU available to it.
+// (4 wave64) per CU; all LDS is static (lds.h), 152 KiB of the CU's 160 KiB.
 constexpr unsigned BLOCK_THREADS = 256;
-constexpr unsigned LDS_BYTES = 152u * 1024u;
 
-// LDS map used by the GEMV op (bytes):
-//   [0, 64)              reduction scratch (8 doubles)
-//   [64, 64+QBUF)        quantised activation (int8 codes, scales, bsums)
-//   then two weight tile buffers of TILE_BYTES each, then per-block terms.
-constexpr unsigned RED_BYTES = 128;
-constexpr unsigned QBUF_BYTES = 36u * 1024u;   // Q8_K K<=17408: 19856 B; BF16 K<=17408: 34816 B
-constexpr unsigned TILE_BYTES = 52u * 1024u;
-constexpr unsigned CB_BYTES = 256u * 8u;       // one fp64 term per (row, block) item
-constexpr unsigned ROWV_BYTES = 256u * 4u;
-static_assert(RED_BYTES + QBUF_BYTES + 2 * TILE_BYTES + CB_BYTES + ROWV_BYTES <= LDS_BYTES, "lds map");
+// GEMV LDS: three 36 KiB weight-tile buffers filled by LDS-DMA, each wave
+// issuing TILE_CPW 1 KiB chunks per tile; the quantised activation; the
+// buffered row results.
+constexpr unsigned TILE_BYTES = 36u * 1024u;
+constexpr unsigned TILE_CPW = TILE_BYTES / 1024u / (BLOCK_THREADS / 64u);
+constexpr unsigned QBUF_BYTES = 40u * 1024u;   // padded activation: Q8_K K=17408 20944 B; BF16 K=17408 39168 B
+constexpr unsigned RES_CAP = 512u;             // rows buffered before the epilogue runs
+constexpr unsigned CB_CAP = 512u;              // item terms of one tile (rows of up to 512 items)
+static_assert(TILE_CPW * 4u * 1024u == TILE_BYTES, "tile = whole chunks per wave");
 
 // bytes of one row of k elements of a ggml type
 __host__ __device__ inline size_t sinter_row_bytes_dev(int t, int64_t k) {
