@@ -661,9 +661,20 @@ __device__ __forceinline__ void tile_compute_t(const Tile &t, const char *buf, u
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
+    // ascending fold of each row's terms; the terms are fetched 8 at a time
+    // (one LDS round trip per 8) before the dependent fp64 adds
     for (uint32_t v = threadIdx.x; v < nv; v += BLOCK_THREADS) {
+        const double *c = g_cb + v * ipr;
         double s = 0.0;
-        for (uint32_t k = 0; k < ipr; k++) s += g_cb[v * ipr + k];
+        uint32_t k = 0;
+        for (; k + 8 <= ipr; k += 8) {
+            double b[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) b[i] = c[k + i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) s += b[i];
+        }
+        for (; k < ipr; k++) s += c[k];
         const uint32_t row = v < t.nr ? v : v - t.nr;
         g_res[2 * (slot0 + row) + (v < t.nr ? 0 : 1)] = (float)s;
     }
