@@ -18,6 +18,11 @@
 namespace sinter {
 
 typedef __attribute__((address_space(3))) void lds_void;
+// Explicit LDS (address space 3) pointers: a generic pointer into LDS makes
+// the compiler emit flat loads, which also count against vmcnt and so wait
+// for every in-flight LDS-DMA load.
+#define LDS __attribute__((address_space(3)))
+typedef LDS char lds_char;
 
 // ---------------------------------------------------------------- static LDS
 // g_tiles: the GEMV's three LDS-DMA tile buffers (other ops use the space as
@@ -27,7 +32,7 @@ __shared__ __attribute__((aligned(16))) char g_qbuf[QBUF_BYTES];
 __shared__ float g_res[2 * RES_CAP];
 __shared__ double g_red[16];
 __shared__ double g_part[16];
-__shared__ double g_cb[CB_CAP];           // GEMV item terms of the current tile
+__shared__ double g_cb[CB_CAP];           // GEMV item terms of the last two tiles
 // the running op's payload, copied out of the program once per op so that
 // reading it never waits behind tile LDS-DMA (lgkmcnt, not vmcnt)
 __shared__ __attribute__((aligned(16))) unsigned char g_args[240];

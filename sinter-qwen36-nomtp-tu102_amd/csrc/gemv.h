@@ -11,19 +11,19 @@
 //
 // Work split: the rows of all segments form one byte-weighted row space; the
 // participating workgroups take contiguous, byte-balanced row ranges.  A
-// workgroup streams its rows through three 36 KiB LDS tiles with gfx950
+// workgroup streams its share through three 36 KiB LDS tiles with gfx950
 // LDS-DMA (global_load_lds_dwordx4: 16 B per lane straight into LDS, no
-// VGPRs), two tiles in flight while one is computed; compute reads the
-// (arbitrarily aligned) ggml blocks from LDS, one wave per row, lanes over
-// 32-element units, and a wave-wide fp64 sum per row.  Row results stay in
-// LDS; the epilogues run once over the block's rows at the end.
+// VGPRs), two tiles in flight while one is computed.  A tile is a run of
+// whole items (ggml blocks) that ignores row boundaries, sized so that every
+// lane of the workgroup has one item (or half of one) per tile; item terms go
+// to an LDS ring, and one tile later the lanes that own the touched rows add
+// them to per-row running sums.  One workgroup barrier per tile.  Row results
+// stay in LDS; the epilogues run over the buffered rows.
 //
 // Declared numerics (oracle/oracle.c): integer block dots are exact; each
-// unit's term is an fp64 expression of exact integers and the f16/f32
-// scales; a row is the fp64 sum of its terms rounded to fp32 once.  The
-// oracle sums in ascending order, the kernel in wave order; both round the
-// same ~1e-16-accurate fp64 value, so outputs agree to the last bit except
-// with probability ~1e-8 per row (1 ulp then).
+// item's term is an fp64 expression of exact integers and the f16/f32
+// scales; a row is the ascending fp64 sum of its item terms, rounded to fp32
+// once, so outputs are bit-identical to the oracle's.
 #pragma once
 #include "dev_common.h"
 
@@ -59,32 +59,18 @@ __device__ __forceinline__ uint16_t lds_u16(const char *lds, uint32_t off) {
 }
 
 // ------------------------------------------------------------ activation layout in LDS
-// Padded so that lanes working on different groups/chunks start on
-// different LDS banks (an unpadded 256-byte group stride puts every group on
-// bank 0 and serialises the activation reads):
-//   Q8_K: int8 codes, group g at g*ACT_GSTRIDE | d f32[G] | bsums i16[16G]
-//   Q8_0: int8 codes, group g at g*ACT_GSTRIDE | d f32[K/32] (f16-rounded)
-//   BF16: 64-element chunk c at c*ACT_BF_CSTRIDE (u16)
-//   F32:  64-element chunk c at c*ACT_F_CSTRIDE
-constexpr uint32_t ACT_GSTRIDE = 272;
-constexpr uint32_t ACT_BF_CSTRIDE = 144;
-constexpr uint32_t ACT_F_CSTRIDE = 272;
-__host__ __device__ inline uint32_t act_bytes(int vt, uint32_t K) {
-    if (vt == SINTER_Q8_K) return (K / 256) * ACT_GSTRIDE + (K / 256) * 4 + (K / 16) * 2;
-    if (vt == SINTER_Q8_0) return (K / 256) * ACT_GSTRIDE + (K / 32) * 4;
-    if (vt == SINTER_BF16) return (K / 64) * ACT_BF_CSTRIDE;
-    return (K / 64) * ACT_F_CSTRIDE;
-}
+// (ACT_* constants and act_bytes are in isa.h, shared with host validation)
 struct ActView {
-    const char *q;       // codes / bf16 / f32 chunks
-    const float *d;
-    const int16_t *bs;
+    const lds_char *q;   // codes / bf16 / f32 chunks
+    const LDS float *d;
+    const LDS int16_t *bs;
 };
-__device__ __forceinline__ ActView act_view(char *q, uint32_t K, int vt) {
+__device__ __forceinline__ ActView act_view(char *qg, uint32_t K, int vt) {
+    const lds_char *q = (const lds_char *)qg;
     ActView v{};
     v.q = q;
-    v.d = reinterpret_cast<const float *>(q + (K / 256) * ACT_GSTRIDE);
-    v.bs = reinterpret_cast<const int16_t *>(q + (K / 256) * ACT_GSTRIDE + (K / 256) * 4);
+    v.d = reinterpret_cast<const LDS float *>(q + (K / 256) * ACT_GSTRIDE);
+    v.bs = reinterpret_cast<const LDS int16_t *>(q + act_bs_off(K));
     (void)vt;
     return v;
 }
@@ -183,7 +169,7 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
     const int lane = lane_id();
     const int nw = blockDim.x >> 6;
     float *qd = reinterpret_cast<float *>(q + (K / 256) * ACT_GSTRIDE);
-    int16_t *qb = reinterpret_cast<int16_t *>(q + (K / 256) * ACT_GSTRIDE + (K / 256) * 4);
+    int16_t *qb = reinterpret_cast<int16_t *>(q + act_bs_off(K));
     // one wave per 256-element chunk, 4 consecutive elements per lane
     for (uint32_t c = wave_id(); c < K / 256; c += nw) {
         const uint32_t e = c * 256 + lane * 4;
@@ -284,23 +270,45 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
 // ------------------------------------------------------------ item terms
 // A weight row is a sequence of items: one 256-element group for the
 // quantised types (one Q4_K / Q6_K block, eight Q8_0 blocks), 64 elements
-// for BF16 / F32.  One lane computes one item's term: an fp64 expression of
-// exact integer block dots and the f16/f32 scales (a float sum of exact
-// products for BF16/F32).  A row is the ascending fp64 sum of its item terms,
-// rounded to fp32 once -- the fold oracle/oracle.c declares.
+// for BF16 / F32.  An item's term is an fp64 expression of exact integer
+// block dots and the f16/f32 scales (a float sum of exact products for
+// BF16/F32).  A row is the ascending fp64 sum of its item terms, rounded to
+// fp32 once -- the fold oracle/oracle.c declares.
+//
+// Lanes per item: one for Q4_K / BF16 / F32; two for Q6_K (one 128-element
+// half each, integer partials added exactly) and Q8_0 (blocks 0-3 and 4-7;
+// the second lane continues the first lane's ascending block sum).  The term
+// ends up on the item's last lane.
+//
+// With one wave per SIMD nothing hides LDS latency, so each item function
+// issues all of its LDS reads first and only then computes (a scheduling
+// barrier keeps the compiler from interleaving loads into the arithmetic,
+// which would expose one LDS round trip per use).
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// n words (4 bytes each) at a 2-aligned LDS byte offset
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
+__device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
+__device__ __forceinline__ uint16_t ld_u16(const lds_char *p) { return *reinterpret_cast<const LDS uint16_t *>(p); }
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// The N+1 aligned dwords covering N words at a 2-aligned LDS address, and
+// the byte shift that extracts them (unaligned LDS reads stall the LDS
+// pipeline on gfx950, so reads stay dword-aligned).
 template <int N>
-__device__ __forceinline__ void lds_words(const char *lds, uint32_t off, uint32_t w[N]) {
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(lds + (off & ~3u));
-    const uint32_t sh = off & 3u;
-    uint32_t d[N + 1];
+__device__ __forceinline__ uint32_t ld_span(const lds_char *p, uint32_t d[N + 1]) {
+    const uint32_t off = (uint32_t)(uintptr_t)p;
+    const LDS uint32_t *q = reinterpret_cast<const LDS uint32_t *>(p - (off & 3u));
 #pragma unroll
-    for (int i = 0; i <= N; i++) d[i] = p[i];
+    for (int i = 0; i <= N; i++) d[i] = q[i];
+    return off & 3u;
+}
+template <int N>
+__device__ __forceinline__ void span_words(const uint32_t d[N + 1], uint32_t sh, uint32_t w[N]) {
 #pragma unroll
     for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
 }
@@ -315,14 +323,31 @@ __device__ __forceinline__ uint32_t item_bytes(int t) {
     default: return 256;
     }
 }
+// items of one matrix per tile: every lane busy, at most TILE_BYTES - 16
+__device__ __forceinline__ uint32_t items_per_tile(int t, bool swiglu) {
+    const uint32_t n = (t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u;
+    return swiglu ? n / 2 : n;
+}
 
 // Q4_K block (16-aligned in LDS) against Q8_K group g
-__device__ __forceinline__ double term_q4k(const char *blk, const ActView &x, uint32_t g) {
-    const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
-    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};   // scales[0..11]
+__device__ __forceinline__ double term_q4k(const lds_char *blk, const ActView &x, uint32_t g) {
+    u32x4 wv[9], xv[16], bsv[2];
+#pragma unroll
+    for (int i = 0; i < 9; i++) wv[i] = lds16(blk + 16 * i);
+    const lds_char *xq = x.q + g * ACT_GSTRIDE;
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = lds16(xq + 16 * i);
+    const lds_char *bsp = reinterpret_cast<const lds_char *>(x.bs + g * 16);
+    bsv[0] = lds16(bsp);
+    bsv[1] = lds16(bsp + 16);
+    const float dxf = x.d[g];
+    sched_fence();
+    const uint32_t sw[3] = {wv[0].y, wv[0].z, wv[0].w};   // scales[0..11]
     auto byte = [&](uint32_t i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xff); };
-    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE);
-    const int16_t *bs = x.bs + g * 16;
+    auto bsum = [&](int j) -> int {                       // bsums[j], int16
+        const uint32_t wd = bsv[j >> 3][(j >> 1) & 3];
+        return (j & 1) ? ((int)wd >> 16) : (int)(int16_t)(wd & 0xffff);
+    };
     int isum = 0, imin = 0;
 #pragma unroll
     for (int p = 0; p < 4; p++) {
@@ -335,130 +360,153 @@ __device__ __forceinline__ double term_q4k(const char *blk, const ActView &x, ui
             sc0 = (byte(s0 + 4) & 0xF) | ((byte(s0 - 4) >> 6) << 4); m0 = (byte(s0 + 4) >> 4) | ((byte(s0) >> 6) << 4);
             sc1 = (byte(s1 + 4) & 0xF) | ((byte(s1 - 4) >> 6) << 4); m1 = (byte(s1 + 4) >> 4) | ((byte(s1) >> 6) << 4);
         }
-        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
-        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * p);
+        const u32x4 qa = wv[1 + 2 * p], qb = wv[2 + 2 * p];
         const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const u32x4 x0 = xv[4 * p], x1 = xv[4 * p + 1], x2 = xv[4 * p + 2], x3 = xv[4 * p + 3];
+        const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
         int dlo = 0, dhi = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            dlo = sdot4(w[i] & 0x0F0F0F0Fu, xq[16 * p + i], dlo);
-            dhi = sdot4((w[i] >> 4) & 0x0F0F0F0Fu, xq[16 * p + 8 + i], dhi);
+            dlo = sdot4(w[i] & 0x0F0F0F0Fu, xl[i], dlo);
+            dhi = sdot4((w[i] >> 4) & 0x0F0F0F0Fu, xh[i], dhi);
         }
         isum += sc0 * dlo + sc1 * dhi;
-        imin += m0 * ((int)bs[4 * p] + (int)bs[4 * p + 1]) + m1 * ((int)bs[4 * p + 2] + (int)bs[4 * p + 3]);
+        imin += m0 * (bsum(4 * p) + bsum(4 * p + 1)) + m1 * (bsum(4 * p + 2) + bsum(4 * p + 3));
     }
-    const double dx = (double)x.d[g];
-    const double dw = (double)h2f((uint16_t)(hdr.x & 0xffff));
-    const double dm = (double)h2f((uint16_t)(hdr.x >> 16));
+    const double dx = (double)dxf;
+    const double dw = (double)h2f((uint16_t)(wv[0].x & 0xffff));
+    const double dm = (double)h2f((uint16_t)(wv[0].x >> 16));
     return (dw * dx) * (double)isum - (dm * dx) * (double)imin;
 }
 
-// Q6_K block at a 2-aligned LDS offset against Q8_K group g.  Codes are
-// taken unsigned (0..63) and the -32 offset folds through the bsums:
-// sum((c-32)*x) = sum(c*x) - 32*bsum, exact in integers.
-__device__ __forceinline__ double term_q6k(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
-    const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE);
-    const int16_t *bs = x.bs + g * 16;
-    uint32_t scw[4];
-    lds_words<4>(lds, off + 192, scw);                 // int8 scales[16]
+// Half n (elements [128n, 128n+128)) of a Q6_K block at a 2-aligned LDS
+// address against Q8_K group g: the exact integer sum over its 8 sub-blocks
+// of scale * (code dot x).  Codes are taken unsigned (0..63) and the -32
+// offset folds through the bsums: sum((c-32)*x) = sum(c*x) - 32*bsum.
+__device__ __forceinline__ int q6k_half(const lds_char *blk, const ActView &x, uint32_t g, uint32_t n) {
+    uint32_t dl[17], dh[9], ds[3];
+    const uint32_t shl = ld_span<16>(blk + 64 * n, dl);          // ql[64n .. 64n+64)
+    const uint32_t shh = ld_span<8>(blk + 128 + 32 * n, dh);     // qh[32n .. 32n+32)
+    const uint32_t shs = ld_span<2>(blk + 192 + 8 * n, ds);      // int8 scales[8n .. 8n+8)
+    const lds_char *xq = x.q + g * ACT_GSTRIDE + 128 * n;
+    u32x4 xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) xv[i] = lds16(xq + 16 * i);
+    const u32x4 bsv = lds16(reinterpret_cast<const lds_char *>(x.bs + g * 16 + 8 * n));
+    sched_fence();
+    uint32_t ql[16], qh[8], scw[2];
+    span_words<16>(dl, shl, ql);
+    span_words<8>(dh, shh, qh);
+    span_words<2>(ds, shs, scw);
+    uint32_t xw[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        xw[4 * i] = xv[i].x; xw[4 * i + 1] = xv[i].y; xw[4 * i + 2] = xv[i].z; xw[4 * i + 3] = xv[i].w;
+    }
+    int dot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // [quarter][16-element half]
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t qa = ql[i], qb = ql[8 + i];
+        const uint32_t c0 = (qa & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u);
+        const uint32_t c1 = (qb & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u);
+        const uint32_t c2 = ((qa >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u);
+        const uint32_t c3 = ((qb >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u);
+        const int hf = i >> 2;                     // l = 4i.. : half hf of each quarter
+        dot[0][hf] = sdot4(c0, xw[i], dot[0][hf]);
+        dot[1][hf] = sdot4(c1, xw[8 + i], dot[1][hf]);
+        dot[2][hf] = sdot4(c2, xw[16 + i], dot[2][hf]);
+        dot[3][hf] = sdot4(c3, xw[24 + i], dot[3][hf]);
+    }
     int isum = 0;
 #pragma unroll
-    for (int n = 0; n < 2; n++) {
-        uint32_t qa[8], qb[8], qh[8];
-        lds_words<8>(lds, off + 64 * n, qa);           // ql[64n .. 64n+32)
-        lds_words<8>(lds, off + 64 * n + 32, qb);      // ql[64n+32 .. 64n+64)
-        lds_words<8>(lds, off + 128 + 32 * n, qh);     // qh[32n .. 32n+32)
-        int dot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // [quarter][16-element half]
+    for (int t = 0; t < 4; t++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t c0 = (qa[i] & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u);
-            const uint32_t c1 = (qb[i] & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u);
-            const uint32_t c2 = ((qa[i] >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u);
-            const uint32_t c3 = ((qb[i] >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u);
-            const int hf = i >> 2;                     // l = 4i.. : half hf of each quarter
-            dot[0][hf] = sdot4(c0, xq[(128 * n + 0) / 4 + i], dot[0][hf]);
-            dot[1][hf] = sdot4(c1, xq[(128 * n + 32) / 4 + i], dot[1][hf]);
-            dot[2][hf] = sdot4(c2, xq[(128 * n + 64) / 4 + i], dot[2][hf]);
-            dot[3][hf] = sdot4(c3, xq[(128 * n + 96) / 4 + i], dot[3][hf]);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-#pragma unroll
-            for (int hf = 0; hf < 2; hf++) {
-                const int j = 8 * n + 2 * t + hf;      // 16-element sub-block
-                const int sc = (int)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xff);
-                isum += sc * (dot[t][hf] - 32 * (int)bs[j]);
-            }
+        for (int hf = 0; hf < 2; hf++) {
+            const int j = 2 * t + hf;              // 16-element sub-block within the half
+            const int sc = (int)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xff);
+            const uint32_t bw = bsv[j >> 1];
+            const int bs = (j & 1) ? ((int)bw >> 16) : (int)(int16_t)(bw & 0xffff);
+            isum += sc * (dot[t][hf] - 32 * bs);
         }
     }
-    const double dw = (double)h2f(lds_u16(lds, off + 208));
-    return (dw * (double)x.d[g]) * (double)isum;
+    return isum;
 }
 
-// 8 Q8_0 blocks (272 B group) against Q8_0 activation blocks 8g..8g+7,
-// block terms summed in ascending order inside the group
-__device__ __forceinline__ double term_q80(const char *lds, uint32_t off, const ActView &x, uint32_t g) {
-    double acc = 0.0;
+// Blocks 4h .. 4h+3 of an 8-block Q8_0 item (34-byte blocks, 2-aligned)
+// against Q8_0 activation blocks 8g+4h ..: the four block terms.
+__device__ __forceinline__ void q80_quad(const lds_char *item, const ActView &x, uint32_t g, uint32_t h, double t[4]) {
+    uint32_t dw[4][9], sh[4];
+    uint16_t dh[4];
+    u32x4 xv[8];
+    float dx[4];
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
-        const uint32_t bo = off + 34 * b;
+    for (int j = 0; j < 4; j++) {
+        const uint32_t b = 4 * h + j;
+        const lds_char *bo = item + 34 * b;
+        sh[j] = ld_span<8>(bo + 2, dw[j]);
+        dh[j] = ld_u16(bo);
+        const lds_char *xq = x.q + g * ACT_GSTRIDE + 32 * b;
+        xv[2 * j] = lds16(xq);
+        xv[2 * j + 1] = lds16(xq + 16);
+        dx[j] = x.d[8 * g + b];
+    }
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
         uint32_t w[8];
-        lds_words<8>(lds, bo + 2, w);
-        const uint32_t *xq = reinterpret_cast<const uint32_t *>(x.q + g * ACT_GSTRIDE + 32 * b);
+        span_words<8>(dw[j], sh[j], w);
+        const u32x4 x0 = xv[2 * j], x1 = xv[2 * j + 1];
+        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         int isum = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) isum = sdot4(w[i], xq[i], isum);
-        const double dw = (double)h2f(lds_u16(lds, bo));
-        acc += (dw * (double)x.d[8 * g + b]) * (double)isum;
+        for (int i = 0; i < 8; i++) isum = sdot4(w[i], xw[i], isum);
+        t[j] = ((double)h2f(dh[j]) * (double)dx[j]) * (double)isum;
     }
-    return acc;
 }
 
 // 64 bf16 elements (128 B, 16-aligned), products exact in fp64, ascending
-__device__ __forceinline__ double term_bf16(const char *lds, uint32_t off, const ActView &x, uint32_t k) {
-    const uint4 *w = reinterpret_cast<const uint4 *>(lds + off);
-    const uint4 *xx = reinterpret_cast<const uint4 *>(x.q + k * ACT_BF_CSTRIDE);
+__device__ __forceinline__ double term_bf16(const lds_char *blk, const ActView &x, uint32_t k) {
+    const lds_char *xx = x.q + k * ACT_BF_CSTRIDE;
+    u32x4 av[8], bv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) { av[i] = lds16(blk + 16 * i); bv[i] = lds16(xx + 16 * i); }
+    sched_fence();
     double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const uint4 a = w[i], b = xx[i];
-        const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            acc += (double)__uint_as_float(aw[j] << 16) * (double)__uint_as_float(bw[j] << 16);
-            acc += (double)__uint_as_float(aw[j] & 0xffff0000u) * (double)__uint_as_float(bw[j] & 0xffff0000u);
+            const uint32_t aw = av[i][j], bw = bv[i][j];
+            acc += (double)__uint_as_float(aw << 16) * (double)__uint_as_float(bw << 16);
+            acc += (double)__uint_as_float(aw & 0xffff0000u) * (double)__uint_as_float(bw & 0xffff0000u);
         }
     }
     return acc;
 }
 
 // 64 f32 elements (256 B, 16-aligned), products exact in fp64, ascending
-__device__ __forceinline__ double term_f32(const char *lds, uint32_t off, const ActView &x, uint32_t k) {
-    const float4 *w = reinterpret_cast<const float4 *>(lds + off);
-    const float4 *xx = reinterpret_cast<const float4 *>(x.q + k * ACT_F_CSTRIDE);
+__device__ __forceinline__ double term_f32(const lds_char *blk, const ActView &x, uint32_t k) {
+    const lds_char *xx = x.q + k * ACT_F_CSTRIDE;
     double acc = 0.0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float4 a = w[i], b = xx[i];
-        acc += (double)a.x * (double)b.x;
-        acc += (double)a.y * (double)b.y;
-        acc += (double)a.z * (double)b.z;
-        acc += (double)a.w * (double)b.w;
+    for (int h = 0; h < 2; h++) {
+        f32x4 av[8], bv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) { av[i] = ldsf16(blk + 128 * h + 16 * i); bv[i] = ldsf16(xx + 128 * h + 16 * i); }
+        sched_fence();
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            acc += (double)av[i].x * (double)bv[i].x;
+            acc += (double)av[i].y * (double)bv[i].y;
+            acc += (double)av[i].z * (double)bv[i].z;
+            acc += (double)av[i].w * (double)bv[i].w;
+        }
     }
     return acc;
 }
 
-__device__ __forceinline__ double item_term(int type, const char *tile, uint32_t off, const ActView &x, uint32_t k) {
-    switch (type) {
-    case SINTER_Q4_K: return term_q4k(tile + off, x, k);
-    case SINTER_Q6_K: return term_q6k(tile, off, x, k);
-    case SINTER_Q8_0: return term_q80(tile, off, x, k);
-    case SINTER_BF16: return term_bf16(tile, off, x, k);
-    default: return term_f32(tile, off, x, k);
-    }
-}
-
-// ------------------------------------------------------------ row ranges and tiles
+// ------------------------------------------------------------ work split
 
 // Row cut for workgroup w of n: the global row nearest to byte w*T/n of the
 // concatenated (byte-weighted) row space.
@@ -484,97 +532,147 @@ __device__ __forceinline__ uint32_t row_cut(const sinter_gemv_args &a, const uin
     return rows;
 }
 
-struct Tile {
-    uint32_t seg;
-    uint32_t r0, nr;           // output rows [r0, r0+nr) of segment seg
-    uint32_t skew_a, n16_a;    // range A (w): byte skew in its first uint4, uint4 count
-    uint32_t skew_b, n16_b;    // range B (w2, SwiGLU only)
-    const uint4 *src_a, *src_b;
-};
-
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// per-segment geometry, read from the payload (scalar loads; no private arrays)
-__device__ __forceinline__ uint32_t seg_rb(const sinter_gemv_args &a, uint32_t s) {
-    return (uint32_t)sinter_row_bytes_dev(a.seg[s].type, a.K);
-}
-__device__ __forceinline__ uint32_t seg_rb_eff(const sinter_gemv_args &a, uint32_t s) {
-    return seg_rb(a, s) * (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
-}
-// segment holding global row grow, and its first global row
-__device__ __forceinline__ uint32_t seg_of(const sinter_gemv_args &a, uint32_t grow, uint32_t &base) {
-    uint32_t s = 0, b = 0;
-    while (s + 1 < a.n_seg && grow >= b + a.seg[s].rows) { b += a.seg[s].rows; s++; }
-    base = b;
-    return s;
+// This workgroup's share of each segment, computed once per op (LDS):
+enum : int {
+    GS_ROW_LO = 0,   // segment-local rows [row_lo, row_hi) of this workgroup
+    GS_ROW_HI,
+    GS_LR_BASE,      // workgroup-local index of segment-local row 0
+    GS_TYPE,
+    GS_SWIGLU,
+    GS_IB,           // item bytes
+    GS_T,            // items of each matrix per tile
+    GS_QT,           // T / ipr
+    GS_RT,           // T % ipr
+    GS_W_LO, GS_W_HI, GS_W2_LO, GS_W2_HI,
+    GS_STRIDE = 16
+};
+__shared__ uint32_t g_gseg[SINTER_GEMV_MAX_SEG * GS_STRIDE];
+__device__ __forceinline__ uint32_t gs(uint32_t s, int f) { return uni(g_gseg[s * GS_STRIDE + f]); }
+
+// q = v / d, r = v % d from m = floor((2^32-1) / d): the estimate is q or
+// q-1, one correction step makes it exact (v < 2^31)
+__device__ __forceinline__ uint32_t divm(uint32_t v, uint32_t d, uint32_t m, uint32_t &r) {
+    uint32_t q = __umulhi(v, m);
+    r = v - q * d;
+    if (r >= d) { r -= d; q += 1; }
+    return q;
 }
 
-// Tile starting at global row grow (caller checks grow < row_hi).
-__device__ __forceinline__ Tile tile_at(const sinter_gemv_args &a, uint32_t grow, uint32_t row_hi) {
-    Tile t;
-    uint32_t base;
-    t.seg = uni(seg_of(a, grow, base));
-    base = uni(base);
-    const sinter_gemv_seg &sg = a.seg[t.seg];
-    const uint32_t rb = seg_rb(a, t.seg);
-    uint32_t nr = (TILE_BYTES - 64) / seg_rb_eff(a, t.seg);
-    // one lane per item: at most BLOCK_THREADS items per tile (a longer row
-    // still gets a tile of its own and is looped over)
-    const uint32_t ipr = a.K / item_elems(sg.type) * (sg.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
-    nr = min(nr, max(1u, BLOCK_THREADS / ipr));
-    const uint32_t seg_end = min(base + sg.rows, row_hi);
-    if (nr > RES_CAP) nr = RES_CAP;
-    if (grow + nr > seg_end) nr = seg_end - grow;
-    nr = uni(nr);
-    t.r0 = grow - base;
-    t.nr = nr;
-    const uintptr_t A = reinterpret_cast<uintptr_t>(sg.w) + (uintptr_t)t.r0 * rb;
-    t.src_a = reinterpret_cast<const uint4 *>(A & ~(uintptr_t)15);
-    t.skew_a = (uint32_t)(A & 15);
-    t.n16_a = (t.skew_a + nr * rb + 15) / 16;
-    if (sg.epi == SINTER_EPI_SWIGLU) {
-        const uintptr_t B = reinterpret_cast<uintptr_t>(sg.w2) + (uintptr_t)t.r0 * rb;
-        t.src_b = reinterpret_cast<const uint4 *>(B & ~(uintptr_t)15);
-        t.skew_b = (uint32_t)(B & 15);
-        t.n16_b = (t.skew_b + nr * rb + 15) / 16;
-    } else {
-        t.src_b = nullptr; t.skew_b = 0; t.n16_b = 0;
+// The term ring: row-aligned.  The row of workgroup-local index lr owns
+// slot lr % R; its term k sits at slot*P + k (P = ipr rounded up to even, the
+// pad slot holds -0.0, an exact no-op in the fold).  SwiGLU up terms use a
+// second ring of R*P behind the first.  Rows are folded once, complete, in
+// ascending k.  "Deferred" rings fold a tile's rows one tile later (no extra
+// barrier; R covers the rows of two tiles); otherwise the rows are folded
+// right after an extra barrier.
+struct Ring {
+    uint32_t ipr, mipr, P, R, mR, RP, defer;
+};
+
+// ------------------------------------------------------------ tiles
+// A tile is a run of whole items of one segment: items [a, a+cnt) of its
+// matrix (and the same items of w2 for a SwiGLU pair), a contiguous byte
+// range of the row-major weights.  Tiles ignore row boundaries, so every lane
+// has an item; a row's terms may span tiles.  a = ra*ipr + ka.
+//
+// The DMA cursor walks the tiles of this workgroup in order and keeps the
+// current segment's constants in registers; consecutive tiles of a segment
+// differ by constants, so creating a tile is a handful of scalar operations.
+struct TD {                 // what compute and fold need of a tile
+    uint32_t ok, a, cnt, ra, ka;
+    uint32_t type, swig, lr0;           // weight type, SwiGLU pair, workgroup-local index of row ra
+    uint32_t skew_a, base_b;            // LDS byte offsets of matrix A's and B's first item
+};
+struct Cursor {
+    uint32_t ok, seg, a, ra, ka;        // next tile to create
+    uint32_t end, T, qT, rT, ib, type, swig, lrb;   // current segment
+    uintptr_t wa, wb;                   // weights of the current segment
+};
+
+__device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s, uint32_t n_seg, uint32_t ipr) {
+    c.ok = 0;
+    for (; s < n_seg; s++) {
+        const uint32_t lo = gs(s, GS_ROW_LO), hi = gs(s, GS_ROW_HI);
+        if (lo < hi) {
+            c.ok = 1; c.seg = s; c.a = lo * ipr; c.ra = lo; c.ka = 0;
+            c.end = hi * ipr; c.T = gs(s, GS_T); c.qT = gs(s, GS_QT); c.rT = gs(s, GS_RT);
+            c.ib = gs(s, GS_IB); c.type = gs(s, GS_TYPE); c.swig = gs(s, GS_SWIGLU); c.lrb = gs(s, GS_LR_BASE);
+            c.wa = ((uintptr_t)gs(s, GS_W_HI) << 32) | gs(s, GS_W_LO);
+            c.wb = ((uintptr_t)gs(s, GS_W2_HI) << 32) | gs(s, GS_W2_LO);
+            return;
+        }
     }
-    return t;
 }
 
-// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at src land at
+// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at base + voff land at
 // lds_base + 16*l.  Issued from inline asm so the compiler does not treat the
 // pending DMA as aliasing every later LDS read (it would insert vmcnt(0)
 // before them and serialise the pipeline); the tile loop below waits for it
 // explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends.
-__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
+__device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %2, off\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(lds_base), "v"(src)
+        : "s"(lds_base), "v"(voff), "s"(base)
         : "memory");
 }
 
-// LDS-DMA one tile into a 36 KiB buffer: every wave issues exactly
-// TILE_CPW 1-KiB chunks (lanes past the tile re-read its first 16 bytes into
-// the unused tail of the buffer), so the number of outstanding loads per wave
-// is a compile-time constant and the tile waits below can be partial.
-__device__ __forceinline__ void tile_issue(const Tile &t, char *buf) {
-    const uint32_t w = uni(wave_id()), lane = lane_id();
-    const uint32_t n16 = t.n16_a + t.n16_b;
-    const uint32_t base = (uint32_t)(uintptr_t)(lds_void *)buf;
+// Create the tile at the cursor, LDS-DMA it into a 36 KiB buffer and advance
+// the cursor.  Every wave issues exactly TILE_CPW 1-KiB chunks, so the number
+// of outstanding loads per wave is a compile-time constant and the tile waits
+// can be partial.  Matrix A fills the first chunks; a SwiGLU matrix B starts
+// at the next 1 KiB chunk boundary, so every chunk reads from one matrix;
+// lanes past a matrix's end re-read its last 16 bytes into the unused tail.
+__device__ __forceinline__ TD tile_next(Cursor &c, char *buf, uint32_t n_seg, uint32_t ipr) {
+    TD t;
+    t.ok = c.ok;
+    t.a = 0; t.cnt = 0; t.ra = 0; t.ka = 0; t.type = 0; t.swig = 0; t.lr0 = 0; t.skew_a = 0; t.base_b = 0;
+    if (!c.ok) return t;
+    t.a = c.a; t.ra = c.ra; t.ka = c.ka;
+    t.cnt = min(c.T, c.end - c.a);
+    t.type = c.type; t.swig = c.swig; t.lr0 = c.lrb + c.ra;
+    const uint32_t bytes = t.cnt * c.ib;
+    const uintptr_t A = c.wa + (uintptr_t)c.a * c.ib;
+    t.skew_a = (uint32_t)(A & 15);
+    const uintptr_t sa = A & ~(uintptr_t)15;
+    const uint32_t last_a = ((t.skew_a + bytes - 1) >> 4) << 4;       // offset of A's last 16 B
+    const uint32_t chunks_a = (t.skew_a + bytes + 1023) >> 10;
+    uintptr_t sb = sa;
+    uint32_t last_b = last_a;
+    if (c.swig) {
+        const uintptr_t B = c.wb + (uintptr_t)c.a * c.ib;
+        sb = B & ~(uintptr_t)15;
+        const uint32_t skew_b = (uint32_t)(B & 15);
+        t.base_b = chunks_a * 1024 + skew_b;
+        last_b = ((skew_b + bytes - 1) >> 4) << 4;
+    }
+    const uint32_t w = uni(wave_id()), lane16 = lane_id() * 16;
+    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void *)buf;
 #pragma unroll
     for (uint32_t k = 0; k < TILE_CPW; k++) {
         const uint32_t j = w + 4 * k;
-        const uint32_t idx = j * 64 + lane;
-        const uint4 *src = idx < t.n16_a ? t.src_a + idx : (idx < n16 ? t.src_b + (idx - t.n16_a) : t.src_a);
-        lds_dma16(src, uni(base + j * 1024));
+        const bool in_a = j < chunks_a;
+        const uintptr_t src = in_a ? sa : sb;
+        const uint32_t j0 = in_a ? j : j - chunks_a;
+        const uint32_t voff = min(j0 * 1024 + lane16, in_a ? last_a : last_b);
+        lds_dma16(src, voff, lbase + j * 1024);
     }
+    // advance
+    c.a += t.cnt;
+    if (c.a >= c.end) {
+        cur_seg(c, c.seg + 1, n_seg, ipr);
+    } else {
+        c.ra += c.qT;
+        c.ka += c.rT;
+        if (c.ka >= ipr) { c.ka -= ipr; c.ra += 1; }
+    }
+    return t;
 }
 
 template <int N>
@@ -582,6 +680,110 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(0) as a real instruction the compiler's wait-count pass
+// sees: after it, no compiler-visible memory operation is pending, so the
+// pass does not put a vmcnt(0) (which would also wait for the in-flight tile
+// DMA) in front of later register reuse.  gfx9 encoding: vmcnt 0, expcnt 7,
+// lgkmcnt 15.
+__device__ __forceinline__ void settle_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Item terms of a landed tile into the term ring.
+template <int TYPE>
+__device__ __forceinline__ void tile_terms_t(const TD &t, const lds_char *buf, LDS double *ring, bool swig,
+                                             const Ring &rg, const ActView &x) {
+    constexpr uint32_t LPI = (TYPE == SINTER_Q6_K || TYPE == SINTER_Q8_0) ? 2u : 1u;
+    constexpr uint32_t IB = TYPE == SINTER_Q4_K ? 144u : TYPE == SINTER_Q6_K ? 210u : TYPE == SINTER_Q8_0 ? 272u
+                          : TYPE == SINTER_BF16 ? 128u : 256u;
+    const uint32_t l = threadIdx.x;
+    const uint32_t m = swig ? (l >> 7) : 0u;
+    const uint32_t ll = swig ? (l & 127u) : l;
+    const uint32_t u = ll / LPI, part = ll % LPI;
+    if (u < t.cnt) {   // the lanes of one item are active together
+        uint32_t k, slot;
+        const uint32_t q = divm(t.ka + u, rg.ipr, rg.mipr, k);
+        (void)divm(t.lr0 + q, rg.R, rg.mR, slot);
+        const lds_char *blk = buf + (m ? t.base_b : t.skew_a) + u * IB;
+        double term;
+        if constexpr (TYPE == SINTER_Q4_K) {
+            term = term_q4k(blk, x, k);
+        } else if constexpr (TYPE == SINTER_Q6_K) {
+            const uint16_t dh = ld_u16(blk + 208);
+            const float dxf = x.d[k];
+            int is = q6k_half(blk, x, k, part);
+            is += __shfl_xor(is, 1, 64);
+            term = ((double)h2f(dh) * (double)dxf) * (double)is;
+        } else if constexpr (TYPE == SINTER_Q8_0) {
+            double tt[4];
+            q80_quad(blk, x, k, part, tt);
+            const double lo4 = (((0.0 + tt[0]) + tt[1]) + tt[2]) + tt[3];   // blocks 0-3 (part 0)
+            const double prev = __shfl_xor(lo4, 1, 64);
+            term = (((prev + tt[0]) + tt[1]) + tt[2]) + tt[3];             // blocks 4-7 continue it (part 1)
+        } else if constexpr (TYPE == SINTER_BF16) {
+            term = term_bf16(blk, x, k);
+        } else {
+            term = term_f32(blk, x, k);
+        }
+        if (part == LPI - 1) ring[m * rg.RP + slot * rg.P + k] = term;
+    }
+}
+
+__device__ __forceinline__ void tile_terms(const TD &t, const char *bufg, const Ring &rg, const ActView &x) {
+    const bool swig = t.swig != 0;
+    const lds_char *buf = (const lds_char *)bufg;
+    LDS double *ring = (LDS double *)g_cb;
+    switch (t.type) {
+    case SINTER_Q4_K: tile_terms_t<SINTER_Q4_K>(t, buf, ring, swig, rg, x); break;
+    case SINTER_Q6_K: tile_terms_t<SINTER_Q6_K>(t, buf, ring, swig, rg, x); break;
+    case SINTER_Q8_0: tile_terms_t<SINTER_Q8_0>(t, buf, ring, swig, rg, x); break;
+    case SINTER_BF16: tile_terms_t<SINTER_BF16>(t, buf, ring, swig, rg, x); break;
+    default: tile_terms_t<SINTER_F32>(t, buf, ring, swig, rg, x); break;
+    }
+}
+
+// workgroup-local rows completed once this tile is computed
+__device__ __forceinline__ uint32_t td_done_after(const TD &t, const Ring &rg) {
+    uint32_t r;
+    return t.lr0 + divm(t.ka + t.cnt, rg.ipr, rg.mipr, r);
+}
+
+// One row's P ring terms summed in ascending order (fp64), 8 at a time.
+__device__ __forceinline__ double fold_row(const LDS double *g, uint32_t P) {
+    double s = 0.0;
+    uint32_t k = 0;
+    for (; k + 8 <= P; k += 8) {
+        double b[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) b[i] = g[k + i];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += b[i];
+    }
+    for (; k < P; k += 2) {
+        const double b0 = g[k], b1 = g[k + 1];
+        s += b0;
+        s += b1;
+    }
+    return s;
+}
+
+// Fold the rows this tile completed: rows [t.lr0, done_after).  The row of
+// workgroup-local index lr is folded by lane ((lr%4)<<6) | ((lr/4)%64) and
+// rounded to fp32 into g_res.
+__device__ __forceinline__ void tile_fold(const TD &t, const Ring &rg, uint32_t res_row0) {
+    const LDS double *ring = (const LDS double *)g_cb;
+    LDS float *res = (LDS float *)g_res;
+    const uint32_t nf = td_done_after(t, rg) - t.lr0;
+    const uint32_t l = threadIdx.x;
+    const uint32_t c = ((l & 63u) << 2) | (l >> 6);
+    const uint32_t d = (c - t.lr0) & 255u;
+    if (d < nf) {
+        const uint32_t lr = t.lr0 + d;
+        uint32_t slot;
+        (void)divm(lr, rg.R, rg.mR, slot);
+        const uint32_t i = lr - res_row0;
+        res[2 * i] = (float)fold_row(ring + slot * rg.P, rg.P);
+        if (t.swig) res[2 * i + 1] = (float)fold_row(ring + rg.RP + slot * rg.P, rg.P);
+    }
+}
 
 // ------------------------------------------------------------ the op
 
@@ -589,16 +791,14 @@ __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0
 // block behind at the next grid barrier).
 __device__ __forceinline__ bool gemv_args_ok(const sinter_gemv_args &a) {
     if (a.n_seg < 1 || a.n_seg > SINTER_GEMV_MAX_SEG) return false;
-    if (a.K == 0 || (a.K & 255u) != 0) return false;
+    if (a.K == 0 || (a.K & 255u) != 0 || a.K > (1u << 20)) return false;
     const int vt = vec_dot_type(a.seg[0].type);
     if (act_bytes(vt, a.K) > QBUF_BYTES) return false;
     if (a.pro == SINTER_PRO_GATED && (a.gn_log2d < 2 || a.gn_log2d > 8)) return false;
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
         if (vec_dot_type(g.type) != vt) return false;
-        const uint32_t rbe = (uint32_t)sinter_row_bytes_dev(g.type, a.K) * (g.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
-        if (rbe == 0 || rbe > TILE_BYTES - 64) return false;
-        if ((a.K / item_elems(g.type)) * (g.epi == SINTER_EPI_SWIGLU ? 2u : 1u) > CB_CAP) return false;
+        if (sinter_row_bytes_dev(g.type, a.K) == 0) return false;
         if (g.epi == SINTER_EPI_CONV && (g.dconv < 2 || g.dconv > 8)) return false;
     }
     return true;
@@ -609,8 +809,8 @@ __device__ __forceinline__ bool gemv_args_ok(const sinter_gemv_args &a) {
 __device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
     for (uint32_t i = threadIdx.x; i < n; i += BLOCK_THREADS) {
         const uint32_t grow = row0 + i;
-        uint32_t base;
-        const uint32_t s = seg_of(a, grow, base);
+        uint32_t s = 0, base = 0;
+        while (s + 1 < a.n_seg && grow >= base + a.seg[s].rows) { base += a.seg[s].rows; s++; }
         const sinter_gemv_seg &sg = a.seg[s];
         const uint32_t r = grow - base;
         const float dot = g_res[2 * i];
@@ -645,55 +845,26 @@ __device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n,
     }
 }
 
-// Compute one landed tile: one lane per (virtual row, item) writes the item
-// term to LDS, then one lane per virtual row sums its terms in ascending
-// order.  A SwiGLU tile has nr gate rows then nr up rows.  Row results go to
-// g_res[2*(slot0 + row) + {0: gate/plain, 1: up}].
-template <int TYPE>
-__device__ __forceinline__ void tile_compute_t(const Tile &t, const char *buf, uint32_t ipr, uint32_t nv,
-                                               uint32_t rb, uint32_t slot0, const ActView &x) {
-    const uint32_t ib = item_bytes(TYPE);
-    const uint32_t n_items = nv * ipr;
-    for (uint32_t it = threadIdx.x; it < n_items; it += BLOCK_THREADS) {
-        const uint32_t v = it / ipr, k = it - v * ipr;
-        const uint32_t roff = v < t.nr ? t.skew_a + v * rb : t.n16_a * 16 + t.skew_b + (v - t.nr) * rb;
-        g_cb[it] = item_term(TYPE, buf, roff + k * ib, x, k);
+// Ring geometry of an op (uniform); false if the shape cannot be folded.
+__device__ __forceinline__ bool ring_geometry(const sinter_gemv_args &a, uint32_t ipr, Ring &rg) {
+    bool any_swig = false;
+    uint32_t tmax = 0;
+    for (int s = 0; s < a.n_seg; s++) {
+        const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
+        any_swig |= sw;
+        tmax = max(tmax, items_per_tile(a.seg[s].type, sw));
     }
-    wait_lgkm0();
-    __builtin_amdgcn_s_barrier();
-    // ascending fold of each row's terms; the terms are fetched 8 at a time
-    // (one LDS round trip per 8) before the dependent fp64 adds
-    for (uint32_t v = threadIdx.x; v < nv; v += BLOCK_THREADS) {
-        const double *c = g_cb + v * ipr;
-        double s = 0.0;
-        uint32_t k = 0;
-        for (; k + 8 <= ipr; k += 8) {
-            double b[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) b[i] = c[k + i];
-#pragma unroll
-            for (int i = 0; i < 8; i++) s += b[i];
-        }
-        for (; k < ipr; k++) s += c[k];
-        const uint32_t row = v < t.nr ? v : v - t.nr;
-        g_res[2 * (slot0 + row) + (v < t.nr ? 0 : 1)] = (float)s;
-    }
-}
-
-__device__ __forceinline__ void tile_compute(const sinter_gemv_args &a, const Tile &t, const char *buf,
-                                          uint32_t slot0, const ActView &x) {
-    const sinter_gemv_seg &sg = a.seg[t.seg];
-    const int type = (int)uni(sg.type);
-    const uint32_t ipr = a.K / item_elems(type);
-    const uint32_t nv = t.nr * (sg.epi == SINTER_EPI_SWIGLU ? 2u : 1u);
-    const uint32_t rb = uni(seg_rb(a, t.seg));
-    switch (type) {
-    case SINTER_Q4_K: tile_compute_t<SINTER_Q4_K>(t, buf, ipr, nv, rb, slot0, x); break;
-    case SINTER_Q6_K: tile_compute_t<SINTER_Q6_K>(t, buf, ipr, nv, rb, slot0, x); break;
-    case SINTER_Q8_0: tile_compute_t<SINTER_Q8_0>(t, buf, ipr, nv, rb, slot0, x); break;
-    case SINTER_BF16: tile_compute_t<SINTER_BF16>(t, buf, ipr, nv, rb, slot0, x); break;
-    default: tile_compute_t<SINTER_F32>(t, buf, ipr, nv, rb, slot0, x); break;
-    }
+    rg.ipr = ipr;
+    rg.mipr = 0xFFFFFFFFu / ipr;
+    rg.P = ipr + (ipr & 1u);
+    const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP;
+    rg.R = cap / rg.P;
+    const uint32_t tpr = (tmax + ipr - 1) / ipr;   // rows one tile can touch, less one
+    rg.defer = rg.R >= 2 * tpr + 2 ? 1u : 0u;
+    if (rg.R < tpr + 1) return false;
+    rg.mR = 0xFFFFFFFFu / rg.R;
+    rg.RP = rg.R * rg.P;
+    return true;
 }
 
 __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
@@ -702,67 +873,125 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
     __syncthreads();
     const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
     const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
-    if (!gemv_args_ok(a)) {
+    const uint32_t K = a.K;
+    const uint32_t ipr = uni(K / item_elems(a.seg[0].type));
+    Ring rg;
+    if (!gemv_args_ok(a) || !ring_geometry(a, ipr, rg)) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
         return;
     }
-    const uint32_t K = a.K;
     const int vt = vec_dot_type(a.seg[0].type);
-    uint32_t rb_eff[SINTER_GEMV_MAX_SEG];
-    uint64_t total = 0;
-#pragma unroll
-    for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
-        rb_eff[s] = s < a.n_seg ? seg_rb_eff(a, s) : 0u;
-        total += s < a.n_seg ? (uint64_t)a.seg[s].rows * rb_eff[s] : 0ull;
-    }
-    const uint32_t row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
-    const uint32_t row_hi = uni(row_cut(a, rb_eff, total, rel + 1, nblk));
+    const uint32_t n_seg = uni(a.n_seg);
 
-    // Three-buffer rotation over tiles identified by their first row (the
-    // geometry is recomputed).  X = tile being computed (buffer bx), Y = the
-    // next tile, already in flight.  Before computing X each wave waits for
-    // its own DMA into X -- Y's TILE_CPW loads may stay outstanding -- and a
-    // barrier makes every wave's chunks visible; after the compute a barrier
-    // frees buffer bx+2 (computed last step) for the tile after Y.
-    uint32_t gx = row_lo, gy = 0, next = row_lo, bx = 0;
-    bool hx = gx < row_hi, hy = false;
-    if (hx) { const Tile t = tile_at(a, gx, row_hi); next += t.nr; tile_issue(t, g_tiles); }
-    if (hx && next < row_hi) {
-        gy = next; hy = true;
-        const Tile t = tile_at(a, gy, row_hi); next += t.nr; tile_issue(t, g_tiles + TILE_BYTES);
+    // byte-balanced row range [row_lo, row_hi) of this workgroup (global rows
+    // of the concatenated segments), then its share of each segment
+    uint32_t row_lo;
+    {
+        uint32_t rb_eff[SINTER_GEMV_MAX_SEG];
+        uint64_t total = 0;
+#pragma unroll
+        for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
+            const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
+            rb_eff[s] = s < a.n_seg ? (uint32_t)sinter_row_bytes_dev(a.seg[s].type, K) * (sw ? 2u : 1u) : 0u;
+            total += s < a.n_seg ? (uint64_t)a.seg[s].rows * rb_eff[s] : 0ull;
+        }
+        row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
+        const uint32_t row_hi = uni(row_cut(a, rb_eff, total, rel + 1, nblk));
+        const uint32_t s = threadIdx.x;
+        if (s < n_seg) {
+            uint32_t base = 0;
+            for (uint32_t j = 0; j < s; j++) base += a.seg[j].rows;
+            const sinter_gemv_seg &g = a.seg[s];
+            const uint32_t lo = min(max(row_lo, base), base + g.rows) - base;
+            const uint32_t hi = min(max(row_hi, base), base + g.rows) - base;
+            const bool sw = g.epi == SINTER_EPI_SWIGLU;
+            const uint32_t T = items_per_tile(g.type, sw);
+            uint32_t *e = g_gseg + s * GS_STRIDE;
+            e[GS_ROW_LO] = lo;
+            e[GS_ROW_HI] = hi;
+            e[GS_LR_BASE] = base - row_lo;   // workgroup-local index of segment row r is r + this
+            e[GS_TYPE] = (uint32_t)g.type;
+            e[GS_SWIGLU] = sw ? 1u : 0u;
+            e[GS_IB] = item_bytes(g.type);
+            e[GS_T] = T;
+            e[GS_QT] = T / ipr;
+            e[GS_RT] = T % ipr;
+            e[GS_W_LO] = (uint32_t)reinterpret_cast<uintptr_t>(g.w);
+            e[GS_W_HI] = (uint32_t)(reinterpret_cast<uintptr_t>(g.w) >> 32);
+            e[GS_W2_LO] = (uint32_t)reinterpret_cast<uintptr_t>(g.w2);
+            e[GS_W2_HI] = (uint32_t)(reinterpret_cast<uintptr_t>(g.w2) >> 32);
+        }
+        // every ring slot starts as -0.0 (pad slots keep it)
+        for (uint32_t i = threadIdx.x; i < CB_CAP; i += BLOCK_THREADS) g_cb[i] = -0.0;
+        __syncthreads();
     }
+
+    // The tile pipeline: X = tile being computed (buffer bx), Y = next (in
+    // flight), the tile after Y is created and issued this iteration into the
+    // buffer that X-1 occupied, P = the previous tile.  One barrier per tile
+    // makes X's DMA and the previous terms visible to every wave and frees
+    // P's buffer; a deferred ring folds P's rows in the same step, otherwise
+    // X's rows are folded after a second barrier.
+    Cursor cur;
+    cur_seg(cur, 0, n_seg, ipr);
+    TD X = tile_next(cur, g_tiles, n_seg, ipr);
+    TD Y = tile_next(cur, g_tiles + TILE_BYTES, n_seg, ipr);
 
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
     gemv_prologue(a, vt, write_x, g_qbuf, g_red, err);   // ends with __syncthreads()
+    settle_vmem();
     const ActView x = act_view(g_qbuf, K, vt);
 
     float bv = -INFINITY;
     int32_t bi = 0x7fffffff;
-    uint32_t res_row0 = row_lo, res_n = 0;
-    while (hx) {
-        const Tile t = tile_at(a, gx, row_hi);
-        if (res_n + t.nr > RES_CAP) {
-            __syncthreads();
-            gemv_flush(a, res_row0, res_n, bv, bi);
-            res_row0 += res_n;
-            res_n = 0;
-            __syncthreads();
-        }
-        if (hy) wait_vmcnt<TILE_CPW>(); else wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        tile_compute(a, t, g_tiles + bx * TILE_BYTES, res_n, x);
-        res_n += t.nr;
+    uint32_t res_row0 = 0;           // workgroup-local first row not yet flushed
+    TD P;
+    P.ok = 0; P.a = 0; P.cnt = 0; P.ra = 0; P.ka = 0; P.type = 0; P.swig = 0; P.lr0 = 0; P.skew_a = 0; P.base_b = 0;
+    uint32_t bx = 0;
+    while (X.ok) {
+        if (Y.ok) wait_vmcnt<TILE_CPW>(); else wait_vmcnt<0>();
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
         const uint32_t bz = bx == 0 ? 2u : bx - 1;
-        bool hz = hy && next < row_hi;
-        uint32_t gz = 0;
-        if (hz) { gz = next; const Tile tz = tile_at(a, gz, row_hi); next += tz.nr; tile_issue(tz, g_tiles + bz * TILE_BYTES); }
-        gx = gy; hx = hy; gy = gz; hy = hz;
+        const TD Z = tile_next(cur, g_tiles + bz * TILE_BYTES, n_seg, ipr);
+        const TD &F = rg.defer ? P : X;       // the tile whose rows this step folds
+        if (rg.defer && P.ok && td_done_after(P, rg) - res_row0 > RES_CAP) {
+            gemv_flush(a, row_lo + res_row0, P.lr0 - res_row0, bv, bi);
+            settle_vmem();
+            res_row0 = P.lr0;
+            __syncthreads();
+        }
+        tile_terms(X, g_tiles + bx * TILE_BYTES, rg, x);
+        if (!rg.defer) {
+            wait_lgkm0();
+            __builtin_amdgcn_s_barrier();
+            if (td_done_after(X, rg) - res_row0 > RES_CAP) {
+                gemv_flush(a, row_lo + res_row0, X.lr0 - res_row0, bv, bi);
+                settle_vmem();
+                res_row0 = X.lr0;
+                __syncthreads();
+            }
+        }
+        if (F.ok) tile_fold(F, rg, res_row0);
+        P = X; X = Y; Y = Z;
         bx = bx == 2 ? 0u : bx + 1;
     }
+    wait_lgkm0();
     __syncthreads();
-    gemv_flush(a, res_row0, res_n, bv, bi);
+    uint32_t rows_total = 0;
+    if (P.ok) {
+        rows_total = td_done_after(P, rg);
+        if (rg.defer) {
+            if (rows_total - res_row0 > RES_CAP) {
+                gemv_flush(a, row_lo + res_row0, P.lr0 - res_row0, bv, bi);
+                res_row0 = P.lr0;
+                __syncthreads();
+            }
+            tile_fold(P, rg, res_row0);
+        }
+    }
+    __syncthreads();
+    gemv_flush(a, row_lo + res_row0, rows_total - res_row0, bv, bi);
 
     // greedy argmax: block-local best, then the last-arriving block reduces
     bool any_argmax = false;

@@ -13,6 +13,7 @@
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -96,12 +97,10 @@ static int vdot(int t) {
 int validate_gemv(const sinter_gemv_args &a, const char **why) {
     auto bad = [&](const char *w) { *why = w; return SINTER_ERR_ARG; };
     if (a.n_seg < 1 || a.n_seg > SINTER_GEMV_MAX_SEG) return bad("n_seg out of range");
-    if (a.K == 0 || a.K % 256) return bad("K must be a positive multiple of 256");
+    if (a.K == 0 || a.K % 256 || a.K > (1u << 20)) return bad("K must be a positive multiple of 256, at most 2^20");
     const int vt = vdot(a.seg[0].type);
     if (vt < 0) return bad("unsupported weight type");
-    const uint64_t need = vt == SINTER_Q8_K ? (uint64_t)(a.K / 256) * 276 + (a.K / 16) * 2
-                        : vt == SINTER_Q8_0 ? (uint64_t)(a.K / 256) * 272 + (a.K / 32) * 4
-                        : vt == SINTER_BF16 ? (uint64_t)(a.K / 64) * 144 : (uint64_t)(a.K / 64) * 272;
+    const uint64_t need = act_bytes(vt, a.K);
     if (need > QBUF_BYTES) return bad("K too large for the activation buffer");
     switch (a.pro) {
     case SINTER_PRO_PLAIN:
@@ -122,15 +121,25 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
         break;
     default: return bad("unknown prologue");
     }
+    // the term ring (gemv.h ring_geometry): R rows of P terms must cover the
+    // rows one tile can touch
+    {
+        const uint32_t ipr = a.K / ((a.seg[0].type == SINTER_BF16 || a.seg[0].type == SINTER_F32) ? 64u : 256u);
+        bool any_swig = false;
+        uint32_t tmax = 0;
+        for (int s = 0; s < a.n_seg; s++) {
+            const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
+            const int t = a.seg[s].type;
+            any_swig |= sw;
+            tmax = std::max(tmax, ((t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u) / (sw ? 2u : 1u));
+        }
+        const uint32_t P = ipr + (ipr & 1u), R = (any_swig ? CB_CAP / 2 : CB_CAP) / P;
+        if (R < (tmax + ipr - 1) / ipr + 1) return bad("rows too long for the term ring");
+    }
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
         if (vdot(g.type) != vt) return bad("segments must share one vec_dot type");
         if (!g.w || !al16(g.w) || !g.y) return bad("segment weights must be 16-byte aligned; y required");
-        const bool sw = g.epi == SINTER_EPI_SWIGLU;
-        const uint64_t rbe = sinter_row_bytes_dev(g.type, a.K) * (sw ? 2 : 1);
-        if (rbe > TILE_BYTES - 64) return bad("row too long for one LDS tile");
-        const uint32_t ie = (g.type == SINTER_BF16 || g.type == SINTER_F32) ? 64u : 256u;
-        if ((a.K / ie) * (sw ? 2u : 1u) > CB_CAP) return bad("row has too many items for one tile");
         switch (g.epi) {
         case SINTER_EPI_STORE: break;
         case SINTER_EPI_RESID: if (!g.aux) return bad("resid: aux"); break;

@@ -26,8 +26,29 @@ constexpr unsigned TILE_BYTES = 36u * 1024u;
 constexpr unsigned TILE_CPW = TILE_BYTES / 1024u / (BLOCK_THREADS / 64u);
 constexpr unsigned QBUF_BYTES = 40u * 1024u;   // padded activation: Q8_K K=17408 20944 B; BF16 K=17408 39168 B
 constexpr unsigned RES_CAP = 512u;             // rows buffered before the epilogue runs
-constexpr unsigned CB_CAP = 512u;              // item terms of one tile (rows of up to 512 items)
+constexpr unsigned CB_CAP = 776u;              // GEMV term ring: two tiles of up to 256 item terms,
+                                               // plus the fold's masked over-read (8-term groups)
 static_assert(TILE_CPW * 4u * 1024u == TILE_BYTES, "tile = whole chunks per wave");
+
+// GEMV activation layout in LDS.  Padded so that lanes working on different
+// groups/chunks start on different LDS banks (an unpadded 256-byte group
+// stride puts every group on bank 0 and serialises the activation reads):
+//   Q8_K: int8 codes, group g at g*ACT_GSTRIDE | d f32[G] | (16-aligned) bsums i16[16G]
+//   Q8_0: int8 codes, group g at g*ACT_GSTRIDE | d f32[K/32] (f16-rounded)
+//   BF16: 64-element chunk c at c*ACT_BF_CSTRIDE (u16)
+//   F32:  64-element chunk c at c*ACT_F_CSTRIDE
+constexpr uint32_t ACT_GSTRIDE = 272;
+constexpr uint32_t ACT_BF_CSTRIDE = 144;
+constexpr uint32_t ACT_F_CSTRIDE = 272;
+__host__ __device__ inline uint32_t act_bs_off(uint32_t K) {
+    return (K / 256) * ACT_GSTRIDE + (((K / 256) * 4 + 15u) & ~15u);
+}
+__host__ __device__ inline uint32_t act_bytes(int vt, uint32_t K) {
+    if (vt == SINTER_Q8_K) return act_bs_off(K) + (K / 16) * 2;
+    if (vt == SINTER_Q8_0) return (K / 256) * ACT_GSTRIDE + (K / 32) * 4;
+    if (vt == SINTER_BF16) return (K / 64) * ACT_BF_CSTRIDE;
+    return (K / 64) * ACT_F_CSTRIDE;
+}
 
 // bytes of one row of k elements of a ggml type
 __host__ __device__ inline size_t sinter_row_bytes_dev(int t, int64_t k) {
