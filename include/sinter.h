@@ -186,14 +186,22 @@ typedef struct sinter_attn_args {
     const float *k_norm;    /* [HD] */
     uint16_t *kc;           /* K cache f16 [n_ctx][NKV*HD] */
     uint16_t *vc;           /* V cache f16 [n_ctx][NKV*HD] */
-    double *part;           /* partials [NKV][n_chunks][NQ/NKV][HD+2] fp64 */
-    uint32_t *count;        /* [NKV] arrival counters, 0 before first use (self-resetting) */
+    double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64, then the merge-tree
+                               nodes [NKV][ceil(n_chunks/8)][NQ/NKV][HD+2]; sinter_attn_part_len */
+    uint32_t *count;        /* arrival counters, sinter_attn_count_len words, 0 before first use
+                               (self-resetting) */
     float *out;             /* [NQ*HD] gated attention output */
     const int32_t *pass_cell; /* sinter_pass_cell (pos) */
     uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;
     float theta_scale, eps, scale;
     uint32_t _pad;
 } sinter_attn_args;
+
+/* Buffer sizes for sinter_attn_args (n_chunks <= 64): part in doubles,
+ * count in 32-bit words.  No counterpart in the reference (its merge reads a
+ * fixed 72-way partial array); the split-K merge here is a fan-in-8 tree. */
+size_t   sinter_attn_part_len(uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t n_chunks);
+uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks);
 
 /* ------------------------------------------------------------------ host control plane */
 /* core/host.h:62-80.  Lifecycle: init -> upload -> launch -> run_pass* ->

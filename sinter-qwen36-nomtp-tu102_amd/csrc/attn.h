@@ -56,13 +56,87 @@ __device__ __forceinline__ void att_norm_rope(float x, const float *w, float eps
     __syncthreads();
 }
 
+constexpr uint32_t ATT_FAN = 8;   // partials merged per step of the merge tree
+
+// Merge n (<= ATT_FAN) consecutive partials {acc[HD], m, l} of each of gqa
+// q heads (fp64, coherent reads): M = max m_i, acc = sum_i e_i acc_i,
+// l = sum_i e_i l_i with e_i = exp(m_i - M), in ascending i; a partial with
+// m = -inf contributes nothing.  Thread t owns dim t.  With dst, the merged
+// unnormalised partial goes there; otherwise out = acc/l * sigmoid(gate).
+// ew: LDS scratch of ATT_MAXG * (ATT_FAN + 1) doubles.
+__device__ void att_merge(const sinter_attn_args &a, const double *src, uint32_t n, uint32_t gqa, uint32_t g,
+                          double *dst, double *ew) {
+    const uint32_t t = threadIdx.x, HD = a.hd, PS = HD + 2;
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * gqa * PS * 8);
+    // weights e[hh][i] and the max, one lane per q head
+    if (t < gqa) {
+        double m[ATT_FAN], M = -INFINITY;
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++) {
+            m[i] = i < n ? ld_coh8(r, ((i * gqa + t) * PS + HD) * 8) : -INFINITY;
+            M = fmax(M, m[i]);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++)
+            ew[t * (ATT_FAN + 1) + i] = (m[i] == -INFINITY) ? 0.0 : exp(m[i] - M);
+        ew[t * (ATT_FAN + 1) + ATT_FAN] = M;
+    }
+    __syncthreads();
+    for (uint32_t hh = 0; hh < gqa; hh++) {
+        const double *e = ew + hh * (ATT_FAN + 1);
+        double pv[ATT_FAN], lv[ATT_FAN];
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++) {
+            const uint32_t o = (i * gqa + hh) * PS;
+            pv[i] = i < n ? ld_coh8(r, (o + t) * 8) : 0.0;
+            lv[i] = i < n ? ld_coh8(r, (o + HD + 1) * 8) : 0.0;
+        }
+        double O = 0.0, L = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++) {
+            if (i < n && e[i] != 0.0) {
+                O = fma(e[i], pv[i], O);
+                L = fma(e[i], lv[i], L);
+            }
+        }
+        if (dst) {
+            double *d = dst + hh * PS;
+            st_coh(d + t, O);
+            if (t == 0) { st_coh(d + HD, e[ATT_FAN]); st_coh(d + HD + 1, L); }
+        } else {
+            const uint32_t h = g * gqa + hh;
+            const float att = (float)(O / L);
+            const float gate = ld_coh(a.qg + (size_t)h * 2 * HD + HD + t);
+            st_coh(a.out + (size_t)h * HD + t, att * dev_sigmoid(gate));
+        }
+    }
+    settle_vmem();
+    __syncthreads();
+}
+
+// Count one arrival at *cnt of `total`; true (uniform) for the last arriver,
+// which also resets the counter for the next use.
+__device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, unsigned *flag) {
+    settle_vmem();   // every wave's partial stores complete before the count
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned last = (old == total - 1) ? 1u : 0u;
+        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
 __device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
     const sinter_attn_args &a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
-    const int pos = reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos;
+    const int pos = ld_coh(&reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos);
     const uint32_t gqa = NKV ? NQ / NKV : 0;
     const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 &&
+                    C <= ATT_FAN * ATT_FAN &&
                     a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 && (uint32_t)pos < a.n_ctx;
     if (!ok) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
@@ -88,6 +162,7 @@ __device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
     double *red = corr + ATT_MAXG;                                       // 16
     float *knf = reinterpret_cast<float *>(red + 16);                    // [256] k scratch
     unsigned *flag = reinterpret_cast<unsigned *>(knf + 256);
+    double *ew = reinterpret_cast<double *>(g_tiles + 2 * TILE_BYTES);    // [ATT_MAXG][ATT_FAN+1] merge weights
 
     for (uint32_t item = rel; item < NKV * C; item += nblk) {
         const uint32_t g = item / C, c = item % C;
@@ -96,16 +171,16 @@ __device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
 
         for (uint32_t hh = 0; hh < gqa; hh++) {
             const uint32_t h = g * gqa + hh;
-            att_norm_rope(a.qg[(size_t)h * 2 * HD + t], a.q_norm, a.eps, pos, a.theta_scale, a.rope_dims,
+            att_norm_rope(ld_coh(a.qg + (size_t)h * 2 * HD + t), a.q_norm, a.eps, pos, a.theta_scale, a.rope_dims,
                           qf + hh * 256, red);
         }
         if (owner) {
-            att_norm_rope(a.k[(size_t)g * HD + t], a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, knf, red);
-            const uint16_t kh = f2h(knf[t]), vh = f2h(a.v[(size_t)g * HD + t]);
+            att_norm_rope(ld_coh(a.k + (size_t)g * HD + t), a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, knf, red);
+            const uint16_t kh = f2h(knf[t]), vh = f2h(ld_coh(a.v + (size_t)g * HD + t));
             knew[t] = kh;
             vnew[t] = vh;
-            a.kc[(size_t)pos * RW + (size_t)g * HD + t] = kh;
-            a.vc[(size_t)pos * RW + (size_t)g * HD + t] = vh;
+            st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
+            st_coh(a.vc + (size_t)pos * RW + (size_t)g * HD + t, vh);
         }
         if (t < gqa) { mrun[t] = -INFINITY; lrun[t] = 0.0; }
         double acc[ATT_MAXG];
@@ -182,42 +257,24 @@ __device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
             __syncthreads();
         }
 
-        // publish the partial, count in; the last block of kv head g merges
-        double *pbase = a.part + ((size_t)g * C + c) * gqa * (HD + 2);
+        // publish the partial; the merge is a tree of fan-in ATT_FAN over
+        // the chunks, each node merged by the last arriver of its children
+        const uint32_t PS = HD + 2, G1 = (C + ATT_FAN - 1) / ATT_FAN, g1 = c / ATT_FAN;
+        double *pbase = a.part + ((size_t)g * C + c) * gqa * PS;
         for (uint32_t hh = 0; hh < gqa; hh++) {
-            double *p = pbase + hh * (HD + 2);
-            p[t] = acc[hh];
-            if (t == 0) { p[HD] = mrun[hh]; p[HD + 1] = lrun[hh]; }
+            double *p = pbase + hh * PS;
+            st_coh(p + t, acc[hh]);
+            if (t == 0) { st_coh(p + HD, mrun[hh]); st_coh(p + HD + 1, lrun[hh]); }
         }
-        __syncthreads();
-        if (t == 0) {
-            fence_release_agent();
-            const unsigned old = __hip_atomic_fetch_add(a.count + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned last = (old == C - 1) ? 1u : 0u;
-            if (last) fence_acquire_agent();
-            *flag = last;
-        }
-        __syncthreads();
-        if (*flag) {
-            const double *gbase = a.part + (size_t)g * C * gqa * (HD + 2);
-            for (uint32_t hh = 0; hh < gqa; hh++) {
-                double M = -INFINITY;
-                for (uint32_t cc = 0; cc < C; cc++) M = fmax(M, gbase[(cc * gqa + hh) * (HD + 2) + HD]);
-                double O = 0.0, L = 0.0;
-                for (uint32_t cc = 0; cc < C; cc++) {
-                    const double *p = gbase + (cc * gqa + hh) * (HD + 2);
-                    const double m = p[HD];
-                    if (m == -INFINITY) continue;
-                    const double e = exp(m - M);
-                    O = fma(e, p[t], O);
-                    L = fma(e, p[HD + 1], L);
-                }
-                const uint32_t h = g * gqa + hh;
-                const float att = (float)(O / L);
-                const float gate = a.qg[(size_t)h * 2 * HD + HD + t];
-                a.out[(size_t)h * HD + t] = att * dev_sigmoid(gate);
+        const uint32_t n1 = min(ATT_FAN, C - g1 * ATT_FAN);
+        double *lvl1 = a.part + (size_t)NKV * C * gqa * PS;                 // [NKV][G1][gqa][PS]
+        if (att_arrive(a.count + NKV + g * G1 + g1, n1, flag)) {
+            double *node = lvl1 + ((size_t)g * G1 + g1) * gqa * PS;
+            att_merge(a, a.part + ((size_t)g * C + g1 * ATT_FAN) * gqa * PS, n1, gqa, g, G1 > 1 ? node : nullptr, ew);
+            if (G1 > 1 && att_arrive(a.count + g, G1, flag)) {
+                // G1 <= ATT_FAN: the root merges the group nodes
+                att_merge(a, lvl1 + (size_t)g * G1 * gqa * PS, G1, gqa, g, nullptr, ew);
             }
-            if (t == 0) __hip_atomic_store(a.count + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
     }

@@ -108,12 +108,63 @@ __device__ __forceinline__ float dev_softplus(float x) {
 __device__ __forceinline__ unsigned atomic_load_relaxed_agent(const unsigned *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void fence_release_agent() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+
+// Cross-workgroup data -- every activation, partial and pass-cell word that
+// one workgroup writes and another reads later in the pass -- moves through
+// device-coherent accesses (agent-scope relaxed atomics: sc1 loads and
+// stores, which neither hit nor leave stale lines in an XCD's L2).  A
+// workgroup's coherent stores are complete once it has waited vmcnt(0), so
+// the grid barrier needs no L2 writeback or invalidate (each costs
+// microseconds on gfx950) and orders them by the barrier counter alone.
+// Immutable data (weights, norms) and data a workgroup only shares with
+// itself across passes (recurrent and conv state) use ordinary cached
+// accesses.
+template <class T>
+__device__ __forceinline__ T ld_coh(const T *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <class T>
+__device__ __forceinline__ void st_coh(T *p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// 16 bytes (16-aligned) as two coherent 8-byte loads / stores
+__device__ __forceinline__ float4 ld_coh4(const float *p) {
+    const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+    const uint64_t a = ld_coh(q), b = ld_coh(q + 1);
+    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
+                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
 }
-__device__ __forceinline__ void fence_acquire_agent() {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+__device__ __forceinline__ void st_coh4(float *p, float4 v) {
+    uint64_t *q = reinterpret_cast<uint64_t *>(p);
+    st_coh(q, (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32));
+    st_coh(q + 1, (uint64_t)__float_as_uint(v.z) | ((uint64_t)__float_as_uint(v.w) << 32));
 }
+// Bulk coherent reads: raw buffer loads with the sc1 cache policy (plain,
+// non-atomic loads the compiler batches freely; a load past num_records
+// returns 0 instead of faulting).  The base must be wave-uniform.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void *base, uint32_t bytes) {
+    // readfirstlane returns int: widen through uint32_t (a sign-extended low
+    // word with bit 31 set would overwrite the high word)
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uintptr_t u = ((uintptr_t)hi << 32) | (uintptr_t)lo;
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(u), (short)0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+__device__ __forceinline__ float4 ld_coh16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ double ld_coh8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ float ld_coh4b(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
+}
+
+// wait until this wave's memory operations are complete (a real s_waitcnt
+// the compiler's wait-count pass accounts for); gfx9 encoding vmcnt 0,
+// expcnt 7, lgkmcnt 15
+__device__ __forceinline__ void settle_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Record the first error: err[0] = code (first writer wins), err[1] = aux.
 // Ops call this and return normally so every block still reaches the next

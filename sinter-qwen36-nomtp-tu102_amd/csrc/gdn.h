@@ -54,8 +54,8 @@ __device__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
         double sq = 0.0, sk = 0.0;
         float qv = 0.0f, kv = 0.0f;
         if (threadIdx.x < D) {
-            qv = qsrc[threadIdx.x];
-            kv = ksrc[threadIdx.x];
+            qv = ld_coh(qsrc + threadIdx.x);
+            kv = ld_coh(ksrc + threadIdx.x);
             sq = (double)(qv * qv);
             sk = (double)(kv * kv);
         }
@@ -66,9 +66,9 @@ __device__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
             ks[threadIdx.x] = kv * (1.0f / fmaxf(sqrtf((float)sk), a.eps));
         }
         if (threadIdx.x == 0) {
-            const float sp = dev_softplus(a.alpha[h] + a.dt_bias[h]);
+            const float sp = dev_softplus(ld_coh(a.alpha + h) + a.dt_bias[h]);
             gb[0] = (float)exp((double)(sp * a.ssm_a[h]));
-            gb[1] = dev_sigmoid(a.beta[h]);
+            gb[1] = dev_sigmoid(ld_coh(a.beta + h));
         }
         __syncthreads();
         const float g = gb[0], beta = gb[1];
@@ -92,7 +92,7 @@ __device__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
         for (uint32_t o = 1; o < tpc; o <<= 1) dkv += __shfl_xor(dkv, (int)o, 64);
         const float kvf = (float)dkv;
         const float t1 = g * kvf;
-        const float t2 = vsrc[col] - t1;
+        const float t2 = ld_coh(vsrc + col) - t1;
         const float delta = t2 * beta;
         double dout = 0.0;
 #pragma unroll
@@ -108,7 +108,7 @@ __device__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
 #pragma unroll
         for (uint32_t r = 0; r < 32; r += 4)
             if (r < rpt) *reinterpret_cast<float4 *>(srow + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
-        if ((threadIdx.x % tpc) == 0) a.o[(size_t)h * D + col] = (float)dout * a.scale;
+        if ((threadIdx.x % tpc) == 0) st_coh(a.o + (size_t)h * D + col, (float)dout * a.scale);
         __syncthreads();  // qs/ks/gb reused by the next item
     }
 }

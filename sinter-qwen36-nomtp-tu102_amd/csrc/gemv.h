@@ -127,11 +127,12 @@ __device__ __forceinline__ void dequant4(const void *row, int type, uint32_t e, 
 // ------------------------------------------------------------ prologue
 
 // Raw input value of elements [e, e+4): x, or the embedding row.
-__device__ __forceinline__ void pro_raw4(const sinter_gemv_args &a, const void *erow, uint32_t e, float v[4]) {
+__device__ __forceinline__ void pro_raw4(const sinter_gemv_args &a, __amdgpu_buffer_rsrc_t xr, const void *erow,
+                                         uint32_t e, float v[4]) {
     if (a.pro == SINTER_PRO_EMBED) {
         dequant4(erow, a.aux_type, e, v);
     } else {
-        const float4 t = *reinterpret_cast<const float4 *>(a.x + e);
+        const float4 t = ld_coh16(xr, e * 4);
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     }
 }
@@ -141,9 +142,11 @@ __device__ __forceinline__ void pro_raw4(const sinter_gemv_args &a, const void *
 __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, char *q, double *red,
                               unsigned *err) {
     const uint32_t K = a.K;
+    const __amdgpu_buffer_rsrc_t xr = coh_rsrc(a.x, K * 4);
+    const __amdgpu_buffer_rsrc_t zr = coh_rsrc(a.aux, a.pro == SINTER_PRO_GATED ? K * 4 : 0);
     const void *erow = nullptr;
     if (a.pro == SINTER_PRO_EMBED) {
-        int32_t tok = *a.token;
+        int32_t tok = ld_coh(a.token);
         if (tok < 0 || (uint32_t)tok >= a.aux_rows) {   // never read outside the table
             if (threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, 0xE0000000u);
             tok = 0;
@@ -157,7 +160,7 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
         double s = 0.0;
         for (uint32_t e = threadIdx.x * 4; e < K; e += blockDim.x * 4) {
             float v[4];
-            pro_raw4(a, erow, e, v);
+            pro_raw4(a, xr, erow, e, v);
 #pragma unroll
             for (int i = 0; i < 4; i++) s += (double)(v[i] * v[i]);
         }
@@ -174,8 +177,8 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
     for (uint32_t c = wave_id(); c < K / 256; c += nw) {
         const uint32_t e = c * 256 + lane * 4;
         float v[4], t[4];
-        pro_raw4(a, erow, e, v);
-        if (write_x) *reinterpret_cast<float4 *>(a.x_out + e) = make_float4(v[0], v[1], v[2], v[3]);
+        pro_raw4(a, xr, erow, e, v);
+        if (write_x) st_coh4(a.x_out + e, make_float4(v[0], v[1], v[2], v[3]));
         if (a.pro == SINTER_PRO_PLAIN) {
 #pragma unroll
             for (int i = 0; i < 4; i++) t[i] = v[i];
@@ -187,7 +190,7 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
             for (uint32_t o = 1; o < gd / 4; o <<= 1) s += __shfl_xor(s, (int)o, 64);
             const float mean = (float)(s / (double)gd);
             const float hs = 1.0f / sqrtf(mean + a.eps);
-            const float4 z = *reinterpret_cast<const float4 *>(static_cast<const float *>(a.aux) + e);
+            const float4 z = ld_coh16(zr, e * 4);
             const float zz[4] = {z.x, z.y, z.z, z.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -680,12 +683,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-// s_waitcnt vmcnt(0) as a real instruction the compiler's wait-count pass
-// sees: after it, no compiler-visible memory operation is pending, so the
-// pass does not put a vmcnt(0) (which would also wait for the in-flight tile
-// DMA) in front of later register reuse.  gfx9 encoding: vmcnt 0, expcnt 7,
-// lgkmcnt 15.
-__device__ __forceinline__ void settle_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Item terms of a landed tile into the term ring.
 template <int TYPE>
@@ -818,7 +815,7 @@ __device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n,
         if (sg.epi == SINTER_EPI_SWIGLU) {
             y = dev_silu(dot) * g_res[2 * i + 1];
         } else if (sg.epi == SINTER_EPI_RESID) {
-            y = sg.aux[r] + dot;
+            y = ld_coh(sg.aux + r) + dot;
         } else if (sg.epi == SINTER_EPI_CONV) {
             // causal conv over {state[0..dc-2], dot}, fp64 sum rounded once,
             // then silu; the state shifts by one tap (this block owns row r)
@@ -841,7 +838,7 @@ __device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n,
         } else if (sg.epi == SINTER_EPI_ARGMAX) {
             if (y > bv || (y == bv && (int32_t)r < bi)) { bv = y; bi = (int32_t)r; }
         }
-        sg.y[r] = y;
+        st_coh(sg.y + r, y);
     }
 }
 
@@ -1018,26 +1015,26 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
         raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
     } else if (any_argmax && threadIdx.x == 0) {
         sinter_argmax_ws *ws = static_cast<sinter_argmax_ws *>(a.epi_ws);
-        ws->part_val[rel] = bv;
-        ws->part_idx[rel] = bi;
-        fence_release_agent();
+        st_coh(ws->part_val + rel, bv);
+        st_coh(ws->part_idx + rel, bi);
+        settle_vmem();
         const unsigned old = __hip_atomic_fetch_add(ws->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == nblk - 1) {
-            fence_acquire_agent();
             float best = -INFINITY;
             int32_t bidx = 0x7fffffff;
+            const __amdgpu_buffer_rsrc_t vr = coh_rsrc(ws->part_val, nblk * 4), ir = coh_rsrc(ws->part_idx, nblk * 4);
             for (uint32_t w = 0; w < nblk; w++) {
-                const float v = __hip_atomic_load(ws->part_val + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const int32_t i = __hip_atomic_load(ws->part_idx + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float v = ld_coh4b(vr, w * 4);
+                const int32_t i = __float_as_int(ld_coh4b(ir, w * 4));
                 if (v > best || (v == best && i < bidx)) { best = v; bidx = i; }
             }
             sinter_pass_cell *pc = reinterpret_cast<sinter_pass_cell *>(ws->pass_cell);
-            if (ws->history && (uint32_t)pc->steps < ws->history_cap) ws->history[pc->steps] = bidx;
-            pc->steps += 1;
-            pc->token = bidx;
-            pc->pos += 1;
+            const int32_t steps = ld_coh(&pc->steps);
+            if (ws->history && (uint32_t)steps < ws->history_cap) st_coh(ws->history + steps, bidx);
+            st_coh(&pc->steps, steps + 1);
+            st_coh(&pc->token, bidx);
+            st_coh(&pc->pos, ld_coh(&pc->pos) + 1);
             __hip_atomic_store(ws->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            fence_release_agent();
         }
     }
     __syncthreads();

@@ -226,11 +226,21 @@ int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream) 
     return run_one(SINTER_OP_GDN_STEP, *a, blocks, stream);
 }
 
+size_t sinter_attn_part_len(uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t n_chunks) {
+    if (!nkv || !n_chunks) return 0;
+    return (size_t)nkv * (n_chunks + (n_chunks + 7) / 8) * (nq / nkv) * (hd + 2);
+}
+
+uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks) {
+    return nkv * (1 + (n_chunks + 7) / 8);
+}
+
 int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream) {
     if (!a || !a->qg || !a->k || !a->v || !a->q_norm || !a->k_norm || !a->kc || !a->vc || !a->part || !a->count ||
         !a->out || !a->pass_cell)
         return set_error(SINTER_ERR_ARG, "attn: null pointer");
-    if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->rope_dims > a->hd ||
+    if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
+        a->rope_dims > a->hd ||
         a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
         return set_error(SINTER_ERR_ARG, "attn: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
     return run_one(SINTER_OP_ATTN_DECODE, *a, blocks, stream);
@@ -326,12 +336,17 @@ int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k
 
 // ----------------------------------------------------------------- host control plane
 
+// control cells: barrier root, error cell, pass cell, then the barrier group
+// counters for up to 64 groups (1024 workgroups)
+static constexpr size_t CELL_GROUPS = 4096, CELL_GROUP_BYTES = 64 * 128, CELL_BYTES = CELL_GROUPS + CELL_GROUP_BYTES;
+
 struct sinter_host {
     int device = -1;
     hipStream_t stream = nullptr;
     sinter_instr *d_prog = nullptr;
     uint32_t n_instr = 0, epoch_stride = 0;
-    unsigned *d_cells = nullptr;          // [0] barrier counter | [32] err[2]
+    unsigned *d_cells = nullptr;          // [0] barrier root | [32] err[2] | byte 1024 pass cell |
+                                          // byte CELL_GROUPS: barrier group counters (128 B each)
     sinter_pass_cell *d_pass = nullptr;
     int32_t *d_history = nullptr;
     uint32_t history_cap = 0;
@@ -352,6 +367,7 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     InterpCtl ctl;
     std::memset(&ctl, 0, sizeof ctl);
     ctl.bar = h->d_cells;
+    ctl.groups = h->d_cells + CELL_GROUPS / 4;
     ctl.err = h->d_cells + 32;
     ctl.pass_cycles = h->d_pass_cycles;
     ctl.pass_cycles_cap = h->pass_cycles_cap;
@@ -360,7 +376,9 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     ctl.spin_limit = h->spin_limit;
     ctl.n_instr = h->n_instr;
     ctl.n_passes = n_passes;
-    if (!hip_ok(hipMemsetAsync(h->d_cells, 0, 4, h->stream), "barrier reset")) return SINTER_RUN_ERR;
+    if (!hip_ok(hipMemsetAsync(h->d_cells, 0, 4, h->stream), "barrier reset") ||
+        !hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream), "barrier groups reset"))
+        return SINTER_RUN_ERR;
     if (!hip_ok(hipEventRecord(h->ev0, h->stream), "event")) return SINTER_RUN_ERR;
     if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream), "cooperative launch")) return SINTER_RUN_ERR;
     if (!hip_ok(hipEventRecord(h->ev1, h->stream), "event")) return SINTER_RUN_ERR;
@@ -414,7 +432,7 @@ int sinter_host_init(sinter_host **out, int device, unsigned pass_cycles_cap) {
     h->spin_limit = h->clock_khz * 1000ull * 10ull;  // 10 s
     bool ok = hip_ok(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "stream") &&
               hip_ok(hipEventCreate(&h->ev0), "event") && hip_ok(hipEventCreate(&h->ev1), "event") &&
-              hip_ok(hipMalloc(&h->d_cells, 4096), "cells") && hip_ok(hipMemset(h->d_cells, 0, 4096), "cells clear");
+              hip_ok(hipMalloc(&h->d_cells, CELL_BYTES), "cells") && hip_ok(hipMemset(h->d_cells, 0, CELL_BYTES), "cells clear");
     if (ok) h->d_pass = reinterpret_cast<sinter_pass_cell *>(reinterpret_cast<char *>(h->d_cells) + 1024);
     h->pass_cycles_cap = pass_cycles_cap;
     if (ok && pass_cycles_cap) {
@@ -569,7 +587,7 @@ int sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32
 }
 
 int sinter_host_set_grid(sinter_host *h, uint32_t blocks) {
-    if (!h || blocks == 0) return set_error(SINTER_ERR_ARG, "set_grid: args");
+    if (!h || blocks == 0 || blocks > CELL_GROUP_BYTES / 128 * 16) return set_error(SINTER_ERR_ARG, "set_grid: args");
     if (h->launched) return set_error(SINTER_ERR_STATE, "set_grid after launch");
     hipDeviceProp_t p;
     if (!hip_ok(hipGetDeviceProperties(&p, h->device), "device properties")) return SINTER_ERR_HIP;

@@ -38,21 +38,28 @@ __device__ __forceinline__ void dispatch(const sinter_instr &ins, unsigned *err)
     }
 }
 
-// Grid barrier over a monotonic counter (zeroed before the launch): every
-// workgroup release-arrives, one thread spins until epoch*gridDim arrivals,
-// then acquires.  The agent-scope release writes back this XCD's L2 and the
-// acquire invalidates L1/L2, so plain loads after the barrier observe every
-// store made before any workgroup's arrival.  Returns false on timeout.
-__device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned &epoch, uint64_t spin_limit_ticks,
-                                             unsigned *err) {
+// Grid barrier, two-level, over monotonic counters (zeroed before the
+// launch): workgroup w counts into group counter w/16 (its own 128-byte
+// line); the group's last arriver counts into the root; every workgroup's
+// thread 0 spins on the root until epoch*groups arrivals.  Sixteen arrivals
+// per line instead of the whole grid on one line (atomics to one address
+// serialise at the memory side).  No cache writeback or invalidate: every
+// wave first waits for its own memory operations, and all data that crosses
+// workgroups moves through device-coherent loads and stores (dev_common.h).
+// Returns false on timeout.
+__device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned *groups, unsigned &epoch,
+                                             uint64_t spin_limit_ticks, unsigned *err) {
+    settle_vmem();
     __syncthreads();
     epoch += 1;
     __shared__ unsigned timed_out;
     if (threadIdx.x == 0) {
         timed_out = 0;
-        fence_release_agent();
-        __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned target = epoch * gridDim.x;
+        const unsigned g = blockIdx.x >> 4, ng = (gridDim.x + 15u) >> 4;
+        const unsigned gsize = min(16u, gridDim.x - g * 16u);
+        const unsigned old = __hip_atomic_fetch_add(groups + g * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned target = epoch * ng;
         const uint64_t t0 = wall_clock64();
         while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
             __builtin_amdgcn_s_sleep(1);
@@ -62,7 +69,6 @@ __device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned &epoch, uin
                 break;
             }
         }
-        fence_acquire_agent();
     }
     __syncthreads();
     return timed_out == 0;
@@ -82,7 +88,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             const unsigned kind = ins.kind;
             if (kind == SINTER_OP_BOUNDARY) {
                 const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
-                if (!grid_barrier(ctl.bar, epoch, ctl.spin_limit, ctl.err)) return;
+                if (!grid_barrier(ctl.bar, ctl.groups, epoch, ctl.spin_limit, ctl.err)) return;
                 if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
                     ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(wall_clock64() - s);
                 continue;
@@ -103,7 +109,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             }
         }
         // pass epilogue: everyone finished, then a uniform error sample
-        if (!grid_barrier(ctl.bar, epoch, ctl.spin_limit, ctl.err)) return;
+        if (!grid_barrier(ctl.bar, ctl.groups, epoch, ctl.spin_limit, ctl.err)) return;
         __shared__ unsigned e;
         if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();

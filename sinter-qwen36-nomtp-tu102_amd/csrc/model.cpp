@@ -58,6 +58,12 @@ bool is_attn(const sinter_model_config &c, int il) {
 
 }  // namespace
 
+// split-K chunks per kv head: one (kv head, chunk) item per workgroup, at
+// most 64 (the merge tree's two levels of fan-in 8)
+static uint32_t attn_chunks(uint32_t blocks, uint32_t nkv) {
+    return std::min(64u, std::max(1u, blocks / nkv));
+}
+
 struct sinter_model {
     sinter_model_config cfg{};
     int device = 0;
@@ -216,7 +222,7 @@ void build_program(sinter_model *m) {
             a.hd = (uint32_t)HD;
             a.rope_dims = (uint32_t)c.rope_dims;
             a.n_ctx = (uint32_t)c.n_ctx;
-            a.n_chunks = std::max(1u, m->blocks / (uint32_t)c.attn_nkv);
+            a.n_chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
             a.theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
             a.eps = c.eps;
             a.scale = 1.0f / std::sqrt((float)HD);
@@ -391,9 +397,9 @@ int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t see
     ok = ok && (m->X = fa(E)) && (m->H = fa(E)) && (m->qkv = fa(C)) && (m->z = fa(VD)) && (m->al = fa(HV)) &&
          (m->be = fa(HV)) && (m->o = fa(VD)) && (m->ffn = fa(F)) && (m->qg = fa((size_t)NQ * 2 * HD)) &&
          (m->kk = fa(RW)) && (m->vv = fa(RW)) && (m->att = fa((size_t)NQ * HD)) && (m->logits = fa(c.n_vocab));
-    const uint32_t chunks = std::max(1u, m->blocks / (uint32_t)NKV);
-    ok = ok && (m->part = (double *)dalloc(m, (size_t)NKV * chunks * (NQ / NKV) * (HD + 2) * 8));
-    ok = ok && (m->count = (unsigned *)dalloc(m, 256));
+    const uint32_t chunks = attn_chunks(m->blocks, NKV);
+    ok = ok && (m->part = (double *)dalloc(m, sinter_attn_part_len(NQ, NKV, HD, chunks) * 8));
+    ok = ok && (m->count = (unsigned *)dalloc(m, (size_t)sinter_attn_count_len(NKV, chunks) * 4));
     if (!ok) return fail(set_error(SINTER_ERR_NOMEM, "model: device allocation or synthesis failed"));
     if (!hip_ok(hipStreamSynchronize(m->stream), "model synthesis")) return fail(SINTER_ERR_HIP);
     uint32_t hcap = 0;

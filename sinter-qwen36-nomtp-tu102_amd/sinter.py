@@ -121,6 +121,8 @@ def lib():
         "sinter_abi_version": (I, []),
         "sinter_device_info": (I, [I, C.c_char_p, C.c_size_t]),
         "sinter_row_bytes": (C.c_size_t, [I, I64]),
+        "sinter_attn_part_len": (C.c_size_t, [U32, U32, U32, U32]),
+        "sinter_attn_count_len": (U32, [U32, U32]),
         "sinter_op_gemv": (I, [C.POINTER(GemvArgs), U32, vp]),
         "sinter_op_gdn_step": (I, [C.POINTER(GdnArgs), U32, vp]),
         "sinter_op_attn_decode": (I, [C.POINTER(AttnArgs), U32, vp]),

@@ -270,7 +270,8 @@ def test_gdn_step_matches_oracle(sn, orc, torch_gpu):
 
 
 @pytest.mark.parametrize("pos,n_ctx,chunks", [(0, 64, 64), (5, 4096, 64), (1000, 4096, 64), (4095, 4096, 64),
-                                              (4095, 4096, 7), (40000, 40960, 64)])
+                                              (4095, 4096, 7), (40000, 40960, 64), (300, 4096, 1),
+                                              (2000, 4096, 9), (3000, 4096, 17)])
 def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     torch = torch_gpu
     NQ, NKV, HD = 24, 4, 256
@@ -288,8 +289,8 @@ def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     ts = orc.lib().or_rope_theta_scale(1e7, 64)
     dK, dV = dev(torch, K.view(np.uint16)), dev(torch, V.view(np.uint16))
     dqg, dk, dv_, dqn, dkn = dev(torch, qg), dev(torch, k), dev(torch, v), dev(torch, qn), dev(torch, kn)
-    part = torch.zeros(NKV * chunks * (NQ // NKV) * (HD + 2), dtype=torch.float64, device="cuda")
-    cnt = torch.zeros(64, dtype=torch.int32, device="cuda")
+    part = torch.zeros(sn.lib().sinter_attn_part_len(NQ, NKV, HD, chunks), dtype=torch.float64, device="cuda")
+    cnt = torch.zeros(sn.lib().sinter_attn_count_len(NKV, chunks), dtype=torch.int32, device="cuda")
     out = empty_f32(torch, NQ * HD)
     cell = dev(torch, np.array([0, pos, 0, 0], np.int32))
     a = sn.AttnArgs(nq=NQ, nkv=NKV, hd=HD, rope_dims=64, n_ctx=n_ctx, n_chunks=chunks, theta_scale=ts, eps=1e-6,
