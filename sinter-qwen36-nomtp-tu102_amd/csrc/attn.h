@@ -64,7 +64,7 @@ constexpr uint32_t ATT_FAN = 8;   // partials merged per step of the merge tree
 // m = -inf contributes nothing.  Thread t owns dim t.  With dst, the merged
 // unnormalised partial goes there; otherwise out = acc/l * sigmoid(gate).
 // ew: LDS scratch of ATT_MAXG * (ATT_FAN + 1) doubles.
-__device__ void att_merge(const sinter_attn_args &a, const double *src, uint32_t n, uint32_t gqa, uint32_t g,
+__device__ __forceinline__ void att_merge(const sinter_attn_args &a, const double *src, uint32_t n, uint32_t gqa, uint32_t g,
                           double *dst, double *ew) {
     const uint32_t t = threadIdx.x, HD = a.hd, PS = HD + 2;
     const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * gqa * PS * 8);
@@ -129,7 +129,7 @@ __device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, unsign
     return *flag != 0;
 }
 
-__device__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
+__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
     const sinter_attn_args &a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;

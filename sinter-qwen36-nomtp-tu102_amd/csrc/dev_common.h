@@ -161,6 +161,9 @@ __device__ __forceinline__ float ld_coh4b(__amdgpu_buffer_rsrc_t r, uint32_t off
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
 }
 
+// the compiler's scheduler moves no instruction across this point
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 // wait until this wave's memory operations are complete (a real s_waitcnt
 // the compiler's wait-count pass accounts for); gfx9 encoding vmcnt 0,
 // expcnt 7, lgkmcnt 15

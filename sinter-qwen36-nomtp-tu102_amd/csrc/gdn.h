@@ -21,7 +21,7 @@
 
 namespace sinter {
 
-__device__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
+__device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
     char *lds = g_tiles;
     const sinter_gdn_args &a = *reinterpret_cast<const sinter_gdn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;

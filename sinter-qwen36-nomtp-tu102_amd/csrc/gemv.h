@@ -126,26 +126,90 @@ __device__ __forceinline__ void dequant4(const void *row, int type, uint32_t e, 
 
 // ------------------------------------------------------------ prologue
 
-// Raw input value of elements [e, e+4): x, or the embedding row.
-__device__ __forceinline__ void pro_raw4(const sinter_gemv_args &a, __amdgpu_buffer_rsrc_t xr, const void *erow,
-                                         uint32_t e, float v[4]) {
-    if (a.pro == SINTER_PRO_EMBED) {
-        dequant4(erow, a.aux_type, e, v);
+// Quantise one 256-element chunk c (values t[4] per lane, 4 consecutive
+// elements each) into the activation layout at q.
+__device__ __forceinline__ void quant_chunk(int vt, uint32_t c, uint32_t e, const float t[4], char *q, float *qd,
+                                            int16_t *qb) {
+    const int lane = lane_id();
+    if (vt == SINTER_Q8_K) {
+        // ggml quantize_row_q8_K_ref: signed element of largest |x|, first index wins
+        float bmax = 0.0f, bamax = 0.0f;
+        int bidx = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float ax = fabsf(t[i]);
+            if (ax > bamax) { bamax = ax; bmax = t[i]; bidx = lane * 4 + i; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float oa = __shfl_xor(bamax, o, 64);
+            const float om = __shfl_xor(bmax, o, 64);
+            const int oi = __shfl_xor(bidx, o, 64);
+            if (oa > bamax || (oa == bamax && oi < bidx)) { bamax = oa; bmax = om; bidx = oi; }
+        }
+        int qv[4] = {0, 0, 0, 0};
+        float dd = 0.0f;
+        if (bamax != 0.0f) {
+            const float iscale = -127.f / bmax;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = (int)__builtin_rintf(iscale * t[i]);
+                qv[i] = r < 127 ? r : 127;
+            }
+            dd = 1.0f / iscale;
+        }
+        const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
+                                ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
+        *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
+        int bsum = qv[0] + qv[1] + qv[2] + qv[3];
+        bsum += __shfl_xor(bsum, 1, 64);
+        bsum += __shfl_xor(bsum, 2, 64);
+        if ((lane & 3) == 0) qb[e / 16] = (int16_t)bsum;
+        if (lane == 0) qd[c] = dd;
+    } else if (vt == SINTER_Q8_0) {
+        // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax)
+        float am = fmaxf(fmaxf(fabsf(t[0]), fabsf(t[1])), fmaxf(fabsf(t[2]), fabsf(t[3])));
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        am = fmaxf(am, __shfl_xor(am, 4, 64));
+        const float d = am / 127.f;
+        const float id = (am != 0.0f) ? 127.f / am : 0.0f;
+        int qv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
+        const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
+                                ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
+        *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
+        if ((lane & 7) == 0) qd[e / 32] = h2f(f2h(d));
+    } else if (vt == SINTER_BF16) {
+        uint16_t *bf = reinterpret_cast<uint16_t *>(q + (e >> 6) * ACT_BF_CSTRIDE) + (e & 63);
+#pragma unroll
+        for (int i = 0; i < 4; i++) bf[i] = f2bf(t[i]);
     } else {
-        const float4 t = ld_coh16(xr, e * 4);
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        float *f = reinterpret_cast<float *>(q + (e >> 6) * ACT_F_CSTRIDE) + (e & 63);
+#pragma unroll
+        for (int i = 0; i < 4; i++) f[i] = t[i];
     }
 }
 
+// chunks per wave the prologue loads per round (all loads of a round are
+// issued before any of them is used)
+constexpr uint32_t PRO_PF = 8;
+
 // Build the quantised activation in LDS at `q`.  Every thread of the block
-// calls this.  `red` is 128 B of LDS scratch.
-__device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, char *q, double *red,
-                              unsigned *err) {
+// calls this.  `red` is 128 B of LDS scratch.  Wave w owns chunks w, w+4, ...
+// and reads them in rounds of PRO_PF chunks, so the prologue pays one memory
+// latency per round instead of one per chunk (a single round for K <= 8192;
+// an RMSNorm with more chunks makes one extra pass for its sum of squares).
+__device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, char *q, double *red,
+                                              unsigned *err) {
     const uint32_t K = a.K;
-    const __amdgpu_buffer_rsrc_t xr = coh_rsrc(a.x, K * 4);
-    const __amdgpu_buffer_rsrc_t zr = coh_rsrc(a.aux, a.pro == SINTER_PRO_GATED ? K * 4 : 0);
+    const bool embed = a.pro == SINTER_PRO_EMBED, gated = a.pro == SINTER_PRO_GATED;
+    const bool rms = a.pro == SINTER_PRO_RMSNORM || embed;
+    const __amdgpu_buffer_rsrc_t xr = coh_rsrc(a.x, embed ? 0u : K * 4);
+    const __amdgpu_buffer_rsrc_t zr = coh_rsrc(a.aux, gated ? K * 4 : 0u);
     const void *erow = nullptr;
-    if (a.pro == SINTER_PRO_EMBED) {
+    if (embed) {
         int32_t tok = ld_coh(a.token);
         if (tok < 0 || (uint32_t)tok >= a.aux_rows) {   // never read outside the table
             if (threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, 0xE0000000u);
@@ -153,118 +217,102 @@ __device__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, c
         }
         erow = static_cast<const char *>(a.aux) + (size_t)tok * sinter_row_bytes_dev(a.aux_type, K);
     }
+    const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
+    const uint32_t lane = lane_id(), w = wave_id(), nw = BLOCK_THREADS / 64, nchunk = K / 256;
+    const uint32_t mine = nchunk > w ? (nchunk - w + nw - 1) / nw : 0u;   // chunks of this wave
+    auto raw4 = [&](uint32_t e, float v[4]) {
+        if (embed) {
+            dequant4(erow, a.aux_type, e, v);
+        } else {
+            const float4 t = ld_coh16(xr, e * 4);
+            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        }
+    };
+    // the second per-element input: the gate z (gated) or the norm weights
+    auto raw4b = [&](uint32_t e, float y[4]) {
+        if (gated) {
+            const float4 z = ld_coh16(zr, e * 4);
+            y[0] = z.x; y[1] = z.y; y[2] = z.z; y[3] = z.w;
+        } else if (rms) {
+            const float4 nv = *reinterpret_cast<const float4 *>(a.norm_w + e);
+            y[0] = nv.x; y[1] = nv.y; y[2] = nv.z; y[3] = nv.w;
+        } else {
+            y[0] = y[1] = y[2] = y[3] = 0.0f;
+        }
+    };
+    float gw[4] = {0.f, 0.f, 0.f, 0.f};     // gated-norm weights: the same for every chunk
+    if (gated) {
+        const float4 t = *reinterpret_cast<const float4 *>(a.norm_w + ((lane * 4) & (gd - 1)));
+        gw[0] = t.x; gw[1] = t.y; gw[2] = t.z; gw[3] = t.w;
+    }
+    float xv[PRO_PF][4], yv[PRO_PF][4];
+    auto load_round = [&](uint32_t j0, bool both) {
+#pragma unroll
+        for (uint32_t j = 0; j < PRO_PF; j++) {
+            if (j0 + j < mine) {
+                const uint32_t e = (w + nw * (j0 + j)) * 256 + lane * 4;
+                raw4(e, xv[j]);
+                if (both) raw4b(e, yv[j]);
+            }
+        }
+    };
     // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
     // scale = 1/sqrtf(mean + eps))
     float gscale = 1.0f;
-    if (a.pro == SINTER_PRO_RMSNORM || a.pro == SINTER_PRO_EMBED) {
+    const bool one_round = mine <= PRO_PF;
+    if (one_round) load_round(0, true);
+    if (rms) {
         double s = 0.0;
-        for (uint32_t e = threadIdx.x * 4; e < K; e += blockDim.x * 4) {
-            float v[4];
-            pro_raw4(a, xr, erow, e, v);
+        for (uint32_t j0 = 0; j0 < mine; j0 += PRO_PF) {
+            if (!one_round) load_round(j0, false);
 #pragma unroll
-            for (int i = 0; i < 4; i++) s += (double)(v[i] * v[i]);
+            for (uint32_t j = 0; j < PRO_PF; j++)
+                if (j0 + j < mine)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s += (double)(xv[j][i] * xv[j][i]);
         }
         s = block_sum_f64(s, red);
         const float mean = (float)(s / (double)K);
         gscale = 1.0f / sqrtf(mean + a.eps);
     }
-    const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (64..256)
-    const int lane = lane_id();
-    const int nw = blockDim.x >> 6;
     float *qd = reinterpret_cast<float *>(q + (K / 256) * ACT_GSTRIDE);
     int16_t *qb = reinterpret_cast<int16_t *>(q + act_bs_off(K));
-    // one wave per 256-element chunk, 4 consecutive elements per lane
-    for (uint32_t c = wave_id(); c < K / 256; c += nw) {
-        const uint32_t e = c * 256 + lane * 4;
-        float v[4], t[4];
-        pro_raw4(a, xr, erow, e, v);
-        if (write_x) st_coh4(a.x_out + e, make_float4(v[0], v[1], v[2], v[3]));
-        if (a.pro == SINTER_PRO_PLAIN) {
+    for (uint32_t j0 = 0; j0 < mine; j0 += PRO_PF) {
+        if (!one_round) load_round(j0, true);
 #pragma unroll
-            for (int i = 0; i < 4; i++) t[i] = v[i];
-        } else if (a.pro == SINTER_PRO_GATED) {
-            // per-head sum over gd/4 lanes (heads never straddle a chunk)
-            double s = 0.0;
+        for (uint32_t j = 0; j < PRO_PF; j++) {
+            if (j0 + j < mine) {
+                const uint32_t c = w + nw * (j0 + j), e = c * 256 + lane * 4;
+                const float *v = xv[j], *y = yv[j];
+                float t[4];
+                if (write_x) st_coh4(a.x_out + e, make_float4(v[0], v[1], v[2], v[3]));
+                if (a.pro == SINTER_PRO_PLAIN) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) s += (double)(v[i] * v[i]);
-            for (uint32_t o = 1; o < gd / 4; o <<= 1) s += __shfl_xor(s, (int)o, 64);
-            const float mean = (float)(s / (double)gd);
-            const float hs = 1.0f / sqrtf(mean + a.eps);
-            const float4 z = ld_coh16(zr, e * 4);
-            const float zz[4] = {z.x, z.y, z.z, z.w};
+                    for (int i = 0; i < 4; i++) t[i] = v[i];
+                } else if (gated) {
+                    // per-head sum over gd/4 lanes (heads never straddle a chunk)
+                    double hsum = 0.0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float nrm = v[i] * hs;
-                const float wn = nrm * a.norm_w[(e + i) & (gd - 1)];
-                t[i] = wn * dev_silu(zz[i]);
-            }
-        } else {
-            const float4 w = *reinterpret_cast<const float4 *>(a.norm_w + e);
-            const float ww[4] = {w.x, w.y, w.z, w.w};
+                    for (int i = 0; i < 4; i++) hsum += (double)(v[i] * v[i]);
+                    for (uint32_t o = 1; o < gd / 4; o <<= 1) hsum += __shfl_xor(hsum, (int)o, 64);
+                    const float mean = (float)(hsum / (double)gd);
+                    const float hs = 1.0f / sqrtf(mean + a.eps);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float nrm = v[i] * gscale;
-                t[i] = nrm * ww[i];
-            }
-        }
-        if (vt == SINTER_Q8_K) {
-            // ggml quantize_row_q8_K_ref: signed element of largest |x|, first index wins
-            float bmax = 0.0f, bamax = 0.0f;
-            int bidx = 0x7fffffff;
+                    for (int i = 0; i < 4; i++) {
+                        const float nrm = v[i] * hs;
+                        const float wn = nrm * gw[i];
+                        t[i] = wn * dev_silu(y[i]);
+                    }
+                } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float ax = fabsf(t[i]);
-                if (ax > bamax) { bamax = ax; bmax = t[i]; bidx = lane * 4 + i; }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float oa = __shfl_xor(bamax, o, 64);
-                const float om = __shfl_xor(bmax, o, 64);
-                const int oi = __shfl_xor(bidx, o, 64);
-                if (oa > bamax || (oa == bamax && oi < bidx)) { bamax = oa; bmax = om; bidx = oi; }
-            }
-            int qv[4] = {0, 0, 0, 0};
-            float dd = 0.0f;
-            if (bamax != 0.0f) {
-                const float iscale = -127.f / bmax;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int r = (int)__builtin_rintf(iscale * t[i]);
-                    qv[i] = r < 127 ? r : 127;
+                    for (int i = 0; i < 4; i++) {
+                        const float nrm = v[i] * gscale;
+                        t[i] = nrm * y[i];
+                    }
                 }
-                dd = 1.0f / iscale;
+                quant_chunk(vt, c, e, t, q, qd, qb);
+                sched_fence();
             }
-            const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
-                                    ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-            *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
-            int bsum = qv[0] + qv[1] + qv[2] + qv[3];
-            bsum += __shfl_xor(bsum, 1, 64);
-            bsum += __shfl_xor(bsum, 2, 64);
-            if ((lane & 3) == 0) qb[e / 16] = (int16_t)bsum;
-            if (lane == 0) qd[c] = dd;
-        } else if (vt == SINTER_Q8_0) {
-            // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax)
-            float am = fmaxf(fmaxf(fabsf(t[0]), fabsf(t[1])), fmaxf(fabsf(t[2]), fabsf(t[3])));
-            am = fmaxf(am, __shfl_xor(am, 1, 64));
-            am = fmaxf(am, __shfl_xor(am, 2, 64));
-            am = fmaxf(am, __shfl_xor(am, 4, 64));
-            const float d = am / 127.f;
-            const float id = (am != 0.0f) ? 127.f / am : 0.0f;
-            int qv[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
-            const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
-                                    ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-            *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
-            if ((lane & 7) == 0) qd[e / 32] = h2f(f2h(d));
-        } else if (vt == SINTER_BF16) {
-            uint16_t *bf = reinterpret_cast<uint16_t *>(q + (e >> 6) * ACT_BF_CSTRIDE) + (e & 63);
-#pragma unroll
-            for (int i = 0; i < 4; i++) bf[i] = f2bf(t[i]);
-        } else {
-            float *f = reinterpret_cast<float *>(q + (e >> 6) * ACT_F_CSTRIDE) + (e & 63);
-#pragma unroll
-            for (int i = 0; i < 4; i++) f[i] = t[i];
         }
     }
     __syncthreads();
@@ -297,7 +345,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
 __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
 __device__ __forceinline__ uint16_t ld_u16(const lds_char *p) { return *reinterpret_cast<const LDS uint16_t *>(p); }
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // The N+1 aligned dwords covering N words at a 2-aligned LDS address, and
 // the byte shift that extracts them (unaligned LDS reads stall the LDS
@@ -803,7 +850,7 @@ __device__ __forceinline__ bool gemv_args_ok(const sinter_gemv_args &a) {
 
 // Apply the epilogues to the buffered rows [row0, row0 + n) and store them;
 // greedy-argmax candidates fold into (bv, bi).  All threads.
-__device__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
+__device__ __forceinline__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
     for (uint32_t i = threadIdx.x; i < n; i += BLOCK_THREADS) {
         const uint32_t grow = row0 + i;
         uint32_t s = 0, base = 0;
@@ -864,7 +911,21 @@ __device__ __forceinline__ bool ring_geometry(const sinter_gemv_args &a, uint32_
     return true;
 }
 
-__device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
+// What gemv_begin leaves for gemv_run (wave-uniform registers): the op can
+// be begun before the grid barrier that precedes it -- its weights do not
+// depend on the barrier -- so the first two tiles stream in while the
+// workgroup waits.
+struct GemvState {
+    uint32_t ok, row_lo, ipr, n_seg;
+    Ring rg;
+    Cursor cur;
+    TD X, Y;
+};
+
+// Copy the payload to LDS, split the rows, build the segment table, clear the
+// term ring and LDS-DMA the first two tiles.  Uses LDS (the GEMV buffers)
+// only, so it may run as soon as the previous op of the pass has returned.
+__device__ __forceinline__ void gemv_begin(const sinter_instr &ins, unsigned *err, GemvState &st) {
     if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
         reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
     __syncthreads();
@@ -872,17 +933,18 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
     const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
     const uint32_t K = a.K;
     const uint32_t ipr = uni(K / item_elems(a.seg[0].type));
-    Ring rg;
-    if (!gemv_args_ok(a) || !ring_geometry(a, ipr, rg)) {
+    st.ok = 0;
+    if (!gemv_args_ok(a) || !ring_geometry(a, ipr, st.rg)) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
         return;
     }
-    const int vt = vec_dot_type(a.seg[0].type);
+    st.ok = 1;
+    st.ipr = ipr;
     const uint32_t n_seg = uni(a.n_seg);
+    st.n_seg = n_seg;
 
     // byte-balanced row range [row_lo, row_hi) of this workgroup (global rows
     // of the concatenated segments), then its share of each segment
-    uint32_t row_lo;
     {
         uint32_t rb_eff[SINTER_GEMV_MAX_SEG];
         uint64_t total = 0;
@@ -892,7 +954,8 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
             rb_eff[s] = s < a.n_seg ? (uint32_t)sinter_row_bytes_dev(a.seg[s].type, K) * (sw ? 2u : 1u) : 0u;
             total += s < a.n_seg ? (uint64_t)a.seg[s].rows * rb_eff[s] : 0ull;
         }
-        row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
+        const uint32_t row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
+        st.row_lo = row_lo;
         const uint32_t row_hi = uni(row_cut(a, rb_eff, total, rel + 1, nblk));
         const uint32_t s = threadIdx.x;
         if (s < n_seg) {
@@ -922,6 +985,22 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
         for (uint32_t i = threadIdx.x; i < CB_CAP; i += BLOCK_THREADS) g_cb[i] = -0.0;
         __syncthreads();
     }
+    cur_seg(st.cur, 0, n_seg, ipr);
+    st.X = tile_next(st.cur, g_tiles, n_seg, ipr);
+    st.Y = tile_next(st.cur, g_tiles + TILE_BYTES, n_seg, ipr);
+}
+
+// The rest of the op: prologue, tile pipeline, epilogues.
+__device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err, GemvState &st) {
+    if (!st.ok) return;
+    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
+    const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
+    const uint32_t K = a.K;
+    const int vt = vec_dot_type(a.seg[0].type);
+    const uint32_t ipr = st.ipr, n_seg = st.n_seg, row_lo = st.row_lo;
+    const Ring rg = st.rg;
+    Cursor cur = st.cur;
+    TD X = st.X, Y = st.Y;
 
     // The tile pipeline: X = tile being computed (buffer bx), Y = next (in
     // flight), the tile after Y is created and issued this iteration into the
@@ -929,11 +1008,6 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
     // makes X's DMA and the previous terms visible to every wave and frees
     // P's buffer; a deferred ring folds P's rows in the same step, otherwise
     // X's rows are folded after a second barrier.
-    Cursor cur;
-    cur_seg(cur, 0, n_seg, ipr);
-    TD X = tile_next(cur, g_tiles, n_seg, ipr);
-    TD Y = tile_next(cur, g_tiles + TILE_BYTES, n_seg, ipr);
-
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
     gemv_prologue(a, vt, write_x, g_qbuf, g_red, err);   // ends with __syncthreads()
     settle_vmem();
@@ -1038,6 +1112,12 @@ __device__ void op_gemv(const sinter_instr &ins, unsigned *err) {
         }
     }
     __syncthreads();
+}
+
+__device__ __forceinline__ void op_gemv(const sinter_instr &ins, unsigned *err) {
+    GemvState st;
+    gemv_begin(ins, err, st);
+    gemv_run(ins, err, st);
 }
 
 }  // namespace sinter

@@ -46,20 +46,26 @@ __device__ __forceinline__ void dispatch(const sinter_instr &ins, unsigned *err)
 // serialise at the memory side).  No cache writeback or invalidate: every
 // wave first waits for its own memory operations, and all data that crosses
 // workgroups moves through device-coherent loads and stores (dev_common.h).
-// Returns false on timeout.
-__device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned *groups, unsigned &epoch,
-                                             uint64_t spin_limit_ticks, unsigned *err) {
+// Split in two so that work that does not depend on the barrier (the next
+// GEMV's first weight tiles) can be issued between arriving and waiting.
+__device__ __forceinline__ void grid_arrive(unsigned *bar, unsigned *groups, unsigned &epoch) {
     settle_vmem();
     __syncthreads();
     epoch += 1;
-    __shared__ unsigned timed_out;
     if (threadIdx.x == 0) {
-        timed_out = 0;
-        const unsigned g = blockIdx.x >> 4, ng = (gridDim.x + 15u) >> 4;
+        const unsigned g = blockIdx.x >> 4;
         const unsigned gsize = min(16u, gridDim.x - g * 16u);
         const unsigned old = __hip_atomic_fetch_add(groups + g * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned target = epoch * ng;
+    }
+}
+
+// Returns false on timeout.
+__device__ __forceinline__ bool grid_wait(unsigned *bar, unsigned epoch, uint64_t spin_limit_ticks, unsigned *err) {
+    __shared__ unsigned timed_out;
+    if (threadIdx.x == 0) {
+        timed_out = 0;
+        const unsigned target = epoch * ((gridDim.x + 15u) >> 4);
         const uint64_t t0 = wall_clock64();
         while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
             __builtin_amdgcn_s_sleep(1);
@@ -74,6 +80,17 @@ __device__ __forceinline__ bool grid_barrier(unsigned *bar, unsigned *groups, un
     return timed_out == 0;
 }
 
+// Between arriving at a barrier and waiting on it: if instruction nx is a
+// GEMV this workgroup runs, begin it (its first tiles start streaming).
+__device__ __forceinline__ void prefetch_next(const sinter_instr *prog, uint32_t nx, unsigned *err, GemvState &pf,
+                                              uint32_t &pf_i) {
+    const sinter_instr &ins = prog[nx];
+    if (ins.kind == SINTER_OP_GEMV && blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
+        gemv_begin(ins, err, pf);
+        pf_i = nx;
+    }
+}
+
 }  // namespace sinter
 
 using namespace sinter;
@@ -81,6 +98,8 @@ using namespace sinter;
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
 sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     unsigned epoch = 0;
+    GemvState pf;                 // a GEMV begun before the barrier that precedes it
+    uint32_t pf_i = 0xffffffffu;  // its instruction index
     for (uint32_t pass = 0; pass < ctl.n_passes; ++pass) {
         const uint64_t t0 = wall_clock64();
         for (uint32_t i = 0; i < ctl.n_instr; ++i) {
@@ -88,7 +107,9 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             const unsigned kind = ins.kind;
             if (kind == SINTER_OP_BOUNDARY) {
                 const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
-                if (!grid_barrier(ctl.bar, ctl.groups, epoch, ctl.spin_limit, ctl.err)) return;
+                grid_arrive(ctl.bar, ctl.groups, epoch);
+                if (i + 1 < ctl.n_instr) prefetch_next(prog, i + 1, ctl.err, pf, pf_i);
+                if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
                 if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
                     ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(wall_clock64() - s);
                 continue;
@@ -96,26 +117,32 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
                 if (blockIdx.x == 0 && threadIdx.x == 0)
                     raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
+                settle_vmem();
                 return;
             }
             if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
-                if (ctl.op_cycles && blockIdx.x == 0) {
-                    const uint64_t s = wall_clock64();
-                    dispatch(ins, ctl.err);
-                    if (threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
+                const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
+                if (kind == SINTER_OP_GEMV && pf_i == i) {
+                    pf_i = 0xffffffffu;
+                    gemv_run(ins, ctl.err, pf);
                 } else {
                     dispatch(ins, ctl.err);
                 }
+                if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
+                    ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
             }
         }
-        // pass epilogue: everyone finished, then a uniform error sample
-        if (!grid_barrier(ctl.bar, ctl.groups, epoch, ctl.spin_limit, ctl.err)) return;
+        // pass epilogue: everyone finished, then a uniform error sample; the
+        // next pass's first GEMV is begun while waiting
+        grid_arrive(ctl.bar, ctl.groups, epoch);
+        if (pass + 1 < ctl.n_passes) prefetch_next(prog, 0, ctl.err, pf, pf_i);
+        if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
         __shared__ unsigned e;
         if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (blockIdx.x == 0 && threadIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
             ctl.pass_cycles[(ctl.pass_base + pass) % ctl.pass_cycles_cap] = (long long)(wall_clock64() - t0);
-        if (e) return;
+        if (e) { settle_vmem(); return; }
     }
 }
 
