@@ -60,14 +60,63 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
     return v;
 }
 
-// Block-wide fp64 sum (blockDim.x a multiple of 64, <= 1024); every thread
-// gets the total.  `red` is LDS scratch of >= 16 doubles.  The result is
-// order-dependent only at fp64 rounding level (callers round to fp32).
+// ---------------------------------------------------------------- DPP rows
+// In-VALU lane exchanges within a 16-lane row (no LDS round trip).  Every
+// lane of the row must be active.  After the four steps of row16_* every lane
+// of the row holds the same value: each step combines a lane with its
+// partner in a commutative operation, so partners compute identical results.
+enum : int {
+    DPP_XOR1 = 0xB1,         // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,         // quad_perm [2,3,0,1]
+    DPP_HALF_MIRROR = 0x141, // lane i <- lane 7-i within each half-row
+    DPP_MIRROR = 0x140,      // lane i <- lane 15-i within the row
+};
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)u), hi = (uint32_t)dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    return fmaxf(v, dpp_f<DPP_MIRROR>(v));
+}
+__device__ __forceinline__ int row16_min(int v) {
+    v = min(v, dpp_i<DPP_XOR1>(v));
+    v = min(v, dpp_i<DPP_XOR2>(v));
+    v = min(v, dpp_i<DPP_HALF_MIRROR>(v));
+    return min(v, dpp_i<DPP_MIRROR>(v));
+}
+__device__ __forceinline__ double row16_sum_f64(double v) {
+    v += dpp_d<DPP_XOR1>(v);
+    v += dpp_d<DPP_XOR2>(v);
+    v += dpp_d<DPP_HALF_MIRROR>(v);
+    return v + dpp_d<DPP_MIRROR>(v);
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t u = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Block-wide fp64 sum (blockDim.x a multiple of 64, <= 1024, every thread
+// active); every thread gets the same total.  `red` is LDS scratch of >= 16
+// doubles.  Rows are reduced with DPP, the four row sums of a wave and then
+// the wave sums are added in a fixed order; the result is order-dependent
+// only at fp64 rounding level (callers round to fp32).
 __device__ __forceinline__ double block_sum_f64(double v, double *red) {
-    v = wave_sum_f64(v);
+    v = row16_sum_f64(v);
+    const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
     const int nw = blockDim.x >> 6;
     __syncthreads();
-    if (lane_id() == 0) red[wave_id()] = v;
+    if (lane_id() == 0) red[wave_id()] = w;
     __syncthreads();
     double t = 0.0;
     for (int i = 0; i < nw; i++) t += red[i];

@@ -126,82 +126,98 @@ __device__ __forceinline__ void dequant4(const void *row, int type, uint32_t e, 
 
 // ------------------------------------------------------------ prologue
 
-// Quantise one 256-element chunk c (values t[4] per lane, 4 consecutive
-// elements each) into the activation layout at q.
-__device__ __forceinline__ void quant_chunk(int vt, uint32_t c, uint32_t e, const float t[4], char *q, float *qd,
-                                            int16_t *qb) {
-    const int lane = lane_id();
+// The prologue gives each 256-element chunk to one 16-lane DPP row, 16
+// consecutive elements per lane: a per-chunk reduction is four in-VALU DPP
+// steps and a Q8_K bsum (16 elements) is one lane's own sum.
+constexpr uint32_t PRO_ROWS = BLOCK_THREADS / 16;
+// chunks per row per round (all loads of a round are issued before any of
+// them is used): one round up to K = 16 * 5 * 256 = 20480
+constexpr uint32_t PRO_RC = 5;
+
+__device__ __forceinline__ void lds_st16(lds_char *p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    u32x4_t v = {a, b, c, d};
+    *reinterpret_cast<LDS u32x4_t *>(p) = v;
+}
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+}
+
+// Quantise this lane's 16 elements [e0, e0+16) of chunk c (every lane of the
+// row calls this with the same c) into the activation layout at q.
+__device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t e0, const float t[16], lds_char *q,
+                                        LDS float *qd, LDS int16_t *qb) {
+    int qv[16];
     if (vt == SINTER_Q8_K) {
-        // ggml quantize_row_q8_K_ref: signed element of largest |x|, first index wins
-        float bmax = 0.0f, bamax = 0.0f;
-        int bidx = 0x7fffffff;
+        // ggml quantize_row_q8_K_ref: the signed element of largest |x|,
+        // first index wins; q = min(127, rne(x * -127/max)), d = 1/iscale
+        float am = 0.0f, sv = 0.0f;
+        int fi = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 16; i++) {
             const float ax = fabsf(t[i]);
-            if (ax > bamax) { bamax = ax; bmax = t[i]; bidx = lane * 4 + i; }
+            if (ax > am) { am = ax; sv = t[i]; fi = i; }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float oa = __shfl_xor(bamax, o, 64);
-            const float om = __shfl_xor(bmax, o, 64);
-            const int oi = __shfl_xor(bidx, o, 64);
-            if (oa > bamax || (oa == bamax && oi < bidx)) { bamax = oa; bmax = om; bidx = oi; }
-        }
-        int qv[4] = {0, 0, 0, 0};
+        const float A = row16_max(am);
+        // (index, sign) of the first element reaching the row maximum
+        const int key = row16_min(am == A ? (int)(((r * 16 + fi) << 1) | (sv < 0.0f ? 1u : 0u)) : 0x7fffffff);
         float dd = 0.0f;
-        if (bamax != 0.0f) {
+        if (A != 0.0f) {
+            const float bmax = (key & 1) ? -A : A;
             const float iscale = -127.f / bmax;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = (int)__builtin_rintf(iscale * t[i]);
-                qv[i] = r < 127 ? r : 127;
+            for (int i = 0; i < 16; i++) {
+                const int v = (int)__builtin_rintf(iscale * t[i]);
+                qv[i] = v < 127 ? v : 127;
             }
             dd = 1.0f / iscale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) qv[i] = 0;
         }
-        const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
-                                ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-        *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
-        int bsum = qv[0] + qv[1] + qv[2] + qv[3];
-        bsum += __shfl_xor(bsum, 1, 64);
-        bsum += __shfl_xor(bsum, 2, 64);
-        if ((lane & 3) == 0) qb[e / 16] = (int16_t)bsum;
-        if (lane == 0) qd[c] = dd;
+        int bsum = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) bsum += qv[i];
+        lds_st16(q + c * ACT_GSTRIDE + r * 16, pack4_i8(qv[0], qv[1], qv[2], qv[3]), pack4_i8(qv[4], qv[5], qv[6], qv[7]),
+                 pack4_i8(qv[8], qv[9], qv[10], qv[11]), pack4_i8(qv[12], qv[13], qv[14], qv[15]));
+        qb[e0 / 16] = (int16_t)bsum;
+        if (r == 0) qd[c] = dd;
     } else if (vt == SINTER_Q8_0) {
-        // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax)
-        float am = fmaxf(fmaxf(fabsf(t[0]), fabsf(t[1])), fmaxf(fabsf(t[2]), fabsf(t[3])));
-        am = fmaxf(am, __shfl_xor(am, 1, 64));
-        am = fmaxf(am, __shfl_xor(am, 2, 64));
-        am = fmaxf(am, __shfl_xor(am, 4, 64));
+        // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax);
+        // a 32-element block is two lanes
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) am = fmaxf(am, fabsf(t[i]));
+        am = fmaxf(am, dpp_f<DPP_XOR1>(am));
         const float d = am / 127.f;
         const float id = (am != 0.0f) ? 127.f / am : 0.0f;
-        int qv[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
-        const uint32_t packed = (uint32_t)(qv[0] & 0xff) | ((uint32_t)(qv[1] & 0xff) << 8) |
-                                ((uint32_t)(qv[2] & 0xff) << 16) | ((uint32_t)(qv[3] & 0xff) << 24);
-        *reinterpret_cast<uint32_t *>(q + act_qoff(e)) = packed;
-        if ((lane & 7) == 0) qd[e / 32] = h2f(f2h(d));
+        for (int i = 0; i < 16; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
+        lds_st16(q + c * ACT_GSTRIDE + r * 16, pack4_i8(qv[0], qv[1], qv[2], qv[3]), pack4_i8(qv[4], qv[5], qv[6], qv[7]),
+                 pack4_i8(qv[8], qv[9], qv[10], qv[11]), pack4_i8(qv[12], qv[13], qv[14], qv[15]));
+        if ((r & 1) == 0) qd[e0 / 32] = h2f(f2h(d));
     } else if (vt == SINTER_BF16) {
-        uint16_t *bf = reinterpret_cast<uint16_t *>(q + (e >> 6) * ACT_BF_CSTRIDE) + (e & 63);
+        uint32_t h[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) bf[i] = f2bf(t[i]);
+        for (int i = 0; i < 8; i++) h[i] = (uint32_t)f2bf(t[2 * i]) | ((uint32_t)f2bf(t[2 * i + 1]) << 16);
+        lds_char *p = q + (e0 >> 6) * ACT_BF_CSTRIDE + (e0 & 63) * 2;
+        lds_st16(p, h[0], h[1], h[2], h[3]);
+        lds_st16(p + 16, h[4], h[5], h[6], h[7]);
     } else {
-        float *f = reinterpret_cast<float *>(q + (e >> 6) * ACT_F_CSTRIDE) + (e & 63);
+        lds_char *p = q + (e0 >> 6) * ACT_F_CSTRIDE + (e0 & 63) * 4;
 #pragma unroll
-        for (int i = 0; i < 4; i++) f[i] = t[i];
+        for (int k = 0; k < 4; k++)
+            lds_st16(p + 16 * k, __float_as_uint(t[4 * k]), __float_as_uint(t[4 * k + 1]), __float_as_uint(t[4 * k + 2]),
+                     __float_as_uint(t[4 * k + 3]));
     }
 }
 
-// chunks per wave the prologue loads per round (all loads of a round are
-// issued before any of them is used)
-constexpr uint32_t PRO_PF = 8;
-
-// Build the quantised activation in LDS at `q`.  Every thread of the block
-// calls this.  `red` is 128 B of LDS scratch.  Wave w owns chunks w, w+4, ...
-// and reads them in rounds of PRO_PF chunks, so the prologue pays one memory
-// latency per round instead of one per chunk (a single round for K <= 8192;
-// an RMSNorm with more chunks makes one extra pass for its sum of squares).
-__device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, char *q, double *red,
+// Build the quantised activation in LDS (g_qbuf).  Every thread of the block
+// calls this.  `red` is 128 B of LDS scratch.  Row g of the block (16 lanes)
+// owns chunks g, g+16, ... and reads them in rounds of PRO_RC chunks, so the
+// prologue pays one memory latency per round (one round up to K = 20480; an
+// RMSNorm with more chunks makes one extra pass for its sum of squares).
+__device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
                                               unsigned *err) {
     const uint32_t K = a.K;
     const bool embed = a.pro == SINTER_PRO_EMBED, gated = a.pro == SINTER_PRO_GATED;
@@ -218,101 +234,141 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         erow = static_cast<const char *>(a.aux) + (size_t)tok * sinter_row_bytes_dev(a.aux_type, K);
     }
     const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
-    const uint32_t lane = lane_id(), w = wave_id(), nw = BLOCK_THREADS / 64, nchunk = K / 256;
-    const uint32_t mine = nchunk > w ? (nchunk - w + nw - 1) / nw : 0u;   // chunks of this wave
-    auto raw4 = [&](uint32_t e, float v[4]) {
+    // the lane's indices, opaque to the compiler so that the per-lane address
+    // arithmetic below is not hoisted out of the interpreter loop (where it
+    // would stay live, in registers, for the whole kernel)
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
+    const uint32_t mine = nchunk > g ? (nchunk - g + PRO_ROWS - 1) / PRO_ROWS : 0u;   // chunks of this row
+    auto raw16 = [&](uint32_t e0, float v[16]) {
         if (embed) {
-            dequant4(erow, a.aux_type, e, v);
+#pragma unroll
+            for (int k = 0; k < 4; k++) dequant4(erow, a.aux_type, e0 + 4 * k, v + 4 * k);
         } else {
-            const float4 t = ld_coh16(xr, e * 4);
-            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float4 t = ld_coh16(xr, (e0 + 4 * k) * 4);
+                v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+            }
         }
     };
     // the second per-element input: the gate z (gated) or the norm weights
-    auto raw4b = [&](uint32_t e, float y[4]) {
-        if (gated) {
-            const float4 z = ld_coh16(zr, e * 4);
-            y[0] = z.x; y[1] = z.y; y[2] = z.z; y[3] = z.w;
-        } else if (rms) {
-            const float4 nv = *reinterpret_cast<const float4 *>(a.norm_w + e);
-            y[0] = nv.x; y[1] = nv.y; y[2] = nv.z; y[3] = nv.w;
-        } else {
-            y[0] = y[1] = y[2] = y[3] = 0.0f;
+    auto raw16b = [&](uint32_t e0, float y[16]) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (gated) t = ld_coh16(zr, (e0 + 4 * k) * 4);
+            else if (rms) t = *reinterpret_cast<const float4 *>(a.norm_w + e0 + 4 * k);
+            y[4 * k] = t.x; y[4 * k + 1] = t.y; y[4 * k + 2] = t.z; y[4 * k + 3] = t.w;
         }
     };
-    float gw[4] = {0.f, 0.f, 0.f, 0.f};     // gated-norm weights: the same for every chunk
-    if (gated) {
-        const float4 t = *reinterpret_cast<const float4 *>(a.norm_w + ((lane * 4) & (gd - 1)));
-        gw[0] = t.x; gw[1] = t.y; gw[2] = t.z; gw[3] = t.w;
+    // gated-norm weights: element i of this lane is norm_w[(16r + i) % gd] in every chunk
+    float gw[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gated) t = *reinterpret_cast<const float4 *>(a.norm_w + ((r * 16 + 4 * k) & (gd - 1)));
+        gw[4 * k] = t.x; gw[4 * k + 1] = t.y; gw[4 * k + 2] = t.z; gw[4 * k + 3] = t.w;
     }
-    float xv[PRO_PF][4], yv[PRO_PF][4];
+    float xv[PRO_RC][16], yv[PRO_RC][16];
     auto load_round = [&](uint32_t j0, bool both) {
 #pragma unroll
-        for (uint32_t j = 0; j < PRO_PF; j++) {
+        for (uint32_t j = 0; j < PRO_RC; j++) {
             if (j0 + j < mine) {
-                const uint32_t e = (w + nw * (j0 + j)) * 256 + lane * 4;
-                raw4(e, xv[j]);
-                if (both) raw4b(e, yv[j]);
+                const uint32_t e0 = (g + PRO_ROWS * (j0 + j)) * 256 + r * 16;
+                raw16(e0, xv[j]);
+                if (both) raw16b(e0, yv[j]);
             }
         }
     };
     // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
     // scale = 1/sqrtf(mean + eps))
     float gscale = 1.0f;
-    const bool one_round = mine <= PRO_PF;
+    const bool one_round = nchunk <= PRO_ROWS * PRO_RC;
     if (one_round) load_round(0, true);
     if (rms) {
         double s = 0.0;
-        for (uint32_t j0 = 0; j0 < mine; j0 += PRO_PF) {
+        for (uint32_t j0 = 0; j0 < mine; j0 += PRO_RC) {
             if (!one_round) load_round(j0, false);
 #pragma unroll
-            for (uint32_t j = 0; j < PRO_PF; j++)
+            for (uint32_t j = 0; j < PRO_RC; j++)
                 if (j0 + j < mine)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) s += (double)(xv[j][i] * xv[j][i]);
+                    for (int i = 0; i < 16; i++) s += (double)(xv[j][i] * xv[j][i]);
         }
         s = block_sum_f64(s, red);
         const float mean = (float)(s / (double)K);
         gscale = 1.0f / sqrtf(mean + a.eps);
     }
-    float *qd = reinterpret_cast<float *>(q + (K / 256) * ACT_GSTRIDE);
-    int16_t *qb = reinterpret_cast<int16_t *>(q + act_bs_off(K));
-    for (uint32_t j0 = 0; j0 < mine; j0 += PRO_PF) {
+    lds_char *q = (lds_char *)g_qbuf;
+    LDS float *qd = reinterpret_cast<LDS float *>(q + (K / 256) * ACT_GSTRIDE);
+    LDS int16_t *qb = reinterpret_cast<LDS int16_t *>(q + act_bs_off(K));
+    const bool has_y = gated || rms;
+    for (uint32_t j0 = 0; j0 < mine; j0 += PRO_RC) {
         if (!one_round) load_round(j0, true);
+        const uint32_t cnt = min(PRO_RC, mine - j0);
+        // slot 0 is processed, then the slots shift down by one: the code of
+        // a chunk exists once (a loop body, fetched once per op) rather than
+        // once per slot -- straight-line code is fetched from L2 every time
+#pragma unroll 1
+        for (uint32_t j = 0; j < cnt; j++) {
+            if (j) {
 #pragma unroll
-        for (uint32_t j = 0; j < PRO_PF; j++) {
-            if (j0 + j < mine) {
-                const uint32_t c = w + nw * (j0 + j), e = c * 256 + lane * 4;
-                const float *v = xv[j], *y = yv[j];
-                float t[4];
-                if (write_x) st_coh4(a.x_out + e, make_float4(v[0], v[1], v[2], v[3]));
-                if (a.pro == SINTER_PRO_PLAIN) {
+                for (uint32_t k = 0; k + 1 < PRO_RC; k++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) t[i] = v[i];
-                } else if (gated) {
-                    // per-head sum over gd/4 lanes (heads never straddle a chunk)
-                    double hsum = 0.0;
+                    for (int i = 0; i < 16; i++) xv[k][i] = xv[k + 1][i];
+                if (has_y)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) hsum += (double)(v[i] * v[i]);
-                    for (uint32_t o = 1; o < gd / 4; o <<= 1) hsum += __shfl_xor(hsum, (int)o, 64);
+                    for (uint32_t k = 0; k + 1 < PRO_RC; k++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) yv[k][i] = yv[k + 1][i];
+            }
+            const uint32_t c = g + PRO_ROWS * (j0 + j), e0 = c * 256 + r * 16;
+            const float *v = xv[0], *y = yv[0];
+            float t[16];
+            if (write_x)
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    st_coh4(a.x_out + e0 + 4 * k, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
+            if (a.pro == SINTER_PRO_PLAIN) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) t[i] = v[i];
+            } else if (gated) {
+                // per-head sums of squares in double: heads of 4 or 8
+                // elements inside the lane, wider heads over gd/16 lanes
+                double s4[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    double h = 0.0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) h += (double)(v[4 * k + i] * v[4 * k + i]);
+                    s4[k] = h;
+                }
+                const double s8a = s4[0] + s4[1], s8b = s4[2] + s4[3];
+                double s16 = s8a + s8b;
+                if (gd >= 32) s16 += dpp_d<DPP_XOR1>(s16);
+                if (gd >= 64) s16 += dpp_d<DPP_XOR2>(s16);
+                if (gd >= 128) s16 += dpp_d<DPP_HALF_MIRROR>(s16);
+                if (gd >= 256) s16 += dpp_d<DPP_MIRROR>(s16);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const double hsum = gd == 4 ? s4[i / 4] : gd == 8 ? (i < 8 ? s8a : s8b) : s16;
                     const float mean = (float)(hsum / (double)gd);
                     const float hs = 1.0f / sqrtf(mean + a.eps);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float nrm = v[i] * hs;
-                        const float wn = nrm * gw[i];
-                        t[i] = wn * dev_silu(y[i]);
-                    }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float nrm = v[i] * gscale;
-                        t[i] = nrm * y[i];
-                    }
+                    const float nrm = v[i] * hs;
+                    const float wn = nrm * gw[i];
+                    t[i] = wn * dev_silu(y[i]);
+                    if ((i & 3) == 3) sched_fence();   // bounds the live fp64 temporaries
                 }
-                quant_chunk(vt, c, e, t, q, qd, qb);
-                sched_fence();
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float nrm = v[i] * gscale;
+                    t[i] = nrm * y[i];
+                }
             }
+            quant16(vt, c, r, e0, t, q, qd, qb);
         }
     }
     __syncthreads();
@@ -1009,7 +1065,7 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
     // P's buffer; a deferred ring folds P's rows in the same step, otherwise
     // X's rows are folded after a second barrier.
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
-    gemv_prologue(a, vt, write_x, g_qbuf, g_red, err);   // ends with __syncthreads()
+    gemv_prologue(a, vt, write_x, g_red, err);   // ends with __syncthreads()
     settle_vmem();
     const ActView x = act_view(g_qbuf, K, vt);
 

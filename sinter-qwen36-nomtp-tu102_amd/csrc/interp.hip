@@ -80,16 +80,6 @@ __device__ __forceinline__ bool grid_wait(unsigned *bar, unsigned epoch, uint64_
     return timed_out == 0;
 }
 
-// Between arriving at a barrier and waiting on it: if instruction nx is a
-// GEMV this workgroup runs, begin it (its first tiles start streaming).
-__device__ __forceinline__ void prefetch_next(const sinter_instr *prog, uint32_t nx, unsigned *err, GemvState &pf,
-                                              uint32_t &pf_i) {
-    const sinter_instr &ins = prog[nx];
-    if (ins.kind == SINTER_OP_GEMV && blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
-        gemv_begin(ins, err, pf);
-        pf_i = nx;
-    }
-}
 
 }  // namespace sinter
 
@@ -100,20 +90,39 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     unsigned epoch = 0;
     GemvState pf;                 // a GEMV begun before the barrier that precedes it
     uint32_t pf_i = 0xffffffffu;  // its instruction index
+    const uint32_t n = ctl.n_instr;
+    // one copy of each op's code in the kernel: the pass end is handled as a
+    // barrier at index n, and every GEMV runs through gemv_begin + gemv_run
     for (uint32_t pass = 0; pass < ctl.n_passes; ++pass) {
         const uint64_t t0 = wall_clock64();
-        for (uint32_t i = 0; i < ctl.n_instr; ++i) {
-            const sinter_instr &ins = prog[i];
-            const unsigned kind = ins.kind;
+        for (uint32_t i = 0; i <= n; ++i) {
+            const unsigned kind = i < n ? prog[i].kind : (unsigned)SINTER_OP_BOUNDARY;
             if (kind == SINTER_OP_BOUNDARY) {
                 const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
                 grid_arrive(ctl.bar, ctl.groups, epoch);
-                if (i + 1 < ctl.n_instr) prefetch_next(prog, i + 1, ctl.err, pf, pf_i);
+                // begin the next GEMV (the next pass's first one at the pass end)
+                const uint32_t nx = i + 1 < n ? i + 1 : (i == n && pass + 1 < ctl.n_passes ? 0u : 0xffffffffu);
+                if (nx != 0xffffffffu) {
+                    const sinter_instr &ni = prog[nx];
+                    if (ni.kind == SINTER_OP_GEMV && blockIdx.x >= ni.block_lo && blockIdx.x < ni.block_hi) {
+                        gemv_begin(ni, ctl.err, pf);
+                        pf_i = nx;
+                    }
+                }
                 if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
                 if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
                     ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(wall_clock64() - s);
+                if (i < n) continue;
+                // pass end: a uniform error sample after everyone finished
+                __shared__ unsigned e;
+                if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __syncthreads();
+                if (blockIdx.x == 0 && threadIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
+                    ctl.pass_cycles[(ctl.pass_base + pass) % ctl.pass_cycles_cap] = (long long)(wall_clock64() - t0);
+                if (e) { settle_vmem(); return; }
                 continue;
             }
+            const sinter_instr &ins = prog[i];
             if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
                 if (blockIdx.x == 0 && threadIdx.x == 0)
                     raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
@@ -122,27 +131,19 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             }
             if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
                 const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
-                if (kind == SINTER_OP_GEMV && pf_i == i) {
+                if (kind == SINTER_OP_GEMV) {
+                    if (pf_i != i) gemv_begin(ins, ctl.err, pf);
                     pf_i = 0xffffffffu;
                     gemv_run(ins, ctl.err, pf);
-                } else {
-                    dispatch(ins, ctl.err);
+                } else if (kind == SINTER_OP_GDN_STEP) {
+                    op_gdn_step(ins, ctl.err);
+                } else if (kind == SINTER_OP_ATTN_DECODE) {
+                    op_attn_decode(ins, ctl.err);
                 }
                 if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
                     ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
             }
         }
-        // pass epilogue: everyone finished, then a uniform error sample; the
-        // next pass's first GEMV is begun while waiting
-        grid_arrive(ctl.bar, ctl.groups, epoch);
-        if (pass + 1 < ctl.n_passes) prefetch_next(prog, 0, ctl.err, pf, pf_i);
-        if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
-        __shared__ unsigned e;
-        if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (blockIdx.x == 0 && threadIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
-            ctl.pass_cycles[(ctl.pass_base + pass) % ctl.pass_cycles_cap] = (long long)(wall_clock64() - t0);
-        if (e) { settle_vmem(); return; }
     }
 }
 
