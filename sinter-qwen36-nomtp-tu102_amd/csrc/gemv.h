@@ -419,22 +419,6 @@ __device__ __forceinline__ void span_words(const uint32_t d[N + 1], uint32_t sh,
     for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
 }
 
-__device__ __forceinline__ uint32_t item_elems(int t) { return (t == SINTER_BF16 || t == SINTER_F32) ? 64u : 256u; }
-__device__ __forceinline__ uint32_t item_bytes(int t) {
-    switch (t) {
-    case SINTER_Q4_K: return 144;
-    case SINTER_Q6_K: return 210;
-    case SINTER_Q8_0: return 272;
-    case SINTER_BF16: return 128;
-    default: return 256;
-    }
-}
-// items of one matrix per tile: every lane busy, at most TILE_BYTES - 16
-__device__ __forceinline__ uint32_t items_per_tile(int t, bool swiglu) {
-    const uint32_t n = (t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u;
-    return swiglu ? n / 2 : n;
-}
-
 // Q4_K block (16-aligned in LDS) against Q8_K group g
 __device__ __forceinline__ double term_q4k(const lds_char *blk, const ActView &x, uint32_t g) {
     u32x4 wv[9], xv[16], bsv[2];
@@ -613,49 +597,13 @@ __device__ __forceinline__ double term_f32(const lds_char *blk, const ActView &x
 }
 
 // ------------------------------------------------------------ work split
-
-// Row cut for workgroup w of n: the global row nearest to byte w*T/n of the
-// concatenated (byte-weighted) row space.
-__device__ __forceinline__ uint32_t row_cut(const sinter_gemv_args &a, const uint32_t *rb_eff,
-                                            uint64_t total, uint32_t w, uint32_t n) {
-    if (w >= n) {
-        uint32_t r = 0;
-        for (int s = 0; s < a.n_seg; s++) r += a.seg[s].rows;
-        return r;
-    }
-    const uint64_t target = total * w / n;
-    uint64_t acc = 0;
-    uint32_t rows = 0;
-#pragma unroll
-    for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
-        if (s < a.n_seg) {
-            const uint64_t sb = (uint64_t)a.seg[s].rows * rb_eff[s];
-            if (target < acc + sb) return rows + (uint32_t)((target - acc + rb_eff[s] / 2) / rb_eff[s]);
-            acc += sb;
-            rows += a.seg[s].rows;
-        }
-    }
-    return rows;
-}
+// The host compiles each GEMV into a GemvPlan (isa.h): per-segment constants,
+// the term ring geometry and the workgroups' row cuts.  The kernel reads it
+// through the constant address space, so every field is a scalar load.
+typedef const __attribute__((address_space(4))) GemvPlan cplan_t;
+typedef const __attribute__((address_space(4))) uint32_t cu32_t;
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// This workgroup's share of each segment, computed once per op (LDS):
-enum : int {
-    GS_ROW_LO = 0,   // segment-local rows [row_lo, row_hi) of this workgroup
-    GS_ROW_HI,
-    GS_LR_BASE,      // workgroup-local index of segment-local row 0
-    GS_TYPE,
-    GS_SWIGLU,
-    GS_IB,           // item bytes
-    GS_T,            // items of each matrix per tile
-    GS_QT,           // T / ipr
-    GS_RT,           // T % ipr
-    GS_W_LO, GS_W_HI, GS_W2_LO, GS_W2_HI,
-    GS_STRIDE = 16
-};
-__shared__ uint32_t g_gseg[SINTER_GEMV_MAX_SEG * GS_STRIDE];
-__device__ __forceinline__ uint32_t gs(uint32_t s, int f) { return uni(g_gseg[s * GS_STRIDE + f]); }
 
 // q = v / d, r = v % d from m = floor((2^32-1) / d): the estimate is q or
 // q-1, one correction step makes it exact (v < 2^31)
@@ -695,18 +643,23 @@ struct Cursor {
     uint32_t ok, seg, a, ra, ka;        // next tile to create
     uint32_t end, T, qT, rT, ib, type, swig, lrb;   // current segment
     uintptr_t wa, wb;                   // weights of the current segment
+    uint32_t n_seg, ipr, row_lo, row_hi;            // the op: this workgroup's global rows
+    cplan_t *pl;
 };
 
-__device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s, uint32_t n_seg, uint32_t ipr) {
+// Move the cursor to the first segment >= s with rows in [row_lo, row_hi).
+__device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s) {
     c.ok = 0;
-    for (; s < n_seg; s++) {
-        const uint32_t lo = gs(s, GS_ROW_LO), hi = gs(s, GS_ROW_HI);
+    for (; s < c.n_seg; s++) {
+        const uint32_t base = c.pl->seg[s].base, rows = c.pl->seg[s].rows;
+        const uint32_t lo = min(max(c.row_lo, base), base + rows) - base;
+        const uint32_t hi = min(max(c.row_hi, base), base + rows) - base;
         if (lo < hi) {
-            c.ok = 1; c.seg = s; c.a = lo * ipr; c.ra = lo; c.ka = 0;
-            c.end = hi * ipr; c.T = gs(s, GS_T); c.qT = gs(s, GS_QT); c.rT = gs(s, GS_RT);
-            c.ib = gs(s, GS_IB); c.type = gs(s, GS_TYPE); c.swig = gs(s, GS_SWIGLU); c.lrb = gs(s, GS_LR_BASE);
-            c.wa = ((uintptr_t)gs(s, GS_W_HI) << 32) | gs(s, GS_W_LO);
-            c.wb = ((uintptr_t)gs(s, GS_W2_HI) << 32) | gs(s, GS_W2_LO);
+            c.ok = 1; c.seg = s; c.a = lo * c.ipr; c.ra = lo; c.ka = 0;
+            c.end = hi * c.ipr; c.T = c.pl->seg[s].T; c.qT = c.pl->seg[s].qT; c.rT = c.pl->seg[s].rT;
+            c.ib = c.pl->seg[s].ib; c.type = c.pl->seg[s].type; c.swig = c.pl->seg[s].swig; c.lrb = base - c.row_lo;
+            c.wa = (uintptr_t)c.pl->seg[s].wa;
+            c.wb = (uintptr_t)c.pl->seg[s].wb;
             return;
         }
     }
@@ -717,12 +670,16 @@ __device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s, uint32_t n_seg, u
 // pending DMA as aliasing every later LDS read (it would insert vmcnt(0)
 // before them and serialise the pipeline); the tile loop below waits for it
 // explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends.
+// Weights are read once per pass, so the load is non-temporal (nt): streamed
+// through L2 without displacing the lines that are reused (the kernel's own
+// code, which every instruction-cache miss refetches from L2, and the
+// activations).
 __device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %2, %3\n\t"
+        "global_load_lds_dwordx4 %2, %3 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "s"(lds_base), "v"(voff), "s"(base)
@@ -735,7 +692,7 @@ __device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_
 // can be partial.  Matrix A fills the first chunks; a SwiGLU matrix B starts
 // at the next 1 KiB chunk boundary, so every chunk reads from one matrix;
 // lanes past a matrix's end re-read its last 16 bytes into the unused tail.
-__device__ __forceinline__ TD tile_next(Cursor &c, char *buf, uint32_t n_seg, uint32_t ipr) {
+__device__ __forceinline__ TD tile_next(Cursor &c, char *buf) {
     TD t;
     t.ok = c.ok;
     t.a = 0; t.cnt = 0; t.ra = 0; t.ka = 0; t.type = 0; t.swig = 0; t.lr0 = 0; t.skew_a = 0; t.base_b = 0;
@@ -772,11 +729,11 @@ __device__ __forceinline__ TD tile_next(Cursor &c, char *buf, uint32_t n_seg, ui
     // advance
     c.a += t.cnt;
     if (c.a >= c.end) {
-        cur_seg(c, c.seg + 1, n_seg, ipr);
+        cur_seg(c, c.seg + 1);
     } else {
         c.ra += c.qT;
         c.ka += c.rT;
-        if (c.ka >= ipr) { c.ka -= ipr; c.ra += 1; }
+        if (c.ka >= c.ipr) { c.ka -= c.ipr; c.ra += 1; }
     }
     return t;
 }
@@ -887,23 +844,6 @@ __device__ __forceinline__ void tile_fold(const TD &t, const Ring &rg, uint32_t 
 
 // ------------------------------------------------------------ the op
 
-// Payload checks every block evaluates identically (so an error leaves no
-// block behind at the next grid barrier).
-__device__ __forceinline__ bool gemv_args_ok(const sinter_gemv_args &a) {
-    if (a.n_seg < 1 || a.n_seg > SINTER_GEMV_MAX_SEG) return false;
-    if (a.K == 0 || (a.K & 255u) != 0 || a.K > (1u << 20)) return false;
-    const int vt = vec_dot_type(a.seg[0].type);
-    if (act_bytes(vt, a.K) > QBUF_BYTES) return false;
-    if (a.pro == SINTER_PRO_GATED && (a.gn_log2d < 2 || a.gn_log2d > 8)) return false;
-    for (int s = 0; s < a.n_seg; s++) {
-        const sinter_gemv_seg &g = a.seg[s];
-        if (vec_dot_type(g.type) != vt) return false;
-        if (sinter_row_bytes_dev(g.type, a.K) == 0) return false;
-        if (g.epi == SINTER_EPI_CONV && (g.dconv < 2 || g.dconv > 8)) return false;
-    }
-    return true;
-}
-
 // Apply the epilogues to the buffered rows [row0, row0 + n) and store them;
 // greedy-argmax candidates fold into (bv, bi).  All threads.
 __device__ __forceinline__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
@@ -945,105 +885,48 @@ __device__ __forceinline__ void gemv_flush(const sinter_gemv_args &a, uint32_t r
     }
 }
 
-// Ring geometry of an op (uniform); false if the shape cannot be folded.
-__device__ __forceinline__ bool ring_geometry(const sinter_gemv_args &a, uint32_t ipr, Ring &rg) {
-    bool any_swig = false;
-    uint32_t tmax = 0;
-    for (int s = 0; s < a.n_seg; s++) {
-        const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
-        any_swig |= sw;
-        tmax = max(tmax, items_per_tile(a.seg[s].type, sw));
-    }
-    rg.ipr = ipr;
-    rg.mipr = 0xFFFFFFFFu / ipr;
-    rg.P = ipr + (ipr & 1u);
-    const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP;
-    rg.R = cap / rg.P;
-    const uint32_t tpr = (tmax + ipr - 1) / ipr;   // rows one tile can touch, less one
-    rg.defer = rg.R >= 2 * tpr + 2 ? 1u : 0u;
-    if (rg.R < tpr + 1) return false;
-    rg.mR = 0xFFFFFFFFu / rg.R;
-    rg.RP = rg.R * rg.P;
-    return true;
-}
-
 // What gemv_begin leaves for gemv_run (wave-uniform registers): the op can
 // be begun before the grid barrier that precedes it -- its weights do not
 // depend on the barrier -- so the first two tiles stream in while the
 // workgroup waits.
 struct GemvState {
-    uint32_t ok, row_lo, ipr, n_seg;
+    uint32_t ok, row_lo;
     Ring rg;
     Cursor cur;
     TD X, Y;
 };
 
-// Copy the payload to LDS, split the rows, build the segment table, clear the
-// term ring and LDS-DMA the first two tiles.  Uses LDS (the GEMV buffers)
-// only, so it may run as soon as the previous op of the pass has returned.
-__device__ __forceinline__ void gemv_begin(const sinter_instr &ins, unsigned *err, GemvState &st) {
+// Copy the payload to LDS, read the plan, clear the term ring and LDS-DMA the
+// first two tiles.  Uses LDS (the GEMV buffers) only, so it may run as soon
+// as the previous op of the pass has returned.
+__device__ __forceinline__ void gemv_begin(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
+                                           unsigned *err, GemvState &st) {
     if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
         reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
-    __syncthreads();
-    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
-    const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
-    const uint32_t K = a.K;
-    const uint32_t ipr = uni(K / item_elems(a.seg[0].type));
-    st.ok = 0;
-    if (!gemv_args_ok(a) || !ring_geometry(a, ipr, st.rg)) {
+    // every ring slot starts as -0.0 (pad slots keep it)
+    for (uint32_t i = threadIdx.x; i < CB_CAP; i += BLOCK_THREADS) g_cb[i] = -0.0;
+    cplan_t *pl = (cplan_t *)plan;
+    cu32_t *cu = (cu32_t *)cuts;
+    const uint32_t rel = uni(blockIdx.x - ins.block_lo);
+    st.ok = pl->ok;
+    if (!st.ok) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
+        __syncthreads();
         return;
     }
-    st.ok = 1;
-    st.ipr = ipr;
-    const uint32_t n_seg = uni(a.n_seg);
-    st.n_seg = n_seg;
-
-    // byte-balanced row range [row_lo, row_hi) of this workgroup (global rows
-    // of the concatenated segments), then its share of each segment
-    {
-        uint32_t rb_eff[SINTER_GEMV_MAX_SEG];
-        uint64_t total = 0;
-#pragma unroll
-        for (int s = 0; s < SINTER_GEMV_MAX_SEG; s++) {
-            const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
-            rb_eff[s] = s < a.n_seg ? (uint32_t)sinter_row_bytes_dev(a.seg[s].type, K) * (sw ? 2u : 1u) : 0u;
-            total += s < a.n_seg ? (uint64_t)a.seg[s].rows * rb_eff[s] : 0ull;
-        }
-        const uint32_t row_lo = uni(row_cut(a, rb_eff, total, rel, nblk));
-        st.row_lo = row_lo;
-        const uint32_t row_hi = uni(row_cut(a, rb_eff, total, rel + 1, nblk));
-        const uint32_t s = threadIdx.x;
-        if (s < n_seg) {
-            uint32_t base = 0;
-            for (uint32_t j = 0; j < s; j++) base += a.seg[j].rows;
-            const sinter_gemv_seg &g = a.seg[s];
-            const uint32_t lo = min(max(row_lo, base), base + g.rows) - base;
-            const uint32_t hi = min(max(row_hi, base), base + g.rows) - base;
-            const bool sw = g.epi == SINTER_EPI_SWIGLU;
-            const uint32_t T = items_per_tile(g.type, sw);
-            uint32_t *e = g_gseg + s * GS_STRIDE;
-            e[GS_ROW_LO] = lo;
-            e[GS_ROW_HI] = hi;
-            e[GS_LR_BASE] = base - row_lo;   // workgroup-local index of segment row r is r + this
-            e[GS_TYPE] = (uint32_t)g.type;
-            e[GS_SWIGLU] = sw ? 1u : 0u;
-            e[GS_IB] = item_bytes(g.type);
-            e[GS_T] = T;
-            e[GS_QT] = T / ipr;
-            e[GS_RT] = T % ipr;
-            e[GS_W_LO] = (uint32_t)reinterpret_cast<uintptr_t>(g.w);
-            e[GS_W_HI] = (uint32_t)(reinterpret_cast<uintptr_t>(g.w) >> 32);
-            e[GS_W2_LO] = (uint32_t)reinterpret_cast<uintptr_t>(g.w2);
-            e[GS_W2_HI] = (uint32_t)(reinterpret_cast<uintptr_t>(g.w2) >> 32);
-        }
-        // every ring slot starts as -0.0 (pad slots keep it)
-        for (uint32_t i = threadIdx.x; i < CB_CAP; i += BLOCK_THREADS) g_cb[i] = -0.0;
-        __syncthreads();
-    }
-    cur_seg(st.cur, 0, n_seg, ipr);
-    st.X = tile_next(st.cur, g_tiles, n_seg, ipr);
-    st.Y = tile_next(st.cur, g_tiles + TILE_BYTES, n_seg, ipr);
+    st.rg.ipr = pl->ipr; st.rg.mipr = pl->mipr; st.rg.P = pl->P; st.rg.R = pl->R;
+    st.rg.mR = pl->mR; st.rg.RP = pl->RP; st.rg.defer = pl->defer;
+    Cursor &c = st.cur;
+    c.pl = pl;
+    c.n_seg = pl->n_seg;
+    c.ipr = pl->ipr;
+    c.row_lo = cu[rel];
+    c.row_hi = cu[rel + 1];
+    st.row_lo = c.row_lo;
+    cur_seg(c, 0);
+    st.X = tile_next(c, g_tiles);
+    st.Y = tile_next(c, g_tiles + TILE_BYTES);
+    __syncthreads();
 }
 
 // The rest of the op: prologue, tile pipeline, epilogues.
@@ -1052,8 +935,9 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
     const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
     const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
     const uint32_t K = a.K;
-    const int vt = vec_dot_type(a.seg[0].type);
-    const uint32_t ipr = st.ipr, n_seg = st.n_seg, row_lo = st.row_lo;
+    const int vt = (int)st.cur.pl->vt;
+    const bool any_argmax = st.cur.pl->any_argmax != 0;
+    const uint32_t row_lo = st.row_lo;
     const Ring rg = st.rg;
     Cursor cur = st.cur;
     TD X = st.X, Y = st.Y;
@@ -1080,7 +964,7 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();
         const uint32_t bz = bx == 0 ? 2u : bx - 1;
-        const TD Z = tile_next(cur, g_tiles + bz * TILE_BYTES, n_seg, ipr);
+        const TD Z = tile_next(cur, g_tiles + bz * TILE_BYTES);
         const TD &F = rg.defer ? P : X;       // the tile whose rows this step folds
         if (rg.defer && P.ok && td_done_after(P, rg) - res_row0 > RES_CAP) {
             gemv_flush(a, row_lo + res_row0, P.lr0 - res_row0, bv, bi);
@@ -1121,8 +1005,6 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
     gemv_flush(a, row_lo + res_row0, rows_total - res_row0, bv, bi);
 
     // greedy argmax: block-local best, then the last-arriving block reduces
-    bool any_argmax = false;
-    for (int s = 0; s < a.n_seg; s++) any_argmax |= a.seg[s].epi == SINTER_EPI_ARGMAX;
     if (any_argmax) {
         // block reduction of (value, index): larger value, then smaller index
 #pragma unroll
@@ -1170,9 +1052,10 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
     __syncthreads();
 }
 
-__device__ __forceinline__ void op_gemv(const sinter_instr &ins, unsigned *err) {
+__device__ __forceinline__ void op_gemv(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
+                                        unsigned *err) {
     GemvState st;
-    gemv_begin(ins, err, st);
+    gemv_begin(ins, plan, cuts, err, st);
     gemv_run(ins, err, st);
 }
 

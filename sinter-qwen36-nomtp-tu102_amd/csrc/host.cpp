@@ -12,6 +12,7 @@
 
 #include <chrono>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
@@ -49,9 +50,14 @@ bool hip_ok(hipError_t e, const char *what) {
 // as the interpreter does).  A slot is reused after OP_RING launches; the
 // copy into it is ordered on the caller's stream.
 constexpr unsigned OP_RING = 256;
+struct OpSlot {
+    sinter_instr ins;
+    GemvPlan plan;
+    uint32_t cuts[PLAN_CUTS];
+};
 struct OpDev {
     unsigned *err = nullptr;
-    sinter_instr *ring = nullptr;
+    OpSlot *ring = nullptr;
     unsigned next = 0;
 };
 
@@ -64,10 +70,10 @@ static OpDev *op_dev() {
     OpDev &d = devs[dev];
     if (!d.err) {
         char *p = nullptr;
-        if (!hip_ok(hipMalloc(&p, 256 + OP_RING * sizeof(sinter_instr)), "op state: hipMalloc")) return nullptr;
+        if (!hip_ok(hipMalloc(&p, 256 + OP_RING * sizeof(OpSlot)), "op state: hipMalloc")) return nullptr;
         if (!hip_ok(hipMemset(p, 0, 256), "op state: hipMemset")) return nullptr;
         d.err = reinterpret_cast<unsigned *>(p);
-        d.ring = reinterpret_cast<sinter_instr *>(p + 256);
+        d.ring = reinterpret_cast<OpSlot *>(p + 256);
     }
     return &d;
 }
@@ -77,7 +83,7 @@ unsigned *op_err_cell() {
     return d ? d->err : nullptr;
 }
 
-sinter_instr *op_instr_slot() {
+static OpSlot *op_slot() {
     OpDev *d = op_dev();
     if (!d) return nullptr;
     static std::mutex mu;
@@ -154,22 +160,95 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
     return SINTER_OK;
 }
 
+// Row cut of workgroup w of n: the global row nearest to byte w*total/n of
+// the concatenated, byte-weighted row space (a SwiGLU row weighs both
+// matrices).  Any monotone split is correct; this one balances bytes.
+static uint32_t row_cut(const sinter_gemv_args &a, uint64_t total, uint32_t w, uint32_t n) {
+    uint32_t rows = 0;
+    if (w >= n) {
+        for (int s = 0; s < a.n_seg; s++) rows += a.seg[s].rows;
+        return rows;
+    }
+    const uint64_t target = total * w / n;
+    uint64_t acc = 0;
+    for (int s = 0; s < a.n_seg; s++) {
+        const uint64_t rb = sinter_row_bytes_dev(a.seg[s].type, a.K) * (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
+        const uint64_t sb = (uint64_t)a.seg[s].rows * rb;
+        if (target < acc + sb) return rows + (uint32_t)((target - acc + rb / 2) / rb);
+        acc += sb;
+        rows += a.seg[s].rows;
+    }
+    return rows;
+}
+
+void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts) {
+    std::memset(&p, 0, sizeof p);
+    p.ok = 1;
+    p.n_seg = a.n_seg;
+    p.ipr = a.K / item_elems(a.seg[0].type);
+    p.vt = (uint32_t)vdot(a.seg[0].type);
+    bool any_swig = false;
+    uint32_t tmax = 0, base = 0;
+    uint64_t total = 0;
+    for (int s = 0; s < a.n_seg; s++) {
+        const sinter_gemv_seg &g = a.seg[s];
+        const bool sw = g.epi == SINTER_EPI_SWIGLU;
+        GemvSegPlan &q = p.seg[s];
+        q.wa = reinterpret_cast<uint64_t>(g.w);
+        q.wb = sw ? reinterpret_cast<uint64_t>(g.w2) : 0;
+        q.rows = g.rows;
+        q.base = base;
+        q.type = g.type;
+        q.swig = sw ? 1u : 0u;
+        q.ib = item_bytes(g.type);
+        q.T = items_per_tile(g.type, sw);
+        q.qT = q.T / p.ipr;
+        q.rT = q.T % p.ipr;
+        any_swig |= sw;
+        tmax = std::max(tmax, q.T);
+        if (g.epi == SINTER_EPI_ARGMAX) p.any_argmax = 1;
+        base += g.rows;
+        total += (uint64_t)g.rows * sinter_row_bytes_dev(g.type, a.K) * (sw ? 2u : 1u);
+    }
+    p.total_rows = base;
+    p.mipr = 0xFFFFFFFFu / p.ipr;
+    p.P = p.ipr + (p.ipr & 1u);
+    p.R = (any_swig ? CB_CAP / 2 : CB_CAP) / p.P;
+    const uint32_t tpr = (tmax + p.ipr - 1) / p.ipr;   // rows one tile can touch, less one
+    p.defer = p.R >= 2 * tpr + 2 ? 1u : 0u;
+    p.mR = 0xFFFFFFFFu / p.R;
+    p.RP = p.R * p.P;
+    for (uint32_t w = 0; w <= nblk; w++) cuts[w] = row_cut(a, total, w, nblk);
+}
+
 template <class T>
 static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
     if (blocks == 0 || blocks > 65535) return set_error(SINTER_ERR_ARG, "blocks must be 1..65535");
+    if (kind == SINTER_OP_GEMV && blocks > PLAN_MAX_BLOCKS)
+        return set_error(SINTER_ERR_ARG, "gemv: at most %u blocks", PLAN_MAX_BLOCKS);
     unsigned *err = op_err_cell();
     if (!err) return SINTER_ERR_HIP;
-    sinter_instr ins;
-    std::memset(&ins, 0, sizeof ins);
-    ins.kind = (uint16_t)kind;
-    ins.block_lo = 0;
-    ins.block_hi = (uint16_t)blocks;
-    std::memcpy(ins.payload, &args, sizeof args);
-    sinter_instr *slot = op_instr_slot();
+    static thread_local OpSlot host;
+    std::memset(&host.ins, 0, sizeof host.ins);
+    std::memset(&host.plan, 0, sizeof host.plan);
+    host.ins.kind = (uint16_t)kind;
+    host.ins.block_lo = 0;
+    host.ins.block_hi = (uint16_t)blocks;
+    std::memcpy(host.ins.payload, &args, sizeof args);
+    size_t bytes = offsetof(OpSlot, cuts);
+    if (kind == SINTER_OP_GEMV) {
+        sinter_gemv_args g;
+        std::memcpy(&g, host.ins.payload, sizeof g);
+        build_gemv_plan(g, blocks, host.plan, host.cuts);
+        bytes += (size_t)(blocks + 1) * 4;
+    }
+    OpSlot *slot = op_slot();
     if (!slot) return SINTER_ERR_HIP;
-    if (!hip_ok(hipMemcpyAsync(slot, &ins, sizeof ins, hipMemcpyHostToDevice, (hipStream_t)stream), "op upload"))
+    // pageable source: the copy is staged before hipMemcpyAsync returns
+    if (!hip_ok(hipMemcpyAsync(slot, &host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream), "op upload"))
         return SINTER_ERR_HIP;
-    if (!hip_ok(launch_op(slot, blocks, err, (hipStream_t)stream), "op launch")) return SINTER_ERR_HIP;
+    if (!hip_ok(launch_op(&slot->ins, &slot->plan, slot->cuts, blocks, err, (hipStream_t)stream), "op launch"))
+        return SINTER_ERR_HIP;
     return SINTER_OK;
 }
 
@@ -344,6 +423,8 @@ struct sinter_host {
     int device = -1;
     hipStream_t stream = nullptr;
     sinter_instr *d_prog = nullptr;
+    GemvPlan *d_plans = nullptr;          // [n_instr]
+    uint32_t *d_cuts = nullptr;           // [n_instr][PLAN_CUTS]
     uint32_t n_instr = 0, epoch_stride = 0;
     unsigned *d_cells = nullptr;          // [0] barrier root | [32] err[2] | byte 1024 pass cell |
                                           // byte CELL_GROUPS: barrier group counters (128 B each)
@@ -374,6 +455,8 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     ctl.pass_base = h->passes_done;
     ctl.op_cycles = h->profile_ops ? h->d_op_cycles : nullptr;
     ctl.spin_limit = h->spin_limit;
+    ctl.plans = h->d_plans;
+    ctl.cuts = h->d_cuts;
     ctl.n_instr = h->n_instr;
     ctl.n_passes = n_passes;
     if (!hip_ok(hipMemsetAsync(h->d_cells, 0, 4, h->stream), "barrier reset") ||
@@ -470,11 +553,31 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
                 return set_error(SINTER_ERR_ARG, "instruction %u (gemv): %s", i, why);
         }
     }
+    std::vector<GemvPlan> plans(n_instr);
+    std::vector<uint32_t> cuts((size_t)n_instr * PLAN_CUTS, 0u);
+    for (uint32_t i = 0; i < n_instr; i++) {
+        std::memset(&plans[i], 0, sizeof(GemvPlan));
+        if (prog[i].kind != SINTER_OP_GEMV) continue;
+        sinter_gemv_args a;
+        std::memcpy(&a, prog[i].payload, sizeof a);
+        build_gemv_plan(a, prog[i].block_hi - prog[i].block_lo, plans[i], cuts.data() + (size_t)i * PLAN_CUTS);
+    }
     if (h->d_prog) (void)hipFree(h->d_prog);
+    if (h->d_plans) (void)hipFree(h->d_plans);
+    if (h->d_cuts) (void)hipFree(h->d_cuts);
     h->d_prog = nullptr;
-    if (!hip_ok(hipMalloc(&h->d_prog, (size_t)n_instr * sizeof(sinter_instr)), "program alloc")) return SINTER_ERR_HIP;
+    h->d_plans = nullptr;
+    h->d_cuts = nullptr;
+    h->n_instr = 0;
+    if (!hip_ok(hipMalloc(&h->d_prog, (size_t)n_instr * sizeof(sinter_instr)), "program alloc") ||
+        !hip_ok(hipMalloc(&h->d_plans, (size_t)n_instr * sizeof(GemvPlan)), "plan alloc") ||
+        !hip_ok(hipMalloc(&h->d_cuts, cuts.size() * 4), "cuts alloc"))
+        return SINTER_ERR_HIP;
     if (!hip_ok(hipMemcpy(h->d_prog, prog, (size_t)n_instr * sizeof(sinter_instr), hipMemcpyHostToDevice),
-                "program upload"))
+                "program upload") ||
+        !hip_ok(hipMemcpy(h->d_plans, plans.data(), (size_t)n_instr * sizeof(GemvPlan), hipMemcpyHostToDevice),
+                "plan upload") ||
+        !hip_ok(hipMemcpy(h->d_cuts, cuts.data(), cuts.size() * 4, hipMemcpyHostToDevice), "cuts upload"))
         return SINTER_ERR_HIP;
     h->n_instr = n_instr;
     h->epoch_stride = epoch_stride;
@@ -528,6 +631,8 @@ void sinter_host_destroy(sinter_host *h) {
     if (!h) return;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     if (h->d_prog) (void)hipFree(h->d_prog);
+    if (h->d_plans) (void)hipFree(h->d_plans);
+    if (h->d_cuts) (void)hipFree(h->d_cuts);
     if (h->d_cells) (void)hipFree(h->d_cells);
     if (h->d_pass_cycles) (void)hipFree(h->d_pass_cycles);
     if (h->d_op_cycles) (void)hipFree(h->d_op_cycles);

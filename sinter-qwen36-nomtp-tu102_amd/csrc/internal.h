@@ -16,13 +16,16 @@ struct InterpCtl {
     long long *pass_cycles;   // ring of per-pass durations (wall clock ticks), or null
     long long *op_cycles;     // per-kind durations on block 0, or null
     uint64_t spin_limit;      // barrier spin limit in wall clock ticks
+    const GemvPlan *plans;    // [n_instr], GEMV entries filled
+    const uint32_t *cuts;     // [n_instr][PLAN_CUTS]
     uint32_t n_instr;
     uint32_t n_passes;
     uint32_t pass_cycles_cap;
     uint32_t pass_base;
 };
 
-hipError_t launch_op(const sinter_instr *ins_dev, uint32_t blocks, unsigned *err, hipStream_t s);
+hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
+                     unsigned *err, hipStream_t s);
 hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s);
 hipError_t interp_max_blocks(int *blocks_per_cu);
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
@@ -32,8 +35,8 @@ hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_
 int set_error(int status, const char *fmt, ...);
 bool hip_ok(hipError_t e, const char *what);
 unsigned *op_err_cell();  // per-device error cell of the standalone op launches
-// next slot of the per-device ring of standalone-op instructions (device memory)
-sinter_instr *op_instr_slot();
 int validate_gemv(const sinter_gemv_args &a, const char **why);
+// the plan and the nblk + 1 row cuts of a validated GEMV run by nblk workgroups
+void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts);
 
 }  // namespace sinter

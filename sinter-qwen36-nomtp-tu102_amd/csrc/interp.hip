@@ -29,14 +29,6 @@ __device__ __forceinline__ bool kind_wired(unsigned k) {
            k == SINTER_OP_GDN_STEP || k == SINTER_OP_ATTN_DECODE;
 }
 
-__device__ __forceinline__ void dispatch(const sinter_instr &ins, unsigned *err) {
-    switch (ins.kind) {
-    case SINTER_OP_GEMV: op_gemv(ins, err); break;
-    case SINTER_OP_GDN_STEP: op_gdn_step(ins, err); break;
-    case SINTER_OP_ATTN_DECODE: op_attn_decode(ins, err); break;
-    default: break;
-    }
-}
 
 // Grid barrier, two-level, over monotonic counters (zeroed before the
 // launch): workgroup w counts into group counter w/16 (its own 128-byte
@@ -105,7 +97,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 if (nx != 0xffffffffu) {
                     const sinter_instr &ni = prog[nx];
                     if (ni.kind == SINTER_OP_GEMV && blockIdx.x >= ni.block_lo && blockIdx.x < ni.block_hi) {
-                        gemv_begin(ni, ctl.err, pf);
+                        gemv_begin(ni, ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, pf);
                         pf_i = nx;
                     }
                 }
@@ -132,7 +124,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
                 const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
                 if (kind == SINTER_OP_GEMV) {
-                    if (pf_i != i) gemv_begin(ins, ctl.err, pf);
+                    if (pf_i != i) gemv_begin(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, pf);
                     pf_i = 0xffffffffu;
                     gemv_run(ins, ctl.err, pf);
                 } else if (kind == SINTER_OP_GDN_STEP) {
@@ -152,9 +144,15 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
 // so ops index its payload with ordinary loads.  Ops that need cross-block results use last-arriver counters,
 // never a grid barrier, so co-residency is not required here.
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
-sinter_op_kernel(const sinter_instr *__restrict__ ins, unsigned *err) {
+sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restrict__ plan,
+                 const uint32_t *__restrict__ cuts, unsigned *err) {
     // the host sets block_lo = 0, block_hi = gridDim.x
-    dispatch(*ins, err);
+    switch (ins->kind) {
+    case SINTER_OP_GEMV: op_gemv(*ins, plan, cuts, err); break;
+    case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err); break;
+    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err); break;
+    default: break;
+    }
 }
 
 // Synthetic tensor fill: one thread per 256-element group (weights) or per
@@ -181,8 +179,9 @@ extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type,
 
 namespace sinter {
 
-hipError_t launch_op(const sinter_instr *ins_dev, uint32_t blocks, unsigned *err, hipStream_t s) {
-    hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), 0, s, ins_dev, err);
+hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
+                     unsigned *err, hipStream_t s) {
+    hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), 0, s, ins_dev, plan, cuts, err);
     return hipGetLastError();
 }
 

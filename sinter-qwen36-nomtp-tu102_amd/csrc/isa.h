@@ -63,4 +63,38 @@ __host__ __device__ inline size_t sinter_row_bytes_dev(int t, int64_t k) {
     }
 }
 
+// GEMV items: one 256-element group for the quantised types (one Q4_K /
+// Q6_K block, eight Q8_0 blocks), 64 elements for BF16 / F32.
+__host__ __device__ inline uint32_t item_elems(int t) { return (t == SINTER_BF16 || t == SINTER_F32) ? 64u : 256u; }
+__host__ __device__ inline uint32_t item_bytes(int t) {
+    return t == SINTER_Q4_K ? 144u : t == SINTER_Q6_K ? 210u : t == SINTER_Q8_0 ? 272u : t == SINTER_BF16 ? 128u : 256u;
+}
+// items of one matrix per tile: every lane busy, at most TILE_BYTES - 16
+__host__ __device__ inline uint32_t items_per_tile(int t, bool swiglu) {
+    const uint32_t n = (t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u;
+    return swiglu ? n / 2 : n;
+}
+
+// A GEMV instruction compiled for the kernel: everything about its work split
+// that depends only on the instruction, computed by the host when the program
+// is uploaded (or a standalone op is launched), so that starting the op on
+// the device is a few scalar loads instead of divisions and table builds.
+struct GemvSegPlan {
+    uint64_t wa, wb;                    // weights: A (gate rows for SwiGLU), B (up rows) or 0
+    uint32_t rows, base;                // rows; global row of segment row 0
+    uint32_t type, swig, ib, T, qT, rT; // item bytes; items of each matrix per tile; T / ipr; T % ipr
+};
+struct GemvPlan {
+    uint32_t ok;                        // passed validation (otherwise the op raises BAD_SHAPE)
+    uint32_t n_seg, ipr, vt, any_argmax, total_rows;
+    // the term ring: P = ipr rounded up to even, R rows of P terms,
+    // mipr / mR = floor((2^32-1) / ipr or R), RP = R * P, defer = fold one tile late
+    uint32_t mipr, P, R, mR, RP, defer;
+    GemvSegPlan seg[SINTER_GEMV_MAX_SEG];
+};
+// Workgroup w of an op owns global rows [cuts[w], cuts[w+1]); each
+// instruction has PLAN_CUTS cut slots.
+constexpr uint32_t PLAN_MAX_BLOCKS = 1024;
+constexpr uint32_t PLAN_CUTS = PLAN_MAX_BLOCKS + 1;
+
 }  // namespace sinter
