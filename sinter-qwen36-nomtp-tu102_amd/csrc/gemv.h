@@ -669,7 +669,8 @@ __device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s) {
 // lds_base + 16*l.  Issued from inline asm so the compiler does not treat the
 // pending DMA as aliasing every later LDS read (it would insert vmcnt(0)
 // before them and serialise the pipeline); the tile loop below waits for it
-// explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends.
+// explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends;
+// one wait state separates the M0 write from the DMA that reads it.
 // Weights are read once per pass, so the load is non-temporal (nt): streamed
 // through L2 without displacing the lines that are reused (the kernel's own
 // code, which every instruction-cache miss refetches from L2, and the
@@ -679,6 +680,7 @@ __device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %2, %3 nt\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
