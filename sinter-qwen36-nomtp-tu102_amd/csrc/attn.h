@@ -25,33 +25,62 @@ namespace sinter {
 constexpr int ATT_TILE = 32;   // KV positions per LDS tile
 constexpr int ATT_MAXG = 8;    // max q heads per kv head
 
-// y = rmsnorm(x) * w then NEOX RoPE, for one 256-wide head held one element
-// per thread; result in dst (LDS).  Every thread of the block calls this.
-__device__ __forceinline__ void att_norm_rope(float x, const float *w, float eps, int pos, float theta_scale,
-                                              uint32_t rope_dims, float *dst, double *red) {
-    const uint32_t t = threadIdx.x;
-    const double ss = block_sum_f64((double)(x * x), red);
-    const float mean = (float)(ss / 256.0);
-    const float sc = 1.0f / sqrtf(mean + eps);
-    const float nrm = x * sc;
-    dst[t] = nrm * w[t];
-    __syncthreads();
-    const uint32_t half = rope_dims / 2;
-    float y0 = 0.0f, y1 = 0.0f;
+// The q heads of a kv group (and, for the chunk that appends, the new k row)
+// normalised and rotated together: y = rmsnorm(x) * w per 256-wide head, then
+// NEOX RoPE on the first rope_dims dims.  Thread t holds dim t of every head.
+// Per-head sums of squares are reduced like block_sum_f64 (DPP rows, the four
+// row sums of a wave, then the waves in order), all heads at once, so the
+// whole prologue costs three workgroup barriers.  Rope pair i turns by
+// theta_i = pos * theta_scale^i (repeated fp32 products, as ggml's rope
+// cache), cos/sin evaluated in double and rounded to fp32.
+// x[j] for j < nh are the raw values; rows j < nq use qw, row nq (if nh > nq)
+// uses kw.  Results land in dst[j*256 + t].  LDS: qn [ATT_MAXG+1][256]
+// floats, rot [2][128] floats, red [4][ATT_MAXG+1] doubles.
+__device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t nq, uint32_t nh, const float *qw,
+                                         const float *kw, float eps, int pos, float theta_scale, uint32_t rope_dims,
+                                         float *dst, float *qn, float *rot, double *red) {
+    const uint32_t t = threadIdx.x, half = rope_dims / 2;
     if (t < half) {
-        float theta = (float)pos;
-        for (uint32_t i = 0; i < t; i++) theta *= theta_scale;
-        const float c = (float)cos((double)theta), s = (float)sin((double)theta);
-        const float x0 = dst[t], x1 = dst[t + half];
-        const float a0 = x0 * c, a1 = x1 * s;
-        const float b0 = x0 * s, b1 = x1 * c;
-        y0 = a0 - a1;
-        y1 = b0 + b1;
+        float th = (float)pos;
+        for (uint32_t i = 0; i < t; i++) th *= theta_scale;
+        rot[t] = (float)cos((double)th);
+        rot[128 + t] = (float)sin((double)th);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
+        if (j < nh) {
+            const double v = row16_sum_f64((double)(x[j] * x[j]));
+            const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
+            if (lane_id() == 0) red[wave_id() * (ATT_MAXG + 1) + j] = w;
+        }
     }
     __syncthreads();
-    if (t < half) {
-        dst[t] = y0;
-        dst[t + half] = y1;
+#pragma unroll
+    for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
+        if (j < nh) {
+            double ss = 0.0;
+            for (int wv = 0; wv < (int)(BLOCK_THREADS / 64); wv++) ss += red[wv * (ATT_MAXG + 1) + j];
+            const float mean = (float)(ss / 256.0);
+            const float sc = 1.0f / sqrtf(mean + eps);
+            const float nrm = x[j] * sc;
+            qn[j * 256 + t] = nrm * (j < nq ? qw[t] : kw[t]);
+        }
+    }
+    __syncthreads();
+    for (uint32_t j = 0; j < nh; j++) {
+        const float *r = qn + j * 256;
+        float y = r[t];
+        if (t < half) {
+            const float x0 = r[t], x1 = r[t + half], c = rot[t], s = rot[128 + t];
+            const float a0 = x0 * c, a1 = x1 * s;
+            y = a0 - a1;
+        } else if (t < 2 * half) {
+            const uint32_t i = t - half;
+            const float x0 = r[i], x1 = r[t], c = rot[i], s = rot[128 + i];
+            const float b0 = x0 * s, b1 = x1 * c;
+            y = b0 + b1;
+        }
+        dst[j * 256 + t] = y;
     }
     __syncthreads();
 }
@@ -130,7 +159,10 @@ __device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, unsign
 }
 
 __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
-    const sinter_attn_args &a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
+    // the payload, read once into registers: the op stores to the KV cache
+    // and the partials, which the compiler cannot tell apart from the payload
+    // (every field would be reloaded from memory after each such store)
+    const sinter_attn_args a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
     const int pos = ld_coh(&reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos);
@@ -150,8 +182,8 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
 
     // LDS map (two of the GEMV tile buffers): q heads, K tile, new K/V row |
     // V tile, scores, softmax state, scratch
-    float *qf = reinterpret_cast<float *>(g_tiles);                      // [gqa][256]
-    uint16_t *kt = reinterpret_cast<uint16_t *>(qf + ATT_MAXG * 256);    // [32][256]
+    float *qf = reinterpret_cast<float *>(g_tiles);                      // [gqa][256] q, then the new k row
+    uint16_t *kt = reinterpret_cast<uint16_t *>(qf + (ATT_MAXG + 1) * 256);   // [32][256]
     uint16_t *knew = kt + ATT_TILE * 256;                                // [256]
     uint16_t *vnew = knew + 256;                                         // [256]
     uint16_t *vt = reinterpret_cast<uint16_t *>(g_tiles + TILE_BYTES);                // [32][256]
@@ -163,20 +195,32 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     float *knf = reinterpret_cast<float *>(red + 16);                    // [256] k scratch
     unsigned *flag = reinterpret_cast<unsigned *>(knf + 256);
     double *ew = reinterpret_cast<double *>(g_tiles + 2 * TILE_BYTES);    // [ATT_MAXG][ATT_FAN+1] merge weights
+    float *qn = reinterpret_cast<float *>(g_tiles + 2 * TILE_BYTES + 1024);   // [ATT_MAXG+1][256] prep scratch
+    float *rot = qn + (ATT_MAXG + 1) * 256;                                  // [2][128] rope cos | sin
+    double *pred = reinterpret_cast<double *>(rot + 256);                   // [4][ATT_MAXG+1]
 
     for (uint32_t item = rel; item < NKV * C; item += nblk) {
         const uint32_t g = item / C, c = item % C;
         const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
         const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
 
-        for (uint32_t hh = 0; hh < gqa; hh++) {
-            const uint32_t h = g * gqa + hh;
-            att_norm_rope(ld_coh(a.qg + (size_t)h * 2 * HD + t), a.q_norm, a.eps, pos, a.theta_scale, a.rope_dims,
-                          qf + hh * 256, red);
+        {
+            // q heads g*gqa .. and, for the owner, the new k row (as head gqa)
+            float xr[ATT_MAXG + 1];
+#pragma unroll
+            for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
+                xr[hh] = hh < gqa ? ld_coh(a.qg + (size_t)(g * gqa + hh) * 2 * HD + t) : 0.0f;
+            xr[ATT_MAXG] = 0.0f;
+            if (owner) {
+#pragma unroll
+                for (uint32_t hh = 0; hh <= ATT_MAXG; hh++)
+                    if (hh == gqa) xr[hh] = ld_coh(a.k + (size_t)g * HD + t);
+            }
+            att_prep(xr, gqa, owner ? gqa + 1 : gqa, a.q_norm, a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, qf,
+                     qn, rot, pred);
         }
         if (owner) {
-            att_norm_rope(ld_coh(a.k + (size_t)g * HD + t), a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, knf, red);
-            const uint16_t kh = f2h(knf[t]), vh = f2h(ld_coh(a.v + (size_t)g * HD + t));
+            const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = f2h(ld_coh(a.v + (size_t)g * HD + t));
             knew[t] = kh;
             vnew[t] = vh;
             st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
