@@ -719,14 +719,23 @@ __device__ __forceinline__ TD tile_next(Cursor &c, char *buf) {
     }
     const uint32_t w = uni(wave_id()), lane16 = lane_id() * 16;
     const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void *)buf;
+    if (!c.swig) {
+        // one matrix: chunk j of the tile is bytes [1024 j, 1024 j + 1024)
 #pragma unroll
-    for (uint32_t k = 0; k < TILE_CPW; k++) {
-        const uint32_t j = w + 4 * k;
-        const bool in_a = j < chunks_a;
-        const uintptr_t src = in_a ? sa : sb;
-        const uint32_t j0 = in_a ? j : j - chunks_a;
-        const uint32_t voff = min(j0 * 1024 + lane16, in_a ? last_a : last_b);
-        lds_dma16(src, voff, lbase + j * 1024);
+        for (uint32_t k = 0; k < TILE_CPW; k++) {
+            const uint32_t j = w + 4 * k;
+            lds_dma16(sa, min(j * 1024 + lane16, last_a), lbase + j * 1024);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t k = 0; k < TILE_CPW; k++) {
+            const uint32_t j = w + 4 * k;
+            const bool in_a = j < chunks_a;
+            const uintptr_t src = in_a ? sa : sb;
+            const uint32_t j0 = in_a ? j : j - chunks_a;
+            const uint32_t voff = min(j0 * 1024 + lane16, in_a ? last_a : last_b);
+            lds_dma16(src, voff, lbase + j * 1024);
+        }
     }
     // advance
     c.a += t.cnt;
