@@ -32,7 +32,7 @@ __shared__ __attribute__((aligned(16))) char g_qbuf[QBUF_BYTES];
 __shared__ float g_res[2 * RES_CAP];
 __shared__ double g_red[16];
 __shared__ double g_part[16];
-__shared__ double g_cb[CB_CAP];           // GEMV item terms of the last two tiles
+__shared__ __attribute__((aligned(16))) double g_cb[CB_CAP];   // GEMV item terms of the last two tiles
 // the running op's payload, copied out of the program once per op so that
 // reading it never waits behind tile LDS-DMA (lgkmcnt, not vmcnt)
 __shared__ __attribute__((aligned(16))) unsigned char g_args[240];

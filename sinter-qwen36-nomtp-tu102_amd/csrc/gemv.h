@@ -149,21 +149,32 @@ __device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t
                                         LDS float *qd, LDS int16_t *qb) {
     int qv[16];
     if (vt == SINTER_Q8_K) {
-        // ggml quantize_row_q8_K_ref: the signed element of largest |x|,
-        // first index wins; q = min(127, rne(x * -127/max)), d = 1/iscale
-        float am = 0.0f, sv = 0.0f;
-        int fi = 0;
+        // ggml quantize_row_q8_K_ref: the signed element of largest |x|, first
+        // index wins; q = min(127, rne(x * -127/max)), d = 1/iscale.  The
+        // lane's maximum, first index and its sign come from balanced trees
+        // (short dependency chains); NaNs never win (v_max ignores them, and
+        // they compare unequal).
+        float ax[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float ax = fabsf(t[i]);
-            if (ax > am) { am = ax; sv = t[i]; fi = i; }
-        }
+        for (int i = 0; i < 16; i++) ax[i] = fabsf(t[i]);
+        float m4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) m4[i] = fmaxf(fmaxf(ax[4 * i], ax[4 * i + 1]), fmaxf(ax[4 * i + 2], ax[4 * i + 3]));
+        const float am = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
         const float A = row16_max(am);
-        // (index, sign) of the first element reaching the row maximum
-        const int key = row16_min(am == A ? (int)(((r * 16 + fi) << 1) | (sv < 0.0f ? 1u : 0u)) : 0x7fffffff);
+        // (index, sign) keys of the elements reaching A; the smallest wins
+        int key[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) key[i] = ax[i] == A ? ((i << 1) | (t[i] < 0.0f ? 1 : 0)) : 0x7fffffff;
+#pragma unroll
+        for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w; i++) key[i] = min(key[i], key[i + w]);
+        const int lkey = key[0] == 0x7fffffff ? 0x7fffffff : (int)(r << 5) + key[0];
+        const int gkey = row16_min(lkey);
         float dd = 0.0f;
         if (A != 0.0f) {
-            const float bmax = (key & 1) ? -A : A;
+            const float bmax = (gkey & 1) ? -A : A;
             const float iscale = -127.f / bmax;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -175,9 +186,8 @@ __device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t
 #pragma unroll
             for (int i = 0; i < 16; i++) qv[i] = 0;
         }
-        int bsum = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) bsum += qv[i];
+        const int bsum = (((qv[0] + qv[1]) + (qv[2] + qv[3])) + ((qv[4] + qv[5]) + (qv[6] + qv[7]))) +
+                         (((qv[8] + qv[9]) + (qv[10] + qv[11])) + ((qv[12] + qv[13]) + (qv[14] + qv[15])));
         lds_st16(q + c * ACT_GSTRIDE + r * 16, pack4_i8(qv[0], qv[1], qv[2], qv[3]), pack4_i8(qv[4], qv[5], qv[6], qv[7]),
                  pack4_i8(qv[8], qv[9], qv[10], qv[11]), pack4_i8(qv[12], qv[13], qv[14], qv[15]));
         qb[e0 / 16] = (int16_t)bsum;
@@ -615,7 +625,7 @@ __device__ __forceinline__ uint32_t divm(uint32_t v, uint32_t d, uint32_t m, uin
 }
 
 // The term ring: row-aligned.  The row of workgroup-local index lr owns
-// slot lr % R; its term k sits at slot*P + k (P = ipr rounded up to even, the
+// slot lr % R; its term k sits at slot*P + k (P = ipr rounded up to RING_PAD, the
 // pad slot holds -0.0, an exact no-op in the fold).  SwiGLU up terms use a
 // second ring of R*P behind the first.  Rows are folded once, complete, in
 // ascending k.  "Deferred" rings fold a tile's rows one tile later (no extra
@@ -814,21 +824,60 @@ __device__ __forceinline__ uint32_t td_done_after(const TD &t, const Ring &rg) {
     return t.lr0 + divm(t.ka + t.cnt, rg.ipr, rg.mipr, r);
 }
 
-// One row's P ring terms summed in ascending order (fp64), 8 at a time.
+// One row's P ring terms summed in ascending order (fp64); pad terms are
+// -0.0 and rows start 16-byte aligned.  With P a multiple of RING_PAD = 8:
+// rows of up to 24 terms (K <= 6144 for 256-element items) issue every read
+// before the first add -- one LDS round trip; longer rows run 8-term batches
+// with the next batch's reads in flight.  Other P (short rows): pairs.
 __device__ __forceinline__ double fold_row(const LDS double *g, uint32_t P) {
+    typedef double f64x2 __attribute__((ext_vector_type(2)));
+    const LDS f64x2 *v = reinterpret_cast<const LDS f64x2 *>(g);
     double s = 0.0;
-    uint32_t k = 0;
-    for (; k + 8 <= P; k += 8) {
-        double b[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) b[i] = g[k + i];
-#pragma unroll
-        for (int i = 0; i < 8; i++) s += b[i];
+    if ((P & 7u) != 0) {
+        for (uint32_t k = 0; k < P / 2; k++) {
+            const f64x2 b = v[k];
+            s += b.x;
+            s += b.y;
+        }
+        return s;
     }
-    for (; k < P; k += 2) {
-        const double b0 = g[k], b1 = g[k + 1];
-        s += b0;
-        s += b1;
+    if (P <= 24) {
+        f64x2 b[12];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) b[i] = v[i];
+        if (P >= 16) {
+#pragma unroll
+            for (uint32_t i = 4; i < 8; i++) b[i] = v[i];
+        }
+        if (P >= 24) {
+#pragma unroll
+            for (uint32_t i = 8; i < 12; i++) b[i] = v[i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) { s += b[i].x; s += b[i].y; }
+        if (P >= 16) {
+#pragma unroll
+            for (uint32_t i = 4; i < 8; i++) { s += b[i].x; s += b[i].y; }
+        }
+        if (P >= 24) {
+#pragma unroll
+            for (uint32_t i = 8; i < 12; i++) { s += b[i].x; s += b[i].y; }
+        }
+        return s;
+    }
+    f64x2 cur[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) cur[i] = v[i];
+    for (uint32_t k = 0; k < P; k += 8) {
+        f64x2 nxt[4];
+        if (k + 8 < P) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) nxt[i] = v[(k + 8) / 2 + i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) { s += cur[i].x; s += cur[i].y; }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) cur[i] = nxt[i];
     }
     return s;
 }

@@ -139,8 +139,9 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
             any_swig |= sw;
             tmax = std::max(tmax, ((t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u) / (sw ? 2u : 1u));
         }
-        const uint32_t P = ipr + (ipr & 1u), R = (any_swig ? CB_CAP / 2 : CB_CAP) / P;
-        if (R < (tmax + ipr - 1) / ipr + 1) return bad("rows too long for the term ring");
+        const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP, tpr = (tmax + ipr - 1) / ipr;
+        const uint32_t P = ring_row(ipr, cap, tpr), R = cap / P;
+        if (R < tpr + 1) return bad("rows too long for the term ring");
     }
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
@@ -212,9 +213,10 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
     }
     p.total_rows = base;
     p.mipr = 0xFFFFFFFFu / p.ipr;
-    p.P = p.ipr + (p.ipr & 1u);
-    p.R = (any_swig ? CB_CAP / 2 : CB_CAP) / p.P;
     const uint32_t tpr = (tmax + p.ipr - 1) / p.ipr;   // rows one tile can touch, less one
+    const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP;
+    p.P = ring_row(p.ipr, cap, tpr);
+    p.R = cap / p.P;
     p.defer = p.R >= 2 * tpr + 2 ? 1u : 0u;
     p.mR = 0xFFFFFFFFu / p.R;
     p.RP = p.R * p.P;

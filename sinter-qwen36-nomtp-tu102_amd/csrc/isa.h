@@ -26,9 +26,20 @@ constexpr unsigned TILE_BYTES = 36u * 1024u;
 constexpr unsigned TILE_CPW = TILE_BYTES / 1024u / (BLOCK_THREADS / 64u);
 constexpr unsigned QBUF_BYTES = 40u * 1024u;   // padded activation: Q8_K K=17408 20944 B; BF16 K=17408 39168 B
 constexpr unsigned RES_CAP = 512u;             // rows buffered before the epilogue runs
-constexpr unsigned CB_CAP = 776u;              // GEMV term ring: two tiles of up to 256 item terms,
-                                               // plus the fold's masked over-read (8-term groups)
+constexpr unsigned CB_CAP = 776u;              // GEMV term ring (doubles): the rows of two tiles
+                                               // of up to 256 item terms, padded (RING_PAD)
 static_assert(TILE_CPW * 4u * 1024u == TILE_BYTES, "tile = whole chunks per wave");
+// A term-ring row holds a row's item terms padded with -0.0 (an exact no-op
+// in the fold) to a multiple of RING_PAD, so the fold reads whole 16-byte
+// pairs in batches of RING_PAD with no masking -- or, when rows that long
+// would not leave the ring room for the rows one tile touches (short rows,
+// many per tile), to a multiple of 2.  cap = ring capacity in terms, tpr =
+// rows one tile can touch, less one.
+constexpr uint32_t RING_PAD = 8u;
+__host__ __device__ inline uint32_t ring_row(uint32_t ipr, uint32_t cap, uint32_t tpr) {
+    const uint32_t p8 = (ipr + RING_PAD - 1u) & ~(RING_PAD - 1u);
+    return cap / p8 >= tpr + 1u ? p8 : ipr + (ipr & 1u);
+}
 
 // GEMV activation layout in LDS.  Padded so that lanes working on different
 // groups/chunks start on different LDS banks (an unpadded 256-byte group
@@ -87,7 +98,7 @@ struct GemvSegPlan {
 struct GemvPlan {
     uint32_t ok;                        // passed validation (otherwise the op raises BAD_SHAPE)
     uint32_t n_seg, ipr, vt, any_argmax, total_rows;
-    // the term ring: P = ipr rounded up to even, R rows of P terms,
+    // the term ring: P = ipr rounded up to RING_PAD, R rows of P terms,
     // mipr / mR = floor((2^32-1) / ipr or R), RP = R * P, defer = fold one tile late
     uint32_t mipr, P, R, mR, RP, defer;
     GemvSegPlan seg[SINTER_GEMV_MAX_SEG];
