@@ -49,6 +49,23 @@ def bytes_per_token(cfg, m, n_attended):
             "total": weights + gdn_state + conv_state + kv_row * n_attended + kv_row + logits}
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_e2e_q4km_ctx4096.md")
+
+
+def measured_traffic(passes_per_launch):
+    """HBM bytes per launch of the interpreter, from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE per pass, scaled against a copy kernel of
+    known size), or None when no summary exists."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_pass:"):
+                    return round(float(line.split(":", 1)[1]) * passes_per_launch)
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(m, ctx, seconds):
     """Time the CPU oracle decoding from the same synthetic context."""
     import numpy as np
@@ -83,6 +100,9 @@ def main():
                     help="greedy passes per cooperative launch (the warmup is one launch)")
     ap.add_argument("--profile-ops", type=int, default=0,
                     help="after the timed run, N more tokens with block-0 per-kind timers (stderr)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 3 times (torch's copy kernel) and exit: the "
+                         "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the decode path on one GPU "
@@ -90,9 +110,20 @@ def main():
         sys.exit(2)
 
     import torch
-    import sinter
 
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
+        return
+
+    import sinter
+
     n_ctx = args.ctx + args.warmup + args.steps + 8
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
     t0 = time.perf_counter()
@@ -154,7 +185,7 @@ def main():
                    "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl),
                      "kernel": "sinter_interp", "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
