@@ -124,7 +124,7 @@ def main():
 
     import sinter
 
-    n_ctx = args.ctx + args.warmup + args.steps + 8
+    n_ctx = args.ctx + args.warmup + args.steps + args.profile_ops + 8
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
     t0 = time.perf_counter()
     m = sinter.Model(cfg, seed=args.seed)

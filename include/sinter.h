@@ -118,7 +118,7 @@ typedef struct sinter_gemv_seg {
     uint32_t rows;
     uint8_t type;    /* sinter_type of w (and w2) */
     uint8_t epi;     /* sinter_gemv_epi */
-    uint8_t dconv;   /* CONV: taps */
+    uint8_t dconv;   /* CONV: taps (2..4) */
     uint8_t _pad;
 } sinter_gemv_seg;
 
@@ -223,6 +223,14 @@ int  sinter_host_shutdown(sinter_host *h, double timeout_ms);
 void sinter_host_destroy(sinter_host *h);
 int  sinter_host_read_pass_cycles(sinter_host *h, long long *out, unsigned count);
 int  sinter_host_reset_op_cycles(sinter_host *h);
+/* Diagnostics, no counterpart in the reference (its per-op cycle counters,
+ * core/host.h:77-80, are block 0 only): the next launch stamps its first
+ * pass into dev_buf (device memory, >= (n_instr+1)*blocks*4 words): for
+ * instruction i (i = n_instr: the pass-end barrier) and block b, words
+ * [(i*blocks+b)*4 ..] = wall clock (100 MHz) at the instruction's start,
+ * after its barrier wait (a barrier fused with the GEMV after it records
+ * under the GEMV's index), after a GEMV's prologue, at its end. */
+int  sinter_host_trace_next(sinter_host *h, unsigned long long *dev_buf, size_t words);
 int  sinter_host_read_op_cycles(sinter_host *h, long long *out, unsigned count);
 /* device pointers the program payloads reference */
 sinter_pass_cell *sinter_host_pass_cell(sinter_host *h);

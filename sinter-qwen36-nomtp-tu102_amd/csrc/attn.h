@@ -180,13 +180,13 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     uint32_t clen = (n_kv + C - 1) / C;
     clen = (clen + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
 
-    // LDS map (two of the GEMV tile buffers): q heads, K tile, new K/V row |
+    // LDS map (the scratch region): q heads, K tile, new K/V row |
     // V tile, scores, softmax state, scratch
-    float *qf = reinterpret_cast<float *>(g_tiles);                      // [gqa][256] q, then the new k row
+    float *qf = reinterpret_cast<float *>(g_big);                      // [gqa][256] q, then the new k row
     uint16_t *kt = reinterpret_cast<uint16_t *>(qf + (ATT_MAXG + 1) * 256);   // [32][256]
     uint16_t *knew = kt + ATT_TILE * 256;                                // [256]
     uint16_t *vnew = knew + 256;                                         // [256]
-    uint16_t *vt = reinterpret_cast<uint16_t *>(g_tiles + TILE_BYTES);                // [32][256]
+    uint16_t *vt = reinterpret_cast<uint16_t *>(g_big + ATT_REGION);                // [32][256]
     double *sc = reinterpret_cast<double *>(vt + ATT_TILE * 256);        // [gqa][32] scores -> weights
     double *mrun = sc + ATT_MAXG * ATT_TILE;                             // [gqa]
     double *lrun = mrun + ATT_MAXG;                                      // [gqa]
@@ -194,8 +194,8 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     double *red = corr + ATT_MAXG;                                       // 16
     float *knf = reinterpret_cast<float *>(red + 16);                    // [256] k scratch
     unsigned *flag = reinterpret_cast<unsigned *>(knf + 256);
-    double *ew = reinterpret_cast<double *>(g_tiles + 2 * TILE_BYTES);    // [ATT_MAXG][ATT_FAN+1] merge weights
-    float *qn = reinterpret_cast<float *>(g_tiles + 2 * TILE_BYTES + 1024);   // [ATT_MAXG+1][256] prep scratch
+    double *ew = reinterpret_cast<double *>(g_big + 2 * ATT_REGION);    // [ATT_MAXG][ATT_FAN+1] merge weights
+    float *qn = reinterpret_cast<float *>(g_big + 2 * ATT_REGION + 1024);   // [ATT_MAXG+1][256] prep scratch
     float *rot = qn + (ATT_MAXG + 1) * 256;                                  // [2][128] rope cos | sin
     double *pred = reinterpret_cast<double *>(rot + 256);                   // [4][ATT_MAXG+1]
 

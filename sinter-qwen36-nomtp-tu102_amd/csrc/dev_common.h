@@ -2,12 +2,10 @@
 // agent-scope (cross-XCD) loads/stores and fences, f16/bf16 conversions and
 // the activation-quantiser arithmetic.
 //
-// Coherence on gfx950: each of the 8 XCDs has its own L2.  Data written in
-// one phase and read by another workgroup in a later phase is ordered by the
-// grid barrier (sync.h), whose release/acquire fences at agent scope write
-// back and invalidate the L2/L1 of the participating XCDs; after the barrier
-// ordinary loads see the producer's stores.  Weights are immutable and use
-// plain loads throughout.
+// Coherence on gfx950: each of the 8 XCDs has its own L2.  Data that one
+// workgroup writes and another reads later in the pass moves through
+// device-coherent loads and stores (below), ordered by the grid barrier's
+// counter.  Weights are immutable and use plain (non-temporal) loads.
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -25,16 +23,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef LDS char lds_char;
 
 // ---------------------------------------------------------------- static LDS
-// g_tiles: the GEMV's three LDS-DMA tile buffers (other ops use the space as
-// scratch); g_qbuf: the quantised activation.
-__shared__ __attribute__((aligned(16))) char g_tiles[3 * TILE_BYTES];
+// g_big: scratch shared by the ops (GEMV staging then term rings, attention
+// tiles, GDN vectors); g_qbuf: the quantised GEMV activation.
+__shared__ __attribute__((aligned(16))) char g_big[BIG_BYTES];
 __shared__ __attribute__((aligned(16))) char g_qbuf[QBUF_BYTES];
-__shared__ float g_res[2 * RES_CAP];
 __shared__ double g_red[16];
 __shared__ double g_part[16];
-__shared__ __attribute__((aligned(16))) double g_cb[CB_CAP];   // GEMV item terms of the last two tiles
 // the running op's payload, copied out of the program once per op so that
-// reading it never waits behind tile LDS-DMA (lgkmcnt, not vmcnt)
+// reading it is an LDS access rather than a global one
 __shared__ __attribute__((aligned(16))) unsigned char g_args[240];
 
 // ---------------------------------------------------------------- wave64
@@ -225,6 +221,50 @@ __device__ __forceinline__ void raise_error(unsigned *err, unsigned code, unsign
     if (!err) return;
     if (atomicCAS(err, 0u, code) == 0u)
         __hip_atomic_store(err + 1, aux, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- grid barrier
+
+// Grid barrier, two-level, over monotonic counters (zeroed before the
+// launch): workgroup w counts into group counter w/16 (its own 128-byte
+// line); the group's last arriver counts into the root; every workgroup's
+// thread 0 spins on the root until epoch*groups arrivals.  Sixteen arrivals
+// per line instead of the whole grid on one line (atomics to one address
+// serialise at the memory side).  No cache writeback or invalidate: every
+// wave first waits for its own memory operations, and all data that crosses
+// workgroups moves through device-coherent loads and stores (dev_common.h).
+// Split in two so that work that does not depend on the barrier (the next
+// GEMV's first weight tiles) can be issued between arriving and waiting.
+__device__ __forceinline__ void grid_arrive(unsigned *bar, unsigned *groups, unsigned &epoch) {
+    settle_vmem();
+    __syncthreads();
+    epoch += 1;
+    if (threadIdx.x == 0) {
+        const unsigned g = blockIdx.x >> 4;
+        const unsigned gsize = min(16u, gridDim.x - g * 16u);
+        const unsigned old = __hip_atomic_fetch_add(groups + g * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Returns false on timeout.
+__device__ __forceinline__ bool grid_wait(unsigned *bar, unsigned epoch, uint64_t spin_limit_ticks, unsigned *err) {
+    __shared__ unsigned timed_out;
+    if (threadIdx.x == 0) {
+        timed_out = 0;
+        const unsigned target = epoch * ((gridDim.x + 15u) >> 4);
+        const uint64_t t0 = wall_clock64();
+        while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (wall_clock64() - t0 > spin_limit_ticks) {
+                raise_error(err, SINTER_E_TIMEOUT_BARRIER, epoch);
+                timed_out = 1;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    return timed_out == 0;
 }
 
 // ---------------------------------------------------------------- block formats

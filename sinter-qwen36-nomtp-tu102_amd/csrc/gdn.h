@@ -22,7 +22,7 @@
 namespace sinter {
 
 __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
-    char *lds = g_tiles;
+    char *lds = g_big;
     const sinter_gdn_args &a = *reinterpret_cast<const sinter_gdn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t D = a.d, HK = a.hk, HV = a.hv, cols = a.cols;

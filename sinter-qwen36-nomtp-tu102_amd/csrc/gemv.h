@@ -6,25 +6,29 @@
 //             there q8_1; here ggml's Q8_K / Q8_0 / BF16)
 //   body      y = W a for Q4_K / Q6_K / Q8_0 / BF16 / F32 rows, several
 //             matrices ("segments") sharing one activation        (gemv.cuh:256-492)
-//   epilogue  store, residual add, SwiGLU pair, greedy argmax    (gemv.cuh:327-347,
-//             k0/harness.cpp:1187-1195)
+//   epilogue  store, residual add, SwiGLU pair, conv, greedy argmax
+//             (gemv.cuh:327-347, k0/harness.cpp:1187-1195)
 //
 // Work split: the rows of all segments form one byte-weighted row space; the
-// participating workgroups take contiguous, byte-balanced row ranges.  A
-// workgroup streams its share through three 36 KiB LDS tiles with gfx950
-// LDS-DMA (global_load_lds_dwordx4: 16 B per lane straight into LDS, no
-// VGPRs), two tiles in flight while one is computed.  A tile is a run of
-// whole items (ggml blocks) that ignores row boundaries, sized so that every
-// lane of the workgroup has one item (or half of one) per tile; item terms go
-// to an LDS ring, and one tile later the lanes that own the touched rows add
-// them to per-row running sums.  One workgroup barrier per tile.  Row results
-// stay in LDS; the epilogues run over the buffered rows.
+// host cuts it into one contiguous, byte-balanced row range per WAVE (four
+// per workgroup).  A wave streams its range on its own -- no workgroup
+// barrier inside the body: lane l takes items l, l+64, l+128, ... of the
+// range (an item is one ggml block group; items ignore row boundaries, so
+// every lane is busy), loads each item with 16-byte loads straight into
+// registers, D items ahead (the first D are issued before the
+// grid barrier that precedes the op, while the workgroup waits), computes its
+// exact term against the quantised activation in LDS and writes it to the
+// wave's term ring in LDS.  When the ring fills (and at the end) the lanes
+// fold the completed rows -- lane i the i-th row -- in ascending item order
+// and apply the row's epilogue.
 //
 // Declared numerics (oracle/oracle.c): integer block dots are exact; each
 // item's term is an fp64 expression of exact integers and the f16/f32
 // scales; a row is the ascending fp64 sum of its item terms, rounded to fp32
 // once, so outputs are bit-identical to the oracle's.
 #pragma once
+#include <type_traits>
+
 #include "dev_common.h"
 
 namespace sinter {
@@ -34,30 +38,6 @@ __device__ __forceinline__ int vec_dot_type(int t) {
          : (t == SINTER_Q8_0) ? SINTER_Q8_0
          : (t == SINTER_BF16) ? SINTER_BF16 : SINTER_F32;
 }
-// bytes of one 256-element group of a weight row
-__device__ __forceinline__ uint32_t group_bytes(int t) {
-    switch (t) {
-    case SINTER_Q4_K: return 144;
-    case SINTER_Q6_K: return 210;
-    case SINTER_Q8_0: return 272;
-    case SINTER_BF16: return 512;
-    default: return 1024;
-    }
-}
-
-// ------------------------------------------------------------ LDS helpers
-
-// 4 bytes at an arbitrary 2-aligned LDS byte offset
-__device__ __forceinline__ uint32_t lds_u32(const char *lds, uint32_t off) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(lds + (off & ~3u));
-    const uint32_t lo = w[0];
-    if ((off & 3u) == 0) return lo;
-    return __builtin_amdgcn_alignbyte(w[1], lo, off & 3u);
-}
-__device__ __forceinline__ uint16_t lds_u16(const char *lds, uint32_t off) {
-    return *reinterpret_cast<const uint16_t *>(lds + off);
-}
-
 // ------------------------------------------------------------ activation layout in LDS
 // (ACT_* constants and act_bytes are in isa.h, shared with host validation)
 struct ActView {
@@ -124,15 +104,64 @@ __device__ __forceinline__ void dequant4(const void *row, int type, uint32_t e, 
     }
 }
 
+// ------------------------------------------------------------ LDS-DMA
+
+// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at base + voff land at
+// lds_base + 16*l (gfx950 global_load_lds_dwordx4: no VGPRs involved).
+// Issued from inline asm so the compiler does not treat the pending DMA as
+// aliasing every later LDS access; callers wait for it explicitly
+// (dma_wait).  M0 (the LDS base of the DMA) is restored before the asm ends;
+// one wait state separates the M0 write from the DMA that reads it.  COH
+// selects the device-coherent cache policy (sc1) for data another workgroup
+// wrote earlier in the pass.
+template <bool COH>
+__device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
+    uint32_t saved;
+    if (COH) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %3 sc1\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds_base), "v"(voff), "s"(base)
+            : "memory");
+    } else {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %3\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds_base), "v"(voff), "s"(base)
+            : "memory");
+    }
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Copy n floats (n a multiple of 256) from global p into LDS dst: the
+// workgroup's waves take 1 KiB chunks round-robin.
+template <bool COH>
+__device__ __forceinline__ void dma_vec(const float *p, uint32_t n, char *dst) {
+    // readfirstlane returns int: widen each word through uint32_t (a
+    // sign-extended low word with bit 31 set would overwrite the high word)
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)p >> 32));
+    const uintptr_t base = ((uintptr_t)hi << 32) | (uintptr_t)lo;
+    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void *)dst;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(wave_id()), lane16 = lane_id() * 16;
+    const uint32_t nch = n / 256;
+    for (uint32_t j = w; j < nch; j += WAVES) lds_dma16<COH>(base, j * 1024 + lane16, lbase + j * 1024);
+}
+
 // ------------------------------------------------------------ prologue
 
 // The prologue gives each 256-element chunk to one 16-lane DPP row, 16
 // consecutive elements per lane: a per-chunk reduction is four in-VALU DPP
 // steps and a Q8_K bsum (16 elements) is one lane's own sum.
 constexpr uint32_t PRO_ROWS = BLOCK_THREADS / 16;
-// chunks per row per round (all loads of a round are issued before any of
-// them is used): one round up to K = 16 * 5 * 256 = 20480
-constexpr uint32_t PRO_RC = 5;
 
 __device__ __forceinline__ void lds_st16(lds_char *p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -222,27 +251,50 @@ __device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t
     }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
+__device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
+
 // Build the quantised activation in LDS (g_qbuf).  Every thread of the block
-// calls this.  `red` is 128 B of LDS scratch.  Row g of the block (16 lanes)
-// owns chunks g, g+16, ... and reads them in rounds of PRO_RC chunks, so the
-// prologue pays one memory latency per round (one round up to K = 20480; an
-// RMSNorm with more chunks makes one extra pass for its sum of squares).
+// calls this.  Phase 1 stages the f32 inputs in g_big with LDS-DMA -- x (and
+// z for the gated norm) device-coherently, the norm weights cached --
+// without holding any registers (the caller may hold prefetched weights).
+// Phase 2: row g of the block (16 lanes) owns chunks g, g+16, ... and reads
+// its elements from the staging area; RMSNorm first sums squares over its
+// chunks for the block-wide scale.
 __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
                                               unsigned *err) {
     const uint32_t K = a.K;
     const bool embed = a.pro == SINTER_PRO_EMBED, gated = a.pro == SINTER_PRO_GATED;
     const bool rms = a.pro == SINTER_PRO_RMSNORM || embed;
-    const __amdgpu_buffer_rsrc_t xr = coh_rsrc(a.x, embed ? 0u : K * 4);
-    const __amdgpu_buffer_rsrc_t zr = coh_rsrc(a.aux, gated ? K * 4 : 0u);
-    const void *erow = nullptr;
+    char *xs_g = g_big, *ys_g = g_big + K * 4;
     if (embed) {
         int32_t tok = ld_coh(a.token);
         if (tok < 0 || (uint32_t)tok >= a.aux_rows) {   // never read outside the table
             if (threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, 0xE0000000u);
             tok = 0;
         }
-        erow = static_cast<const char *>(a.aux) + (size_t)tok * sinter_row_bytes_dev(a.aux_type, K);
+        const void *erow = static_cast<const char *>(a.aux) + (size_t)tok * sinter_row_bytes_dev(a.aux_type, K);
+        dma_vec<false>(a.norm_w, K, ys_g);
+        LDS float *xs = reinterpret_cast<LDS float *>((lds_char *)xs_g);
+        for (uint32_t i = threadIdx.x; i < K / 4; i += BLOCK_THREADS) {
+            float v[4];
+            dequant4(erow, a.aux_type, 4 * i, v);
+            if (write_x) st_coh4(a.x_out + 4 * i, make_float4(v[0], v[1], v[2], v[3]));
+#pragma unroll
+            for (int k = 0; k < 4; k++) xs[4 * i + k] = v[k];
+        }
+    } else {
+        dma_vec<true>(a.x, K, xs_g);
+        if (gated) dma_vec<true>(static_cast<const float *>(a.aux), K, ys_g);
+        else if (rms) dma_vec<false>(a.norm_w, K, ys_g);
     }
+    dma_wait();
+    __syncthreads();
+
+    const LDS float *xs = reinterpret_cast<const LDS float *>((const lds_char *)xs_g);
+    const LDS float *ys = reinterpret_cast<const LDS float *>((const lds_char *)ys_g);
     const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
     // the lane's indices, opaque to the compiler so that the per-lane address
     // arithmetic below is not hoisted out of the interpreter loop (where it
@@ -250,29 +302,28 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
-    const uint32_t mine = nchunk > g ? (nchunk - g + PRO_ROWS - 1) / PRO_ROWS : 0u;   // chunks of this row
-    auto raw16 = [&](uint32_t e0, float v[16]) {
-        if (embed) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) dequant4(erow, a.aux_type, e0 + 4 * k, v + 4 * k);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float4 t = ld_coh16(xr, (e0 + 4 * k) * 4);
-                v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-            }
-        }
-    };
-    // the second per-element input: the gate z (gated) or the norm weights
-    auto raw16b = [&](uint32_t e0, float y[16]) {
+    auto ld16 = [&](const LDS float *base, uint32_t e0, float v[16]) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (gated) t = ld_coh16(zr, (e0 + 4 * k) * 4);
-            else if (rms) t = *reinterpret_cast<const float4 *>(a.norm_w + e0 + 4 * k);
-            y[4 * k] = t.x; y[4 * k + 1] = t.y; y[4 * k + 2] = t.z; y[4 * k + 3] = t.w;
+            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(base + e0 + 4 * k);
+            v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
         }
     };
+    // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
+    // scale = 1/sqrtf(mean + eps))
+    float gscale = 1.0f;
+    if (rms) {
+        double s = 0.0;
+        for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
+            float v[16];
+            ld16(xs, c * 256 + r * 16, v);
+#pragma unroll
+            for (int i = 0; i < 16; i++) s += (double)(v[i] * v[i]);
+        }
+        s = block_sum_f64(s, red);
+        const float mean = (float)(s / (double)K);
+        gscale = 1.0f / sqrtf(mean + a.eps);
+    }
     // gated-norm weights: element i of this lane is norm_w[(16r + i) % gd] in every chunk
     float gw[16];
 #pragma unroll
@@ -281,105 +332,53 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         if (gated) t = *reinterpret_cast<const float4 *>(a.norm_w + ((r * 16 + 4 * k) & (gd - 1)));
         gw[4 * k] = t.x; gw[4 * k + 1] = t.y; gw[4 * k + 2] = t.z; gw[4 * k + 3] = t.w;
     }
-    float xv[PRO_RC][16], yv[PRO_RC][16];
-    auto load_round = [&](uint32_t j0, bool both) {
-#pragma unroll
-        for (uint32_t j = 0; j < PRO_RC; j++) {
-            if (j0 + j < mine) {
-                const uint32_t e0 = (g + PRO_ROWS * (j0 + j)) * 256 + r * 16;
-                raw16(e0, xv[j]);
-                if (both) raw16b(e0, yv[j]);
-            }
-        }
-    };
-    // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
-    // scale = 1/sqrtf(mean + eps))
-    float gscale = 1.0f;
-    const bool one_round = nchunk <= PRO_ROWS * PRO_RC;
-    if (one_round) load_round(0, true);
-    if (rms) {
-        double s = 0.0;
-        for (uint32_t j0 = 0; j0 < mine; j0 += PRO_RC) {
-            if (!one_round) load_round(j0, false);
-#pragma unroll
-            for (uint32_t j = 0; j < PRO_RC; j++)
-                if (j0 + j < mine)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) s += (double)(xv[j][i] * xv[j][i]);
-        }
-        s = block_sum_f64(s, red);
-        const float mean = (float)(s / (double)K);
-        gscale = 1.0f / sqrtf(mean + a.eps);
-    }
     lds_char *q = (lds_char *)g_qbuf;
     LDS float *qd = reinterpret_cast<LDS float *>(q + (K / 256) * ACT_GSTRIDE);
     LDS int16_t *qb = reinterpret_cast<LDS int16_t *>(q + act_bs_off(K));
-    const bool has_y = gated || rms;
-    for (uint32_t j0 = 0; j0 < mine; j0 += PRO_RC) {
-        if (!one_round) load_round(j0, true);
-        const uint32_t cnt = min(PRO_RC, mine - j0);
-        // slot 0 is processed, then the slots shift down by one: the code of
-        // a chunk exists once (a loop body, fetched once per op) rather than
-        // once per slot -- straight-line code is fetched from L2 every time
 #pragma unroll 1
-        for (uint32_t j = 0; j < cnt; j++) {
-            if (j) {
+    for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
+        const uint32_t e0 = c * 256 + r * 16;
+        float v[16], y[16], t[16];
+        ld16(xs, e0, v);
+        if (a.pro != SINTER_PRO_PLAIN) ld16(ys, e0, y);
+        if (a.pro == SINTER_PRO_PLAIN) {
 #pragma unroll
-                for (uint32_t k = 0; k + 1 < PRO_RC; k++)
+            for (int i = 0; i < 16; i++) t[i] = v[i];
+        } else if (gated) {
+            // per-head sums of squares in double: heads of 4 or 8
+            // elements inside the lane, wider heads over gd/16 lanes
+            double s4[4];
 #pragma unroll
-                    for (int i = 0; i < 16; i++) xv[k][i] = xv[k + 1][i];
-                if (has_y)
+            for (int k = 0; k < 4; k++) {
+                double h = 0.0;
 #pragma unroll
-                    for (uint32_t k = 0; k + 1 < PRO_RC; k++)
-#pragma unroll
-                        for (int i = 0; i < 16; i++) yv[k][i] = yv[k + 1][i];
+                for (int i = 0; i < 4; i++) h += (double)(v[4 * k + i] * v[4 * k + i]);
+                s4[k] = h;
             }
-            const uint32_t c = g + PRO_ROWS * (j0 + j), e0 = c * 256 + r * 16;
-            const float *v = xv[0], *y = yv[0];
-            float t[16];
-            if (write_x)
+            const double s8a = s4[0] + s4[1], s8b = s4[2] + s4[3];
+            double s16 = s8a + s8b;
+            if (gd >= 32) s16 += dpp_d<DPP_XOR1>(s16);
+            if (gd >= 64) s16 += dpp_d<DPP_XOR2>(s16);
+            if (gd >= 128) s16 += dpp_d<DPP_HALF_MIRROR>(s16);
+            if (gd >= 256) s16 += dpp_d<DPP_MIRROR>(s16);
 #pragma unroll
-                for (int k = 0; k < 4; k++)
-                    st_coh4(a.x_out + e0 + 4 * k, make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]));
-            if (a.pro == SINTER_PRO_PLAIN) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) t[i] = v[i];
-            } else if (gated) {
-                // per-head sums of squares in double: heads of 4 or 8
-                // elements inside the lane, wider heads over gd/16 lanes
-                double s4[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    double h = 0.0;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) h += (double)(v[4 * k + i] * v[4 * k + i]);
-                    s4[k] = h;
-                }
-                const double s8a = s4[0] + s4[1], s8b = s4[2] + s4[3];
-                double s16 = s8a + s8b;
-                if (gd >= 32) s16 += dpp_d<DPP_XOR1>(s16);
-                if (gd >= 64) s16 += dpp_d<DPP_XOR2>(s16);
-                if (gd >= 128) s16 += dpp_d<DPP_HALF_MIRROR>(s16);
-                if (gd >= 256) s16 += dpp_d<DPP_MIRROR>(s16);
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const double hsum = gd == 4 ? s4[i / 4] : gd == 8 ? (i < 8 ? s8a : s8b) : s16;
-                    const float mean = (float)(hsum / (double)gd);
-                    const float hs = 1.0f / sqrtf(mean + a.eps);
-                    const float nrm = v[i] * hs;
-                    const float wn = nrm * gw[i];
-                    t[i] = wn * dev_silu(y[i]);
-                    if ((i & 3) == 3) sched_fence();   // bounds the live fp64 temporaries
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float nrm = v[i] * gscale;
-                    t[i] = nrm * y[i];
-                }
+            for (int i = 0; i < 16; i++) {
+                const double hsum = gd == 4 ? s4[i / 4] : gd == 8 ? (i < 8 ? s8a : s8b) : s16;
+                const float mean = (float)(hsum / (double)gd);
+                const float hs = 1.0f / sqrtf(mean + a.eps);
+                const float nrm = v[i] * hs;
+                const float wn = nrm * gw[i];
+                t[i] = wn * dev_silu(y[i]);
+                if ((i & 3) == 3) sched_fence();   // bounds the live fp64 temporaries
             }
-            quant16(vt, c, r, e0, t, q, qd, qb);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float nrm = v[i] * gscale;
+                t[i] = nrm * y[i];
+            }
         }
+        quant16(vt, c, r, e0, t, q, qd, qb);
     }
     __syncthreads();
 }
@@ -390,50 +389,17 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
 // for BF16 / F32.  An item's term is an fp64 expression of exact integer
 // block dots and the f16/f32 scales (a float sum of exact products for
 // BF16/F32).  A row is the ascending fp64 sum of its item terms, rounded to
-// fp32 once -- the fold oracle/oracle.c declares.
-//
-// Lanes per item: one for Q4_K / BF16 / F32; two for Q6_K (one 128-element
-// half each, integer partials added exactly) and Q8_0 (blocks 0-3 and 4-7;
-// the second lane continues the first lane's ascending block sum).  The term
-// ends up on the item's last lane.
-//
-// With one wave per SIMD nothing hides LDS latency, so each item function
-// issues all of its LDS reads first and only then computes (a scheduling
-// barrier keeps the compiler from interleaving loads into the arithmetic,
-// which would expose one LDS round trip per use).
+// fp32 once -- the fold oracle/oracle.c declares.  Each term function takes
+// the item's bytes from registers (one lane, one item) and the activation
+// from LDS; it issues all of its LDS reads before computing.
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
-__device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
-__device__ __forceinline__ uint16_t ld_u16(const lds_char *p) { return *reinterpret_cast<const LDS uint16_t *>(p); }
-
-// The N+1 aligned dwords covering N words at a 2-aligned LDS address, and
-// the byte shift that extracts them (unaligned LDS reads stall the LDS
-// pipeline on gfx950, so reads stay dword-aligned).
-template <int N>
-__device__ __forceinline__ uint32_t ld_span(const lds_char *p, uint32_t d[N + 1]) {
-    const uint32_t off = (uint32_t)(uintptr_t)p;
-    const LDS uint32_t *q = reinterpret_cast<const LDS uint32_t *>(p - (off & 3u));
-#pragma unroll
-    for (int i = 0; i <= N; i++) d[i] = q[i];
-    return off & 3u;
-}
-template <int N>
-__device__ __forceinline__ void span_words(const uint32_t d[N + 1], uint32_t sh, uint32_t w[N]) {
-#pragma unroll
-    for (int i = 0; i < N; i++) w[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
-}
-
-// Q4_K block (16-aligned in LDS) against Q8_K group g
-__device__ __forceinline__ double term_q4k(const lds_char *blk, const ActView &x, uint32_t g) {
-    u32x4 wv[9], xv[16], bsv[2];
-#pragma unroll
-    for (int i = 0; i < 9; i++) wv[i] = lds16(blk + 16 * i);
+// Q4_K block (144 B = 9 x 16 B) against Q8_K group g
+__device__ __forceinline__ double term_q4k(const u32x4 *wv, const ActView &x, uint32_t g) {
+    u32x4 xv[16], bsv[2];
     const lds_char *xq = x.q + g * ACT_GSTRIDE;
 #pragma unroll
     for (int i = 0; i < 16; i++) xv[i] = lds16(xq + 16 * i);
@@ -441,7 +407,6 @@ __device__ __forceinline__ double term_q4k(const lds_char *blk, const ActView &x
     bsv[0] = lds16(bsp);
     bsv[1] = lds16(bsp + 16);
     const float dxf = x.d[g];
-    sched_fence();
     const uint32_t sw[3] = {wv[0].y, wv[0].z, wv[0].w};   // scales[0..11]
     auto byte = [&](uint32_t i) -> int { return (int)((sw[i >> 2] >> (8 * (i & 3))) & 0xff); };
     auto bsum = [&](int j) -> int {                       // bsums[j], int16
@@ -480,98 +445,102 @@ __device__ __forceinline__ double term_q4k(const lds_char *blk, const ActView &x
     return (dw * dx) * (double)isum - (dm * dx) * (double)imin;
 }
 
-// Half n (elements [128n, 128n+128)) of a Q6_K block at a 2-aligned LDS
-// address against Q8_K group g: the exact integer sum over its 8 sub-blocks
-// of scale * (code dot x).  Codes are taken unsigned (0..63) and the -32
-// offset folds through the bsums: sum((c-32)*x) = sum(c*x) - 32*bsum.
-__device__ __forceinline__ int q6k_half(const lds_char *blk, const ActView &x, uint32_t g, uint32_t n) {
-    uint32_t dl[17], dh[9], ds[3];
-    const uint32_t shl = ld_span<16>(blk + 64 * n, dl);          // ql[64n .. 64n+64)
-    const uint32_t shh = ld_span<8>(blk + 128 + 32 * n, dh);     // qh[32n .. 32n+32)
-    const uint32_t shs = ld_span<2>(blk + 192 + 8 * n, ds);      // int8 scales[8n .. 8n+8)
-    const lds_char *xq = x.q + g * ACT_GSTRIDE + 128 * n;
-    u32x4 xv[8];
+// Q6_K block (210 B at byte `sh` (0 or 2) of a 212-byte window -- 53 dwords
+// -- read from a 4-aligned address) against Q8_K group g.  Codes are taken
+// unsigned (0..63) and the -32 offset folds through the bsums:
+// sum((c-32)*x) = sum(c*x) - 32*bsum; the block's integer sum is exact.
+__device__ __forceinline__ double term_q6k(const u32x4 *wv, uint32_t sh, const ActView &x, uint32_t g) {
+    const lds_char *xq = x.q + g * ACT_GSTRIDE;
+    u32x4 xv[16], bsv[2];
 #pragma unroll
-    for (int i = 0; i < 8; i++) xv[i] = lds16(xq + 16 * i);
-    const u32x4 bsv = lds16(reinterpret_cast<const lds_char *>(x.bs + g * 16 + 8 * n));
-    sched_fence();
-    uint32_t ql[16], qh[8], scw[2];
-    span_words<16>(dl, shl, ql);
-    span_words<8>(dh, shh, qh);
-    span_words<2>(ds, shs, scw);
-    uint32_t xw[32];
+    for (int i = 0; i < 16; i++) xv[i] = lds16(xq + 16 * i);
+    const lds_char *bsp = reinterpret_cast<const lds_char *>(x.bs + g * 16);
+    bsv[0] = lds16(bsp);
+    bsv[1] = lds16(bsp + 16);
+    const float dxf = x.d[g];
+    uint32_t d[53];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        xw[4 * i] = xv[i].x; xw[4 * i + 1] = xv[i].y; xw[4 * i + 2] = xv[i].z; xw[4 * i + 3] = xv[i].w;
-    }
-    int dot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // [quarter][16-element half]
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t qa = ql[i], qb = ql[8 + i];
-        const uint32_t c0 = (qa & 0x0F0F0F0Fu) | ((qh[i] << 4) & 0x30303030u);
-        const uint32_t c1 = (qb & 0x0F0F0F0Fu) | ((qh[i] << 2) & 0x30303030u);
-        const uint32_t c2 = ((qa >> 4) & 0x0F0F0F0Fu) | (qh[i] & 0x30303030u);
-        const uint32_t c3 = ((qb >> 4) & 0x0F0F0F0Fu) | ((qh[i] >> 2) & 0x30303030u);
-        const int hf = i >> 2;                     // l = 4i.. : half hf of each quarter
-        dot[0][hf] = sdot4(c0, xw[i], dot[0][hf]);
-        dot[1][hf] = sdot4(c1, xw[8 + i], dot[1][hf]);
-        dot[2][hf] = sdot4(c2, xw[16 + i], dot[2][hf]);
-        dot[3][hf] = sdot4(c3, xw[24 + i], dot[3][hf]);
-    }
+    for (int i = 0; i < 13; i++) { d[4 * i] = wv[i].x; d[4 * i + 1] = wv[i].y; d[4 * i + 2] = wv[i].z; d[4 * i + 3] = wv[i].w; }
+    d[52] = wv[13].x;
+    auto W = [&](int j) -> uint32_t { return __builtin_amdgcn_alignbyte(d[j + 1], d[j], sh); };
     int isum = 0;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+    for (int n = 0; n < 2; n++) {
+        uint32_t xw[32];
 #pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const int j = 2 * t + hf;              // 16-element sub-block within the half
-            const int sc = (int)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xff);
-            const uint32_t bw = bsv[j >> 1];
-            const int bs = (j & 1) ? ((int)bw >> 16) : (int)(int16_t)(bw & 0xffff);
-            isum += sc * (dot[t][hf] - 32 * bs);
+        for (int i = 0; i < 8; i++) {
+            const u32x4 t = xv[8 * n + i];
+            xw[4 * i] = t.x; xw[4 * i + 1] = t.y; xw[4 * i + 2] = t.z; xw[4 * i + 3] = t.w;
+        }
+        int dot[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // [quarter][16-element half]
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t qa = W(16 * n + i), qb = W(16 * n + 8 + i), qh = W(32 + 8 * n + i);
+            const uint32_t c0 = (qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+            const uint32_t c1 = (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+            const uint32_t c2 = ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+            const uint32_t c3 = ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+            const int hf = i >> 2;                     // l = 4i.. : half hf of each quarter
+            dot[0][hf] = sdot4(c0, xw[i], dot[0][hf]);
+            dot[1][hf] = sdot4(c1, xw[8 + i], dot[1][hf]);
+            dot[2][hf] = sdot4(c2, xw[16 + i], dot[2][hf]);
+            dot[3][hf] = sdot4(c3, xw[24 + i], dot[3][hf]);
+        }
+        const uint32_t scw[2] = {W(48 + 2 * n), W(49 + 2 * n)};
+        const u32x4 bs = bsv[n];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const int j = 2 * t + hf;              // 16-element sub-block within the half
+                const int sc = (int)(int8_t)((scw[j >> 2] >> (8 * (j & 3))) & 0xff);
+                const uint32_t bw = bs[j >> 1];
+                const int b = (j & 1) ? ((int)bw >> 16) : (int)(int16_t)(bw & 0xffff);
+                isum += sc * (dot[t][hf] - 32 * b);
+            }
         }
     }
-    return isum;
+    const uint16_t dh = (uint16_t)((sh ? d[52] >> 16 : d[52]) & 0xffff);   // block bytes 208..209
+    return ((double)h2f(dh) * (double)dxf) * (double)isum;
 }
 
-// Blocks 4h .. 4h+3 of an 8-block Q8_0 item (34-byte blocks, 2-aligned)
-// against Q8_0 activation blocks 8g+4h ..: the four block terms.
-__device__ __forceinline__ void q80_quad(const lds_char *item, const ActView &x, uint32_t g, uint32_t h, double t[4]) {
-    uint32_t dw[4][9], sh[4];
-    uint16_t dh[4];
-    u32x4 xv[8];
-    float dx[4];
+// Q8_0 item: eight 34-byte blocks (272 B = 17 x 16 B, 16-aligned) against
+// Q8_0 activation blocks 8g ..; the block terms summed in ascending order.
+__device__ __forceinline__ double term_q80(const u32x4 *wv, const ActView &x, uint32_t g) {
+    const lds_char *xq = x.q + g * ACT_GSTRIDE;
+    u32x4 xv[16];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t b = 4 * h + j;
-        const lds_char *bo = item + 34 * b;
-        sh[j] = ld_span<8>(bo + 2, dw[j]);
-        dh[j] = ld_u16(bo);
-        const lds_char *xq = x.q + g * ACT_GSTRIDE + 32 * b;
-        xv[2 * j] = lds16(xq);
-        xv[2 * j + 1] = lds16(xq + 16);
-        dx[j] = x.d[8 * g + b];
-    }
-    sched_fence();
+    for (int i = 0; i < 16; i++) xv[i] = lds16(xq + 16 * i);
+    float dx[8];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        uint32_t w[8];
-        span_words<8>(dw[j], sh[j], w);
-        const u32x4 x0 = xv[2 * j], x1 = xv[2 * j + 1];
-        const uint32_t xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    for (int j = 0; j < 8; j++) dx[j] = x.d[8 * g + j];
+    uint32_t d[68];
+#pragma unroll
+    for (int i = 0; i < 17; i++) { d[4 * i] = wv[i].x; d[4 * i + 1] = wv[i].y; d[4 * i + 2] = wv[i].z; d[4 * i + 3] = wv[i].w; }
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int b0 = 34 * j;                       // block start byte
+        const uint32_t dw16 = __builtin_amdgcn_alignbyte(d[b0 / 4 + 1], d[b0 / 4], b0 % 4) & 0xffff;
+        const int q0 = b0 + 2;                       // codes start byte
         int isum = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) isum = sdot4(w[i], xw[i], isum);
-        t[j] = ((double)h2f(dh[j]) * (double)dx[j]) * (double)isum;
+        for (int i = 0; i < 8; i++) {
+            const int bb = q0 + 4 * i;
+            const uint32_t w = (bb % 4) == 0 ? d[bb / 4] : __builtin_amdgcn_alignbyte(d[bb / 4 + 1], d[bb / 4], bb % 4);
+            isum = sdot4(w, xv[2 * j + i / 4][i % 4], isum);
+        }
+        acc += ((double)h2f((uint16_t)dw16) * (double)dx[j]) * (double)isum;
     }
+    return acc;
 }
 
-// 64 bf16 elements (128 B, 16-aligned), products exact in fp64, ascending
-__device__ __forceinline__ double term_bf16(const lds_char *blk, const ActView &x, uint32_t k) {
+// 64 bf16 elements (128 B = 8 x 16 B), products exact in fp64, ascending
+__device__ __forceinline__ double term_bf16(const u32x4 *av, const ActView &x, uint32_t k) {
     const lds_char *xx = x.q + k * ACT_BF_CSTRIDE;
-    u32x4 av[8], bv[8];
+    u32x4 bv[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) { av[i] = lds16(blk + 16 * i); bv[i] = lds16(xx + 16 * i); }
-    sched_fence();
+    for (int i = 0; i < 8; i++) bv[i] = lds16(xx + 16 * i);
     double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -585,33 +554,43 @@ __device__ __forceinline__ double term_bf16(const lds_char *blk, const ActView &
     return acc;
 }
 
-// 64 f32 elements (256 B, 16-aligned), products exact in fp64, ascending
-__device__ __forceinline__ double term_f32(const lds_char *blk, const ActView &x, uint32_t k) {
+// 64 f32 elements (256 B = 16 x 16 B), products exact in fp64, ascending
+__device__ __forceinline__ double term_f32(const u32x4 *av, const ActView &x, uint32_t k) {
     const lds_char *xx = x.q + k * ACT_F_CSTRIDE;
     double acc = 0.0;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        f32x4 av[8], bv[8];
+        f32x4 bv[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) { av[i] = ldsf16(blk + 128 * h + 16 * i); bv[i] = ldsf16(xx + 128 * h + 16 * i); }
-        sched_fence();
+        for (int i = 0; i < 8; i++) bv[i] = ldsf16(xx + 128 * h + 16 * i);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            acc += (double)av[i].x * (double)bv[i].x;
-            acc += (double)av[i].y * (double)bv[i].y;
-            acc += (double)av[i].z * (double)bv[i].z;
-            acc += (double)av[i].w * (double)bv[i].w;
+            const u32x4 a = av[8 * h + i];
+            acc += (double)__uint_as_float(a.x) * (double)bv[i].x;
+            acc += (double)__uint_as_float(a.y) * (double)bv[i].y;
+            acc += (double)__uint_as_float(a.z) * (double)bv[i].z;
+            acc += (double)__uint_as_float(a.w) * (double)bv[i].w;
         }
     }
     return acc;
 }
 
-// ------------------------------------------------------------ work split
+template <int T>
+__device__ __forceinline__ double item_term(const u32x4 *wv, uint32_t sh, const ActView &x, uint32_t k) {
+    if constexpr (T == SINTER_Q4_K) return term_q4k(wv, x, k);
+    else if constexpr (T == SINTER_Q6_K) return term_q6k(wv, sh, x, k);
+    else if constexpr (T == SINTER_Q8_0) return term_q80(wv, x, k);
+    else if constexpr (T == SINTER_BF16) return term_bf16(wv, x, k);
+    else return term_f32(wv, x, k);
+}
+
+// ------------------------------------------------------------ runs
 // The host compiles each GEMV into a GemvPlan (isa.h): per-segment constants,
-// the term ring geometry and the workgroups' row cuts.  The kernel reads it
+// the term ring geometry and the waves' row cuts.  The kernel reads it
 // through the constant address space, so every field is a scalar load.
 typedef const __attribute__((address_space(4))) GemvPlan cplan_t;
 typedef const __attribute__((address_space(4))) uint32_t cu32_t;
+#define GLB __attribute__((address_space(1)))
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -624,204 +603,183 @@ __device__ __forceinline__ uint32_t divm(uint32_t v, uint32_t d, uint32_t m, uin
     return q;
 }
 
-// The term ring: row-aligned.  The row of workgroup-local index lr owns
-// slot lr % R; its term k sits at slot*P + k (P = ipr rounded up to RING_PAD, the
-// pad slot holds -0.0, an exact no-op in the fold).  SwiGLU up terms use a
-// second ring of R*P behind the first.  Rows are folded once, complete, in
-// ascending k.  "Deferred" rings fold a tile's rows one tile later (no extra
-// barrier; R covers the rows of two tiles); otherwise the rows are folded
-// right after an extra barrier.
-struct Ring {
-    uint32_t ipr, mipr, P, R, mR, RP, defer;
+// A run: the rows of a wave's range that lie in one segment, streamed as one
+// flat sequence of items.  Plain: lane l takes items l, l+64, ...; SwiGLU
+// pair: even lanes take gate items l/2, l/2+32, ..., odd lanes the same up
+// items, so a step covers 32 items of each matrix and every lane holds one
+// item.  Item f of the run is item f + L of the segment (L = first item).
+struct Run {
+    uint32_t ok, s, type, swig;
+    uint32_t g0, g1, n;                 // global rows [g0, g1); n = items (per matrix)
+    uint64_t VA, VB;                    // address of the run's item 0 in matrix A, B
 };
 
-// ------------------------------------------------------------ tiles
-// A tile is a run of whole items of one segment: items [a, a+cnt) of its
-// matrix (and the same items of w2 for a SwiGLU pair), a contiguous byte
-// range of the row-major weights.  Tiles ignore row boundaries, so every lane
-// has an item; a row's terms may span tiles.  a = ra*ipr + ka.
-//
-// The DMA cursor walks the tiles of this workgroup in order and keeps the
-// current segment's constants in registers; consecutive tiles of a segment
-// differ by constants, so creating a tile is a handful of scalar operations.
-struct TD {                 // what compute and fold need of a tile
-    uint32_t ok, a, cnt, ra, ka;
-    uint32_t type, swig, lr0;           // weight type, SwiGLU pair, workgroup-local index of row ra
-    uint32_t skew_a, base_b;            // LDS byte offsets of matrix A's and B's first item
-};
-struct Cursor {
-    uint32_t ok, seg, a, ra, ka;        // next tile to create
-    uint32_t end, T, qT, rT, ib, type, swig, lrb;   // current segment
-    uintptr_t wa, wb;                   // weights of the current segment
-    uint32_t n_seg, ipr, row_lo, row_hi;            // the op: this workgroup's global rows
-    cplan_t *pl;
-};
+__device__ __forceinline__ bool epi_loads(uint32_t epi) { return epi == SINTER_EPI_RESID || epi == SINTER_EPI_CONV; }
 
-// Move the cursor to the first segment >= s with rows in [row_lo, row_hi).
-__device__ __forceinline__ void cur_seg(Cursor &c, uint32_t s) {
-    c.ok = 0;
-    for (; s < c.n_seg; s++) {
-        const uint32_t base = c.pl->seg[s].base, rows = c.pl->seg[s].rows;
-        const uint32_t lo = min(max(c.row_lo, base), base + rows) - base;
-        const uint32_t hi = min(max(c.row_hi, base), base + rows) - base;
-        if (lo < hi) {
-            c.ok = 1; c.seg = s; c.a = lo * c.ipr; c.ra = lo; c.ka = 0;
-            c.end = hi * c.ipr; c.T = c.pl->seg[s].T; c.qT = c.pl->seg[s].qT; c.rT = c.pl->seg[s].rT;
-            c.ib = c.pl->seg[s].ib; c.type = c.pl->seg[s].type; c.swig = c.pl->seg[s].swig; c.lrb = base - c.row_lo;
-            c.wa = (uintptr_t)c.pl->seg[s].wa;
-            c.wb = (uintptr_t)c.pl->seg[s].wb;
-            return;
-        }
+// The run of rows [lo, hi) in the first segment >= s holding any of them
+// (at most min(64, R) rows for an operand-reading epilogue).
+__device__ __forceinline__ Run make_run(cplan_t *pl, uint32_t s, uint32_t lo, uint32_t hi) {
+    Run r;
+    r.ok = 0; r.s = 0; r.type = 0; r.swig = 0; r.g0 = lo; r.g1 = lo; r.n = 0; r.VA = 0; r.VB = 0;
+    const uint32_t nseg = pl->n_seg;
+    for (; s < nseg; s++) {
+        const uint32_t base = pl->seg[s].base, rows = pl->seg[s].rows;
+        if (max(lo, base) < min(hi, base + rows)) break;
     }
+    if (s >= nseg) return r;
+    const uint32_t base = pl->seg[s].base, rows = pl->seg[s].rows, ib = pl->seg[s].ib, ipr = pl->ipr;
+    r.ok = 1; r.s = s; r.type = pl->seg[s].type; r.swig = pl->seg[s].swig;
+    r.g0 = max(lo, base);
+    r.g1 = min(hi, base + rows);
+    if (epi_loads(pl->seg[s].epi)) r.g1 = min(r.g1, r.g0 + min(64u, pl->R));
+    r.n = (r.g1 - r.g0) * ipr;
+    const uint64_t off = (uint64_t)(r.g0 - base) * ipr * ib;
+    r.VA = pl->seg[s].wa + off;
+    r.VB = pl->seg[s].wb + off;
+    return r;
 }
 
-// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at base + voff land at
-// lds_base + 16*l.  Issued from inline asm so the compiler does not treat the
-// pending DMA as aliasing every later LDS read (it would insert vmcnt(0)
-// before them and serialise the pipeline); the tile loop below waits for it
-// explicitly.  M0 (the LDS base of the DMA) is restored before the asm ends;
-// one wait state separates the M0 write from the DMA that reads it.
-// Weights are read once per pass, so the load is non-temporal (nt): streamed
-// through L2 without displacing the lines that are reused (the kernel's own
-// code, which every instruction-cache miss refetches from L2, and the
-// activations).
-__device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %2, %3 nt\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds_base), "v"(voff), "s"(base)
-        : "memory");
+// ------------------------------------------------------------ streaming
+
+// Registers of the weight items in flight: D slots of NI 16-byte loads per
+// lane.  Before the prologue (across the grid barrier) only the first DPRE
+// slots are loaded -- at most PF_PRE registers of 16 B stay live through
+// it.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
+// 4-aligned address at or below it: every byte read lies in
+// [block - 2, block + 210), never past the end of the weights.
+constexpr int PF_MAX = 36, PF_PRE = 28;
+template <int T> struct TypeCfg;
+template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 3, DPRE = 3; };
+template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 2, DPRE = 2; };
+template <> struct TypeCfg<SINTER_Q8_0> { static constexpr int NI = 17, IB = 272, D = 2, DPRE = 1; };
+template <> struct TypeCfg<SINTER_BF16> { static constexpr int NI = 8, IB = 128, D = 4, DPRE = 3; };
+template <> struct TypeCfg<SINTER_F32> { static constexpr int NI = 16, IB = 256, D = 2, DPRE = 1; };
+
+// Weight loads use the default cache policy: a lane's item spans several
+// 16-byte loads whose cache lines the other loads of the same step share,
+// so the lines must stay in L1/L2 until all of them have read (measured: a
+// non-temporal policy re-fetches them and halves the streaming rate).
+__device__ __forceinline__ u32x4 ldw16(uint64_t p) { return *reinterpret_cast<const GLB u32x4 *>(p); }
+__device__ __forceinline__ uint32_t ldw4(uint64_t p) { return *reinterpret_cast<const GLB uint32_t *>(p); }
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u32x4 ldw16a4(uint64_t p) {
+    const u32x4a4 v = *reinterpret_cast<const GLB u32x4a4 *>(p);
+    u32x4 o = {v.x, v.y, v.z, v.w};
+    return o;
 }
 
-// Create the tile at the cursor, LDS-DMA it into a 36 KiB buffer and advance
-// the cursor.  Every wave issues exactly TILE_CPW 1-KiB chunks, so the number
-// of outstanding loads per wave is a compile-time constant and the tile waits
-// can be partial.  Matrix A fills the first chunks; a SwiGLU matrix B starts
-// at the next 1 KiB chunk boundary, so every chunk reads from one matrix;
-// lanes past a matrix's end re-read its last 16 bytes into the unused tail.
-__device__ __forceinline__ TD tile_next(Cursor &c, char *buf) {
-    TD t;
-    t.ok = c.ok;
-    t.a = 0; t.cnt = 0; t.ra = 0; t.ka = 0; t.type = 0; t.swig = 0; t.lr0 = 0; t.skew_a = 0; t.base_b = 0;
-    if (!c.ok) return t;
-    t.a = c.a; t.ra = c.ra; t.ka = c.ka;
-    t.cnt = min(c.T, c.end - c.a);
-    t.type = c.type; t.swig = c.swig; t.lr0 = c.lrb + c.ra;
-    const uint32_t bytes = t.cnt * c.ib;
-    const uintptr_t A = c.wa + (uintptr_t)c.a * c.ib;
-    t.skew_a = (uint32_t)(A & 15);
-    const uintptr_t sa = A & ~(uintptr_t)15;
-    const uint32_t last_a = ((t.skew_a + bytes - 1) >> 4) << 4;       // offset of A's last 16 B
-    const uint32_t chunks_a = (t.skew_a + bytes + 1023) >> 10;
-    uintptr_t sb = sa;
-    uint32_t last_b = last_a;
-    if (c.swig) {
-        const uintptr_t B = c.wb + (uintptr_t)c.a * c.ib;
-        sb = B & ~(uintptr_t)15;
-        const uint32_t skew_b = (uint32_t)(B & 15);
-        t.base_b = chunks_a * 1024 + skew_b;
-        last_b = ((skew_b + bytes - 1) >> 4) << 4;
-    }
-    const uint32_t w = uni(wave_id()), lane16 = lane_id() * 16;
-    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void *)buf;
-    if (!c.swig) {
-        // one matrix: chunk j of the tile is bytes [1024 j, 1024 j + 1024)
+// the lane's matrix (SwiGLU pair: odd lanes read B) and its item within a step
+__device__ __forceinline__ uint32_t lane_item(bool swig) { return swig ? (uint32_t)lane_id() >> 1 : (uint32_t)lane_id(); }
+
+// Load item f of the run into slot S.  Every step loads unconditionally, so
+// the compiler counts the loads in flight exactly and waits for a slot with
+// a partial vmcnt (a load that might be skipped makes it wait for all of
+// them): lanes past the run's end read the same bytes of `dummy` (the op's
+// plan in device memory, L2-resident) instead.
+template <int T, int S>
+__device__ __forceinline__ void issue_item(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint32_t f,
+                                           uint64_t dummy) {
+    constexpr int NI = TypeCfg<T>::NI, IB = TypeCfg<T>::IB;
+    static_assert((S + 1) * NI <= PF_MAX, "prefetch slots");
+    uint64_t A = ((r.swig && (lane_id() & 1)) ? r.VB : r.VA) + (uint64_t)f * IB;
+    A = f < r.n ? A : dummy;
+    if constexpr (T == SINTER_Q6_K) {
+        sh[S] = (uint32_t)A & 3u;
+        A &= ~(uint64_t)3;
 #pragma unroll
-        for (uint32_t k = 0; k < TILE_CPW; k++) {
-            const uint32_t j = w + 4 * k;
-            lds_dma16(sa, min(j * 1024 + lane16, last_a), lbase + j * 1024);
-        }
+        for (int i = 0; i < NI - 1; i++) pf[S * NI + i] = ldw16a4(A + 16 * i);
+        pf[S * NI + NI - 1].x = ldw4(A + 16 * (NI - 1));
     } else {
 #pragma unroll
-        for (uint32_t k = 0; k < TILE_CPW; k++) {
-            const uint32_t j = w + 4 * k;
-            const bool in_a = j < chunks_a;
-            const uintptr_t src = in_a ? sa : sb;
-            const uint32_t j0 = in_a ? j : j - chunks_a;
-            const uint32_t voff = min(j0 * 1024 + lane16, in_a ? last_a : last_b);
-            lds_dma16(src, voff, lbase + j * 1024);
+        for (int i = 0; i < NI; i++) pf[S * NI + i] = ldw16(A + 16 * i);
+    }
+}
+
+// Load slots [S0, S1) of the run's first steps.
+template <int T, int S0, int S1>
+__device__ __forceinline__ void issue_slots(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
+    const uint32_t si = r.swig ? 32u : 64u, f0 = lane_item(r.swig != 0);
+    if constexpr (S0 <= 0 && 0 < S1) issue_item<T, 0>(pf, sh, r, f0, dummy);
+    if constexpr (S0 <= 1 && 1 < S1) issue_item<T, 1>(pf, sh, r, f0 + si, dummy);
+    if constexpr (S0 <= 2 && 2 < S1) issue_item<T, 2>(pf, sh, r, f0 + 2 * si, dummy);
+    if constexpr (S0 <= 3 && 3 < S1) issue_item<T, 3>(pf, sh, r, f0 + 3 * si, dummy);
+}
+
+// The slots loaded before the prologue (dispatch on the run's type).
+__device__ __forceinline__ void issue_pre(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
+    if (!r.ok) return;
+    switch (r.type) {
+    case SINTER_Q4_K: issue_slots<SINTER_Q4_K, 0, TypeCfg<SINTER_Q4_K>::DPRE>(pf, sh, r, dummy); break;
+    case SINTER_Q6_K: issue_slots<SINTER_Q6_K, 0, TypeCfg<SINTER_Q6_K>::DPRE>(pf, sh, r, dummy); break;
+    case SINTER_Q8_0: issue_slots<SINTER_Q8_0, 0, TypeCfg<SINTER_Q8_0>::DPRE>(pf, sh, r, dummy); break;
+    case SINTER_BF16: issue_slots<SINTER_BF16, 0, TypeCfg<SINTER_BF16>::DPRE>(pf, sh, r, dummy); break;
+    default: issue_slots<SINTER_F32, 0, TypeCfg<SINTER_F32>::DPRE>(pf, sh, r, dummy); break;
+    }
+}
+
+// Epilogues that read operands (residual add, conv) run only in the fold at
+// the end of a run, whose rows are capped at 64 (longer ranges are split into
+// runs): row q's operands are loaded into lane q right after the grid
+// barrier, so they queue behind the weights loaded before it and have landed
+// when the prologue's DMA wait returns -- a load inside the streaming loop
+// would wait for every weight load in flight (vmcnt counts in order).
+// RESID: v[0] = residual; CONV (dc <= 4 taps): v[0..dc-2] = state,
+// v[3..3+dc) = conv weights.
+struct EpiPre {
+    float v[7];
+};
+__device__ __forceinline__ void epi_preload(cplan_t *pl, const Run &r, EpiPre &ev) {
+#pragma unroll
+    for (int j = 0; j < 7; j++) ev.v[j] = 0.0f;
+    if (!r.ok) return;
+    const uint32_t epi = pl->seg[r.s].epi, q = lane_id(), row = r.g0 + q - pl->seg[r.s].base;
+    if (q >= r.g1 - r.g0) return;
+    if (epi == SINTER_EPI_RESID) {
+        const __amdgpu_buffer_rsrc_t ar = coh_rsrc(reinterpret_cast<const void *>(pl->seg[r.s].aux), 0x7fffffff);
+        ev.v[0] = ld_coh4b(ar, row * 4);
+    } else if (epi == SINTER_EPI_CONV) {
+        const uint32_t dc = pl->seg[r.s].dconv;
+        const GLB float *st = reinterpret_cast<const GLB float *>(pl->seg[r.s].aux) + (size_t)row * (dc - 1);
+        const GLB float *cw = reinterpret_cast<const GLB float *>(pl->seg[r.s].w2) + (size_t)row * dc;
+#pragma unroll
+        for (uint32_t j = 0; j < 3; j++) if (j + 1 < dc) ev.v[j] = st[j];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) if (j < dc) ev.v[3 + j] = cw[j];
+    }
+}
+
+// Row epilogue of segment row r (segment s of the plan): dot (and the up dot
+// of a SwiGLU pair); greedy-argmax candidates fold into (bv, bi).  FULL: the
+// end-of-run fold (every mode; RESID/CONV use this lane's preloaded
+// operands); otherwise the in-loop fold (STORE / SWIGLU / ARGMAX only).
+template <bool FULL>
+__device__ __forceinline__ void epi_row(cplan_t *pl, uint32_t s, __amdgpu_buffer_rsrc_t yr, uint32_t r, float dot,
+                                        float up, float &bv, int32_t &bi, const EpiPre &ev) {
+    float y = dot;
+    const uint32_t epi = pl->seg[s].epi;
+    if (epi == SINTER_EPI_SWIGLU) {
+        y = dev_silu(dot) * up;
+    } else if (FULL && epi == SINTER_EPI_RESID) {
+        y = ev.v[0] + dot;
+    } else if (FULL && epi == SINTER_EPI_CONV) {
+        // causal conv over {state[0..dc-2], dot}, fp64 sum rounded once,
+        // then silu; the state shifts by one tap (this wave owns row r)
+        const uint32_t dc = pl->seg[s].dconv;
+        GLB float *st = reinterpret_cast<GLB float *>(pl->seg[s].aux) + (size_t)r * (dc - 1);
+        double cacc = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const float wv = (j + 1 < dc) ? ev.v[j < 3 ? j : 2] : dot;
+            if (j < dc) cacc += (double)wv * (double)ev.v[3 + j];
         }
+        y = dev_silu((float)cacc);
+#pragma unroll
+        for (uint32_t j = 0; j < 3; j++)
+            if (j + 1 < dc) st[j] = (j + 2 < dc) ? ev.v[j + 1 < 3 ? j + 1 : 2] : dot;
+    } else if (epi == SINTER_EPI_ARGMAX) {
+        if (y > bv || (y == bv && (int32_t)r < bi)) { bv = y; bi = (int32_t)r; }
     }
-    // advance
-    c.a += t.cnt;
-    if (c.a >= c.end) {
-        cur_seg(c, c.seg + 1);
-    } else {
-        c.ra += c.qT;
-        c.ka += c.rT;
-        if (c.ka >= c.ipr) { c.ka -= c.ipr; c.ra += 1; }
-    }
-    return t;
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// Item terms of a landed tile into the term ring.
-template <int TYPE>
-__device__ __forceinline__ void tile_terms_t(const TD &t, const lds_char *buf, LDS double *ring, bool swig,
-                                             const Ring &rg, const ActView &x) {
-    constexpr uint32_t LPI = (TYPE == SINTER_Q6_K || TYPE == SINTER_Q8_0) ? 2u : 1u;
-    constexpr uint32_t IB = TYPE == SINTER_Q4_K ? 144u : TYPE == SINTER_Q6_K ? 210u : TYPE == SINTER_Q8_0 ? 272u
-                          : TYPE == SINTER_BF16 ? 128u : 256u;
-    const uint32_t l = threadIdx.x;
-    const uint32_t m = swig ? (l >> 7) : 0u;
-    const uint32_t ll = swig ? (l & 127u) : l;
-    const uint32_t u = ll / LPI, part = ll % LPI;
-    if (u < t.cnt) {   // the lanes of one item are active together
-        uint32_t k, slot;
-        const uint32_t q = divm(t.ka + u, rg.ipr, rg.mipr, k);
-        (void)divm(t.lr0 + q, rg.R, rg.mR, slot);
-        const lds_char *blk = buf + (m ? t.base_b : t.skew_a) + u * IB;
-        double term;
-        if constexpr (TYPE == SINTER_Q4_K) {
-            term = term_q4k(blk, x, k);
-        } else if constexpr (TYPE == SINTER_Q6_K) {
-            const uint16_t dh = ld_u16(blk + 208);
-            const float dxf = x.d[k];
-            int is = q6k_half(blk, x, k, part);
-            is += __shfl_xor(is, 1, 64);
-            term = ((double)h2f(dh) * (double)dxf) * (double)is;
-        } else if constexpr (TYPE == SINTER_Q8_0) {
-            double tt[4];
-            q80_quad(blk, x, k, part, tt);
-            const double lo4 = (((0.0 + tt[0]) + tt[1]) + tt[2]) + tt[3];   // blocks 0-3 (part 0)
-            const double prev = __shfl_xor(lo4, 1, 64);
-            term = (((prev + tt[0]) + tt[1]) + tt[2]) + tt[3];             // blocks 4-7 continue it (part 1)
-        } else if constexpr (TYPE == SINTER_BF16) {
-            term = term_bf16(blk, x, k);
-        } else {
-            term = term_f32(blk, x, k);
-        }
-        if (part == LPI - 1) ring[m * rg.RP + slot * rg.P + k] = term;
-    }
-}
-
-__device__ __forceinline__ void tile_terms(const TD &t, const char *bufg, const Ring &rg, const ActView &x) {
-    const bool swig = t.swig != 0;
-    const lds_char *buf = (const lds_char *)bufg;
-    LDS double *ring = (LDS double *)g_cb;
-    switch (t.type) {
-    case SINTER_Q4_K: tile_terms_t<SINTER_Q4_K>(t, buf, ring, swig, rg, x); break;
-    case SINTER_Q6_K: tile_terms_t<SINTER_Q6_K>(t, buf, ring, swig, rg, x); break;
-    case SINTER_Q8_0: tile_terms_t<SINTER_Q8_0>(t, buf, ring, swig, rg, x); break;
-    case SINTER_BF16: tile_terms_t<SINTER_BF16>(t, buf, ring, swig, rg, x); break;
-    default: tile_terms_t<SINTER_F32>(t, buf, ring, swig, rg, x); break;
-    }
-}
-
-// workgroup-local rows completed once this tile is computed
-__device__ __forceinline__ uint32_t td_done_after(const TD &t, const Ring &rg) {
-    uint32_t r;
-    return t.lr0 + divm(t.ka + t.cnt, rg.ipr, rg.mipr, r);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), yr, r * 4, 0, CPOL_SC1);
 }
 
 // One row's P ring terms summed in ascending order (fp64); pad terms are
@@ -882,189 +840,191 @@ __device__ __forceinline__ double fold_row(const LDS double *g, uint32_t P) {
     return s;
 }
 
-// Fold the rows this tile completed: rows [t.lr0, done_after).  The row of
-// workgroup-local index lr is folded by lane ((lr%4)<<6) | ((lr/4)%64) and
-// rounded to fp32 into g_res.
-__device__ __forceinline__ void tile_fold(const TD &t, const Ring &rg, uint32_t res_row0) {
-    const LDS double *ring = (const LDS double *)g_cb;
-    LDS float *res = (LDS float *)g_res;
-    const uint32_t nf = td_done_after(t, rg) - t.lr0;
-    const uint32_t l = threadIdx.x;
-    const uint32_t c = ((l & 63u) << 2) | (l >> 6);
-    const uint32_t d = (c - t.lr0) & 255u;
-    if (d < nf) {
-        const uint32_t lr = t.lr0 + d;
-        uint32_t slot;
-        (void)divm(lr, rg.R, rg.mR, slot);
-        const uint32_t i = lr - res_row0;
-        res[2 * i] = (float)fold_row(ring + slot * rg.P, rg.P);
-        if (t.swig) res[2 * i + 1] = (float)fold_row(ring + rg.RP + slot * rg.P, rg.P);
+// What the streaming loop keeps of the op (wave-uniform).
+struct GemvCtx {
+    uint32_t ipr, mipr, P, R, mR;
+    uint32_t qs, rs, qs2, rs2;          // a 64-item step (32 for SwiGLU pairs) in rows + items
+    LDS double *ring;                   // this wave's ring (A); B = ring + RING_CAP/2
+    uint64_t dummy;                     // readable device bytes for loads past a run's end
+};
+
+// Fold the run's rows [lo, hi) (run-local) -- row q on lane q % 64 -- and
+// apply the epilogues.
+template <bool FULL>
+__device__ __forceinline__ void fold_rows(const GemvCtx &c, cplan_t *pl, const Run &r, uint32_t lo, uint32_t hi,
+                                          float &bv, int32_t &bi, const EpiPre &ev) {
+    const uint32_t lane = lane_id();
+    const bool swig = r.swig != 0;
+    const uint32_t seg_base = pl->seg[r.s].base;
+    const __amdgpu_buffer_rsrc_t yr = coh_rsrc(reinterpret_cast<const void *>(pl->seg[r.s].y), 0x7fffffff);
+    for (uint32_t b = lo & ~63u; b < hi; b += 64) {
+        const uint32_t q = b + lane;
+        if (q >= lo && q < hi) {
+            uint32_t slot;
+            (void)divm(q, c.R, c.mR, slot);
+            const double s = fold_row(c.ring + slot * c.P, c.P);
+            double u = 0.0;
+            if (swig) u = fold_row(c.ring + RING_CAP / 2 + slot * c.P, c.P);
+            epi_row<FULL>(pl, r.s, yr, r.g0 + q - seg_base, (float)s, (float)u, bv, bi, ev);
+        }
+    }
+}
+
+// The body of one run whose first DPRE slots were loaded: the remaining
+// slots, then steps of terms into the ring, rows folded as the ring fills.
+template <int T>
+__device__ __forceinline__ void run_body(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const GemvCtx &c, cplan_t *pl,
+                                         const Run &r, const ActView &x, float &bv, int32_t &bi, const EpiPre &ev) {
+    constexpr int D = TypeCfg<T>::D, NI = TypeCfg<T>::NI;
+    issue_slots<T, TypeCfg<T>::DPRE, D>(pf, sh, r, c.dummy);
+    const bool swig = r.swig != 0;
+    const uint32_t si = swig ? 32u : 64u, qs = swig ? c.qs2 : c.qs, rs = swig ? c.rs2 : c.rs;
+    const uint32_t n = r.n, nJ = (n + si - 1) / si, nrows = r.g1 - r.g0;
+    // lane state: item f = si*j + lane_item is item k of run-local row q (ring slot)
+    const uint32_t f0 = lane_item(swig);
+    uint32_t k, q = divm(f0, c.ipr, c.mipr, k), slot;
+    (void)divm(q, c.R, c.mR, slot);
+    uint32_t folded = 0;
+    LDS double *ring = c.ring + ((swig && (lane_id() & 1)) ? RING_CAP / 2 : 0u);
+    // every step computes (lanes past the end masked) and loads D steps
+    // ahead (past the end: the dummy), whole groups of D steps
+    auto step = [&](auto Sc, uint32_t j) {
+        constexpr int S = decltype(Sc)::value;
+        const uint32_t f = si * j + f0;
+        if (f < n) ring[slot * c.P + k] = item_term<T>(&pf[S * NI], sh[S], x, k);
+        // this lane's next item
+        k += rs;
+        q += qs;
+        slot += qs;
+        if (k >= c.ipr) { k -= c.ipr; q += 1; slot += 1; }
+        if (slot >= c.R) slot -= c.R;
+        issue_item<T, S>(pf, sh, r, f + si * D, c.dummy);
+    };
+    for (uint32_t j0 = 0; j0 < nJ; j0 += D) {
+        // ring room for rows [folded, last row of this group of D steps]
+        // (runs with operand-reading epilogues have at most R rows, so this
+        // never fires for them)
+        uint32_t rem;
+        const uint32_t last = divm(min(n, si * (j0 + D)) - 1, c.ipr, c.mipr, rem);
+        if (last - folded + 1 > c.R) {
+            const uint32_t first = divm(si * j0, c.ipr, c.mipr, rem);
+            fold_rows<false>(c, pl, r, folded, first, bv, bi, ev);
+            folded = first;
+        }
+        step(std::integral_constant<int, 0>{}, j0);
+        if constexpr (D > 1) step(std::integral_constant<int, 1>{}, j0 + 1);
+        if constexpr (D > 2) step(std::integral_constant<int, 2>{}, j0 + 2);
+        if constexpr (D > 3) step(std::integral_constant<int, 3>{}, j0 + 3);
+    }
+    fold_rows<true>(c, pl, r, folded, nrows, bv, bi, ev);
+}
+
+__device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const GemvCtx &c, cplan_t *pl,
+                                             const Run &r, const ActView &x, float &bv, int32_t &bi,
+                                             const EpiPre &ev) {
+    switch (r.type) {
+    case SINTER_Q4_K: run_body<SINTER_Q4_K>(pf, sh, c, pl, r, x, bv, bi, ev); break;
+    case SINTER_Q6_K: run_body<SINTER_Q6_K>(pf, sh, c, pl, r, x, bv, bi, ev); break;
+    case SINTER_Q8_0: run_body<SINTER_Q8_0>(pf, sh, c, pl, r, x, bv, bi, ev); break;
+    case SINTER_BF16: run_body<SINTER_BF16>(pf, sh, c, pl, r, x, bv, bi, ev); break;
+    default: run_body<SINTER_F32>(pf, sh, c, pl, r, x, bv, bi, ev); break;
     }
 }
 
 // ------------------------------------------------------------ the op
 
-// Apply the epilogues to the buffered rows [row0, row0 + n) and store them;
-// greedy-argmax candidates fold into (bv, bi).  All threads.
-__device__ __forceinline__ void gemv_flush(const sinter_gemv_args &a, uint32_t row0, uint32_t n, float &bv, int32_t &bi) {
-    for (uint32_t i = threadIdx.x; i < n; i += BLOCK_THREADS) {
-        const uint32_t grow = row0 + i;
-        uint32_t s = 0, base = 0;
-        while (s + 1 < a.n_seg && grow >= base + a.seg[s].rows) { base += a.seg[s].rows; s++; }
-        const sinter_gemv_seg &sg = a.seg[s];
-        const uint32_t r = grow - base;
-        const float dot = g_res[2 * i];
-        float y = dot;
-        if (sg.epi == SINTER_EPI_SWIGLU) {
-            y = dev_silu(dot) * g_res[2 * i + 1];
-        } else if (sg.epi == SINTER_EPI_RESID) {
-            y = ld_coh(sg.aux + r) + dot;
-        } else if (sg.epi == SINTER_EPI_CONV) {
-            // causal conv over {state[0..dc-2], dot}, fp64 sum rounded once,
-            // then silu; the state shifts by one tap (this block owns row r)
-            const uint32_t dc = sg.dconv;
-            float *st = sg.aux + (size_t)r * (dc - 1);
-            const float *cw = static_cast<const float *>(sg.w2) + (size_t)r * dc;
-            float win[8];
-#pragma unroll
-            for (uint32_t j = 0; j < 8; j++) win[j] = (j + 1 < dc) ? st[j] : 0.0f;
-            double cacc = 0.0;
-#pragma unroll
-            for (uint32_t j = 0; j < 8; j++) {
-                const float wv = (j + 1 < dc) ? win[j] : (j + 1 == dc ? dot : 0.0f);
-                if (j < dc) cacc += (double)wv * (double)cw[j];
-            }
-            y = dev_silu((float)cacc);
-#pragma unroll
-            for (uint32_t j = 0; j < 7; j++)
-                if (j + 1 < dc) st[j] = (j + 2 < dc) ? win[j + 1] : dot;
-        } else if (sg.epi == SINTER_EPI_ARGMAX) {
-            if (y > bv || (y == bv && (int32_t)r < bi)) { bv = y; bi = (int32_t)r; }
-        }
-        st_coh(sg.y + r, y);
-    }
-}
-
-// What gemv_begin leaves for gemv_run (wave-uniform registers): the op can
-// be begun before the grid barrier that precedes it -- its weights do not
-// depend on the barrier -- so the first two tiles stream in while the
-// workgroup waits.
-struct GemvState {
-    uint32_t ok, row_lo;
-    Ring rg;
-    Cursor cur;
-    TD X, Y;
+// The grid barrier the op may be fused with (interp.hip): crossed after the
+// first weight slots are issued.  arrive/wait are the interpreter's.
+struct GridCross {
+    unsigned *bar, *groups, *err;
+    unsigned *epoch;
+    uint64_t spin_limit;
+    bool pass_end;              // sample the error cell after the wait
+    long long *pass_slot;       // record (wall clock - t0) after the wait (block 0), or null
+    uint64_t t0;
+    uint64_t t_wait_end;        // out: wall clock after the wait (block 0 timing)
 };
 
-// Copy the payload to LDS, read the plan, clear the term ring and LDS-DMA the
-// first two tiles.  Uses LDS (the GEMV buffers) only, so it may run as soon
-// as the previous op of the pass has returned.
-__device__ __forceinline__ void gemv_begin(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
-                                           unsigned *err, GemvState &st) {
+// Returns false when the kernel must stop (barrier timeout, or an error seen
+// at a pass end).
+// ts (thread 0, or null): wall clock stamps [1] after the barrier wait,
+// [2] after the prologue.
+__device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
+                                       unsigned *err, GridCross *gx, uint64_t *ts) {
     if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
         reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
-    // every ring slot starts as -0.0 (pad slots keep it)
-    for (uint32_t i = threadIdx.x; i < CB_CAP; i += BLOCK_THREADS) g_cb[i] = -0.0;
     cplan_t *pl = (cplan_t *)plan;
     cu32_t *cu = (cu32_t *)cuts;
-    const uint32_t rel = uni(blockIdx.x - ins.block_lo);
-    st.ok = pl->ok;
-    if (!st.ok) {
-        if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
-        __syncthreads();
-        return;
-    }
-    st.rg.ipr = pl->ipr; st.rg.mipr = pl->mipr; st.rg.P = pl->P; st.rg.R = pl->R;
-    st.rg.mR = pl->mR; st.rg.RP = pl->RP; st.rg.defer = pl->defer;
-    Cursor &c = st.cur;
-    c.pl = pl;
-    c.n_seg = pl->n_seg;
-    c.ipr = pl->ipr;
-    c.row_lo = cu[rel];
-    c.row_hi = cu[rel + 1];
-    st.row_lo = c.row_lo;
-    cur_seg(c, 0);
-    st.X = tile_next(c, g_tiles);
-    st.Y = tile_next(c, g_tiles + TILE_BYTES);
-    __syncthreads();
-}
-
-// The rest of the op: prologue, tile pipeline, epilogues.
-__device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err, GemvState &st) {
-    if (!st.ok) return;
-    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
     const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
+    const bool ok = pl->ok != 0;
+    const uint32_t wv = rel * WAVES + uni(wave_id());
+    const uint32_t row_lo = ok ? cu[wv] : 0u, row_hi = ok ? cu[wv + 1] : 0u;
+    Run run = make_run(pl, 0, row_lo, row_hi);
+    u32x4 pf[PF_MAX];
+    uint32_t sh[4] = {0, 0, 0, 0};
+    if (gx) {
+        grid_arrive(gx->bar, gx->groups, *gx->epoch);   // publishes g_args too
+        issue_pre(pf, sh, run, (uint64_t)plan);
+        const bool crossed = grid_wait(gx->bar, *gx->epoch, gx->spin_limit, gx->err);
+        gx->t_wait_end = wall_clock64();
+        if (!crossed) { settle_vmem(); return false; }
+        if (gx->pass_end) {
+            __shared__ unsigned e;
+            if (threadIdx.x == 0) {
+                e = __hip_atomic_load(gx->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (gx->pass_slot) *gx->pass_slot = (long long)(gx->t_wait_end - gx->t0);
+            }
+            __syncthreads();
+            if (e) { settle_vmem(); return false; }
+        }
+    } else {
+        issue_pre(pf, sh, run, (uint64_t)plan);
+        __syncthreads();
+    }
+    if (ts) ts[1] = wall_clock64();
+    EpiPre ev;
+    epi_preload(pl, run, ev);
+    if (!ok) {
+        if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
+        settle_vmem();
+        __syncthreads();
+        return true;
+    }
+    const sinter_gemv_args &a = *reinterpret_cast<const sinter_gemv_args *>(g_args);
     const uint32_t K = a.K;
-    const int vt = (int)st.cur.pl->vt;
-    const bool any_argmax = st.cur.pl->any_argmax != 0;
-    const uint32_t row_lo = st.row_lo;
-    const Ring rg = st.rg;
-    Cursor cur = st.cur;
-    TD X = st.X, Y = st.Y;
-
-    // The tile pipeline: X = tile being computed (buffer bx), Y = next (in
-    // flight), the tile after Y is created and issued this iteration into the
-    // buffer that X-1 occupied, P = the previous tile.  One barrier per tile
-    // makes X's DMA and the previous terms visible to every wave and frees
-    // P's buffer; a deferred ring folds P's rows in the same step, otherwise
-    // X's rows are folded after a second barrier.
+    const int vt = (int)pl->vt;
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
     gemv_prologue(a, vt, write_x, g_red, err);   // ends with __syncthreads()
-    settle_vmem();
+    if (ts) ts[2] = wall_clock64();
     const ActView x = act_view(g_qbuf, K, vt);
+
+    // this wave's term ring (aliases the prologue's staging, done now): every
+    // slot starts as -0.0 (pad slots keep it)
+    GemvCtx c;
+    c.ipr = pl->ipr; c.mipr = pl->mipr; c.P = pl->P; c.R = pl->R; c.mR = pl->mR;
+    c.qs = pl->q64; c.rs = pl->r64; c.qs2 = pl->q32; c.rs2 = pl->r32;
+    c.ring = reinterpret_cast<LDS double *>((lds_char *)g_big) + uni(wave_id()) * RING_CAP;
+    c.dummy = (uint64_t)plan;
+    {
+        typedef double f64x2 __attribute__((ext_vector_type(2)));
+        LDS f64x2 *rv = reinterpret_cast<LDS f64x2 *>(c.ring);
+        const f64x2 mz = {-0.0, -0.0};
+#pragma unroll
+        for (uint32_t i = 0; i < RING_CAP / 128; i++) rv[i * 64 + lane_id()] = mz;
+    }
 
     float bv = -INFINITY;
     int32_t bi = 0x7fffffff;
-    uint32_t res_row0 = 0;           // workgroup-local first row not yet flushed
-    TD P;
-    P.ok = 0; P.a = 0; P.cnt = 0; P.ra = 0; P.ka = 0; P.type = 0; P.swig = 0; P.lr0 = 0; P.skew_a = 0; P.base_b = 0;
-    uint32_t bx = 0;
-    while (X.ok) {
-        if (Y.ok) wait_vmcnt<TILE_CPW>(); else wait_vmcnt<0>();
-        wait_lgkm0();
-        __builtin_amdgcn_s_barrier();
-        const uint32_t bz = bx == 0 ? 2u : bx - 1;
-        const TD Z = tile_next(cur, g_tiles + bz * TILE_BYTES);
-        const TD &F = rg.defer ? P : X;       // the tile whose rows this step folds
-        if (rg.defer && P.ok && td_done_after(P, rg) - res_row0 > RES_CAP) {
-            gemv_flush(a, row_lo + res_row0, P.lr0 - res_row0, bv, bi);
-            settle_vmem();
-            res_row0 = P.lr0;
-            __syncthreads();
-        }
-        tile_terms(X, g_tiles + bx * TILE_BYTES, rg, x);
-        if (!rg.defer) {
-            wait_lgkm0();
-            __builtin_amdgcn_s_barrier();
-            if (td_done_after(X, rg) - res_row0 > RES_CAP) {
-                gemv_flush(a, row_lo + res_row0, X.lr0 - res_row0, bv, bi);
-                settle_vmem();
-                res_row0 = X.lr0;
-                __syncthreads();
-            }
-        }
-        if (F.ok) tile_fold(F, rg, res_row0);
-        P = X; X = Y; Y = Z;
-        bx = bx == 2 ? 0u : bx + 1;
+    while (run.ok) {
+        run_dispatch(pf, sh, c, pl, run, x, bv, bi, ev);
+        run = make_run(pl, run.s, run.g1, row_hi);
+        if (!run.ok) break;
+        issue_pre(pf, sh, run, (uint64_t)plan);
+        epi_preload(pl, run, ev);
     }
-    wait_lgkm0();
-    __syncthreads();
-    uint32_t rows_total = 0;
-    if (P.ok) {
-        rows_total = td_done_after(P, rg);
-        if (rg.defer) {
-            if (rows_total - res_row0 > RES_CAP) {
-                gemv_flush(a, row_lo + res_row0, P.lr0 - res_row0, bv, bi);
-                res_row0 = P.lr0;
-                __syncthreads();
-            }
-            tile_fold(P, rg, res_row0);
-        }
-    }
-    __syncthreads();
-    gemv_flush(a, row_lo + res_row0, rows_total - res_row0, bv, bi);
 
     // greedy argmax: block-local best, then the last-arriving block reduces
+    const bool any_argmax = pl->any_argmax != 0;
     if (any_argmax) {
         // block reduction of (value, index): larger value, then smaller index
 #pragma unroll
@@ -1075,11 +1035,10 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
         }
         float *rv = reinterpret_cast<float *>(g_part);
         int32_t *ri = reinterpret_cast<int32_t *>(g_part + 4);
-        __syncthreads();
         if (lane_id() == 0) { rv[wave_id()] = bv; ri[wave_id()] = bi; }
         __syncthreads();
         if (threadIdx.x == 0) {
-            for (int w = 1; w < (int)(BLOCK_THREADS / 64); w++)
+            for (int w = 1; w < (int)WAVES; w++)
                 if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) { bv = rv[w]; bi = ri[w]; }
         }
     }
@@ -1110,13 +1069,7 @@ __device__ __forceinline__ void gemv_run(const sinter_instr &ins, unsigned *err,
         }
     }
     __syncthreads();
-}
-
-__device__ __forceinline__ void op_gemv(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
-                                        unsigned *err) {
-    GemvState st;
-    gemv_begin(ins, plan, cuts, err, st);
-    gemv_run(ins, err, st);
+    return true;
 }
 
 }  // namespace sinter

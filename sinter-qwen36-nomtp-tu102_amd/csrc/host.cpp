@@ -127,33 +127,35 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
         break;
     default: return bad("unknown prologue");
     }
-    // the term ring (gemv.h ring_geometry): R rows of P terms must cover the
-    // rows one tile can touch
+    // the prologue stages x (and the norm weights or z) as f32 in the LDS
+    // scratch region
+    if ((uint64_t)a.K * 4 * (a.pro == SINTER_PRO_PLAIN ? 1u : 2u) > BIG_BYTES)
+        return bad("K too large for the prologue's staging area");
+    // the term ring (gemv.h): R rows of P terms per wave must hold the rows
+    // one 64-item step touches plus one
     {
-        const uint32_t ipr = a.K / ((a.seg[0].type == SINTER_BF16 || a.seg[0].type == SINTER_F32) ? 64u : 256u);
+        const uint32_t ipr = a.K / item_elems(a.seg[0].type);
         bool any_swig = false;
-        uint32_t tmax = 0;
-        for (int s = 0; s < a.n_seg; s++) {
-            const bool sw = a.seg[s].epi == SINTER_EPI_SWIGLU;
-            const int t = a.seg[s].type;
-            any_swig |= sw;
-            tmax = std::max(tmax, ((t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u) / (sw ? 2u : 1u));
-        }
-        const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP, tpr = (tmax + ipr - 1) / ipr;
+        for (int s = 0; s < a.n_seg; s++) any_swig |= a.seg[s].epi == SINTER_EPI_SWIGLU;
+        // one group of GEMV_DMAX 64-item steps (32 for SwiGLU pairs)
+        const uint32_t si = any_swig ? 32u : 64u;
+        const uint32_t cap = any_swig ? RING_CAP / 2 : RING_CAP, tpr = (si * GEMV_DMAX - 1) / ipr + 2;
         const uint32_t P = ring_row(ipr, cap, tpr), R = cap / P;
-        if (R < tpr + 1) return bad("rows too long for the term ring");
+        if (R < tpr) return bad("rows too long for the term ring");
     }
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
         if (vdot(g.type) != vt) return bad("segments must share one vec_dot type");
         if (!g.w || !al16(g.w) || !g.y) return bad("segment weights must be 16-byte aligned; y required");
+        if ((uint64_t)g.rows * sinter_row_bytes_dev(g.type, a.K) >= (1ull << 32))
+            return bad("segment larger than 4 GiB");
         switch (g.epi) {
         case SINTER_EPI_STORE: break;
         case SINTER_EPI_RESID: if (!g.aux) return bad("resid: aux"); break;
         case SINTER_EPI_SWIGLU: if (!g.w2 || !al16(g.w2)) return bad("swiglu: w2"); break;
         case SINTER_EPI_ARGMAX: if (!a.epi_ws) return bad("argmax: epi_ws"); break;
         case SINTER_EPI_CONV:
-            if (!g.w2 || !g.aux || g.dconv < 2 || g.dconv > 8) return bad("conv: w2 / aux / dconv");
+            if (!g.w2 || !g.aux || g.dconv < 2 || g.dconv > 4) return bad("conv: w2 / aux / dconv (2..4 taps)");
             break;
         default: return bad("unknown epilogue");
         }
@@ -161,18 +163,22 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
     return SINTER_OK;
 }
 
-// Row cut of workgroup w of n: the global row nearest to byte w*total/n of
-// the concatenated, byte-weighted row space (a SwiGLU row weighs both
-// matrices).  Any monotone split is correct; this one balances bytes.
-static uint32_t row_cut(const sinter_gemv_args &a, uint64_t total, uint32_t w, uint32_t n) {
-    uint32_t rows = 0;
+// Byte-balanced row cut w of n over the concatenated, byte-weighted row
+// space of segments [s0, s1) (a SwiGLU row weighs both matrices), as a
+// global row.  Any monotone split is correct; this one balances bytes.
+static uint32_t row_cut(const sinter_gemv_args &a, int s0, int s1, uint32_t row0, uint32_t w, uint32_t n) {
+    uint64_t total = 0;
+    for (int s = s0; s < s1; s++)
+        total += (uint64_t)a.seg[s].rows * sinter_row_bytes_dev(a.seg[s].type, a.K) *
+                 (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
+    uint32_t rows = row0;
     if (w >= n) {
-        for (int s = 0; s < a.n_seg; s++) rows += a.seg[s].rows;
+        for (int s = s0; s < s1; s++) rows += a.seg[s].rows;
         return rows;
     }
     const uint64_t target = total * w / n;
     uint64_t acc = 0;
-    for (int s = 0; s < a.n_seg; s++) {
+    for (int s = s0; s < s1; s++) {
         const uint64_t rb = sinter_row_bytes_dev(a.seg[s].type, a.K) * (a.seg[s].epi == SINTER_EPI_SWIGLU ? 2u : 1u);
         const uint64_t sb = (uint64_t)a.seg[s].rows * rb;
         if (target < acc + sb) return rows + (uint32_t)((target - acc + rb / 2) / rb);
@@ -189,8 +195,7 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
     p.ipr = a.K / item_elems(a.seg[0].type);
     p.vt = (uint32_t)vdot(a.seg[0].type);
     bool any_swig = false;
-    uint32_t tmax = 0, base = 0;
-    uint64_t total = 0;
+    uint32_t base = 0;
     for (int s = 0; s < a.n_seg; s++) {
         const sinter_gemv_seg &g = a.seg[s];
         const bool sw = g.epi == SINTER_EPI_SWIGLU;
@@ -202,25 +207,78 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
         q.type = g.type;
         q.swig = sw ? 1u : 0u;
         q.ib = item_bytes(g.type);
-        q.T = items_per_tile(g.type, sw);
-        q.qT = q.T / p.ipr;
-        q.rT = q.T % p.ipr;
+        q.y = reinterpret_cast<uint64_t>(g.y);
+        q.aux = reinterpret_cast<uint64_t>(g.aux);
+        q.w2 = reinterpret_cast<uint64_t>(g.w2);
+        q.epi = g.epi;
+        q.dconv = g.dconv;
         any_swig |= sw;
-        tmax = std::max(tmax, q.T);
         if (g.epi == SINTER_EPI_ARGMAX) p.any_argmax = 1;
         base += g.rows;
-        total += (uint64_t)g.rows * sinter_row_bytes_dev(g.type, a.K) * (sw ? 2u : 1u);
     }
     p.total_rows = base;
     p.mipr = 0xFFFFFFFFu / p.ipr;
-    const uint32_t tpr = (tmax + p.ipr - 1) / p.ipr;   // rows one tile can touch, less one
-    const uint32_t cap = any_swig ? CB_CAP / 2 : CB_CAP;
-    p.P = ring_row(p.ipr, cap, tpr);
+    p.q64 = 64 / p.ipr;
+    p.r64 = 64 % p.ipr;
+    p.q32 = 32 / p.ipr;
+    p.r32 = 32 % p.ipr;
+    const uint32_t cap = any_swig ? RING_CAP / 2 : RING_CAP;
+    p.P = ring_row(p.ipr, cap, ((any_swig ? 32u : 64u) * GEMV_DMAX - 1) / p.ipr + 2);
     p.R = cap / p.P;
-    p.defer = p.R >= 2 * tpr + 2 ? 1u : 0u;
     p.mR = 0xFFFFFFFFu / p.R;
-    p.RP = p.R * p.P;
-    for (uint32_t w = 0; w <= nblk; w++) cuts[w] = row_cut(a, total, w, nblk);
+
+    // wave cuts.  Every segment gets whole waves, in proportion to its bytes
+    // (at least one), so that a wave's rows are one streaming loop over one
+    // matrix; rows are byte-balanced inside a segment.  With fewer waves than
+    // segments, the cuts balance bytes over all rows and a wave streams the
+    // segments of its range one after another.
+    const uint32_t nw = nblk * WAVES;
+    int rs[SINTER_GEMV_MAX_SEG + 1], nruns = 0;
+    for (int s = 0; s < a.n_seg; s++)
+        rs[nruns++] = s;
+    rs[nruns] = a.n_seg;
+    if ((uint32_t)nruns > nw) {
+        for (uint32_t w = 0; w <= nw; w++) cuts[w] = row_cut(a, 0, a.n_seg, 0, w, nw);
+        return;
+    }
+    uint64_t rb[SINTER_GEMV_MAX_SEG], total = 0;
+    for (int r = 0; r < nruns; r++) {
+        rb[r] = 0;
+        for (int s = rs[r]; s < rs[r + 1]; s++)
+            rb[r] += (uint64_t)a.seg[s].rows * sinter_row_bytes_dev(a.seg[s].type, a.K) * (p.seg[s].swig ? 2u : 1u);
+        total += rb[r];
+    }
+    // largest remainder, at least one wave per run
+    uint32_t nwr[SINTER_GEMV_MAX_SEG], used = 0;
+    double frac[SINTER_GEMV_MAX_SEG];
+    for (int r = 0; r < nruns; r++) {
+        const double qv = total ? (double)nw * (double)rb[r] / (double)total : 0.0;
+        nwr[r] = std::max(1u, (uint32_t)qv);
+        frac[r] = qv - (double)(uint32_t)qv;
+        used += nwr[r];
+    }
+    while (used > nw) {   // the minimum of one wave pushed the total over
+        int big = -1;
+        for (int r = 0; r < nruns; r++)
+            if (nwr[r] > 1 && (big < 0 || nwr[r] > nwr[big])) big = r;
+        nwr[big]--;
+        used--;
+    }
+    while (used < nw) {
+        int best = 0;
+        for (int r = 1; r < nruns; r++)
+            if (frac[r] > frac[best]) best = r;
+        nwr[best]++;
+        frac[best] = -1.0;
+        used++;
+    }
+    uint32_t w0 = 0, row0 = 0;
+    for (int r = 0; r < nruns; r++) {
+        for (uint32_t w = 0; w < nwr[r]; w++) cuts[w0 + w] = row_cut(a, rs[r], rs[r + 1], row0, w, nwr[r]);
+        w0 += nwr[r];
+        for (int s = rs[r]; s < rs[r + 1]; s++) row0 += a.seg[s].rows;
+    }
+    cuts[nw] = row0;
 }
 
 template <class T>
@@ -242,7 +300,7 @@ static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
         sinter_gemv_args g;
         std::memcpy(&g, host.ins.payload, sizeof g);
         build_gemv_plan(g, blocks, host.plan, host.cuts);
-        bytes += (size_t)(blocks + 1) * 4;
+        bytes += (size_t)(blocks * WAVES + 1) * 4;
     }
     OpSlot *slot = op_slot();
     if (!slot) return SINTER_ERR_HIP;
@@ -437,6 +495,7 @@ struct sinter_host {
     unsigned pass_cycles_cap = 0;
     uint32_t passes_done = 0;
     long long *d_op_cycles = nullptr;
+    unsigned long long *d_trace = nullptr;  // caller-owned, consumed by the next launch
     uint32_t blocks = 0;
     uint64_t spin_limit = 0;
     uint64_t clock_khz = 0;
@@ -456,6 +515,8 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     ctl.pass_cycles_cap = h->pass_cycles_cap;
     ctl.pass_base = h->passes_done;
     ctl.op_cycles = h->profile_ops ? h->d_op_cycles : nullptr;
+    ctl.trace = h->d_trace;
+    h->d_trace = nullptr;
     ctl.spin_limit = h->spin_limit;
     ctl.plans = h->d_plans;
     ctl.cuts = h->d_cuts;
@@ -652,6 +713,13 @@ int sinter_host_read_pass_cycles(sinter_host *h, long long *out, unsigned count)
     return SINTER_OK;
 }
 
+int sinter_host_trace_next(sinter_host *h, unsigned long long *dev_buf, size_t words) {
+    if (!h || !dev_buf) return set_error(SINTER_ERR_ARG, "trace: args");
+    if (words < ((size_t)h->n_instr + 1) * h->blocks * 4) return set_error(SINTER_ERR_ARG, "trace: buffer too small");
+    h->d_trace = dev_buf;
+    return SINTER_OK;
+}
+
 int sinter_host_reset_op_cycles(sinter_host *h) {
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
     h->profile_ops = true;
@@ -689,7 +757,7 @@ int sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
     if (blocks) *blocks = h->blocks;
     if (threads) *threads = BLOCK_THREADS;
-    if (lds_bytes) *lds_bytes = 3 * TILE_BYTES + QBUF_BYTES + 2 * RES_CAP * 4 + 256;
+    if (lds_bytes) *lds_bytes = BIG_BYTES + QBUF_BYTES + 512;
     return SINTER_OK;
 }
 

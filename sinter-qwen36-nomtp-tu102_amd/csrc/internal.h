@@ -15,6 +15,7 @@ struct InterpCtl {
     unsigned *err;            // [0] code, [1] aux
     long long *pass_cycles;   // ring of per-pass durations (wall clock ticks), or null
     long long *op_cycles;     // per-kind durations on block 0, or null
+    unsigned long long *trace;  // [n_instr + 1][blocks][4] wall clock stamps of the launch's first pass, or null
     uint64_t spin_limit;      // barrier spin limit in wall clock ticks
     const GemvPlan *plans;    // [n_instr], GEMV entries filled
     const uint32_t *cuts;     // [n_instr][PLAN_CUTS]

@@ -30,49 +30,6 @@ __device__ __forceinline__ bool kind_wired(unsigned k) {
 }
 
 
-// Grid barrier, two-level, over monotonic counters (zeroed before the
-// launch): workgroup w counts into group counter w/16 (its own 128-byte
-// line); the group's last arriver counts into the root; every workgroup's
-// thread 0 spins on the root until epoch*groups arrivals.  Sixteen arrivals
-// per line instead of the whole grid on one line (atomics to one address
-// serialise at the memory side).  No cache writeback or invalidate: every
-// wave first waits for its own memory operations, and all data that crosses
-// workgroups moves through device-coherent loads and stores (dev_common.h).
-// Split in two so that work that does not depend on the barrier (the next
-// GEMV's first weight tiles) can be issued between arriving and waiting.
-__device__ __forceinline__ void grid_arrive(unsigned *bar, unsigned *groups, unsigned &epoch) {
-    settle_vmem();
-    __syncthreads();
-    epoch += 1;
-    if (threadIdx.x == 0) {
-        const unsigned g = blockIdx.x >> 4;
-        const unsigned gsize = min(16u, gridDim.x - g * 16u);
-        const unsigned old = __hip_atomic_fetch_add(groups + g * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-// Returns false on timeout.
-__device__ __forceinline__ bool grid_wait(unsigned *bar, unsigned epoch, uint64_t spin_limit_ticks, unsigned *err) {
-    __shared__ unsigned timed_out;
-    if (threadIdx.x == 0) {
-        timed_out = 0;
-        const unsigned target = epoch * ((gridDim.x + 15u) >> 4);
-        const uint64_t t0 = wall_clock64();
-        while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
-            __builtin_amdgcn_s_sleep(1);
-            if (wall_clock64() - t0 > spin_limit_ticks) {
-                raise_error(err, SINTER_E_TIMEOUT_BARRIER, epoch);
-                timed_out = 1;
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    return timed_out == 0;
-}
-
-
 }  // namespace sinter
 
 using namespace sinter;
@@ -80,62 +37,94 @@ using namespace sinter;
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
 sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     unsigned epoch = 0;
-    GemvState pf;                 // a GEMV begun before the barrier that precedes it
-    uint32_t pf_i = 0xffffffffu;  // its instruction index
     const uint32_t n = ctl.n_instr;
-    // one copy of each op's code in the kernel: the pass end is handled as a
-    // barrier at index n, and every GEMV runs through gemv_begin + gemv_run
-    for (uint32_t pass = 0; pass < ctl.n_passes; ++pass) {
-        const uint64_t t0 = wall_clock64();
-        for (uint32_t i = 0; i <= n; ++i) {
-            const unsigned kind = i < n ? prog[i].kind : (unsigned)SINTER_OP_BOUNDARY;
-            if (kind == SINTER_OP_BOUNDARY) {
-                const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
+    const bool timed = ctl.op_cycles && blockIdx.x == 0;
+    // i in [0, n]: i == n is the pass-end barrier.  A barrier followed by a
+    // GEMV this block takes part in runs as one op (gemv_op): the GEMV's
+    // first weight slots are loaded between arriving and waiting, so the
+    // barrier wait overlaps weight streaming; the pass end's successor is the
+    // next pass's first instruction.  One copy of each op's code.
+    uint32_t pass = 0, i = 0;
+    uint64_t t0 = wall_clock64();
+    const bool traced = ctl.trace != nullptr;
+    auto stamp = [&](uint32_t ii, uint32_t k, uint64_t v) {
+        if (traced && pass == 0 && threadIdx.x == 0) ctl.trace[((size_t)ii * gridDim.x + blockIdx.x) * 4 + k] = v;
+    };
+    while (pass < ctl.n_passes) {
+        const unsigned kind = i < n ? prog[i].kind : (unsigned)SINTER_OP_BOUNDARY;
+        if (kind == SINTER_OP_BOUNDARY) {
+            const bool pass_end = i == n;
+            const uint32_t nx = pass_end ? 0u : i + 1;
+            const bool more = nx < n && (pass + (pass_end ? 1u : 0u)) < ctl.n_passes;
+            const bool fused = more && prog[nx].kind == SINTER_OP_GEMV && blockIdx.x >= prog[nx].block_lo &&
+                               blockIdx.x < prog[nx].block_hi;
+            const uint64_t s = timed ? wall_clock64() : 0;
+            GridCross gx;
+            gx.bar = ctl.bar; gx.groups = ctl.groups; gx.err = ctl.err; gx.epoch = &epoch;
+            gx.spin_limit = ctl.spin_limit; gx.pass_end = pass_end; gx.t0 = t0; gx.t_wait_end = 0;
+            gx.pass_slot = (pass_end && blockIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
+                               ? ctl.pass_cycles + (ctl.pass_base + pass) % ctl.pass_cycles_cap
+                               : nullptr;
+            if (fused) {
+                uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
+                if (ts) ts[0] = s ? s : wall_clock64();
+                if (!gemv_op(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
+                if (ts) ts[3] = wall_clock64();
+            } else {
+                stamp(i, 0, wall_clock64());
                 grid_arrive(ctl.bar, ctl.groups, epoch);
-                // begin the next GEMV (the next pass's first one at the pass end)
-                const uint32_t nx = i + 1 < n ? i + 1 : (i == n && pass + 1 < ctl.n_passes ? 0u : 0xffffffffu);
-                if (nx != 0xffffffffu) {
-                    const sinter_instr &ni = prog[nx];
-                    if (ni.kind == SINTER_OP_GEMV && blockIdx.x >= ni.block_lo && blockIdx.x < ni.block_hi) {
-                        gemv_begin(ni, ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, pf);
-                        pf_i = nx;
-                    }
-                }
                 if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
-                if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
-                    ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(wall_clock64() - s);
-                if (i < n) continue;
-                // pass end: a uniform error sample after everyone finished
-                __shared__ unsigned e;
-                if (threadIdx.x == 0) e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __syncthreads();
-                if (blockIdx.x == 0 && threadIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
-                    ctl.pass_cycles[(ctl.pass_base + pass) % ctl.pass_cycles_cap] = (long long)(wall_clock64() - t0);
-                if (e) { settle_vmem(); return; }
-                continue;
-            }
-            const sinter_instr &ins = prog[i];
-            if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
-                if (blockIdx.x == 0 && threadIdx.x == 0)
-                    raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
-                settle_vmem();
-                return;
-            }
-            if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
-                const uint64_t s = (ctl.op_cycles && blockIdx.x == 0) ? wall_clock64() : 0;
-                if (kind == SINTER_OP_GEMV) {
-                    if (pf_i != i) gemv_begin(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, pf);
-                    pf_i = 0xffffffffu;
-                    gemv_run(ins, ctl.err, pf);
-                } else if (kind == SINTER_OP_GDN_STEP) {
-                    op_gdn_step(ins, ctl.err);
-                } else if (kind == SINTER_OP_ATTN_DECODE) {
-                    op_attn_decode(ins, ctl.err);
+                gx.t_wait_end = wall_clock64();
+                if (pass_end) {
+                    // a uniform error sample after everyone finished the pass
+                    __shared__ unsigned e;
+                    if (threadIdx.x == 0) {
+                        e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (gx.pass_slot) *gx.pass_slot = (long long)(gx.t_wait_end - t0);
+                    }
+                    __syncthreads();
+                    if (e) { settle_vmem(); return; }
                 }
-                if (ctl.op_cycles && blockIdx.x == 0 && threadIdx.x == 0)
-                    ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
+                stamp(i, 1, gx.t_wait_end);
             }
+            if (timed && threadIdx.x == 0) {
+                const uint64_t e = wall_clock64();
+                ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(gx.t_wait_end - s);
+                if (fused) ctl.op_cycles[SINTER_OP_GEMV] += (long long)(e - gx.t_wait_end);
+            }
+            if (pass_end) {
+                pass += 1;
+                t0 = gx.t_wait_end;
+                i = fused ? 1u : 0u;
+            } else {
+                i += fused ? 2u : 1u;
+            }
+            continue;
         }
+        const sinter_instr &ins = prog[i];
+        if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
+            if (blockIdx.x == 0 && threadIdx.x == 0)
+                raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
+            settle_vmem();
+            return;
+        }
+        if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
+            const uint64_t s = timed ? wall_clock64() : 0;
+            stamp(i, 0, wall_clock64());
+            if (kind == SINTER_OP_GEMV) {
+                uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
+                (void)gemv_op(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
+            } else if (kind == SINTER_OP_GDN_STEP) {
+                op_gdn_step(ins, ctl.err);
+            } else if (kind == SINTER_OP_ATTN_DECODE) {
+                op_attn_decode(ins, ctl.err);
+            }
+            if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
+            stamp(i, 3, wall_clock64());
+        }
+        i += 1;
     }
 }
 
@@ -148,7 +137,7 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
                  const uint32_t *__restrict__ cuts, unsigned *err) {
     // the host sets block_lo = 0, block_hi = gridDim.x
     switch (ins->kind) {
-    case SINTER_OP_GEMV: op_gemv(*ins, plan, cuts, err); break;
+    case SINTER_OP_GEMV: (void)gemv_op(*ins, plan, cuts, err, nullptr, nullptr); break;
     case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err); break;
     case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err); break;
     default: break;

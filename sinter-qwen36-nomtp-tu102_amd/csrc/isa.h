@@ -16,29 +16,33 @@ static_assert(sizeof(sinter_gemv_seg) == 40, "gemv segment");
 namespace sinter {
 
 // Launch envelope of the cooperative interpreter: one 256-thread workgroup
-// (4 wave64) per CU; all LDS is static (lds.h), 152 KiB of the CU's 160 KiB.
+// (4 wave64) per CU; all LDS is static (dev_common.h).
 constexpr unsigned BLOCK_THREADS = 256;
+constexpr unsigned WAVES = BLOCK_THREADS / 64u;
 
-// GEMV LDS: three 36 KiB weight-tile buffers filled by LDS-DMA, each wave
-// issuing TILE_CPW 1 KiB chunks per tile; the quantised activation; the
-// buffered row results.
-constexpr unsigned TILE_BYTES = 36u * 1024u;
-constexpr unsigned TILE_CPW = TILE_BYTES / 1024u / (BLOCK_THREADS / 64u);
+// LDS: the quantised GEMV activation, and one 96 KiB scratch region shared by
+// the ops: the GEMV's activation staging (prologue) and then its per-wave
+// item-term rings; attention's tiles; the GDN step's vectors.
 constexpr unsigned QBUF_BYTES = 40u * 1024u;   // padded activation: Q8_K K=17408 20944 B; BF16 K=17408 39168 B
-constexpr unsigned RES_CAP = 512u;             // rows buffered before the epilogue runs
-constexpr unsigned CB_CAP = 776u;              // GEMV term ring (doubles): the rows of two tiles
-                                               // of up to 256 item terms, padded (RING_PAD)
-static_assert(TILE_CPW * 4u * 1024u == TILE_BYTES, "tile = whole chunks per wave");
+constexpr unsigned BIG_BYTES = 96u * 1024u;
+constexpr unsigned ATT_REGION = 36u * 1024u;   // attention: three regions at 0, 36 and 72 KiB
+// GEMV item-term ring of one wave, in doubles (8 KiB; a SwiGLU pair splits
+// it into a gate half and an up half)
+constexpr uint32_t RING_CAP = 1024u;
+// the deepest weight prefetch of any item type (items in flight per lane):
+// the ring must hold the rows one group of that many steps touches
+constexpr uint32_t GEMV_DMAX = 4u;
+static_assert(WAVES * RING_CAP * 8u <= BIG_BYTES, "rings fit the scratch region");
 // A term-ring row holds a row's item terms padded with -0.0 (an exact no-op
 // in the fold) to a multiple of RING_PAD, so the fold reads whole 16-byte
 // pairs in batches of RING_PAD with no masking -- or, when rows that long
-// would not leave the ring room for the rows one tile touches (short rows,
-// many per tile), to a multiple of 2.  cap = ring capacity in terms, tpr =
-// rows one tile can touch, less one.
+// would not leave the ring room for the rows one 64-item step touches (short
+// rows), to a multiple of 2.  cap = ring capacity in terms, tpr = rows one
+// step can touch, plus one.
 constexpr uint32_t RING_PAD = 8u;
 __host__ __device__ inline uint32_t ring_row(uint32_t ipr, uint32_t cap, uint32_t tpr) {
     const uint32_t p8 = (ipr + RING_PAD - 1u) & ~(RING_PAD - 1u);
-    return cap / p8 >= tpr + 1u ? p8 : ipr + (ipr & 1u);
+    return cap / p8 >= tpr ? p8 : ipr + (ipr & 1u);
 }
 
 // GEMV activation layout in LDS.  Padded so that lanes working on different
@@ -80,10 +84,10 @@ __host__ __device__ inline uint32_t item_elems(int t) { return (t == SINTER_BF16
 __host__ __device__ inline uint32_t item_bytes(int t) {
     return t == SINTER_Q4_K ? 144u : t == SINTER_Q6_K ? 210u : t == SINTER_Q8_0 ? 272u : t == SINTER_BF16 ? 128u : 256u;
 }
-// items of one matrix per tile: every lane busy, at most TILE_BYTES - 16
-__host__ __device__ inline uint32_t items_per_tile(int t, bool swiglu) {
-    const uint32_t n = (t == SINTER_Q4_K || t == SINTER_BF16) ? 256u : 128u;
-    return swiglu ? n / 2 : n;
+// 16-byte loads that bring one item into registers (Q6_K: a 4-aligned
+// 224-byte window around the 2-aligned 210-byte block)
+__host__ __device__ inline uint32_t item_loads(int t) {
+    return t == SINTER_Q4_K ? 9u : t == SINTER_Q6_K ? 14u : t == SINTER_Q8_0 ? 17u : t == SINTER_BF16 ? 8u : 16u;
 }
 
 // A GEMV instruction compiled for the kernel: everything about its work split
@@ -92,20 +96,27 @@ __host__ __device__ inline uint32_t items_per_tile(int t, bool swiglu) {
 // the device is a few scalar loads instead of divisions and table builds.
 struct GemvSegPlan {
     uint64_t wa, wb;                    // weights: A (gate rows for SwiGLU), B (up rows) or 0
+    uint64_t y, aux, w2;                // the segment's epilogue operands (sinter_gemv_seg)
     uint32_t rows, base;                // rows; global row of segment row 0
-    uint32_t type, swig, ib, T, qT, rT; // item bytes; items of each matrix per tile; T / ipr; T % ipr
+    uint32_t type, swig, ib;            // weight type; SwiGLU pair; item bytes
+    uint32_t epi, dconv, _pad;          // epilogue mode, conv taps
 };
 struct GemvPlan {
     uint32_t ok;                        // passed validation (otherwise the op raises BAD_SHAPE)
     uint32_t n_seg, ipr, vt, any_argmax, total_rows;
-    // the term ring: P = ipr rounded up to RING_PAD, R rows of P terms,
-    // mipr / mR = floor((2^32-1) / ipr or R), RP = R * P, defer = fold one tile late
-    uint32_t mipr, P, R, mR, RP, defer;
+    uint32_t mipr;                      // floor((2^32-1) / ipr)
+    // the term ring of a wave: R rows of P terms (per matrix); mR = floor((2^32-1) / R)
+    uint32_t P, R, mR;
+    uint32_t q64, r64;                  // 64 / ipr, 64 % ipr: one 64-item step in rows + items
+    uint32_t q32, r32;                  // the same for a 32-item step (SwiGLU pairs)
     GemvSegPlan seg[SINTER_GEMV_MAX_SEG];
 };
-// Workgroup w of an op owns global rows [cuts[w], cuts[w+1]); each
-// instruction has PLAN_CUTS cut slots.
+// a GEMV's loads past the end of its rows read the plan instead: it must
+// cover the largest item load (272 B)
+static_assert(sizeof(GemvPlan) >= 272, "plan doubles as the dummy load target");
+// Wave v of an op (v = 4 * (block - block_lo) + wave) owns global rows
+// [cuts[v], cuts[v+1]); each instruction has PLAN_CUTS cut slots.
 constexpr uint32_t PLAN_MAX_BLOCKS = 1024;
-constexpr uint32_t PLAN_CUTS = PLAN_MAX_BLOCKS + 1;
+constexpr uint32_t PLAN_CUTS = PLAN_MAX_BLOCKS * WAVES + 1;
 
 }  // namespace sinter

@@ -141,6 +141,7 @@ def lib():
         "sinter_host_read_pass_cycles": (I, [vp, C.POINTER(C.c_longlong), C.c_uint]),
         "sinter_host_reset_op_cycles": (I, [vp]),
         "sinter_host_read_op_cycles": (I, [vp, C.POINTER(C.c_longlong), C.c_uint]),
+        "sinter_host_trace_next": (I, [vp, vp, C.c_size_t]),
         "sinter_host_pass_cell": (vp, [vp]),
         "sinter_host_history": (vp, [vp, C.POINTER(U32)]),
         "sinter_host_error": (I, [vp, C.POINTER(U32), C.POINTER(U32)]),
