@@ -97,7 +97,9 @@ enum sinter_gemv_pro {
     SINTER_PRO_PLAIN = 0,   /* a = x */
     SINTER_PRO_RMSNORM = 1, /* a = rmsnorm(x) * norm_w          (glue.cuh:56-152) */
     SINTER_PRO_GATED = 2,   /* per head of 2^gn_log2d: rmsnorm(x_h)*norm_w*silu(z_h) (gdn.cuh:339-383) */
-    SINTER_PRO_EMBED = 3    /* x = dequant(embd[token]); block_lo writes x_out; a = rmsnorm(x)*norm_w (glue.cuh:202-227) */
+    SINTER_PRO_EMBED = 3,   /* x = dequant(embd[token]); block_lo writes x_out; a = rmsnorm(x)*norm_w (glue.cuh:202-227) */
+    SINTER_PRO_GATED_G = 4  /* as GATED with aux = silu(z) already applied (an EPI_SILU segment made it):
+                               per head rmsnorm(x_h)*norm_w*aux_h */
 };
 /* SINTER_OP_GEMV epilogue modes, per segment */
 enum sinter_gemv_epi {
@@ -105,9 +107,10 @@ enum sinter_gemv_epi {
     SINTER_EPI_RESID = 1,  /* y[r] = res[r] + dot (residual add fused) */
     SINTER_EPI_SWIGLU = 2, /* y[r] = silu(w.a) * (w2.a)   (gemv.cuh:327-347) */
     SINTER_EPI_ARGMAX = 3, /* y[r] = dot, plus greedy argmax over all rows (harness.cpp:1187-1195) */
-    SINTER_EPI_CONV = 4    /* causal conv + silu per row (channel):          (gdn.cuh:106-171)
+    SINTER_EPI_CONV = 4,   /* causal conv + silu per row (channel):          (gdn.cuh:106-171)
                               y[r] = silu(sum_j win_j * w2[r*dconv+j]), win = {aux[r*(dconv-1)..], dot};
                               aux (conv state) <- win[1..] */
+    SINTER_EPI_SILU = 5    /* y[r] = silu(dot): the gate of a later GATED_G prologue (gdn.cuh:356-383) */
 };
 
 typedef struct sinter_gemv_seg {
@@ -229,7 +232,9 @@ int  sinter_host_reset_op_cycles(sinter_host *h);
  * instruction i (i = n_instr: the pass-end barrier) and block b, words
  * [(i*blocks+b)*4 ..] = wall clock (100 MHz) at the instruction's start,
  * after its barrier wait (a barrier fused with the GEMV after it records
- * under the GEMV's index), after a GEMV's prologue, at its end. */
+ * under the GEMV's index), after a GEMV's prologue (attention: after its q
+ * prep; GDN step: after its norms and gates), [2] (attention: after its KV
+ * tiles; GDN: after its state update), at its end. */
 int  sinter_host_trace_next(sinter_host *h, unsigned long long *dev_buf, size_t words);
 int  sinter_host_read_op_cycles(sinter_host *h, long long *out, unsigned count);
 /* device pointers the program payloads reference */

@@ -38,7 +38,7 @@ constexpr int ATT_MAXG = 8;    // max q heads per kv head
 // floats, rot [2][128] floats, red [4][ATT_MAXG+1] doubles.
 __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t nq, uint32_t nh, const float *qw,
                                          const float *kw, float eps, int pos, float theta_scale, uint32_t rope_dims,
-                                         float *dst, float *qn, float *rot, double *red) {
+                                         LDS float *dst, LDS float *qn, LDS float *rot, LDS double *red) {
     const uint32_t t = threadIdx.x, half = rope_dims / 2;
     if (t < half) {
         float th = (float)pos;
@@ -63,12 +63,12 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
             const float mean = (float)(ss / 256.0);
             const float sc = 1.0f / sqrtf(mean + eps);
             const float nrm = x[j] * sc;
-            qn[j * 256 + t] = nrm * (j < nq ? qw[t] : kw[t]);
+            qn[j * 256 + t] = nrm * (j < nq ? gp(qw)[t] : gp(kw)[t]);
         }
     }
     __syncthreads();
     for (uint32_t j = 0; j < nh; j++) {
-        const float *r = qn + j * 256;
+        const LDS float *r = qn + j * 256;
         float y = r[t];
         if (t < half) {
             const float x0 = r[t], x1 = r[t + half], c = rot[t], s = rot[128 + t];
@@ -90,44 +90,50 @@ constexpr uint32_t ATT_FAN = 8;   // partials merged per step of the merge tree
 // Merge n (<= ATT_FAN) consecutive partials {acc[HD], m, l} of each of gqa
 // q heads (fp64, coherent reads): M = max m_i, acc = sum_i e_i acc_i,
 // l = sum_i e_i l_i with e_i = exp(m_i - M), in ascending i; a partial with
-// m = -inf contributes nothing.  Thread t owns dim t.  With dst, the merged
+// m = -inf contributes nothing.  Thread t owns dim t; every load is issued
+// before the first is used (one memory round trip).  With dst, the merged
 // unnormalised partial goes there; otherwise out = acc/l * sigmoid(gate).
-// ew: LDS scratch of ATT_MAXG * (ATT_FAN + 1) doubles.
+// ew: LDS scratch of ATT_MAXG * (ATT_FAN + 2) doubles.
 __device__ __forceinline__ void att_merge(const sinter_attn_args &a, const double *src, uint32_t n, uint32_t gqa, uint32_t g,
-                          double *dst, double *ew) {
+                          double *dst, LDS double *ew) {
     const uint32_t t = threadIdx.x, HD = a.hd, PS = HD + 2;
     const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * gqa * PS * 8);
-    // weights e[hh][i] and the max, one lane per q head
+    double pv[ATT_MAXG][ATT_FAN], m[ATT_FAN], lv[ATT_FAN];
+#pragma unroll
+    for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++)
+            pv[hh][i] = (hh < gqa && i < n) ? ld_coh8(r, ((i * gqa + hh) * PS + t) * 8) : 0.0;
+    // weights e[hh][i], the max and l, one lane per q head
     if (t < gqa) {
-        double m[ATT_FAN], M = -INFINITY;
 #pragma unroll
         for (uint32_t i = 0; i < ATT_FAN; i++) {
             m[i] = i < n ? ld_coh8(r, ((i * gqa + t) * PS + HD) * 8) : -INFINITY;
-            M = fmax(M, m[i]);
+            lv[i] = i < n ? ld_coh8(r, ((i * gqa + t) * PS + HD + 1) * 8) : 0.0;
         }
+        double M = -INFINITY;
 #pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++)
-            ew[t * (ATT_FAN + 1) + i] = (m[i] == -INFINITY) ? 0.0 : exp(m[i] - M);
-        ew[t * (ATT_FAN + 1) + ATT_FAN] = M;
+        for (uint32_t i = 0; i < ATT_FAN; i++) M = fmax(M, m[i]);
+        double L = 0.0;
+#pragma unroll
+        for (uint32_t i = 0; i < ATT_FAN; i++) {
+            const double e = (m[i] == -INFINITY) ? 0.0 : exp(m[i] - M);
+            ew[t * (ATT_FAN + 2) + i] = e;
+            if (i < n && e != 0.0) L = fma(e, lv[i], L);
+        }
+        ew[t * (ATT_FAN + 2) + ATT_FAN] = M;
+        ew[t * (ATT_FAN + 2) + ATT_FAN + 1] = L;
     }
     __syncthreads();
-    for (uint32_t hh = 0; hh < gqa; hh++) {
-        const double *e = ew + hh * (ATT_FAN + 1);
-        double pv[ATT_FAN], lv[ATT_FAN];
 #pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++) {
-            const uint32_t o = (i * gqa + hh) * PS;
-            pv[i] = i < n ? ld_coh8(r, (o + t) * 8) : 0.0;
-            lv[i] = i < n ? ld_coh8(r, (o + HD + 1) * 8) : 0.0;
-        }
-        double O = 0.0, L = 0.0;
+    for (uint32_t hh = 0; hh < ATT_MAXG; hh++) {
+        if (hh >= gqa) break;
+        const LDS double *e = ew + hh * (ATT_FAN + 2);
+        double O = 0.0;
 #pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++) {
-            if (i < n && e[i] != 0.0) {
-                O = fma(e[i], pv[i], O);
-                L = fma(e[i], lv[i], L);
-            }
-        }
+        for (uint32_t i = 0; i < ATT_FAN; i++)
+            if (i < n && e[i] != 0.0) O = fma(e[i], pv[hh][i], O);
+        const double L = e[ATT_FAN + 1];
         if (dst) {
             double *d = dst + hh * PS;
             st_coh(d + t, O);
@@ -145,20 +151,22 @@ __device__ __forceinline__ void att_merge(const sinter_attn_args &a, const doubl
 
 // Count one arrival at *cnt of `total`; true (uniform) for the last arriver,
 // which also resets the counter for the next use.
-__device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, unsigned *flag) {
+__device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, LDS unsigned *flag) {
     settle_vmem();   // every wave's partial stores complete before the count
     __syncthreads();
     if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(gp(cnt), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned last = (old == total - 1) ? 1u : 0u;
-        if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last) __hip_atomic_store(gp(cnt), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = last;
     }
     __syncthreads();
     return *flag != 0;
 }
 
-__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err) {
+// ts (thread 0, or null): wall clock stamps [1] after the q prep of the
+// first item, [2] after its KV tiles.
+__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts) {
     // the payload, read once into registers: the op stores to the KV cache
     // and the partials, which the compiler cannot tell apart from the payload
     // (every field would be reloaded from memory after each such store)
@@ -180,109 +188,169 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     uint32_t clen = (n_kv + C - 1) / C;
     clen = (clen + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
 
-    // LDS map (the scratch region): q heads, K tile, new K/V row |
-    // V tile, scores, softmax state, scratch
-    float *qf = reinterpret_cast<float *>(g_big);                      // [gqa][256] q, then the new k row
-    uint16_t *kt = reinterpret_cast<uint16_t *>(qf + (ATT_MAXG + 1) * 256);   // [32][256]
-    uint16_t *knew = kt + ATT_TILE * 256;                                // [256]
-    uint16_t *vnew = knew + 256;                                         // [256]
-    uint16_t *vt = reinterpret_cast<uint16_t *>(g_big + ATT_REGION);                // [32][256]
-    double *sc = reinterpret_cast<double *>(vt + ATT_TILE * 256);        // [gqa][32] scores -> weights
-    double *mrun = sc + ATT_MAXG * ATT_TILE;                             // [gqa]
-    double *lrun = mrun + ATT_MAXG;                                      // [gqa]
-    double *corr = lrun + ATT_MAXG;                                      // [gqa]
-    double *red = corr + ATT_MAXG;                                       // 16
-    float *knf = reinterpret_cast<float *>(red + 16);                    // [256] k scratch
-    unsigned *flag = reinterpret_cast<unsigned *>(knf + 256);
-    double *ew = reinterpret_cast<double *>(g_big + 2 * ATT_REGION);    // [ATT_MAXG][ATT_FAN+1] merge weights
-    float *qn = reinterpret_cast<float *>(g_big + 2 * ATT_REGION + 1024);   // [ATT_MAXG+1][256] prep scratch
-    float *rot = qn + (ATT_MAXG + 1) * 256;                                  // [2][128] rope cos | sin
-    double *pred = reinterpret_cast<double *>(rot + 256);                   // [4][ATT_MAXG+1]
+    // LDS map (the scratch region): K and V tiles double-buffered by LDS-DMA,
+    // q heads (and the new k row), prep scratch, scores, softmax state
+    lds_char *L = (lds_char *)g_big;
+    LDS uint16_t *kb = reinterpret_cast<LDS uint16_t *>(L);                          // [2][32][256]
+    LDS uint16_t *vb = reinterpret_cast<LDS uint16_t *>(L + 2 * ATT_TILE * 512);     // [2][32][256]
+    LDS float *qf = reinterpret_cast<LDS float *>(L + 4 * ATT_TILE * 512);           // [gqa][256] q, then the new k row
+    LDS float *qn = qf + (ATT_MAXG + 1) * 256;    // [ATT_MAXG+2][256] raw q / k / v rows, then prep scratch
+    LDS float *rot = qn + (ATT_MAXG + 2) * 256;                                      // [2][128] rope cos | sin
+    LDS double *pred = reinterpret_cast<LDS double *>(rot + 256);                    // [4][ATT_MAXG+1]
+    LDS double *sc = pred + 4 * (ATT_MAXG + 1);                                      // [32][ATT_MAXG] scores -> weights
+    LDS double *mrun = sc + ATT_MAXG * ATT_TILE;                                     // [gqa]
+    LDS double *lrun = mrun + ATT_MAXG;                                              // [gqa]
+    LDS double *corr = lrun + ATT_MAXG;                                              // [gqa]
+    LDS double *ew = corr + ATT_MAXG;                                                // [ATT_MAXG][ATT_FAN+2] merge weights
+    LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(ew + ATT_MAXG * (ATT_FAN + 2));   // [256]
+    LDS uint16_t *vnew = knew + 256;                                                 // [256]
+    LDS unsigned *flag = reinterpret_cast<LDS unsigned *>(vnew + 256);
+    const uint32_t w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+    const uint32_t kbase = (uint32_t)(uintptr_t)kb, vbase = (uint32_t)(uintptr_t)vb;
 
     for (uint32_t item = rel; item < NKV * C; item += nblk) {
         const uint32_t g = item / C, c = item % C;
         const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
         const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
-
+        const uint32_t ntile = (kv1 - kv0 + ATT_TILE - 1) / ATT_TILE;
+        // Tile j (32 rows of this kv head: 512 B of K and of V each) into
+        // buffer j % 2: each wave DMAs rows 2k, 2k+1 for k = w, w+4, w+8,
+        // w+12 of K and of V (lane l: row 2k + l/32, bytes 16 (l%32) ..);
+        // rows past kv1 re-read row kv1-1 (masked in the scores).
+        auto issue_tile = [&](uint32_t j) {
+            const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4; kk++) {
+                const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
+                const uint32_t voff = (row * RW + g * HD) * 2 + (lane & 31) * 16;
+                lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
+                lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
+            }
+        };
         {
-            // q heads g*gqa .. and, for the owner, the new k row (as head gqa)
+            // The raw q heads g*gqa .. (and, for the owner, the new k and v
+            // rows) by LDS-DMA into qn rows 0..gqa+1, one 1 KiB row per wave
+            // instruction; then the first two tiles.  Every wait is explicit,
+            // so the prep below runs while the tiles still stream in.
+            const uint32_t nraw = owner ? gqa + 2 : gqa;
+            const uint32_t qnbase = (uint32_t)(uintptr_t)qn;
+            for (uint32_t j = w; j < nraw; j += WAVES) {
+                const float *src = j < gqa ? a.qg + (size_t)(g * gqa + j) * 2 * HD
+                                 : j == gqa ? a.k + (size_t)g * HD : a.v + (size_t)g * HD;
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)src);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)src >> 32));
+                lds_dma16<true>(((uintptr_t)hi << 32) | lo, lane * 16, qnbase + j * 1024);
+            }
+            // this wave's raw-row DMAs, then 8 per tile
+            const uint32_t my_raw = nraw > w ? (nraw - w + WAVES - 1) / WAVES : 0u;
+            if (ntile > 0) issue_tile(0);
+            if (ntile > 1) issue_tile(1);
+            const uint32_t behind = (ntile > 0 ? 8u : 0u) + (ntile > 1 ? 8u : 0u);
+            (void)my_raw;
+            if (behind == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+            else if (behind == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            else dma_wait();
+            __syncthreads();
             float xr[ATT_MAXG + 1];
 #pragma unroll
-            for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
-                xr[hh] = hh < gqa ? ld_coh(a.qg + (size_t)(g * gqa + hh) * 2 * HD + t) : 0.0f;
-            xr[ATT_MAXG] = 0.0f;
-            if (owner) {
-#pragma unroll
-                for (uint32_t hh = 0; hh <= ATT_MAXG; hh++)
-                    if (hh == gqa) xr[hh] = ld_coh(a.k + (size_t)g * HD + t);
-            }
+            for (uint32_t hh = 0; hh <= ATT_MAXG; hh++) xr[hh] = hh < nraw && hh <= gqa ? qn[hh * 256 + t] : 0.0f;
+            const float vraw = owner ? qn[(gqa + 1) * 256 + t] : 0.0f;
+            __syncthreads();
             att_prep(xr, gqa, owner ? gqa + 1 : gqa, a.q_norm, a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, qf,
                      qn, rot, pred);
+            if (owner) vnew[t] = f2h(vraw);
         }
         if (owner) {
-            const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = f2h(ld_coh(a.v + (size_t)g * HD + t));
+            const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = vnew[t];
             knew[t] = kh;
-            vnew[t] = vh;
             st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
             st_coh(a.vc + (size_t)pos * RW + (size_t)g * HD + t, vh);
         }
+        if (ts && item == rel) ts[1] = wall_clock64();
         if (t < gqa) { mrun[t] = -INFINITY; lrun[t] = 0.0; }
         double acc[ATT_MAXG];
 #pragma unroll
         for (int hh = 0; hh < ATT_MAXG; hh++) acc[hh] = 0.0;
-        __syncthreads();
 
-        for (uint32_t t0 = kv0; t0 < kv1; t0 += ATT_TILE) {
-            // K and V tiles of this kv head: 32 rows x 512 B each
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t idx = t + k * 256, r = idx >> 5, ch = idx & 31, j = t0 + r;
-                uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
-                if (j < kv1) {
-                    if (owner && j == (uint32_t)pos) {
-                        kv4 = reinterpret_cast<const uint4 *>(knew)[ch];
-                        vv4 = reinterpret_cast<const uint4 *>(vnew)[ch];
-                    } else {
-                        const size_t o = (size_t)j * RW + (size_t)g * HD;
-                        kv4 = reinterpret_cast<const uint4 *>(a.kc + o)[ch];
-                        vv4 = reinterpret_cast<const uint4 *>(a.vc + o)[ch];
-                    }
-                }
-                reinterpret_cast<uint4 *>(kt)[idx] = kv4;
-                reinterpret_cast<uint4 *>(vt)[idx] = vv4;
+        for (uint32_t j = 0; j < ntile; j++) {
+            const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 256;
+            if (j == 0) {
+                dma_wait();   // (also the owner's cache stores)
+            } else {
+                // tile j landed; tile j+1 (issued last step) may still fly
+                if (j + 1 < ntile) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+                else dma_wait();
             }
             __syncthreads();
             // scores: thread (r = t/8, part = t%8) covers dims [32 part, 32 part + 32)
+            // of every q head slot (k converted once); the eight parts are
+            // combined with DPP in the butterfly order (d0+d1)+(d2+d3) + ...
+            // Slots past gqa compute on stale rows and are weighted 0 below.
+            // sc is position-major: sc[r * ATT_MAXG + hh].
             {
                 const uint32_t r = t >> 3, part = t & 7;
-                const uint16_t *kr = kt + r * 256 + part * 32;
-                for (uint32_t hh = 0; hh < gqa; hh++) {
-                    const float *q = qf + hh * 256 + part * 32;
-                    double d = 0.0;
+                const LDS uint16_t *kr = ((owner && t0 + r == (uint32_t)pos) ? knew : kb + bo + r * 256) + part * 32;
+                double kd[32];
 #pragma unroll
-                    for (int i = 0; i < 32; i++) d = fma((double)q[i], (double)h2f(kr[i]), d);
-                    d += __shfl_xor(d, 1, 64);
-                    d += __shfl_xor(d, 2, 64);
-                    d += __shfl_xor(d, 4, 64);
-                    if (part == 0) sc[hh * ATT_TILE + r] = (t0 + r < kv1) ? d * (double)a.scale : -INFINITY;
+                for (int i = 0; i < 32; i += 8) {
+                    const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(kr + i);
+                    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        kd[i + 2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
+                        kd[i + 2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
+                    }
                 }
+                // dims ascending per head; the eight head chains interleaved
+                double d[ATT_MAXG];
+#pragma unroll
+                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    f32x4 qv[ATT_MAXG];
+#pragma unroll
+                    for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
+                        qv[hh] = reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + part * 32)[i];
+#pragma unroll
+                    for (uint32_t hh = 0; hh < ATT_MAXG; hh++) {
+                        d[hh] = fma((double)qv[hh].x, kd[4 * i], d[hh]);
+                        d[hh] = fma((double)qv[hh].y, kd[4 * i + 1], d[hh]);
+                        d[hh] = fma((double)qv[hh].z, kd[4 * i + 2], d[hh]);
+                        d[hh] = fma((double)qv[hh].w, kd[4 * i + 3], d[hh]);
+                    }
+                }
+#pragma unroll
+                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_XOR1>(d[hh]);
+#pragma unroll
+                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_XOR2>(d[hh]);
+#pragma unroll
+                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_HALF_MIRROR>(d[hh]);
+                // lane `part` stores head slot `part`
+                double mine = d[0];
+#pragma unroll
+                for (uint32_t hh = 1; hh < ATT_MAXG; hh++) mine = part == hh ? d[hh] : mine;
+                sc[r * ATT_MAXG + part] = (t0 + r < kv1) ? mine * (double)a.scale : -INFINITY;
             }
             __syncthreads();
-            // online softmax per head: 32 lanes per head
-            if (t < gqa * ATT_TILE) {
+            // online softmax: head slot hh = t/32 over its 32 rows (lane r);
+            // max and sum over the 32 lanes with DPP plus one cross-row step
+            {
                 const uint32_t hh = t / ATT_TILE, r = t % ATT_TILE;
-                const double s = sc[hh * ATT_TILE + r];
+                const double s = sc[r * ATT_MAXG + hh];
                 double mt = s;
-#pragma unroll
-                for (int o = 16; o > 0; o >>= 1) mt = fmax(mt, __shfl_xor(mt, o, 64));
+                mt = fmax(mt, dpp_d<DPP_XOR1>(mt));
+                mt = fmax(mt, dpp_d<DPP_XOR2>(mt));
+                mt = fmax(mt, dpp_d<DPP_HALF_MIRROR>(mt));
+                mt = fmax(mt, dpp_d<DPP_MIRROR>(mt));
+                mt = fmax(mt, __shfl_xor(mt, 16, 64));
                 const double mo = mrun[hh];
                 const double mn = fmax(mo, mt);
-                const double w = (s == -INFINITY) ? 0.0 : exp(s - mn);
-                double ws = w;
+                const double wgt = (s == -INFINITY || hh >= gqa) ? 0.0 : exp(s - mn);
+                double ws = wgt;
 #pragma unroll
                 for (int o = 16; o > 0; o >>= 1) ws += __shfl_xor(ws, o, 64);
-                sc[hh * ATT_TILE + r] = w;
-                if (r == 0) {
+                sc[r * ATT_MAXG + hh] = wgt;
+                if (r == 0 && hh < gqa) {
                     const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
                     corr[hh] = cf;
                     lrun[hh] = lrun[hh] * cf + ws;
@@ -290,17 +358,29 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
                 }
             }
             __syncthreads();
-            // V accumulation: thread t owns dim t
-            for (uint32_t hh = 0; hh < gqa; hh++) {
-                double v = acc[hh] * corr[hh];
-                const double *w = sc + hh * ATT_TILE;
-#pragma unroll 8
-                for (int r = 0; r < ATT_TILE; r++) v = fma(w[r], (double)h2f(vt[r * 256 + t]), v);
-                acc[hh] = v;
+            // V accumulation: thread t owns dim t; per row, v converted once
+            // and the eight slot weights read as four broadcast 16-byte loads
+#pragma unroll
+            for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
+                if (hh < gqa) acc[hh] = acc[hh] * corr[hh];
+#pragma unroll 4
+            for (uint32_t r = 0; r < ATT_TILE; r++) {
+                const LDS uint16_t *vr = (owner && t0 + r == (uint32_t)pos) ? vnew : vb + bo + r * 256;
+                const double v = (double)h2f(vr[t]);
+                typedef double f64x2 __attribute__((ext_vector_type(2)));
+                const LDS f64x2 *w2 = reinterpret_cast<const LDS f64x2 *>(sc + r * ATT_MAXG);
+                f64x2 wv[ATT_MAXG / 2];
+#pragma unroll
+                for (uint32_t k = 0; k < ATT_MAXG / 2; k++) wv[k] = w2[k];
+#pragma unroll
+                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) acc[hh] = fma(wv[hh / 2][hh % 2], v, acc[hh]);
             }
             __syncthreads();
+            // the tile after next into the buffer just freed
+            if (j + 2 < ntile) issue_tile(j + 2);
         }
 
+        if (ts && item == rel) ts[2] = wall_clock64();
         // publish the partial; the merge is a tree of fan-in ATT_FAN over
         // the chunks, each node merged by the last arriver of its children
         const uint32_t PS = HD + 2, G1 = (C + ATT_FAN - 1) / ATT_FAN, g1 = c / ATT_FAN;

@@ -20,6 +20,16 @@ typedef __attribute__((address_space(3))) void lds_void;
 // the compiler emit flat loads, which also count against vmcnt and so wait
 // for every in-flight LDS-DMA load.
 #define LDS __attribute__((address_space(3)))
+// Explicit global (address space 1) pointers for the same reason: flat
+// instructions also count against lgkmcnt, so every LDS wait after a flat
+// global access would wait for it too.
+#define GLB __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ GLB T *gp(T *p) { return (GLB T *)p; }
+template <class T>
+__device__ __forceinline__ const GLB T *gp(const T *p) { return (const GLB T *)p; }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef LDS char lds_char;
 
 // ---------------------------------------------------------------- static LDS
@@ -107,7 +117,8 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
 // doubles.  Rows are reduced with DPP, the four row sums of a wave and then
 // the wave sums are added in a fixed order; the result is order-dependent
 // only at fp64 rounding level (callers round to fp32).
-__device__ __forceinline__ double block_sum_f64(double v, double *red) {
+template <class P>
+__device__ __forceinline__ double block_sum_f64(double v, P red) {
     v = row16_sum_f64(v);
     const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
     const int nw = blockDim.x >> 6;
@@ -151,7 +162,7 @@ __device__ __forceinline__ float dev_softplus(float x) {
 // ---------------------------------------------------------------- memory scope
 
 __device__ __forceinline__ unsigned atomic_load_relaxed_agent(const unsigned *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cross-workgroup data -- every activation, partial and pass-cell word that
@@ -164,10 +175,19 @@ __device__ __forceinline__ unsigned atomic_load_relaxed_agent(const unsigned *p)
 // Immutable data (weights, norms) and data a workgroup only shares with
 // itself across passes (recurrent and conv state) use ordinary cached
 // accesses.
+// (through global-address-space pointers: a generic pointer would make the
+// compiler emit flat instructions, which also count against lgkmcnt and so
+// make every LDS wait after them wait for the global access too)
 template <class T>
-__device__ __forceinline__ T ld_coh(const T *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ T ld_coh(const T *p) {
+    return __hip_atomic_load((const __attribute__((address_space(1))) T *)(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
 template <class T>
-__device__ __forceinline__ void st_coh(T *p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_coh(T *p, T v) {
+    __hip_atomic_store((__attribute__((address_space(1))) T *)(p), v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
 // 16 bytes (16-aligned) as two coherent 8-byte loads / stores
 __device__ __forceinline__ float4 ld_coh4(const float *p) {
     const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
@@ -220,8 +240,45 @@ __device__ __forceinline__ void settle_vmem() { __builtin_amdgcn_s_waitcnt(0x0F7
 __device__ __forceinline__ void raise_error(unsigned *err, unsigned code, unsigned aux) {
     if (!err) return;
     if (atomicCAS(err, 0u, code) == 0u)
-        __hip_atomic_store(err + 1, aux, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(err + 1), aux, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// ---------------------------------------------------------------- LDS-DMA
+
+// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at base + voff land at
+// lds_base + 16*l (gfx950 global_load_lds_dwordx4: no VGPRs involved).
+// Issued from inline asm so the compiler does not treat the pending DMA as
+// aliasing every later LDS access; callers wait for it explicitly
+// (dma_wait).  M0 (the LDS base of the DMA) is restored before the asm ends;
+// one wait state separates the M0 write from the DMA that reads it.  COH
+// selects the device-coherent cache policy (sc1) for data another workgroup
+// wrote earlier in the pass.
+template <bool COH>
+__device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
+    uint32_t saved;
+    if (COH) {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %3 sc1\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds_base), "v"(voff), "s"(base)
+            : "memory");
+    } else {
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "s_nop 0\n\t"
+            "global_load_lds_dwordx4 %2, %3\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds_base), "v"(voff), "s"(base)
+            : "memory");
+    }
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------- grid barrier
 
@@ -242,8 +299,8 @@ __device__ __forceinline__ void grid_arrive(unsigned *bar, unsigned *groups, uns
     if (threadIdx.x == 0) {
         const unsigned g = blockIdx.x >> 4;
         const unsigned gsize = min(16u, gridDim.x - g * 16u);
-        const unsigned old = __hip_atomic_fetch_add(groups + g * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(gp(groups + g * 32u), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(gp(bar), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -21,8 +21,10 @@
 
 namespace sinter {
 
-__device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *err) {
-    char *lds = g_big;
+// ts (thread 0, or null): wall clock stamps [1] after the first item's
+// norms and gates, [2] after its state update.
+__device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *err, uint64_t *ts) {
+    lds_char *lds = (lds_char *)g_big;
     const sinter_gdn_args &a = *reinterpret_cast<const sinter_gdn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t D = a.d, HK = a.hk, HV = a.hv, cols = a.cols;
@@ -37,10 +39,10 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
         return;
     }
     const uint32_t rpt = D / tpc;  // rows per thread
-    float *qs = reinterpret_cast<float *>(lds);          // [D] normalised q
-    float *ks = qs + 256;                                 // [D] normalised k
-    double *red = reinterpret_cast<double *>(ks + 256);   // 16 doubles
-    float *gb = reinterpret_cast<float *>(red + 16);      // g, beta
+    LDS float *qs = reinterpret_cast<LDS float *>(lds);          // [D] normalised q
+    LDS float *ks = qs + 256;                                     // [D] normalised k
+    LDS double *red = reinterpret_cast<LDS double *>(ks + 256);   // 16 doubles
+    LDS float *gb = reinterpret_cast<LDS float *>(red + 16);      // g, beta
     const uint32_t slices = D / cols, n_items = HV * slices;
 
     for (uint32_t item = rel; item < n_items; item += nblk) {
@@ -66,22 +68,23 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
             ks[threadIdx.x] = kv * (1.0f / fmaxf(sqrtf((float)sk), a.eps));
         }
         if (threadIdx.x == 0) {
-            const float sp = dev_softplus(ld_coh(a.alpha + h) + a.dt_bias[h]);
-            gb[0] = (float)exp((double)(sp * a.ssm_a[h]));
+            const float sp = dev_softplus(ld_coh(a.alpha + h) + gp(a.dt_bias)[h]);
+            gb[0] = (float)exp((double)(sp * gp(a.ssm_a)[h]));
             gb[1] = dev_sigmoid(ld_coh(a.beta + h));
         }
         __syncthreads();
+        if (ts && item == rel) ts[1] = wall_clock64();
         const float g = gb[0], beta = gb[1];
 
         // this thread: column c0 + threadIdx.x / tpc, rows [i0, i0 + rpt)
         const uint32_t col = c0 + threadIdx.x / tpc;
         const uint32_t i0 = (threadIdx.x % tpc) * rpt;
-        float *srow = a.state + ((size_t)h * D + col) * D + i0;
+        GLB float *srow = gp(a.state + ((size_t)h * D + col) * D + i0);
         float s[32];
 #pragma unroll
         for (uint32_t r = 0; r < 32; r += 4) {
             if (r < rpt) {
-                const float4 t = *reinterpret_cast<const float4 *>(srow + r);
+                const f32x4 t = *reinterpret_cast<const GLB f32x4 *>(srow + r);
                 s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
             }
         }
@@ -107,8 +110,12 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
         for (uint32_t o = 1; o < tpc; o <<= 1) dout += __shfl_xor(dout, (int)o, 64);
 #pragma unroll
         for (uint32_t r = 0; r < 32; r += 4)
-            if (r < rpt) *reinterpret_cast<float4 *>(srow + r) = make_float4(s[r], s[r + 1], s[r + 2], s[r + 3]);
+            if (r < rpt) {
+                const f32x4 v = {s[r], s[r + 1], s[r + 2], s[r + 3]};
+                *reinterpret_cast<GLB f32x4 *>(srow + r) = v;
+            }
         if ((threadIdx.x % tpc) == 0) st_coh(a.o + (size_t)h * D + col, (float)dout * a.scale);
+        if (ts && item == rel) ts[2] = wall_clock64();
         __syncthreads();  // qs/ks/gb reused by the next item
     }
 }

@@ -104,43 +104,6 @@ __device__ __forceinline__ void dequant4(const void *row, int type, uint32_t e, 
     }
 }
 
-// ------------------------------------------------------------ LDS-DMA
-
-// One 1 KiB LDS-DMA chunk per wave: lane l's 16 bytes at base + voff land at
-// lds_base + 16*l (gfx950 global_load_lds_dwordx4: no VGPRs involved).
-// Issued from inline asm so the compiler does not treat the pending DMA as
-// aliasing every later LDS access; callers wait for it explicitly
-// (dma_wait).  M0 (the LDS base of the DMA) is restored before the asm ends;
-// one wait state separates the M0 write from the DMA that reads it.  COH
-// selects the device-coherent cache policy (sc1) for data another workgroup
-// wrote earlier in the pass.
-template <bool COH>
-__device__ __forceinline__ void lds_dma16(uintptr_t base, uint32_t voff, uint32_t lds_base) {
-    uint32_t saved;
-    if (COH) {
-        asm volatile(
-            "s_mov_b32 %0, m0\n\t"
-            "s_mov_b32 m0, %1\n\t"
-            "s_nop 0\n\t"
-            "global_load_lds_dwordx4 %2, %3 sc1\n\t"
-            "s_mov_b32 m0, %0"
-            : "=&s"(saved)
-            : "s"(lds_base), "v"(voff), "s"(base)
-            : "memory");
-    } else {
-        asm volatile(
-            "s_mov_b32 %0, m0\n\t"
-            "s_mov_b32 m0, %1\n\t"
-            "s_nop 0\n\t"
-            "global_load_lds_dwordx4 %2, %3\n\t"
-            "s_mov_b32 m0, %0"
-            : "=&s"(saved)
-            : "s"(lds_base), "v"(voff), "s"(base)
-            : "memory");
-    }
-}
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 // Copy n floats (n a multiple of 256) from global p into LDS dst: the
 // workgroup's waves take 1 KiB chunks round-robin.
 template <bool COH>
@@ -172,10 +135,13 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
-// Quantise this lane's 16 elements [e0, e0+16) of chunk c (every lane of the
-// row calls this with the same c) into the activation layout at q.
-__device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t e0, const float t[16], lds_char *q,
-                                        LDS float *qd, LDS int16_t *qb) {
+// Lane r of a 16-lane row holds elements 64q + 4r + i (q, i = 0..3) of its
+// 256-element chunk c: four float4 at 64-element strides, so the 16 lanes of a
+// row read 256 contiguous bytes per q (no LDS bank conflicts) and a Q8_K
+// 16-element sub-block 4q + r/4 sits on the four lanes r/4 (two DPP steps).
+// Quantise the lane's t[4q + i] into the activation layout at q.
+__device__ __forceinline__ void quant_chunk(int vt, uint32_t c, uint32_t r, const float t[16], lds_char *q,
+                                            LDS float *qd, LDS int16_t *qb) {
     int qv[16];
     if (vt == SINTER_Q8_K) {
         // ggml quantize_row_q8_K_ref: the signed element of largest |x|, first
@@ -191,16 +157,20 @@ __device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t
         for (int i = 0; i < 4; i++) m4[i] = fmaxf(fmaxf(ax[4 * i], ax[4 * i + 1]), fmaxf(ax[4 * i + 2], ax[4 * i + 3]));
         const float am = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
         const float A = row16_max(am);
-        // (index, sign) keys of the elements reaching A; the smallest wins
+        // (group index, sign) keys of the elements reaching A; the smallest wins
         int key[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) key[i] = ax[i] == A ? ((i << 1) | (t[i] < 0.0f ? 1 : 0)) : 0x7fffffff;
+        for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = 64 * qq + 4 * (int)r + i;
+                key[4 * qq + i] = ax[4 * qq + i] == A ? ((e << 1) | (t[4 * qq + i] < 0.0f ? 1 : 0)) : 0x7fffffff;
+            }
 #pragma unroll
         for (int w = 8; w > 0; w >>= 1)
 #pragma unroll
             for (int i = 0; i < w; i++) key[i] = min(key[i], key[i + w]);
-        const int lkey = key[0] == 0x7fffffff ? 0x7fffffff : (int)(r << 5) + key[0];
-        const int gkey = row16_min(lkey);
+        const int gkey = row16_min(key[0]);
         float dd = 0.0f;
         if (A != 0.0f) {
             const float bmax = (gkey & 1) ? -A : A;
@@ -215,44 +185,53 @@ __device__ __forceinline__ void quant16(int vt, uint32_t c, uint32_t r, uint32_t
 #pragma unroll
             for (int i = 0; i < 16; i++) qv[i] = 0;
         }
-        const int bsum = (((qv[0] + qv[1]) + (qv[2] + qv[3])) + ((qv[4] + qv[5]) + (qv[6] + qv[7]))) +
-                         (((qv[8] + qv[9]) + (qv[10] + qv[11])) + ((qv[12] + qv[13]) + (qv[14] + qv[15])));
-        lds_st16(q + c * ACT_GSTRIDE + r * 16, pack4_i8(qv[0], qv[1], qv[2], qv[3]), pack4_i8(qv[4], qv[5], qv[6], qv[7]),
-                 pack4_i8(qv[8], qv[9], qv[10], qv[11]), pack4_i8(qv[12], qv[13], qv[14], qv[15]));
-        qb[e0 / 16] = (int16_t)bsum;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            *reinterpret_cast<LDS uint32_t *>(q + c * ACT_GSTRIDE + 64 * qq + 4 * r) =
+                pack4_i8(qv[4 * qq], qv[4 * qq + 1], qv[4 * qq + 2], qv[4 * qq + 3]);
+            // bsum of sub-block 4qq + r/4: the four lanes' sums, in a tree
+            int s = (qv[4 * qq] + qv[4 * qq + 1]) + (qv[4 * qq + 2] + qv[4 * qq + 3]);
+            s += dpp_i<DPP_XOR1>(s);
+            s += dpp_i<DPP_XOR2>(s);
+            if ((r & 3) == 0) qb[16 * c + 4 * qq + r / 4] = (int16_t)s;
+        }
         if (r == 0) qd[c] = dd;
     } else if (vt == SINTER_Q8_0) {
         // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax);
-        // a 32-element block is two lanes
-        float am = 0.0f;
+        // 32-element block 2q + r/8 is the lane's four elements of each q on
+        // the eight lanes r/8
+        float dblk[4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) am = fmaxf(am, fabsf(t[i]));
-        am = fmaxf(am, dpp_f<DPP_XOR1>(am));
-        const float d = am / 127.f;
-        const float id = (am != 0.0f) ? 127.f / am : 0.0f;
+        for (int qq = 0; qq < 4; qq++) {
+            float am = fmaxf(fmaxf(fabsf(t[4 * qq]), fabsf(t[4 * qq + 1])), fmaxf(fabsf(t[4 * qq + 2]), fabsf(t[4 * qq + 3])));
+            am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+            am = fmaxf(am, dpp_f<DPP_XOR2>(am));
+            am = fmaxf(am, dpp_f<DPP_HALF_MIRROR>(am));
+            const float id = (am != 0.0f) ? 127.f / am : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) qv[i] = (int)__builtin_rintf(t[i] * id);
-        lds_st16(q + c * ACT_GSTRIDE + r * 16, pack4_i8(qv[0], qv[1], qv[2], qv[3]), pack4_i8(qv[4], qv[5], qv[6], qv[7]),
-                 pack4_i8(qv[8], qv[9], qv[10], qv[11]), pack4_i8(qv[12], qv[13], qv[14], qv[15]));
-        if ((r & 1) == 0) qd[e0 / 32] = h2f(f2h(d));
+            for (int i = 0; i < 4; i++) qv[4 * qq + i] = (int)__builtin_rintf(t[4 * qq + i] * id);
+            dblk[qq] = am / 127.f;
+            *reinterpret_cast<LDS uint32_t *>(q + c * ACT_GSTRIDE + 64 * qq + 4 * r) =
+                pack4_i8(qv[4 * qq], qv[4 * qq + 1], qv[4 * qq + 2], qv[4 * qq + 3]);
+            if ((r & 7) == 0) qd[8 * c + 2 * qq + r / 8] = h2f(f2h(dblk[qq]));
+        }
     } else if (vt == SINTER_BF16) {
-        uint32_t h[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = (uint32_t)f2bf(t[2 * i]) | ((uint32_t)f2bf(t[2 * i + 1]) << 16);
-        lds_char *p = q + (e0 >> 6) * ACT_BF_CSTRIDE + (e0 & 63) * 2;
-        lds_st16(p, h[0], h[1], h[2], h[3]);
-        lds_st16(p + 16, h[4], h[5], h[6], h[7]);
+        for (int qq = 0; qq < 4; qq++) {
+            const uint32_t h0 = (uint32_t)f2bf(t[4 * qq]) | ((uint32_t)f2bf(t[4 * qq + 1]) << 16);
+            const uint32_t h1 = (uint32_t)f2bf(t[4 * qq + 2]) | ((uint32_t)f2bf(t[4 * qq + 3]) << 16);
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t v = {h0, h1};
+            *reinterpret_cast<LDS u32x2_t *>(q + (4 * c + qq) * ACT_BF_CSTRIDE + 8 * r) = v;
+        }
     } else {
-        lds_char *p = q + (e0 >> 6) * ACT_F_CSTRIDE + (e0 & 63) * 4;
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            lds_st16(p + 16 * k, __float_as_uint(t[4 * k]), __float_as_uint(t[4 * k + 1]), __float_as_uint(t[4 * k + 2]),
-                     __float_as_uint(t[4 * k + 3]));
+        for (int qq = 0; qq < 4; qq++)
+            lds_st16(q + (4 * c + qq) * ACT_F_CSTRIDE + 16 * r, __float_as_uint(t[4 * qq]), __float_as_uint(t[4 * qq + 1]),
+                     __float_as_uint(t[4 * qq + 2]), __float_as_uint(t[4 * qq + 3]));
     }
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
 __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
 
@@ -266,7 +245,8 @@ __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret
 __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
                                               unsigned *err) {
     const uint32_t K = a.K;
-    const bool embed = a.pro == SINTER_PRO_EMBED, gated = a.pro == SINTER_PRO_GATED;
+    const bool embed = a.pro == SINTER_PRO_EMBED;
+    const bool gpre = a.pro == SINTER_PRO_GATED_G, gated = a.pro == SINTER_PRO_GATED || gpre;
     const bool rms = a.pro == SINTER_PRO_RMSNORM || embed;
     char *xs_g = g_big, *ys_g = g_big + K * 4;
     if (embed) {
@@ -302,11 +282,12 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
-    auto ld16 = [&](const LDS float *base, uint32_t e0, float v[16]) {
+    // the lane's 16 elements of chunk c: 64q + 4r + i
+    auto ld16 = [&](const LDS float *base, uint32_t c, float v[16]) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(base + e0 + 4 * k);
-            v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+        for (int qq = 0; qq < 4; qq++) {
+            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(base + c * 256 + 64 * qq + 4 * r);
+            v[4 * qq] = t.x; v[4 * qq + 1] = t.y; v[4 * qq + 2] = t.z; v[4 * qq + 3] = t.w;
         }
     };
     // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
@@ -316,7 +297,7 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         double s = 0.0;
         for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
             float v[16];
-            ld16(xs, c * 256 + r * 16, v);
+            ld16(xs, c, v);
 #pragma unroll
             for (int i = 0; i < 16; i++) s += (double)(v[i] * v[i]);
         }
@@ -324,51 +305,51 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         const float mean = (float)(s / (double)K);
         gscale = 1.0f / sqrtf(mean + a.eps);
     }
-    // gated-norm weights: element i of this lane is norm_w[(16r + i) % gd] in every chunk
+    // gated-norm weights: element 64q + 4r + i of every chunk uses
+    // norm_w[(64q + 4r + i) % gd]
     float gw[16];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gated) t = *reinterpret_cast<const float4 *>(a.norm_w + ((r * 16 + 4 * k) & (gd - 1)));
-        gw[4 * k] = t.x; gw[4 * k + 1] = t.y; gw[4 * k + 2] = t.z; gw[4 * k + 3] = t.w;
+    for (int qq = 0; qq < 4; qq++) {
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        if (gated) t = *reinterpret_cast<const GLB f32x4 *>(gp(a.norm_w + ((64 * qq + r * 4) & (gd - 1))));
+        gw[4 * qq] = t.x; gw[4 * qq + 1] = t.y; gw[4 * qq + 2] = t.z; gw[4 * qq + 3] = t.w;
     }
     lds_char *q = (lds_char *)g_qbuf;
     LDS float *qd = reinterpret_cast<LDS float *>(q + (K / 256) * ACT_GSTRIDE);
     LDS int16_t *qb = reinterpret_cast<LDS int16_t *>(q + act_bs_off(K));
 #pragma unroll 1
     for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
-        const uint32_t e0 = c * 256 + r * 16;
         float v[16], y[16], t[16];
-        ld16(xs, e0, v);
-        if (a.pro != SINTER_PRO_PLAIN) ld16(ys, e0, y);
+        ld16(xs, c, v);
+        if (a.pro != SINTER_PRO_PLAIN) ld16(ys, c, y);
         if (a.pro == SINTER_PRO_PLAIN) {
 #pragma unroll
             for (int i = 0; i < 16; i++) t[i] = v[i];
         } else if (gated) {
-            // per-head sums of squares in double: heads of 4 or 8
-            // elements inside the lane, wider heads over gd/16 lanes
+            // per-head sums of squares in double.  Head h of width gd holds,
+            // on lane r, the elements of each q with (64q + 4r) / gd == h:
+            // its sum combines lanes (DPP) and, for gd >= 128, q's
             double s4[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int qq = 0; qq < 4; qq++) {
                 double h = 0.0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) h += (double)(v[4 * k + i] * v[4 * k + i]);
-                s4[k] = h;
+                for (int i = 0; i < 4; i++) h += (double)(v[4 * qq + i] * v[4 * qq + i]);
+                if (gd >= 8) h += dpp_d<DPP_XOR1>(h);
+                if (gd >= 16) h += dpp_d<DPP_XOR2>(h);
+                if (gd >= 32) h += dpp_d<DPP_HALF_MIRROR>(h);
+                if (gd >= 64) h += dpp_d<DPP_MIRROR>(h);
+                s4[qq] = h;
             }
-            const double s8a = s4[0] + s4[1], s8b = s4[2] + s4[3];
-            double s16 = s8a + s8b;
-            if (gd >= 32) s16 += dpp_d<DPP_XOR1>(s16);
-            if (gd >= 64) s16 += dpp_d<DPP_XOR2>(s16);
-            if (gd >= 128) s16 += dpp_d<DPP_HALF_MIRROR>(s16);
-            if (gd >= 256) s16 += dpp_d<DPP_MIRROR>(s16);
+            if (gd >= 128) { const double a01 = s4[0] + s4[1], a23 = s4[2] + s4[3]; s4[0] = s4[1] = a01; s4[2] = s4[3] = a23; }
+            if (gd >= 256) { const double all = s4[0] + s4[2]; s4[0] = s4[1] = s4[2] = s4[3] = all; }
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const double hsum = gd == 4 ? s4[i / 4] : gd == 8 ? (i < 8 ? s8a : s8b) : s16;
-                const float mean = (float)(hsum / (double)gd);
+                const float mean = (float)(s4[i / 4] / (double)gd);
                 const float hs = 1.0f / sqrtf(mean + a.eps);
                 const float nrm = v[i] * hs;
                 const float wn = nrm * gw[i];
-                t[i] = wn * dev_silu(y[i]);
+                t[i] = wn * (gpre ? y[i] : dev_silu(y[i]));
                 if ((i & 3) == 3) sched_fence();   // bounds the live fp64 temporaries
             }
         } else {
@@ -378,7 +359,7 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
                 t[i] = nrm * y[i];
             }
         }
-        quant16(vt, c, r, e0, t, q, qd, qb);
+        quant_chunk(vt, c, r, t, q, qd, qb);
     }
     __syncthreads();
 }
@@ -590,7 +571,6 @@ __device__ __forceinline__ double item_term(const u32x4 *wv, uint32_t sh, const 
 // through the constant address space, so every field is a scalar load.
 typedef const __attribute__((address_space(4))) GemvPlan cplan_t;
 typedef const __attribute__((address_space(4))) uint32_t cu32_t;
-#define GLB __attribute__((address_space(1)))
 
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -759,6 +739,8 @@ __device__ __forceinline__ void epi_row(cplan_t *pl, uint32_t s, __amdgpu_buffer
     const uint32_t epi = pl->seg[s].epi;
     if (epi == SINTER_EPI_SWIGLU) {
         y = dev_silu(dot) * up;
+    } else if (epi == SINTER_EPI_SILU) {
+        y = dev_silu(dot);
     } else if (FULL && epi == SINTER_EPI_RESID) {
         y = ev.v[0] + dot;
     } else if (FULL && epi == SINTER_EPI_CONV) {
@@ -1033,8 +1015,8 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
             const int32_t oi = __shfl_xor(bi, o, 64);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        float *rv = reinterpret_cast<float *>(g_part);
-        int32_t *ri = reinterpret_cast<int32_t *>(g_part + 4);
+        LDS float *rv = reinterpret_cast<LDS float *>((LDS double *)g_part);
+        LDS int32_t *ri = reinterpret_cast<LDS int32_t *>((LDS double *)g_part + 4);
         if (lane_id() == 0) { rv[wave_id()] = bv; ri[wave_id()] = bi; }
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -1049,7 +1031,7 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
         st_coh(ws->part_val + rel, bv);
         st_coh(ws->part_idx + rel, bi);
         settle_vmem();
-        const unsigned old = __hip_atomic_fetch_add(ws->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(gp(ws->count), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == nblk - 1) {
             float best = -INFINITY;
             int32_t bidx = 0x7fffffff;
@@ -1065,7 +1047,7 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
             st_coh(&pc->steps, steps + 1);
             st_coh(&pc->token, bidx);
             st_coh(&pc->pos, ld_coh(&pc->pos) + 1);
-            __hip_atomic_store(ws->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gp(ws->count), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();

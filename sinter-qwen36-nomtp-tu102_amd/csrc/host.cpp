@@ -116,6 +116,7 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
         if (!a.x || !al16(a.x) || !a.norm_w || !al16(a.norm_w)) return bad("x / norm_w missing or unaligned");
         break;
     case SINTER_PRO_GATED:
+    case SINTER_PRO_GATED_G:
         if (!a.x || !al16(a.x) || !a.norm_w || !a.aux || !al16(a.aux)) return bad("gated: x / norm_w / z");
         if (a.gn_log2d < 2 || a.gn_log2d > 8) return bad("gated: head width must be 4..256");
         break;
@@ -150,7 +151,7 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
         if ((uint64_t)g.rows * sinter_row_bytes_dev(g.type, a.K) >= (1ull << 32))
             return bad("segment larger than 4 GiB");
         switch (g.epi) {
-        case SINTER_EPI_STORE: break;
+        case SINTER_EPI_STORE: case SINTER_EPI_SILU: break;
         case SINTER_EPI_RESID: if (!g.aux) return bad("resid: aux"); break;
         case SINTER_EPI_SWIGLU: if (!g.w2 || !al16(g.w2)) return bad("swiglu: w2"); break;
         case SINTER_EPI_ARGMAX: if (!a.epi_ws) return bad("argmax: epi_ws"); break;

@@ -116,10 +116,11 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
                 (void)gemv_op(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
-            } else if (kind == SINTER_OP_GDN_STEP) {
-                op_gdn_step(ins, ctl.err);
-            } else if (kind == SINTER_OP_ATTN_DECODE) {
-                op_attn_decode(ins, ctl.err);
+            } else {
+                uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
+                if (kind == SINTER_OP_GDN_STEP) op_gdn_step(ins, ctl.err, ts);
+                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode(ins, ctl.err, ts);
             }
             if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
             stamp(i, 3, wall_clock64());
@@ -138,8 +139,8 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
     // the host sets block_lo = 0, block_hi = gridDim.x
     switch (ins->kind) {
     case SINTER_OP_GEMV: (void)gemv_op(*ins, plan, cuts, err, nullptr, nullptr); break;
-    case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err); break;
-    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err); break;
+    case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err, nullptr); break;
+    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err, nullptr); break;
     default: break;
     }
 }

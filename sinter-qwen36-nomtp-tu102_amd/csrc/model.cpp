@@ -196,7 +196,7 @@ void build_program(sinter_model *m) {
         } else {
             g1.n_seg = 4;
             g1.seg[0] = seg(w[S_QKV], m->qkv, SINTER_EPI_CONV, w[S_CONV_W].d, (float *)m->S[il][0].d, c.conv_k);
-            g1.seg[1] = seg(w[S_Z], m->z, SINTER_EPI_STORE);
+            g1.seg[1] = seg(w[S_Z], m->z, SINTER_EPI_SILU);   // the gate silu(z), once
             g1.seg[2] = seg(w[S_ALPHA], m->al, SINTER_EPI_STORE);
             g1.seg[3] = seg(w[S_BETA], m->be, SINTER_EPI_STORE);
         }
@@ -258,7 +258,7 @@ void build_program(sinter_model *m) {
             g3.seg[0] = seg(w[S_WO], m->H, SINTER_EPI_RESID, nullptr, m->X);
         } else {
             g3.K = (uint32_t)(c.gdn_hv * D);
-            g3.pro = SINTER_PRO_GATED;
+            g3.pro = SINTER_PRO_GATED_G;
             g3.x = m->o;
             g3.norm_w = (const float *)w[S_SSM_NORM].d;
             g3.aux = m->z;

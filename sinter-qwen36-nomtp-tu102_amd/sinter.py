@@ -14,8 +14,8 @@ LIB_PATH = os.path.join(HERE, "libsinter.so")
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 8, 12, 14, 15, 30
 # ops
 OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range(6)
-PRO_PLAIN, PRO_RMSNORM, PRO_GATED, PRO_EMBED = range(4)
-EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV = range(5)
+PRO_PLAIN, PRO_RMSNORM, PRO_GATED, PRO_EMBED, PRO_GATED_G = range(5)
+EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV, EPI_SILU = range(6)
 SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16 = range(5)
 OK, ERR_ARG, ERR_HIP, ERR_DEVICE, ERR_TIMEOUT, ERR_STATE, ERR_NOMEM = 0, -1, -2, -3, -4, -5, -6
 RUN_OK, RUN_ERR, RUN_TIMEOUT = 0, 1, 2

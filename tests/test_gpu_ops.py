@@ -133,6 +133,39 @@ def test_gemv_gated_prologue(sn, orc, torch_gpu):
     assert_ulp(host(dy), orc.gemv(Q4_K, w, rows, k, on))
 
 
+@pytest.mark.parametrize("log2d", [7, 2, 3, 4, 5, 6, 8])
+def test_gemv_silu_epilogue_then_gated_g_prologue(sn, orc, torch_gpu, log2d):
+    """The model's ssm path: a z projection with EPI_SILU stores silu(z); the
+    ssm_out GEMV's GATED_G prologue uses it as the gate.  Equal to the gated
+    RMSNorm of the raw z (the oracle) for every head width."""
+    torch = torch_gpu
+    d = 1 << log2d
+    k, zr, rows = 4096, 4096, 384
+    hv = k // d
+    o = xvec(k, 21, zero_block=False)
+    xz = xvec(2048, 22, zero_block=False)
+    wz = synth_w(sn, Q4_K, zr, 2048, 310)
+    nw = (1 + 0.02 * np.random.default_rng(23).standard_normal(d)).astype(np.float32)
+    w = synth_w(sn, Q4_K, rows, k, 320)
+    dxz, dwz, dz = dev(torch, xz), dev(torch, wz), empty_f32(torch, zr)
+    az = sn.GemvArgs(K=2048, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    az.x = dxz.data_ptr()
+    az.seg[0] = sn.GemvSeg(w=dwz.data_ptr(), y=dz.data_ptr(), rows=zr, type=Q4_K, epi=sn.EPI_SILU)
+    run_gemv(sn, torch, az, 200)
+    zraw = orc.gemv(Q4_K, wz, zr, 2048, xz)
+    L = orc.lib()
+    gate = np.array([L.or_silu(float(v)) for v in zraw], np.float32)
+    assert np.array_equal(host(dz), gate)
+    do, dn, dw, dy = dev(torch, o), dev(torch, nw), dev(torch, w), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_GATED_G, n_seg=1, eps=1e-6, gn_log2d=log2d)
+    a.x, a.norm_w, a.aux = do.data_ptr(), dn.data_ptr(), dz.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=Q4_K, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 256)
+    on = np.zeros(k, np.float32)
+    L.or_gated_rmsnorm(o.ctypes.data, zraw.ctypes.data, nw.ctypes.data, on.ctypes.data, hv, d, 1e-6)
+    assert_ulp(host(dy), orc.gemv(Q4_K, w, rows, k, on))
+
+
 @pytest.mark.parametrize("et", [Q4_K, BF16])
 def test_gemv_embed_prologue(sn, orc, torch_gpu, et):
     torch = torch_gpu
