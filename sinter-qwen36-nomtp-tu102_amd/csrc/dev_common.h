@@ -93,6 +93,12 @@ __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
     return fmaxf(v, dpp_f<DPP_MIRROR>(v));
 }
+__device__ __forceinline__ float row16_minf(float v) {
+    v = fminf(v, dpp_f<DPP_XOR1>(v));
+    v = fminf(v, dpp_f<DPP_XOR2>(v));
+    v = fminf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    return fminf(v, dpp_f<DPP_MIRROR>(v));
+}
 __device__ __forceinline__ int row16_min(int v) {
     v = min(v, dpp_i<DPP_XOR1>(v));
     v = min(v, dpp_i<DPP_XOR2>(v));
@@ -129,6 +135,40 @@ __device__ __forceinline__ double block_sum_f64(double v, P red) {
     for (int i = 0; i < nw; i++) t += red[i];
     __syncthreads();
     return t;
+}
+
+// Two block sums at once (the same fold as block_sum_f64 for each).
+template <class P>
+__device__ __forceinline__ void block_sum2_f64(double &a, double &b, P red) {
+    a = row16_sum_f64(a);
+    b = row16_sum_f64(b);
+    const double wa = ((readlane_f64(a, 0) + readlane_f64(a, 16)) + readlane_f64(a, 32)) + readlane_f64(a, 48);
+    const double wb = ((readlane_f64(b, 0) + readlane_f64(b, 16)) + readlane_f64(b, 32)) + readlane_f64(b, 48);
+    const int nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane_id() == 0) { red[2 * wave_id()] = wa; red[2 * wave_id() + 1] = wb; }
+    __syncthreads();
+    double ta = 0.0, tb = 0.0;
+    for (int i = 0; i < nw; i++) { ta += red[2 * i]; tb += red[2 * i + 1]; }
+    __syncthreads();
+    a = ta;
+    b = tb;
+}
+
+// Sum over aligned groups of n lanes (n a power of two, 1..64), every lane of
+// a group getting the group's sum: the butterfly over lane distances 1, 2,
+// 4, ..., n/2.  Within a 16-lane row the steps at distance 4 and 8 use the
+// half-row and row mirrors (the partner holds the same partial sum as the
+// lane at distance 4 / 8 once the smaller steps are done, so the sums are
+// bit-identical); wider steps use cross-lane shuffles.
+__device__ __forceinline__ double lanes_sum_f64(double v, uint32_t n) {
+    if (n >= 2) v += dpp_d<DPP_XOR1>(v);
+    if (n >= 4) v += dpp_d<DPP_XOR2>(v);
+    if (n >= 8) v += dpp_d<DPP_HALF_MIRROR>(v);
+    if (n >= 16) v += dpp_d<DPP_MIRROR>(v);
+    if (n >= 32) v += __shfl_xor(v, 16, 64);
+    if (n >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
 }
 
 // ---------------------------------------------------------------- conversions

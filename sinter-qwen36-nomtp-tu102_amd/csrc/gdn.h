@@ -17,6 +17,8 @@
 // exact fp32 products rounded to fp32 once; delta and the state update are
 // the reference's fp32 expressions (mul, mul, add; no contraction).
 #pragma once
+#include <type_traits>
+
 #include "dev_common.h"
 
 namespace sinter {
@@ -42,81 +44,85 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
     LDS float *qs = reinterpret_cast<LDS float *>(lds);          // [D] normalised q
     LDS float *ks = qs + 256;                                     // [D] normalised k
     LDS double *red = reinterpret_cast<LDS double *>(ks + 256);   // 16 doubles
-    LDS float *gb = reinterpret_cast<LDS float *>(red + 16);      // g, beta
     const uint32_t slices = D / cols, n_items = HV * slices;
 
+    // the item loop with the rows per thread a compile-time constant, so the
+    // state loads are unconditional and the wait counts exact
+    auto items = [&](auto rptc) {
+    constexpr uint32_t RPT = decltype(rptc)::value;
     for (uint32_t item = rel; item < n_items; item += nblk) {
         const uint32_t h = item / slices, c0 = (item % slices) * cols;
         const uint32_t hk = h % HK;
         const float *qsrc = a.qkv + (size_t)hk * D;
         const float *ksrc = a.qkv + (size_t)HK * D + (size_t)hk * D;
         const float *vsrc = a.qkv + (size_t)2 * HK * D + (size_t)h * D;
-        // l2 norm of q and k (ggml: fp32 squares summed in double,
-        // scale = 1/fmaxf(sqrtf(sum), eps))
-        double sq = 0.0, sk = 0.0;
-        float qv = 0.0f, kv = 0.0f;
-        if (threadIdx.x < D) {
-            qv = ld_coh(qsrc + threadIdx.x);
-            kv = ld_coh(ksrc + threadIdx.x);
-            sq = (double)(qv * qv);
-            sk = (double)(kv * kv);
+        // this thread: column c0 + threadIdx.x / tpc, rows [i0, i0 + rpt)
+        const uint32_t col = c0 + threadIdx.x / tpc;
+        const uint32_t i0 = (threadIdx.x % tpc) * RPT;
+        // every load of the item first (one memory round trip): q, k, v and
+        // the raw gates (written by the projection), then the state slice
+        // (unconditional: lanes past D re-read element t % D and drop it,
+        // so no divergent branch hides the loads' order from the wait counts)
+        const uint32_t tq = threadIdx.x & (D - 1);
+        const float qv = ld_coh(qsrc + tq), kv = ld_coh(ksrc + tq);
+        const float vcol = ld_coh(vsrc + col);
+        const float alpha = ld_coh(a.alpha + h), braw = ld_coh(a.beta + h);
+        const float dtb = gp(a.dt_bias)[h], sa = gp(a.ssm_a)[h];
+        GLB float *srow = gp(a.state + ((size_t)h * D + col) * D + i0);
+        float s[RPT];
+#pragma unroll
+        for (uint32_t r = 0; r < RPT; r += 4) {
+            const f32x4 t = *reinterpret_cast<const GLB f32x4 *>(srow + r);
+            s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
         }
-        sq = block_sum_f64(sq, red);
-        sk = block_sum_f64(sk, red);
+        // l2 norm of q and k (ggml: fp32 squares summed in double,
+        // scale = 1/fmaxf(sqrtf(sum), eps)); both sums in one reduction
+        const bool mine = threadIdx.x < D;
+        double sq = mine ? (double)(qv * qv) : 0.0, sk = mine ? (double)(kv * kv) : 0.0;
+        block_sum2_f64(sq, sk, red);
         if (threadIdx.x < D) {
             qs[threadIdx.x] = qv * (1.0f / fmaxf(sqrtf((float)sq), a.eps));
             ks[threadIdx.x] = kv * (1.0f / fmaxf(sqrtf((float)sk), a.eps));
         }
-        if (threadIdx.x == 0) {
-            const float sp = dev_softplus(ld_coh(a.alpha + h) + gp(a.dt_bias)[h]);
-            gb[0] = (float)exp((double)(sp * gp(a.ssm_a)[h]));
-            gb[1] = dev_sigmoid(ld_coh(a.beta + h));
-        }
+        // gates, in every lane (no broadcast needed) while the state lands
+        const float sp = dev_softplus(alpha + dtb);
+        const float g = (float)exp((double)(sp * sa));
+        const float beta = dev_sigmoid(braw);
         __syncthreads();
         if (ts && item == rel) ts[1] = wall_clock64();
-        const float g = gb[0], beta = gb[1];
 
-        // this thread: column c0 + threadIdx.x / tpc, rows [i0, i0 + rpt)
-        const uint32_t col = c0 + threadIdx.x / tpc;
-        const uint32_t i0 = (threadIdx.x % tpc) * rpt;
-        GLB float *srow = gp(a.state + ((size_t)h * D + col) * D + i0);
-        float s[32];
-#pragma unroll
-        for (uint32_t r = 0; r < 32; r += 4) {
-            if (r < rpt) {
-                const f32x4 t = *reinterpret_cast<const GLB f32x4 *>(srow + r);
-                s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
-            }
-        }
         double dkv = 0.0;
 #pragma unroll
-        for (uint32_t r = 0; r < 32; r++)
-            if (r < rpt) dkv += (double)s[r] * (double)ks[i0 + r];
-        for (uint32_t o = 1; o < tpc; o <<= 1) dkv += __shfl_xor(dkv, (int)o, 64);
+        for (uint32_t r = 0; r < RPT; r++) dkv += (double)s[r] * (double)ks[i0 + r];
+        dkv = lanes_sum_f64(dkv, tpc);
         const float kvf = (float)dkv;
         const float t1 = g * kvf;
-        const float t2 = ld_coh(vsrc + col) - t1;
+        const float t2 = vcol - t1;
         const float delta = t2 * beta;
         double dout = 0.0;
 #pragma unroll
-        for (uint32_t r = 0; r < 32; r++) {
-            if (r < rpt) {
-                const float u1 = g * s[r];
-                const float u2 = ks[i0 + r] * delta;
-                s[r] = u1 + u2;
-                dout += (double)s[r] * (double)qs[i0 + r];
-            }
+        for (uint32_t r = 0; r < RPT; r++) {
+            const float u1 = g * s[r];
+            const float u2 = ks[i0 + r] * delta;
+            s[r] = u1 + u2;
+            dout += (double)s[r] * (double)qs[i0 + r];
         }
-        for (uint32_t o = 1; o < tpc; o <<= 1) dout += __shfl_xor(dout, (int)o, 64);
+        dout = lanes_sum_f64(dout, tpc);
 #pragma unroll
-        for (uint32_t r = 0; r < 32; r += 4)
-            if (r < rpt) {
-                const f32x4 v = {s[r], s[r + 1], s[r + 2], s[r + 3]};
-                *reinterpret_cast<GLB f32x4 *>(srow + r) = v;
-            }
+        for (uint32_t r = 0; r < RPT; r += 4) {
+            const f32x4 v = {s[r], s[r + 1], s[r + 2], s[r + 3]};
+            *reinterpret_cast<GLB f32x4 *>(srow + r) = v;
+        }
         if ((threadIdx.x % tpc) == 0) st_coh(a.o + (size_t)h * D + col, (float)dout * a.scale);
         if (ts && item == rel) ts[2] = wall_clock64();
-        __syncthreads();  // qs/ks/gb reused by the next item
+        __syncthreads();  // qs/ks reused by the next item
+    }
+    };
+    switch (rpt) {
+    case 4: items(std::integral_constant<uint32_t, 4>{}); break;
+    case 8: items(std::integral_constant<uint32_t, 8>{}); break;
+    case 16: items(std::integral_constant<uint32_t, 16>{}); break;
+    default: items(std::integral_constant<uint32_t, 32>{}); break;
     }
 }
 

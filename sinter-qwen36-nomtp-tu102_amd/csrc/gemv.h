@@ -135,6 +135,43 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
+// ggml quantize_row_q8_K_ref element by element for the lane's t[4q + i]
+// (elements 64q + 4r + i of a chunk held by a 16-lane row): the first
+// element reaching the row's max |x| (a (index, sign) key, smallest wins)
+// gives bmax.  Writes b[i] = (int8 code) + 0x4B400000 and returns d.
+__device__ __forceinline__ float quant_q8k_exact(uint32_t r, const float t[16], uint32_t b[16]) {
+    float ax[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) ax[i] = fabsf(t[i]);
+    float am = ax[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) am = fmaxf(am, ax[i]);
+    const float A = row16_max(am);
+    int key = 0x7fffffff;
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = 64 * qq + 4 * (int)r + i;
+            if (ax[4 * qq + i] == A) key = min(key, (e << 1) | (t[4 * qq + i] < 0.0f ? 1 : 0));
+        }
+    const int gkey = row16_min(key);
+    if (!(A > 0.0f)) {    // max |x| == 0 (NaNs never win): all codes 0, d = 0
+#pragma unroll
+        for (int i = 0; i < 16; i++) b[i] = 0x4B400000u;
+        return 0.0f;
+    }
+    const float bmax = (gkey & 1) ? -A : A;
+    const float iscale = -127.f / bmax;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float f = iscale * t[i];
+        const int v = (int)(__float_as_uint(f + 12582912.f) & 0x007fffffu) - 0x00400000;
+        b[i] = (uint32_t)(int32_t)(int8_t)(v < 127 ? v : 127) + 0x4B400000u;   // the stored int8
+    }
+    return 1.0f / iscale;
+}
+
 // Lane r of a 16-lane row holds elements 64q + 4r + i (q, i = 0..3) of its
 // 256-element chunk c: four float4 at 64-element strides, so the 16 lanes of a
 // row read 256 contiguous bytes per q (no LDS bank conflicts) and a Q8_K
@@ -142,61 +179,64 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
 // Quantise the lane's t[4q + i] into the activation layout at q.
 __device__ __forceinline__ void quant_chunk(int vt, uint32_t c, uint32_t r, const float t[16], lds_char *q,
                                             LDS float *qd, LDS int16_t *qb) {
-    int qv[16];
     if (vt == SINTER_Q8_K) {
-        // ggml quantize_row_q8_K_ref: the signed element of largest |x|, first
-        // index wins; q = min(127, rne(x * -127/max)), d = 1/iscale.  The
-        // lane's maximum, first index and its sign come from balanced trees
-        // (short dependency chains); NaNs never win (v_max ignores them, and
-        // they compare unequal).
-        float ax[16];
+        // ggml quantize_row_q8_K_ref: bmax = the signed element of largest |x|
+        // (first index wins; NaNs never win), iscale = -127/bmax,
+        // q = min(127, nearest_int(iscale * x)) with nearest_int's 1.5*2^23
+        // magic add, d = 1/iscale; a chunk with max |x| = 0 gets q = 0, d = 0.
+        // The chunk's signed max mx and min mn fix bmax's sign unless both +A
+        // and -A occur.  For finite x, b = bits(iscale*x + 1.5*2^23) lies in
+        // 0x4B400000 +- 127 and b - 0x4B400000 is the code, so the code byte
+        // is b's low byte and the bsum is the sum of b's minus the bias.  A
+        // wave in which any row has a +-A tie, a non-finite maximum or a b out
+        // of that range (NaN or infinite inputs) recomputes its codes element
+        // by element (quant_q8k_exact), which is exact for every input.
+        float m2[8], n2[8];
 #pragma unroll
-        for (int i = 0; i < 16; i++) ax[i] = fabsf(t[i]);
-        float m4[4];
+        for (int i = 0; i < 8; i++) { m2[i] = fmaxf(t[2 * i], t[2 * i + 1]); n2[i] = fminf(t[2 * i], t[2 * i + 1]); }
 #pragma unroll
-        for (int i = 0; i < 4; i++) m4[i] = fmaxf(fmaxf(ax[4 * i], ax[4 * i + 1]), fmaxf(ax[4 * i + 2], ax[4 * i + 3]));
-        const float am = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-        const float A = row16_max(am);
-        // (group index, sign) keys of the elements reaching A; the smallest wins
-        int key[16];
+        for (int w = 4; w > 0; w >>= 1)
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++)
+            for (int i = 0; i < w; i++) { m2[i] = fmaxf(m2[i], m2[i + w]); n2[i] = fminf(n2[i], n2[i + w]); }
+        const float mx = row16_max(m2[0]), mn = row16_minf(n2[0]);
+        const float A = fmaxf(mx, -mn);
+        const bool zero = A == 0.0f;
+        const float bm = mx > -mn ? mx : mn;
+        const float is = -127.f / bm;
+        const float iscale = zero ? 0.0f : is;
+        uint32_t b[16], hi = 0u, lo = 0xffffffffu;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int e = 64 * qq + 4 * (int)r + i;
-                key[4 * qq + i] = ax[4 * qq + i] == A ? ((e << 1) | (t[4 * qq + i] < 0.0f ? 1 : 0)) : 0x7fffffff;
-            }
-#pragma unroll
-        for (int w = 8; w > 0; w >>= 1)
-#pragma unroll
-            for (int i = 0; i < w; i++) key[i] = min(key[i], key[i + w]);
-        const int gkey = row16_min(key[0]);
-        float dd = 0.0f;
-        if (A != 0.0f) {
-            const float bmax = (gkey & 1) ? -A : A;
-            const float iscale = -127.f / bmax;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int v = (int)__builtin_rintf(iscale * t[i]);
-                qv[i] = v < 127 ? v : 127;
-            }
-            dd = 1.0f / iscale;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) qv[i] = 0;
+        for (int i = 0; i < 16; i++) {
+            const float f = iscale * t[i];
+            b[i] = __float_as_uint(f + 12582912.f);
+            hi = max(hi, b[i]);
+            lo = min(lo, b[i]);
         }
+        float dd = zero ? 0.0f : 1.0f / iscale;
+        const bool bad = !(A <= 3.40282347e38f) || (mx == -mn && !zero) || hi > 0x4B40007Fu || lo < 0x4B3FFF81u;
+        if (__builtin_amdgcn_ballot_w64(bad)) dd = quant_q8k_exact(r, t, b);
 #pragma unroll
         for (int qq = 0; qq < 4; qq++) {
-            *reinterpret_cast<LDS uint32_t *>(q + c * ACT_GSTRIDE + 64 * qq + 4 * r) =
-                pack4_i8(qv[4 * qq], qv[4 * qq + 1], qv[4 * qq + 2], qv[4 * qq + 3]);
-            // bsum of sub-block 4qq + r/4: the four lanes' sums, in a tree
-            int s = (qv[4 * qq] + qv[4 * qq + 1]) + (qv[4 * qq + 2] + qv[4 * qq + 3]);
-            s += dpp_i<DPP_XOR1>(s);
-            s += dpp_i<DPP_XOR2>(s);
-            if ((r & 3) == 0) qb[16 * c + 4 * qq + r / 4] = (int16_t)s;
+            const uint32_t w01 = __builtin_amdgcn_perm(b[4 * qq + 1], b[4 * qq], 0x0c0c0400u);
+            const uint32_t w23 = __builtin_amdgcn_perm(b[4 * qq + 3], b[4 * qq + 2], 0x04000c0cu);
+            *reinterpret_cast<LDS uint32_t *>(q + c * ACT_GSTRIDE + 64 * qq + 4 * r) = w01 | w23;
         }
+        // bsum of sub-block 4qq + r/4: the four lanes r/4 hold it after two
+        // DPP steps; lane r writes the one of qq = r & 3
+        uint32_t s4[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            uint32_t s = (b[4 * qq] + b[4 * qq + 1]) + (b[4 * qq + 2] + b[4 * qq + 3]);
+            s += (uint32_t)dpp_i<DPP_XOR1>((int)s);
+            s += (uint32_t)dpp_i<DPP_XOR2>((int)s);
+            s4[qq] = s;
+        }
+        const uint32_t j = r & 3;
+        const uint32_t sj = j == 0 ? s4[0] : j == 1 ? s4[1] : j == 2 ? s4[2] : s4[3];
+        qb[16 * c + 4 * j + r / 4] = (int16_t)(int32_t)(sj - 16u * 0x4B400000u);
         if (r == 0) qd[c] = dd;
     } else if (vt == SINTER_Q8_0) {
+        int qv[16];
         // ggml-cpu x86 quantize_row_q8_0: d = f16(amax/127), q = rne(x * 127/amax);
         // 32-element block 2q + r/8 is the lane's four elements of each q on
         // the eight lanes r/8

@@ -83,6 +83,36 @@ def test_gemv_plain_matches_oracle(sn, orc, torch_gpu, t, k, rows, blocks):
     assert np.array_equal(host(dy), orc.gemv(t, w, rows, k, x))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_gemv_q8k_quantiser_edge_chunks(sn, orc, torch_gpu, t):
+    """Q8_K activation chunks that leave the quantiser's fast path: +-max ties
+    in either order (first index decides the sign), NaN elements (code 0),
+    a zero chunk holding a NaN and -0.0, ties among small integers; beside
+    them ordinary chunks and one whose maximum is its last element."""
+    torch = torch_gpu
+    k, rows = 2304, 257
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal(k).astype(np.float32)
+    c = [x[256 * i:256 * (i + 1)] for i in range(k // 256)]
+    c[0][17], c[0][200] = -9.0, 9.0          # tie, negative first
+    c[1][3], c[1][4] = 7.5, -7.5             # tie, positive first, same lane
+    c[2][100] = np.nan
+    c[3][:] = 0.0; c[3][9] = -0.0; c[3][77] = np.nan
+    c[4][:] = 0.0
+    c[5][255] = 50.0                         # maximum at the last element
+    c[6][:] = rng.integers(-3, 4, 256)       # many +-3 ties
+    c[7][64], c[7][3] = -6.0, 6.0            # tie across the lane's q groups
+    w = synth_w(sn, t, rows, k, 300 + t)
+    dw, dx, dy = dev(torch, w), dev(torch, x), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    a.x = dx.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=t, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 64)
+    ref = orc.gemv(t, w, rows, k, x)
+    assert np.isfinite(ref).all()
+    assert np.array_equal(host(dy), ref)
+
+
 def test_gemv_rmsnorm_resid_and_multiseg(sn, orc, torch_gpu):
     """attention-style phase: RMSNORM prologue, three segments (Q4_K, Q4_K,
     Q6_K) sharing one Q8_K activation; then an EPI_RESID segment."""
@@ -262,7 +292,10 @@ def test_gemv_argmax_epilogue(sn, orc, torch_gpu):
         sn.lib().sinter_argmax_ws_destroy(ws)
 
 
-def test_gdn_step_matches_oracle(sn, orc, torch_gpu):
+@pytest.mark.parametrize("cols,blocks", [(16, 256), (32, 256), (32, 64), (8, 256)])
+def test_gdn_step_matches_oracle(sn, orc, torch_gpu, cols, blocks):
+    """cols sets the threads summing one state column (256 / cols: 16, 8,
+    32 lanes); blocks=64 makes each workgroup loop over several items."""
     torch = torch_gpu
     HK, HV, D = 16, 32, 128
     rng = np.random.default_rng(19)
@@ -276,12 +309,12 @@ def test_gdn_step_matches_oracle(sn, orc, torch_gpu):
     M = (rng.standard_normal((HV, D, D)) * 0.1).astype(np.float32)
     d = {n: dev(torch, v) for n, v in dict(qkv=qkv, al=al, be=be, dt=dt, A=A, M=M).items()}
     do = empty_f32(torch, HV * D)
-    a = sn.GdnArgs(hk=HK, hv=HV, d=D, cols=16, eps=1e-6, scale=np.float32(1) / np.sqrt(np.float32(D)))
+    a = sn.GdnArgs(hk=HK, hv=HV, d=D, cols=cols, eps=1e-6, scale=np.float32(1) / np.sqrt(np.float32(D)))
     a.qkv, a.alpha, a.beta, a.dt_bias, a.ssm_a = (d["qkv"].data_ptr(), d["al"].data_ptr(), d["be"].data_ptr(),
                                                   d["dt"].data_ptr(), d["A"].data_ptr())
     a.state, a.o = d["M"].data_ptr(), do.data_ptr()
-    print("gdn_step HK=16 HV=32 D=128 cols=16 blocks=256", flush=True)
-    sn.check(sn.lib().sinter_op_gdn_step(C.byref(a), 256, C.c_void_p(stream(torch))), "gdn")
+    print(f"gdn_step HK=16 HV=32 D=128 cols={cols} blocks={blocks}", flush=True)
+    sn.check(sn.lib().sinter_op_gdn_step(C.byref(a), blocks, C.c_void_p(stream(torch))), "gdn")
     torch.cuda.synchronize()
     assert sn.op_error()[0] == 0
     L = orc.lib()
