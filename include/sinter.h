@@ -189,10 +189,9 @@ typedef struct sinter_attn_args {
     const float *k_norm;    /* [HD] */
     uint16_t *kc;           /* K cache f16 [n_ctx][NKV*HD] */
     uint16_t *vc;           /* V cache f16 [n_ctx][NKV*HD] */
-    double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64, then the merge-tree
-                               nodes [NKV][ceil(n_chunks/8)][NQ/NKV][HD+2]; sinter_attn_part_len */
-    uint32_t *count;        /* arrival counters, sinter_attn_count_len words, 0 before first use
-                               (self-resetting) */
+    double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64; sinter_attn_part_len */
+    uint32_t *count;        /* arrival counters, sinter_attn_count_len words, 0 before first use;
+                               monotonic: each call adds n_chunks to words 0..NKV-1 */
     float *out;             /* [NQ*HD] gated attention output */
     const int32_t *pass_cell; /* sinter_pass_cell (pos) */
     uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;
@@ -202,7 +201,10 @@ typedef struct sinter_attn_args {
 
 /* Buffer sizes for sinter_attn_args (n_chunks <= 64): part in doubles,
  * count in 32-bit words.  No counterpart in the reference (its merge reads a
- * fixed 72-way partial array); the split-K merge here is a fan-in-8 tree. */
+ * fixed 72-way partial array).  The op runs one (kv head, chunk) item per
+ * workgroup (blocks >= nkv * n_chunks, all resident: sinter_op_attn_decode
+ * launches cooperatively); the chunks of a kv head wait for each other, then
+ * each merges a slice of the head group's output. */
 size_t   sinter_attn_part_len(uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t n_chunks);
 uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks);
 

@@ -25,6 +25,15 @@ namespace sinter {
 constexpr int ATT_TILE = 32;   // KV positions per LDS tile
 constexpr int ATT_MAXG = 8;    // max q heads per kv head
 
+// Per-pass cache (interpreter only): every attention op of one pass reads the
+// same position from the same pass cell, so the first one of the pass loads
+// it and computes the rope rotation; the others reuse both.  Key: pass
+// index, pos, theta_scale bits, rope_dims, pass cell address (lo, hi); the
+// interpreter invalidates it (key[0] = ~0) at launch.
+__shared__ __attribute__((aligned(16))) float g_att_rot[256];
+__shared__ uint32_t g_att_key[6];
+constexpr uint32_t ATT_NO_CACHE = 0xffffffffu;
+
 // The q heads of a kv group (and, for the chunk that appends, the new k row)
 // normalised and rotated together: y = rmsnorm(x) * w per 256-wide head, then
 // NEOX RoPE on the first rope_dims dims.  Thread t holds dim t of every head.
@@ -33,18 +42,23 @@ constexpr int ATT_MAXG = 8;    // max q heads per kv head
 // whole prologue costs three workgroup barriers.  Rope pair i turns by
 // theta_i = pos * theta_scale^i (repeated fp32 products, as ggml's rope
 // cache), cos/sin evaluated in double and rounded to fp32.
-// x[j] for j < nh are the raw values; rows j < nq use qw, row nq (if nh > nq)
-// uses kw.  Results land in dst[j*256 + t].  LDS: qn [ATT_MAXG+1][256]
-// floats, rot [2][128] floats, red [4][ATT_MAXG+1] doubles.
-__device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t nq, uint32_t nh, const float *qw,
-                                         const float *kw, float eps, int pos, float theta_scale, uint32_t rope_dims,
-                                         LDS float *dst, LDS float *qn, LDS float *rot, LDS double *red) {
+// x[j] for j < nh are the raw values; rows j < nq use qw (this thread's
+// element of the q norm weight), row nq (if nh > nq) uses kw.  Results land
+// in dst[j*256 + t].  LDS: qn [ATT_MAXG+1][256]
+// floats, rot [2][128] floats, red [5][ATT_MAXG+1] doubles.
+__device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t nq, uint32_t nh, float qw, float kw,
+                                         float eps, int pos, float theta_scale, uint32_t rope_dims,
+                                         LDS float *dst, LDS float *qn, LDS float *rot, LDS double *red,
+                                         bool compute_rot) {
     const uint32_t t = threadIdx.x, half = rope_dims / 2;
-    if (t < half) {
+    // cos on wave 0, sin on wave 1 (the two run side by side); skipped when
+    // rot already holds this position's rotation
+    const uint32_t ri = t < 64 ? t : t - 64;
+    if (compute_rot && t < 128 && ri < half) {
         float th = (float)pos;
-        for (uint32_t i = 0; i < t; i++) th *= theta_scale;
-        rot[t] = (float)cos((double)th);
-        rot[128 + t] = (float)sin((double)th);
+        for (uint32_t i = 0; i < ri; i++) th *= theta_scale;
+        if (t < 64) rot[ri] = (float)cos((double)th);
+        else rot[128 + ri] = (float)sin((double)th);
     }
 #pragma unroll
     for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
@@ -55,15 +69,20 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
         }
     }
     __syncthreads();
+    // head j's scale on lane j (one sqrt/divide chain instead of nh in a row)
+    LDS float *hs = reinterpret_cast<LDS float *>(red + 4 * (ATT_MAXG + 1));
+    if (t < nh) {
+        double ss = 0.0;
+        for (int wv = 0; wv < (int)(BLOCK_THREADS / 64); wv++) ss += red[wv * (ATT_MAXG + 1) + t];
+        const float mean = (float)(ss / 256.0);
+        hs[t] = 1.0f / sqrtf(mean + eps);
+    }
+    __syncthreads();
 #pragma unroll
     for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
         if (j < nh) {
-            double ss = 0.0;
-            for (int wv = 0; wv < (int)(BLOCK_THREADS / 64); wv++) ss += red[wv * (ATT_MAXG + 1) + j];
-            const float mean = (float)(ss / 256.0);
-            const float sc = 1.0f / sqrtf(mean + eps);
-            const float nrm = x[j] * sc;
-            qn[j * 256 + t] = nrm * (j < nq ? gp(qw)[t] : gp(kw)[t]);
+            const float nrm = x[j] * hs[j];
+            qn[j * 256 + t] = nrm * (j < nq ? qw : kw);
         }
     }
     __syncthreads();
@@ -85,323 +104,433 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
     __syncthreads();
 }
 
-constexpr uint32_t ATT_FAN = 8;   // partials merged per step of the merge tree
+// Tile-loop thread roles: t = 64 rg + 32 hg + p.  Thread t covers tile rows
+// [8 rg, 8 rg + 8), q head slots [4 hg, 4 hg + 4) and dims [8 p, 8 p + 8):
+// for the scores it holds the slots' q (fp64) for its dims and forms the
+// 8 x 4 partial dot products over them; for V it accumulates the same
+// rows x slots x dims.  Every K/V element of a tile is converted by two
+// threads (the two slot groups), every product appears once.
+constexpr uint32_t ATT_RG = 8, ATT_HG = 4, ATT_DP = 8;
 
-// Merge n (<= ATT_FAN) consecutive partials {acc[HD], m, l} of each of gqa
-// q heads (fp64, coherent reads): M = max m_i, acc = sum_i e_i acc_i,
-// l = sum_i e_i l_i with e_i = exp(m_i - M), in ascending i; a partial with
-// m = -inf contributes nothing.  Thread t owns dim t; every load is issued
-// before the first is used (one memory round trip).  With dst, the merged
-// unnormalised partial goes there; otherwise out = acc/l * sigmoid(gate).
-// ew: LDS scratch of ATT_MAXG * (ATT_FAN + 2) doubles.
-__device__ __forceinline__ void att_merge(const sinter_attn_args &a, const double *src, uint32_t n, uint32_t gqa, uint32_t g,
-                          double *dst, LDS double *ew) {
-    const uint32_t t = threadIdx.x, HD = a.hd, PS = HD + 2;
-    const __amdgpu_buffer_rsrc_t r = coh_rsrc(src, n * gqa * PS * 8);
-    double pv[ATT_MAXG][ATT_FAN], m[ATT_FAN], lv[ATT_FAN];
+// One step of the reduce-scatter of 2N fp64 values over lanes paired by
+// CTRL: a lane with `upper` set keeps v[N..2N), the other v[0..N); each
+// sends the half it does not keep and adds the partner's copy of the half
+// it keeps, into v[0..N).
+template <int CTRL, int N>
+__device__ __forceinline__ void att_rs_step(double v[], bool upper) {
 #pragma unroll
-    for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
-#pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++)
-            pv[hh][i] = (hh < gqa && i < n) ? ld_coh8(r, ((i * gqa + hh) * PS + t) * 8) : 0.0;
-    // weights e[hh][i], the max and l, one lane per q head
-    if (t < gqa) {
-#pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++) {
-            m[i] = i < n ? ld_coh8(r, ((i * gqa + t) * PS + HD) * 8) : -INFINITY;
-            lv[i] = i < n ? ld_coh8(r, ((i * gqa + t) * PS + HD + 1) * 8) : 0.0;
-        }
-        double M = -INFINITY;
-#pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++) M = fmax(M, m[i]);
-        double L = 0.0;
-#pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++) {
-            const double e = (m[i] == -INFINITY) ? 0.0 : exp(m[i] - M);
-            ew[t * (ATT_FAN + 2) + i] = e;
-            if (i < n && e != 0.0) L = fma(e, lv[i], L);
-        }
-        ew[t * (ATT_FAN + 2) + ATT_FAN] = M;
-        ew[t * (ATT_FAN + 2) + ATT_FAN + 1] = L;
+    for (int k = 0; k < N; k++) {
+        const double send = upper ? v[k] : v[k + N];
+        const double keep = upper ? v[k + N] : v[k];
+        v[k] = keep + dpp_d<CTRL>(send);
     }
-    __syncthreads();
+}
+template <int N>
+__device__ __forceinline__ void att_rs_step_x16(double v[], bool upper) {
 #pragma unroll
-    for (uint32_t hh = 0; hh < ATT_MAXG; hh++) {
-        if (hh >= gqa) break;
-        const LDS double *e = ew + hh * (ATT_FAN + 2);
-        double O = 0.0;
-#pragma unroll
-        for (uint32_t i = 0; i < ATT_FAN; i++)
-            if (i < n && e[i] != 0.0) O = fma(e[i], pv[hh][i], O);
-        const double L = e[ATT_FAN + 1];
-        if (dst) {
-            double *d = dst + hh * PS;
-            st_coh(d + t, O);
-            if (t == 0) { st_coh(d + HD, e[ATT_FAN]); st_coh(d + HD + 1, L); }
-        } else {
-            const uint32_t h = g * gqa + hh;
-            const float att = (float)(O / L);
-            const float gate = ld_coh(a.qg + (size_t)h * 2 * HD + HD + t);
-            st_coh(a.out + (size_t)h * HD + t, att * dev_sigmoid(gate));
-        }
+    for (int k = 0; k < N; k++) {
+        const double send = upper ? v[k] : v[k + N];
+        const double keep = upper ? v[k + N] : v[k];
+        v[k] = keep + __shfl_xor(send, 16, 64);
     }
-    settle_vmem();
-    __syncthreads();
 }
 
-// Count one arrival at *cnt of `total`; true (uniform) for the last arriver,
-// which also resets the counter for the next use.
-__device__ __forceinline__ bool att_arrive(uint32_t *cnt, uint32_t total, LDS unsigned *flag) {
-    settle_vmem();   // every wave's partial stores complete before the count
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(gp(cnt), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned last = (old == total - 1) ? 1u : 0u;
-        if (last) __hip_atomic_store(gp(cnt), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last;
+// Wait until the monotonic counter *cnt reaches target (wrap-safe), thread 0
+// only; false on timeout (error raised).
+__device__ __forceinline__ bool att_wait_count(uint32_t *cnt, uint32_t target, uint64_t spin_limit, unsigned *err,
+                                               uint32_t aux) {
+    const uint64_t t0 = wall_clock64();
+    while ((int)(atomic_load_relaxed_agent(cnt) - target) < 0) {
+        __builtin_amdgcn_s_sleep(1);
+        if (wall_clock64() - t0 > spin_limit) {
+            raise_error(err, SINTER_E_TIMEOUT_BARRIER, aux);
+            return false;
+        }
     }
-    __syncthreads();
-    return *flag != 0;
+    return true;
 }
 
-// ts (thread 0, or null): wall clock stamps [1] after the q prep of the
-// first item, [2] after its KV tiles.
-__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts) {
+// ts (thread 0, or null): wall clock stamps [1] after the q prep, [2] after
+// the KV tiles.  spin_limit bounds the wait for the other chunks of the kv
+// head (wall clock ticks).  pass_id: the interpreter's pass index (the
+// per-pass cache above), or ATT_NO_CACHE.
+__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts,
+                                               uint64_t spin_limit, uint32_t pass_id) {
     // the payload, read once into registers: the op stores to the KV cache
     // and the partials, which the compiler cannot tell apart from the payload
     // (every field would be reloaded from memory after each such store)
     const sinter_attn_args a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
-    const int pos = ld_coh(&reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos);
+    const uint32_t pc_lo = (uint32_t)(uintptr_t)a.pass_cell, pc_hi = (uint32_t)((uintptr_t)a.pass_cell >> 32);
+    const bool cached = pass_id != ATT_NO_CACHE && g_att_key[0] == pass_id && g_att_key[4] == pc_lo &&
+                        g_att_key[5] == pc_hi;
+    const int pos = cached ? (int)g_att_key[1] : ld_coh(&reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos);
+    const bool rot_cached = cached && g_att_key[2] == __float_as_uint(a.theta_scale) && g_att_key[3] == a.rope_dims;
     const uint32_t gqa = NKV ? NQ / NKV : 0;
-    const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 &&
-                    C <= ATT_FAN * ATT_FAN &&
-                    a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 && (uint32_t)pos < a.n_ctx;
+    const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 && C <= 64 &&
+                    NKV * C <= nblk && a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 &&
+                    (uint32_t)pos < a.n_ctx;
     if (!ok) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
         return;
     }
+    if (rel >= NKV * C) return;   // one item per workgroup (the merge waits for its kv head's chunks)
     const uint32_t t = threadIdx.x;
-    const uint32_t RW = NKV * HD;
+    const uint32_t RW = NKV * HD, PS = HD + 2;
     const uint32_t n_kv = (uint32_t)pos + 1;
-    uint32_t clen = (n_kv + C - 1) / C;
-    clen = (clen + ATT_TILE - 1) / ATT_TILE * ATT_TILE;
+    const uint32_t clen = (n_kv + C - 1) / C;
 
     // LDS map (the scratch region): K and V tiles double-buffered by LDS-DMA,
-    // q heads (and the new k row), prep scratch, scores, softmax state
+    // q heads (and the new k row), prep scratch, scores -> weights, softmax
+    // corrections; after the tiles the K/V area holds the row-group sums,
+    // then the merge's weights.
     lds_char *L = (lds_char *)g_big;
     LDS uint16_t *kb = reinterpret_cast<LDS uint16_t *>(L);                          // [2][32][256]
     LDS uint16_t *vb = reinterpret_cast<LDS uint16_t *>(L + 2 * ATT_TILE * 512);     // [2][32][256]
     LDS float *qf = reinterpret_cast<LDS float *>(L + 4 * ATT_TILE * 512);           // [gqa][256] q, then the new k row
-    LDS float *qn = qf + (ATT_MAXG + 1) * 256;    // [ATT_MAXG+2][256] raw q / k / v rows, then prep scratch
-    LDS float *rot = qn + (ATT_MAXG + 2) * 256;                                      // [2][128] rope cos | sin
-    LDS double *pred = reinterpret_cast<LDS double *>(rot + 256);                    // [4][ATT_MAXG+1]
-    LDS double *sc = pred + 4 * (ATT_MAXG + 1);                                      // [32][ATT_MAXG] scores -> weights
-    LDS double *mrun = sc + ATT_MAXG * ATT_TILE;                                     // [gqa]
-    LDS double *lrun = mrun + ATT_MAXG;                                              // [gqa]
-    LDS double *corr = lrun + ATT_MAXG;                                              // [gqa]
-    LDS double *ew = corr + ATT_MAXG;                                                // [ATT_MAXG][ATT_FAN+2] merge weights
-    LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(ew + ATT_MAXG * (ATT_FAN + 2));   // [256]
+    LDS float *qn = qf + (ATT_MAXG + 1) * 256;    // [ATT_MAXG+4][256] raw q / k / v rows (then prep scratch), q_norm, k_norm
+    LDS float *rot = (LDS float *)g_att_rot;                                         // [2][128] rope cos | sin
+    LDS double *pred = reinterpret_cast<LDS double *>(qn + (ATT_MAXG + 4) * 256);    // [5][ATT_MAXG+1]
+    LDS double *sc = pred + 5 * (ATT_MAXG + 1);                                      // [ATT_MAXG][32] scores -> weights
+    LDS double *corr = sc + ATT_MAXG * ATT_TILE;                                     // [ATT_MAXG]
+    LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(corr + ATT_MAXG);          // [256]
     LDS uint16_t *vnew = knew + 256;                                                 // [256]
     LDS unsigned *flag = reinterpret_cast<LDS unsigned *>(vnew + 256);
+    LDS double *comb = reinterpret_cast<LDS double *>(L);       // after the tiles: [4 rg][16][64 lanes]
+    LDS double *mw = reinterpret_cast<LDS double *>(L);         // merge: [C][gqa] m, then weights e
+    LDS double *mlv = mw + 64 * ATT_MAXG;                       //        [C][gqa] l
+    LDS double *mM = mlv + 64 * ATT_MAXG;                       //        [ATT_MAXG + gqa]: L at ATT_MAXG + h
+    LDS double *msum = mM + 2 * ATT_MAXG;                       //        [256] per-thread element partials
     const uint32_t w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
     const uint32_t kbase = (uint32_t)(uintptr_t)kb, vbase = (uint32_t)(uintptr_t)vb;
 
-    for (uint32_t item = rel; item < NKV * C; item += nblk) {
-        const uint32_t g = item / C, c = item % C;
-        const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
-        const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
-        const uint32_t ntile = (kv1 - kv0 + ATT_TILE - 1) / ATT_TILE;
-        // Tile j (32 rows of this kv head: 512 B of K and of V each) into
-        // buffer j % 2: each wave DMAs rows 2k, 2k+1 for k = w, w+4, w+8,
-        // w+12 of K and of V (lane l: row 2k + l/32, bytes 16 (l%32) ..);
-        // rows past kv1 re-read row kv1-1 (masked in the scores).
-        auto issue_tile = [&](uint32_t j) {
-            const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
+    const uint32_t g = rel / C, c = rel % C;
+    const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
+    const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
+    const uint32_t ntile = (kv1 - kv0 + ATT_TILE - 1) / ATT_TILE;
+    // Tile j (32 rows of this kv head: 512 B of K and of V each) into
+    // buffer j % 2: each wave DMAs rows 2k, 2k+1 for k = w, w+4, w+8,
+    // w+12 of K and of V (lane l: row 2k + l/32, bytes 16 (l%32) ..);
+    // rows past kv1 re-read row kv1-1 (masked in the scores).
+    auto issue_tile = [&](uint32_t j) {
+        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
 #pragma unroll
-            for (uint32_t kk = 0; kk < 4; kk++) {
-                const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
-                const uint32_t voff = (row * RW + g * HD) * 2 + (lane & 31) * 16;
-                lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
-                lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
-            }
-        };
-        {
-            // The raw q heads g*gqa .. (and, for the owner, the new k and v
-            // rows) by LDS-DMA into qn rows 0..gqa+1, one 1 KiB row per wave
-            // instruction; then the first two tiles.  Every wait is explicit,
-            // so the prep below runs while the tiles still stream in.
-            const uint32_t nraw = owner ? gqa + 2 : gqa;
-            const uint32_t qnbase = (uint32_t)(uintptr_t)qn;
-            for (uint32_t j = w; j < nraw; j += WAVES) {
-                const float *src = j < gqa ? a.qg + (size_t)(g * gqa + j) * 2 * HD
-                                 : j == gqa ? a.k + (size_t)g * HD : a.v + (size_t)g * HD;
-                const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)src);
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)src >> 32));
-                lds_dma16<true>(((uintptr_t)hi << 32) | lo, lane * 16, qnbase + j * 1024);
-            }
-            // this wave's raw-row DMAs, then 8 per tile
-            const uint32_t my_raw = nraw > w ? (nraw - w + WAVES - 1) / WAVES : 0u;
-            if (ntile > 0) issue_tile(0);
-            if (ntile > 1) issue_tile(1);
-            const uint32_t behind = (ntile > 0 ? 8u : 0u) + (ntile > 1 ? 8u : 0u);
-            (void)my_raw;
-            if (behind == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-            else if (behind == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        for (uint32_t kk = 0; kk < 4; kk++) {
+            const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
+            const uint32_t voff = (row * RW + g * HD) * 2 + (lane & 31) * 16;
+            lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
+            lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
+        }
+    };
+    const uint32_t rg = t >> 6, hg = (t >> 5) & 1, p = t & 31;
+    double qd[ATT_HG][ATT_DP];      // q slots 4hg.., dims 8p.. (fp64)
+    double acc[ATT_HG][ATT_DP];     // V sums over this thread's rows
+    double mrun = -INFINITY, lrun = 0.0;   // softmax state of slot t/32 (every lane of the half-wave)
+    {
+        // The raw q heads g*gqa .. (and, for the owner, the new k and v
+        // rows) by LDS-DMA into qn rows 0..gqa+1, the q and k norm weights
+        // into rows ATT_MAXG+2, +3, one 1 KiB row per wave instruction; then
+        // the first two tiles.  Every load before the tiles is a DMA, so the
+        // explicit wait below is exact (a compiler-visible load here would
+        // make the compiler's own wait count the tiles too) and the prep runs
+        // while the tiles still stream in.
+        const uint32_t nraw = owner ? gqa + 2 : gqa;
+        const uint32_t qnbase = (uint32_t)(uintptr_t)qn;
+        if (w < 2) {
+            const float *src = w == 0 ? a.q_norm : a.k_norm;
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)src);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)src >> 32));
+            lds_dma16<false>(((uintptr_t)hi << 32) | lo, lane * 16, qnbase + (ATT_MAXG + 2 + w) * 1024);
+        }
+        for (uint32_t j = w; j < nraw; j += WAVES) {
+            const float *src = j < gqa ? a.qg + (size_t)(g * gqa + j) * 2 * HD
+                             : j == gqa ? a.k + (size_t)g * HD : a.v + (size_t)g * HD;
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)src);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)src >> 32));
+            lds_dma16<true>(((uintptr_t)hi << 32) | lo, lane * 16, qnbase + j * 1024);
+        }
+        if (ntile > 0) issue_tile(0);
+        if (ntile > 1) issue_tile(1);
+        const uint32_t behind = (ntile > 0 ? 8u : 0u) + (ntile > 1 ? 8u : 0u);
+        if (behind == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (behind == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else dma_wait();
+        __syncthreads();
+        float xr[ATT_MAXG + 1];
+#pragma unroll
+        for (uint32_t hh = 0; hh <= ATT_MAXG; hh++) xr[hh] = hh < nraw && hh <= gqa ? qn[hh * 256 + t] : 0.0f;
+        const float vraw = owner ? qn[(gqa + 1) * 256 + t] : 0.0f;
+        const float qwv = qn[(ATT_MAXG + 2) * 256 + t], kwv = qn[(ATT_MAXG + 3) * 256 + t];
+        __syncthreads();
+        att_prep(xr, gqa, owner ? gqa + 1 : gqa, qwv, kwv, a.eps, pos, a.theta_scale, a.rope_dims, qf, qn, rot, pred,
+                 !rot_cached);
+        if (owner) vnew[t] = f2h(vraw);
+        // (att_prep ended with a workgroup barrier: every thread has read the key)
+        if (pass_id != ATT_NO_CACHE && t == 0) {
+            g_att_key[0] = pass_id; g_att_key[1] = (uint32_t)pos; g_att_key[2] = __float_as_uint(a.theta_scale);
+            g_att_key[3] = a.rope_dims; g_att_key[4] = pc_lo; g_att_key[5] = pc_hi;
+        }
+    }
+    if (owner) {
+        const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = vnew[t];
+        knew[t] = kh;
+        st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
+        st_coh(a.vc + (size_t)pos * RW + (size_t)g * HD + t, vh);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < ATT_HG; j++) {
+        const uint32_t hh = ATT_HG * hg + j;
+        const f32x4 q0 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p);
+        const f32x4 q1 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p + 4);
+        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (uint32_t d = 0; d < ATT_DP; d++) {
+            qd[j][d] = hh < gqa ? (double)qv[d] : 0.0;
+            acc[j][d] = 0.0;
+        }
+    }
+    if (ts) ts[1] = wall_clock64();
+
+    for (uint32_t j = 0; j < ntile; j++) {
+        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 256;
+        if (j == 0) {
+            dma_wait();   // (also the owner's cache stores)
+        } else {
+            // tile j landed; tile j+1 (issued last step) may still fly
+            if (j + 1 < ntile) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
             else dma_wait();
-            __syncthreads();
-            float xr[ATT_MAXG + 1];
-#pragma unroll
-            for (uint32_t hh = 0; hh <= ATT_MAXG; hh++) xr[hh] = hh < nraw && hh <= gqa ? qn[hh * 256 + t] : 0.0f;
-            const float vraw = owner ? qn[(gqa + 1) * 256 + t] : 0.0f;
-            __syncthreads();
-            att_prep(xr, gqa, owner ? gqa + 1 : gqa, a.q_norm, a.k_norm, a.eps, pos, a.theta_scale, a.rope_dims, qf,
-                     qn, rot, pred);
-            if (owner) vnew[t] = f2h(vraw);
         }
-        if (owner) {
-            const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = vnew[t];
-            knew[t] = kh;
-            st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
-            st_coh(a.vc + (size_t)pos * RW + (size_t)g * HD + t, vh);
-        }
-        if (ts && item == rel) ts[1] = wall_clock64();
-        if (t < gqa) { mrun[t] = -INFINITY; lrun[t] = 0.0; }
-        double acc[ATT_MAXG];
+        __syncthreads();
+        // scores: partial dots of rows 8rg+i and slots 4hg+jj over dims
+        // 8p..8p+7 (dims ascending), then a reduce-scatter over the 32 lanes
+        // of the half-wave leaves lane p with row 8rg + p/4, slot 4hg + p%4
+        {
+            double part[ATT_RG * ATT_HG];
 #pragma unroll
-        for (int hh = 0; hh < ATT_MAXG; hh++) acc[hh] = 0.0;
-
-        for (uint32_t j = 0; j < ntile; j++) {
-            const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 256;
-            if (j == 0) {
-                dma_wait();   // (also the owner's cache stores)
-            } else {
-                // tile j landed; tile j+1 (issued last step) may still fly
-                if (j + 1 < ntile) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-                else dma_wait();
-            }
-            __syncthreads();
-            // scores: thread (r = t/8, part = t%8) covers dims [32 part, 32 part + 32)
-            // of every q head slot (k converted once); the eight parts are
-            // combined with DPP in the butterfly order (d0+d1)+(d2+d3) + ...
-            // Slots past gqa compute on stale rows and are weighted 0 below.
-            // sc is position-major: sc[r * ATT_MAXG + hh].
-            {
-                const uint32_t r = t >> 3, part = t & 7;
-                const LDS uint16_t *kr = ((owner && t0 + r == (uint32_t)pos) ? knew : kb + bo + r * 256) + part * 32;
-                double kd[32];
+            for (uint32_t i = 0; i < ATT_RG; i++) {
+                const uint32_t r = ATT_RG * rg + i;
+                const LDS uint16_t *kr = ((owner && t0 + r == (uint32_t)pos) ? knew : kb + bo + r * 256) + ATT_DP * p;
+                const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(kr);
+                const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+                double kd[ATT_DP];
 #pragma unroll
-                for (int i = 0; i < 32; i += 8) {
-                    const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(kr + i);
-                    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        kd[i + 2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
-                        kd[i + 2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
-                    }
-                }
-                // dims ascending per head; the eight head chains interleaved
-                double d[ATT_MAXG];
-#pragma unroll
-                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] = 0.0;
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    f32x4 qv[ATT_MAXG];
-#pragma unroll
-                    for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
-                        qv[hh] = reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + part * 32)[i];
-#pragma unroll
-                    for (uint32_t hh = 0; hh < ATT_MAXG; hh++) {
-                        d[hh] = fma((double)qv[hh].x, kd[4 * i], d[hh]);
-                        d[hh] = fma((double)qv[hh].y, kd[4 * i + 1], d[hh]);
-                        d[hh] = fma((double)qv[hh].z, kd[4 * i + 2], d[hh]);
-                        d[hh] = fma((double)qv[hh].w, kd[4 * i + 3], d[hh]);
-                    }
+                for (uint32_t k = 0; k < 4; k++) {
+                    kd[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
+                    kd[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
                 }
 #pragma unroll
-                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_XOR1>(d[hh]);
+                for (uint32_t jj = 0; jj < ATT_HG; jj++) {
+                    double d = 0.0;
 #pragma unroll
-                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_XOR2>(d[hh]);
-#pragma unroll
-                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) d[hh] += dpp_d<DPP_HALF_MIRROR>(d[hh]);
-                // lane `part` stores head slot `part`
-                double mine = d[0];
-#pragma unroll
-                for (uint32_t hh = 1; hh < ATT_MAXG; hh++) mine = part == hh ? d[hh] : mine;
-                sc[r * ATT_MAXG + part] = (t0 + r < kv1) ? mine * (double)a.scale : -INFINITY;
-            }
-            __syncthreads();
-            // online softmax: head slot hh = t/32 over its 32 rows (lane r);
-            // max and sum over the 32 lanes with DPP plus one cross-row step
-            {
-                const uint32_t hh = t / ATT_TILE, r = t % ATT_TILE;
-                const double s = sc[r * ATT_MAXG + hh];
-                double mt = s;
-                mt = fmax(mt, dpp_d<DPP_XOR1>(mt));
-                mt = fmax(mt, dpp_d<DPP_XOR2>(mt));
-                mt = fmax(mt, dpp_d<DPP_HALF_MIRROR>(mt));
-                mt = fmax(mt, dpp_d<DPP_MIRROR>(mt));
-                mt = fmax(mt, __shfl_xor(mt, 16, 64));
-                const double mo = mrun[hh];
-                const double mn = fmax(mo, mt);
-                const double wgt = (s == -INFINITY || hh >= gqa) ? 0.0 : exp(s - mn);
-                double ws = wgt;
-#pragma unroll
-                for (int o = 16; o > 0; o >>= 1) ws += __shfl_xor(ws, o, 64);
-                sc[r * ATT_MAXG + hh] = wgt;
-                if (r == 0 && hh < gqa) {
-                    const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
-                    corr[hh] = cf;
-                    lrun[hh] = lrun[hh] * cf + ws;
-                    mrun[hh] = mn;
+                    for (uint32_t dd = 0; dd < ATT_DP; dd++) d = fma(qd[jj][dd], kd[dd], d);
+                    part[i * ATT_HG + jj] = d;
                 }
             }
-            __syncthreads();
-            // V accumulation: thread t owns dim t; per row, v converted once
-            // and the eight slot weights read as four broadcast 16-byte loads
+            att_rs_step_x16<16>(part, (p & 16) != 0);
+            att_rs_step<DPP_MIRROR, 8>(part, (p & 8) != 0);
+            att_rs_step<DPP_HALF_MIRROR, 4>(part, (p & 4) != 0);
+            att_rs_step<DPP_XOR2, 2>(part, (p & 2) != 0);
+            att_rs_step<DPP_XOR1, 1>(part, (p & 1) != 0);
+            const uint32_t r = ATT_RG * rg + (p >> 2), hh = ATT_HG * hg + (p & 3);
+            sc[hh * ATT_TILE + r] = (t0 + r < kv1) ? part[0] * (double)a.scale : -INFINITY;
+        }
+        __syncthreads();
+        // online softmax: head slot hh = t/32 over its 32 rows (lane r);
+        // max and sum over the 32 lanes with DPP plus one cross-row step
+        {
+            const uint32_t hh = t / ATT_TILE, r = t % ATT_TILE;
+            const double s = sc[hh * ATT_TILE + r];
+            double mt = s;
+            mt = fmax(mt, dpp_d<DPP_XOR1>(mt));
+            mt = fmax(mt, dpp_d<DPP_XOR2>(mt));
+            mt = fmax(mt, dpp_d<DPP_HALF_MIRROR>(mt));
+            mt = fmax(mt, dpp_d<DPP_MIRROR>(mt));
+            mt = fmax(mt, __shfl_xor(mt, 16, 64));
+            const double mo = mrun;
+            const double mn = fmax(mo, mt);
+            const double wgt = (s == -INFINITY || hh >= gqa) ? 0.0 : exp(s - mn);
+            double ws = wgt;
 #pragma unroll
-            for (uint32_t hh = 0; hh < ATT_MAXG; hh++)
-                if (hh < gqa) acc[hh] = acc[hh] * corr[hh];
-#pragma unroll 4
-            for (uint32_t r = 0; r < ATT_TILE; r++) {
-                const LDS uint16_t *vr = (owner && t0 + r == (uint32_t)pos) ? vnew : vb + bo + r * 256;
-                const double v = (double)h2f(vr[t]);
-                typedef double f64x2 __attribute__((ext_vector_type(2)));
-                const LDS f64x2 *w2 = reinterpret_cast<const LDS f64x2 *>(sc + r * ATT_MAXG);
-                f64x2 wv[ATT_MAXG / 2];
+            for (int o = 16; o > 0; o >>= 1) ws += __shfl_xor(ws, o, 64);
+            sc[hh * ATT_TILE + r] = wgt;
+            const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
+            lrun = lrun * cf + ws;
+            mrun = mn;
+            if (r == 0) corr[hh] = cf;
+        }
+        __syncthreads();
+        // V: rows 8rg+i, slots 4hg+jj, dims 8p.. (the weights are broadcast reads)
+        {
 #pragma unroll
-                for (uint32_t k = 0; k < ATT_MAXG / 2; k++) wv[k] = w2[k];
+            for (uint32_t jj = 0; jj < ATT_HG; jj++) {
+                const double cf = corr[ATT_HG * hg + jj];
 #pragma unroll
-                for (uint32_t hh = 0; hh < ATT_MAXG; hh++) acc[hh] = fma(wv[hh / 2][hh % 2], v, acc[hh]);
+                for (uint32_t dd = 0; dd < ATT_DP; dd++) acc[jj][dd] = acc[jj][dd] * cf;
             }
-            __syncthreads();
-            // the tile after next into the buffer just freed
-            if (j + 2 < ntile) issue_tile(j + 2);
-        }
-
-        if (ts && item == rel) ts[2] = wall_clock64();
-        // publish the partial; the merge is a tree of fan-in ATT_FAN over
-        // the chunks, each node merged by the last arriver of its children
-        const uint32_t PS = HD + 2, G1 = (C + ATT_FAN - 1) / ATT_FAN, g1 = c / ATT_FAN;
-        double *pbase = a.part + ((size_t)g * C + c) * gqa * PS;
-        for (uint32_t hh = 0; hh < gqa; hh++) {
-            double *p = pbase + hh * PS;
-            st_coh(p + t, acc[hh]);
-            if (t == 0) { st_coh(p + HD, mrun[hh]); st_coh(p + HD + 1, lrun[hh]); }
-        }
-        const uint32_t n1 = min(ATT_FAN, C - g1 * ATT_FAN);
-        double *lvl1 = a.part + (size_t)NKV * C * gqa * PS;                 // [NKV][G1][gqa][PS]
-        if (att_arrive(a.count + NKV + g * G1 + g1, n1, flag)) {
-            double *node = lvl1 + ((size_t)g * G1 + g1) * gqa * PS;
-            att_merge(a, a.part + ((size_t)g * C + g1 * ATT_FAN) * gqa * PS, n1, gqa, g, G1 > 1 ? node : nullptr, ew);
-            if (G1 > 1 && att_arrive(a.count + g, G1, flag)) {
-                // G1 <= ATT_FAN: the root merges the group nodes
-                att_merge(a, lvl1 + (size_t)g * G1 * gqa * PS, G1, gqa, g, nullptr, ew);
+#pragma unroll
+            for (uint32_t i = 0; i < ATT_RG; i++) {
+                const uint32_t r = ATT_RG * rg + i;
+                const LDS uint16_t *vr = ((owner && t0 + r == (uint32_t)pos) ? vnew : vb + bo + r * 256) + ATT_DP * p;
+                const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(vr);
+                const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+                double wt[ATT_HG];
+#pragma unroll
+                for (uint32_t jj = 0; jj < ATT_HG; jj++) wt[jj] = sc[(ATT_HG * hg + jj) * ATT_TILE + r];
+                double vd[ATT_DP];
+#pragma unroll
+                for (uint32_t k = 0; k < 4; k++) {
+                    vd[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
+                    vd[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
+                }
+#pragma unroll
+                for (uint32_t jj = 0; jj < ATT_HG; jj++)
+#pragma unroll
+                    for (uint32_t dd = 0; dd < ATT_DP; dd++) acc[jj][dd] = fma(wt[jj], vd[dd], acc[jj][dd]);
             }
         }
         __syncthreads();
+        // the tile after next into the buffer just freed
+        if (j + 2 < ntile) issue_tile(j + 2);
     }
+    if (ts) ts[2] = wall_clock64();
+
+    // the chunk's partial: the four row groups' V sums added in order (two
+    // rounds of four dims each through LDS), published with m and l
+    double *pbase = a.part + ((size_t)g * C + c) * gqa * PS;
+    {
+        const uint32_t hh = t >> 5, pp = t & 31;   // output: slot hh, dims 8pp + 4k + 0..3
+#pragma unroll
+        for (uint32_t k = 0; k < 2; k++) {
+            // value (jj, dd) of lane l of row group rg at comb[(rg*16 + jj*4 + dd)*64 + l]:
+            // every write and read instruction touches 64 consecutive doubles
+#pragma unroll
+            for (uint32_t jj = 0; jj < ATT_HG; jj++)
+#pragma unroll
+                for (uint32_t dd = 0; dd < 4; dd++) comb[(rg * 16 + jj * 4 + dd) * 64 + (t & 63)] = acc[jj][4 * k + dd];
+            __syncthreads();
+            // thread (hh, pp) sums row groups 0..3 of wave lane (hh/4)*32 + pp
+            const uint32_t src_lane = (hh / ATT_HG) * 32 + pp, jj = hh % ATT_HG;
+            double o[4];
+#pragma unroll
+            for (uint32_t dd = 0; dd < 4; dd++) {
+                double sum = 0.0;
+#pragma unroll
+                for (uint32_t r4 = 0; r4 < 4; r4++) sum += comb[(r4 * 16 + jj * 4 + dd) * 64 + src_lane];
+                o[dd] = sum;
+            }
+            if (hh < gqa) {
+                double *d = pbase + hh * PS + ATT_DP * pp + 4 * k;
+                st_coh(d, o[0]); st_coh(d + 1, o[1]); st_coh(d + 2, o[2]); st_coh(d + 3, o[3]);
+            }
+            __syncthreads();
+        }
+        if ((t & 31) == 0 && hh < gqa) {
+            st_coh(pbase + hh * PS + HD, mrun);
+            st_coh(pbase + hh * PS + HD + 1, lrun);
+        }
+    }
+
+    // the merge's element mapping (below) and its gates, loaded before the
+    // wait: this workgroup finalises elements [c*ne, ...) of the head
+    // group's gqa*HD outputs, tpe threads per element
+    const uint32_t E = gqa * HD, ne = (E + C - 1) / C, e0 = c * ne, e1 = min(e0 + ne, E);
+    uint32_t tpe = 1;                           // a power of two <= C
+    while (tpe * 2 <= C && tpe * 2 * ne <= BLOCK_THREADS) tpe *= 2;
+    const uint32_t cpt = (C + tpe - 1) / tpe;   // chunks per thread
+    const uint32_t ept = BLOCK_THREADS / tpe;   // elements per pass
+    float gate0 = 0.0f;
+    {
+        const uint32_t el = min(e0 + t / tpe, E - 1);
+        gate0 = ld_coh(a.qg + (size_t)(g * gqa + el / HD) * 2 * HD + HD + el % HD);
+    }
+
+    // wait for the kv head's C chunks (a monotonic counter: each use adds C)
+    settle_vmem();
+    __syncthreads();
+    if (t == 0) {
+        const unsigned old = __hip_atomic_fetch_add(gp(a.count + g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned target = (old / C + 1u) * C;
+        // the last arriver has seen the count complete
+        *flag = (old + 1u == target || att_wait_count(a.count + g, target, spin_limit, err, ins.dbg_node)) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (*flag == 0) return;
+
+    // merge: M = max m_i, acc = sum_i e_i acc_i, l = sum_i e_i l_i with
+    // e_i = exp(m_i - M), chunks ascending (runs of cpt chunks per thread,
+    // the runs then ascending); out = acc/l * sigmoid(gate).  Every load of
+    // the first pass is issued at once: m and l of each (chunk, slot) and
+    // this thread's first eight chunk values.
+    {
+        const __amdgpu_buffer_rsrc_t r = coh_rsrc(a.part + (size_t)g * C * gqa * PS, C * gqa * PS * 8);
+        double vpre[8];
+        {
+            const uint32_t el = min(e0 + t / tpe, e1 - 1), hh = el / HD, dd = el % HD, i0 = (t % tpe) * cpt;
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint32_t i = min(i0 + k, C - 1);
+                vpre[k] = ld_coh8(r, (((size_t)i * gqa + hh) * PS + dd) * 8);
+            }
+        }
+        {
+            // (C*gqa <= 512: two per thread)
+            const uint32_t n = C * gqa, i0 = t, i1 = t + BLOCK_THREADS;
+            const uint32_t j0 = min(i0, n - 1), j1 = min(i1, n - 1);
+            const double m0 = ld_coh8(r, ((size_t)j0 * PS + HD) * 8), l0 = ld_coh8(r, ((size_t)j0 * PS + HD + 1) * 8);
+            const double m1 = ld_coh8(r, ((size_t)j1 * PS + HD) * 8), l1 = ld_coh8(r, ((size_t)j1 * PS + HD + 1) * 8);
+            if (i0 < n) { mw[i0] = m0; mlv[i0] = l0; }
+            if (i1 < n) { mw[i1] = m1; mlv[i1] = l1; }
+        }
+        __syncthreads();
+        // slot h on wave h % 4, chunk i on lane i: M by a wave max, then the
+        // weights e_i and L = sum_i e_i l_i (a wave sum)
+        for (uint32_t h = w; h < gqa; h += WAVES) {
+            const double m = lane < C ? mw[lane * gqa + h] : -INFINITY;
+            double M = m;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) M = fmax(M, __shfl_xor(M, o, 64));
+            const double e = (m == -INFINITY) ? 0.0 : exp(m - M);
+            const double le = (lane < C && e != 0.0) ? e * mlv[lane * gqa + h] : 0.0;
+            const double Ls = wave_sum_f64(le);
+            if (lane < C) mw[lane * gqa + h] = e;
+            if (lane == 0) mM[ATT_MAXG + h] = Ls;
+        }
+        __syncthreads();
+        for (uint32_t eb = e0; eb < e1; eb += ept) {
+            const uint32_t el = eb + t / tpe, sub = t % tpe;
+            const uint32_t elc = min(el, e1 - 1), hh = elc / HD, dd = elc % HD;
+            const uint32_t i0 = sub * cpt, i1 = min(i0 + cpt, C);
+            double O = 0.0;
+            // eight chunks' values per batch, all loads issued first (the
+            // first batch of the first pass is already in flight)
+            for (uint32_t ib = i0; ib < i1; ib += 8) {
+                double v[8];
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++) {
+                    const uint32_t i = min(ib + k, C - 1);
+                    v[k] = (eb == e0 && ib == i0) ? vpre[k] : ld_coh8(r, (((size_t)i * gqa + hh) * PS + dd) * 8);
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < 8; k++) {
+                    const double e = ib + k < i1 ? mw[(ib + k) * gqa + hh] : 0.0;
+                    if (e != 0.0) O = fma(e, v[k], O);
+                }
+            }
+            msum[t] = O;
+            __syncthreads();
+            if (el < e1 && sub == 0) {
+                double tot = 0.0;
+                for (uint32_t s2 = 0; s2 < tpe; s2++) tot += msum[t + s2];
+                const uint32_t h = g * gqa + hh;
+                const float att = (float)(tot / mM[ATT_MAXG + hh]);
+                const float gate = eb == e0 ? gate0 : ld_coh(a.qg + (size_t)h * 2 * HD + HD + dd);
+                st_coh(a.out + (size_t)h * HD + dd, att * dev_sigmoid(gate));
+            }
+            __syncthreads();
+        }
+    }
+    settle_vmem();
 }
 
 }  // namespace sinter

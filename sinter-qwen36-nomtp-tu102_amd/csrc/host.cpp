@@ -308,7 +308,8 @@ static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
     // pageable source: the copy is staged before hipMemcpyAsync returns
     if (!hip_ok(hipMemcpyAsync(slot, &host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream), "op upload"))
         return SINTER_ERR_HIP;
-    if (!hip_ok(launch_op(&slot->ins, &slot->plan, slot->cuts, blocks, err, (hipStream_t)stream), "op launch"))
+    if (!hip_ok(launch_op(&slot->ins, &slot->plan, slot->cuts, blocks, err, (hipStream_t)stream,
+                          kind == SINTER_OP_ATTN_DECODE), "op launch"))
         return SINTER_ERR_HIP;
     return SINTER_OK;
 }
@@ -383,6 +384,11 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
         a->rope_dims > a->hd ||
         a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
         return set_error(SINTER_ERR_ARG, "attn: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
+    // one (kv head, chunk) item per workgroup, all of them resident (the
+    // chunks of a kv head wait for each other before merging)
+    if ((uint64_t)a->nkv * a->n_chunks > blocks)
+        return set_error(SINTER_ERR_ARG, "attn: blocks (%u) must be >= nkv * n_chunks (%u)", blocks,
+                         a->nkv * a->n_chunks);
     return run_one(SINTER_OP_ATTN_DECODE, *a, blocks, stream);
 }
 

@@ -26,7 +26,7 @@ struct InterpCtl {
 };
 
 hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
-                     unsigned *err, hipStream_t s);
+                     unsigned *err, hipStream_t s, bool cooperative);
 hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s);
 hipError_t interp_max_blocks(int *blocks_per_cu);
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,

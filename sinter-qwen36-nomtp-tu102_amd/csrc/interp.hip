@@ -46,6 +46,8 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     // next pass's first instruction.  One copy of each op's code.
     uint32_t pass = 0, i = 0;
     uint64_t t0 = wall_clock64();
+    if (threadIdx.x == 0) g_att_key[0] = ATT_NO_CACHE;   // no attention cache from an earlier launch
+    __syncthreads();
     const bool traced = ctl.trace != nullptr;
     auto stamp = [&](uint32_t ii, uint32_t k, uint64_t v) {
         if (traced && pass == 0 && threadIdx.x == 0) ctl.trace[((size_t)ii * gridDim.x + blockIdx.x) * 4 + k] = v;
@@ -120,7 +122,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
                 if (kind == SINTER_OP_GDN_STEP) op_gdn_step(ins, ctl.err, ts);
-                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode(ins, ctl.err, ts);
+                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode(ins, ctl.err, ts, ctl.spin_limit, pass);
             }
             if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
             stamp(i, 3, wall_clock64());
@@ -140,7 +142,9 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
     switch (ins->kind) {
     case SINTER_OP_GEMV: (void)gemv_op(*ins, plan, cuts, err, nullptr, nullptr); break;
     case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err, nullptr); break;
-    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err, nullptr); break;
+    // (attention launches cooperatively: its chunks of one kv head wait for
+    // each other, bounded by a 2 s spin limit at 100 MHz)
+    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err, nullptr, 200000000ull, ATT_NO_CACHE); break;
     default: break;
     }
 }
@@ -170,7 +174,15 @@ extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type,
 namespace sinter {
 
 hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
-                     unsigned *err, hipStream_t s) {
+                     unsigned *err, hipStream_t s, bool cooperative) {
+    if (cooperative) {
+        const sinter_instr *i = ins_dev;
+        const GemvPlan *pl = plan;
+        const uint32_t *cu = cuts;
+        unsigned *e = err;
+        void *args[] = {(void *)&i, (void *)&pl, (void *)&cu, (void *)&e};
+        return hipLaunchCooperativeKernel((const void *)sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), args, 0, s);
+    }
     hipLaunchKernelGGL(sinter_op_kernel, dim3(blocks), dim3(BLOCK_THREADS), 0, s, ins_dev, plan, cuts, err);
     return hipGetLastError();
 }

@@ -84,6 +84,14 @@ def test_gemv_argument_validation_rejects_before_launch(sn):
     assert L.sinter_op_gdn_step(C.byref(g), 4, None) == sn.ERR_ARG
     t = sn.AttnArgs()
     assert L.sinter_op_attn_decode(C.byref(t), 4, None) == sn.ERR_ARG
+    # a valid shape, but fewer workgroups than (kv head, chunk) items: the
+    # chunks of a kv head wait for each other, so every item needs its own
+    t = sn.AttnArgs(nq=24, nkv=4, hd=256, rope_dims=64, n_ctx=64, n_chunks=16, theta_scale=0.5, eps=1e-6,
+                    scale=0.0625)
+    t.qg = t.k = t.v = t.q_norm = t.k_norm = t.part = t.count = t.out = t.pass_cell = 256
+    t.kc = t.vc = 256
+    assert L.sinter_op_attn_decode(C.byref(t), 63, None) == sn.ERR_ARG
+    assert b"nkv * n_chunks" in L.sinter_last_error()
 
 
 def test_model_config_validation(sn):

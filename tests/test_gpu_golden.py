@@ -51,7 +51,7 @@ def test_gdn_golden(sn, torch_gpu):
     assert np.array_equal(host(do), f["o"])
 
 
-@pytest.mark.parametrize("chunks,blocks", [(1, 2), (4, 8), (9, 5)])
+@pytest.mark.parametrize("chunks,blocks", [(1, 2), (4, 8), (9, 18), (9, 23)])
 def test_attn_golden(sn, torch_gpu, chunks, blocks):
     torch = torch_gpu
     f = load("attn.npz")
@@ -71,6 +71,7 @@ def test_attn_golden(sn, torch_gpu, chunks, blocks):
     sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), blocks, C.c_void_p(stream(torch))), "attn")
     torch.cuda.synchronize()
     assert sn.op_error()[0] == 0
-    assert np.all(host(cnt) == 0)
+    cn = host(cnt)
+    assert np.all(cn[:NKV] == chunks) and np.all(cn[NKV:] == 0)   # monotonic: one arrival per chunk
     assert np.array_equal(host(dK)[pos], f["k_row"]) and np.array_equal(host(dV)[pos], f["v_row"])
     assert_ulp(host(out).reshape(NQ, HD), f["out"], max_ulp=1)

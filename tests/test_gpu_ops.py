@@ -368,7 +368,17 @@ def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), 256, C.c_void_p(stream(torch))), "attn")
     torch.cuda.synchronize()
     assert sn.op_error()[0] == 0
-    assert np.all(host(cnt) == 0)            # counters self-reset
+    cn = host(cnt)
+    assert np.all(cn[:NKV] == chunks) and np.all(cn[NKV:] == 0)   # one arrival per chunk per kv head
+    first = host(out).copy()
+    # a second call continues from the monotonic counters (same inputs: the
+    # appended row is rewritten with the same values) and gives the same output
+    print(f"attn_decode again pos={pos} chunks={chunks}", flush=True)
+    sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), 256, C.c_void_p(stream(torch))), "attn")
+    torch.cuda.synchronize()
+    assert sn.op_error()[0] == 0
+    assert np.all(host(cnt)[:NKV] == 2 * chunks)
+    assert np.array_equal(host(out), first)
     # oracle: norms + rope, append, attention, gate
     L = orc.lib()
     qr = np.zeros((NQ, HD), np.float32)
