@@ -1064,30 +1064,65 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
                 if (rv[w] > bv || (rv[w] == bv && ri[w] < bi)) { bv = rv[w]; bi = ri[w]; }
         }
     }
-    if (any_argmax && threadIdx.x == 0 && rel >= static_cast<sinter_argmax_ws *>(a.epi_ws)->capacity) {
-        raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
-    } else if (any_argmax && threadIdx.x == 0) {
+    if (any_argmax) {
         sinter_argmax_ws *ws = static_cast<sinter_argmax_ws *>(a.epi_ws);
-        st_coh(ws->part_val + rel, bv);
-        st_coh(ws->part_idx + rel, bi);
-        settle_vmem();
-        const unsigned old = __hip_atomic_fetch_add(gp(ws->count), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == nblk - 1) {
+        __shared__ unsigned am_last;
+        if (threadIdx.x == 0) {
+            am_last = 0;
+            if (rel >= ws->capacity) {
+                raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
+            } else {
+                st_coh(ws->part_val + rel, bv);
+                st_coh(ws->part_idx + rel, bi);
+                settle_vmem();
+                const unsigned old = __hip_atomic_fetch_add(gp(ws->count), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                am_last = old == nblk - 1 ? 1u : 0u;
+            }
+        }
+        __syncthreads();
+        if (am_last) {
+            // the last arriver reduces the nblk partials: every load at once
+            // (thread t takes t, t+256, ...), then lanes and waves combined;
+            // larger value wins, then the smaller index (NaNs never win: each
+            // lane starts from -inf)
             float best = -INFINITY;
             int32_t bidx = 0x7fffffff;
             const __amdgpu_buffer_rsrc_t vr = coh_rsrc(ws->part_val, nblk * 4), ir = coh_rsrc(ws->part_idx, nblk * 4);
-            for (uint32_t w = 0; w < nblk; w++) {
-                const float v = ld_coh4b(vr, w * 4);
-                const int32_t i = __float_as_int(ld_coh4b(ir, w * 4));
-                if (v > best || (v == best && i < bidx)) { best = v; bidx = i; }
+            float pv[PLAN_MAX_BLOCKS / BLOCK_THREADS];
+            int32_t pi[PLAN_MAX_BLOCKS / BLOCK_THREADS];
+#pragma unroll
+            for (uint32_t k = 0; k < PLAN_MAX_BLOCKS / BLOCK_THREADS; k++) {
+                const uint32_t w = min(threadIdx.x + k * BLOCK_THREADS, nblk - 1);
+                pv[k] = ld_coh4b(vr, w * 4);
+                pi[k] = __float_as_int(ld_coh4b(ir, w * 4));
             }
-            sinter_pass_cell *pc = reinterpret_cast<sinter_pass_cell *>(ws->pass_cell);
-            const int32_t steps = ld_coh(&pc->steps);
-            if (ws->history && (uint32_t)steps < ws->history_cap) st_coh(ws->history + steps, bidx);
-            st_coh(&pc->steps, steps + 1);
-            st_coh(&pc->token, bidx);
-            st_coh(&pc->pos, ld_coh(&pc->pos) + 1);
-            __hip_atomic_store(gp(ws->count), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (uint32_t k = 0; k < PLAN_MAX_BLOCKS / BLOCK_THREADS; k++) {
+                const bool in = threadIdx.x + k * BLOCK_THREADS < nblk;
+                if (in && (pv[k] > best || (pv[k] == best && pi[k] < bidx))) { best = pv[k]; bidx = pi[k]; }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(best, o, 64);
+                const int32_t oi = __shfl_xor(bidx, o, 64);
+                if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+            }
+            LDS float *rv = reinterpret_cast<LDS float *>((LDS double *)g_part);
+            LDS int32_t *ri = reinterpret_cast<LDS int32_t *>((LDS double *)g_part + 4);
+            __syncthreads();
+            if (lane_id() == 0) { rv[wave_id()] = best; ri[wave_id()] = bidx; }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                for (int w = 1; w < (int)WAVES; w++)
+                    if (rv[w] > best || (rv[w] == best && ri[w] < bidx)) { best = rv[w]; bidx = ri[w]; }
+                sinter_pass_cell *pc = reinterpret_cast<sinter_pass_cell *>(ws->pass_cell);
+                const int32_t steps = ld_coh(&pc->steps);
+                if (ws->history && (uint32_t)steps < ws->history_cap) st_coh(ws->history + steps, bidx);
+                st_coh(&pc->steps, steps + 1);
+                st_coh(&pc->token, bidx);
+                st_coh(&pc->pos, ld_coh(&pc->pos) + 1);
+                __hip_atomic_store(gp(ws->count), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     __syncthreads();
