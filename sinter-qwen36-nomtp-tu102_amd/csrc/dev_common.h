@@ -322,43 +322,54 @@ __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" :
 
 // ---------------------------------------------------------------- grid barrier
 
-// Grid barrier, two-level, over monotonic counters (zeroed before the
-// launch): workgroup w counts into group counter w/16 (its own 128-byte
-// line); the group's last arriver counts into the root; every workgroup's
-// thread 0 spins on the root until epoch*groups arrivals.  Sixteen arrivals
-// per line instead of the whole grid on one line (atomics to one address
-// serialise at the memory side).  No cache writeback or invalidate: every
-// wave first waits for its own memory operations, and all data that crosses
-// workgroups moves through device-coherent loads and stores (dev_common.h).
-// Split in two so that work that does not depend on the barrier (the next
-// GEMV's first weight tiles) can be issued between arriving and waiting.
-__device__ __forceinline__ void grid_arrive(unsigned *bar, unsigned *groups, unsigned &epoch) {
+// Grid barrier over per-workgroup flags (zeroed before the launch, packed 4
+// bytes apart after the barrier cells): workgroup w stores its epoch into
+// flag w (a plain device-coherent store, no atomic and no reply to wait
+// for); wave 0 of every workgroup polls all flags at once -- one 16-byte
+// load per lane covers 256 workgroups -- until each holds at least the
+// epoch.  The arrival costs one store, the release one load round trip.  No
+// cache writeback or invalidate: every wave first waits for its own memory
+// operations, and all data that crosses workgroups moves through
+// device-coherent loads and stores (dev_common.h).  Split in two so that work
+// that does not depend on the barrier (the next GEMV's first weight slots) can
+// be issued between arriving and waiting.  `flags` holds gridDim.x words
+// (<= 1024).
+__device__ __forceinline__ void grid_arrive(unsigned *flags, unsigned &epoch) {
     settle_vmem();
     __syncthreads();
     epoch += 1;
-    if (threadIdx.x == 0) {
-        const unsigned g = blockIdx.x >> 4;
-        const unsigned gsize = min(16u, gridDim.x - g * 16u);
-        const unsigned old = __hip_atomic_fetch_add(gp(groups + g * 32u), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == epoch * gsize) __hip_atomic_fetch_add(gp(bar), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (threadIdx.x == 0) __hip_atomic_store(gp(flags + blockIdx.x), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Returns false on timeout.
-__device__ __forceinline__ bool grid_wait(unsigned *bar, unsigned epoch, uint64_t spin_limit_ticks, unsigned *err) {
+// Returns false on timeout (after spin_limit_ticks < 2^32 wall clock ticks).
+__device__ __forceinline__ bool grid_wait(const unsigned *flags, unsigned epoch, uint64_t spin_limit_ticks,
+                                          unsigned *err) {
     __shared__ unsigned timed_out;
-    if (threadIdx.x == 0) {
-        timed_out = 0;
-        const unsigned target = epoch * ((gridDim.x + 15u) >> 4);
+    if (threadIdx.x < 64) {
+        const uint32_t n = gridDim.x, lane = threadIdx.x;
+        const __amdgpu_buffer_rsrc_t r = coh_rsrc(flags, n * 4);
         const uint64_t t0 = wall_clock64();
-        while ((int)(atomic_load_relaxed_agent(bar) - target) < 0) {
+        unsigned to = 0;
+        while (true) {
+            bool ok = true;
+            for (uint32_t base = 0; base < n; base += 256) {
+                const uint32_t i = base + lane * 4;
+                const float4 f4 = ld_coh16(r, i * 4);   // past n: zeros, skipped below
+                const unsigned fv[4] = {__float_as_uint(f4.x), __float_as_uint(f4.y), __float_as_uint(f4.z),
+                                        __float_as_uint(f4.w)};
+#pragma unroll
+                for (int k = 0; k < 4; k++) ok = ok && (i + k >= n || (int)(fv[k] - epoch) >= 0);
+            }
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
             __builtin_amdgcn_s_sleep(1);
-            if (wall_clock64() - t0 > spin_limit_ticks) {
-                raise_error(err, SINTER_E_TIMEOUT_BARRIER, epoch);
-                timed_out = 1;
+            const uint32_t el = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wall_clock64() - t0));
+            if (el > spin_limit_ticks) {
+                if (lane == 0) raise_error(err, SINTER_E_TIMEOUT_BARRIER, epoch);
+                to = 1;
                 break;
             }
         }
+        if (lane == 0) timed_out = to;
     }
     __syncthreads();
     return timed_out == 0;

@@ -958,7 +958,7 @@ __device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)
 // The grid barrier the op may be fused with (interp.hip): crossed after the
 // first weight slots are issued.  arrive/wait are the interpreter's.
 struct GridCross {
-    unsigned *bar, *groups, *err;
+    unsigned *flags, *err;
     unsigned *epoch;
     uint64_t spin_limit;
     bool pass_end;              // sample the error cell after the wait
@@ -985,9 +985,9 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     u32x4 pf[PF_MAX];
     uint32_t sh[4] = {0, 0, 0, 0};
     if (gx) {
-        grid_arrive(gx->bar, gx->groups, *gx->epoch);   // publishes g_args too
+        grid_arrive(gx->flags, *gx->epoch);   // publishes g_args too
         issue_pre(pf, sh, run, (uint64_t)plan);
-        const bool crossed = grid_wait(gx->bar, *gx->epoch, gx->spin_limit, gx->err);
+        const bool crossed = grid_wait(gx->flags, *gx->epoch, gx->spin_limit, gx->err);
         gx->t_wait_end = wall_clock64();
         if (!crossed) { settle_vmem(); return false; }
         if (gx->pass_end) {

@@ -482,8 +482,8 @@ int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k
 
 // ----------------------------------------------------------------- host control plane
 
-// control cells: barrier root, error cell, pass cell, then the barrier group
-// counters for up to 64 groups (1024 workgroups)
+// control cells: error cell, pass cell, then the grid barrier's flags (one
+// word per workgroup, up to 1024; the region is 8 KiB)
 static constexpr size_t CELL_GROUPS = 4096, CELL_GROUP_BYTES = 64 * 128, CELL_BYTES = CELL_GROUPS + CELL_GROUP_BYTES;
 
 struct sinter_host {
@@ -493,8 +493,8 @@ struct sinter_host {
     GemvPlan *d_plans = nullptr;          // [n_instr]
     uint32_t *d_cuts = nullptr;           // [n_instr][PLAN_CUTS]
     uint32_t n_instr = 0, epoch_stride = 0;
-    unsigned *d_cells = nullptr;          // [0] barrier root | [32] err[2] | byte 1024 pass cell |
-                                          // byte CELL_GROUPS: barrier group counters (128 B each)
+    unsigned *d_cells = nullptr;          // [32] err[2] | byte 1024 pass cell |
+                                          // byte CELL_GROUPS: grid barrier flags (4 B per workgroup)
     sinter_pass_cell *d_pass = nullptr;
     int32_t *d_history = nullptr;
     uint32_t history_cap = 0;
@@ -515,8 +515,7 @@ struct sinter_host {
 static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     InterpCtl ctl;
     std::memset(&ctl, 0, sizeof ctl);
-    ctl.bar = h->d_cells;
-    ctl.groups = h->d_cells + CELL_GROUPS / 4;
+    ctl.flags = h->d_cells + CELL_GROUPS / 4;
     ctl.err = h->d_cells + 32;
     ctl.pass_cycles = h->d_pass_cycles;
     ctl.pass_cycles_cap = h->pass_cycles_cap;
@@ -529,8 +528,7 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     ctl.cuts = h->d_cuts;
     ctl.n_instr = h->n_instr;
     ctl.n_passes = n_passes;
-    if (!hip_ok(hipMemsetAsync(h->d_cells, 0, 4, h->stream), "barrier reset") ||
-        !hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream), "barrier groups reset"))
+    if (!hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream), "barrier flags reset"))
         return SINTER_RUN_ERR;
     if (!hip_ok(hipEventRecord(h->ev0, h->stream), "event")) return SINTER_RUN_ERR;
     if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream), "cooperative launch")) return SINTER_RUN_ERR;

@@ -10,8 +10,7 @@ namespace sinter {
 
 // Kernel-side control block of one interpreter launch (core/interp.cuh:60-75)
 struct InterpCtl {
-    unsigned *bar;            // grid barrier root counter, zeroed before the launch
-    unsigned *groups;         // grid barrier group counters (one 128-byte line per 16 workgroups), zeroed
+    unsigned *flags;          // grid barrier flags, one word per workgroup, zeroed before the launch
     unsigned *err;            // [0] code, [1] aux
     long long *pass_cycles;   // ring of per-pass durations (wall clock ticks), or null
     long long *op_cycles;     // per-kind durations on block 0, or null

@@ -62,7 +62,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                                blockIdx.x < prog[nx].block_hi;
             const uint64_t s = timed ? wall_clock64() : 0;
             GridCross gx;
-            gx.bar = ctl.bar; gx.groups = ctl.groups; gx.err = ctl.err; gx.epoch = &epoch;
+            gx.flags = ctl.flags; gx.err = ctl.err; gx.epoch = &epoch;
             gx.spin_limit = ctl.spin_limit; gx.pass_end = pass_end; gx.t0 = t0; gx.t_wait_end = 0;
             gx.pass_slot = (pass_end && blockIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
                                ? ctl.pass_cycles + (ctl.pass_base + pass) % ctl.pass_cycles_cap
@@ -75,8 +75,8 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 if (ts) ts[3] = wall_clock64();
             } else {
                 stamp(i, 0, wall_clock64());
-                grid_arrive(ctl.bar, ctl.groups, epoch);
-                if (!grid_wait(ctl.bar, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
+                grid_arrive(ctl.flags, epoch);
+                if (!grid_wait(ctl.flags, epoch, ctl.spin_limit, ctl.err)) { settle_vmem(); return; }
                 gx.t_wait_end = wall_clock64();
                 if (pass_end) {
                     // a uniform error sample after everyone finished the pass
