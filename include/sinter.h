@@ -190,8 +190,8 @@ typedef struct sinter_attn_args {
     uint16_t *kc;           /* K cache f16 [n_ctx][NKV*HD] */
     uint16_t *vc;           /* V cache f16 [n_ctx][NKV*HD] */
     double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64; sinter_attn_part_len */
-    uint32_t *count;        /* arrival counters, sinter_attn_count_len words, 0 before first use;
-                               monotonic: each call adds n_chunks to words 0..NKV-1 */
+    uint32_t *count;        /* per-(kv head, chunk) generation flags, sinter_attn_count_len words,
+                               0 before first use; each call adds 1 to each of the NKV*n_chunks */
     float *out;             /* [NQ*HD] gated attention output */
     const int32_t *pass_cell; /* sinter_pass_cell (pos) */
     uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;

@@ -135,19 +135,25 @@ __device__ __forceinline__ void att_rs_step_x16(double v[], bool upper) {
     }
 }
 
-// Wait until the monotonic counter *cnt reaches target (wrap-safe), thread 0
-// only; false on timeout (error raised).
-__device__ __forceinline__ bool att_wait_count(uint32_t *cnt, uint32_t target, uint64_t spin_limit, unsigned *err,
-                                               uint32_t aux) {
+// Wave 0: wait until each of the n (<= 64) generation flags at f holds at
+// least target (wrap-safe); lane l polls flag l, one round trip per round.
+// False on timeout (error raised); the result is wave-uniform.
+__device__ __forceinline__ bool att_wait_flags(const uint32_t *f, uint32_t n, uint32_t target, uint64_t spin_limit,
+                                               unsigned *err, uint32_t aux) {
+    const uint32_t lane = lane_id();
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(f, n * 4);
     const uint64_t t0 = wall_clock64();
-    while ((int)(atomic_load_relaxed_agent(cnt) - target) < 0) {
+    while (true) {
+        bool ok = true;
+        if (lane < n) ok = (int)(__float_as_uint(ld_coh4b(r, lane * 4)) - target) >= 0;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
         __builtin_amdgcn_s_sleep(1);
-        if (wall_clock64() - t0 > spin_limit) {
-            raise_error(err, SINTER_E_TIMEOUT_BARRIER, aux);
+        const uint32_t el = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wall_clock64() - t0));
+        if (el > spin_limit) {
+            if (lane == 0) raise_error(err, SINTER_E_TIMEOUT_BARRIER, aux);
             return false;
         }
     }
-    return true;
 }
 
 // ts (thread 0, or null): wall clock stamps [1] after the q prep, [2] after
@@ -176,6 +182,8 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
         return;
     }
     if (rel >= NKV * C) return;   // one item per workgroup (the merge waits for its kv head's chunks)
+    // this chunk's generation flag (written only by this item, once per call)
+    const uint32_t gen = ld_coh(a.count + rel);
     const uint32_t t = threadIdx.x;
     const uint32_t RW = NKV * HD, PS = HD + 2;
     const uint32_t n_kv = (uint32_t)pos + 1;
@@ -445,14 +453,15 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
         gate0 = ld_coh(a.qg + (size_t)(g * gqa + el / HD) * 2 * HD + HD + el % HD);
     }
 
-    // wait for the kv head's C chunks (a monotonic counter: each use adds C)
+    // wait for the kv head's C chunks: each publishes generation gen + 1 in
+    // its own flag (one store, after its partial's stores completed) and
+    // waits for all C flags of the head
     settle_vmem();
     __syncthreads();
-    if (t == 0) {
-        const unsigned old = __hip_atomic_fetch_add(gp(a.count + g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned target = (old / C + 1u) * C;
-        // the last arriver has seen the count complete
-        *flag = (old + 1u == target || att_wait_count(a.count + g, target, spin_limit, err, ins.dbg_node)) ? 1u : 0u;
+    if (t < 64) {
+        if (t == 0) st_coh(a.count + rel, gen + 1u);
+        const bool okw = att_wait_flags(a.count + g * C, C, gen + 1u, spin_limit, err, ins.dbg_node);
+        if (t == 0) *flag = okw ? 1u : 0u;
     }
     __syncthreads();
     if (*flag == 0) return;

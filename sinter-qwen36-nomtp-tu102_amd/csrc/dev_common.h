@@ -347,14 +347,16 @@ __device__ __forceinline__ bool grid_wait(const unsigned *flags, unsigned epoch,
     __shared__ unsigned timed_out;
     if (threadIdx.x < 64) {
         const uint32_t n = gridDim.x, lane = threadIdx.x;
-        const __amdgpu_buffer_rsrc_t r = coh_rsrc(flags, n * 4);
+        // (the range a whole number of 16-byte loads: the region past the
+        // flags is zeroed too, and those words are skipped below)
+        const __amdgpu_buffer_rsrc_t r = coh_rsrc(flags, ((n + 3u) & ~3u) * 4);
         const uint64_t t0 = wall_clock64();
         unsigned to = 0;
         while (true) {
             bool ok = true;
             for (uint32_t base = 0; base < n; base += 256) {
                 const uint32_t i = base + lane * 4;
-                const float4 f4 = ld_coh16(r, i * 4);   // past n: zeros, skipped below
+                const float4 f4 = ld_coh16(r, i * 4);
                 const unsigned fv[4] = {__float_as_uint(f4.x), __float_as_uint(f4.y), __float_as_uint(f4.z),
                                         __float_as_uint(f4.w)};
 #pragma unroll

@@ -373,7 +373,7 @@ size_t sinter_attn_part_len(uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t n_c
 }
 
 uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks) {
-    return nkv * (1 + (n_chunks + 7) / 8);
+    return nkv * n_chunks;
 }
 
 int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream) {

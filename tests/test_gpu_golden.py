@@ -71,7 +71,6 @@ def test_attn_golden(sn, torch_gpu, chunks, blocks):
     sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), blocks, C.c_void_p(stream(torch))), "attn")
     torch.cuda.synchronize()
     assert sn.op_error()[0] == 0
-    cn = host(cnt)
-    assert np.all(cn[:NKV] == chunks) and np.all(cn[NKV:] == 0)   # monotonic: one arrival per chunk
+    assert np.all(host(cnt) == 1)            # every (kv head, chunk) flag at generation 1
     assert np.array_equal(host(dK)[pos], f["k_row"]) and np.array_equal(host(dV)[pos], f["v_row"])
     assert_ulp(host(out).reshape(NQ, HD), f["out"], max_ulp=1)
