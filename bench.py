@@ -52,10 +52,13 @@ def bytes_per_token(cfg, m, n_attended):
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_e2e_q4km_ctx4096.md")
 
 
-def measured_traffic(passes_per_launch):
+def measured_traffic(passes_per_launch, quant, ctx):
     """HBM bytes per launch of the interpreter, from the committed counter
     summary (FETCH_SIZE + WRITE_SIZE per pass, scaled against a copy kernel of
-    known size), or None when no summary exists."""
+    known size), or None when no summary exists or the run is not the
+    summarised workload (q4_k_m weights, 4096-token context)."""
+    if quant != "q4_k_m" or ctx != 4096:
+        return None
     try:
         with open(TRAFFIC_SUMMARY) as f:
             for line in f:
@@ -179,13 +182,13 @@ def main():
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if args.quant == "q4_k_m" else "bf16",
-        "data": "synthetic (seeded random-init weights and 4096-token synthetic KV/recurrent state)",
+        "data": f"synthetic (seeded random-init weights and {args.ctx}-token synthetic KV/recurrent state)",
         "config": {"workload": f"e2e greedy decode, Qwen3.6-27B-shaped hybrid (48 GDN + 16 attention), "
                                f"{args.quant} weights, {args.ctx}-token context",
                    "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl),
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl, args.quant, args.ctx),
                      "kernel": "sinter_interp", "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},

@@ -83,6 +83,25 @@ def test_gemv_plain_matches_oracle(sn, orc, torch_gpu, t, k, rows, blocks):
     assert np.array_equal(host(dy), orc.gemv(t, w, rows, k, x))
 
 
+def test_gemv_q8_0_full_shape(sn, orc, torch_gpu):
+    """The single-op GEMV configuration at its full shape: Q8_0 W[17408][5120]
+    (codes uniform in [-127, 127], scales f16(|N(0, 0.02)|)), x ~ N(0, 1);
+    bit-exact with the oracle (the pass bar is rel L2 <= 1e-5)."""
+    torch = torch_gpu
+    k, rows = 5120, 17408
+    w = synth_w(sn, Q8_0, rows, k, 4242, cfg1=True)
+    x = np.random.default_rng(4243).standard_normal(k).astype(np.float32)
+    dw, dx, dy = dev(torch, w), dev(torch, x), empty_f32(torch, rows)
+    a = sn.GemvArgs(K=k, pro=sn.PRO_PLAIN, n_seg=1, eps=1e-6)
+    a.x = dx.data_ptr()
+    a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dy.data_ptr(), rows=rows, type=Q8_0, epi=sn.EPI_STORE)
+    run_gemv(sn, torch, a, 256)
+    ref = orc.gemv(Q8_0, w, rows, k, x)
+    got = host(dy)
+    assert np.linalg.norm(got - ref) <= 1e-5 * np.linalg.norm(ref)
+    assert np.array_equal(got, ref)
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
 def test_gemv_q8k_quantiser_edge_chunks(sn, orc, torch_gpu, t):
     """Q8_K activation chunks that leave the quantiser's fast path: +-max ties
@@ -337,7 +356,8 @@ def test_gdn_step_matches_oracle(sn, orc, torch_gpu, cols, blocks):
 
 @pytest.mark.parametrize("pos,n_ctx,chunks", [(0, 64, 64), (5, 4096, 64), (1000, 4096, 64), (4095, 4096, 64),
                                               (4095, 4096, 7), (40000, 40960, 64), (300, 4096, 1),
-                                              (2000, 4096, 9), (3000, 4096, 17)])
+                                              (2000, 4096, 9), (3000, 4096, 17), (32767, 32768, 64),
+                                              (131071, 131072, 64)])
 def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     torch = torch_gpu
     NQ, NKV, HD = 24, 4, 256
