@@ -112,27 +112,26 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
 // threads (the two slot groups), every product appears once.
 constexpr uint32_t ATT_RG = 8, ATT_HG = 4, ATT_DP = 8;
 
-// One step of the reduce-scatter of 2N fp64 values over lanes paired by
-// CTRL: a lane with `upper` set keeps v[N..2N), the other v[0..N); each
-// sends the half it does not keep and adds the partner's copy of the half
-// it keeps, into v[0..N).
-template <int CTRL, int N>
-__device__ __forceinline__ void att_rs_step(double v[], bool upper) {
-#pragma unroll
-    for (int k = 0; k < N; k++) {
-        const double send = upper ? v[k] : v[k + N];
-        const double keep = upper ? v[k + N] : v[k];
-        v[k] = keep + dpp_d<CTRL>(send);
-    }
+// Reduce-scatter of 32 fp64 partials over the 32 lanes of a half-wave
+// without selects: lane p keeps its partials permuted, physical slot k
+// holding logical index k ^ att_perm(p), where att_perm is the GF(2)-linear
+// map taking the lane bits (1, 2, 4, 8, 16) to (1, 2, 7, 12, 16).  Every step
+// then pairs each lane with one whose permutation differs by exactly the
+// half being folded -- xor 16 (a shuffle), the row mirror (p ^ 15 within the
+// row, whose image differs by 8), the half-row mirror (p ^ 7: by 4), xor 2,
+// xor 1 -- so all lanes add the partner's upper half to their lower half:
+// v[k] += partner's v[k + N].  Lane p ends with logical index att_perm(p).
+__device__ __forceinline__ uint32_t att_perm(uint32_t p) {
+    return (p & 16u) | ((p & 1u) ? 1u : 0u) ^ ((p & 2u) ? 2u : 0u) ^ ((p & 4u) ? 7u : 0u) ^ ((p & 8u) ? 12u : 0u);
 }
-template <int N>
-__device__ __forceinline__ void att_rs_step_x16(double v[], bool upper) {
+template <int CTRL, int N>
+__device__ __forceinline__ void att_rs_step(double v[]) {
 #pragma unroll
-    for (int k = 0; k < N; k++) {
-        const double send = upper ? v[k] : v[k + N];
-        const double keep = upper ? v[k + N] : v[k];
-        v[k] = keep + __shfl_xor(send, 16, 64);
-    }
+    for (int k = 0; k < N; k++) v[k] = v[k] + dpp_d<CTRL>(v[k + N]);
+}
+__device__ __forceinline__ void att_rs_step_x16(double v[]) {
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = v[k] + __shfl_xor(v[k + 16], 16, 64);
 }
 
 // Wave 0: wait until each of the n (<= 64) generation flags at f holds at
@@ -231,8 +230,8 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
             lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
         }
     };
-    const uint32_t rg = t >> 6, hg = (t >> 5) & 1, p = t & 31;
-    double qd[ATT_HG][ATT_DP];      // q slots 4hg.., dims 8p.. (fp64)
+    const uint32_t rg = t >> 6, hg = (t >> 5) & 1, p = t & 31, mp = att_perm(p);
+    double qd[ATT_HG][ATT_DP];      // q slots 4hg + (j ^ mp%4), dims 8p.. (fp64)
     double acc[ATT_HG][ATT_DP];     // V sums over this thread's rows
     double mrun = -INFINITY, lrun = 0.0;   // softmax state of slot t/32 (every lane of the half-wave)
     {
@@ -288,7 +287,7 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     }
 #pragma unroll
     for (uint32_t j = 0; j < ATT_HG; j++) {
-        const uint32_t hh = ATT_HG * hg + j;
+        const uint32_t hh = ATT_HG * hg + (j ^ (mp & 3));
         const f32x4 q0 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p);
         const f32x4 q1 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p + 4);
         const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
@@ -310,14 +309,15 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
             else dma_wait();
         }
         __syncthreads();
-        // scores: partial dots of rows 8rg+i and slots 4hg+jj over dims
-        // 8p..8p+7 (dims ascending), then a reduce-scatter over the 32 lanes
-        // of the half-wave leaves lane p with row 8rg + p/4, slot 4hg + p%4
+        // scores: partial dots over dims 8p..8p+7 (ascending) of rows
+        // 8rg + (i ^ mp/4) and slots 4hg + (jj ^ mp%4) in slot i*4 + jj (the
+        // permuted order above), then the reduce-scatter over the 32 lanes of
+        // the half-wave leaves lane p with row 8rg + mp/4, slot 4hg + mp%4
         {
             double part[ATT_RG * ATT_HG];
 #pragma unroll
             for (uint32_t i = 0; i < ATT_RG; i++) {
-                const uint32_t r = ATT_RG * rg + i;
+                const uint32_t r = ATT_RG * rg + (i ^ (mp >> 2));
                 const LDS uint16_t *kr = ((owner && t0 + r == (uint32_t)pos) ? knew : kb + bo + r * 256) + ATT_DP * p;
                 const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(kr);
                 const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
@@ -335,12 +335,12 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
                     part[i * ATT_HG + jj] = d;
                 }
             }
-            att_rs_step_x16<16>(part, (p & 16) != 0);
-            att_rs_step<DPP_MIRROR, 8>(part, (p & 8) != 0);
-            att_rs_step<DPP_HALF_MIRROR, 4>(part, (p & 4) != 0);
-            att_rs_step<DPP_XOR2, 2>(part, (p & 2) != 0);
-            att_rs_step<DPP_XOR1, 1>(part, (p & 1) != 0);
-            const uint32_t r = ATT_RG * rg + (p >> 2), hh = ATT_HG * hg + (p & 3);
+            att_rs_step_x16(part);
+            att_rs_step<DPP_MIRROR, 8>(part);
+            att_rs_step<DPP_HALF_MIRROR, 4>(part);
+            att_rs_step<DPP_XOR2, 2>(part);
+            att_rs_step<DPP_XOR1, 1>(part);
+            const uint32_t r = ATT_RG * rg + (mp >> 2), hh = ATT_HG * hg + (mp & 3);
             sc[hh * ATT_TILE + r] = (t0 + r < kv1) ? part[0] * (double)a.scale : -INFINITY;
         }
         __syncthreads();
@@ -358,9 +358,8 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
             const double mo = mrun;
             const double mn = fmax(mo, mt);
             const double wgt = (s == -INFINITY || hh >= gqa) ? 0.0 : exp(s - mn);
-            double ws = wgt;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) ws += __shfl_xor(ws, o, 64);
+            double ws = row16_sum_f64(wgt);
+            ws += __shfl_xor(ws, 16, 64);
             sc[hh * ATT_TILE + r] = wgt;
             const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
             lrun = lrun * cf + ws;
