@@ -89,6 +89,35 @@ def cpu_baseline(m, ctx, seconds):
                       f"(CPU oracle, OpenMP over rows, {threads} threads; weights copied to host in {copy_s:.1f} s)"}
 
 
+def parity(m, cfg, args):
+    """Greedy decode on the GPU and on the CPU oracle from the same synthetic
+    context, step by step (one interpreter pass per step, logits read back)."""
+    import numpy as np
+    import oracle
+    t0 = time.perf_counter()
+    mirror = oracle.ModelMirror(m)
+    copy_s = time.perf_counter() - t0
+    tok, pos = 1, args.ctx
+    worst_rel, mism, toks = 0.0, 0, []
+    t_cpu = 0.0
+    for i in range(args.parity_steps):
+        logits = np.zeros(cfg.n_vocab, np.float32)
+        nxt = m.decode(tok, pos, logits)
+        s = time.perf_counter()
+        rtok, rlog = mirror.step(tok, pos)
+        t_cpu += time.perf_counter() - s
+        rel = float(np.linalg.norm(logits - rlog) / np.linalg.norm(rlog))
+        worst_rel = max(worst_rel, rel)
+        mism += int(nxt != rtok)
+        print(f"# step {i}: gpu {nxt} cpu {rtok} logits rel L2 {rel:.3e}", file=sys.stderr, flush=True)
+        toks.append(nxt)
+        tok, pos = rtok, pos + 1
+    print(json.dumps({"parity_steps": args.parity_steps, "quant": args.quant, "context": args.ctx,
+                      "token_mismatches": mism, "worst_logits_rel_l2": worst_rel, "tokens": toks,
+                      "cpu_seconds": round(t_cpu, 1), "mirror_copy_seconds": round(copy_s, 1),
+                      "pass": mism == 0 and worst_rel <= 1e-2}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -103,6 +132,10 @@ def main():
                     help="greedy passes per cooperative launch (the warmup is one launch)")
     ap.add_argument("--profile-ops", type=int, default=0,
                     help="after the timed run, N more tokens with block-0 per-kind timers (stderr)")
+    ap.add_argument("--parity-steps", type=int, default=0, metavar="N",
+                    help="only check parity: from a fresh synthetic context, N greedy decode steps on the GPU "
+                         "and on the CPU oracle (same weights and state); token ids must be identical, logits "
+                         "within rel L2 1e-2; prints one JSON line and exits")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 3 times (torch's copy kernel) and exit: the "
                          "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -134,6 +167,11 @@ def main():
     m.synth_context(args.ctx, seed=args.seed + 1)
     setup_s = time.perf_counter() - t0
     print(f"# model ready in {setup_s:.1f} s: {m.info()}", file=sys.stderr, flush=True)
+
+    if args.parity_steps:
+        parity(m, cfg, args)
+        m.close()
+        return
 
     L = sinter.lib()
     ppl = max(1, min(args.passes_per_launch, args.steps))

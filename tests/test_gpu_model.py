@@ -52,6 +52,32 @@ def test_small_model_decode_matches_oracle(sn, orc, torch_gpu, quant):
         m.close()
 
 
+def test_full_shape_decode_matches_oracle(sn, orc, torch_gpu):
+    """The benchmark configuration itself (64 layers, Qwen3.6-27B shapes,
+    Q4_K_M mix, 4096-token synthetic context): four greedy steps on the GPU
+    and on the CPU oracle from the same weights and state; identical token ids,
+    logits within rel L2 1e-5 (the pass bar is 1e-2)."""
+    cfg = sn.qwen36_27b_config(n_ctx=4096 + 8, quant="q4_k_m")
+    print("full shape: create", flush=True)
+    m = sn.Model(cfg, seed=2026)
+    try:
+        m.synth_context(4096, seed=2027)
+        print("full shape: mirror to host", flush=True)
+        mirror = orc.ModelMirror(m)
+        tok, pos = 1, 4096
+        for step in range(4):
+            logits = np.zeros(cfg.n_vocab, np.float32)
+            nxt = m.decode(tok, pos, logits)
+            rtok, rlog = mirror.step(tok, pos)
+            rel = np.linalg.norm(logits - rlog) / np.linalg.norm(rlog)
+            print(f"full shape step {step}: gpu {nxt} oracle {rtok} rel {rel:.2e}", flush=True)
+            assert nxt == rtok == int(np.argmax(rlog))
+            assert rel < 1e-5, rel
+            tok, pos = nxt, pos + 1
+    finally:
+        m.close()
+
+
 def test_greedy_multi_pass_equals_single_passes(sn, orc, torch_gpu):
     cfg = small_config(sn, n_layer=8)
     m = sn.Model(cfg, seed=21)
