@@ -282,13 +282,32 @@ __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret
 // Phase 2: row g of the block (16 lanes) owns chunks g, g+16, ... and reads
 // its elements from the staging area; RMSNorm first sums squares over its
 // chunks for the block-wide scale.
+template <class Post>
 __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
-                                              unsigned *err) {
+                                              unsigned *err, Post &&post) {
     const uint32_t K = a.K;
     const bool embed = a.pro == SINTER_PRO_EMBED;
     const bool gpre = a.pro == SINTER_PRO_GATED_G, gated = a.pro == SINTER_PRO_GATED || gpre;
     const bool rms = a.pro == SINTER_PRO_RMSNORM || embed;
     char *xs_g = g_big, *ys_g = g_big + K * 4;
+    const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
+    // the lane's indices, opaque to the compiler so that the per-lane address
+    // arithmetic below is not hoisted out of the interpreter loop (where it
+    // would stay live, in registers, for the whole kernel)
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
+    // gated norms: the gd head-width norm weights go to the last KiB of the
+    // staging area by one LDS-DMA (lanes past gd/4 re-read the last 16 bytes,
+    // in bounds), so that no compiler-visible load precedes the weight slots
+    // post() issues (a wait for it would wait for those too)
+    char *ws_g = g_big + BIG_BYTES - 1024;
+    if (gated && wave_id() == 0) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)a.norm_w);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)a.norm_w >> 32));
+        lds_dma16<false>(((uintptr_t)hi << 32) | lo, min((uint32_t)lane_id() * 16u, gd * 4u - 16u),
+                         (uint32_t)(uintptr_t)(lds_void *)ws_g);
+    }
     if (embed) {
         int32_t tok = ld_coh(a.token);
         if (tok < 0 || (uint32_t)tok >= a.aux_rows) {   // never read outside the table
@@ -305,23 +324,28 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
 #pragma unroll
             for (int k = 0; k < 4; k++) xs[4 * i + k] = v[k];
         }
+        post();
     } else {
         dma_vec<true>(a.x, K, xs_g);
         if (gated) dma_vec<true>(static_cast<const float *>(a.aux), K, ys_g);
         else if (rms) dma_vec<false>(a.norm_w, K, ys_g);
+        post();
     }
-    dma_wait();
     __syncthreads();
 
     const LDS float *xs = reinterpret_cast<const LDS float *>((const lds_char *)xs_g);
     const LDS float *ys = reinterpret_cast<const LDS float *>((const lds_char *)ys_g);
-    const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
-    // the lane's indices, opaque to the compiler so that the per-lane address
-    // arithmetic below is not hoisted out of the interpreter loop (where it
-    // would stay live, in registers, for the whole kernel)
-    uint32_t tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
+    // gated-norm weights: element 64q + 4r + i of every chunk uses
+    // norm_w[(64q + 4r + i) % gd]
+    float gw[16];
+    if (gated) {
+        const LDS float *ws = reinterpret_cast<const LDS float *>((const lds_char *)ws_g);
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(ws + ((64 * qq + r * 4) & (gd - 1)));
+            gw[4 * qq] = t.x; gw[4 * qq + 1] = t.y; gw[4 * qq + 2] = t.z; gw[4 * qq + 3] = t.w;
+        }
+    }
     // the lane's 16 elements of chunk c: 64q + 4r + i
     auto ld16 = [&](const LDS float *base, uint32_t c, float v[16]) {
 #pragma unroll
@@ -344,15 +368,6 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         s = block_sum_f64(s, red);
         const float mean = (float)(s / (double)K);
         gscale = 1.0f / sqrtf(mean + a.eps);
-    }
-    // gated-norm weights: element 64q + 4r + i of every chunk uses
-    // norm_w[(64q + 4r + i) % gd]
-    float gw[16];
-#pragma unroll
-    for (int qq = 0; qq < 4; qq++) {
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
-        if (gated) t = *reinterpret_cast<const GLB f32x4 *>(gp(a.norm_w + ((64 * qq + r * 4) & (gd - 1))));
-        gw[4 * qq] = t.x; gw[4 * qq + 1] = t.y; gw[4 * qq + 2] = t.z; gw[4 * qq + 3] = t.w;
     }
     lds_char *q = (lds_char *)g_qbuf;
     LDS float *qd = reinterpret_cast<LDS float *>(q + (K / 256) * ACT_GSTRIDE);
@@ -662,18 +677,23 @@ __device__ __forceinline__ Run make_run(cplan_t *pl, uint32_t s, uint32_t lo, ui
 // ------------------------------------------------------------ streaming
 
 // Registers of the weight items in flight: D slots of NI 16-byte loads per
-// lane.  Before the prologue (across the grid barrier) only the first DPRE
-// slots are loaded -- at most PF_PRE registers of 16 B stay live through
-// it.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
+// lane.  The first DPRE slots are loaded across the grid barrier, slots up
+// to DPRO during the prologue (issued behind its activation DMAs), the rest
+// when the body starts -- at most PF_PRE registers of 16 B stay live through
+// the prologue.  Measured on the 27B decode: one more Q4_K slot in the body
+// (D = 4) is 1 % faster; moving a slot from across the barrier to the
+// prologue (DPRE < DPRO), or more slots live through the prologue (which
+// then spill), is slower -- loads issued behind the activation DMAs delay
+// the activation reads of the workgroups released later.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
 // 4-aligned address at or below it: every byte read lies in
 // [block - 2, block + 210), never past the end of the weights.
 constexpr int PF_MAX = 36, PF_PRE = 28;
 template <int T> struct TypeCfg;
-template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 3, DPRE = 3; };
-template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 2, DPRE = 2; };
-template <> struct TypeCfg<SINTER_Q8_0> { static constexpr int NI = 17, IB = 272, D = 2, DPRE = 1; };
-template <> struct TypeCfg<SINTER_BF16> { static constexpr int NI = 8, IB = 128, D = 4, DPRE = 3; };
-template <> struct TypeCfg<SINTER_F32> { static constexpr int NI = 16, IB = 256, D = 2, DPRE = 1; };
+template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 4, DPRE = 3, DPRO = 3; };
+template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 2, DPRE = 2, DPRO = 2; };
+template <> struct TypeCfg<SINTER_Q8_0> { static constexpr int NI = 17, IB = 272, D = 2, DPRE = 1, DPRO = 1; };
+template <> struct TypeCfg<SINTER_BF16> { static constexpr int NI = 8, IB = 128, D = 4, DPRE = 3, DPRO = 3; };
+template <> struct TypeCfg<SINTER_F32> { static constexpr int NI = 16, IB = 256, D = 2, DPRE = 1, DPRO = 1; };
 
 // Weight loads use the default cache policy: a lane's item spans several
 // 16-byte loads whose cache lines the other loads of the same step share,
@@ -734,6 +754,34 @@ __device__ __forceinline__ void issue_pre(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4]
     case SINTER_Q8_0: issue_slots<SINTER_Q8_0, 0, TypeCfg<SINTER_Q8_0>::DPRE>(pf, sh, r, dummy); break;
     case SINTER_BF16: issue_slots<SINTER_BF16, 0, TypeCfg<SINTER_BF16>::DPRE>(pf, sh, r, dummy); break;
     default: issue_slots<SINTER_F32, 0, TypeCfg<SINTER_F32>::DPRE>(pf, sh, r, dummy); break;
+    }
+}
+
+// Slots [DPRE, DPRO), issued right after the prologue's LDS-DMAs
+// so that they stream while the activation is normalised and quantised;
+// then the wait for those DMAs, which leaves exactly these loads in flight
+// (vmcnt counts in order).  Without a run nothing is issued and the wait is
+// for everything.  WAIT = false: issue only (a later run of the wave).
+template <int T, bool WAIT>
+__device__ __forceinline__ void issue_post_t(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
+    constexpr int DPRO = TypeCfg<T>::DPRO, DPRE = TypeCfg<T>::DPRE, N = (DPRO - DPRE) * TypeCfg<T>::NI;
+    static_assert(N < 64 && DPRO * TypeCfg<T>::NI <= PF_PRE && DPRE <= DPRO && DPRO <= TypeCfg<T>::D,
+                  "vmcnt range, registers live through the prologue");
+    issue_slots<T, DPRE, DPRO>(pf, sh, r, dummy);
+    if constexpr (WAIT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <bool WAIT>
+__device__ __forceinline__ void issue_post(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
+    if (!r.ok) {
+        if constexpr (WAIT) dma_wait();
+        return;
+    }
+    switch (r.type) {
+    case SINTER_Q4_K: issue_post_t<SINTER_Q4_K, WAIT>(pf, sh, r, dummy); break;
+    case SINTER_Q6_K: issue_post_t<SINTER_Q6_K, WAIT>(pf, sh, r, dummy); break;
+    case SINTER_Q8_0: issue_post_t<SINTER_Q8_0, WAIT>(pf, sh, r, dummy); break;
+    case SINTER_BF16: issue_post_t<SINTER_BF16, WAIT>(pf, sh, r, dummy); break;
+    default: issue_post_t<SINTER_F32, WAIT>(pf, sh, r, dummy); break;
     }
 }
 
@@ -892,13 +940,13 @@ __device__ __forceinline__ void fold_rows(const GemvCtx &c, cplan_t *pl, const R
     }
 }
 
-// The body of one run whose first DPRE slots were loaded: the remaining
+// The body of one run whose first DPRO slots were loaded: the remaining
 // slots, then steps of terms into the ring, rows folded as the ring fills.
 template <int T>
 __device__ __forceinline__ void run_body(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const GemvCtx &c, cplan_t *pl,
                                          const Run &r, const ActView &x, float &bv, int32_t &bi, const EpiPre &ev) {
     constexpr int D = TypeCfg<T>::D, NI = TypeCfg<T>::NI;
-    issue_slots<T, TypeCfg<T>::DPRE, D>(pf, sh, r, c.dummy);
+    issue_slots<T, TypeCfg<T>::DPRO, D>(pf, sh, r, c.dummy);
     const bool swig = r.swig != 0;
     const uint32_t si = swig ? 32u : 64u, qs = swig ? c.qs2 : c.qs, rs = swig ? c.rs2 : c.rs;
     const uint32_t n = r.n, nJ = (n + si - 1) / si, nrows = r.g1 - r.g0;
@@ -1016,7 +1064,9 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     const uint32_t K = a.K;
     const int vt = (int)pl->vt;
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
-    gemv_prologue(a, vt, write_x, g_red, err);   // ends with __syncthreads()
+    // the remaining weight slots stream during the prologue (issued after
+    // its activation DMAs, which the prologue then waits for)
+    gemv_prologue(a, vt, write_x, g_red, err, [&] { issue_post<true>(pf, sh, run, (uint64_t)plan); });
     if (ts) ts[2] = wall_clock64();
     const ActView x = act_view(g_qbuf, K, vt);
 
@@ -1042,6 +1092,7 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
         run = make_run(pl, run.s, run.g1, row_hi);
         if (!run.ok) break;
         issue_pre(pf, sh, run, (uint64_t)plan);
+        issue_post<false>(pf, sh, run, (uint64_t)plan);
         epi_preload(pl, run, ev);
     }
 

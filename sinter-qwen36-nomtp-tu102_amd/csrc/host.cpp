@@ -129,8 +129,10 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
     default: return bad("unknown prologue");
     }
     // the prologue stages x (and the norm weights or z) as f32 in the LDS
-    // scratch region
-    if ((uint64_t)a.K * 4 * (a.pro == SINTER_PRO_PLAIN ? 1u : 2u) > BIG_BYTES)
+    // scratch region; the gated norms also the head-width norm weights, in
+    // its last KiB
+    const bool gated_pro = a.pro == SINTER_PRO_GATED || a.pro == SINTER_PRO_GATED_G;
+    if ((uint64_t)a.K * 4 * (a.pro == SINTER_PRO_PLAIN ? 1u : 2u) + (gated_pro ? 1024u : 0u) > BIG_BYTES)
         return bad("K too large for the prologue's staging area");
     // the term ring (gemv.h): R rows of P terms per wave must hold the rows
     // one 64-item step touches plus one
