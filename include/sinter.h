@@ -247,6 +247,14 @@ int  sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint3
 int  sinter_host_set_pos(sinter_host *h, int32_t pos);
 /* cooperative grid size (default: one workgroup per CU); before launch() */
 int  sinter_host_set_grid(sinter_host *h, uint32_t blocks);
+/* Work shares of one GEMV instruction of the uploaded program: block b of its
+ * range streams a part of its rows' bytes proportional to share[b] (n = the
+ * instruction's block count; each share positive and finite, taken relative to
+ * their mean and clamped to [1/16, 16] of it).  Only which workgroup computes
+ * which rows changes; every row's value is bit-identical.  Waits for the
+ * host's stream.  No counterpart in the reference, whose rows per block are
+ * fixed (k0/ops/gemv.cuh:256-321): it is for the static load balance below. */
+int  sinter_host_set_gemv_shares(sinter_host *h, uint32_t instr, const float *share, uint32_t n);
 /* device time of the last interpreter launch: HIP events recorded on the
  * launch stream immediately before and after the kernel */
 float sinter_host_last_launch_ms(sinter_host *h);
@@ -318,6 +326,11 @@ int  sinter_model_copy(sinter_model *m, void *dst, const void *src, size_t bytes
 int  sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr,
                        uint32_t *n_boundaries, uint32_t *blocks);
 sinter_host *sinter_model_host(sinter_model *m);
+/* Static load balance of the model's GEMVs: `rounds` rounds of `traces`
+ * traced greedy passes from (*token, *pos) (both advanced), each round
+ * rescaling every workgroup's GEMV share so that the workgroups would end
+ * together (sinter_host_set_gemv_shares).  Results are unchanged. */
+int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,7 @@
 #include <cstddef>
 #include <cstdio>
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -169,7 +170,7 @@ int validate_gemv(const sinter_gemv_args &a, const char **why) {
 // Byte-balanced row cut w of n over the concatenated, byte-weighted row
 // space of segments [s0, s1) (a SwiGLU row weighs both matrices), as a
 // global row.  Any monotone split is correct; this one balances bytes.
-static uint32_t row_cut(const sinter_gemv_args &a, int s0, int s1, uint32_t row0, uint32_t w, uint32_t n) {
+static uint32_t row_cut(const sinter_gemv_args &a, int s0, int s1, uint32_t row0, uint64_t w, uint64_t n) {
     uint64_t total = 0;
     for (int s = s0; s < s1; s++)
         total += (uint64_t)a.seg[s].rows * sinter_row_bytes_dev(a.seg[s].type, a.K) *
@@ -191,7 +192,7 @@ static uint32_t row_cut(const sinter_gemv_args &a, int s0, int s1, uint32_t row0
     return rows;
 }
 
-void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts) {
+void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts, const uint32_t *bw) {
     std::memset(&p, 0, sizeof p);
     p.ok = 1;
     p.n_seg = a.n_seg;
@@ -241,7 +242,7 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
         rs[nruns++] = s;
     rs[nruns] = a.n_seg;
     if ((uint32_t)nruns > nw) {
-        for (uint32_t w = 0; w <= nw; w++) cuts[w] = row_cut(a, 0, a.n_seg, 0, w, nw);
+        for (uint32_t w = 0; w <= nw; w++) cuts[w] = row_cut(a, 0, a.n_seg, 0, w, nw);   // (shares ignored)
         return;
     }
     uint64_t rb[SINTER_GEMV_MAX_SEG], total = 0;
@@ -275,9 +276,17 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
         frac[best] = -1.0;
         used++;
     }
+    // inside a run, wave w's share of the bytes is proportional to its
+    // block's weight bw (uniform without one)
     uint32_t w0 = 0, row0 = 0;
     for (int r = 0; r < nruns; r++) {
-        for (uint32_t w = 0; w < nwr[r]; w++) cuts[w0 + w] = row_cut(a, rs[r], rs[r + 1], row0, w, nwr[r]);
+        uint64_t tw = 0;
+        for (uint32_t w = 0; w < nwr[r]; w++) tw += bw ? bw[(w0 + w) / WAVES] : 1u;
+        uint64_t cw = 0;
+        for (uint32_t w = 0; w < nwr[r]; w++) {
+            cuts[w0 + w] = row_cut(a, rs[r], rs[r + 1], row0, cw, tw);
+            cw += bw ? bw[(w0 + w) / WAVES] : 1u;
+        }
         w0 += nwr[r];
         for (int s = rs[r]; s < rs[r + 1]; s++) row0 += a.seg[s].rows;
     }
@@ -302,7 +311,7 @@ static int run_one(int kind, const T &args, uint32_t blocks, void *stream) {
     if (kind == SINTER_OP_GEMV) {
         sinter_gemv_args g;
         std::memcpy(&g, host.ins.payload, sizeof g);
-        build_gemv_plan(g, blocks, host.plan, host.cuts);
+        build_gemv_plan(g, blocks, host.plan, host.cuts, nullptr);
         bytes += (size_t)(blocks * WAVES + 1) * 4;
     }
     OpSlot *slot = op_slot();
@@ -512,6 +521,7 @@ struct sinter_host {
     bool profile_ops = false;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // bracket every interpreter launch
     float last_ms = 0.0f;
+    std::vector<sinter_instr> prog;       // host copy of the uploaded program
 };
 
 static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
@@ -630,7 +640,7 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
         if (prog[i].kind != SINTER_OP_GEMV) continue;
         sinter_gemv_args a;
         std::memcpy(&a, prog[i].payload, sizeof a);
-        build_gemv_plan(a, prog[i].block_hi - prog[i].block_lo, plans[i], cuts.data() + (size_t)i * PLAN_CUTS);
+        build_gemv_plan(a, prog[i].block_hi - prog[i].block_lo, plans[i], cuts.data() + (size_t)i * PLAN_CUTS, nullptr);
     }
     if (h->d_prog) (void)hipFree(h->d_prog);
     if (h->d_plans) (void)hipFree(h->d_plans);
@@ -651,6 +661,40 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
         return SINTER_ERR_HIP;
     h->n_instr = n_instr;
     h->epoch_stride = epoch_stride;
+    h->prog.assign(prog, prog + n_instr);
+    return SINTER_OK;
+}
+
+int sinter_host_set_gemv_shares(sinter_host *h, uint32_t instr, const float *share, uint32_t n) {
+    if (!h || !h->d_cuts || instr >= h->n_instr || !share) return set_error(SINTER_ERR_ARG, "set_gemv_shares: args");
+    const sinter_instr &in = h->prog[instr];
+    if (in.kind != SINTER_OP_GEMV) return set_error(SINTER_ERR_ARG, "set_gemv_shares: instruction %u is not a GEMV", instr);
+    const uint32_t nblk = in.block_hi - in.block_lo;
+    if (n != nblk) return set_error(SINTER_ERR_ARG, "set_gemv_shares: %u shares for %u blocks", n, nblk);
+    // weights in 1/4096 of the mean share, each in [1/16, 16] of it
+    double sum = 0.0;
+    for (uint32_t b = 0; b < n; b++) {
+        if (!(share[b] > 0.0f) || !std::isfinite(share[b]))
+            return set_error(SINTER_ERR_ARG, "set_gemv_shares: share %u not positive and finite", b);
+        sum += share[b];
+    }
+    std::vector<uint32_t> bw(n);
+    for (uint32_t b = 0; b < n; b++)
+        bw[b] = (uint32_t)std::lround(std::min(16.0, std::max(1.0 / 16.0, share[b] * n / sum)) * 4096.0);
+    sinter_gemv_args a;
+    std::memcpy(&a, in.payload, sizeof a);
+    GemvPlan plan;
+    std::vector<uint32_t> cuts(PLAN_CUTS, 0u);
+    build_gemv_plan(a, nblk, plan, cuts.data(), bw.data());
+    // a monotone split of all rows from row 0 (what the kernel requires)
+    bool mono = cuts[0] == 0 && cuts[nblk * WAVES] == plan.total_rows;
+    for (uint32_t w = 0; w < nblk * WAVES; w++) mono = mono && cuts[w] <= cuts[w + 1];
+    if (!mono) return set_error(SINTER_ERR_ARG, "set_gemv_shares: cuts not monotone");
+    // the kernel reads the cuts of a launch from device memory: none may run
+    if (!hip_ok(hipStreamSynchronize(h->stream), "set_gemv_shares sync") ||
+        !hip_ok(hipMemcpy(h->d_cuts + (size_t)instr * PLAN_CUTS, cuts.data(), (size_t)(nblk * WAVES + 1) * 4,
+                          hipMemcpyHostToDevice), "cuts upload"))
+        return SINTER_ERR_HIP;
     return SINTER_OK;
 }
 

@@ -37,6 +37,7 @@ bool hip_ok(hipError_t e, const char *what);
 unsigned *op_err_cell();  // per-device error cell of the standalone op launches
 int validate_gemv(const sinter_gemv_args &a, const char **why);
 // the plan and the nblk + 1 row cuts of a validated GEMV run by nblk workgroups
-void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts);
+// bw: per-block work weights (null: uniform)
+void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts, const uint32_t *bw);
 
 }  // namespace sinter

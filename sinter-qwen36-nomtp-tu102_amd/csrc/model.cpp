@@ -507,4 +507,81 @@ int sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr
 
 sinter_host *sinter_model_host(sinter_model *m) { return m ? m->host : nullptr; }
 
+// Static load balance of the GEMVs: every workgroup of a GEMV streams an equal
+// share of its bytes, but some workgroups are released from the barrier, or
+// stream, systematically later than others (the spread follows the
+// workgroup's XCD and is stable across layers), and the phase ends with the
+// last one.  Each round traces `traces` greedy passes; for every workgroup b
+// of every GEMV, with d_b its streaming time after the prologue and E_b its
+// end minus the mean end, the workgroup's share is scaled by
+// (d_b - E_b) / d_b (averaged over the traces and over the GEMVs of the same
+// shape, clamped to [0.7, 1.3]), which would end every workgroup together.
+// Only the row ranges change: every row's value is bit-identical.  Decodes
+// rounds * traces tokens from (*token, *pos), which are advanced.
+int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces) {
+    if (!m || !token || !pos || traces == 0 || *pos < 0 ||
+        (int64_t)*pos + (int64_t)rounds * traces > m->cfg.n_ctx)
+        return set_error(SINTER_ERR_ARG, "balance: args");
+    const size_t n = m->prog.size(), B = m->blocks, words = (n + 1) * B * 4;
+    // GEMVs of one shape share their statistics
+    std::vector<int> grp(n, -1);
+    std::vector<std::array<uint32_t, 6>> keys;
+    for (size_t i = 0; i < n; i++) {
+        if (m->prog[i].kind != SINTER_OP_GEMV || m->prog[i].block_lo != 0 || m->prog[i].block_hi != B) continue;
+        sinter_gemv_args a;
+        std::memcpy(&a, m->prog[i].payload, sizeof a);
+        const std::array<uint32_t, 6> k = {a.pro, a.K, a.n_seg, a.seg[0].rows, (uint32_t)a.seg[0].type, a.seg[0].epi};
+        size_t g = 0;
+        while (g < keys.size() && keys[g] != k) g++;
+        if (g == keys.size()) keys.push_back(k);
+        grp[i] = (int)g;
+    }
+    std::vector<float> share(n * B, 1.0f);
+    unsigned long long *d_trace = nullptr;
+    if (!hip_ok(hipMalloc(&d_trace, words * 8), "balance trace alloc")) return SINTER_ERR_HIP;
+    std::vector<unsigned long long> t(words);
+    int rc = SINTER_OK;
+    for (uint32_t r = 0; r < rounds && rc == SINTER_OK; r++) {
+        std::vector<double> acc(keys.size() * B, 0.0);
+        std::vector<uint32_t> cnt(keys.size(), 0);
+        for (uint32_t k = 0; k < traces && rc == SINTER_OK; k++) {
+            int32_t next = 0;
+            rc = sinter_host_trace_next(m->host, d_trace, words);
+            if (rc == SINTER_OK) rc = sinter_model_greedy(m, *token, *pos, 1, &next);
+            if (rc != SINTER_OK) break;
+            if (!hip_ok(hipMemcpy(t.data(), d_trace, words * 8, hipMemcpyDeviceToHost), "balance trace read")) {
+                rc = SINTER_ERR_HIP;
+                break;
+            }
+            *token = next;
+            *pos += 1;
+            for (size_t i = 0; i < n; i++) {
+                if (grp[i] < 0) continue;
+                const unsigned long long *ti = t.data() + i * B * 4;
+                double emean = 0.0;
+                for (size_t b = 0; b < B; b++) emean += (double)ti[b * 4 + 3];
+                emean /= (double)B;
+                bool ok = true;
+                for (size_t b = 0; b < B; b++) ok = ok && ti[b * 4 + 3] > ti[b * 4 + 2] && ti[b * 4 + 2] > 0;
+                if (!ok) continue;
+                for (size_t b = 0; b < B; b++) {
+                    const double d = (double)(ti[b * 4 + 3] - ti[b * 4 + 2]);
+                    const double e = (double)ti[b * 4 + 3] - emean;
+                    acc[grp[i] * B + b] += std::min(1.3, std::max(0.7, (d - e) / d));
+                }
+                cnt[grp[i]]++;
+            }
+        }
+        if (rc != SINTER_OK) break;
+        for (size_t i = 0; i < n && rc == SINTER_OK; i++) {
+            if (grp[i] < 0 || cnt[grp[i]] == 0) continue;
+            float *sh = share.data() + i * B;
+            for (size_t b = 0; b < B; b++) sh[b] *= (float)(acc[grp[i] * B + b] / cnt[grp[i]]);
+            rc = sinter_host_set_gemv_shares(m->host, (uint32_t)i, sh, (uint32_t)B);
+        }
+    }
+    (void)hipFree(d_trace);
+    return rc;
+}
+
 }  // extern "C"

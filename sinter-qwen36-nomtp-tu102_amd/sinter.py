@@ -148,6 +148,7 @@ def lib():
         "sinter_host_grid": (I, [vp, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
         "sinter_host_set_pos": (I, [vp, C.c_int32]),
         "sinter_host_set_grid": (I, [vp, U32]),
+        "sinter_host_set_gemv_shares": (I, [vp, U32, C.POINTER(C.c_float), U32]),
         "sinter_host_last_launch_ms": (C.c_float, [vp]),
         "sinter_model_create": (I, [C.POINTER(ModelConfig), I, U64, U32, C.POINTER(vp)]),
         "sinter_model_destroy": (None, [vp]),
@@ -159,6 +160,7 @@ def lib():
         "sinter_model_copy": (I, [vp, vp, vp, C.c_size_t, I]),
         "sinter_model_info": (I, [vp, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
         "sinter_model_host": (vp, [vp]),
+        "sinter_model_balance": (I, [vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32), U32, U32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -248,3 +250,11 @@ class Model:
 
     def host(self):
         return lib().sinter_model_host(self.h)
+
+    def balance(self, token, pos, rounds=2, traces=4):
+        """Static GEMV load balance (sinter_model_balance): decodes
+        rounds*traces greedy tokens from (token, pos); returns the next
+        (token, pos)."""
+        t, p = C.c_int32(token), C.c_int32(pos)
+        check(lib().sinter_model_balance(self.h, C.byref(t), C.byref(p), rounds, traces), "balance")
+        return t.value, p.value

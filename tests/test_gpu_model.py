@@ -95,6 +95,32 @@ def test_greedy_multi_pass_equals_single_passes(sn, orc, torch_gpu):
         m.close()
 
 
+def test_gemv_balance_leaves_results_unchanged(sn, torch_gpu):
+    """sinter_model_balance moves GEMV rows between workgroups: the tokens it
+    decodes and every later token and logit equal those of a model that was
+    never rebalanced (rows are folded by one lane each, wherever they run)."""
+    cfg = small_config(sn, n_layer=8)
+    a, b = sn.Model(cfg, seed=31), sn.Model(cfg, seed=31)
+    try:
+        for m in (a, b):
+            m.synth_context(100, seed=32)
+        ref = a.greedy(5, 100, 14)
+        tok, pos = b.balance(5, 100, rounds=3, traces=2)
+        assert (tok, pos) == (ref[5], 106)
+        assert b.greedy(tok, pos, 8) == ref[6:14]
+        la, lb = np.zeros(cfg.n_vocab, np.float32), np.zeros(cfg.n_vocab, np.float32)
+        assert a.decode(ref[13], 114, la) == b.decode(ref[13], 114, lb)
+        assert np.array_equal(la, lb)
+        # the low-level entry point refuses what it cannot apply
+        h = b.host()
+        one = (C.c_float * cfg.n_vocab)(*([1.0] * cfg.n_vocab))
+        assert sn.lib().sinter_host_set_gemv_shares(h, 1, one, 3) == sn.ERR_ARG   # wrong count / not a GEMV
+        assert sn.lib().sinter_host_set_gemv_shares(h, 10 ** 6, one, 3) == sn.ERR_ARG
+    finally:
+        a.close()
+        b.close()
+
+
 def test_error_cell_path_bad_kind(sn, torch_gpu):
     """An unknown instruction kind ends the pass with RUN_ERR and the
     instruction index in the error cell (core/interp.cuh error protocol)."""
