@@ -145,7 +145,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the decode path on one GPU "
-              "(the 27B model fits one MI355X; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the 27B model fits one MI355X; no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
 
     import torch
