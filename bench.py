@@ -124,8 +124,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--balance", type=int, nargs=2, default=(2, 4), metavar=("ROUNDS", "TRACES"),
-                    help="static GEMV load balance before the warmup: ROUNDS rounds of TRACES traced greedy "
-                         "passes (sinter_model_balance; 0 0 = off)")
+                    help="static GEMV load balance before the warmup: ROUNDS updates, each measured on TRACES "
+                         "traced greedy passes (sinter_model_balance; TRACES = 0: off)")
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--quant", default="q4_k_m", choices=["q4_k_m", "bf16"])
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -163,7 +163,7 @@ def main():
 
     import sinter
 
-    n_bal = args.balance[0] * args.balance[1]
+    n_bal = (args.balance[0] + 1) * args.balance[1] if args.balance[1] else 0
     n_ctx = args.ctx + n_bal + args.warmup + args.steps + args.profile_ops + 8
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
     t0 = time.perf_counter()
@@ -231,7 +231,7 @@ def main():
         "config": {"workload": f"e2e greedy decode, Qwen3.6-27B-shaped hybrid (48 GDN + 16 attention), "
                                f"{args.quant} weights, {args.ctx}-token context",
                    "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
-                   "gemv_balance": f"{args.balance[0]} rounds x {args.balance[1]} traced passes (untimed)",
+                   "gemv_balance": f"{args.balance[0]} updates, {n_bal} traced passes (untimed)",
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl, args.quant, args.ctx),

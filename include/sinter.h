@@ -326,10 +326,12 @@ int  sinter_model_copy(sinter_model *m, void *dst, const void *src, size_t bytes
 int  sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr,
                        uint32_t *n_boundaries, uint32_t *blocks);
 sinter_host *sinter_model_host(sinter_model *m);
-/* Static load balance of the model's GEMVs: `rounds` rounds of `traces`
- * traced greedy passes from (*token, *pos) (both advanced), each round
- * rescaling every workgroup's GEMV share so that the workgroups would end
- * together (sinter_host_set_gemv_shares).  Results are unchanged. */
+/* Static load balance of the model's GEMVs: rounds + 1 measurements of
+ * `traces` traced greedy passes each from (*token, *pos) (both advanced by
+ * (rounds + 1) * traces); after each of the first `rounds` every workgroup's
+ * GEMV share is rescaled so that the workgroups would end together
+ * (sinter_host_set_gemv_shares), and a GEMV shape whose tail got longer keeps
+ * its best shares.  Results are unchanged. */
 int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces);
 
 #ifdef __cplusplus

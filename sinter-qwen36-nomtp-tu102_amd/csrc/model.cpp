@@ -24,6 +24,7 @@
 // 5 barriers per layer (the reference schedule has 15) plus the pass-end one.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <array>
 #include <cmath>
 #include <cstring>
@@ -516,11 +517,13 @@ sinter_host *sinter_model_host(sinter_model *m) { return m ? m->host : nullptr; 
 // end minus the mean end, the workgroup's share is scaled by
 // (d_b - E_b) / d_b (averaged over the traces and over the GEMVs of the same
 // shape, clamped to [0.7, 1.3]), which would end every workgroup together.
-// Only the row ranges change: every row's value is bit-identical.  Decodes
-// rounds * traces tokens from (*token, *pos), which are advanced.
+// After `rounds` updates a last measurement keeps, per shape, the shares
+// with the shortest tail.  Only the row ranges change: every row's value is
+// bit-identical.  Decodes (rounds + 1) * traces tokens from (*token, *pos),
+// which are advanced.
 int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces) {
     if (!m || !token || !pos || traces == 0 || *pos < 0 ||
-        (int64_t)*pos + (int64_t)rounds * traces > m->cfg.n_ctx)
+        (int64_t)*pos + (int64_t)(rounds + 1) * traces > m->cfg.n_ctx)
         return set_error(SINTER_ERR_ARG, "balance: args");
     const size_t n = m->prog.size(), B = m->blocks, words = (n + 1) * B * 4;
     // GEMVs of one shape share their statistics
@@ -536,13 +539,18 @@ int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t
         if (g == keys.size()) keys.push_back(k);
         grp[i] = (int)g;
     }
-    std::vector<float> share(n * B, 1.0f);
+    std::vector<float> share(n * B, 1.0f), best(n * B, 1.0f);
+    std::vector<double> best_tail(keys.size(), 0.0);
+    std::vector<char> frozen(keys.size(), 0);
     unsigned long long *d_trace = nullptr;
     if (!hip_ok(hipMalloc(&d_trace, words * 8), "balance trace alloc")) return SINTER_ERR_HIP;
     std::vector<unsigned long long> t(words);
     int rc = SINTER_OK;
-    for (uint32_t r = 0; r < rounds && rc == SINTER_OK; r++) {
-        std::vector<double> acc(keys.size() * B, 0.0);
+    // rounds + 1 measurements: each after the previous update; a shape whose
+    // tail (last end minus mean end) got longer returns to its best shares
+    // and is not updated again
+    for (uint32_t r = 0; r <= rounds && rc == SINTER_OK; r++) {
+        std::vector<double> acc(keys.size() * B, 0.0), tail(keys.size(), 0.0);
         std::vector<uint32_t> cnt(keys.size(), 0);
         for (uint32_t k = 0; k < traces && rc == SINTER_OK; k++) {
             int32_t next = 0;
@@ -558,26 +566,47 @@ int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t
             for (size_t i = 0; i < n; i++) {
                 if (grp[i] < 0) continue;
                 const unsigned long long *ti = t.data() + i * B * 4;
-                double emean = 0.0;
-                for (size_t b = 0; b < B; b++) emean += (double)ti[b * 4 + 3];
-                emean /= (double)B;
                 bool ok = true;
                 for (size_t b = 0; b < B; b++) ok = ok && ti[b * 4 + 3] > ti[b * 4 + 2] && ti[b * 4 + 2] > 0;
                 if (!ok) continue;
+                double emean = 0.0, emax = 0.0;
+                for (size_t b = 0; b < B; b++) {
+                    emean += (double)ti[b * 4 + 3];
+                    emax = std::max(emax, (double)ti[b * 4 + 3]);
+                }
+                emean /= (double)B;
                 for (size_t b = 0; b < B; b++) {
                     const double d = (double)(ti[b * 4 + 3] - ti[b * 4 + 2]);
                     const double e = (double)ti[b * 4 + 3] - emean;
                     acc[grp[i] * B + b] += std::min(1.3, std::max(0.7, (d - e) / d));
                 }
+                tail[grp[i]] += emax - emean;
                 cnt[grp[i]]++;
             }
         }
         if (rc != SINTER_OK) break;
-        for (size_t i = 0; i < n && rc == SINTER_OK; i++) {
-            if (grp[i] < 0 || cnt[grp[i]] == 0) continue;
-            float *sh = share.data() + i * B;
-            for (size_t b = 0; b < B; b++) sh[b] *= (float)(acc[grp[i] * B + b] / cnt[grp[i]]);
-            rc = sinter_host_set_gemv_shares(m->host, (uint32_t)i, sh, (uint32_t)B);
+        for (size_t g = 0; g < keys.size(); g++) {
+            if (cnt[g] == 0) continue;
+            const double tg = tail[g] / cnt[g];
+            const bool worse = r > 0 && tg > best_tail[g];
+            if (!worse) best_tail[g] = tg;
+            for (size_t i = 0; i < n; i++) {
+                if (grp[i] != (int)g) continue;
+                float *sh = share.data() + i * B, *bs = best.data() + i * B;
+                if (worse) {
+                    frozen[g] = 1;
+                    std::copy(bs, bs + B, sh);
+                } else {
+                    std::copy(sh, sh + B, bs);
+                    if (r < rounds && !frozen[g])
+                        for (size_t b = 0; b < B; b++) sh[b] *= (float)(acc[g * B + b] / cnt[g]);
+                }
+                if (worse || (r < rounds && !frozen[g])) {
+                    rc = sinter_host_set_gemv_shares(m->host, (uint32_t)i, sh, (uint32_t)B);
+                    if (rc != SINTER_OK) break;
+                }
+            }
+            if (rc != SINTER_OK) break;
         }
     }
     (void)hipFree(d_trace);

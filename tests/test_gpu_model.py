@@ -104,12 +104,12 @@ def test_gemv_balance_leaves_results_unchanged(sn, torch_gpu):
     try:
         for m in (a, b):
             m.synth_context(100, seed=32)
-        ref = a.greedy(5, 100, 14)
-        tok, pos = b.balance(5, 100, rounds=3, traces=2)
-        assert (tok, pos) == (ref[5], 106)
-        assert b.greedy(tok, pos, 8) == ref[6:14]
+        ref = a.greedy(5, 100, 16)
+        tok, pos = b.balance(5, 100, rounds=3, traces=2)   # 4 measurements of 2 passes
+        assert (tok, pos) == (ref[7], 108)
+        assert b.greedy(tok, pos, 8) == ref[8:16]
         la, lb = np.zeros(cfg.n_vocab, np.float32), np.zeros(cfg.n_vocab, np.float32)
-        assert a.decode(ref[13], 114, la) == b.decode(ref[13], 114, lb)
+        assert a.decode(ref[15], 116, la) == b.decode(ref[15], 116, lb)
         assert np.array_equal(la, lb)
         # the low-level entry point refuses what it cannot apply
         h = b.host()
