@@ -48,8 +48,9 @@ enum sinter_err_code {
     SINTER_E_BAD_KIND = 1,        /* kind >= SINTER_OP_KIND_COUNT */
     SINTER_E_UNWIRED_KIND = 2,    /* valid kind without an implementation */
     SINTER_E_BAD_SHAPE = 3,       /* an op found its payload inconsistent */
-    SINTER_E_ATTN_SENTINEL = 4,   /* a split-K partial was never written */
-    SINTER_E_TIMEOUT_BARRIER = 5  /* a grid-barrier wait exceeded the spin limit */
+    /* 4 is unused: the split-K merge waits on per-chunk generation flags, so
+       a partial that was never written is a flag wait that times out (5) */
+    SINTER_E_TIMEOUT_BARRIER = 5  /* a grid-barrier or merge-flag wait exceeded the spin limit */
 };
 
 const char *sinter_last_error(void);
@@ -313,6 +314,9 @@ int  sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *log
 /* n greedy passes from (token, pos) in one launch */
 int  sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
                          int32_t *tokens_out);
+/* the logits of the last pass (n_vocab floats to host): the result_output
+ * cell of k0/program.json, read after run_pass / greedy */
+int  sinter_model_logits(sinter_model *m, float *logits_host);
 /* fill KV caches / recurrent states with seeded synthetic values, as if a
  * context of n_past tokens had been prefilled */
 int  sinter_model_synth_context(sinter_model *m, int32_t n_past, uint64_t seed);

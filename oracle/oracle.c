@@ -545,9 +545,12 @@ void or_rope_neox(float *x, int hd, int n_dims, int pos, float theta_scale) {
 void or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc, int n_kv,
                     int nq, int nkv, int hd, int row_width, float scale, float *out) {
     const int gqa = nq / nkv;
-    double *s = (double *)malloc(sizeof(double) * (size_t)(n_kv > 0 ? n_kv : 1));
-    double *acc = (double *)malloc(sizeof(double) * (size_t)hd);
+    /* heads are independent: one thread per head (results do not depend on
+     * the thread count) */
+#pragma omp parallel for schedule(static)
     for (int h = 0; h < nq; h++) {
+        double *s = (double *)malloc(sizeof(double) * (size_t)(n_kv > 0 ? n_kv : 1));
+        double *acc = (double *)malloc(sizeof(double) * (size_t)hd);
         const int g = h / gqa;
         const float *qh = q + (size_t)h * hd;
         double m = -INFINITY;
@@ -567,9 +570,9 @@ void or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc, int 
             for (int d = 0; d < hd; d++) acc[d] += p * (double)or_f16_to_f32(vr[d]);
         }
         for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(acc[d] / sum);
+        free(s);
+        free(acc);
     }
-    free(s);
-    free(acc);
 }
 
 /* ------------------------------------------------------------ layers */

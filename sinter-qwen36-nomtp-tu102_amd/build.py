@@ -1,24 +1,44 @@
-"""Build libsinter.so (HIP for gfx950) in-tree.
+"""Build libsinter.so (HIP for gfx950) in-tree, behind a resource gate.
 
 Run as `python sinter-qwen36-nomtp-tu102_amd/build.py`; __graft_entry__.build()
 calls build().  Every translation unit gets the same numerics flags: no
 floating-point contraction (the declared fp32 expressions are evaluated
 exactly as written, matching the CPU oracle) and no packed-fp32 instructions.
+
+Resource gate: the compiler's kernel-resource-usage remarks are parsed for
+every kernel.  The build fails if any kernel uses scratch (private memory:
+register spills to memory or stack arrays), has a dynamic stack, or if a
+persistent-grid kernel cannot keep one 256-thread workgroup per CU (LDS over
+160 KiB or occupancy below one wave per SIMD).  The figures are written to
+resource_usage.txt beside the library.
 """
 import os
+import re
 import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsinter.so")
+REPORT = os.path.join(HERE, "resource_usage.txt")
 SOURCES = ["interp.hip", "host.cpp", "model.cpp"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+# kernels that run as one resident workgroup per CU (cooperative grids)
+PERSISTENT = {"sinter_interp", "sinter_op_kernel"}
+LDS_LIMIT = 160 * 1024
+
+_FIELDS = {
+    "TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs",
+    "ScratchSize [bytes/lane]": "scratch", "Dynamic Stack": "dyn_stack",
+    "Occupancy [waves/SIMD]": "occupancy", "SGPRs Spill": "sgpr_spill",
+    "VGPRs Spill": "vgpr_spill", "LDS Size [bytes/block]": "lds",
+}
 
 
 def hipcc():
@@ -28,6 +48,51 @@ def hipcc():
     return "hipcc"
 
 
+def parse_resource_usage(text):
+    """{kernel: {field: value}} from -Rpass-analysis=kernel-resource-usage
+    remarks (the device pass prints one block of remarks per kernel)."""
+    kernels, cur = {}, None
+    for line in text.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", line)
+        if m:
+            cur = kernels.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z][A-Za-z /\[\]]*?): (\S+) \[-Rpass-analysis", line)
+        if m and cur is not None and m.group(1) in _FIELDS:
+            v = m.group(2)
+            cur[_FIELDS[m.group(1)]] = v if v in ("True", "False") else int(v)
+    return kernels
+
+
+def gate(kernels):
+    """Reasons the build must fail (empty: pass)."""
+    bad = []
+    if not kernels:
+        bad.append("no kernel-resource-usage remarks found")
+    for name, k in kernels.items():
+        if k.get("scratch", 0) != 0:
+            bad.append(f"{name}: {k['scratch']} bytes/lane of scratch")
+        if k.get("dyn_stack") == "True":
+            bad.append(f"{name}: dynamic stack")
+        if name in PERSISTENT:
+            if k.get("lds", 0) > LDS_LIMIT:
+                bad.append(f"{name}: {k['lds']} B of LDS per workgroup (> {LDS_LIMIT})")
+            if k.get("occupancy", 0) < 1:
+                bad.append(f"{name}: occupancy {k.get('occupancy')} waves/SIMD")
+    for name in PERSISTENT:
+        if kernels and name not in kernels:
+            bad.append(f"{name}: no resource remarks")
+    return bad
+
+
+def report_text(kernels):
+    cols = ["vgprs", "agprs", "sgprs", "vgpr_spill", "sgpr_spill", "scratch", "lds", "occupancy"]
+    lines = ["kernel " + " ".join(cols)]
+    for name in sorted(kernels):
+        lines.append(name + " " + " ".join(str(kernels[name].get(c, "?")) for c in cols))
+    return "\n".join(lines) + "\n"
+
+
 def build(verbose=False):
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = LIB + ".tmp"
@@ -35,10 +100,23 @@ def build(verbose=False):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
-    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
+    text = r.stdout + r.stderr
+    out = "\n".join(l for l in text.splitlines()
+                    if "packed-fp32-ops" not in l and "remark:" not in l and "-Rpass-analysis" not in l
+                    and not re.match(r"^\s*\d+ \|", l) and not re.match(r"^\s*\|\s*\^", l))
     if r.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + out)
+    kernels = parse_resource_usage(text)
+    bad = gate(kernels)
+    if bad:
+        if os.path.exists(tmp):
+            os.remove(tmp)
+        raise RuntimeError("resource gate failed:\n  " + "\n  ".join(bad) + "\n" + report_text(kernels))
+    with open(REPORT, "w") as f:
+        f.write(report_text(kernels))
     os.replace(tmp, LIB)
+    if verbose:
+        print(report_text(kernels), end="", flush=True)
     return LIB
 
 

@@ -12,8 +12,8 @@
 // workgroup at the same instruction, all return, no barrier is left half
 // arrived.  Ops raise into the error cell and return normally; the cell is
 // sampled after the pass-end barrier, uniformly.  A barrier wait that exceeds
-// the spin limit raises SINTER_E_BAD_KIND+16 (timeout) and returns, so a
-// broken program ends the kernel instead of hanging the device.
+// the spin limit raises SINTER_E_TIMEOUT_BARRIER and returns, so a broken
+// program ends the kernel instead of hanging the device.
 #include <hip/hip_runtime.h>
 
 #include "internal.h"
@@ -156,10 +156,8 @@ extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type,
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_units) return;
     if (kind == SINTER_SYN_WEIGHT || kind == SINTER_SYN_Q8_0_CFG1) {
-        const uint32_t gb = sx_group_bytes(type);
-        uint8_t tmp[1024];
-        sx_weight_group(seed, i, type, kind == SINTER_SYN_Q8_0_CFG1, tmp);
-        for (uint32_t k = 0; k < gb; k++) dst[i * gb + k] = tmp[k];
+        // written in place (a private staging array would live in scratch)
+        sx_weight_group(seed, i, type, kind == SINTER_SYN_Q8_0_CFG1, dst + i * sx_group_bytes(type));
     } else if (kind == SINTER_SYN_NORMAL) {
         reinterpret_cast<float *>(dst)[i] = a + b * sx_normal(seed, i);
     } else if (kind == SINTER_SYN_UNIFORM) {

@@ -468,6 +468,13 @@ int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
     return SINTER_OK;
 }
 
+int sinter_model_logits(sinter_model *m, float *logits_host) {
+    if (!m || !logits_host) return set_error(SINTER_ERR_ARG, "logits: args");
+    return hip_ok(hipMemcpy(logits_host, m->logits, (size_t)m->cfg.n_vocab * 4, hipMemcpyDeviceToHost), "logits")
+               ? SINTER_OK
+               : SINTER_ERR_HIP;
+}
+
 int sinter_model_tensor_info(sinter_model *m, int64_t layer, int slot, void **dev_ptr, size_t *bytes, int *type) {
     if (!m || slot < 0 || slot >= NSLOT || layer < 0 || layer > m->cfg.n_layer) return set_error(SINTER_ERR_ARG, "slot");
     const Tensor *t = nullptr;

@@ -19,7 +19,7 @@ EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV, EPI_SILU = range(6)
 SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16 = range(5)
 OK, ERR_ARG, ERR_HIP, ERR_DEVICE, ERR_TIMEOUT, ERR_STATE, ERR_NOMEM = 0, -1, -2, -3, -4, -5, -6
 RUN_OK, RUN_ERR, RUN_TIMEOUT = 0, 1, 2
-E_NONE, E_BAD_KIND, E_UNWIRED_KIND, E_BAD_SHAPE, E_ATTN_SENTINEL, E_TIMEOUT_BARRIER = range(6)
+E_NONE, E_BAD_KIND, E_UNWIRED_KIND, E_BAD_SHAPE, E_TIMEOUT_BARRIER = 0, 1, 2, 3, 5
 
 BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
 BLOCK_ELEMS = {F32: 1, F16: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
@@ -155,6 +155,7 @@ def lib():
         "sinter_model_decode": (I, [vp, C.c_int32, C.c_int32, vp, C.POINTER(C.c_int32)]),
         "sinter_model_greedy": (I, [vp, C.c_int32, C.c_int32, U32, C.POINTER(C.c_int32)]),
         "sinter_model_synth_context": (I, [vp, C.c_int32, U64]),
+        "sinter_model_logits": (I, [vp, vp]),
         "sinter_model_tensor_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t), C.POINTER(I)]),
         "sinter_model_state_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t)]),
         "sinter_model_copy": (I, [vp, vp, vp, C.c_size_t, I]),
@@ -231,6 +232,14 @@ class Model:
         out = (C.c_int32 * n)()
         check(lib().sinter_model_greedy(self.h, token, pos, n, out), "greedy")
         return list(out)
+
+    def logits(self, out=None):
+        """Logits of the last decoded pass (float32[n_vocab])."""
+        import numpy as np
+        if out is None:
+            out = np.zeros(self.cfg.n_vocab, np.float32)
+        check(lib().sinter_model_logits(self.h, out.ctypes.data), "logits")
+        return out
 
     def tensor(self, layer, slot):
         p, nb, t = vp(), C.c_size_t(), C.c_int()
