@@ -337,6 +337,52 @@ sinter_host *sinter_model_host(sinter_model *m);
  * (sinter_host_set_gemv_shares), and a GEMV shape whose tail got longer keeps
  * its best shares.  Results are unchanged. */
 int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces);
+/* the configuration the model was created with */
+int sinter_model_get_config(sinter_model *m, sinter_model_config *cfg);
+
+/* ------------------------------------------------------------------ GGUF */
+/* A read-only GGUF v3 file (k0/gguf.h:30-246 File::open/parse/find/find_kv,
+ * with the K-quant, Q8_0 and BF16 block sizes added).  The file is
+ * memory-mapped; tensor data pointers point into the mapping and stay valid
+ * until sinter_gguf_close.  Malformed files (magic, version, truncation,
+ * unknown tensor type, partial blocks, misaligned or out-of-file data) are
+ * refused with SINTER_ERR_ARG. */
+typedef struct sinter_gguf sinter_gguf;
+typedef struct sinter_gguf_tensor {
+    const char *name;     /* owned by the handle */
+    uint32_t type;        /* ggml type id (sinter_type numbering) */
+    uint32_t n_dims;
+    uint64_t ne[4];       /* ne[0] = elements per row */
+    uint64_t offset;      /* from the start of the data section */
+    uint64_t nbytes;
+    const void *data;     /* host pointer into the mapping */
+} sinter_gguf_tensor;
+int  sinter_gguf_open(const char *path, sinter_gguf **out);
+void sinter_gguf_close(sinter_gguf *g);
+int  sinter_gguf_info(sinter_gguf *g, uint32_t *version, uint64_t *n_tensors, uint64_t *n_kv, uint64_t *alignment);
+int  sinter_gguf_get_tensor(sinter_gguf *g, uint64_t i, sinter_gguf_tensor *out);
+/* index of the named tensor, or -1 */
+int64_t sinter_gguf_find(sinter_gguf *g, const char *name);
+int  sinter_gguf_kv_i64(sinter_gguf *g, const char *key, int64_t *out);   /* integer or bool */
+int  sinter_gguf_kv_f64(sinter_gguf *g, const char *key, double *out);    /* any number */
+int  sinter_gguf_kv_str(sinter_gguf *g, const char *key, char *buf, size_t n);
+/* integer array: copies min(cap, length) values, *n = length */
+int  sinter_gguf_kv_arr_i64(sinter_gguf *g, const char *key, int64_t *out, size_t cap, size_t *n);
+/* The model shape of a GGUF file (k0/harness.cpp:315-400 Residency): sizes
+ * from the tensor table -- n_embd and n_vocab from token_embd, blocks from
+ * blk.N.attn_norm (less <arch>.nextn_predict_layers), attention blocks from
+ * blk.N.attn_q (every attn_every-th), head sizes from the q/k norms, the
+ * gated-DeltaNet heads from ssm_norm / ssm_a / attn_qkv -- and rope
+ * dimensions, rope base and the RMS eps from <arch>.rope.dimension_count,
+ * <arch>.rope.freq_base, <arch>.attention.layer_norm_rms_epsilon. */
+int  sinter_model_config_from_gguf(sinter_gguf *g, int32_t n_ctx, sinter_model_config *cfg);
+/* A model whose weights are the file's tensors, uploaded as they lie in the
+ * file (GGUF names blk.N.<name>.weight, ssm_dt.bias, ssm_a; without
+ * output.weight the head is token_embd).  Each tensor keeps its own type
+ * (Q4_K, Q6_K, Q8_0, BF16 or F32 weights; F32 norms and conv weights); the
+ * segments of one fused GEMV must share an activation type.  The file may be
+ * closed after this returns. */
+int  sinter_model_create_from_gguf(sinter_gguf *g, int device, int32_t n_ctx, uint32_t blocks, sinter_model **out);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsinter.so")
 REPORT = os.path.join(HERE, "resource_usage.txt")
-SOURCES = ["interp.hip", "host.cpp", "model.cpp"]
+SOURCES = ["interp.hip", "host.cpp", "model.cpp", "gguf.cpp"]
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",

@@ -84,6 +84,7 @@ struct sinter_model {
     uint64_t weight_bytes = 0;
     std::vector<void *> allocs;
     uint64_t seed = 0;
+    sinter_gguf *gg = nullptr;   // weights come from this file when set (else synthesised)
 };
 
 namespace {
@@ -98,7 +99,58 @@ void *dalloc(sinter_model *m, size_t bytes) {
     return p;
 }
 
+// GGUF tensor name of a weight: blk.<il>.<name>.weight (globals: <name>.weight)
+std::string gguf_name(const char *name, int il) {
+    std::string n = name;
+    n = n == "ssm_dt_bias" ? "ssm_dt.bias" : n == "ssm_a" ? n : n + ".weight";
+    return il >= 0 ? "blk." + std::to_string(il) + "." + n : n;
+}
+
+// The GGUF tensor for a weight of `rows` rows of k elements: it must exist
+// with exactly that shape and a type the kernels read.  Returns its index
+// (set_error and -1 otherwise).
+int64_t gguf_lookup(sinter_model *m, const char *name, int il, int64_t rows, int64_t k, bool want_f32) {
+    const std::string gn = gguf_name(name, il);
+    const int64_t i = sinter_gguf_find(m->gg, gn.c_str());
+    sinter_gguf_tensor t;
+    if (i < 0 || sinter_gguf_get_tensor(m->gg, (uint64_t)i, &t) != SINTER_OK) {
+        set_error(SINTER_ERR_ARG, "gguf: tensor %s missing", gn.c_str());
+        return -1;
+    }
+    // weights: rows of k elements; f32 vectors (norms, conv taps [dconv x C]
+    // with the taps of a channel contiguous): the element count
+    const bool shape_ok = want_f32 ? (int64_t)(t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3]) == rows * k
+                                   : (int64_t)t.ne[0] == k && (int64_t)(t.ne[1] * t.ne[2] * t.ne[3]) == rows;
+    if (!shape_ok) {
+        set_error(SINTER_ERR_ARG, "gguf: tensor %s is %llux%llu, the model needs %lldx%lld", gn.c_str(),
+                  (unsigned long long)t.ne[0], (unsigned long long)(t.ne[1] * t.ne[2] * t.ne[3]), (long long)k,
+                  (long long)rows);
+        return -1;
+    }
+    const bool ok = want_f32 ? t.type == SINTER_F32
+                             : (t.type == SINTER_Q4_K || t.type == SINTER_Q6_K || t.type == SINTER_Q8_0 ||
+                                t.type == SINTER_BF16 || t.type == SINTER_F32);
+    if (!ok) {
+        set_error(SINTER_ERR_ARG, "gguf: tensor %s has type %u, which the kernels do not read here", gn.c_str(), t.type);
+        return -1;
+    }
+    return i;
+}
+
+bool upload(sinter_model *m, Tensor &t, int64_t gi) {
+    sinter_gguf_tensor g;
+    if (sinter_gguf_get_tensor(m->gg, (uint64_t)gi, &g) != SINTER_OK || g.nbytes != t.bytes) return false;
+    return hip_ok(hipMemcpyAsync(t.d, g.data, t.bytes, hipMemcpyHostToDevice, m->stream), "gguf upload");
+}
+
 bool make_weight(sinter_model *m, Tensor &t, const char *name, int il, int type, int64_t rows, int64_t k) {
+    int64_t gi = -1;
+    if (m->gg) {
+        if ((gi = gguf_lookup(m, name, il, rows, k, false)) < 0) return false;
+        sinter_gguf_tensor g;
+        sinter_gguf_get_tensor(m->gg, (uint64_t)gi, &g);
+        type = (int)g.type;
+    }
     t.type = type;
     t.rows = rows;
     t.k = k;
@@ -106,11 +158,14 @@ bool make_weight(sinter_model *m, Tensor &t, const char *name, int il, int type,
     t.d = dalloc(m, t.bytes);
     if (!t.d) return false;
     m->weight_bytes += t.bytes;
+    if (m->gg) return upload(m, t, gi);
     return launch_synth(t.d, SINTER_SYN_WEIGHT, type, (uint64_t)rows * (uint64_t)(k / 256),
                         sinter_seed(m->seed, name, il), 0.f, 0.f, m->stream) == hipSuccess;
 }
 
 bool make_vec(sinter_model *m, Tensor &t, const char *name, int il, int64_t n, int kind, float a, float b) {
+    int64_t gi = -1;
+    if (m->gg && (gi = gguf_lookup(m, name, il, 1, n, true)) < 0) return false;
     t.type = SINTER_F32;
     t.rows = 1;
     t.k = n;
@@ -118,6 +173,7 @@ bool make_vec(sinter_model *m, Tensor &t, const char *name, int il, int64_t n, i
     t.d = dalloc(m, t.bytes);
     if (!t.d) return false;
     m->weight_bytes += t.bytes;
+    if (m->gg) return upload(m, t, gi);
     return launch_synth(t.d, kind, SINTER_F32, (uint64_t)n, sinter_seed(m->seed, name, il), a, b, m->stream) ==
            hipSuccess;
 }
@@ -335,7 +391,10 @@ void sinter_model_destroy(sinter_model *m) {
     delete m;
 }
 
-int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks,
+}  // extern "C"
+
+// Allocate, fill (synthesise, or upload from gg) and program a model.
+static int model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks, sinter_gguf *gg,
                         sinter_model **out) {
     if (!cfg || !out) return set_error(SINTER_ERR_ARG, "model: null argument");
     *out = nullptr;
@@ -345,7 +404,8 @@ int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t see
     m->cfg = *cfg;
     m->device = device;
     m->seed = seed;
-    auto fail = [&](int st) { sinter_model_destroy(m); return st; };
+    m->gg = gg;
+    auto fail = [&](int st) { m->gg = nullptr; sinter_model_destroy(m); return st; };
     if ((rc = sinter_host_init(&m->host, device, 1024)) != SINTER_OK) return fail(rc);
     uint32_t hb = 0;
     sinter_host_grid(m->host, &hb, nullptr, nullptr);
@@ -396,7 +456,9 @@ int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t see
     }
     ok = ok && make_weight(m, m->embd, "token_embd", -1, c.t_embd, c.n_vocab, E);
     ok = ok && make_vec(m, m->onorm, "output_norm", -1, E, SINTER_SYN_NORMAL, 1.0f, 0.02f);
-    ok = ok && make_weight(m, m->output, "output", -1, c.t_output, c.n_vocab, E);
+    // a GGUF without output.weight ties the head to the embedding
+    const bool tied = gg && sinter_gguf_find(gg, "output.weight") < 0;
+    ok = ok && make_weight(m, m->output, tied ? "token_embd" : "output", -1, c.t_output, c.n_vocab, E);
     auto fa = [&](size_t n) { return (float *)dalloc(m, n * 4); };
     ok = ok && (m->X = fa(E)) && (m->H = fa(E)) && (m->qkv = fa(C)) && (m->z = fa(VD)) && (m->al = fa(HV)) &&
          (m->be = fa(HV)) && (m->o = fa(VD)) && (m->ffn = fa(F)) && (m->qg = fa((size_t)NQ * 2 * HD)) &&
@@ -404,8 +466,12 @@ int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t see
     const uint32_t chunks = attn_chunks(m->blocks, NKV);
     ok = ok && (m->part = (double *)dalloc(m, sinter_attn_part_len(NQ, NKV, HD, chunks) * 8));
     ok = ok && (m->count = (unsigned *)dalloc(m, (size_t)sinter_attn_count_len(NKV, chunks) * 4));
-    if (!ok) return fail(set_error(SINTER_ERR_NOMEM, "model: device allocation or synthesis failed"));
+    if (!ok) {
+        if (gg && std::strncmp(sinter_last_error(), "gguf", 4) == 0) return fail(SINTER_ERR_ARG);
+        return fail(set_error(SINTER_ERR_NOMEM, "model: device allocation or synthesis failed"));
+    }
     if (!hip_ok(hipStreamSynchronize(m->stream), "model synthesis")) return fail(SINTER_ERR_HIP);
+    m->gg = nullptr;   // every byte is on the device now; the caller owns the file
     uint32_t hcap = 0;
     int32_t *hist = sinter_host_history(m->host, &hcap);
     if ((rc = sinter_argmax_ws_create(m->blocks, &sinter_host_pass_cell(m->host)->token, hist, hcap, &m->ws)))
@@ -415,6 +481,108 @@ int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t see
         return fail(rc);
     if ((rc = sinter_host_launch(m->host))) return fail(rc);
     *out = m;
+    return SINTER_OK;
+}
+
+// The model shape of a GGUF file, from its tensor table (shapes are what the
+// weights are) and, for the scalars no tensor carries, its metadata.
+static int gguf_config(sinter_gguf *g, int32_t n_ctx, sinter_model_config *c) {
+    auto tensor = [&](const std::string &n, sinter_gguf_tensor *t) {
+        const int64_t i = sinter_gguf_find(g, n.c_str());
+        return i >= 0 && sinter_gguf_get_tensor(g, (uint64_t)i, t) == SINTER_OK;
+    };
+    std::memset(c, 0, sizeof *c);
+    sinter_gguf_tensor t;
+    if (!tensor("token_embd.weight", &t)) return set_error(SINTER_ERR_ARG, "gguf: no token_embd.weight");
+    c->n_embd = (int32_t)t.ne[0];
+    c->n_vocab = (int32_t)t.ne[1];
+    c->t_embd = (int32_t)t.type;
+    char arch[128] = "";
+    (void)sinter_gguf_kv_str(g, "general.architecture", arch, sizeof arch);
+    const std::string a = arch;
+    int64_t iv = 0;
+    double fv = 0.0;
+    // decoder blocks: blk.0 .. blk.N-1 with a mixer, less the multi-token
+    // prediction blocks the decode graph does not run
+    int n = 0;
+    while (tensor("blk." + std::to_string(n) + ".attn_norm.weight", &t)) n++;
+    if (sinter_gguf_kv_i64(g, (a + ".nextn_predict_layers").c_str(), &iv) == SINTER_OK && iv > 0 && iv < n) n -= (int)iv;
+    c->n_layer = n;
+    if (n < 1) return set_error(SINTER_ERR_ARG, "gguf: no decoder blocks");
+    int first_attn = -1;
+    for (int il = 0; il < n && first_attn < 0; il++)
+        if (tensor("blk." + std::to_string(il) + ".attn_q.weight", &t)) first_attn = il;
+    c->attn_every = first_attn + 1;
+    for (int il = 0; il < n; il++) {
+        const std::string b = "blk." + std::to_string(il) + ".";
+        const bool at = tensor(b + "attn_q.weight", &t), dn = tensor(b + "ssm_a", &t);
+        const bool want = first_attn >= 0 && il % c->attn_every == c->attn_every - 1;
+        if (at == dn) return set_error(SINTER_ERR_ARG, "gguf: block %d is neither an attention nor a gated-DeltaNet block", il);
+        if (at != want) return set_error(SINTER_ERR_ARG, "gguf: attention blocks are not every %d-th block", c->attn_every);
+    }
+    if (!tensor("blk.0.ffn_gate.weight", &t)) return set_error(SINTER_ERR_ARG, "gguf: no blk.0.ffn_gate.weight");
+    c->n_ff = (int32_t)t.ne[1];
+    c->t_default = (int32_t)t.type;
+    if (tensor("blk.0.ffn_down.weight", &t)) c->t_ffn_down = (int32_t)t.type;
+    int gdn = -1;   // the first gated-DeltaNet block
+    for (int il = 0; il < n && gdn < 0; il++)
+        if (!(c->attn_every > 0 && il % c->attn_every == c->attn_every - 1)) gdn = il;
+    if (gdn >= 0) {
+        const std::string b = "blk." + std::to_string(gdn) + ".";
+        sinter_gguf_tensor qkv, cw;
+        if (!tensor(b + "ssm_norm.weight", &t) || !tensor(b + "ssm_a", &cw) || !tensor(b + "attn_qkv.weight", &qkv))
+            return set_error(SINTER_ERR_ARG, "gguf: gated-DeltaNet block %d lacks ssm_norm / ssm_a / attn_qkv", gdn);
+        c->gdn_d = (int32_t)t.ne[0];
+        c->gdn_hv = (int32_t)cw.ne[0];
+        c->gdn_hk = (int32_t)(((int64_t)qkv.ne[1] - (int64_t)c->gdn_hv * c->gdn_d) / (2 * c->gdn_d));
+        if (!tensor(b + "ssm_conv1d.weight", &t)) return set_error(SINTER_ERR_ARG, "gguf: no %sssm_conv1d.weight", b.c_str());
+        c->conv_k = (int32_t)t.ne[0];
+    }
+    if (first_attn >= 0) {
+        const std::string b = "blk." + std::to_string(first_attn) + ".";
+        sinter_gguf_tensor q, k, v;
+        if (!tensor(b + "attn_q_norm.weight", &t) || !tensor(b + "attn_q.weight", &q) || !tensor(b + "attn_k.weight", &k) ||
+            !tensor(b + "attn_v.weight", &v))
+            return set_error(SINTER_ERR_ARG, "gguf: attention block %d lacks q_norm / q / k / v", first_attn);
+        c->head_dim = (int32_t)t.ne[0];
+        c->attn_nq = (int32_t)(q.ne[1] / (2 * (uint64_t)c->head_dim));
+        c->attn_nkv = (int32_t)(k.ne[1] / (uint64_t)c->head_dim);
+        c->t_attn_v = (int32_t)v.type;
+    }
+    c->rope_dims = c->head_dim / 4;
+    if (sinter_gguf_kv_i64(g, (a + ".rope.dimension_count").c_str(), &iv) == SINTER_OK) c->rope_dims = (int32_t)iv;
+    c->rope_base = 10000.0f;
+    if (sinter_gguf_kv_f64(g, (a + ".rope.freq_base").c_str(), &fv) == SINTER_OK) c->rope_base = (float)fv;
+    c->eps = 1e-6f;
+    if (sinter_gguf_kv_f64(g, (a + ".attention.layer_norm_rms_epsilon").c_str(), &fv) == SINTER_OK) c->eps = (float)fv;
+    c->n_ctx = n_ctx;
+    c->t_output = tensor("output.weight", &t) ? (int32_t)t.type : c->t_embd;
+    return SINTER_OK;
+}
+
+extern "C" {
+
+int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks,
+                        sinter_model **out) {
+    return model_create(cfg, device, seed, blocks, nullptr, out);
+}
+
+int sinter_model_config_from_gguf(sinter_gguf *g, int32_t n_ctx, sinter_model_config *cfg) {
+    if (!g || !cfg || n_ctx < 1) return set_error(SINTER_ERR_ARG, "config_from_gguf: args");
+    return gguf_config(g, n_ctx, cfg);
+}
+
+int sinter_model_create_from_gguf(sinter_gguf *g, int device, int32_t n_ctx, uint32_t blocks, sinter_model **out) {
+    if (!g || !out) return set_error(SINTER_ERR_ARG, "create_from_gguf: null argument");
+    sinter_model_config c;
+    const int rc = gguf_config(g, n_ctx, &c);
+    if (rc != SINTER_OK) return rc;
+    return model_create(&c, device, 0, blocks, g, out);
+}
+
+int sinter_model_get_config(sinter_model *m, sinter_model_config *cfg) {
+    if (!m || !cfg) return set_error(SINTER_ERR_ARG, "get_config: args");
+    *cfg = m->cfg;
     return SINTER_OK;
 }
 

@@ -64,6 +64,11 @@ class AttnArgs(C.Structure):
                 ("eps", C.c_float), ("scale", C.c_float), ("_pad", C.c_uint32)]
 
 
+class GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("data", vp)]
+
+
 class PassCell(C.Structure):
     _fields_ = [("token", C.c_int32), ("pos", C.c_int32), ("steps", C.c_int32), ("_pad", C.c_int32)]
 
@@ -162,6 +167,18 @@ def lib():
         "sinter_model_info": (I, [vp, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
         "sinter_model_host": (vp, [vp]),
         "sinter_model_balance": (I, [vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32), U32, U32]),
+        "sinter_model_get_config": (I, [vp, C.POINTER(ModelConfig)]),
+        "sinter_gguf_open": (I, [C.c_char_p, C.POINTER(vp)]),
+        "sinter_gguf_close": (None, [vp]),
+        "sinter_gguf_info": (I, [vp, C.POINTER(U32), C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+        "sinter_gguf_get_tensor": (I, [vp, U64, C.POINTER(GgufTensor)]),
+        "sinter_gguf_find": (I64, [vp, C.c_char_p]),
+        "sinter_gguf_kv_i64": (I, [vp, C.c_char_p, C.POINTER(I64)]),
+        "sinter_gguf_kv_f64": (I, [vp, C.c_char_p, C.POINTER(C.c_double)]),
+        "sinter_gguf_kv_str": (I, [vp, C.c_char_p, C.c_char_p, C.c_size_t]),
+        "sinter_gguf_kv_arr_i64": (I, [vp, C.c_char_p, C.POINTER(I64), C.c_size_t, C.POINTER(C.c_size_t)]),
+        "sinter_model_config_from_gguf": (I, [vp, C.c_int32, C.POINTER(ModelConfig)]),
+        "sinter_model_create_from_gguf": (I, [vp, I, C.c_int32, U32, C.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -194,13 +211,79 @@ def op_error():
     return code.value, aux.value
 
 
+class Gguf:
+    """A read-only GGUF file (sinter_gguf_*)."""
+
+    def __init__(self, path):
+        h = vp()
+        check(lib().sinter_gguf_open(path.encode(), C.byref(h)), "gguf_open")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().sinter_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def info(self):
+        v, nt, nk, al = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        check(lib().sinter_gguf_info(self.h, C.byref(v), C.byref(nt), C.byref(nk), C.byref(al)), "gguf_info")
+        return {"version": v.value, "n_tensors": nt.value, "n_kv": nk.value, "alignment": al.value}
+
+    def tensor(self, i):
+        t = GgufTensor()
+        check(lib().sinter_gguf_get_tensor(self.h, i, C.byref(t)), "gguf_tensor")
+        return t
+
+    def find(self, name):
+        return lib().sinter_gguf_find(self.h, name.encode())
+
+    def kv_i64(self, key):
+        v = C.c_int64()
+        check(lib().sinter_gguf_kv_i64(self.h, key.encode(), C.byref(v)), "gguf_kv_i64")
+        return v.value
+
+    def kv_f64(self, key):
+        v = C.c_double()
+        check(lib().sinter_gguf_kv_f64(self.h, key.encode(), C.byref(v)), "gguf_kv_f64")
+        return v.value
+
+    def kv_str(self, key):
+        buf = C.create_string_buffer(4096)
+        check(lib().sinter_gguf_kv_str(self.h, key.encode(), buf, 4096), "gguf_kv_str")
+        return buf.value.decode()
+
+    def kv_arr_i64(self, key):
+        n = C.c_size_t()
+        check(lib().sinter_gguf_kv_arr_i64(self.h, key.encode(), None, 0, C.byref(n)), "gguf_kv_arr")
+        out = (C.c_int64 * max(1, n.value))()
+        check(lib().sinter_gguf_kv_arr_i64(self.h, key.encode(), out, n.value, C.byref(n)), "gguf_kv_arr")
+        return list(out)[:n.value]
+
+    def config(self, n_ctx):
+        c = ModelConfig()
+        check(lib().sinter_model_config_from_gguf(self.h, n_ctx, C.byref(c)), "config_from_gguf")
+        return c
+
+
 class Model:
     """Owner of a sinter_model handle."""
 
-    def __init__(self, cfg, seed=1, device=0, blocks=0):
-        self.cfg = cfg
+    def __init__(self, cfg, seed=1, device=0, blocks=0, gguf=None):
         h = vp()
-        check(lib().sinter_model_create(C.byref(cfg), device, seed, blocks, C.byref(h)), "model_create")
+        if gguf is not None:
+            check(lib().sinter_model_create_from_gguf(gguf.h, device, cfg.n_ctx, blocks, C.byref(h)),
+                  "model_create_from_gguf")
+            cfg = ModelConfig()
+            check(lib().sinter_model_get_config(h, C.byref(cfg)), "get_config")
+        else:
+            check(lib().sinter_model_create(C.byref(cfg), device, seed, blocks, C.byref(h)), "model_create")
+        self.cfg = cfg
         self.h = h
 
     def close(self):
