@@ -267,7 +267,19 @@ float sinter_host_last_launch_ms(sinter_host *h);
 int sinter_op_gemv(const sinter_gemv_args *a, uint32_t blocks, void *stream);
 int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream);
 int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream);
-/* synchronise the device and read/clear the op error cell of the current device */
+/* The attention op without caller workspace, allocating nothing: no
+ * counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  As sinter_op_attn_decode, except that a->part and
+ * a->count must be NULL: the split-K partials (at most 4 MiB,
+ * sinter_attn_part_len(...) * 8 bytes) and the generation flags (at most
+ * 1024, sinter_attn_count_len(...)) live in a fixed device array the library
+ * holds on each GPU it runs on until the process ends; larger shapes are
+ * refused with SINTER_ERR_ARG.  Every call on a GPU shares that array (its
+ * flags are cleared by a small kernel at the start of each call): calls that
+ * overlap on one GPU race.  Errors go to the cell sinter_op_error reads. */
+int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, void *stream);
+/* synchronise the device and read/clear the op error cells of the current device */
 int sinter_op_error(uint32_t *code, uint32_t *aux);
 /* argmax workspace for `blocks` workgroups (allocated on the current device) */
 int sinter_argmax_ws_create(uint32_t blocks, int32_t *pass_cell, int32_t *history,

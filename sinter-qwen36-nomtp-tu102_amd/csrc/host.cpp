@@ -403,6 +403,20 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
     return run_one(SINTER_OP_ATTN_DECODE, *a, blocks, stream);
 }
 
+int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, void *stream) {
+    if (!a || !a->qg || !a->k || !a->v || !a->q_norm || !a->k_norm || !a->kc || !a->vc || !a->out || !a->pass_cell)
+        return set_error(SINTER_ERR_ARG, "attn_noalloc: null pointer");
+    if (a->part || a->count)
+        return set_error(SINTER_ERR_ARG, "attn_noalloc: part and count must be NULL (the library supplies them)");
+    if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
+        a->rope_dims > a->hd || a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
+        return set_error(SINTER_ERR_ARG, "attn_noalloc: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
+    if ((uint64_t)a->nkv * a->n_chunks > blocks || blocks > PLAN_MAX_BLOCKS)
+        return set_error(SINTER_ERR_ARG, "attn_noalloc: blocks (%u) must be >= nkv * n_chunks (%u) and <= %u", blocks,
+                         a->nkv * a->n_chunks, PLAN_MAX_BLOCKS);
+    return attn_noalloc(*a, blocks, (hipStream_t)stream);
+}
+
 int sinter_op_error(uint32_t *code, uint32_t *aux) {
     unsigned *err = op_err_cell();
     if (!err) return set_error(SINTER_ERR_HIP, "no error cell");
@@ -410,6 +424,15 @@ int sinter_op_error(uint32_t *code, uint32_t *aux) {
     unsigned h[2] = {0, 0};
     if (!hip_ok(hipMemcpy(h, err, 8, hipMemcpyDeviceToHost), "error cell read")) return SINTER_ERR_HIP;
     if (!hip_ok(hipMemset(err, 0, 8), "error cell clear")) return SINTER_ERR_HIP;
+    // the no-allocation op's cell on this device, when it has run here
+    if (unsigned *e2 = noalloc_err_cell()) {
+        unsigned h2[2] = {0, 0};
+        const unsigned zero[2] = {0, 0};
+        if (!hip_ok(hipMemcpy(h2, e2, 8, hipMemcpyDeviceToHost), "error cell read") ||
+            !hip_ok(hipMemcpy(e2, zero, 8, hipMemcpyHostToDevice), "error cell clear"))
+            return SINTER_ERR_HIP;
+        if (!h[0]) { h[0] = h2[0]; h[1] = h2[1]; }
+    }
     if (code) *code = h[0];
     if (aux) *aux = h[1];
     return SINTER_OK;

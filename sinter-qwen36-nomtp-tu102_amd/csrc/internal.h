@@ -35,6 +35,10 @@ hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_
 int set_error(int status, const char *fmt, ...);
 bool hip_ok(hipError_t e, const char *what);
 unsigned *op_err_cell();  // per-device error cell of the standalone op launches
+// the no-allocation attention op (interp.hip): validate sizes, launch on s
+int attn_noalloc(const sinter_attn_args &a, uint32_t blocks, hipStream_t s);
+// its error cell on the current device (null before its first call there)
+unsigned *noalloc_err_cell();
 int validate_gemv(const sinter_gemv_args &a, const char **why);
 // the plan and the nblk + 1 row cuts of a validated GEMV run by nblk workgroups
 // bw: per-block work weights (null: uniform)

@@ -16,6 +16,9 @@
 // program ends the kernel instead of hanging the device.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+#include <mutex>
+
 #include "internal.h"
 #include "gemv.h"
 #include "gdn.h"
@@ -149,6 +152,30 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
     }
 }
 
+// ---------------------------------------------------------------- no-allocation attention
+// sinter_op_attn_decode_noalloc: the standalone attention op with its split-K
+// partials, per-chunk generation flags and error cell in this file-scope
+// device array instead of caller-allocated workspace.  Layout: error cell
+// [0, 256) | flags [256, 256 + 4 * NOALLOC_FLAG_WORDS) | partials (fp64).
+// Every call on a device shares the array; calls that overlap on one
+// device race.
+constexpr size_t NOALLOC_FLAG_WORDS = 1024;
+constexpr size_t NOALLOC_PART_BYTES = 4u << 20;
+constexpr size_t NOALLOC_FLAG_OFF = 256, NOALLOC_PART_OFF = NOALLOC_FLAG_OFF + NOALLOC_FLAG_WORDS * 4;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_PART_OFF + NOALLOC_PART_BYTES];
+
+// p[0..n) = 0 (a kernel rather than a memset node, so a caller may capture it)
+extern "C" __global__ void sinter_clear_u32(unsigned *p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The attention op with its instruction passed by value (nothing staged in
+// device memory for it).
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS) sinter_op_noalloc_kernel(sinter_instr ins, unsigned *err) {
+    op_attn_decode(ins, err, nullptr, 200000000ull, ATT_NO_CACHE);
+}
+
 // Synthetic tensor fill: one thread per 256-element group (weights) or per
 // element (f32 / f16 tensors).
 extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type, uint64_t n_units,
@@ -195,6 +222,63 @@ hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_
 hipError_t interp_max_blocks(int *blocks_per_cu) {
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void *)sinter_interp,
                                                         BLOCK_THREADS, 0);
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (hipGetSymbolAddress with that device current) and kept: the
+// array's name is not a device address in host code.
+static std::mutex g_noalloc_mu;
+static unsigned char *g_noalloc_ptr[64];
+
+static unsigned char *noalloc_scratch(int *dev_out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (dev_out) *dev_out = dev;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_noalloc_ptr[dev] = static_cast<unsigned char *>(p);
+    }
+    return g_noalloc_ptr[dev];
+}
+
+unsigned *noalloc_err_cell() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    return reinterpret_cast<unsigned *>(g_noalloc_ptr[dev]);
+}
+
+int attn_noalloc(const sinter_attn_args &args, uint32_t blocks, hipStream_t s) {
+    const size_t part_bytes = sinter_attn_part_len(args.nq, args.nkv, args.hd, args.n_chunks) * 8;
+    const uint32_t flags = sinter_attn_count_len(args.nkv, args.n_chunks);
+    if (part_bytes > NOALLOC_PART_BYTES || flags > NOALLOC_FLAG_WORDS)
+        return set_error(SINTER_ERR_ARG,
+                         "attn_noalloc: %zu B of partials and %u flags exceed the scratch maximum (%zu B, %zu flags)",
+                         part_bytes, flags, NOALLOC_PART_BYTES, NOALLOC_FLAG_WORDS);
+    unsigned char *p = noalloc_scratch(nullptr);
+    if (!p) return set_error(SINTER_ERR_HIP, "attn_noalloc: hipGetSymbolAddress(scratch) failed");
+    sinter_instr ins;
+    std::memset(&ins, 0, sizeof ins);
+    ins.kind = SINTER_OP_ATTN_DECODE;
+    ins.block_lo = 0;
+    ins.block_hi = (uint16_t)blocks;
+    sinter_attn_args a = args;
+    a.part = reinterpret_cast<double *>(p + NOALLOC_PART_OFF);
+    a.count = reinterpret_cast<uint32_t *>(p + NOALLOC_FLAG_OFF);
+    std::memcpy(ins.payload, &a, sizeof a);
+    // every chunk starts the call at generation 0 (an earlier call may have
+    // used another chunk split, leaving mixed generations in one head)
+    hipLaunchKernelGGL(sinter_clear_u32, dim3((flags + 255) / 256), dim3(256), 0, s, a.count, flags);
+    if (!hip_ok(hipGetLastError(), "attn_noalloc: flag clear")) return SINTER_ERR_HIP;
+    unsigned *err = reinterpret_cast<unsigned *>(p);
+    void *kargs[] = {(void *)&ins, (void *)&err};
+    if (!hip_ok(hipLaunchCooperativeKernel((const void *)sinter_op_noalloc_kernel, dim3(blocks), dim3(BLOCK_THREADS),
+                                           kargs, 0, s),
+                "attn_noalloc: launch"))
+        return SINTER_ERR_HIP;
+    return SINTER_OK;
 }
 
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
