@@ -38,6 +38,9 @@ __device__ __forceinline__ int vec_dot_type(int t) {
          : (t == SINTER_Q8_0) ? SINTER_Q8_0
          : (t == SINTER_BF16) ? SINTER_BF16 : SINTER_F32;
 }
+// wave-uniform copy of a value (its first active lane), kept in an SGPR
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // ------------------------------------------------------------ activation layout in LDS
 // (ACT_* constants and act_bytes are in isa.h, shared with host validation)
 struct ActView {
@@ -272,6 +275,122 @@ __device__ __forceinline__ void quant_chunk(int vt, uint32_t c, uint32_t r, cons
     }
 }
 
+// Q8_K with one sub-block per lane: lane r of a 16-lane row holds elements
+// 16r + i (i = 0..15) of its chunk, i.e. Q8_K sub-block r, so its 16 codes
+// are one 16-byte store and its bsum is the lane's own sum.  The row's
+// signed max and min come from IEEE-2019 maximum / minimum (v_maximum3 /
+// v_minimum3: NaNs propagate, so a chunk holding a NaN fails the finite-max
+// test and takes the exact path).  Bit-identical to quant_chunk's Q8_K
+// branch: the same bmax, iscale, codes, d and bsums.
+__device__ __forceinline__ float fmax2019(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmin2019(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+// quant_q8k_exact for the sub-block-per-lane layout (element 16r + i)
+__device__ __forceinline__ float quant_q8k_exact_span(uint32_t r, const float t[16], uint32_t b[16]) {
+    float ax[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) ax[i] = fabsf(t[i]);
+    float am = ax[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) am = fmaxf(am, ax[i]);
+    const float A = row16_max(am);
+    int key = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int e = 16 * (int)r + i;
+        if (ax[i] == A) key = min(key, (e << 1) | (t[i] < 0.0f ? 1 : 0));
+    }
+    const int gkey = row16_min(key);
+    if (!(A > 0.0f)) {    // max |x| == 0 (NaNs never win): all codes 0, d = 0
+#pragma unroll
+        for (int i = 0; i < 16; i++) b[i] = 0x4B400000u;
+        return 0.0f;
+    }
+    const float bmax = (gkey & 1) ? -A : A;
+    const float iscale = -127.f / bmax;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float f = iscale * t[i];
+        const int v = (int)(__float_as_uint(f + 12582912.f) & 0x007fffffu) - 0x00400000;
+        b[i] = (uint32_t)(int32_t)(int8_t)(v < 127 ? v : 127) + 0x4B400000u;   // the stored int8
+    }
+    return 1.0f / iscale;
+}
+
+// Fast path of quant_q8k_span: b[i] = bits(iscale*t[i] + 1.5*2^23) (the
+// code is b's low byte) and d; returns true when the row must take the
+// exact path instead.  With NaN-propagating max / min, a NaN or infinite
+// element makes A non-finite; with A finite and non-zero and iscale =
+// -127/bmax finite, every |iscale*t| <= 127 (1 + 2^-24)^2 < 127.5, so every
+// code lies in [-127, 127] and min(127, .) is a no-op.  Left for the exact
+// path: non-finite A, iscale overflow (denormal A) and +-A ties.
+__device__ __forceinline__ bool q8k_fast(const float t[16], uint32_t b[16], float &dd) {
+    float mx = fmax2019(t[0], t[1]), mn = fmin2019(t[0], t[1]);
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) {
+        mx = fmax2019(mx, fmax2019(t[i], t[i + 1]));
+        mn = fmin2019(mn, fmin2019(t[i], t[i + 1]));
+    }
+    mx = fmax2019(mx, dpp_f<DPP_XOR1>(mx));
+    mn = fmin2019(mn, dpp_f<DPP_XOR1>(mn));
+    mx = fmax2019(mx, dpp_f<DPP_XOR2>(mx));
+    mn = fmin2019(mn, dpp_f<DPP_XOR2>(mn));
+    mx = fmax2019(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+    mn = fmin2019(mn, dpp_f<DPP_HALF_MIRROR>(mn));
+    mx = fmax2019(mx, dpp_f<DPP_MIRROR>(mx));
+    mn = fmin2019(mn, dpp_f<DPP_MIRROR>(mn));
+    // as quant_chunk: bmax's sign from mx / mn unless +A and -A both occur
+    const float A = fmax2019(mx, -mn);
+    const bool zero = A == 0.0f;
+    const float bm = mx > -mn ? mx : mn;
+    const float is = -127.f / bm;
+    const float iscale = zero ? 0.0f : is;
+#pragma unroll
+    for (int i = 0; i < 16; i++) b[i] = __float_as_uint(iscale * t[i] + 12582912.f);
+    dd = zero ? 0.0f : 1.0f / iscale;
+    return !(A <= 3.40282347e38f) || (!zero && (mx == -mn || !(fabsf(is) <= 3.40282347e38f)));
+}
+
+// Store chunk c's codes (b's low bytes), its sub-block bsum and d.
+__device__ __forceinline__ void q8k_store(uint32_t c, uint32_t r, const uint32_t b[16], float dd, lds_char *q,
+                                          LDS float *qd, LDS int16_t *qb) {
+    uint32_t w[4];
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++)
+        w[qq] = __builtin_amdgcn_perm(b[4 * qq + 1], b[4 * qq], 0x0c0c0400u) |
+                __builtin_amdgcn_perm(b[4 * qq + 3], b[4 * qq + 2], 0x04000c0cu);
+    lds_st16(q + c * ACT_GSTRIDE + 16 * r, w[0], w[1], w[2], w[3]);
+    // the bsum: the sub-block's 16 signed codes, summed exactly
+    int bs = __builtin_amdgcn_sdot4((int)w[0], 0x01010101, 0, false);
+    bs = __builtin_amdgcn_sdot4((int)w[1], 0x01010101, bs, false);
+    bs = __builtin_amdgcn_sdot4((int)w[2], 0x01010101, bs, false);
+    bs = __builtin_amdgcn_sdot4((int)w[3], 0x01010101, bs, false);
+    qb[16 * c + r] = (int16_t)bs;
+    if (r == 0) qd[c] = dd;
+}
+
+__device__ __forceinline__ void quant_q8k_span(uint32_t c, uint32_t r, const float t[16], lds_char *q, LDS float *qd,
+                                               LDS int16_t *qb) {
+    uint32_t b[16];
+    float dd;
+    const bool bad = q8k_fast(t, b, dd);
+    if (__builtin_amdgcn_ballot_w64(bad)) dd = quant_q8k_exact_span(r, t, b);
+    q8k_store(c, r, b, dd, q, qd, qb);
+}
+
+// Two chunks at once (independent chains the compiler interleaves).
+__device__ __forceinline__ void quant_q8k_span2(uint32_t c0, uint32_t c1, uint32_t r, const float t0[16],
+                                                const float t1[16], lds_char *q, LDS float *qd, LDS int16_t *qb) {
+    uint32_t b0[16], b1[16];
+    float d0, d1;
+    const bool bad0 = q8k_fast(t0, b0, d0);
+    const bool bad1 = q8k_fast(t1, b1, d1);
+    if (__builtin_amdgcn_ballot_w64(bad0)) d0 = quant_q8k_exact_span(r, t0, b0);
+    if (__builtin_amdgcn_ballot_w64(bad1)) d1 = quant_q8k_exact_span(r, t1, b1);
+    q8k_store(c0, r, b0, d0, q, qd, qb);
+    q8k_store(c1, r, b1, d1, q, qd, qb);
+}
+
 __device__ __forceinline__ u32x4 lds16(const lds_char *p) { return *reinterpret_cast<const LDS u32x4 *>(p); }
 __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret_cast<const LDS f32x4 *>(p); }
 
@@ -283,20 +402,13 @@ __device__ __forceinline__ f32x4 ldsf16(const lds_char *p) { return *reinterpret
 // its elements from the staging area; RMSNorm first sums squares over its
 // chunks for the block-wide scale.
 template <class Post>
-__device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
-                                              unsigned *err, Post &&post) {
+__device__ __forceinline__ void prologue_stage(const sinter_gemv_args &a, bool write_x, unsigned *err, Post &&post) {
     const uint32_t K = a.K;
     const bool embed = a.pro == SINTER_PRO_EMBED;
     const bool gpre = a.pro == SINTER_PRO_GATED_G, gated = a.pro == SINTER_PRO_GATED || gpre;
     const bool rms = a.pro == SINTER_PRO_RMSNORM || embed;
     char *xs_g = g_big, *ys_g = g_big + K * 4;
     const uint32_t gd = 1u << a.gn_log2d;  // gated-norm head width (4..256)
-    // the lane's indices, opaque to the compiler so that the per-lane address
-    // arithmetic below is not hoisted out of the interpreter loop (where it
-    // would stay live, in registers, for the whole kernel)
-    uint32_t tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
     // gated norms: the gd head-width norm weights go to the last KiB of the
     // staging area by one LDS-DMA (lanes past gd/4 re-read the last 16 bytes,
     // in bounds), so that no compiler-visible load precedes the weight slots
@@ -332,91 +444,215 @@ __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt,
         post();
     }
     __syncthreads();
+}
 
-    const LDS float *xs = reinterpret_cast<const LDS float *>((const lds_char *)xs_g);
-    const LDS float *ys = reinterpret_cast<const LDS float *>((const lds_char *)ys_g);
-    // gated-norm weights: element 64q + 4r + i of every chunk uses
-    // norm_w[(64q + 4r + i) % gd]
-    float gw[16];
-    if (gated) {
-        const LDS float *ws = reinterpret_cast<const LDS float *>((const lds_char *)ws_g);
+// The lane's 16 elements of chunk c from LDS: elements 16r + i (SPAN, the
+// Q8_K sub-block-per-lane layout) or 64q + 4r + i (q, i = 0..3: the layout
+// quant_chunk takes).
+template <bool SPAN>
+__device__ __forceinline__ void ld16(const LDS float *base, uint32_t c, uint32_t r, float v[16]) {
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(ws + ((64 * qq + r * 4) & (gd - 1)));
-            gw[4 * qq] = t.x; gw[4 * qq + 1] = t.y; gw[4 * qq + 2] = t.z; gw[4 * qq + 3] = t.w;
-        }
+    for (int qq = 0; qq < 4; qq++) {
+        const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(base + c * 256 + (SPAN ? 16 * r + 4 * qq : 64 * qq + 4 * r));
+        v[4 * qq] = t.x; v[4 * qq + 1] = t.y; v[4 * qq + 2] = t.z; v[4 * qq + 3] = t.w;
     }
-    // the lane's 16 elements of chunk c: 64q + 4r + i
-    auto ld16 = [&](const LDS float *base, uint32_t c, float v[16]) {
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(base + c * 256 + 64 * qq + 4 * r);
-            v[4 * qq] = t.x; v[4 * qq + 1] = t.y; v[4 * qq + 2] = t.z; v[4 * qq + 3] = t.w;
+}
+
+// Norm + quantisation of the staged f32 inputs into the activation layout in
+// g_qbuf, for one vec_dot type VT; the prologue kind and sizes are
+// wave-uniform (scalar branches only).  Row g (16 lanes) owns chunks g,
+// g+16, ...; the next chunk's inputs are read while the current one is
+// quantised.
+template <int VT>
+__device__ __forceinline__ void prologue_quant(uint32_t K, uint32_t pro, uint32_t log2d, float eps, double *red) {
+    constexpr bool SPAN = VT == SINTER_Q8_K;
+    // the lane's indices, opaque to the compiler so that the per-lane address
+    // arithmetic below is not hoisted out of the interpreter loop (where it
+    // would stay live, in registers, for the whole kernel)
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t r = tid & 15, g = tid >> 4, nchunk = K / 256;
+    const LDS float *xs = reinterpret_cast<const LDS float *>((const lds_char *)g_big);
+    const LDS float *ys = xs + K;
+    lds_char *q = (lds_char *)g_qbuf;
+    LDS float *qd = reinterpret_cast<LDS float *>(q + nchunk * ACT_GSTRIDE);
+    LDS int16_t *qb = reinterpret_cast<LDS int16_t *>(q + act_bs_off(K));
+    auto quantize = [&](uint32_t c, const float t[16]) {
+        if constexpr (SPAN) quant_q8k_span(c, r, t, q, qd, qb);
+        else quant_chunk(VT, c, r, t, q, qd, qb);
+    };
+    auto quantize2 = [&](uint32_t c0, uint32_t c1, const float t0[16], const float t1[16]) {
+        if constexpr (SPAN) {
+            quant_q8k_span2(c0, c1, r, t0, t1, q, qd, qb);
+        } else {
+            quant_chunk(VT, c0, r, t0, q, qd, qb);
+            quant_chunk(VT, c1, r, t1, q, qd, qb);
         }
     };
-    // global RMSNorm scale (ggml: fp32 squares summed in double, mean -> f32,
-    // scale = 1/sqrtf(mean + eps))
-    float gscale = 1.0f;
-    if (rms) {
-        double s = 0.0;
-        for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
-            float v[16];
-            ld16(xs, c, v);
-#pragma unroll
-            for (int i = 0; i < 16; i++) s += (double)(v[i] * v[i]);
-        }
-        s = block_sum_f64(s, red);
-        const float mean = (float)(s / (double)K);
-        gscale = 1.0f / sqrtf(mean + a.eps);
-    }
-    lds_char *q = (lds_char *)g_qbuf;
-    LDS float *qd = reinterpret_cast<LDS float *>(q + (K / 256) * ACT_GSTRIDE);
-    LDS int16_t *qb = reinterpret_cast<LDS int16_t *>(q + act_bs_off(K));
+    if (pro == SINTER_PRO_PLAIN) {
+        // chunks in pairs (c, c + 16)
 #pragma unroll 1
-    for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
-        float v[16], y[16], t[16];
-        ld16(xs, c, v);
-        if (a.pro != SINTER_PRO_PLAIN) ld16(ys, c, y);
-        if (a.pro == SINTER_PRO_PLAIN) {
+        for (uint32_t c = g; c < nchunk; c += 2 * PRO_ROWS) {
+            float t0[16];
+            ld16<SPAN>(xs, c, r, t0);
+            if (c + PRO_ROWS < nchunk) {
+                float t1[16];
+                ld16<SPAN>(xs, c + PRO_ROWS, r, t1);
+                quantize2(c, c + PRO_ROWS, t0, t1);
+            } else {
+                quantize(c, t0);
+            }
+        }
+    } else if (pro == SINTER_PRO_RMSNORM || pro == SINTER_PRO_EMBED) {
+        // global RMSNorm scale (ggml: fp32 squares summed in double, mean ->
+        // f32, scale = 1/sqrtf(mean + eps)); the fp64 sum is a fixed tree:
+        // per lane four partial sums over its chunks, then the 16-lane row,
+        // the wave's rows and the waves in order.  The row's first two
+        // chunks stay in registers for the second pass.
+        float v0[16], v1[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) t[i] = v[i];
-        } else if (gated) {
-            // per-head sums of squares in double.  Head h of width gd holds,
-            // on lane r, the elements of each q with (64q + 4r) / gd == h:
-            // its sum combines lanes (DPP) and, for gd >= 128, q's
+        for (int i = 0; i < 16; i++) { v0[i] = 0.0f; v1[i] = 0.0f; }
+        if (g < nchunk) ld16<SPAN>(xs, g, r, v0);
+        if (g + PRO_ROWS < nchunk) ld16<SPAN>(xs, g + PRO_ROWS, r, v1);
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 1
+        for (uint32_t c = g + 2 * PRO_ROWS; c < nchunk; c += PRO_ROWS) {
+            float v[16];
+            ld16<SPAN>(xs, c, r, v);
+#pragma unroll
+            for (int i = 0; i < 16; i++) s4[i / 4] += (double)(v[i] * v[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) s4[i / 4] += (double)(v0[i] * v0[i]);
+#pragma unroll
+        for (int i = 0; i < 16; i++) s4[i / 4] += (double)(v1[i] * v1[i]);
+        double s = row16_sum_f64((s4[0] + s4[1]) + (s4[2] + s4[3]));
+        s = ((readlane_f64(s, 0) + readlane_f64(s, 16)) + readlane_f64(s, 32)) + readlane_f64(s, 48);
+        // every wave has passed the staging barrier, so no reader of an
+        // earlier sum is left; the next writer is past this op's last barrier
+        if (lane_id() == 0) red[wave_id()] = s;
+        float y0[16], y1[16];
+        if (g < nchunk) ld16<SPAN>(ys, g, r, y0);
+        if (g + PRO_ROWS < nchunk) ld16<SPAN>(ys, g + PRO_ROWS, r, y1);
+        __syncthreads();
+        s = ((red[0] + red[1]) + red[2]) + red[3];
+        const float mean = (float)(s / (double)K);
+        const float gscale = 1.0f / sqrtf(mean + eps);
+        // chunks in pairs (c, c + 16), the first pair from registers
+#pragma unroll 1
+        for (uint32_t c = g; c < nchunk; c += 2 * PRO_ROWS) {
+            if (c != g) {
+                ld16<SPAN>(xs, c, r, v0);
+                ld16<SPAN>(ys, c, r, y0);
+                if (c + PRO_ROWS < nchunk) {
+                    ld16<SPAN>(xs, c + PRO_ROWS, r, v1);
+                    ld16<SPAN>(ys, c + PRO_ROWS, r, y1);
+                }
+            }
+            float t0[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) t0[i] = (v0[i] * gscale) * y0[i];
+            if (c + PRO_ROWS < nchunk) {
+                float t1[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) t1[i] = (v1[i] * gscale) * y1[i];
+                quantize2(c, c + PRO_ROWS, t0, t1);
+            } else {
+                quantize(c, t0);
+            }
+        }
+    } else {
+        // gated norm per head of gd = 2^log2d elements: rmsnorm(x_h) * norm_w
+        // * g_h, g = z (GATED_G) or silu(z) (GATED).  Element e of every chunk
+        // uses norm_w[e % gd] (staged in the last KiB of g_big); each group
+        // of four elements of the lane (e, .., e+3) lies in one head (gd >= 4).
+        const bool gpre = pro == SINTER_PRO_GATED_G;
+        const uint32_t gd = 1u << log2d;
+        const double inv_gd = __longlong_as_double((long long)(1023 - log2d) << 52);   // 2^-log2d exactly
+        const LDS float *ws = reinterpret_cast<const LDS float *>((const lds_char *)(g_big + BIG_BYTES - 1024));
+        float gw[16];
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const uint32_t e = SPAN ? 16 * r + 4 * qq : 64 * qq + 4 * r;
+            const f32x4 t = *reinterpret_cast<const LDS f32x4 *>(ws + (e & (gd - 1)));
+            gw[4 * qq] = t.x; gw[4 * qq + 1] = t.y; gw[4 * qq + 2] = t.z; gw[4 * qq + 3] = t.w;
+        }
+#pragma unroll 1
+        for (uint32_t c = g; c < nchunk; c += PRO_ROWS) {
+            float v[16], y[16], t[16];
+            ld16<SPAN>(xs, c, r, v);
+            ld16<SPAN>(ys, c, r, y);
+            // per-head sums of squares in double, s4[qq] for the lane's
+            // elements of group qq
             double s4[4];
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
                 double h = 0.0;
 #pragma unroll
                 for (int i = 0; i < 4; i++) h += (double)(v[4 * qq + i] * v[4 * qq + i]);
-                if (gd >= 8) h += dpp_d<DPP_XOR1>(h);
-                if (gd >= 16) h += dpp_d<DPP_XOR2>(h);
-                if (gd >= 32) h += dpp_d<DPP_HALF_MIRROR>(h);
-                if (gd >= 64) h += dpp_d<DPP_MIRROR>(h);
                 s4[qq] = h;
             }
-            if (gd >= 128) { const double a01 = s4[0] + s4[1], a23 = s4[2] + s4[3]; s4[0] = s4[1] = a01; s4[2] = s4[3] = a23; }
-            if (gd >= 256) { const double all = s4[0] + s4[2]; s4[0] = s4[1] = s4[2] = s4[3] = all; }
+            if constexpr (SPAN) {
+                // the lane's 16 elements are one head (gd >= 16; its sum then
+                // spans gd/16 lanes), two (gd = 8) or four (gd = 4)
+                if (gd == 8) {
+                    const double a01 = s4[0] + s4[1], a23 = s4[2] + s4[3];
+                    s4[0] = s4[1] = a01; s4[2] = s4[3] = a23;
+                } else if (gd >= 16) {
+                    double h = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+                    if (gd >= 32) h += dpp_d<DPP_XOR1>(h);
+                    if (gd >= 64) h += dpp_d<DPP_XOR2>(h);
+                    if (gd >= 128) h += dpp_d<DPP_HALF_MIRROR>(h);
+                    if (gd >= 256) h += dpp_d<DPP_MIRROR>(h);
+                    s4[0] = s4[1] = s4[2] = s4[3] = h;
+                }
+            } else {
+                // head h of width gd holds, on lane r, the elements of each q
+                // with (64q + 4r) / gd == h: its sum combines lanes (DPP)
+                // and, for gd >= 128, q's
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    double h = s4[qq];
+                    if (gd >= 8) h += dpp_d<DPP_XOR1>(h);
+                    if (gd >= 16) h += dpp_d<DPP_XOR2>(h);
+                    if (gd >= 32) h += dpp_d<DPP_HALF_MIRROR>(h);
+                    if (gd >= 64) h += dpp_d<DPP_MIRROR>(h);
+                    s4[qq] = h;
+                }
+                if (gd >= 128) { const double a01 = s4[0] + s4[1], a23 = s4[2] + s4[3]; s4[0] = s4[1] = a01; s4[2] = s4[3] = a23; }
+                if (gd >= 256) { const double all = s4[0] + s4[2]; s4[0] = s4[1] = s4[2] = s4[3] = all; }
+            }
+            float hs[4];
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) hs[qq] = 1.0f / sqrtf((float)(s4[qq] * inv_gd) + eps);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float mean = (float)(s4[i / 4] / (double)gd);
-                const float hs = 1.0f / sqrtf(mean + a.eps);
-                const float nrm = v[i] * hs;
-                const float wn = nrm * gw[i];
+                const float wn = (v[i] * hs[i / 4]) * gw[i];
                 t[i] = wn * (gpre ? y[i] : dev_silu(y[i]));
                 if ((i & 3) == 3) sched_fence();   // bounds the live fp64 temporaries
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float nrm = v[i] * gscale;
-                t[i] = nrm * y[i];
-            }
+            quantize(c, t);
         }
-        quant_chunk(vt, c, r, t, q, qd, qb);
     }
     __syncthreads();
+}
+
+__device__ __forceinline__ void prologue_compute(const sinter_gemv_args &a, int vt, double *red) {
+    const uint32_t K = uni(a.K), pro = uni(a.pro), log2d = uni(a.gn_log2d);
+    const float eps = __uint_as_float(uni(__float_as_uint(a.eps)));
+    switch (vt) {
+    case SINTER_Q8_K: prologue_quant<SINTER_Q8_K>(K, pro, log2d, eps, red); break;
+    case SINTER_Q8_0: prologue_quant<SINTER_Q8_0>(K, pro, log2d, eps, red); break;
+    case SINTER_BF16: prologue_quant<SINTER_BF16>(K, pro, log2d, eps, red); break;
+    default: prologue_quant<SINTER_F32>(K, pro, log2d, eps, red); break;
+    }
+}
+
+template <class Post>
+__device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
+                                              unsigned *err, Post &&post) {
+    prologue_stage(a, write_x, err, post);
+    prologue_compute(a, vt, red);
 }
 
 // ------------------------------------------------------------ item terms
@@ -627,7 +863,6 @@ __device__ __forceinline__ double item_term(const u32x4 *wv, uint32_t sh, const 
 typedef const __attribute__((address_space(4))) GemvPlan cplan_t;
 typedef const __attribute__((address_space(4))) uint32_t cu32_t;
 
-__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // q = v / d, r = v % d from m = floor((2^32-1) / d): the estimate is q or
 // q-1, one correction step makes it exact (v < 2^31)
