@@ -377,6 +377,39 @@ __device__ __forceinline__ bool grid_wait(const unsigned *flags, unsigned epoch,
     return timed_out == 0;
 }
 
+// A grid barrier fused with the op after it (interp.hip): the op's loads that
+// do not depend on the barrier are issued between arriving and waiting.
+struct GridCross {
+    unsigned *flags, *err;
+    unsigned *epoch;
+    uint64_t spin_limit;
+    bool pass_end;              // sample the error cell after the wait
+    long long *pass_slot;       // record (wall clock - t0) after the wait (block 0), or null
+    uint64_t t0;
+    uint64_t t_wait_end;        // out: wall clock after the wait (block 0 timing)
+};
+
+// Arrive, run pre() (the op's barrier-independent loads), wait.  False when
+// the kernel must stop: a barrier timeout, or an error seen at a pass end.
+template <class Pre>
+__device__ __forceinline__ bool cross_barrier(GridCross &gx, Pre &&pre) {
+    grid_arrive(gx.flags, *gx.epoch);
+    pre();
+    const bool crossed = grid_wait(gx.flags, *gx.epoch, gx.spin_limit, gx.err);
+    gx.t_wait_end = wall_clock64();
+    if (!crossed) { settle_vmem(); return false; }
+    if (gx.pass_end) {
+        __shared__ unsigned e;
+        if (threadIdx.x == 0) {
+            e = __hip_atomic_load(gx.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (gx.pass_slot) *gx.pass_slot = (long long)(gx.t_wait_end - gx.t0);
+        }
+        __syncthreads();
+        if (e) { settle_vmem(); return false; }
+    }
+    return true;
+}
+
 // ---------------------------------------------------------------- block formats
 
 struct blk_q8_0 { uint16_t d; int8_t qs[32]; };                                  // 34 B

@@ -24,8 +24,11 @@
 namespace sinter {
 
 // ts (thread 0, or null): wall clock stamps [1] after the first item's
-// norms and gates, [2] after its state update.
-__device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *err, uint64_t *ts) {
+// norms and gates, [2] after its state update.  gx (or null): the grid
+// barrier before the op, crossed here with the first item's state slice
+// loaded between arriving and waiting (the state is this workgroup's own
+// from the previous pass); false when the kernel must stop.
+__device__ __forceinline__ bool op_gdn_step(const sinter_instr &ins, unsigned *err, uint64_t *ts, GridCross *gx) {
     lds_char *lds = (lds_char *)g_big;
     const sinter_gdn_args &a = *reinterpret_cast<const sinter_gdn_args *>(ins.payload);
     const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
@@ -37,8 +40,9 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
                     (BLOCK_THREADS % cols) == 0 && tpc && tpc <= 64 && (D % tpc) == 0 && (D / tpc) % 4 == 0 &&
                     (D / tpc) <= 32 && HK && HV % HK == 0;
     if (!ok) {
+        if (gx && !cross_barrier(*gx, [] {})) return false;
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
-        return;
+        return true;
     }
     const uint32_t rpt = D / tpc;  // rows per thread
     LDS float *qs = reinterpret_cast<LDS float *>(lds);          // [D] normalised q
@@ -48,8 +52,24 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
 
     // the item loop with the rows per thread a compile-time constant, so the
     // state loads are unconditional and the wait counts exact
-    auto items = [&](auto rptc) {
+    auto items = [&](auto rptc) -> bool {
     constexpr uint32_t RPT = decltype(rptc)::value;
+    // this thread's state: column c0 + threadIdx.x / tpc of v-head h, rows
+    // [i0, i0 + RPT) (unconditional 16-byte loads: the wait counts stay exact)
+    auto state_row = [&](uint32_t item) {
+        const uint32_t h = item / slices, c0 = (item % slices) * cols;
+        return gp(a.state + ((size_t)h * D + c0 + threadIdx.x / tpc) * D + (threadIdx.x % tpc) * RPT);
+    };
+    float s[RPT];
+    auto load_state = [&](uint32_t item) {
+        const GLB float *srow = state_row(item);
+#pragma unroll
+        for (uint32_t r = 0; r < RPT; r += 4) {
+            const f32x4 t = *reinterpret_cast<const GLB f32x4 *>(srow + r);
+            s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
+        }
+    };
+    if (gx && !cross_barrier(*gx, [&] { if (rel < n_items) load_state(rel); })) return false;
     for (uint32_t item = rel; item < n_items; item += nblk) {
         const uint32_t h = item / slices, c0 = (item % slices) * cols;
         const uint32_t hk = h % HK;
@@ -61,20 +81,16 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
         const uint32_t i0 = (threadIdx.x % tpc) * RPT;
         // every load of the item first (one memory round trip): q, k, v and
         // the raw gates (written by the projection), then the state slice
-        // (unconditional: lanes past D re-read element t % D and drop it,
-        // so no divergent branch hides the loads' order from the wait counts)
+        // unless it crossed the barrier (unconditional: lanes past D re-read
+        // element t % D and drop it, so no divergent branch hides the loads'
+        // order from the wait counts)
         const uint32_t tq = threadIdx.x & (D - 1);
         const float qv = ld_coh(qsrc + tq), kv = ld_coh(ksrc + tq);
         const float vcol = ld_coh(vsrc + col);
         const float alpha = ld_coh(a.alpha + h), braw = ld_coh(a.beta + h);
         const float dtb = gp(a.dt_bias)[h], sa = gp(a.ssm_a)[h];
-        GLB float *srow = gp(a.state + ((size_t)h * D + col) * D + i0);
-        float s[RPT];
-#pragma unroll
-        for (uint32_t r = 0; r < RPT; r += 4) {
-            const f32x4 t = *reinterpret_cast<const GLB f32x4 *>(srow + r);
-            s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
-        }
+        GLB float *srow = state_row(item);
+        if (!gx || item != rel) load_state(item);
         // l2 norm of q and k (ggml: fp32 squares summed in double,
         // scale = 1/fmaxf(sqrtf(sum), eps)); both sums in one reduction
         const bool mine = threadIdx.x < D;
@@ -117,12 +133,13 @@ __device__ __forceinline__ void op_gdn_step(const sinter_instr &ins, unsigned *e
         if (ts && item == rel) ts[2] = wall_clock64();
         __syncthreads();  // qs/ks reused by the next item
     }
+    return true;
     };
     switch (rpt) {
-    case 4: items(std::integral_constant<uint32_t, 4>{}); break;
-    case 8: items(std::integral_constant<uint32_t, 8>{}); break;
-    case 16: items(std::integral_constant<uint32_t, 16>{}); break;
-    default: items(std::integral_constant<uint32_t, 32>{}); break;
+    case 4: return items(std::integral_constant<uint32_t, 4>{});
+    case 8: return items(std::integral_constant<uint32_t, 8>{});
+    case 16: return items(std::integral_constant<uint32_t, 16>{});
+    default: return items(std::integral_constant<uint32_t, 32>{});
     }
 }
 

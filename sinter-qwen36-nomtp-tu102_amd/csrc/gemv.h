@@ -1238,18 +1238,6 @@ __device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)
 
 // ------------------------------------------------------------ the op
 
-// The grid barrier the op may be fused with (interp.hip): crossed after the
-// first weight slots are issued.  arrive/wait are the interpreter's.
-struct GridCross {
-    unsigned *flags, *err;
-    unsigned *epoch;
-    uint64_t spin_limit;
-    bool pass_end;              // sample the error cell after the wait
-    long long *pass_slot;       // record (wall clock - t0) after the wait (block 0), or null
-    uint64_t t0;
-    uint64_t t_wait_end;        // out: wall clock after the wait (block 0 timing)
-};
-
 // Returns false when the kernel must stop (barrier timeout, or an error seen
 // at a pass end).
 // ts (thread 0, or null): wall clock stamps [1] after the barrier wait,
@@ -1268,20 +1256,8 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     u32x4 pf[PF_MAX];
     uint32_t sh[4] = {0, 0, 0, 0};
     if (gx) {
-        grid_arrive(gx->flags, *gx->epoch);   // publishes g_args too
-        issue_pre(pf, sh, run, (uint64_t)plan);
-        const bool crossed = grid_wait(gx->flags, *gx->epoch, gx->spin_limit, gx->err);
-        gx->t_wait_end = wall_clock64();
-        if (!crossed) { settle_vmem(); return false; }
-        if (gx->pass_end) {
-            __shared__ unsigned e;
-            if (threadIdx.x == 0) {
-                e = __hip_atomic_load(gx->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (gx->pass_slot) *gx->pass_slot = (long long)(gx->t_wait_end - gx->t0);
-            }
-            __syncthreads();
-            if (e) { settle_vmem(); return false; }
-        }
+        // (the arrival publishes g_args too)
+        if (!cross_barrier(*gx, [&] { issue_pre(pf, sh, run, (uint64_t)plan); })) return false;
     } else {
         issue_pre(pf, sh, run, (uint64_t)plan);
         __syncthreads();

@@ -61,8 +61,9 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             const bool pass_end = i == n;
             const uint32_t nx = pass_end ? 0u : i + 1;
             const bool more = nx < n && (pass + (pass_end ? 1u : 0u)) < ctl.n_passes;
-            const bool fused = more && prog[nx].kind == SINTER_OP_GEMV && blockIdx.x >= prog[nx].block_lo &&
-                               blockIdx.x < prog[nx].block_hi;
+            const bool in_nx = more && blockIdx.x >= prog[nx].block_lo && blockIdx.x < prog[nx].block_hi;
+            const bool fused = in_nx && prog[nx].kind == SINTER_OP_GEMV;
+            const bool fused_gdn = in_nx && prog[nx].kind == SINTER_OP_GDN_STEP;
             const uint64_t s = timed ? wall_clock64() : 0;
             GridCross gx;
             gx.flags = ctl.flags; gx.err = ctl.err; gx.epoch = &epoch;
@@ -76,6 +77,15 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 if (ts) ts[0] = s ? s : wall_clock64();
                 if (!gemv_op(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
                 if (ts) ts[3] = wall_clock64();
+            } else if (fused_gdn) {
+                // the GDN step loads its state slice across the barrier; the
+                // boundary's record keeps the arrival and the wait's end
+                uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
+                stamp(i, 0, wall_clock64());
+                if (!op_gdn_step(prog[nx], ctl.err, ts, &gx)) return;
+                stamp(i, 1, gx.t_wait_end);
+                if (ts) { ts[0] = gx.t_wait_end; ts[3] = wall_clock64(); }
             } else {
                 stamp(i, 0, wall_clock64());
                 grid_arrive(ctl.flags, epoch);
@@ -97,13 +107,15 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 const uint64_t e = wall_clock64();
                 ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(gx.t_wait_end - s);
                 if (fused) ctl.op_cycles[SINTER_OP_GEMV] += (long long)(e - gx.t_wait_end);
+                if (fused_gdn) ctl.op_cycles[SINTER_OP_GDN_STEP] += (long long)(e - gx.t_wait_end);
             }
+            const bool took_next = fused || fused_gdn;
             if (pass_end) {
                 pass += 1;
                 t0 = gx.t_wait_end;
-                i = fused ? 1u : 0u;
+                i = took_next ? 1u : 0u;
             } else {
-                i += fused ? 2u : 1u;
+                i += took_next ? 2u : 1u;
             }
             continue;
         }
@@ -124,7 +136,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             } else {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
-                if (kind == SINTER_OP_GDN_STEP) op_gdn_step(ins, ctl.err, ts);
+                if (kind == SINTER_OP_GDN_STEP) (void)op_gdn_step(ins, ctl.err, ts, nullptr);
                 else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode(ins, ctl.err, ts, ctl.spin_limit, pass);
             }
             if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
@@ -144,7 +156,7 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
     // the host sets block_lo = 0, block_hi = gridDim.x
     switch (ins->kind) {
     case SINTER_OP_GEMV: (void)gemv_op(*ins, plan, cuts, err, nullptr, nullptr); break;
-    case SINTER_OP_GDN_STEP: op_gdn_step(*ins, err, nullptr); break;
+    case SINTER_OP_GDN_STEP: (void)op_gdn_step(*ins, err, nullptr, nullptr); break;
     // (attention launches cooperatively: its chunks of one kv head wait for
     // each other, bounded by a 2 s spin limit at 100 MHz)
     case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err, nullptr, 200000000ull, ATT_NO_CACHE); break;
