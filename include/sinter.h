@@ -279,6 +279,28 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
  * flags are cleared by a small kernel at the start of each call): calls that
  * overlap on one GPU race.  Errors go to the cell sinter_op_error reads. */
 int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, void *stream);
+/* Grid-barrier litmus on the current device (mirrors tests/litmus_boundary.cu:1-18
+ * and docs/SYNC-FINDINGS.md:9-32 of the reference; a diagnostic, not a decode
+ * entry point).  `blocks` co-resident workgroups cross the interpreter's grid
+ * barrier `epochs` times with pseudo-random arrival order; each publishes a
+ * payload word before arriving and, after crossing, reads the next block's
+ * (another XCD's).  `mode` is one of the SINTER_LITMUS_* protocols, or'ed with
+ * the kind of read the reader makes of that line before arriving (none, plain
+ * cached, or coherent): it leaves the previous epoch's value wherever that read
+ * caches it.  counts[0] = payload reads older than the current epoch (stale),
+ * counts[1] = crossings that saw fewer than epoch*blocks arrivals counted
+ * (early release), counts[2] = the final arrival count (epochs*blocks).
+ * COHERENT is the protocol the ops use (both counts must be 0); the other
+ * protocols break only the payload's visibility. */
+enum {
+    SINTER_LITMUS_COHERENT = 0,       /* sc1 store before arriving, sc1 load after crossing */
+    SINTER_LITMUS_PLAIN_STORE = 1,    /* plain cached store */
+    SINTER_LITMUS_PLAIN_LOAD = 2,     /* plain cached load */
+    SINTER_LITMUS_LATE_PUBLISH = 3,   /* store after arriving */
+    SINTER_LITMUS_WARM_PLAIN = 0x10,  /* pre-read: plain cached load */
+    SINTER_LITMUS_WARM_COHERENT = 0x20 /* pre-read: sc1 load */
+};
+int sinter_litmus_barrier(uint32_t blocks, uint32_t epochs, int mode, uint64_t counts[3]);
 /* synchronise the device and read/clear the op error cells of the current device */
 int sinter_op_error(uint32_t *code, uint32_t *aux);
 /* argmax workspace for `blocks` workgroups (allocated on the current device) */

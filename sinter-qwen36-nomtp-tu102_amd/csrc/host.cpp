@@ -417,6 +417,11 @@ int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, vo
     return attn_noalloc(*a, blocks, (hipStream_t)stream);
 }
 
+int sinter_litmus_barrier(uint32_t blocks, uint32_t epochs, int mode, uint64_t counts[3]) {
+    if (!counts || mode < 0) return set_error(SINTER_ERR_ARG, "litmus: counts / mode");
+    return litmus_barrier(blocks, epochs, (uint32_t)mode, counts);
+}
+
 int sinter_op_error(uint32_t *code, uint32_t *aux) {
     unsigned *err = op_err_cell();
     if (!err) return set_error(SINTER_ERR_HIP, "no error cell");

@@ -39,6 +39,8 @@ unsigned *op_err_cell();  // per-device error cell of the standalone op launches
 int attn_noalloc(const sinter_attn_args &a, uint32_t blocks, hipStream_t s);
 // its error cell on the current device (null before its first call there)
 unsigned *noalloc_err_cell();
+// the grid-barrier litmus (sinter_litmus_barrier)
+int litmus_barrier(uint32_t blocks, uint32_t epochs, uint32_t mode, uint64_t counts[3]);
 int validate_gemv(const sinter_gemv_args &a, const char **why);
 // the plan and the nblk + 1 row cuts of a validated GEMV run by nblk workgroups
 // bw: per-block work weights (null: uniform)

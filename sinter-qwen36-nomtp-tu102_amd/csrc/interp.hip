@@ -188,6 +188,77 @@ extern "C" __global__ void __launch_bounds__(BLOCK_THREADS) sinter_op_noalloc_ke
     op_attn_decode(ins, err, nullptr, 200000000ull, ATT_NO_CACHE);
 }
 
+// ---------------------------------------------------------------- barrier litmus
+// The grid barrier (grid_arrive / grid_wait) and the device-coherent data
+// path under test (tests/litmus_boundary.cu in the reference).  Per epoch e,
+// thread 0 of block b: a pseudo-random delay (so blocks complete in varying
+// order), one device-scope atomic increment of the arrival count, then
+// payload[b] = e, and (optionally) a read of the next block's payload line
+// (that block runs on another XCD: workgroups are dealt to the XCDs in
+// turn), which leaves last epoch's value wherever that read caches it.  After the barrier it
+// reads block (b+1)%G's payload and the count: a payload older than e is a
+// stale observation (a newer one is allowed: that block may already have
+// crossed and published e + 1), a count below e*G an early release.
+// Modes (sinter.h): COHERENT (sc1 store, sc1 load: the protocol the ops
+// use), PLAIN_STORE (plain cached payload store), PLAIN_LOAD (plain cached
+// payload load), LATE_PUBLISH (payload stored after arriving); bits 4-5 the
+// pre-read (0 none, 1 plain, 2 sc1).  Every wait is the barrier's own bounded
+// spin, so the kernel always exits.
+constexpr uint32_t LITMUS_PLAIN_ST = SINTER_LITMUS_PLAIN_STORE, LITMUS_PLAIN_LD = SINTER_LITMUS_PLAIN_LOAD,
+                   LITMUS_LATE = SINTER_LITMUS_LATE_PUBLISH;
+constexpr uint32_t LITMUS_LINE = 64;   // payload stride in words (256 B)
+
+__device__ __forceinline__ uint32_t litmus_hash(uint32_t x) {
+    x ^= x >> 16; x *= 0x7feb352du; x ^= x >> 15; x *= 0x846ca68bu; x ^= x >> 16;
+    return x;
+}
+
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_litmus_kernel(unsigned *flags, unsigned *err, unsigned *counter, unsigned *payload, unsigned *obs,
+                     uint32_t epochs, uint32_t mode, uint64_t spin_limit, uint32_t seed) {
+    unsigned epoch = 0;
+    const uint32_t warm = (mode >> 4) & 3u;
+    mode &= 15u;
+    const uint32_t G = gridDim.x, b = blockIdx.x, rd = (b + 1) % G;
+    unsigned *mine = payload + (size_t)b * LITMUS_LINE;
+    const unsigned *theirs = payload + (size_t)rd * LITMUS_LINE;
+    unsigned sink = 0, stale = 0, early = 0;
+    for (uint32_t e = 1; e <= epochs; e++) {
+        const uint32_t h = litmus_hash(seed ^ (b * 0x9E3779B9u) ^ (e * 0x85EBCA6Bu));
+        if (threadIdx.x == 0) {
+            const uint64_t until = wall_clock64() + (h & 31u);   // 0..0.31 us
+            while (wall_clock64() < until) {}
+            __hip_atomic_fetch_add(gp(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (mode == LITMUS_PLAIN_ST) *gp(mine) = e;
+            else if (mode != LITMUS_LATE) st_coh(mine, e);
+            if (warm == 1) sink += *gp(theirs);   // warm the reader's caches with the old value
+            else if (warm == 2) sink += ld_coh(theirs);
+        }
+        grid_arrive(flags, epoch);
+        if (mode == LITMUS_LATE && threadIdx.x == 0) {
+            const uint64_t until = wall_clock64() + 100u + ((h >> 8) & 255u);   // 1..3.5 us
+            while (wall_clock64() < until) {}
+            st_coh(mine, e);
+        }
+        if (!grid_wait(flags, epoch, spin_limit, err)) { settle_vmem(); return; }
+        if (threadIdx.x == 0) {
+            asm volatile("" ::: "memory");
+            const unsigned v = mode == LITMUS_PLAIN_LD ? *gp(theirs) : ld_coh(theirs);
+            const unsigned c = ld_coh(counter);
+            // older than e is stale; newer is allowed (the writer may have
+            // crossed already and published e + 1 before this read)
+            stale += (int)(v - e) < 0 ? 1u : 0u;
+            early += c < e * G ? 1u : 0u;
+        }
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(gp(obs), stale, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(gp(obs + 1), early, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (sink == 0xFFFFFFFFu) st_coh(obs + 2, sink);   // keeps the warming reads
+    }
+    settle_vmem();
+}
+
 // Synthetic tensor fill: one thread per 256-element group (weights) or per
 // element (f32 / f16 tensors).
 extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type, uint64_t n_units,
@@ -291,6 +362,46 @@ int attn_noalloc(const sinter_attn_args &args, uint32_t blocks, hipStream_t s) {
                 "attn_noalloc: launch"))
         return SINTER_ERR_HIP;
     return SINTER_OK;
+}
+
+int litmus_barrier(uint32_t blocks, uint32_t epochs, uint32_t mode, uint64_t counts[3]) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (!hip_ok(hipGetDevice(&dev), "litmus: device") ||
+        !hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "litmus: CUs") ||
+        !hip_ok(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sinter_litmus_kernel, BLOCK_THREADS, 0),
+                "litmus: occupancy"))
+        return SINTER_ERR_HIP;
+    if (blocks < 2 || blocks > 1024 || blocks > (uint32_t)(per_cu * cus) || (mode & 15u) > LITMUS_LATE ||
+        ((mode >> 4) & 3u) > 2u || (mode & ~0x3Fu) || epochs == 0)
+        return set_error(SINTER_ERR_ARG, "litmus: blocks %u (2..%d co-resident, <= 1024), mode %u, epochs %u", blocks,
+                         per_cu * cus, mode, epochs);
+    // [err 64 B | counter 64 B | observations 64 B | flags 4 KiB | payload lines]
+    const size_t bytes = 192 + 4096 + (size_t)blocks * LITMUS_LINE * 4;
+    unsigned char *buf = nullptr;
+    if (!hip_ok(hipMalloc(&buf, bytes), "litmus: alloc")) return SINTER_ERR_HIP;
+    int rc = SINTER_OK;
+    unsigned *err = reinterpret_cast<unsigned *>(buf), *counter = err + 16, *obs = err + 32, *flags = err + 48;
+    unsigned *payload = flags + 1024;
+    uint64_t spin = 200000000ull;   // 2 s of wall clock ticks per barrier wait
+    uint32_t seed = 0x5151u ^ mode;
+    void *args[] = {&flags, &err, &counter, &payload, &obs, &epochs, &mode, &spin, &seed};
+    unsigned h[34];
+    if (!hip_ok(hipMemset(buf, 0, bytes), "litmus: clear") ||
+        !hip_ok(hipLaunchCooperativeKernel((const void *)sinter_litmus_kernel, dim3(blocks), dim3(BLOCK_THREADS), args,
+                                           0, nullptr),
+                "litmus: launch") ||
+        !hip_ok(hipDeviceSynchronize(), "litmus: run") ||
+        !hip_ok(hipMemcpy(h, buf, sizeof h, hipMemcpyDeviceToHost), "litmus: read"))
+        rc = SINTER_ERR_HIP;
+    else if (h[0])
+        rc = set_error(SINTER_ERR_DEVICE, "litmus: device error %u (aux %u)", h[0], h[1]);
+    else {
+        counts[0] = h[32];
+        counts[1] = h[33];
+        counts[2] = h[16];
+    }
+    (void)hipFree(buf);
+    return rc;
 }
 
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
