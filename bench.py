@@ -69,24 +69,181 @@ def measured_traffic(passes_per_launch, quant, ctx):
     return None
 
 
+CPU_LABEL = "ggml-semantics CPU restatement (oracle/oracle.c: ggml's quantisers and block dots, OpenMP over rows"
+
+
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def cpu_isa():
+    import oracle
+    return "AVX-512 row kernels" if oracle.lib().or_row_isa() == 512 else "baseline-ISA row kernels"
+
+
+def median_timed(fn, runs=5, warmup=1):
+    """Median wall time (s) of fn over `runs` calls after `warmup` calls."""
+    import numpy as np
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        s = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - s)
+    return float(np.median(ts)), ts
+
+
 def cpu_baseline(m, ctx, seconds):
-    """Time the CPU oracle decoding from the same synthetic context."""
+    """Time the CPU oracle decoding from the same synthetic context: one
+    warmup step, then at least 5 timed steps (more while `seconds` lasts);
+    the rate is 1 / the median step time."""
     import numpy as np
     import oracle
     t0 = time.perf_counter()
     mirror = oracle.ModelMirror(m)
     copy_s = time.perf_counter() - t0
-    n, t = 0, 0.0
-    tok = 1
-    while t < seconds or n == 0:
+    state = {"tok": 1, "pos": ctx}
+
+    def step():
+        state["tok"], _ = mirror.step(state["tok"], state["pos"])
+        state["pos"] += 1
+    step()   # warmup
+    ts, spent = [], 0.0
+    while len(ts) < 5 or spent < seconds:
         s = time.perf_counter()
-        tok, _ = mirror.step(tok, ctx + n)
-        t += time.perf_counter() - s
-        n += 1
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": n / t, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps of the same model from position {ctx} "
-                      f"(CPU oracle, OpenMP over rows, {threads} threads; weights copied to host in {copy_s:.1f} s)"}
+        step()
+        ts.append(time.perf_counter() - s)
+        spent += ts[-1]
+    med = float(np.median(ts))
+    threads = cpu_threads()
+    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{CPU_LABEL}, {cpu_isa()}, {threads} threads): greedy decode steps of the same model "
+                      f"from position {ctx}, 1 warmup + {len(ts)} timed, median {med * 1e3:.1f} ms/step "
+                      f"(weights copied to host in {copy_s:.1f} s)"}
+
+
+OP_CONFIGS = {
+    1: ("Q8_0 GEMV y = W x, W 17408x5120 (ffn_gate shape), x fp32[5120], y fp32[17408]", 4),
+    2: ("gated-DeltaNet layer mixer: RMSNorm, Q4_K qkv 8192 / z 4096 / alpha, beta 32 x 5120, causal conv 4, "
+        "l2 norms, gates, delta-rule step on 32 x 128x128 fp32 state, gated RMSNorm, Q4_K out 5120x4096, residual", 6),
+    3: ("attention layer mixer: RMSNorm, Q4_K q|gate 12288 / k 1024 and Q6_K v 1024 x 5120, q/k RMSNorm, "
+        "NEOX RoPE 64/256, f16 KV append, split-K GQA decode 24q/4kv over the cache, sigmoid gate, "
+        "Q4_K out 5120x6144, residual", 4),
+}
+GDN_SLOTS, ATTN_SLOTS = (0, 5, 6, 7, 8, 9, 10, 11, 12, 13), (0, 5, 6, 7, 8, 9, 10)
+
+
+def op_bench(args):
+    """one op group (a GEMV, a GDN mixer, an attention
+    mixer) per layer of a synthetic model, consecutive groups on different
+    weight copies (>= 4, past the 256 MB MALL), each group after a grid
+    barrier as in the decode (sinter_model_bench_program).  Reports the
+    median per-group time over timed launches."""
+    import ctypes as C
+    import numpy as np
+    import sinter
+    c = args.config
+    desc, n_inst = OP_CONFIGS[c]
+    ctx = args.ctx if c == 3 else 0
+    cfg = sinter.qwen36_27b_config(n_ctx=max(ctx, 64), quant="q4_k_m", n_layer=n_inst)
+    cfg.n_vocab = 512
+    cfg.attn_every = 1 if c == 3 else 0
+    if c == 1:
+        cfg.t_default = sinter.Q8_0
+    t0 = time.perf_counter()
+    m = sinter.Model(cfg, seed=args.seed)
+    m.synth_context(max(ctx - 1, 0), seed=args.seed + 1)
+    m.bench_program(c, seed=args.seed + 2)
+    print(f"# config {c}: model ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    pos = max(ctx - 1, 0)
+    ppl = max(1, args.passes_per_launch)
+    for _ in range(2):
+        m.time_passes(pos, ppl)
+    launches = max(5, args.steps // ppl)
+    ms = [m.time_passes(pos, ppl) for _ in range(launches)]
+    us = float(np.median(ms)) * 1e3 / (ppl * n_inst)
+    # algorithmic bytes of one group
+    E = cfg.n_embd
+    if c == 1:
+        _, wbytes, _ = m.tensor(0, 2)
+        nbytes = wbytes + E * 4 + cfg.n_ff * 4
+        parts = {"weights": wbytes, "x": E * 4, "y": cfg.n_ff * 4}
+    elif c == 2:
+        wbytes = sum(m.tensor(0, s)[1] for s in GDN_SLOTS)
+        D, C_ = cfg.gdn_d, (2 * cfg.gdn_hk + cfg.gdn_hv) * cfg.gdn_d
+        state = cfg.gdn_hv * D * D * 4 * 2
+        conv = C_ * (cfg.conv_k - 1) * 4 * 2
+        nbytes = wbytes + state + conv + 2 * E * 4
+        parts = {"weights": wbytes, "ssm_state_rw": state, "conv_state_rw": conv, "x_and_out": 2 * E * 4}
+    else:
+        wbytes = sum(m.tensor(0, s)[1] for s in ATTN_SLOTS)
+        kv_row = cfg.attn_nkv * cfg.head_dim * 2 * 2
+        nbytes = wbytes + kv_row * (pos + 1) + kv_row + 2 * E * 4
+        parts = {"weights": wbytes, "kv_read": kv_row * (pos + 1), "kv_append": kv_row, "x_and_out": 2 * E * 4}
+    achieved = nbytes / (us * 1e-6) / 1e9
+    line = {
+        "metric": f"config {c}: {desc}; time per op group (after its grid barrier) and achieved HBM GB/s vs peak",
+        "value": round(us, 3), "unit": "us", "n_gpus": 1, "steps": launches * ppl * n_inst, "warmup": 2 * ppl * n_inst,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if c == 1 else "int8/f32", "data": "synthetic (seeded random-init weights, x ~ N(0,1), "
+        "states N(0,0.1), f16 KV N(0,1))",
+        "config": {"workload": f"BASELINE config {c}", "instances_rotated": n_inst, "context": ctx if c == 3 else None,
+                   "passes_per_launch": ppl, "launches": launches, "bytes_per_op": nbytes, "bytes_breakdown": parts},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "sinter_interp",
+                     "roofline_us": round(nbytes / (PEAK_GBS * 1e9) * 1e6, 3)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = op_cpu_baseline(m, c, pos)
+    m.close()
+    print(json.dumps(line), flush=True)
+
+
+def op_cpu_baseline(m, c, pos):
+    """The same op group on the CPU oracle (layer 0's weights and state),
+    median of 5 after a warmup."""
+    import ctypes as C
+    import numpy as np
+    import oracle
+    L = oracle.lib()
+    rng = np.random.default_rng(7)
+    E = m.cfg.n_embd
+    x = rng.standard_normal(E).astype(np.float32)
+    threads = cpu_threads()
+    if c == 1:
+        d, nb, t = m.tensor(0, 2)
+        w = np.empty(nb, np.uint8)
+        m.d2h(w, d, nb)
+        med, _ = median_timed(lambda: oracle.gemv(t, w, m.cfg.n_ff, E, x))
+        what = "or_gemv (Q8_0 quantise of x + 17408 rows)"
+    else:
+        mirror = oracle.ModelMirror(m)
+        wl = C.c_void_p(C.addressof(mirror.weights))
+        st = C.c_void_p(C.addressof(mirror.state))
+        out = np.zeros(E, np.float32)
+        if c == 2:
+            med, _ = median_timed(lambda: L.or_gdn_mixer(C.byref(mirror.cfg), wl, st, oracle.P(x), oracle.P(out), None))
+            what = "or_gdn_mixer (projections, conv, step, gated norm, out)"
+        else:
+            med, _ = median_timed(lambda: L.or_attn_mixer(C.byref(mirror.cfg), wl, st, oracle.P(x), pos,
+                                                          oracle.P(out), None))
+            what = f"or_attn_mixer (projections, norms, rope, attention over {pos + 1} positions, gate, out)"
+    return {"value": round(med * 1e6, 1), "unit": "us", "cores": threads, "kind": "port",
+            "sample": f"{CPU_LABEL}, {cpu_isa()}, {threads} threads): {what}, layer 0, 1 warmup + 5 timed, median"}
+
+
+def single_pass_latency(m, tok, pos, n=8):
+    """Per-token latency of one pass per launch (sinter_model_decode: pos and
+    token set, one cooperative launch, the next token read back): median wall
+    time of n calls."""
+    import numpy as np
+    ts = []
+    for i in range(n):
+        s = time.perf_counter()
+        tok = m.decode(tok, pos + i)
+        ts.append(time.perf_counter() - s)
+    return float(np.median(ts)) * 1e3, tok
 
 
 def parity(m, cfg, args):
@@ -143,12 +300,17 @@ def parity(m, cfg, args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", type=int, default=4, choices=[1, 2, 3, 4, 5],
+                    help="BASELINE config: 4 (default) the e2e Q4_K_M decode at 4096 context; 5 the e2e bf16 "
+                         "decode at 131072 KV positions; 1-3 single-op timings (Q8_0 GEMV, GDN mixer, attention "
+                         "mixer at --ctx positions) over rotated weight copies")
+    ap.add_argument("--steps", type=int, default=None, help="timed tokens (default 256; config 5: 128)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed warmup tokens (default 16; config 5: 4)")
     ap.add_argument("--balance", type=int, nargs=2, default=(2, 4), metavar=("ROUNDS", "TRACES"),
                     help="static GEMV load balance before the warmup: ROUNDS updates, each measured on TRACES "
                          "traced greedy passes (sinter_model_balance; TRACES = 0: off)")
-    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--ctx", type=int, default=None,
+                    help="context positions (default 4096; config 5: 131072 less the decoded tokens)")
     ap.add_argument("--quant", default="q4_k_m", choices=["q4_k_m", "bf16"])
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -165,6 +327,17 @@ def main():
                     help="only copy MIB MiB device-to-device 3 times (torch's copy kernel) and exit: the "
                          "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
     args = ap.parse_args()
+    if args.config == 5:
+        args.quant = "bf16"
+    if args.steps is None:
+        args.steps = 128 if args.config == 5 else 256
+    if args.warmup is None:
+        args.warmup = 4 if args.config == 5 else 16
+    if args.ctx is None:
+        # config 5: the KV cache holds 131072 positions, the decoded tokens included
+        n_bal = (args.balance[0] + 1) * args.balance[1] if args.balance[1] else 0
+        args.ctx = 131072 - (n_bal + args.warmup + max(args.steps, args.parity_steps) + args.profile_ops + 24) \
+            if args.config == 5 else 4096
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the decode path on one GPU "
               "(the 27B model fits one MI355X; no multi-GPU path is built)", file=sys.stderr)
@@ -185,8 +358,11 @@ def main():
 
     import sinter
 
+    if args.config in (1, 2, 3):
+        op_bench(args)
+        return
     n_bal = (args.balance[0] + 1) * args.balance[1] if args.balance[1] else 0
-    n_ctx = args.ctx + n_bal + args.warmup + max(args.steps, args.parity_steps) + args.profile_ops + 8
+    n_ctx = args.ctx + n_bal + args.warmup + max(args.steps, args.parity_steps) + args.profile_ops + 24
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
     t0 = time.perf_counter()
     m = sinter.Model(cfg, seed=args.seed)
@@ -241,6 +417,8 @@ def main():
         # wall clock ticks: 100 MHz on MI355X
         rep = {n: round(c / 1e5 / args.profile_ops, 4) for n, c in zip(names, cyc)}
         print(f"# block-0 ms per token by kind: {rep}", file=sys.stderr, flush=True)
+    # one pass per launch (the reference's doorbell rhythm): per-token latency
+    sp_ms, _ = single_pass_latency(m, toks[-1], pos0 + args.steps + args.profile_ops)
     mean_attended = pos0 + (args.steps + 1) / 2.0
     bpt = bytes_per_token(cfg, m, mean_attended)
     tok_s = args.steps / wall
@@ -250,8 +428,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if args.quant == "q4_k_m" else "bf16",
         "data": f"synthetic (seeded random-init weights and {args.ctx}-token synthetic KV/recurrent state)",
-        "config": {"workload": f"e2e greedy decode, Qwen3.6-27B-shaped hybrid (48 GDN + 16 attention), "
-                               f"{args.quant} weights, {args.ctx}-token context",
+        "config": {"workload": f"BASELINE config {args.config}: e2e greedy decode, Qwen3.6-27B-shaped hybrid "
+                               f"(48 GDN + 16 attention), {args.quant} weights, {args.ctx}-token context",
                    "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
                    "gemv_balance": f"{args.balance[0]} updates, {n_bal} traced passes (untimed)",
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
@@ -260,6 +438,8 @@ def main():
                      "kernel": "sinter_interp", "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
+        "single_pass": {"ms_per_token": round(sp_ms, 4), "calls": 8,
+                        "path": "sinter_model_decode: one cooperative launch per token, token read back"},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(m, args.ctx, args.cpu_seconds)

@@ -373,6 +373,21 @@ sinter_host *sinter_model_host(sinter_model *m);
 int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces);
 /* the configuration the model was created with */
 int sinter_model_get_config(sinter_model *m, sinter_model_config *cfg);
+/* Single-op benchmark programs for BASELINE configs 1-3 (no counterpart in the
+ * reference, whose op timings come from its own harness): replaces the
+ * model's program (its decode program is gone afterwards) with, for every
+ * layer, one op group between grid barriers, so consecutive groups read
+ * different weight copies (rotate >= 4 copies past the 256 MB MALL):
+ *   GEMV  y = W x over the layer's ffn_gate matrix (n_ff x n_embd, plain
+ *         prologue, stored output; config 1 with t_default = Q8_0),
+ *   GDN   the gated-DeltaNet mixer of every GDN layer: norm + projections,
+ *         the recurrent step, gated norm + output projection (config 2),
+ *   ATTN  the attention mixer of every attention layer (config 3).
+ * x ~ N(0,1) from `seed`; states and caches as sinter_model_synth_context
+ * left them.  Time it with sinter_host_set_pos + sinter_host_run_passes on
+ * sinter_model_host(m) and sinter_host_last_launch_ms. */
+enum { SINTER_BENCH_GEMV = 1, SINTER_BENCH_GDN = 2, SINTER_BENCH_ATTN = 3 };
+int sinter_model_bench_program(sinter_model *m, int kind, uint64_t seed);
 
 /* ------------------------------------------------------------------ GGUF */
 /* A read-only GGUF v3 file (k0/gguf.h:30-246 File::open/parse/find/find_kv,

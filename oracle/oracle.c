@@ -287,101 +287,55 @@ static int vec_dot_type(int t) {
 }
 
 /* fast per-row kernels (same arithmetic as or_block_term, unrolled so the
- * full-model oracle runs in reasonable time) */
-static double row_q4k(const blk_q4_K *w, const blk_q8_K *x, int64_t nb) {
-    double acc = 0.0;
-    int8_t codes[256];
-    for (int64_t ib = 0; ib < nb; ib++) {
-        const blk_q4_K *b = w + ib;
-        for (int p = 0; p < 4; p++)
-            for (int l = 0; l < 32; l++) {
-                codes[64 * p + l] = (int8_t)(b->qs[32 * p + l] & 0xF);
-                codes[64 * p + 32 + l] = (int8_t)(b->qs[32 * p + l] >> 4);
-            }
-        int64_t isum = 0, imin = 0;
-        for (int s = 0; s < 8; s++) {
-            int sc, m;
-            q4k_scale_min(s, b->scales, &sc, &m);
-            int32_t dot = 0;
-            const int8_t *cq = codes + 32 * s, *xq = x[ib].qs + 32 * s;
-            for (int l = 0; l < 32; l++) dot += (int32_t)cq[l] * (int32_t)xq[l];
-            isum += (int64_t)sc * dot;
-            imin += (int64_t)m * ((int32_t)x[ib].bsums[2 * s] + (int32_t)x[ib].bsums[2 * s + 1]);
-        }
-        const double dx = (double)x[ib].d;
-        acc += ((double)or_f16_to_f32(b->d) * dx) * (double)isum -
-               ((double)or_f16_to_f32(b->dmin) * dx) * (double)imin;
+ * full-model oracle runs in reasonable time): an AVX-512 copy and a baseline
+ * copy of oracle_rows.inc, the one the CPU supports chosen at first use. */
+#pragma GCC push_options
+#pragma GCC target("avx512f,avx512bw,avx512vl,avx2,fma,bmi2")
+#define ROWFN(name) name##_avx512
+#include "oracle_rows.inc"
+#undef ROWFN
+#pragma GCC pop_options
+#define ROWFN(name) name##_base
+#include "oracle_rows.inc"
+#undef ROWFN
+
+static int use_avx512(void) {
+    static int v = -1;
+    if (v < 0) {
+        __builtin_cpu_init();
+        v = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+            __builtin_cpu_supports("avx512vl");
     }
-    return acc;
+    return v;
 }
 
-static double row_q6k(const blk_q6_K *w, const blk_q8_K *x, int64_t nb) {
-    double acc = 0.0;
-    int8_t codes[256];
-    for (int64_t ib = 0; ib < nb; ib++) {
-        const blk_q6_K *b = w + ib;
-        for (int n = 0; n < 2; n++) {
-            const uint8_t *ql = b->ql + 64 * n, *qh = b->qh + 32 * n;
-            int8_t *c = codes + 128 * n;
-            for (int l = 0; l < 32; l++) {
-                c[l] = (int8_t)(((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
-                c[l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
-                c[l + 64] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
-                c[l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
-            }
-        }
-        int64_t isum = 0;
-        for (int j = 0; j < 16; j++) {
-            int32_t dot = 0;
-            const int8_t *cq = codes + 16 * j, *xq = x[ib].qs + 16 * j;
-            for (int l = 0; l < 16; l++) dot += (int32_t)cq[l] * (int32_t)xq[l];
-            isum += (int64_t)b->scales[j] * dot;
-        }
-        acc += ((double)or_f16_to_f32(b->d) * (double)x[ib].d) * (double)isum;
-    }
-    return acc;
-}
-
-static double row_q8_0(const blk_q8_0 *w, const blk_q8_0 *x, int64_t nb) {
-    /* declared fold: groups of 8 blocks (256 elements) summed ascending
-     * inside the group, then the group terms ascending */
-    double acc = 0.0;
-    for (int64_t g = 0; g < nb / 8; g++) {
-        double part = 0.0;
-        for (int64_t ib = 8 * g; ib < 8 * g + 8; ib++) {
-            int32_t isum = 0;
-            for (int l = 0; l < 32; l++) isum += (int32_t)w[ib].qs[l] * (int32_t)x[ib].qs[l];
-            part += ((double)or_f16_to_f32(w[ib].d) * (double)or_f16_to_f32(x[ib].d)) * (double)isum;
-        }
-        acc += part;
-    }
-    return acc;
-}
-
-static double row_bf16(const uint16_t *w, const uint16_t *x, int64_t k) {
-    /* declared fold: 64-element items, exact products, fp64 */
-    double acc = 0.0;
-    for (int64_t g = 0; g < k / 64; g++) {
-        double part = 0.0;
-        for (int64_t i = 64 * g; i < 64 * g + 64; i++)
-            part += (double)or_bf16_to_f32(w[i]) * (double)or_bf16_to_f32(x[i]);
-        acc += part;
-    }
-    return acc;
-}
+int or_row_isa(void) { return use_avx512() ? 512 : 0; }
 
 void or_gemv_q(int t, const void *w, int64_t rows, int64_t k, const void *xq, float *y) {
     const size_t rb = or_row_bytes(t, k);
     const int64_t nb = k / (int64_t)or_type_block_elems(t);
+    const int v512 = use_avx512();
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++) {
         const void *row = (const char *)w + (size_t)r * rb;
         double acc = 0.0;
         switch (t) {
-        case OR_Q4_K: acc = row_q4k((const blk_q4_K *)row, (const blk_q8_K *)xq, nb); break;
-        case OR_Q6_K: acc = row_q6k((const blk_q6_K *)row, (const blk_q8_K *)xq, nb); break;
-        case OR_Q8_0: acc = row_q8_0((const blk_q8_0 *)row, (const blk_q8_0 *)xq, nb); break;
-        case OR_BF16: acc = row_bf16((const uint16_t *)row, (const uint16_t *)xq, k); break;
+        case OR_Q4_K:
+            acc = v512 ? row_q4k_avx512((const blk_q4_K *)row, (const blk_q8_K *)xq, nb)
+                       : row_q4k_base((const blk_q4_K *)row, (const blk_q8_K *)xq, nb);
+            break;
+        case OR_Q6_K:
+            acc = v512 ? row_q6k_avx512((const blk_q6_K *)row, (const blk_q8_K *)xq, nb)
+                       : row_q6k_base((const blk_q6_K *)row, (const blk_q8_K *)xq, nb);
+            break;
+        case OR_Q8_0:
+            acc = v512 ? row_q8_0_avx512((const blk_q8_0 *)row, (const blk_q8_0 *)xq, nb)
+                       : row_q8_0_base((const blk_q8_0 *)row, (const blk_q8_0 *)xq, nb);
+            break;
+        case OR_BF16:
+            acc = v512 ? row_bf16_avx512((const uint16_t *)row, (const uint16_t *)xq, k)
+                       : row_bf16_base((const uint16_t *)row, (const uint16_t *)xq, k);
+            break;
         case OR_F32: {
             const float *wf = (const float *)row, *xf = (const float *)xq;
             for (int64_t g = 0; g < k / 64; g++) {

@@ -57,6 +57,8 @@ double or_block_term(int type, const void *wblk, const void *xblk);
 /* y[r] = W[r,:] . x for r in [0, rows); x is quantised inside to the type's
  * vec_dot type.  Multi-threaded over rows (results are thread-count free). */
 void or_gemv(int type, const void *w, int64_t rows, int64_t k, const float *x, float *y);
+/* the ISA of the GEMV row kernels on this CPU: 512 (AVX-512) or 0 (baseline) */
+int or_row_isa(void);
 /* same, over an already quantised activation */
 void or_gemv_q(int type, const void *w, int64_t rows, int64_t k, const void *xq, float *y);
 

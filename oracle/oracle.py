@@ -60,6 +60,7 @@ def lib():
             "or_attn_decode": (None, [p, p, p, i, i, i, i, i, f, p]),
             "or_is_attn_layer": (i, [C.POINTER(Cfg), i]),
             "or_gdn_mixer": (None, [C.POINTER(Cfg), p, p, p, p, p]),
+            "or_row_isa": (i, []),
             "or_attn_mixer": (None, [C.POINTER(Cfg), p, p, p, i, p, p]),
             "or_ffn": (None, [C.POINTER(Cfg), p, p, p]),
             "or_decode_step": (i, [C.POINTER(Cfg), p, p, i, i, p, p]),

@@ -216,140 +216,159 @@ sinter_gemv_seg seg(const Tensor &w, float *y, int epi, const void *w2 = nullptr
     return s;
 }
 
-void build_program(sinter_model *m) {
+// Steps 1-3 of layer il: mixer input projections (the embedding lookup when
+// `embed`), the recurrent / attention core, the output projection with the
+// residual H = X + W_out . a.
+void push_mixer(sinter_model *m, int il, bool embed) {
     const sinter_model_config &c = m->cfg;
     const int E = c.n_embd, D = c.gdn_d, HD = c.head_dim;
     const sinter_pass_cell *pc = sinter_host_pass_cell(m->host);
-    m->prog.clear();
-    m->n_boundaries = 0;
     int log2d = 0;
     while ((1 << log2d) < D) log2d++;
+    const auto &w = m->W[il];
+    const bool at = is_attn(c, il);
+    const uint32_t dbg = (uint32_t)il * 8;
+    // 1. mixer input projections
+    sinter_gemv_args g1;
+    std::memset(&g1, 0, sizeof g1);
+    g1.K = (uint32_t)E;
+    g1.eps = c.eps;
+    g1.norm_w = (const float *)w[S_ATTN_NORM].d;
+    if (embed) {
+        g1.pro = SINTER_PRO_EMBED;
+        g1.aux = m->embd.d;
+        g1.aux_type = (uint8_t)m->embd.type;
+        g1.aux_rows = (uint32_t)m->embd.rows;
+        g1.token = &pc->token;
+        g1.x_out = m->X;
+    } else {
+        g1.pro = SINTER_PRO_RMSNORM;
+        g1.x = m->X;
+    }
+    if (at) {
+        g1.n_seg = 3;
+        g1.seg[0] = seg(w[S_WQ], m->qg, SINTER_EPI_STORE);
+        g1.seg[1] = seg(w[S_WK], m->kk, SINTER_EPI_STORE);
+        g1.seg[2] = seg(w[S_WV], m->vv, SINTER_EPI_STORE);
+    } else {
+        g1.n_seg = 4;
+        g1.seg[0] = seg(w[S_QKV], m->qkv, SINTER_EPI_CONV, w[S_CONV_W].d, (float *)m->S[il][0].d, c.conv_k);
+        g1.seg[1] = seg(w[S_Z], m->z, SINTER_EPI_SILU);   // the gate silu(z), once
+        g1.seg[2] = seg(w[S_ALPHA], m->al, SINTER_EPI_STORE);
+        g1.seg[3] = seg(w[S_BETA], m->be, SINTER_EPI_STORE);
+    }
+    push(m, SINTER_OP_GEMV, g1, dbg + 0);
+    boundary(m);
+    // 2. recurrent / attention core
+    if (at) {
+        sinter_attn_args a;
+        std::memset(&a, 0, sizeof a);
+        a.qg = m->qg;
+        a.k = m->kk;
+        a.v = m->vv;
+        a.q_norm = (const float *)w[S_Q_NORM].d;
+        a.k_norm = (const float *)w[S_K_NORM].d;
+        a.kc = (uint16_t *)m->S[il][0].d;
+        a.vc = (uint16_t *)m->S[il][1].d;
+        a.part = m->part;
+        a.count = m->count;
+        a.out = m->att;
+        a.pass_cell = &pc->token;
+        a.nq = (uint32_t)c.attn_nq;
+        a.nkv = (uint32_t)c.attn_nkv;
+        a.hd = (uint32_t)HD;
+        a.rope_dims = (uint32_t)c.rope_dims;
+        a.n_ctx = (uint32_t)c.n_ctx;
+        a.n_chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
+        a.theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
+        a.eps = c.eps;
+        a.scale = 1.0f / std::sqrt((float)HD);
+        push(m, SINTER_OP_ATTN_DECODE, a, dbg + 1);
+    } else {
+        sinter_gdn_args a;
+        std::memset(&a, 0, sizeof a);
+        a.qkv = m->qkv;
+        a.alpha = m->al;
+        a.beta = m->be;
+        a.dt_bias = (const float *)w[S_DT_BIAS].d;
+        a.ssm_a = (const float *)w[S_SSM_A].d;
+        a.state = (float *)m->S[il][1].d;
+        a.o = m->o;
+        a.hk = (uint32_t)c.gdn_hk;
+        a.hv = (uint32_t)c.gdn_hv;
+        a.d = (uint32_t)D;
+        // 32 columns per item: 128 items at 32 heads x 128, so half the
+        // grid goes straight on to the next GEMV's first weight loads
+        // (measured faster than 256 items of 16 columns)
+        a.cols = D >= 128 ? 32u : 16u;
+        a.eps = c.eps;
+        a.scale = 1.0f / std::sqrt((float)D);
+        push(m, SINTER_OP_GDN_STEP, a, dbg + 1);
+    }
+    boundary(m);
+    // 3. mixer output projection + residual: H = X + W_out . a
+    sinter_gemv_args g3;
+    std::memset(&g3, 0, sizeof g3);
+    g3.eps = c.eps;
+    g3.n_seg = 1;
+    if (at) {
+        g3.K = (uint32_t)(c.attn_nq * HD);
+        g3.pro = SINTER_PRO_PLAIN;
+        g3.x = m->att;
+        g3.seg[0] = seg(w[S_WO], m->H, SINTER_EPI_RESID, nullptr, m->X);
+    } else {
+        g3.K = (uint32_t)(c.gdn_hv * D);
+        g3.pro = SINTER_PRO_GATED_G;
+        g3.x = m->o;
+        g3.norm_w = (const float *)w[S_SSM_NORM].d;
+        g3.aux = m->z;
+        g3.gn_log2d = (uint8_t)log2d;
+        g3.seg[0] = seg(w[S_SSM_OUT], m->H, SINTER_EPI_RESID, nullptr, m->X);
+    }
+    push(m, SINTER_OP_GEMV, g3, dbg + 2);
+    boundary(m);
+}
+
+// Steps 4-5 of layer il: FFN gate/up with SwiGLU, down with the residual
+// X = H + W_down . f.
+void push_ffn(sinter_model *m, int il) {
+    const sinter_model_config &c = m->cfg;
+    const int E = c.n_embd;
+    const auto &w = m->W[il];
+    const uint32_t dbg = (uint32_t)il * 8;
+    // 4. FFN gate/up with SwiGLU
+    sinter_gemv_args g4;
+    std::memset(&g4, 0, sizeof g4);
+    g4.K = (uint32_t)E;
+    g4.eps = c.eps;
+    g4.pro = SINTER_PRO_RMSNORM;
+    g4.x = m->H;
+    g4.norm_w = (const float *)w[S_POST_NORM].d;
+    g4.n_seg = 1;
+    g4.seg[0] = seg(w[S_FFN_GATE], m->ffn, SINTER_EPI_SWIGLU, w[S_FFN_UP].d);
+    push(m, SINTER_OP_GEMV, g4, dbg + 3);
+    boundary(m);
+    // 5. FFN down + residual: X = H + W_down . f
+    sinter_gemv_args g5;
+    std::memset(&g5, 0, sizeof g5);
+    g5.K = (uint32_t)c.n_ff;
+    g5.eps = c.eps;
+    g5.pro = SINTER_PRO_PLAIN;
+    g5.x = m->ffn;
+    g5.n_seg = 1;
+    g5.seg[0] = seg(w[S_FFN_DOWN], m->X, SINTER_EPI_RESID, nullptr, m->H);
+    push(m, SINTER_OP_GEMV, g5, dbg + 4);
+    boundary(m);
+}
+
+void build_program(sinter_model *m) {
+    const sinter_model_config &c = m->cfg;
+    const int E = c.n_embd;
+    m->prog.clear();
+    m->n_boundaries = 0;
     for (int il = 0; il < c.n_layer; il++) {
-        const auto &w = m->W[il];
-        const bool at = is_attn(c, il);
-        const uint32_t dbg = (uint32_t)il * 8;
-        // 1. mixer input projections
-        sinter_gemv_args g1;
-        std::memset(&g1, 0, sizeof g1);
-        g1.K = (uint32_t)E;
-        g1.eps = c.eps;
-        g1.norm_w = (const float *)w[S_ATTN_NORM].d;
-        if (il == 0) {
-            g1.pro = SINTER_PRO_EMBED;
-            g1.aux = m->embd.d;
-            g1.aux_type = (uint8_t)m->embd.type;
-            g1.aux_rows = (uint32_t)m->embd.rows;
-            g1.token = &pc->token;
-            g1.x_out = m->X;
-        } else {
-            g1.pro = SINTER_PRO_RMSNORM;
-            g1.x = m->X;
-        }
-        if (at) {
-            g1.n_seg = 3;
-            g1.seg[0] = seg(w[S_WQ], m->qg, SINTER_EPI_STORE);
-            g1.seg[1] = seg(w[S_WK], m->kk, SINTER_EPI_STORE);
-            g1.seg[2] = seg(w[S_WV], m->vv, SINTER_EPI_STORE);
-        } else {
-            g1.n_seg = 4;
-            g1.seg[0] = seg(w[S_QKV], m->qkv, SINTER_EPI_CONV, w[S_CONV_W].d, (float *)m->S[il][0].d, c.conv_k);
-            g1.seg[1] = seg(w[S_Z], m->z, SINTER_EPI_SILU);   // the gate silu(z), once
-            g1.seg[2] = seg(w[S_ALPHA], m->al, SINTER_EPI_STORE);
-            g1.seg[3] = seg(w[S_BETA], m->be, SINTER_EPI_STORE);
-        }
-        push(m, SINTER_OP_GEMV, g1, dbg + 0);
-        boundary(m);
-        // 2. recurrent / attention core
-        if (at) {
-            sinter_attn_args a;
-            std::memset(&a, 0, sizeof a);
-            a.qg = m->qg;
-            a.k = m->kk;
-            a.v = m->vv;
-            a.q_norm = (const float *)w[S_Q_NORM].d;
-            a.k_norm = (const float *)w[S_K_NORM].d;
-            a.kc = (uint16_t *)m->S[il][0].d;
-            a.vc = (uint16_t *)m->S[il][1].d;
-            a.part = m->part;
-            a.count = m->count;
-            a.out = m->att;
-            a.pass_cell = &pc->token;
-            a.nq = (uint32_t)c.attn_nq;
-            a.nkv = (uint32_t)c.attn_nkv;
-            a.hd = (uint32_t)HD;
-            a.rope_dims = (uint32_t)c.rope_dims;
-            a.n_ctx = (uint32_t)c.n_ctx;
-            a.n_chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
-            a.theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
-            a.eps = c.eps;
-            a.scale = 1.0f / std::sqrt((float)HD);
-            push(m, SINTER_OP_ATTN_DECODE, a, dbg + 1);
-        } else {
-            sinter_gdn_args a;
-            std::memset(&a, 0, sizeof a);
-            a.qkv = m->qkv;
-            a.alpha = m->al;
-            a.beta = m->be;
-            a.dt_bias = (const float *)w[S_DT_BIAS].d;
-            a.ssm_a = (const float *)w[S_SSM_A].d;
-            a.state = (float *)m->S[il][1].d;
-            a.o = m->o;
-            a.hk = (uint32_t)c.gdn_hk;
-            a.hv = (uint32_t)c.gdn_hv;
-            a.d = (uint32_t)D;
-            // 32 columns per item: 128 items at 32 heads x 128, so half the
-            // grid goes straight on to the next GEMV's first weight loads
-            // (measured faster than 256 items of 16 columns)
-            a.cols = D >= 128 ? 32u : 16u;
-            a.eps = c.eps;
-            a.scale = 1.0f / std::sqrt((float)D);
-            push(m, SINTER_OP_GDN_STEP, a, dbg + 1);
-        }
-        boundary(m);
-        // 3. mixer output projection + residual: H = X + W_out . a
-        sinter_gemv_args g3;
-        std::memset(&g3, 0, sizeof g3);
-        g3.eps = c.eps;
-        g3.n_seg = 1;
-        if (at) {
-            g3.K = (uint32_t)(c.attn_nq * HD);
-            g3.pro = SINTER_PRO_PLAIN;
-            g3.x = m->att;
-            g3.seg[0] = seg(w[S_WO], m->H, SINTER_EPI_RESID, nullptr, m->X);
-        } else {
-            g3.K = (uint32_t)(c.gdn_hv * D);
-            g3.pro = SINTER_PRO_GATED_G;
-            g3.x = m->o;
-            g3.norm_w = (const float *)w[S_SSM_NORM].d;
-            g3.aux = m->z;
-            g3.gn_log2d = (uint8_t)log2d;
-            g3.seg[0] = seg(w[S_SSM_OUT], m->H, SINTER_EPI_RESID, nullptr, m->X);
-        }
-        push(m, SINTER_OP_GEMV, g3, dbg + 2);
-        boundary(m);
-        // 4. FFN gate/up with SwiGLU
-        sinter_gemv_args g4;
-        std::memset(&g4, 0, sizeof g4);
-        g4.K = (uint32_t)E;
-        g4.eps = c.eps;
-        g4.pro = SINTER_PRO_RMSNORM;
-        g4.x = m->H;
-        g4.norm_w = (const float *)w[S_POST_NORM].d;
-        g4.n_seg = 1;
-        g4.seg[0] = seg(w[S_FFN_GATE], m->ffn, SINTER_EPI_SWIGLU, w[S_FFN_UP].d);
-        push(m, SINTER_OP_GEMV, g4, dbg + 3);
-        boundary(m);
-        // 5. FFN down + residual: X = H + W_down . f
-        sinter_gemv_args g5;
-        std::memset(&g5, 0, sizeof g5);
-        g5.K = (uint32_t)c.n_ff;
-        g5.eps = c.eps;
-        g5.pro = SINTER_PRO_PLAIN;
-        g5.x = m->ffn;
-        g5.n_seg = 1;
-        g5.seg[0] = seg(w[S_FFN_DOWN], m->X, SINTER_EPI_RESID, nullptr, m->H);
-        push(m, SINTER_OP_GEMV, g5, dbg + 4);
-        boundary(m);
+        push_mixer(m, il, il == 0);
+        push_ffn(m, il);
     }
     // head: final norm, logits, greedy argmax
     sinter_gemv_args gh;
@@ -608,6 +627,48 @@ int sinter_model_synth_context(sinter_model *m, int32_t n_past, uint64_t seed) {
         if (!hip_ok(e, "context synthesis")) return SINTER_ERR_HIP;
     }
     return hip_ok(hipStreamSynchronize(m->stream), "context synthesis") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+int sinter_model_bench_program(sinter_model *m, int kind, uint64_t seed) {
+    if (!m) return set_error(SINTER_ERR_ARG, "bench_program: null model");
+    const sinter_model_config &c = m->cfg;
+    if (kind < SINTER_BENCH_GEMV || kind > SINTER_BENCH_ATTN) return set_error(SINTER_ERR_ARG, "bench_program: kind");
+    int n = 0;
+    for (int il = 0; il < c.n_layer; il++)
+        n += kind == SINTER_BENCH_GEMV || (kind == SINTER_BENCH_ATTN) == is_attn(c, il);
+    if (n == 0) return set_error(SINTER_ERR_ARG, "bench_program: the model has no layer of that kind");
+    int rc = sinter_host_shutdown(m->host, 60000.0);
+    if (rc) return rc;
+    // x ~ N(0,1): the plain GEMV's input, the mixers' norm input
+    if (!hip_ok(launch_synth(m->X, SINTER_SYN_NORMAL, 0, (uint64_t)c.n_embd, sinter_seed(seed, "bench_x", 0), 0.f,
+                             1.f, m->stream),
+                "bench input"))
+        return SINTER_ERR_HIP;
+    m->prog.clear();
+    m->n_boundaries = 0;
+    for (int il = 0; il < c.n_layer; il++) {
+        if (kind == SINTER_BENCH_GEMV) {
+            // y = W x: the layer's ffn_gate matrix, plain input, stored output
+            sinter_gemv_args g;
+            std::memset(&g, 0, sizeof g);
+            g.K = (uint32_t)c.n_embd;
+            g.eps = c.eps;
+            g.pro = SINTER_PRO_PLAIN;
+            g.x = m->X;
+            g.n_seg = 1;
+            g.seg[0] = seg(m->W[il][S_FFN_GATE], m->ffn, SINTER_EPI_STORE);
+            push(m, SINTER_OP_GEMV, g, (uint32_t)il * 8);
+            boundary(m);
+        } else if ((kind == SINTER_BENCH_ATTN) == is_attn(c, il)) {
+            push_mixer(m, il, false);
+        }
+    }
+    // the pass-end barrier closes the last op
+    m->prog.pop_back();
+    m->n_boundaries--;
+    if (!hip_ok(hipStreamSynchronize(m->stream), "bench input")) return SINTER_ERR_HIP;
+    if ((rc = sinter_host_upload(m->host, m->prog.data(), (uint32_t)m->prog.size(), m->n_boundaries + 1))) return rc;
+    return sinter_host_launch(m->host);
 }
 
 int sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logits_host, int32_t *next_token) {

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libsinter.so")
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 8, 12, 14, 15, 30
 # ops
 OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range(6)
+BENCH_GEMV, BENCH_GDN, BENCH_ATTN = 1, 2, 3
 PRO_PLAIN, PRO_RMSNORM, PRO_GATED, PRO_EMBED, PRO_GATED_G = range(5)
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV, EPI_SILU = range(6)
 SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16 = range(5)
@@ -168,6 +169,7 @@ def lib():
         "sinter_model_copy": (I, [vp, vp, vp, C.c_size_t, I]),
         "sinter_model_info": (I, [vp, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
         "sinter_model_host": (vp, [vp]),
+        "sinter_model_bench_program": (I, [vp, I, C.c_uint64]),
         "sinter_model_balance": (I, [vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32), U32, U32]),
         "sinter_model_get_config": (I, [vp, C.POINTER(ModelConfig)]),
         "sinter_gguf_open": (I, [C.c_char_p, C.POINTER(vp)]),
@@ -344,6 +346,22 @@ class Model:
 
     def host(self):
         return lib().sinter_model_host(self.h)
+
+    def bench_program(self, kind, seed=1):
+        """Replace the decode program with a single-op benchmark program
+        (BENCH_GEMV / BENCH_GDN / BENCH_ATTN; sinter_model_bench_program)."""
+        check(lib().sinter_model_bench_program(self.h, kind, seed), "bench_program")
+
+    def time_passes(self, pos, n):
+        """Run n passes of the uploaded program in one launch at position
+        pos; returns the interpreter kernel's time in ms (HIP events)."""
+        h, L = self.host(), lib()
+        check(L.sinter_host_set_pos(h, pos), "set_pos")
+        out = (C.c_int32 * n)()
+        rs = L.sinter_host_run_passes(h, 0, n, out, 600000.0)
+        if rs != RUN_OK:
+            raise SinterError(f"run_passes: status {rs}: {L.sinter_last_error().decode()}")
+        return float(L.sinter_host_last_launch_ms(h))
 
     def balance(self, token, pos, rounds=2, traces=4):
         """Static GEMV load balance (sinter_model_balance): decodes
