@@ -6,7 +6,9 @@ A step is one decode pass (one token).  Weights are synthetic random-init
 (generated on the device); the 4096-token context is a seeded synthetic KV
 cache / recurrent state.  W warmup tokens (one launch), then K tokens timed
 as launches of --passes-per-launch greedy passes of the cooperative
-interpreter, bracketed by torch.cuda.synchronize().  Prints one JSON line.
+interpreter (each call returns once its launch has finished).  Prints one
+JSON line.  --config selects the other BASELINE configs (1-3: single op
+groups; 5: bf16 at 131072 positions).
 
 The roofline object prices the algorithmic bytes per token (weights read
 once, KV rows read once, recurrent state read+written, logits written)
@@ -324,7 +326,7 @@ def main():
                          "and on the CPU oracle (same weights and state); token ids must be identical, logits "
                          "within rel L2 1e-2; prints one JSON line and exits")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only copy MIB MiB device-to-device 3 times (torch's copy kernel) and exit: the "
+                    help="only copy MIB MiB device-to-device 3 times (the HIP runtime's copy kernel) and exit: the "
                          "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
     args = ap.parse_args()
     if args.config == 5:
@@ -343,20 +345,17 @@ def main():
               "(the 27B model fits one MI355X; no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
 
-    import torch
+    # Only libsinter's HIP runtime is loaded (no torch here): torch bundles its
+    # own HIP and HSA runtimes, and two of each in one process do not tear
+    # down cleanly at exit under rocprofv3.  Every model call below returns
+    # after its device work has finished.
+    import sinter
 
-    torch.cuda.set_device(0)
     if args.copy_calibration:
         n = args.copy_calibration << 20
-        src = torch.ones(n, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        sinter.check(sinter.lib().sinter_copy_calibration(0, n, 3), "copy calibration")
         print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
         return
-
-    import sinter
 
     if args.config in (1, 2, 3):
         op_bench(args)
@@ -389,7 +388,6 @@ def main():
     # takes the remainder); every launch's kernel time comes from HIP events
     # recorded on the interpreter's own stream
     toks, launch_ms = [], []
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     done = 0
     while done < args.steps:
@@ -399,7 +397,6 @@ def main():
         toks += out
         tok = out[-1]
         done += n
-    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kernel_ms = sum(launch_ms)
     print(f"# timed {args.steps} tokens in {len(launch_ms)} launches of <= {ppl} passes: wall {wall * 1e3:.2f} ms, "

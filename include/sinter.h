@@ -279,6 +279,11 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
  * flags are cleared by a small kernel at the start of each call): calls that
  * overlap on one GPU race.  Errors go to the cell sinter_op_error reads. */
 int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, void *stream);
+/* Counter calibration (a diagnostic, no counterpart in the reference): on
+ * `device`, copies `bytes` device-to-device `reps` times with the runtime's
+ * copy kernel, so that FETCH_SIZE / WRITE_SIZE of a copy of known size can
+ * scale the same counters read on the interpreter. */
+int sinter_copy_calibration(int device, size_t bytes, int reps);
 /* Grid-barrier litmus on the current device (mirrors tests/litmus_boundary.cu:1-18
  * and docs/SYNC-FINDINGS.md:9-32 of the reference; a diagnostic, not a decode
  * entry point).  `blocks` co-resident workgroups cross the interpreter's grid

@@ -417,6 +417,22 @@ int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, vo
     return attn_noalloc(*a, blocks, (hipStream_t)stream);
 }
 
+int sinter_copy_calibration(int device, size_t bytes, int reps) {
+    if (bytes == 0 || reps < 1) return set_error(SINTER_ERR_ARG, "copy_calibration: bytes / reps");
+    if (!hip_ok(hipSetDevice(device), "copy_calibration: device")) return SINTER_ERR_HIP;
+    void *a = nullptr, *b = nullptr;
+    int rc = SINTER_OK;
+    if (!hip_ok(hipMalloc(&a, bytes), "copy_calibration: alloc") || !hip_ok(hipMalloc(&b, bytes), "copy_calibration: alloc") ||
+        !hip_ok(hipMemset(a, 1, bytes), "copy_calibration: fill"))
+        rc = SINTER_ERR_HIP;
+    for (int i = 0; rc == SINTER_OK && i < reps; i++)
+        if (!hip_ok(hipMemcpy(b, a, bytes, hipMemcpyDeviceToDevice), "copy_calibration: copy")) rc = SINTER_ERR_HIP;
+    if (rc == SINTER_OK && !hip_ok(hipDeviceSynchronize(), "copy_calibration: sync")) rc = SINTER_ERR_HIP;
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    return rc;
+}
+
 int sinter_litmus_barrier(uint32_t blocks, uint32_t epochs, int mode, uint64_t counts[3]) {
     if (!counts || mode < 0) return set_error(SINTER_ERR_ARG, "litmus: counts / mode");
     return litmus_barrier(blocks, epochs, (uint32_t)mode, counts);

@@ -134,6 +134,7 @@ def lib():
         "sinter_op_attn_decode": (I, [C.POINTER(AttnArgs), U32, vp]),
         "sinter_op_attn_decode_noalloc": (I, [C.POINTER(AttnArgs), U32, vp]),
         "sinter_litmus_barrier": (I, [U32, U32, I, C.POINTER(C.c_uint64)]),
+        "sinter_copy_calibration": (I, [I, C.c_size_t, I]),
         "sinter_op_error": (I, [C.POINTER(U32), C.POINTER(U32)]),
         "sinter_argmax_ws_create": (I, [U32, vp, vp, U32, C.POINTER(vp)]),
         "sinter_argmax_ws_destroy": (None, [vp]),
