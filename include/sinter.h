@@ -378,6 +378,14 @@ sinter_host *sinter_model_host(sinter_model *m);
 int sinter_model_balance(sinter_model *m, int32_t *token, int32_t *pos, uint32_t rounds, uint32_t traces);
 /* the configuration the model was created with */
 int sinter_model_get_config(sinter_model *m, sinter_model_config *cfg);
+/* The symbolic-program packer's view of a model (k0/harness.cpp:589-628 resolves
+ * the reference's buf:/cell: names the same way): the device buffer behind an
+ * activation / workspace name -- X, H (residual stream), qkv, z, alpha, beta,
+ * o (GDN), qg, k, v, att (attention), ffn, logits, attn_part, attn_count,
+ * argmax_ws -- and a copy of the model's uploaded program (n_instr always
+ * set; out may be null). */
+int sinter_model_buffer(sinter_model *m, const char *name, void **dev_ptr, size_t *bytes);
+int sinter_model_program(sinter_model *m, sinter_instr *out, uint32_t cap, uint32_t *n_instr);
 /* Single-op benchmark programs for BASELINE configs 1-3 (no counterpart in the
  * reference, whose op timings come from its own harness): replaces the
  * model's program (its decode program is gone afterwards) with, for every

@@ -744,6 +744,39 @@ int sinter_model_info(sinter_model *m, uint64_t *weight_bytes, uint32_t *n_instr
 
 sinter_host *sinter_model_host(sinter_model *m) { return m ? m->host : nullptr; }
 
+int sinter_model_buffer(sinter_model *m, const char *name, void **dev_ptr, size_t *bytes) {
+    if (!m || !name) return set_error(SINTER_ERR_ARG, "buffer: args");
+    const sinter_model_config &c = m->cfg;
+    const size_t E = (size_t)c.n_embd, VD = (size_t)c.gdn_hv * c.gdn_d, NQHD = (size_t)c.attn_nq * c.head_dim;
+    const size_t C = (size_t)(2 * c.gdn_hk + c.gdn_hv) * c.gdn_d, RW = (size_t)c.attn_nkv * c.head_dim;
+    const uint32_t chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
+    struct B { const char *n; void *p; size_t b; } tab[] = {
+        {"X", m->X, E * 4}, {"H", m->H, E * 4}, {"qkv", m->qkv, C * 4}, {"z", m->z, VD * 4},
+        {"alpha", m->al, (size_t)c.gdn_hv * 4}, {"beta", m->be, (size_t)c.gdn_hv * 4}, {"o", m->o, VD * 4},
+        {"ffn", m->ffn, (size_t)c.n_ff * 4}, {"qg", m->qg, NQHD * 2 * 4}, {"k", m->kk, RW * 4}, {"v", m->vv, RW * 4},
+        {"att", m->att, NQHD * 4}, {"logits", m->logits, (size_t)c.n_vocab * 4},
+        {"attn_part", m->part, sinter_attn_part_len(c.attn_nq, c.attn_nkv, c.head_dim, chunks) * 8},
+        {"attn_count", m->count, (size_t)sinter_attn_count_len(c.attn_nkv, chunks) * 4},
+        {"argmax_ws", m->ws, sizeof(sinter_argmax_ws)}};
+    for (const B &b : tab)
+        if (std::strcmp(b.n, name) == 0) {
+            if (dev_ptr) *dev_ptr = b.p;
+            if (bytes) *bytes = b.b;
+            return SINTER_OK;
+        }
+    return set_error(SINTER_ERR_ARG, "buffer: no buffer named %s", name);
+}
+
+int sinter_model_program(sinter_model *m, sinter_instr *out, uint32_t cap, uint32_t *n_instr) {
+    if (!m) return set_error(SINTER_ERR_ARG, "program: null model");
+    if (n_instr) *n_instr = (uint32_t)m->prog.size();
+    if (out) {
+        if (cap < m->prog.size()) return set_error(SINTER_ERR_ARG, "program: %u slots for %zu instructions", cap, m->prog.size());
+        std::memcpy(out, m->prog.data(), m->prog.size() * sizeof(sinter_instr));
+    }
+    return SINTER_OK;
+}
+
 // Static load balance of the GEMVs: every workgroup of a GEMV streams an equal
 // share of its bytes, but some workgroups are released from the barrier, or
 // stream, systematically later than others (the spread follows the

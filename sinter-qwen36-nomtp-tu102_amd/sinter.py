@@ -171,6 +171,8 @@ def lib():
         "sinter_model_info": (I, [vp, C.POINTER(U64), C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
         "sinter_model_host": (vp, [vp]),
         "sinter_model_bench_program": (I, [vp, I, C.c_uint64]),
+        "sinter_model_buffer": (I, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(C.c_size_t)]),
+        "sinter_model_program": (I, [vp, vp, U32, C.POINTER(U32)]),
         "sinter_model_balance": (I, [vp, C.POINTER(C.c_int32), C.POINTER(C.c_int32), U32, U32]),
         "sinter_model_get_config": (I, [vp, C.POINTER(ModelConfig)]),
         "sinter_gguf_open": (I, [C.c_char_p, C.POINTER(vp)]),
@@ -347,6 +349,24 @@ class Model:
 
     def host(self):
         return lib().sinter_model_host(self.h)
+
+    def program(self):
+        """A copy of the model's uploaded program (sinter_instr records)."""
+        n = C.c_uint32()
+        check(lib().sinter_model_program(self.h, None, 0, C.byref(n)), "program")
+        out = (Instr * n.value)()
+        check(lib().sinter_model_program(self.h, out, n.value, C.byref(n)), "program")
+        return out
+
+    def upload_program(self, instrs):
+        """Replace the model's program with packed instructions (e.g. from
+        schedule.pack): the host is stopped, the program uploaded (one barrier
+        epoch per BOUNDARY plus the pass end) and launched again."""
+        h, L = self.host(), lib()
+        nb = sum(1 for i in instrs if i.kind == OP_BOUNDARY) + 1
+        check(L.sinter_host_shutdown(h, 60000.0), "shutdown")
+        check(L.sinter_host_upload(h, instrs, len(instrs), nb), "upload")
+        check(L.sinter_host_launch(h), "launch")
 
     def bench_program(self, kind, seed=1):
         """Replace the decode program with a single-op benchmark program
