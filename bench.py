@@ -314,6 +314,11 @@ def main():
     ap.add_argument("--ctx", type=int, default=None,
                     help="context positions (default 4096; config 5: 131072 less the decoded tokens)")
     ap.add_argument("--quant", default="q4_k_m", choices=["q4_k_m", "bf16"])
+    ap.add_argument("--context", choices=["prefill", "synth"], default=None,
+                    help="how the context is made: prefill (default for config 4, as BASELINE specifies it): "
+                         "seeded random prompt tokens through sinter_model_prefill on the GPU (decode passes with "
+                         "the prompt's tokens forced); synth (default for config 5, whose 131072-token prefill "
+                         "would take ~35 min, and for --parity-steps): seeded synthetic KV and recurrent state")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2026)
@@ -331,6 +336,8 @@ def main():
     args = ap.parse_args()
     if args.config == 5:
         args.quant = "bf16"
+    if args.context is None:
+        args.context = "synth" if args.config == 5 or args.parity_steps else "prefill"
     if args.steps is None:
         args.steps = 128 if args.config == 5 else 256
     if args.warmup is None:
@@ -365,9 +372,22 @@ def main():
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
     t0 = time.perf_counter()
     m = sinter.Model(cfg, seed=args.seed)
-    m.synth_context(args.ctx, seed=args.seed + 1)
     setup_s = time.perf_counter() - t0
     print(f"# model ready in {setup_s:.1f} s: {m.info()}", file=sys.stderr, flush=True)
+    tok, prefill_info = 1, None
+    if args.context == "prefill" and args.ctx > 0:
+        import random
+        rng = random.Random(args.seed + 1)
+        prompt = [rng.randrange(cfg.n_vocab) for _ in range(args.ctx)]
+        t1 = time.perf_counter()
+        tok = m.prefill(prompt, 0)
+        ps = time.perf_counter() - t1
+        prefill_info = {"tokens": args.ctx, "seconds": round(ps, 3), "tok_s": round(args.ctx / ps, 2),
+                        "path": "sinter_model_prefill: decode passes on the GPU with the prompt's tokens forced",
+                        "prompt": f"random.Random({args.seed + 1}) token ids"}
+        print(f"# prefilled {args.ctx} tokens on the GPU in {ps:.1f} s; next token {tok}", file=sys.stderr, flush=True)
+    else:
+        m.synth_context(args.ctx, seed=args.seed + 1)
 
     if args.parity_steps:
         parity(m, cfg, args)
@@ -376,7 +396,7 @@ def main():
 
     L = sinter.lib()
     ppl = max(1, min(args.passes_per_launch, args.steps))
-    tok, pos = 1, args.ctx
+    pos = args.ctx
     if n_bal:
         # untimed: rebalances the GEMV row ranges (results are unchanged)
         tok, pos = m.balance(tok, pos, args.balance[0], args.balance[1])
@@ -424,7 +444,9 @@ def main():
         "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if args.quant == "q4_k_m" else "bf16",
-        "data": f"synthetic (seeded random-init weights and {args.ctx}-token synthetic KV/recurrent state)",
+        "data": (f"synthetic (seeded random-init weights; {args.ctx}-token context prefilled on the GPU from seeded "
+                 f"random token ids)" if prefill_info else
+                 f"synthetic (seeded random-init weights and {args.ctx}-token synthetic KV/recurrent state)"),
         "config": {"workload": f"BASELINE config {args.config}: e2e greedy decode, Qwen3.6-27B-shaped hybrid "
                                f"(48 GDN + 16 attention), {args.quant} weights, {args.ctx}-token context",
                    "context": args.ctx, "n_ctx": n_ctx, "global_batch": 1, "parallelism": "none (1 GPU)",
@@ -435,6 +457,7 @@ def main():
                      "kernel": "sinter_interp", "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
+        "prefill": prefill_info,
         "single_pass": {"ms_per_token": round(sp_ms, 4), "calls": 8,
                         "path": "sinter_model_decode: one cooperative launch per token, token read back"},
     }

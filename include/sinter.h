@@ -154,6 +154,12 @@ typedef struct sinter_argmax_ws {
     int32_t *history;     /* tokens produced, indexed by pass_cell->steps */
     uint32_t history_cap;
     uint32_t capacity;    /* partial slots (blocks the workspace was created for) */
+    /* forced tokens (prefill): after the pass with pass_cell->steps == s the
+     * next token is forced[s + 1] while s + 1 < n_forced, else the argmax;
+     * null / 0 for plain greedy decoding */
+    const int32_t *forced;
+    uint32_t n_forced;
+    uint32_t _pad;
 } sinter_argmax_ws;
 
 /* Per-pass inputs the kernel reads (harness.cpp:549-566 set_pass_inputs):
@@ -353,6 +359,12 @@ int  sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *log
 /* n greedy passes from (token, pos) in one launch */
 int  sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
                          int32_t *tokens_out);
+/* Prefill on the GPU: tokens[0..n) at positions pos0.. through the decode
+ * passes (KV rows and recurrent state written exactly as decoding them one by
+ * one would), the greedy continuation of the last one in *next_token (may be
+ * null).  Launches run up to the history capacity's passes each. */
+int  sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0,
+                          int32_t *next_token);
 /* the logits of the last pass (n_vocab floats to host): the result_output
  * cell of k0/program.json, read after run_pass / greedy */
 int  sinter_model_logits(sinter_model *m, float *logits_host);

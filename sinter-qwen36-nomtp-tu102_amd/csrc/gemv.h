@@ -1379,6 +1379,8 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
                     if (rv[w] > best || (rv[w] == best && ri[w] < bidx)) { best = rv[w]; bidx = ri[w]; }
                 sinter_pass_cell *pc = reinterpret_cast<sinter_pass_cell *>(ws->pass_cell);
                 const int32_t steps = ld_coh(&pc->steps);
+                // prefill: the prompt's next token instead of the argmax
+                if (ws->forced && (uint32_t)steps + 1u < ws->n_forced) bidx = ws->forced[steps + 1];
                 if (ws->history && (uint32_t)steps < ws->history_cap) st_coh(ws->history + steps, bidx);
                 st_coh(&pc->steps, steps + 1);
                 st_coh(&pc->token, bidx);

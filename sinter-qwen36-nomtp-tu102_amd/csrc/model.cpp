@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstddef>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -695,6 +696,42 @@ int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
     const int rs = sinter_host_run_passes(m->host, token, n, tokens_out, 600000.0);
     if (rs != SINTER_RUN_OK) return rs == SINTER_RUN_TIMEOUT ? SINTER_ERR_TIMEOUT : SINTER_ERR_DEVICE;
     return SINTER_OK;
+}
+
+int sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0, int32_t *next_token) {
+    if (!m || !tokens || n == 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.n_ctx)
+        return set_error(SINTER_ERR_ARG, "prefill: tokens / n / pos0 out of range");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.n_vocab) return set_error(SINTER_ERR_ARG, "prefill: token %u out of range", i);
+    uint32_t cap = 0;
+    (void)sinter_host_history(m->host, &cap);
+    cap = std::max(1u, std::min(cap, 1024u));
+    int32_t *d_tok = nullptr;
+    if (!hip_ok(hipMalloc(&d_tok, (size_t)n * 4), "prefill: token buffer")) return SINTER_ERR_HIP;
+    // forced / n_forced of the argmax workspace (device memory), written
+    // between launches only
+    auto set_forced = [&](const int32_t *p, uint32_t nf) {
+        struct { const int32_t *p; uint32_t n; } f = {p, nf};
+        return hip_ok(hipMemcpy(reinterpret_cast<char *>(m->ws) + offsetof(sinter_argmax_ws, forced), &f.p,
+                                sizeof f.p, hipMemcpyHostToDevice), "prefill: forced") &&
+               hip_ok(hipMemcpy(reinterpret_cast<char *>(m->ws) + offsetof(sinter_argmax_ws, n_forced), &f.n,
+                                sizeof f.n, hipMemcpyHostToDevice), "prefill: n_forced");
+    };
+    int rc = hip_ok(hipMemcpy(d_tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice), "prefill: tokens") ? SINTER_OK
+                                                                                                      : SINTER_ERR_HIP;
+    for (uint32_t b = 0; rc == SINTER_OK && b < n; b += cap) {
+        const uint32_t len = std::min(cap, n - b);
+        if (!set_forced(d_tok + b, n - b)) { rc = SINTER_ERR_HIP; break; }
+        if ((rc = sinter_host_set_pos(m->host, pos0 + (int32_t)b))) break;
+        const int rs = sinter_host_run_passes(m->host, tokens[b], len, nullptr, 600000.0);
+        if (rs != SINTER_RUN_OK) rc = rs == SINTER_RUN_TIMEOUT ? SINTER_ERR_TIMEOUT : SINTER_ERR_DEVICE;
+    }
+    if (!set_forced(nullptr, 0) && rc == SINTER_OK) rc = SINTER_ERR_HIP;
+    (void)hipFree(d_tok);
+    if (rc == SINTER_OK && next_token &&
+        !hip_ok(hipMemcpy(next_token, &sinter_host_pass_cell(m->host)->token, 4, hipMemcpyDeviceToHost), "prefill: token"))
+        rc = SINTER_ERR_HIP;
+    return rc;
 }
 
 int sinter_model_logits(sinter_model *m, float *logits_host) {

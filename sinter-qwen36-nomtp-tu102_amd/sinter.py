@@ -163,6 +163,7 @@ def lib():
         "sinter_model_destroy": (None, [vp]),
         "sinter_model_decode": (I, [vp, C.c_int32, C.c_int32, vp, C.POINTER(C.c_int32)]),
         "sinter_model_greedy": (I, [vp, C.c_int32, C.c_int32, U32, C.POINTER(C.c_int32)]),
+        "sinter_model_prefill": (I, [vp, C.POINTER(C.c_int32), U32, C.c_int32, C.POINTER(C.c_int32)]),
         "sinter_model_synth_context": (I, [vp, C.c_int32, U64]),
         "sinter_model_logits": (I, [vp, vp]),
         "sinter_model_tensor_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t), C.POINTER(I)]),
@@ -322,6 +323,14 @@ class Model:
         out = (C.c_int32 * n)()
         check(lib().sinter_model_greedy(self.h, token, pos, n, out), "greedy")
         return list(out)
+
+    def prefill(self, tokens, pos0=0):
+        """Prefill tokens at positions pos0.. on the GPU (decode passes with
+        the prompt's tokens forced); returns the greedy next token."""
+        arr = (C.c_int32 * len(tokens))(*tokens)
+        nxt = C.c_int32()
+        check(lib().sinter_model_prefill(self.h, arr, len(tokens), pos0, C.byref(nxt)), "prefill")
+        return nxt.value
 
     def logits(self, out=None):
         """Logits of the last decoded pass (float32[n_vocab])."""
