@@ -194,8 +194,8 @@ typedef struct sinter_attn_args {
     const float *v;         /* [NKV*HD] raw v projection */
     const float *q_norm;    /* [HD] */
     const float *k_norm;    /* [HD] */
-    uint16_t *kc;           /* K cache f16 [n_ctx][NKV*HD] */
-    uint16_t *vc;           /* V cache f16 [n_ctx][NKV*HD] */
+    void *kc;               /* K cache [n_ctx][NKV heads]: f16 [HD] or Q8_0 [HD/32 blocks] per head */
+    void *vc;               /* V cache, the same layout */
     double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64; sinter_attn_part_len */
     uint32_t *count;        /* per-(kv head, chunk) generation flags, sinter_attn_count_len words,
                                0 before first use; each call adds 1 to each of the NKV*n_chunks */
@@ -203,7 +203,7 @@ typedef struct sinter_attn_args {
     const int32_t *pass_cell; /* sinter_pass_cell (pos) */
     uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;
     float theta_scale, eps, scale;
-    uint32_t _pad;
+    uint32_t kv_type;       /* SINTER_F16 (also 0) or SINTER_Q8_0 (ggml's f32 -> q8_0 block quantiser on append) */
 } sinter_attn_args;
 
 /* Buffer sizes for sinter_attn_args (n_chunks <= 64): part in doubles,
@@ -328,7 +328,8 @@ enum sinter_synth_kind {
     SINTER_SYN_Q8_0_CFG1 = 1,/* Q8_0: codes U[-127,127], d = f16(|N(0, 0.02)|) */
     SINTER_SYN_NORMAL = 2,  /* f32 ~ mean + std * N(0,1) (Irwin-Hall(4) approximation) */
     SINTER_SYN_UNIFORM = 3, /* f32 ~ U[lo, hi) */
-    SINTER_SYN_NORMAL_F16 = 4 /* f16 ~ std * N(0,1) */
+    SINTER_SYN_NORMAL_F16 = 4,/* f16 ~ std * N(0,1) */
+    SINTER_SYN_NORMAL_Q8_0 = 5 /* Q8_0 blocks of std * N(0,1) (ggml's q8_0 quantiser); k a multiple of 32 */
 };
 /* Fill n elements (rows*k for weights) at dst.  dev != 0: dst is device
  * memory and the fill runs on `stream`; dev == 0: host memory. */
@@ -344,6 +345,7 @@ typedef struct sinter_model_config {
     float rope_base, eps;
     int32_t n_ctx;
     int32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
+    int32_t t_kv;           /* KV cache type: SINTER_F16 (also when 0) or SINTER_Q8_0 */
 } sinter_model_config;
 
 typedef struct sinter_model sinter_model;

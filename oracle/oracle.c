@@ -202,6 +202,22 @@ void or_quant_q8_0(const float *x, void *vy, int64_t k) {
     }
 }
 
+/* ggml quantize_row_q8_0_ref (ggml-quants.c), the form the KV-cache copy
+ * kernels use too: d = amax/127 (f16), id = d ? 1/d : 0, q = roundf(x*id)
+ * (half away from zero). */
+void or_quant_q8_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    for (int64_t ib = 0; ib < k / 32; ib++) {
+        const float *xb = x + ib * 32;
+        float amax = 0.0f;
+        for (int l = 0; l < 32; l++) amax = fmaxf(amax, fabsf(xb[l]));
+        const float d = amax / 127.f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[ib].d = or_f32_to_f16(d);
+        for (int l = 0; l < 32; l++) y[ib].qs[l] = (int8_t)roundf(xb[l] * id);
+    }
+}
+
 /* ggml quantize_row_q8_K_ref: max = signed element of largest |x| (first
  * wins); iscale = -127/max; q = min(127, nearest_int(iscale*x)); bsums over
  * 16; d = 1/iscale. */
@@ -529,6 +545,47 @@ void or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc, int 
     }
 }
 
+/* element e of cache row j (row of row_elems elements) as f32: f16, or a
+ * Q8_0 code times its block's f16 scale (exact in f32) */
+static float kv_elem(const void *cache, int kv_type, size_t row_elems, int j, size_t e) {
+    if (kv_type == OR_Q8_0) {
+        const blk_q8_0 *b = (const blk_q8_0 *)cache + ((size_t)j * row_elems + e) / 32;
+        return (float)b->qs[e % 32] * or_f16_to_f32(b->d);
+    }
+    return or_f16_to_f32(((const uint16_t *)cache)[(size_t)j * row_elems + e]);
+}
+
+/* or_attn_decode with the cache element type a parameter (same arithmetic) */
+void or_attn_decode_kv(const float *q, const void *kc, const void *vc, int kv_type, int n_kv,
+                       int nq, int nkv, int hd, float scale, float *out) {
+    const int gqa = nq / nkv;
+    const size_t rw = (size_t)nkv * hd;
+#pragma omp parallel for schedule(static)
+    for (int h = 0; h < nq; h++) {
+        double *s = (double *)malloc(sizeof(double) * (size_t)(n_kv > 0 ? n_kv : 1));
+        double *acc = (double *)malloc(sizeof(double) * (size_t)hd);
+        const int g = h / gqa;
+        const float *qh = q + (size_t)h * hd;
+        double m = -INFINITY;
+        for (int j = 0; j < n_kv; j++) {
+            double dot = 0.0;
+            for (int d = 0; d < hd; d++) dot += (double)qh[d] * (double)kv_elem(kc, kv_type, rw, j, (size_t)g * hd + d);
+            s[j] = dot * (double)scale;
+            if (s[j] > m) m = s[j];
+        }
+        double sum = 0.0;
+        for (int d = 0; d < hd; d++) acc[d] = 0.0;
+        for (int j = 0; j < n_kv; j++) {
+            const double p = exp(s[j] - m);
+            sum += p;
+            for (int d = 0; d < hd; d++) acc[d] += p * (double)kv_elem(vc, kv_type, rw, j, (size_t)g * hd + d);
+        }
+        for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(acc[d] / sum);
+        free(s);
+        free(acc);
+    }
+}
+
 /* ------------------------------------------------------------ layers */
 
 int or_is_attn_layer(const or_cfg *c, int il) {
@@ -604,12 +661,20 @@ void or_attn_mixer(const or_cfg *c, const void *const *w, void *const *st,
         or_rmsnorm(kk + (size_t)g * HD, (const float *)w[OR_SLOT_K_NORM], kr + (size_t)g * HD, HD, c->eps);
         or_rope_neox(kr + (size_t)g * HD, HD, c->rope_dims, pos, ts);
     }
-    uint16_t *K = (uint16_t *)st[OR_ST_K], *V = (uint16_t *)st[OR_ST_V];
-    for (int i = 0; i < RW; i++) {
-        K[(size_t)pos * RW + i] = or_f32_to_f16(kr[i]);
-        V[(size_t)pos * RW + i] = or_f32_to_f16(vv[i]);
+    if (c->t_kv == OR_Q8_0) {
+        /* the appended rows as Q8_0 blocks (ggml's reference quantiser) */
+        blk_q8_0 *K = (blk_q8_0 *)st[OR_ST_K], *V = (blk_q8_0 *)st[OR_ST_V];
+        or_quant_q8_0_ref(kr, K + (size_t)pos * (RW / 32), RW);
+        or_quant_q8_0_ref(vv, V + (size_t)pos * (RW / 32), RW);
+        or_attn_decode_kv(qr, K, V, OR_Q8_0, pos + 1, NQ, NKV, HD, 1.0f / sqrtf((float)HD), att);
+    } else {
+        uint16_t *K = (uint16_t *)st[OR_ST_K], *V = (uint16_t *)st[OR_ST_V];
+        for (int i = 0; i < RW; i++) {
+            K[(size_t)pos * RW + i] = or_f32_to_f16(kr[i]);
+            V[(size_t)pos * RW + i] = or_f32_to_f16(vv[i]);
+        }
+        or_attn_decode(qr, K, V, pos + 1, NQ, NKV, HD, RW, 1.0f / sqrtf((float)HD), att);
     }
-    or_attn_decode(qr, K, V, pos + 1, NQ, NKV, HD, RW, 1.0f / sqrtf((float)HD), att);
     for (int h = 0; h < NQ; h++)
         for (int d = 0; d < HD; d++) {
             const float gv = qg[(size_t)h * 2 * HD + HD + d];

@@ -48,6 +48,7 @@ void or_dequant_row(int type, const void *row, float *out, int64_t k);
 
 /* activation quantisers */
 void or_quant_q8_0(const float *x, void *y, int64_t k);  /* x86 AVX2 form */
+void or_quant_q8_0_ref(const float *x, void *y, int64_t k);  /* reference form (KV cache rows) */
 void or_quant_q8_K(const float *x, void *y, int64_t k);  /* reference form */
 void or_quant_bf16(const float *x, uint16_t *y, int64_t k);
 
@@ -87,6 +88,10 @@ void  or_rope_neox(float *x, int hd, int n_dims, int pos, float theta_scale);
 void  or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
                      int n_kv, int nq, int nkv, int hd, int row_width, float scale,
                      float *out);
+/* the same over a cache of kv_type OR_F16 or OR_Q8_0 (rows of nkv*hd
+ * elements; a Q8_0 element is dequantised exactly first) */
+void  or_attn_decode_kv(const float *q, const void *kc, const void *vc, int kv_type,
+                        int n_kv, int nq, int nkv, int hd, float scale, float *out);
 
 /* model configuration (mirrors sinter_model_config in include/sinter.h) */
 typedef struct {
@@ -96,6 +101,7 @@ typedef struct {
     float   rope_base, eps;
     int32_t n_ctx;
     int32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
+    int32_t t_kv;   /* KV cache: OR_F16 (also 0) or OR_Q8_0 */
 } or_cfg;
 
 /* per-layer weight slots (NSLOT pointers per layer) */

@@ -22,7 +22,7 @@ class Cfg(C.Structure):
                                          "gdn_hv", "gdn_d", "conv_k", "attn_nq", "attn_nkv", "head_dim",
                                          "rope_dims")] + \
                [("rope_base", C.c_float), ("eps", C.c_float), ("n_ctx", C.c_int32)] + \
-               [(n, C.c_int32) for n in ("t_default", "t_attn_v", "t_ffn_down", "t_output", "t_embd")]
+               [(n, C.c_int32) for n in ("t_default", "t_attn_v", "t_ffn_down", "t_output", "t_embd", "t_kv")]
 
 
 def build():
@@ -47,6 +47,7 @@ def lib():
             "or_row_bytes": (C.c_size_t, [i, i64]),
             "or_dequant_row": (None, [i, p, p, i64]),
             "or_quant_q8_0": (None, [p, p, i64]), "or_quant_q8_K": (None, [p, p, i64]),
+            "or_quant_q8_0_ref": (None, [p, p, i64]),
             "or_quant_bf16": (None, [p, p, i64]),
             "or_block_term": (C.c_double, [i, p, p]),
             "or_gemv": (None, [i, p, i64, i64, p, p]), "or_gemv_q": (None, [i, p, i64, i64, p, p]),
@@ -58,6 +59,7 @@ def lib():
             "or_gated_rmsnorm": (None, [p, p, p, p, i, i, f]),
             "or_rope_theta_scale": (f, [f, i]), "or_rope_neox": (None, [p, i, i, i, f]),
             "or_attn_decode": (None, [p, p, p, i, i, i, i, i, f, p]),
+            "or_attn_decode_kv": (None, [p, p, p, i, i, i, i, i, f, p]),
             "or_is_attn_layer": (i, [C.POINTER(Cfg), i]),
             "or_gdn_mixer": (None, [C.POINTER(Cfg), p, p, p, p, p]),
             "or_row_isa": (i, []),

@@ -2,7 +2,8 @@
 // q|gate / k / v projections, fused:
 //   per-head RMSNorm * weight + NEOX RoPE on the first rope_dims dims
 //                                              (k0/ops/attn.cuh:109-182)
-//   f16 KV append at row pos                   (attn.cuh:184-211)
+//   KV append at row pos, f16 (attn.cuh:184-211) or Q8_0 blocks (ggml's
+//   f32 -> q8_0 block quantiser)
 //   split-K online-softmax partials            (attn.cuh:244-401)
 //   max/LSE merge by the last-arriving block   (attn.cuh:403-458)
 //   sigmoid output gate                        (attn.cuh:460-488)
@@ -14,9 +15,11 @@
 // gate, so the reference's separate FATTN_REDUCE / ATTN_GATE windows (and
 // their barriers) disappear.
 //
-// Declared numerics (oracle/oracle.c or_attn_decode): q/k norms and RoPE in
-// fp32 as ggml; scores are fp64 sums of exact products times the fp32 scale;
-// softmax and the V sum in fp64; the merged output rounded to fp32 once.
+// Declared numerics (oracle/oracle.c or_attn_decode_kv): q/k norms and RoPE
+// in fp32 as ggml; scores are fp64 sums of exact products times the fp32
+// scale; softmax and the V sum in fp64; the merged output rounded to fp32
+// once.  A Q8_0 cache element is dequantised exactly (int8 code times the
+// block's f16 scale, exact in fp32) before it enters the same arithmetic.
 #pragma once
 #include "dev_common.h"
 
@@ -24,6 +27,72 @@ namespace sinter {
 
 constexpr int ATT_TILE = 32;   // KV positions per LDS tile
 constexpr int ATT_MAXG = 8;    // max q heads per kv head
+constexpr uint32_t ATT_Q8_HEAD = 272;   // one head's 256 elements as eight 34-byte Q8_0 blocks
+// Q8_0 tile LDS map (in the f16 tiles' 64 KiB): raw K tiles at 0 and
+// ATT_Q8_RAWB, raw V tiles at 2 * ATT_Q8_RAWB (+ ATT_Q8_RAWB), then the
+// current tile split into codes [32][256] K and V, and scales [32][8] K and V
+constexpr uint32_t ATT_Q8_RAWB = 9600;  // 32 rows x 272 B, plus the third DMA's overrun (56 chunks)
+constexpr uint32_t ATT_Q8_KC = 4 * ATT_Q8_RAWB, ATT_Q8_VC = ATT_Q8_KC + 32 * 256;
+constexpr uint32_t ATT_Q8_KS = ATT_Q8_VC + 32 * 256, ATT_Q8_VS = ATT_Q8_KS + 32 * 8 * 4;
+static_assert(ATT_Q8_VS + 32 * 8 * 4 <= 4 * ATT_TILE * 512, "Q8_0 tiles fit the f16 tile region");
+static_assert(ATT_Q8_RAWB % 16 == 0 && 4 * 136 * 16 + 56 * 16 <= ATT_Q8_RAWB, "raw tile plus overrun");
+
+// The 8 elements [8p, 8p+8) of a 256-element head row, as exact doubles.
+// f16: the row's 512 bytes (16-aligned).  Q8_0: the row split in LDS into
+// its 256 int8 codes (row) and the eight block scales, sc being the scale of
+// block p/4; a code times its scale is exact in fp64.
+template <bool Q8>
+__device__ __forceinline__ void att_row8(const LDS unsigned char *row, uint32_t p, float sc, double out[8]) {
+    if constexpr (!Q8) {
+        (void)sc;
+        const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(row + 16 * p);
+        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            out[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
+            out[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
+        }
+    } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 c = *reinterpret_cast<const LDS u32x2 *>(row + 8 * p);
+        const double d = (double)sc;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint32_t w = k < 4 ? c.x : c.y;
+            out[k] = (double)(int)(int8_t)((w >> (8 * (k & 3))) & 0xffu) * d;
+        }
+    }
+}
+
+// One Q8_0 block (34 bytes at src, 2-aligned: f16 d, 32 int8 codes) split
+// into its codes (32 bytes at dst, 16-aligned) and its scale as f32.
+__device__ __forceinline__ void att_q8_split(const LDS unsigned char *src, LDS unsigned char *dst, LDS float *sc) {
+    const LDS uint16_t *h = reinterpret_cast<const LDS uint16_t *>(src);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+    *sc = h2f(h[0]);
+    const u32x4 a = {w[0], w[1], w[2], w[3]}, b = {w[4], w[5], w[6], w[7]};
+    *reinterpret_cast<LDS u32x4 *>(dst) = a;
+    *reinterpret_cast<LDS u32x4 *>(dst + 16) = b;
+}
+
+// ggml's f32 -> Q8_0 block quantiser (quantize_row_q8_0_ref; the KV-cache
+// copy kernels do the same): per 32 elements amax = max |x|, d = amax / 127,
+// id = d ? 1/d : 0, q = roundf(x * id), d stored as f16.  Thread t holds
+// element t of a 256-element head; each 32-lane half-wave is one block; the
+// 272-byte row lands in LDS at `row`.
+__device__ __forceinline__ void att_quant_q8_0(float x, LDS unsigned char *row) {
+    const uint32_t t = tid(), e = t & 31u;
+    float am = fabsf(x);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    LDS unsigned char *blk = row + (t >> 5) * 34u;
+    blk[2 + e] = (unsigned char)(int8_t)roundf(x * id);
+    if (e == 0) *reinterpret_cast<LDS uint16_t *>(blk) = f2h(d);
+}
 
 // Per-pass cache (interpreter only): every attention op of one pass reads the
 // same position from the same pass cell, so the first one of the pass loads
@@ -50,7 +119,7 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
                                          float eps, int pos, float theta_scale, uint32_t rope_dims,
                                          LDS float *dst, LDS float *qn, LDS float *rot, LDS double *red,
                                          bool compute_rot) {
-    const uint32_t t = threadIdx.x, half = rope_dims / 2;
+    const uint32_t t = tid(), half = rope_dims / 2;
     // cos on wave 0, sin on wave 1 (the two run side by side); skipped when
     // rot already holds this position's rotation
     const uint32_t ri = t < 64 ? t : t - 64;
@@ -65,7 +134,7 @@ __device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t n
         if (j < nh) {
             const double v = row16_sum_f64((double)(x[j] * x[j]));
             const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
-            if (lane_id() == 0) red[wave_id() * (ATT_MAXG + 1) + j] = w;
+            if ((t & 63u) == 0) red[(t >> 6) * (ATT_MAXG + 1) + j] = w;
         }
     }
     __syncthreads();
@@ -159,8 +228,9 @@ __device__ __forceinline__ bool att_wait_flags(const uint32_t *f, uint32_t n, ui
 // the KV tiles.  spin_limit bounds the wait for the other chunks of the kv
 // head (wall clock ticks).  pass_id: the interpreter's pass index (the
 // per-pass cache above), or ATT_NO_CACHE.
-__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts,
-                                               uint64_t spin_limit, uint32_t pass_id) {
+template <bool Q8>
+__device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsigned *err, uint64_t *ts,
+                                                 uint64_t spin_limit, uint32_t pass_id) {
     // the payload, read once into registers: the op stores to the KV cache
     // and the partials, which the compiler cannot tell apart from the payload
     // (every field would be reloaded from memory after each such store)
@@ -173,9 +243,10 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     const int pos = cached ? (int)g_att_key[1] : ld_coh(&reinterpret_cast<const sinter_pass_cell *>(a.pass_cell)->pos);
     const bool rot_cached = cached && g_att_key[2] == __float_as_uint(a.theta_scale) && g_att_key[3] == a.rope_dims;
     const uint32_t gqa = NKV ? NQ / NKV : 0;
+    constexpr bool q8 = Q8;
     const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 && C <= 64 &&
                     NKV * C <= nblk && a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 &&
-                    (uint32_t)pos < a.n_ctx;
+                    (uint32_t)pos < a.n_ctx && (q8 == (a.kv_type == SINTER_Q8_0));
     if (!ok) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
         return;
@@ -183,8 +254,10 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     if (rel >= NKV * C) return;   // one item per workgroup (the merge waits for its kv head's chunks)
     // this chunk's generation flag (written only by this item, once per call)
     const uint32_t gen = ld_coh(a.count + rel);
-    const uint32_t t = threadIdx.x;
-    const uint32_t RW = NKV * HD, PS = HD + 2;
+    const uint32_t t = tid();
+    const uint32_t PS = HD + 2;
+    // cache row: all kv heads of a position; one head HB bytes
+    const uint32_t HB = q8 ? ATT_Q8_HEAD : HD * 2u, RWB = NKV * HB;
     const uint32_t n_kv = (uint32_t)pos + 1;
     const uint32_t clen = (n_kv + C - 1) / C;
 
@@ -193,6 +266,7 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     // corrections; after the tiles the K/V area holds the row-group sums,
     // then the merge's weights.
     lds_char *L = (lds_char *)g_big;
+    LDS unsigned char *Lu = reinterpret_cast<LDS unsigned char *>(L);
     LDS uint16_t *kb = reinterpret_cast<LDS uint16_t *>(L);                          // [2][32][256]
     LDS uint16_t *vb = reinterpret_cast<LDS uint16_t *>(L + 2 * ATT_TILE * 512);     // [2][32][256]
     LDS float *qf = reinterpret_cast<LDS float *>(L + 4 * ATT_TILE * 512);           // [gqa][256] q, then the new k row
@@ -204,30 +278,52 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(corr + ATT_MAXG);          // [256]
     LDS uint16_t *vnew = knew + 256;                                                 // [256]
     LDS unsigned *flag = reinterpret_cast<LDS unsigned *>(vnew + 256);
+    // Q8_0: the appended K / V head rows (16-aligned)
+    LDS unsigned char *knew8 = reinterpret_cast<LDS unsigned char *>(
+        ((uint32_t)(uintptr_t)(flag + 1) + 15u) & ~15u);
+    LDS unsigned char *vnew8 = knew8 + ATT_Q8_HEAD;
+
     LDS double *comb = reinterpret_cast<LDS double *>(L);       // after the tiles: [4 rg][16][64 lanes]
     LDS double *mw = reinterpret_cast<LDS double *>(L);         // merge: [C][gqa] m, then weights e
     LDS double *mlv = mw + 64 * ATT_MAXG;                       //        [C][gqa] l
     LDS double *mM = mlv + 64 * ATT_MAXG;                       //        [ATT_MAXG + gqa]: L at ATT_MAXG + h
     LDS double *msum = mM + 2 * ATT_MAXG;                       //        [256] per-thread element partials
-    const uint32_t w = __builtin_amdgcn_readfirstlane(wave_id()), lane = lane_id();
+    const uint32_t w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63u;
     const uint32_t kbase = (uint32_t)(uintptr_t)kb, vbase = (uint32_t)(uintptr_t)vb;
 
     const uint32_t g = rel / C, c = rel % C;
     const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
     const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
     const uint32_t ntile = (kv1 - kv0 + ATT_TILE - 1) / ATT_TILE;
-    // Tile j (32 rows of this kv head: 512 B of K and of V each) into
-    // buffer j % 2: each wave DMAs rows 2k, 2k+1 for k = w, w+4, w+8,
-    // w+12 of K and of V (lane l: row 2k + l/32, bytes 16 (l%32) ..);
-    // rows past kv1 re-read row kv1-1 (masked in the scores).
+    // Tile j (32 rows of this kv head: HB bytes of K and of V each) into
+    // buffer j % 2 (16 KiB apart), rows back to back.  f16: each wave DMAs
+    // rows 2k, 2k+1 for k = w, w+4, w+8, w+12 of K and of V (lane l: row
+    // 2k + l/32, bytes 16 (l%32) ..) -- 8 DMAs per wave.  Q8_0: the tile's
+    // 32 x 17 16-byte chunks into raw buffer j % 2 (ATT_Q8_RAWB apart),
+    // wave w chunks [136w, 136w + 192) in three whole-wave DMAs per matrix --
+    // 6 per wave; the last 56 chunks of a wave are the next wave's first (the
+    // same bytes written twice), past the tile (wave 3) they land in the
+    // buffer's overrun.  Rows past kv1 re-read row kv1-1 (masked in the
+    // scores).
     auto issue_tile = [&](uint32_t j) {
         const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
+        if (!q8) {
 #pragma unroll
-        for (uint32_t kk = 0; kk < 4; kk++) {
-            const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
-            const uint32_t voff = (row * RW + g * HD) * 2 + (lane & 31) * 16;
-            lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
-            lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
+            for (uint32_t kk = 0; kk < 4; kk++) {
+                const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
+                const uint32_t voff = row * RWB + g * HB + (lane & 31) * 16;
+                lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
+                lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
+            }
+            return;
+        }
+        const uint32_t rb = (j & 1) * ATT_Q8_RAWB;
+#pragma unroll
+        for (uint32_t kk = 0; kk < 3; kk++) {
+            const uint32_t c0 = 136u * w + 64u * kk, ci = c0 + lane;
+            const uint32_t row = min(t0 + ci / 17u, kv1 - 1), voff = row * RWB + g * HB + (ci % 17u) * 16u;
+            lds_dma16<true>((uintptr_t)a.kc, voff, kbase + rb + c0 * 16u);
+            lds_dma16<true>((uintptr_t)a.vc, voff, kbase + 2 * ATT_Q8_RAWB + rb + c0 * 16u);
         }
     };
     const uint32_t rg = t >> 6, hg = (t >> 5) & 1, p = t & 31, mp = att_perm(p);
@@ -259,9 +355,12 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
         }
         if (ntile > 0) issue_tile(0);
         if (ntile > 1) issue_tile(1);
-        const uint32_t behind = (ntile > 0 ? 8u : 0u) + (ntile > 1 ? 8u : 0u);
+        const uint32_t per = q8 ? 6u : 8u;   // DMAs per tile per wave
+        const uint32_t behind = (ntile > 0 ? per : 0u) + (ntile > 1 ? per : 0u);
         if (behind == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (behind == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
         else if (behind == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (behind == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else dma_wait();
         __syncthreads();
         float xr[ATT_MAXG + 1];
@@ -272,18 +371,41 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
         __syncthreads();
         att_prep(xr, gqa, owner ? gqa + 1 : gqa, qwv, kwv, a.eps, pos, a.theta_scale, a.rope_dims, qf, qn, rot, pred,
                  !rot_cached);
-        if (owner) vnew[t] = f2h(vraw);
+        if (owner && !q8) vnew[t] = f2h(vraw);
+        if (owner && q8) att_quant_q8_0(vraw, vnew8);
         // (att_prep ended with a workgroup barrier: every thread has read the key)
         if (pass_id != ATT_NO_CACHE && t == 0) {
             g_att_key[0] = pass_id; g_att_key[1] = (uint32_t)pos; g_att_key[2] = __float_as_uint(a.theta_scale);
             g_att_key[3] = a.rope_dims; g_att_key[4] = pc_lo; g_att_key[5] = pc_hi;
         }
     }
-    if (owner) {
+    if (owner && !q8) {
         const uint16_t kh = f2h(qf[gqa * 256 + t]), vh = vnew[t];
         knew[t] = kh;
-        st_coh(a.kc + (size_t)pos * RW + (size_t)g * HD + t, kh);
-        st_coh(a.vc + (size_t)pos * RW + (size_t)g * HD + t, vh);
+        const size_t o = (size_t)pos * RWB + (size_t)g * HB + 2u * t;
+        st_coh(reinterpret_cast<uint16_t *>(static_cast<char *>(a.kc) + o), kh);
+        st_coh(reinterpret_cast<uint16_t *>(static_cast<char *>(a.vc) + o), vh);
+    }
+    if (owner && q8) {
+        // the head's K row quantised like its V row above, then both rows
+        // (272 B each) stored by 17 lanes of 16 bytes
+        att_quant_q8_0(qf[gqa * 256 + t], knew8);
+        __syncthreads();
+        // the new rows split like the tiles: codes at knew / vnew, scales after them
+        if (t < 16) {
+            LDS unsigned char *nd = reinterpret_cast<LDS unsigned char *>(t < 8 ? knew : vnew);
+            att_q8_split((t < 8 ? knew8 : vnew8) + 34u * (t & 7u), nd + 32u * (t & 7u),
+                         reinterpret_cast<LDS float *>(nd + 256) + (t & 7u));
+        }
+
+        if ((t & 31u) < 17u && t < 64) {
+            const uint32_t i = t & 31u;
+            const LDS unsigned char *src = (t < 32 ? knew8 : vnew8) + 16u * i;
+            const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(src);
+            char *dst = static_cast<char *>(t < 32 ? a.kc : a.vc) + (size_t)pos * RWB + (size_t)g * HB + 16u * i;
+            st_coh(reinterpret_cast<uint64_t *>(dst), (uint64_t)u.x | ((uint64_t)u.y << 32));
+            st_coh(reinterpret_cast<uint64_t *>(dst) + 1, (uint64_t)u.z | ((uint64_t)u.w << 32));
+        }
     }
 #pragma unroll
     for (uint32_t j = 0; j < ATT_HG; j++) {
@@ -300,15 +422,29 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
     if (ts) ts[1] = wall_clock64();
 
     for (uint32_t j = 0; j < ntile; j++) {
-        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 256;
+        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
         if (j == 0) {
             dma_wait();   // (also the owner's cache stores)
         } else {
             // tile j landed; tile j+1 (issued last step) may still fly
-            if (j + 1 < ntile) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-            else dma_wait();
+            if (j + 1 < ntile) {
+                if (q8) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            } else {
+                dma_wait();
+            }
         }
         __syncthreads();
+        if constexpr (Q8) {
+            // thread t splits block t % 8 of row t / 8 of the K and the V tile
+            const uint32_t rr = t >> 3, bb = t & 7u, rb = (j & 1) * ATT_Q8_RAWB;
+            const LDS unsigned char *raw = Lu + rb + rr * ATT_Q8_HEAD + 34u * bb;
+            att_q8_split(raw, Lu + ATT_Q8_KC + rr * 256 + 32u * bb, reinterpret_cast<LDS float *>(Lu + ATT_Q8_KS) + t);
+            sched_fence();   // one block's words live at a time
+            att_q8_split(raw + 2 * ATT_Q8_RAWB, Lu + ATT_Q8_VC + rr * 256 + 32u * bb,
+                         reinterpret_cast<LDS float *>(Lu + ATT_Q8_VS) + t);
+            __syncthreads();
+        }
         // scores: partial dots over dims 8p..8p+7 (ascending) of rows
         // 8rg + (i ^ mp/4) and slots 4hg + (jj ^ mp%4) in slot i*4 + jj (the
         // permuted order above), then the reduce-scatter over the 32 lanes of
@@ -318,15 +454,15 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
 #pragma unroll
             for (uint32_t i = 0; i < ATT_RG; i++) {
                 const uint32_t r = ATT_RG * rg + (i ^ (mp >> 2));
-                const LDS uint16_t *kr = ((owner && t0 + r == (uint32_t)pos) ? knew : kb + bo + r * 256) + ATT_DP * p;
-                const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(kr);
-                const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+                const bool nr = owner && t0 + r == (uint32_t)pos;
+                const LDS unsigned char *kr = nr ? reinterpret_cast<const LDS unsigned char *>(knew)
+                                            : q8 ? Lu + ATT_Q8_KC + r * 256
+                                                 : reinterpret_cast<const LDS unsigned char *>(kb) + bo + r * 512;
+                const float ks = !q8 ? 0.0f
+                                : nr ? reinterpret_cast<const LDS float *>(kr + 256)[p >> 2]
+                                     : reinterpret_cast<const LDS float *>(Lu + ATT_Q8_KS)[r * 8 + (p >> 2)];
                 double kd[ATT_DP];
-#pragma unroll
-                for (uint32_t k = 0; k < 4; k++) {
-                    kd[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
-                    kd[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
-                }
+                att_row8<Q8>(kr, p, ks, kd);
 #pragma unroll
                 for (uint32_t jj = 0; jj < ATT_HG; jj++) {
                     double d = 0.0;
@@ -378,18 +514,18 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
 #pragma unroll
             for (uint32_t i = 0; i < ATT_RG; i++) {
                 const uint32_t r = ATT_RG * rg + i;
-                const LDS uint16_t *vr = ((owner && t0 + r == (uint32_t)pos) ? vnew : vb + bo + r * 256) + ATT_DP * p;
-                const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(vr);
-                const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+                const bool nr = owner && t0 + r == (uint32_t)pos;
+                const LDS unsigned char *vr = nr ? reinterpret_cast<const LDS unsigned char *>(vnew)
+                                            : q8 ? Lu + ATT_Q8_VC + r * 256
+                                                 : reinterpret_cast<const LDS unsigned char *>(vb) + bo + r * 512;
+                const float vs = !q8 ? 0.0f
+                                : nr ? reinterpret_cast<const LDS float *>(vr + 256)[p >> 2]
+                                     : reinterpret_cast<const LDS float *>(Lu + ATT_Q8_VS)[r * 8 + (p >> 2)];
                 double wt[ATT_HG];
 #pragma unroll
                 for (uint32_t jj = 0; jj < ATT_HG; jj++) wt[jj] = sc[(ATT_HG * hg + jj) * ATT_TILE + r];
                 double vd[ATT_DP];
-#pragma unroll
-                for (uint32_t k = 0; k < 4; k++) {
-                    vd[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
-                    vd[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
-                }
+                att_row8<Q8>(vr, p, vs, vd);
 #pragma unroll
                 for (uint32_t jj = 0; jj < ATT_HG; jj++)
 #pragma unroll
@@ -539,6 +675,15 @@ __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned
         }
     }
     settle_vmem();
+}
+
+// the attention op of either KV cache type (the standalone op kernels)
+__device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts,
+                                               uint64_t spin_limit, uint32_t pass_id) {
+    if (reinterpret_cast<const sinter_attn_args *>(ins.payload)->kv_type == SINTER_Q8_0)
+        op_attn_decode_t<true>(ins, err, ts, spin_limit, pass_id);
+    else
+        op_attn_decode_t<false>(ins, err, ts, spin_limit, pass_id);
 }
 
 }  // namespace sinter

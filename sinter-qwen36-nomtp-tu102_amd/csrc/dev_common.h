@@ -46,6 +46,17 @@ __shared__ __attribute__((aligned(16))) unsigned char g_args[240];
 // ---------------------------------------------------------------- wave64
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// The thread index behind an empty asm: the interpreter runs every op inside
+// one persistent loop, and values an op derives from a plain threadIdx.x
+// (LDS addresses, lane permutations) are loop-invariant, so the compiler
+// hoists them all to the kernel entry and keeps them live -- in registers,
+// or in scratch -- for the whole kernel.  Derived from tid() they are
+// recomputed by each op invocation instead.
+__device__ __forceinline__ uint32_t tid() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 __device__ __forceinline__ float wave_max_f32(float v) {

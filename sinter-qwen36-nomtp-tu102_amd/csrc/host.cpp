@@ -387,14 +387,18 @@ uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks) {
     return nkv * n_chunks;
 }
 
+// KV cache element types the attention op reads (0 means f16)
+static bool kv_type_ok(uint32_t t) { return t == 0 || t == SINTER_F16 || t == SINTER_Q8_0; }
+
 int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream) {
     if (!a || !a->qg || !a->k || !a->v || !a->q_norm || !a->k_norm || !a->kc || !a->vc || !a->part || !a->count ||
         !a->out || !a->pass_cell)
         return set_error(SINTER_ERR_ARG, "attn: null pointer");
     if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
         a->rope_dims > a->hd ||
-        a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
-        return set_error(SINTER_ERR_ARG, "attn: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
+        a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
+        return set_error(SINTER_ERR_ARG, "attn: unsupported shape or KV type (hd=%u nq=%u nkv=%u kv_type=%u)", a->hd,
+                         a->nq, a->nkv, a->kv_type);
     // one (kv head, chunk) item per workgroup, all of them resident (the
     // chunks of a kv head wait for each other before merging)
     if ((uint64_t)a->nkv * a->n_chunks > blocks)
@@ -409,8 +413,9 @@ int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, vo
     if (a->part || a->count)
         return set_error(SINTER_ERR_ARG, "attn_noalloc: part and count must be NULL (the library supplies them)");
     if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
-        a->rope_dims > a->hd || a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc))
-        return set_error(SINTER_ERR_ARG, "attn_noalloc: unsupported shape (hd=%u nq=%u nkv=%u)", a->hd, a->nq, a->nkv);
+        a->rope_dims > a->hd || a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
+        return set_error(SINTER_ERR_ARG, "attn_noalloc: unsupported shape or KV type (hd=%u nq=%u nkv=%u kv_type=%u)",
+                         a->hd, a->nq, a->nkv, a->kv_type);
     if ((uint64_t)a->nkv * a->n_chunks > blocks || blocks > PLAN_MAX_BLOCKS)
         return set_error(SINTER_ERR_ARG, "attn_noalloc: blocks (%u) must be >= nkv * n_chunks (%u) and <= %u", blocks,
                          a->nkv * a->n_chunks, PLAN_MAX_BLOCKS);
@@ -500,10 +505,14 @@ int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k
         if (!(type == SINTER_Q4_K || type == SINTER_Q6_K || type == SINTER_Q8_0 || type == SINTER_BF16 ||
               type == SINTER_F16 || type == SINTER_F32))
             return set_error(SINTER_ERR_ARG, "synth: type");
+    } else if (kind == SINTER_SYN_NORMAL_Q8_0) {
+        if (k % 32) return set_error(SINTER_ERR_ARG, "synth: q8_0 k must be a multiple of 32");
     } else if (kind != SINTER_SYN_NORMAL && kind != SINTER_SYN_UNIFORM && kind != SINTER_SYN_NORMAL_F16) {
         return set_error(SINTER_ERR_ARG, "synth: kind");
     }
-    const uint64_t n_units = weight ? (uint64_t)rows * (uint64_t)(k / 256) : (uint64_t)rows * (uint64_t)k;
+    const uint64_t n_units = weight ? (uint64_t)rows * (uint64_t)(k / 256)
+                           : kind == SINTER_SYN_NORMAL_Q8_0 ? (uint64_t)rows * (uint64_t)(k / 32)
+                           : (uint64_t)rows * (uint64_t)k;
     if (dev) {
         if (!hip_ok(launch_synth(dst, kind, type, n_units, seed, a, b, (hipStream_t)stream), "synth launch"))
             return SINTER_ERR_HIP;
@@ -523,6 +532,8 @@ int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k
                     reinterpret_cast<float *>(d)[i] = a + b * sx_normal(seed, i);
                 } else if (kind == SINTER_SYN_UNIFORM) {
                     reinterpret_cast<float *>(d)[i] = a + (b - a) * sx_unit(seed, i);
+                } else if (kind == SINTER_SYN_NORMAL_Q8_0) {
+                    sx_q8_0_normal_block(seed, i, b, d + i * 34);
                 } else {
                     reinterpret_cast<uint16_t *>(d)[i] = sx_f2h(b * sx_normal(seed, i));
                 }

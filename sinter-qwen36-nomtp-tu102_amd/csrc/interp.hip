@@ -274,6 +274,8 @@ extern "C" __global__ void sinter_synth_kernel(uint8_t *dst, int kind, int type,
         reinterpret_cast<float *>(dst)[i] = a + (b - a) * sx_unit(seed, i);
     } else if (kind == SINTER_SYN_NORMAL_F16) {
         reinterpret_cast<uint16_t *>(dst)[i] = sx_f2h(b * sx_normal(seed, i));
+    } else if (kind == SINTER_SYN_NORMAL_Q8_0) {
+        sx_q8_0_normal_block(seed, i, b, dst + i * 34);
     }
 }
 

@@ -269,8 +269,9 @@ void push_mixer(sinter_model *m, int il, bool embed) {
         a.v = m->vv;
         a.q_norm = (const float *)w[S_Q_NORM].d;
         a.k_norm = (const float *)w[S_K_NORM].d;
-        a.kc = (uint16_t *)m->S[il][0].d;
-        a.vc = (uint16_t *)m->S[il][1].d;
+        a.kc = m->S[il][0].d;
+        a.vc = m->S[il][1].d;
+        a.kv_type = (uint32_t)c.t_kv;
         a.part = m->part;
         a.count = m->count;
         a.out = m->att;
@@ -394,6 +395,8 @@ int check_config(const sinter_model_config &c) {
     if (c.head_dim != 256 || c.attn_nkv < 1 || c.attn_nq % c.attn_nkv || c.attn_nq / c.attn_nkv > 8 ||
         c.rope_dims > c.head_dim || c.rope_dims % 2 || c.n_ctx < 1)
         return set_error(SINTER_ERR_ARG, "config: attention shape");
+    if (!(c.t_kv == 0 || c.t_kv == SINTER_F16 || c.t_kv == SINTER_Q8_0))
+        return set_error(SINTER_ERR_ARG, "config: KV cache type must be F16 or Q8_0");
     return SINTER_OK;
 }
 
@@ -422,6 +425,7 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
     if (rc) return rc;
     sinter_model *m = new sinter_model();
     m->cfg = *cfg;
+    if (m->cfg.t_kv == 0) m->cfg.t_kv = SINTER_F16;
     m->device = device;
     m->seed = seed;
     m->gg = gg;
@@ -454,8 +458,9 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
             ok = ok && make_vec(m, w[S_Q_NORM], "attn_q_norm", il, HD, SINTER_SYN_NORMAL, 1.0f, 0.02f);
             ok = ok && make_vec(m, w[S_K_NORM], "attn_k_norm", il, HD, SINTER_SYN_NORMAL, 1.0f, 0.02f);
             Tensor &K = m->S[il][0], &V = m->S[il][1];
-            K.bytes = V.bytes = (size_t)c.n_ctx * RW * 2;
-            K.type = V.type = SINTER_F16;
+            // f16, or Q8_0 blocks of 32 (34 bytes)
+            K.bytes = V.bytes = (size_t)c.n_ctx * (c.t_kv == SINTER_Q8_0 ? (size_t)RW / 32 * 34 : (size_t)RW * 2);
+            K.type = V.type = c.t_kv;
             ok = ok && (K.d = dalloc(m, K.bytes)) && (V.d = dalloc(m, V.bytes));
         } else {
             ok = ok && make_weight(m, w[S_QKV], "attn_qkv", il, c.t_default, C, E);
@@ -613,11 +618,14 @@ int sinter_model_synth_context(sinter_model *m, int32_t n_past, uint64_t seed) {
     for (int il = 0; il < c.n_layer; il++) {
         hipError_t e = hipSuccess;
         if (is_attn(c, il)) {
-            e = launch_synth(m->S[il][0].d, SINTER_SYN_NORMAL_F16, 0, (uint64_t)n_past * RW,
-                             sinter_seed(seed, "cache_k", il), 0.f, 1.0f, m->stream);
+            // f16 elements, or Q8_0 blocks of the same N(0,1) values
+            const bool q8 = c.t_kv == SINTER_Q8_0;
+            const int kind = q8 ? SINTER_SYN_NORMAL_Q8_0 : SINTER_SYN_NORMAL_F16;
+            const uint64_t units = (uint64_t)n_past * RW / (q8 ? 32u : 1u);
+            e = launch_synth(m->S[il][0].d, kind, 0, units, sinter_seed(seed, "cache_k", il), 0.f, 1.0f, m->stream);
             if (e == hipSuccess)
-                e = launch_synth(m->S[il][1].d, SINTER_SYN_NORMAL_F16, 0, (uint64_t)n_past * RW,
-                                 sinter_seed(seed, "cache_v", il), 0.f, 1.0f, m->stream);
+                e = launch_synth(m->S[il][1].d, kind, 0, units, sinter_seed(seed, "cache_v", il), 0.f, 1.0f,
+                                 m->stream);
         } else {
             e = launch_synth(m->S[il][0].d, SINTER_SYN_NORMAL, 0, m->S[il][0].bytes / 4,
                              sinter_seed(seed, "conv_state", il), 0.f, 1.0f, m->stream);

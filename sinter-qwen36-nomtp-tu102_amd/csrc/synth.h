@@ -157,6 +157,23 @@ SX_HD inline uint32_t sx_group_bytes(int type) {
     }
 }
 
+// Q8_0 block b of std * N(0,1) values (elements 32b .. 32b+31), quantised
+// as ggml's quantize_row_q8_0_ref: d = amax / 127, id = d ? 1/d : 0,
+// q = roundf(x * id), d stored as f16.  34 bytes.
+SX_HD inline void sx_q8_0_normal_block(uint64_t seed, uint64_t b, float std, uint8_t *out /*34*/) {
+    float x[32], amax = 0.0f;
+    for (int l = 0; l < 32; l++) {
+        x[l] = std * sx_normal(seed, b * 32 + (uint64_t)l);
+        amax = fmaxf(amax, fabsf(x[l]));
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = sx_f2h(d);
+    out[0] = (uint8_t)(dh & 0xff);
+    out[1] = (uint8_t)(dh >> 8);
+    for (int l = 0; l < 32; l++) out[2 + l] = (uint8_t)(int8_t)roundf(x[l] * id);
+}
+
 // Fill weight group b (256 elements) of a tensor of `type`.
 SX_HD inline void sx_weight_group(uint64_t seed, uint64_t b, int type, bool cfg1, uint8_t *out) {
     switch (type) {

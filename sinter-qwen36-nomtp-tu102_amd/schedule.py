@@ -467,6 +467,7 @@ def pack(model, prog):
             a.theta_scale = float(np.float32(math.pow(float(np.float32(cfg.rope_base)), -2.0 / cfg.rope_dims)))
             a.eps = cfg.eps
             a.scale = float(np.float32(1.0) / np.sqrt(np.float32(cfg.head_dim)))
+            a.kv_type = cfg.t_kv or sinter.F16
         C.memmove(o.payload, C.byref(a), C.sizeof(a))
     return out
 

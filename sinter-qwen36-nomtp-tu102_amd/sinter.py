@@ -17,7 +17,7 @@ OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range
 BENCH_GEMV, BENCH_GDN, BENCH_ATTN = 1, 2, 3
 PRO_PLAIN, PRO_RMSNORM, PRO_GATED, PRO_EMBED, PRO_GATED_G = range(5)
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_ARGMAX, EPI_CONV, EPI_SILU = range(6)
-SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16 = range(5)
+SYN_WEIGHT, SYN_Q8_0_CFG1, SYN_NORMAL, SYN_UNIFORM, SYN_NORMAL_F16, SYN_NORMAL_Q8_0 = range(6)
 OK, ERR_ARG, ERR_HIP, ERR_DEVICE, ERR_TIMEOUT, ERR_STATE, ERR_NOMEM = 0, -1, -2, -3, -4, -5, -6
 RUN_OK, RUN_ERR, RUN_TIMEOUT = 0, 1, 2
 E_NONE, E_BAD_KIND, E_UNWIRED_KIND, E_BAD_SHAPE, E_TIMEOUT_BARRIER = 0, 1, 2, 3, 5
@@ -62,7 +62,7 @@ class AttnArgs(C.Structure):
                 ("part", vp), ("count", vp), ("out", vp), ("pass_cell", vp),
                 ("nq", C.c_uint32), ("nkv", C.c_uint32), ("hd", C.c_uint32), ("rope_dims", C.c_uint32),
                 ("n_ctx", C.c_uint32), ("n_chunks", C.c_uint32), ("theta_scale", C.c_float),
-                ("eps", C.c_float), ("scale", C.c_float), ("_pad", C.c_uint32)]
+                ("eps", C.c_float), ("scale", C.c_float), ("kv_type", C.c_uint32)]
 
 
 class GgufTensor(C.Structure):
@@ -80,15 +80,17 @@ class ModelConfig(C.Structure):
                 ("conv_k", C.c_int32), ("attn_nq", C.c_int32), ("attn_nkv", C.c_int32),
                 ("head_dim", C.c_int32), ("rope_dims", C.c_int32), ("rope_base", C.c_float),
                 ("eps", C.c_float), ("n_ctx", C.c_int32), ("t_default", C.c_int32), ("t_attn_v", C.c_int32),
-                ("t_ffn_down", C.c_int32), ("t_output", C.c_int32), ("t_embd", C.c_int32)]
+                ("t_ffn_down", C.c_int32), ("t_output", C.c_int32), ("t_embd", C.c_int32), ("t_kv", C.c_int32)]
 
 
 assert C.sizeof(Instr) == 256 and C.sizeof(GemvSeg) == 40
 assert C.sizeof(GemvArgs) == 224 and C.sizeof(GdnArgs) == 80 and C.sizeof(AttnArgs) == 128
 
 
-def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64):
-    """The 27B-shaped hybrid: 48 gated-DeltaNet + 16 attention layers."""
+def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64, kv="f16"):
+    """The 27B-shaped hybrid: 48 gated-DeltaNet + 16 attention layers; KV
+    cache f16 or q8_0."""
+    tkv = {"f16": F16, "q8_0": Q8_0}[kv]
     if quant == "q4_k_m":
         td, tv, tdown, tout, temb = Q4_K, Q6_K, Q6_K, Q6_K, Q4_K
     elif quant == "bf16":
@@ -98,7 +100,7 @@ def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64):
     return ModelConfig(n_layer=n_layer, attn_every=4, n_embd=5120, n_ff=17408, n_vocab=151936,
                        gdn_hk=16, gdn_hv=32, gdn_d=128, conv_k=4, attn_nq=24, attn_nkv=4, head_dim=256,
                        rope_dims=64, rope_base=1e7, eps=1e-6, n_ctx=n_ctx, t_default=td, t_attn_v=tv,
-                       t_ffn_down=tdown, t_output=tout, t_embd=temb)
+                       t_ffn_down=tdown, t_output=tout, t_embd=temb, t_kv=tkv)
 
 
 _lib = None

@@ -124,6 +124,21 @@ def test_host_synth_is_deterministic_and_scaled(sn, orc):
     assert s1 == L.sinter_seed(1, b"ffn_up", 3)
 
 
+def test_q8_0_cache_synth_is_the_oracle_quantisation_of_the_normal_synth(sn, orc):
+    """SYN_NORMAL_Q8_0 (the synthetic Q8_0 KV cache) = ggml's reference q8_0
+    quantiser applied to the SYN_NORMAL values of the same seed."""
+    L = sn.lib()
+    rows, k = 13, 1024
+    q = np.zeros(rows * k // 32 * 34, np.uint8)
+    assert L.sinter_synth(0, q.ctypes.data, sn.SYN_NORMAL_Q8_0, 0, rows, k, 31, 0.0, 1.0, None) == 0
+    x = np.zeros(rows * k, np.float32)
+    assert L.sinter_synth(0, x.ctypes.data, sn.SYN_NORMAL, 0, 1, x.size, 31, 0.0, 1.0, None) == 0
+    ref = np.zeros_like(q)
+    orc.lib().or_quant_q8_0_ref(x.ctypes.data, ref.ctypes.data, x.size)
+    assert np.array_equal(q, ref)
+    assert L.sinter_synth(0, q.ctypes.data, sn.SYN_NORMAL_Q8_0, 0, 1, 100, 31, 0.0, 1.0, None) == sn.ERR_ARG
+
+
 def test_cfg1_q8_0_synth_matches_config(sn, orc):
     """config 1: int8 codes uniform in [-127,127], f16 scale |N(0,0.02)|"""
     L = sn.lib()

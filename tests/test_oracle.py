@@ -137,6 +137,75 @@ def test_q8_0_quantizer_invariants(orc):
             assert np.array_equal(qs[i], np.rint(xb * (np.float32(127) / np.float32(amax))).astype(np.int64))
 
 
+def test_q8_0_ref_quantizer_known_answers(orc):
+    """ggml's reference Q8_0 form (the KV cache's): id = 1/d, codes rounded
+    half away from zero -- where the x86 form (id = 127/amax, half to even)
+    differs, this one must be taken."""
+    x = np.zeros(96, np.float32)
+    x[0], x[1], x[2], x[3] = 127.0, 62.5, -62.5, -127.0      # d = 1: ties at +-62.5
+    x[64:96] = (np.random.default_rng(8).standard_normal(32) * 0.37).astype(np.float32)
+    y = np.zeros(3 * 34, np.uint8)
+    orc.lib().or_quant_q8_0_ref(P(x), P(y), 96)
+    b = y.reshape(3, 34)
+    d = b[:, :2].copy().view(np.float16)[:, 0]
+    qs = b[:, 2:].view(np.int8).astype(np.int64)
+    assert d[0] == 1.0 and list(qs[0, :4]) == [127, 63, -63, -127] and not qs[0, 4:].any()
+    assert d[1] == 0 and not qs[1].any()                      # an all-zero block
+    xb = x[64:96].astype(np.float64)
+    amax = np.abs(xb).max()
+    df = np.float32(np.float32(amax) / np.float32(127))
+    assert d[2] == np.float16(df)
+    assert np.abs(qs[2]).max() == 127 and qs[2][np.argmax(np.abs(xb))] * np.sign(xb[np.argmax(np.abs(xb))]) == 127
+    # each code is the nearest integer to x / d (d before its f16 rounding)
+    assert np.all(np.abs(qs[2] - xb / float(df)) <= 0.5 + 1e-6)
+    # where 1/d and 127/amax give different codes, the 1/d one is taken
+    rng = np.random.default_rng(9)
+    found = 0
+    for _ in range(2000):
+        xs = (rng.standard_normal(32) * rng.uniform(0.01, 10)).astype(np.float32)
+        am = np.float32(np.abs(xs).max())
+        dd = np.float32(am / np.float32(127))
+        a_ = np.trunc(xs * (np.float32(1) / dd) + np.copysign(np.float32(0.5), xs))      # roundf(x / d form)
+        b_ = np.rint(xs * (np.float32(127) / am))
+        if np.array_equal(a_, b_):
+            continue
+        found += 1
+        yy = np.zeros(34, np.uint8)
+        orc.lib().or_quant_q8_0_ref(P(xs), P(yy), 32)
+        assert np.array_equal(yy[2:].view(np.int8).astype(np.float32), a_.astype(np.float32))
+    assert found > 0
+
+
+def test_attention_over_q8_0_cache_equals_dequantised_f32(orc):
+    """or_attn_decode_kv over a Q8_0 cache equals the float64 reference over
+    the dequantised cache (codes times block scales)."""
+    rng = np.random.default_rng(19)
+    nq, nkv, hd, n = 6, 2, 256, 130
+    q = rng.standard_normal((nq, hd)).astype(np.float32)
+    kf = rng.standard_normal((n, nkv * hd)).astype(np.float32)
+    vf = rng.standard_normal((n, nkv * hd)).astype(np.float32)
+    K = np.zeros((n, nkv * hd // 32 * 34), np.uint8)
+    V = np.zeros_like(K)
+    for j in range(n):
+        orc.lib().or_quant_q8_0_ref(P(kf[j]), P(K[j]), nkv * hd)
+        orc.lib().or_quant_q8_0_ref(P(vf[j]), P(V[j]), nkv * hd)
+
+    def deq(c):
+        b = c.reshape(n, -1, 34)
+        d = b[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float64)
+        return (b[:, :, 2:].view(np.int8).astype(np.float64) * d[..., None]).reshape(n, -1)
+    out = np.zeros((nq, hd), np.float32)
+    orc.lib().or_attn_decode_kv(P(q), P(K), P(V), Q8_0, n, nq, nkv, hd, 0.0625, P(out))
+    ref = R.attn64(q.astype(np.float64), deq(K), deq(V), nq, nkv, hd, 0.0625)
+    assert np.allclose(out, ref, rtol=1e-6, atol=1e-7)
+    # and over an f16 cache it is or_attn_decode exactly
+    Kh, Vh = kf.astype(np.float16), vf.astype(np.float16)
+    o1, o2 = np.zeros((nq, hd), np.float32), np.zeros((nq, hd), np.float32)
+    orc.lib().or_attn_decode_kv(P(q), P(Kh), P(Vh), 1, n, nq, nkv, hd, 0.0625, P(o1))
+    orc.lib().or_attn_decode(P(q), P(Kh), P(Vh), n, nq, nkv, hd, nkv * hd, 0.0625, P(o2))
+    assert np.array_equal(o1, o2)
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0])
 def test_block_term_equals_float64_dequant_dot(orc, sn, t):
     """integer-sum block term == float64 dequantise-then-dot (different
