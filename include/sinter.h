@@ -361,6 +361,25 @@ int  sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *log
 /* n greedy passes from (token, pos) in one launch */
 int  sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
                          int32_t *tokens_out);
+/* A model over caller-owned device memory (the drop-in path: a host
+ * framework's weight, KV-cache and recurrent-state tensors, by raw pointer;
+ * k0/harness.cpp:589-628 resolves program names to pointers the same way).
+ * The model allocates only its activations, scratch and control cells and
+ * never frees or fills the bound buffers. */
+typedef struct sinter_model_bindings {
+    void *const *tensors;    /* [n_layer * 16 + 3] device pointers, numbered as sinter_model_tensor_info
+                                (16-byte aligned; null for slots the layer kind lacks, and for the
+                                embedding when embed_outside) */
+    const int32_t *types;    /* the same count: each weight's sinter_type (vectors SINTER_F32) */
+    void *const *states;     /* [n_layer * 2]: conv / recurrent state (GDN layers), K / V cache
+                                (attention layers) in the sizes sinter_model_state_info reports */
+    float *logits;           /* n_vocab floats the head writes (null: the model allocates them) */
+    uint32_t embed_outside;  /* 1: the pass starts from the embedded row (n_embd floats) the caller
+                                writes into the "X" buffer (sinter_model_buffer) before it */
+    uint32_t _pad;
+} sinter_model_bindings;
+int  sinter_model_create_bound(const sinter_model_config *cfg, int device, uint32_t blocks,
+                               const sinter_model_bindings *b, sinter_model **out);
 /* Prefill on the GPU: tokens[0..n) at positions pos0.. through the decode
  * passes (KV rows and recurrent state written exactly as decoding them one by
  * one would), the greedy continuation of the last one in *next_token (may be

@@ -916,16 +916,17 @@ __device__ __forceinline__ Run make_run(cplan_t *pl, uint32_t s, uint32_t lo, ui
 // to DPRO during the prologue (issued behind its activation DMAs), the rest
 // when the body starts -- at most PF_PRE registers of 16 B stay live through
 // the prologue.  Measured on the 27B decode: one more Q4_K slot in the body
-// (D = 4) is 1 % faster; moving a slot from across the barrier to the
+// (D = 4) is 1 % faster, a third Q6_K slot 0.4 %; a fourth Q4_K slot across
+// the barrier (DPRE = 4) is 0.6 % slower; moving a slot from across the barrier to the
 // prologue (DPRE < DPRO), or more slots live through the prologue (which
 // then spill), is slower -- loads issued behind the activation DMAs delay
 // the activation reads of the workgroups released later.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
 // 4-aligned address at or below it: every byte read lies in
 // [block - 2, block + 210), never past the end of the weights.
-constexpr int PF_MAX = 36, PF_PRE = 28;
+constexpr int PF_MAX = 42, PF_PRE = 28;
 template <int T> struct TypeCfg;
 template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 4, DPRE = 3, DPRO = 3; };
-template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 2, DPRE = 2, DPRO = 2; };
+template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 3, DPRE = 2, DPRO = 2; };
 template <> struct TypeCfg<SINTER_Q8_0> { static constexpr int NI = 17, IB = 272, D = 2, DPRE = 1, DPRO = 1; };
 template <> struct TypeCfg<SINTER_BF16> { static constexpr int NI = 8, IB = 128, D = 4, DPRE = 3, DPRO = 3; };
 template <> struct TypeCfg<SINTER_F32> { static constexpr int NI = 16, IB = 256, D = 2, DPRE = 1, DPRO = 1; };

@@ -86,6 +86,8 @@ struct sinter_model {
     std::vector<void *> allocs;
     uint64_t seed = 0;
     sinter_gguf *gg = nullptr;   // weights come from this file when set (else synthesised)
+    const sinter_model_bindings *ext = nullptr;   // caller-owned weights and state (creation only)
+    bool embed_outside = false;  // the caller writes the embedded row into X before each pass
 };
 
 namespace {
@@ -144,7 +146,42 @@ bool upload(sinter_model *m, Tensor &t, int64_t gi) {
     return hip_ok(hipMemcpyAsync(t.d, g.data, t.bytes, hipMemcpyHostToDevice, m->stream), "gguf upload");
 }
 
+// A recurrent-state or KV-cache buffer: allocated (zeroed), or the caller's.
+bool state_buffer(sinter_model *m, Tensor &t, int il, int s) {
+    if (!m->ext) return (t.d = dalloc(m, t.bytes)) != nullptr;
+    t.d = m->ext->states ? m->ext->states[(size_t)il * 2 + s] : nullptr;
+    if (!t.d || (reinterpret_cast<uintptr_t>(t.d) & 15u)) {
+        set_error(SINTER_ERR_ARG, "bound model: state %d of layer %d null or unaligned", s, il);
+        return false;
+    }
+    return true;
+}
+
+// A bound model's pointer and type for tensor t of layer il (-1: the
+// globals embd / onorm / output), numbered as sinter_model_tensor_info.
+size_t ext_index(const sinter_model *m, const Tensor &t, int il) {
+    if (il >= 0) return (size_t)il * NSLOT + (size_t)(&t - m->W[il].data());
+    return (size_t)m->cfg.n_layer * NSLOT + (&t == &m->embd ? 0u : &t == &m->onorm ? 1u : 2u);
+}
+
+bool bind(sinter_model *m, Tensor &t, int il, int type, int64_t rows, int64_t k) {
+    const size_t i = ext_index(m, t, il);
+    t.d = m->ext->tensors[i];
+    t.type = m->ext->types ? m->ext->types[i] : type;
+    t.rows = rows;
+    t.k = k;
+    t.bytes = sinter_row_bytes_dev(t.type, k) * (size_t)rows;
+    if (!t.d || (reinterpret_cast<uintptr_t>(t.d) & 15u) || t.bytes == 0) {
+        set_error(SINTER_ERR_ARG, "bound model: tensor %zu (layer %d) null, unaligned or of a type the kernels do "
+                  "not read", i, il);
+        return false;
+    }
+    m->weight_bytes += t.bytes;
+    return true;
+}
+
 bool make_weight(sinter_model *m, Tensor &t, const char *name, int il, int type, int64_t rows, int64_t k) {
+    if (m->ext) return bind(m, t, il, type, rows, k);
     int64_t gi = -1;
     if (m->gg) {
         if ((gi = gguf_lookup(m, name, il, rows, k, false)) < 0) return false;
@@ -165,6 +202,8 @@ bool make_weight(sinter_model *m, Tensor &t, const char *name, int il, int type,
 }
 
 bool make_vec(sinter_model *m, Tensor &t, const char *name, int il, int64_t n, int kind, float a, float b) {
+    if (m->ext) return bind(m, t, il, SINTER_F32, 1, n) && (t.type == SINTER_F32 ||
+                                                            (set_error(SINTER_ERR_ARG, "bound model: vector not f32"), false));
     int64_t gi = -1;
     if (m->gg && (gi = gguf_lookup(m, name, il, 1, n, true)) < 0) return false;
     t.type = SINTER_F32;
@@ -369,7 +408,7 @@ void build_program(sinter_model *m) {
     m->prog.clear();
     m->n_boundaries = 0;
     for (int il = 0; il < c.n_layer; il++) {
-        push_mixer(m, il, il == 0);
+        push_mixer(m, il, il == 0 && !m->embed_outside);
         push_ffn(m, il);
     }
     // head: final norm, logits, greedy argmax
@@ -418,7 +457,7 @@ void sinter_model_destroy(sinter_model *m) {
 
 // Allocate, fill (synthesise, or upload from gg) and program a model.
 static int model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks, sinter_gguf *gg,
-                        sinter_model **out) {
+                        sinter_model **out, const sinter_model_bindings *ext = nullptr) {
     if (!cfg || !out) return set_error(SINTER_ERR_ARG, "model: null argument");
     *out = nullptr;
     int rc = check_config(*cfg);
@@ -429,7 +468,9 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
     m->device = device;
     m->seed = seed;
     m->gg = gg;
-    auto fail = [&](int st) { m->gg = nullptr; sinter_model_destroy(m); return st; };
+    m->ext = ext;
+    m->embed_outside = ext && ext->embed_outside;
+    auto fail = [&](int st) { m->gg = nullptr; m->ext = nullptr; sinter_model_destroy(m); return st; };
     if ((rc = sinter_host_init(&m->host, device, 1024)) != SINTER_OK) return fail(rc);
     uint32_t hb = 0;
     sinter_host_grid(m->host, &hb, nullptr, nullptr);
@@ -461,7 +502,7 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
             // f16, or Q8_0 blocks of 32 (34 bytes)
             K.bytes = V.bytes = (size_t)c.n_ctx * (c.t_kv == SINTER_Q8_0 ? (size_t)RW / 32 * 34 : (size_t)RW * 2);
             K.type = V.type = c.t_kv;
-            ok = ok && (K.d = dalloc(m, K.bytes)) && (V.d = dalloc(m, V.bytes));
+            ok = ok && state_buffer(m, K, il, 0) && state_buffer(m, V, il, 1);
         } else {
             ok = ok && make_weight(m, w[S_QKV], "attn_qkv", il, c.t_default, C, E);
             ok = ok && make_weight(m, w[S_Z], "attn_gate", il, c.t_default, VD, E);
@@ -476,10 +517,10 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
             cs.bytes = (size_t)C * (c.conv_k - 1) * 4;
             ss.bytes = (size_t)HV * D * D * 4;
             cs.type = ss.type = SINTER_F32;
-            ok = ok && (cs.d = dalloc(m, cs.bytes)) && (ss.d = dalloc(m, ss.bytes));
+            ok = ok && state_buffer(m, cs, il, 0) && state_buffer(m, ss, il, 1);
         }
     }
-    ok = ok && make_weight(m, m->embd, "token_embd", -1, c.t_embd, c.n_vocab, E);
+    if (!m->embed_outside) ok = ok && make_weight(m, m->embd, "token_embd", -1, c.t_embd, c.n_vocab, E);
     ok = ok && make_vec(m, m->onorm, "output_norm", -1, E, SINTER_SYN_NORMAL, 1.0f, 0.02f);
     // a GGUF without output.weight ties the head to the embedding
     const bool tied = gg && sinter_gguf_find(gg, "output.weight") < 0;
@@ -487,16 +528,19 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
     auto fa = [&](size_t n) { return (float *)dalloc(m, n * 4); };
     ok = ok && (m->X = fa(E)) && (m->H = fa(E)) && (m->qkv = fa(C)) && (m->z = fa(VD)) && (m->al = fa(HV)) &&
          (m->be = fa(HV)) && (m->o = fa(VD)) && (m->ffn = fa(F)) && (m->qg = fa((size_t)NQ * 2 * HD)) &&
-         (m->kk = fa(RW)) && (m->vv = fa(RW)) && (m->att = fa((size_t)NQ * HD)) && (m->logits = fa(c.n_vocab));
+         (m->kk = fa(RW)) && (m->vv = fa(RW)) && (m->att = fa((size_t)NQ * HD)) &&
+         (m->logits = ext && ext->logits ? ext->logits : fa(c.n_vocab));
     const uint32_t chunks = attn_chunks(m->blocks, NKV);
     ok = ok && (m->part = (double *)dalloc(m, sinter_attn_part_len(NQ, NKV, HD, chunks) * 8));
     ok = ok && (m->count = (unsigned *)dalloc(m, (size_t)sinter_attn_count_len(NKV, chunks) * 4));
     if (!ok) {
         if (gg && std::strncmp(sinter_last_error(), "gguf", 4) == 0) return fail(SINTER_ERR_ARG);
+        if (ext && std::strncmp(sinter_last_error(), "bound model", 11) == 0) return fail(SINTER_ERR_ARG);
         return fail(set_error(SINTER_ERR_NOMEM, "model: device allocation or synthesis failed"));
     }
     if (!hip_ok(hipStreamSynchronize(m->stream), "model synthesis")) return fail(SINTER_ERR_HIP);
     m->gg = nullptr;   // every byte is on the device now; the caller owns the file
+    m->ext = nullptr;  // (the bound pointers live on in the tensors)
     uint32_t hcap = 0;
     int32_t *hist = sinter_host_history(m->host, &hcap);
     if ((rc = sinter_argmax_ws_create(m->blocks, &sinter_host_pass_cell(m->host)->token, hist, hcap, &m->ws)))
@@ -590,6 +634,12 @@ extern "C" {
 int sinter_model_create(const sinter_model_config *cfg, int device, uint64_t seed, uint32_t blocks,
                         sinter_model **out) {
     return model_create(cfg, device, seed, blocks, nullptr, out);
+}
+
+int sinter_model_create_bound(const sinter_model_config *cfg, int device, uint32_t blocks,
+                              const sinter_model_bindings *b, sinter_model **out) {
+    if (!b || !b->tensors) return set_error(SINTER_ERR_ARG, "bound model: no bindings");
+    return model_create(cfg, device, 0, blocks, nullptr, out, b);
 }
 
 int sinter_model_config_from_gguf(sinter_gguf *g, int32_t n_ctx, sinter_model_config *cfg) {
@@ -699,6 +749,8 @@ int sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logi
 int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n, int32_t *tokens_out) {
     if (!m || pos < 0 || (int64_t)pos + n > m->cfg.n_ctx || token < 0 || token >= m->cfg.n_vocab)
         return set_error(SINTER_ERR_ARG, "greedy: token/pos/n out of range");
+    if (m->embed_outside && n > 1)
+        return set_error(SINTER_ERR_STATE, "greedy: the caller embeds each token (one pass per call)");
     int rc = sinter_host_set_pos(m->host, pos);
     if (rc) return rc;
     const int rs = sinter_host_run_passes(m->host, token, n, tokens_out, 600000.0);
@@ -709,6 +761,7 @@ int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
 int sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0, int32_t *next_token) {
     if (!m || !tokens || n == 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.n_ctx)
         return set_error(SINTER_ERR_ARG, "prefill: tokens / n / pos0 out of range");
+    if (m->embed_outside) return set_error(SINTER_ERR_STATE, "prefill: the caller embeds each token");
     for (uint32_t i = 0; i < n; i++)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.n_vocab) return set_error(SINTER_ERR_ARG, "prefill: token %u out of range", i);
     uint32_t cap = 0;

@@ -65,6 +65,11 @@ class AttnArgs(C.Structure):
                 ("eps", C.c_float), ("scale", C.c_float), ("kv_type", C.c_uint32)]
 
 
+class ModelBindings(C.Structure):
+    _fields_ = [("tensors", C.POINTER(vp)), ("types", C.POINTER(C.c_int32)), ("states", C.POINTER(vp)),
+                ("logits", vp), ("embed_outside", C.c_uint32), ("_pad", C.c_uint32)]
+
+
 class GgufTensor(C.Structure):
     _fields_ = [("name", C.c_char_p), ("type", C.c_uint32), ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 4),
                 ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("data", vp)]
@@ -166,6 +171,7 @@ def lib():
         "sinter_model_decode": (I, [vp, C.c_int32, C.c_int32, vp, C.POINTER(C.c_int32)]),
         "sinter_model_greedy": (I, [vp, C.c_int32, C.c_int32, U32, C.POINTER(C.c_int32)]),
         "sinter_model_prefill": (I, [vp, C.POINTER(C.c_int32), U32, C.c_int32, C.POINTER(C.c_int32)]),
+        "sinter_model_create_bound": (I, [C.POINTER(ModelConfig), I, U32, C.POINTER(ModelBindings), C.POINTER(vp)]),
         "sinter_model_synth_context": (I, [vp, C.c_int32, U64]),
         "sinter_model_logits": (I, [vp, vp]),
         "sinter_model_tensor_info": (I, [vp, I64, I, C.POINTER(vp), C.POINTER(C.c_size_t), C.POINTER(I)]),
@@ -284,9 +290,19 @@ class Gguf:
 class Model:
     """Owner of a sinter_model handle."""
 
-    def __init__(self, cfg, seed=1, device=0, blocks=0, gguf=None):
+    def __init__(self, cfg, seed=1, device=0, blocks=0, gguf=None, bindings=None):
+        """bindings: (tensors, types, states, logits, embed_outside) -- device
+        pointers the model runs over without owning them (sinter_model_bindings)."""
         h = vp()
-        if gguf is not None:
+        if bindings is not None:
+            tensors, types, states, logits, embed_outside = bindings
+            self._bind = (
+                (vp * len(tensors))(*tensors), (C.c_int32 * len(types))(*types), (vp * len(states))(*states))
+            b = ModelBindings(tensors=self._bind[0], types=self._bind[1], states=self._bind[2], logits=logits,
+                              embed_outside=1 if embed_outside else 0)
+            check(lib().sinter_model_create_bound(C.byref(cfg), device, blocks, C.byref(b), C.byref(h)),
+                  "model_create_bound")
+        elif gguf is not None:
             check(lib().sinter_model_create_from_gguf(gguf.h, device, cfg.n_ctx, blocks, C.byref(h)),
                   "model_create_from_gguf")
             cfg = ModelConfig()
@@ -360,6 +376,12 @@ class Model:
 
     def host(self):
         return lib().sinter_model_host(self.h)
+
+    def buffer(self, name):
+        """(device pointer, bytes) of one of the model's own buffers (X, H, logits, ...)."""
+        p, nb = vp(), C.c_size_t()
+        check(lib().sinter_model_buffer(self.h, name.encode(), C.byref(p), C.byref(nb)), "buffer " + name)
+        return p.value, nb.value
 
     def program(self):
         """A copy of the model's uploaded program (sinter_instr records)."""
