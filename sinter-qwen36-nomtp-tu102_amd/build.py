@@ -120,5 +120,34 @@ def build(verbose=False):
     return LIB
 
 
+GGML_SHIM_SRC = os.path.join(HERE, "ggml_backend", "sinter_ggml.cpp")
+GGML_SHIM_LIB = os.path.join(HERE, "ggml_backend", "libsinter_ggml.so")
+
+
+def build_ggml_shim(verbose=False):
+    """The ggml dynamic backend (ggml_backend/sinter_ggml.cpp), only when a
+    ggml tree is named: SINTER_GGML_INCLUDE (the directory holding
+    ggml-backend-impl.h and ggml.h) and SINTER_GGML_LIB (holding
+    libggml-base.so).  Returns the library path, or None when not asked for
+    -- no ggml tree ships with this repository, so by default it is skipped."""
+    inc, libdir = os.environ.get("SINTER_GGML_INCLUDE"), os.environ.get("SINTER_GGML_LIB")
+    if not inc:
+        return None
+    if not os.path.exists(os.path.join(inc, "ggml-backend-impl.h")):
+        raise RuntimeError(f"SINTER_GGML_INCLUDE={inc} has no ggml-backend-impl.h")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-I", inc,
+           "-I", os.path.join(os.path.dirname(HERE), "include"), GGML_SHIM_SRC, "-o", GGML_SHIM_LIB,
+           "-L", HERE, "-lsinter", "-Wl,-rpath," + HERE]
+    if libdir:
+        cmd += ["-L", libdir, "-lggml-base", "-Wl,-rpath," + libdir]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("ggml shim build failed:\n" + r.stdout + r.stderr)
+    return GGML_SHIM_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_ggml_shim(verbose="-v" in sys.argv) or "ggml shim: skipped (SINTER_GGML_INCLUDE not set)")
