@@ -104,71 +104,66 @@ __shared__ uint32_t g_att_key[6];
 constexpr uint32_t ATT_NO_CACHE = 0xffffffffu;
 
 // The q heads of a kv group (and, for the chunk that appends, the new k row)
-// normalised and rotated together: y = rmsnorm(x) * w per 256-wide head, then
-// NEOX RoPE on the first rope_dims dims.  Thread t holds dim t of every head.
-// Per-head sums of squares are reduced like block_sum_f64 (DPP rows, the four
-// row sums of a wave, then the waves in order), all heads at once, so the
-// whole prologue costs three workgroup barriers.  Rope pair i turns by
-// theta_i = pos * theta_scale^i (repeated fp32 products, as ggml's rope
-// cache), cos/sin evaluated in double and rounded to fp32.
-// x[j] for j < nh are the raw values; rows j < nq use qw (this thread's
-// element of the q norm weight), row nq (if nh > nq) uses kw.  Results land
-// in dst[j*256 + t].  LDS: qn [ATT_MAXG+1][256]
-// floats, rot [2][128] floats, red [5][ATT_MAXG+1] doubles.
-__device__ __forceinline__ void att_prep(const float x[ATT_MAXG + 1], uint32_t nq, uint32_t nh, float qw, float kw,
-                                         float eps, int pos, float theta_scale, uint32_t rope_dims,
-                                         LDS float *dst, LDS float *qn, LDS float *rot, LDS double *red,
-                                         bool compute_rot) {
-    const uint32_t t = tid(), half = rope_dims / 2;
-    // cos on wave 0, sin on wave 1 (the two run side by side); skipped when
-    // rot already holds this position's rotation
-    const uint32_t ri = t < 64 ? t : t - 64;
-    if (compute_rot && t < 128 && ri < half) {
-        float th = (float)pos;
-        for (uint32_t i = 0; i < ri; i++) th *= theta_scale;
-        if (t < 64) rot[ri] = (float)cos((double)th);
-        else rot[128 + ri] = (float)sin((double)th);
+// normalised and rotated: y = rmsnorm(x) * w per 256-wide head, then NEOX
+// RoPE on the first rope_dims dims.  Wave w takes heads w, w + 4, ...; lane l
+// holds elements 4l .. 4l+3 of a head, so the head's sum of squares is the
+// lane's four fp32 squares added in fp64 in order, then a wave butterfly (no
+// workgroup barrier), and rope pair (i, i + rope_dims/2) lies in lanes i/4
+// and i/4 + rope_dims/8 at the same component (rope_dims a multiple of 8).
+// Rope pair i turns by theta_i = pos * theta_scale^i (repeated fp32
+// products, as ggml's rope cache), cos/sin evaluated in double and rounded
+// to fp32, into rot (cos | sin) -- only when compute_rot; otherwise rot
+// already holds this position's rotation.  Rows j < nq read their raw
+// values from src row j and use the q norm weight qw, row nq (if nh > nq)
+// the k norm weight kw; results land in dst row j.  Ends with a workgroup
+// barrier.
+__device__ __forceinline__ void att_prep(uint32_t nq, uint32_t nh, float eps, int pos, float theta_scale,
+                                         uint32_t rope_dims, const LDS float *src, const LDS float *qw,
+                                         const LDS float *kw, LDS float *dst, LDS float *rot, bool compute_rot) {
+    const uint32_t t = tid(), lane = t & 63u, w = t >> 6, half = rope_dims / 2, pl = half / 4;
+    if (compute_rot) {
+        // cos on wave 0, sin on wave 1 (the two run side by side)
+        const uint32_t ri = t < 64 ? t : t - 64;
+        if (t < 128 && ri < half) {
+            float th = (float)pos;
+            for (uint32_t i = 0; i < ri; i++) th *= theta_scale;
+            if (t < 64) rot[ri] = (float)cos((double)th);
+            else rot[128 + ri] = (float)sin((double)th);
+        }
+        __syncthreads();
     }
+    const uint32_t e0 = 4 * lane, partner = lane < pl ? lane + pl : lane - pl;
+    for (uint32_t j = w; j < nh; j += WAVES) {
+        const f32x4 x = *reinterpret_cast<const LDS f32x4 *>(src + j * 256 + e0);
+        const f32x4 wt = *reinterpret_cast<const LDS f32x4 *>((j < nq ? qw : kw) + e0);
+        double ss = (double)(x.x * x.x);
+        ss += (double)(x.y * x.y);
+        ss += (double)(x.z * x.z);
+        ss += (double)(x.w * x.w);
+        ss = wave_sum_f64(ss);
+        const float hs = 1.0f / sqrtf((float)(ss / 256.0) + eps);
+        const float xv[4] = {x.x, x.y, x.z, x.w}, wv[4] = {wt.x, wt.y, wt.z, wt.w};
+        float y[4], o[4];
 #pragma unroll
-    for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
-        if (j < nh) {
-            const double v = row16_sum_f64((double)(x[j] * x[j]));
-            const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
-            if ((t & 63u) == 0) red[(t >> 6) * (ATT_MAXG + 1) + j] = w;
+        for (uint32_t c = 0; c < 4; c++) {
+            const float nrm = xv[c] * hs;
+            y[c] = nrm * wv[c];
         }
-    }
-    __syncthreads();
-    // head j's scale on lane j (one sqrt/divide chain instead of nh in a row)
-    LDS float *hs = reinterpret_cast<LDS float *>(red + 4 * (ATT_MAXG + 1));
-    if (t < nh) {
-        double ss = 0.0;
-        for (int wv = 0; wv < (int)(BLOCK_THREADS / 64); wv++) ss += red[wv * (ATT_MAXG + 1) + t];
-        const float mean = (float)(ss / 256.0);
-        hs[t] = 1.0f / sqrtf(mean + eps);
-    }
-    __syncthreads();
 #pragma unroll
-    for (uint32_t j = 0; j < ATT_MAXG + 1; j++) {
-        if (j < nh) {
-            const float nrm = x[j] * hs[j];
-            qn[j * 256 + t] = nrm * (j < nq ? qw : kw);
+        for (uint32_t c = 0; c < 4; c++) o[c] = __shfl(y[c], (int)partner, 64);
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++) {
+            const uint32_t i = e0 + c;
+            if (i < half) {
+                const float a0 = y[c] * rot[i], a1 = o[c] * rot[128 + i];
+                y[c] = a0 - a1;
+            } else if (i < 2 * half) {
+                const float b0 = o[c] * rot[128 + i - half], b1 = y[c] * rot[i - half];
+                y[c] = b0 + b1;
+            }
         }
-    }
-    __syncthreads();
-    for (uint32_t j = 0; j < nh; j++) {
-        const LDS float *r = qn + j * 256;
-        float y = r[t];
-        if (t < half) {
-            const float x0 = r[t], x1 = r[t + half], c = rot[t], s = rot[128 + t];
-            const float a0 = x0 * c, a1 = x1 * s;
-            y = a0 - a1;
-        } else if (t < 2 * half) {
-            const uint32_t i = t - half;
-            const float x0 = r[i], x1 = r[t], c = rot[i], s = rot[128 + i];
-            const float b0 = x0 * s, b1 = x1 * c;
-            y = b0 + b1;
-        }
-        dst[j * 256 + t] = y;
+        const f32x4 r = {y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<LDS f32x4 *>(dst + j * 256 + e0) = r;
     }
     __syncthreads();
 }
@@ -245,7 +240,7 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     const uint32_t gqa = NKV ? NQ / NKV : 0;
     constexpr bool q8 = Q8;
     const bool ok = HD == 256 && NKV && NQ % NKV == 0 && gqa >= 1 && gqa <= ATT_MAXG && C >= 1 && C <= 64 &&
-                    NKV * C <= nblk && a.rope_dims <= HD && (a.rope_dims % 2) == 0 && pos >= 0 &&
+                    NKV * C <= nblk && a.rope_dims <= HD && (a.rope_dims % 8) == 0 && pos >= 0 &&
                     (uint32_t)pos < a.n_ctx && (q8 == (a.kv_type == SINTER_Q8_0));
     if (!ok) {
         if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
@@ -363,14 +358,9 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
         else if (behind == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else dma_wait();
         __syncthreads();
-        float xr[ATT_MAXG + 1];
-#pragma unroll
-        for (uint32_t hh = 0; hh <= ATT_MAXG; hh++) xr[hh] = hh < nraw && hh <= gqa ? qn[hh * 256 + t] : 0.0f;
         const float vraw = owner ? qn[(gqa + 1) * 256 + t] : 0.0f;
-        const float qwv = qn[(ATT_MAXG + 2) * 256 + t], kwv = qn[(ATT_MAXG + 3) * 256 + t];
-        __syncthreads();
-        att_prep(xr, gqa, owner ? gqa + 1 : gqa, qwv, kwv, a.eps, pos, a.theta_scale, a.rope_dims, qf, qn, rot, pred,
-                 !rot_cached);
+        att_prep(gqa, owner ? gqa + 1 : gqa, a.eps, pos, a.theta_scale, a.rope_dims, qn, qn + (ATT_MAXG + 2) * 256,
+                 qn + (ATT_MAXG + 3) * 256, qf, rot, !rot_cached);
         if (owner && !q8) vnew[t] = f2h(vraw);
         if (owner && q8) att_quant_q8_0(vraw, vnew8);
         // (att_prep ended with a workgroup barrier: every thread has read the key)
@@ -574,27 +564,27 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
         }
     }
 
-    // the merge's element mapping (below) and its gates, loaded before the
-    // wait: this workgroup finalises elements [c*ne, ...) of the head
-    // group's gqa*HD outputs, tpe threads per element
+    // the merge's element mapping: this workgroup finalises elements
+    // [c*ne, ...) of the head group's gqa*HD outputs, tpe threads per element
     const uint32_t E = gqa * HD, ne = (E + C - 1) / C, e0 = c * ne, e1 = min(e0 + ne, E);
     uint32_t tpe = 1;                           // a power of two <= C
     while (tpe * 2 <= C && tpe * 2 * ne <= BLOCK_THREADS) tpe *= 2;
     const uint32_t cpt = (C + tpe - 1) / tpe;   // chunks per thread
     const uint32_t ept = BLOCK_THREADS / tpe;   // elements per pass
+
+    // wait for the kv head's C chunks: each publishes generation gen + 1 in
+    // its own flag (one store, after its partial's stores completed) and
+    // waits for all C flags of the head; the merge's gates are loaded while
+    // the flags are polled (a load before the settle would be waited for)
+    settle_vmem();
+    __syncthreads();
+    if (t == 0) st_coh(a.count + rel, gen + 1u);
     float gate0 = 0.0f;
     {
         const uint32_t el = min(e0 + t / tpe, E - 1);
         gate0 = ld_coh(a.qg + (size_t)(g * gqa + el / HD) * 2 * HD + HD + el % HD);
     }
-
-    // wait for the kv head's C chunks: each publishes generation gen + 1 in
-    // its own flag (one store, after its partial's stores completed) and
-    // waits for all C flags of the head
-    settle_vmem();
-    __syncthreads();
     if (t < 64) {
-        if (t == 0) st_coh(a.count + rel, gen + 1u);
         const bool okw = att_wait_flags(a.count + g * C, C, gen + 1u, spin_limit, err, ins.dbg_node);
         if (t == 0) *flag = okw ? 1u : 0u;
     }

@@ -396,7 +396,7 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
         return set_error(SINTER_ERR_ARG, "attn: null pointer");
     if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
         a->rope_dims > a->hd ||
-        a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
+        a->rope_dims % 8 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
         return set_error(SINTER_ERR_ARG, "attn: unsupported shape or KV type (hd=%u nq=%u nkv=%u kv_type=%u)", a->hd,
                          a->nq, a->nkv, a->kv_type);
     // one (kv head, chunk) item per workgroup, all of them resident (the
@@ -413,7 +413,7 @@ int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, vo
     if (a->part || a->count)
         return set_error(SINTER_ERR_ARG, "attn_noalloc: part and count must be NULL (the library supplies them)");
     if (a->hd != 256 || !a->nkv || a->nq % a->nkv || a->nq / a->nkv > 8 || !a->n_chunks || a->n_chunks > 64 ||
-        a->rope_dims > a->hd || a->rope_dims % 2 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
+        a->rope_dims > a->hd || a->rope_dims % 8 || !al16(a->kc) || !al16(a->vc) || !kv_type_ok(a->kv_type))
         return set_error(SINTER_ERR_ARG, "attn_noalloc: unsupported shape or KV type (hd=%u nq=%u nkv=%u kv_type=%u)",
                          a->hd, a->nq, a->nkv, a->kv_type);
     if ((uint64_t)a->nkv * a->n_chunks > blocks || blocks > PLAN_MAX_BLOCKS)

@@ -432,7 +432,7 @@ int check_config(const sinter_model_config &c) {
         c.conv_k > 8 || ((2 * c.gdn_hk + c.gdn_hv) * c.gdn_d) % 256 || (c.gdn_hv * c.gdn_d) % 256)
         return set_error(SINTER_ERR_ARG, "config: gated-DeltaNet shape");
     if (c.head_dim != 256 || c.attn_nkv < 1 || c.attn_nq % c.attn_nkv || c.attn_nq / c.attn_nkv > 8 ||
-        c.rope_dims > c.head_dim || c.rope_dims % 2 || c.n_ctx < 1)
+        c.rope_dims > c.head_dim || c.rope_dims % 8 || c.n_ctx < 1)
         return set_error(SINTER_ERR_ARG, "config: attention shape");
     if (!(c.t_kv == 0 || c.t_kv == SINTER_F16 || c.t_kv == SINTER_Q8_0))
         return set_error(SINTER_ERR_ARG, "config: KV cache type must be F16 or Q8_0");
