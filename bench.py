@@ -193,7 +193,7 @@ def op_bench(args):
         "config": {"workload": f"BASELINE config {c}", "instances_rotated": n_inst, "context": ctx if c == 3 else None,
                    "passes_per_launch": ppl, "launches": launches, "bytes_per_op": nbytes, "bytes_breakdown": parts},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": "sinter_interp",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": m.info()["kernel"],
                      "roofline_us": round(nbytes / (PEAK_GBS * 1e9) * 1e6, 3)},
     }
     if not args.no_cpu_baseline:
@@ -454,7 +454,7 @@ def main():
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl, args.quant, args.ctx),
-                     "kernel": "sinter_interp", "passes_per_launch": ppl,
+                     "kernel": m.info()["kernel"], "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
         "prefill": prefill_info,

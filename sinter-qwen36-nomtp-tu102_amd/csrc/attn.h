@@ -667,13 +667,21 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     settle_vmem();
 }
 
-// the attention op of either KV cache type (the standalone op kernels)
+// the attention op of the KV cache types in feature set F
+template <uint32_t F>
 __device__ __forceinline__ void op_attn_decode(const sinter_instr &ins, unsigned *err, uint64_t *ts,
                                                uint64_t spin_limit, uint32_t pass_id) {
-    if (reinterpret_cast<const sinter_attn_args *>(ins.payload)->kv_type == SINTER_Q8_0)
-        op_attn_decode_t<true>(ins, err, ts, spin_limit, pass_id);
-    else
+    // (op_attn_decode_t raises BAD_SHAPE itself for a cache of the other type)
+    if constexpr ((F & FEAT_KV_Q80) == 0) {
         op_attn_decode_t<false>(ins, err, ts, spin_limit, pass_id);
+    } else if constexpr ((F & FEAT_KV_F16) == 0) {
+        op_attn_decode_t<true>(ins, err, ts, spin_limit, pass_id);
+    } else {
+        if (reinterpret_cast<const sinter_attn_args *>(ins.payload)->kv_type == SINTER_Q8_0)
+            op_attn_decode_t<true>(ins, err, ts, spin_limit, pass_id);
+        else
+            op_attn_decode_t<false>(ins, err, ts, spin_limit, pass_id);
+    }
 }
 
 }  // namespace sinter

@@ -637,22 +637,33 @@ __device__ __forceinline__ void prologue_quant(uint32_t K, uint32_t pro, uint32_
     __syncthreads();
 }
 
+// (F: the interpreter's feature set; the op checked that vt is in it)
+template <uint32_t F>
 __device__ __forceinline__ void prologue_compute(const sinter_gemv_args &a, int vt, double *red) {
     const uint32_t K = uni(a.K), pro = uni(a.pro), log2d = uni(a.gn_log2d);
     const float eps = __uint_as_float(uni(__float_as_uint(a.eps)));
+    constexpr uint32_t FX = F & (FEAT_X_Q8K | FEAT_X_Q80 | FEAT_X_BF16 | FEAT_X_F32);
+    if constexpr (FX == FEAT_X_Q8K) {
+        prologue_quant<SINTER_Q8_K>(K, pro, log2d, eps, red);
+        return;
+    } else if constexpr (FX == FEAT_X_BF16) {
+        prologue_quant<SINTER_BF16>(K, pro, log2d, eps, red);
+        return;
+    }
     switch (vt) {
-    case SINTER_Q8_K: prologue_quant<SINTER_Q8_K>(K, pro, log2d, eps, red); break;
-    case SINTER_Q8_0: prologue_quant<SINTER_Q8_0>(K, pro, log2d, eps, red); break;
-    case SINTER_BF16: prologue_quant<SINTER_BF16>(K, pro, log2d, eps, red); break;
-    default: prologue_quant<SINTER_F32>(K, pro, log2d, eps, red); break;
+    case SINTER_Q8_K: if constexpr ((F & FEAT_X_Q8K) != 0) prologue_quant<SINTER_Q8_K>(K, pro, log2d, eps, red); break;
+    case SINTER_Q8_0: if constexpr ((F & FEAT_X_Q80) != 0) prologue_quant<SINTER_Q8_0>(K, pro, log2d, eps, red); break;
+    case SINTER_BF16: if constexpr ((F & FEAT_X_BF16) != 0) prologue_quant<SINTER_BF16>(K, pro, log2d, eps, red); break;
+    case SINTER_F32: if constexpr ((F & FEAT_X_F32) != 0) prologue_quant<SINTER_F32>(K, pro, log2d, eps, red); break;
+    default: break;
     }
 }
 
-template <class Post>
+template <uint32_t F, class Post>
 __device__ __forceinline__ void gemv_prologue(const sinter_gemv_args &a, int vt, bool write_x, double *red,
                                               unsigned *err, Post &&post) {
     prologue_stage(a, write_x, err, post);
-    prologue_compute(a, vt, red);
+    prologue_compute<F>(a, vt, red);
 }
 
 // ------------------------------------------------------------ item terms
@@ -981,16 +992,40 @@ __device__ __forceinline__ void issue_slots(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[
     if constexpr (S0 <= 3 && 3 < S1) issue_item<T, 3>(pf, sh, r, f0 + 3 * si, dummy);
 }
 
+// has_w<F, T>: whether the interpreter compiled for feature set F handles
+// weight type T.  with_wtype<F>(t, f) calls f(integral_constant<int, T>) for
+// run type t: a plain two-way choice in the K-quant interpreter, one case
+// per handled type otherwise (types outside F: no call; the op checked the
+// plan against F first).
+template <uint32_t F, int T> constexpr bool has_w = (F & feat_w(T)) != 0;
+template <uint32_t F, class Fn>
+__device__ __forceinline__ void with_wtype(uint32_t t, Fn &&f) {
+    constexpr uint32_t FW = F & (FEAT_W_Q4K | FEAT_W_Q6K | FEAT_W_Q80 | FEAT_W_BF16 | FEAT_W_F32);
+    if constexpr (FW == (FEAT_W_Q4K | FEAT_W_Q6K)) {
+        if (t == SINTER_Q6_K) f(std::integral_constant<int, SINTER_Q6_K>{});
+        else f(std::integral_constant<int, SINTER_Q4_K>{});
+    } else if constexpr (FW == FEAT_W_BF16) {
+        f(std::integral_constant<int, SINTER_BF16>{});
+    } else {
+        switch (t) {
+        case SINTER_Q4_K: if constexpr (has_w<F, SINTER_Q4_K>) f(std::integral_constant<int, SINTER_Q4_K>{}); break;
+        case SINTER_Q6_K: if constexpr (has_w<F, SINTER_Q6_K>) f(std::integral_constant<int, SINTER_Q6_K>{}); break;
+        case SINTER_Q8_0: if constexpr (has_w<F, SINTER_Q8_0>) f(std::integral_constant<int, SINTER_Q8_0>{}); break;
+        case SINTER_BF16: if constexpr (has_w<F, SINTER_BF16>) f(std::integral_constant<int, SINTER_BF16>{}); break;
+        case SINTER_F32: if constexpr (has_w<F, SINTER_F32>) f(std::integral_constant<int, SINTER_F32>{}); break;
+        default: break;
+        }
+    }
+}
+
 // The slots loaded before the prologue (dispatch on the run's type).
+template <uint32_t F>
 __device__ __forceinline__ void issue_pre(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
     if (!r.ok) return;
-    switch (r.type) {
-    case SINTER_Q4_K: issue_slots<SINTER_Q4_K, 0, TypeCfg<SINTER_Q4_K>::DPRE>(pf, sh, r, dummy); break;
-    case SINTER_Q6_K: issue_slots<SINTER_Q6_K, 0, TypeCfg<SINTER_Q6_K>::DPRE>(pf, sh, r, dummy); break;
-    case SINTER_Q8_0: issue_slots<SINTER_Q8_0, 0, TypeCfg<SINTER_Q8_0>::DPRE>(pf, sh, r, dummy); break;
-    case SINTER_BF16: issue_slots<SINTER_BF16, 0, TypeCfg<SINTER_BF16>::DPRE>(pf, sh, r, dummy); break;
-    default: issue_slots<SINTER_F32, 0, TypeCfg<SINTER_F32>::DPRE>(pf, sh, r, dummy); break;
-    }
+    with_wtype<F>(r.type, [&](auto Tc) {
+        constexpr int T = decltype(Tc)::value;
+        issue_slots<T, 0, TypeCfg<T>::DPRE>(pf, sh, r, dummy);
+    });
 }
 
 // Slots [DPRE, DPRO), issued right after the prologue's LDS-DMAs
@@ -1006,19 +1041,13 @@ __device__ __forceinline__ void issue_post_t(u32x4 (&pf)[PF_MAX], uint32_t (&sh)
     issue_slots<T, DPRE, DPRO>(pf, sh, r, dummy);
     if constexpr (WAIT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-template <bool WAIT>
+template <uint32_t F, bool WAIT>
 __device__ __forceinline__ void issue_post(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const Run &r, uint64_t dummy) {
     if (!r.ok) {
         if constexpr (WAIT) dma_wait();
         return;
     }
-    switch (r.type) {
-    case SINTER_Q4_K: issue_post_t<SINTER_Q4_K, WAIT>(pf, sh, r, dummy); break;
-    case SINTER_Q6_K: issue_post_t<SINTER_Q6_K, WAIT>(pf, sh, r, dummy); break;
-    case SINTER_Q8_0: issue_post_t<SINTER_Q8_0, WAIT>(pf, sh, r, dummy); break;
-    case SINTER_BF16: issue_post_t<SINTER_BF16, WAIT>(pf, sh, r, dummy); break;
-    default: issue_post_t<SINTER_F32, WAIT>(pf, sh, r, dummy); break;
-    }
+    with_wtype<F>(r.type, [&](auto Tc) { issue_post_t<decltype(Tc)::value, WAIT>(pf, sh, r, dummy); });
 }
 
 // Epilogues that read operands (residual add, conv) run only in the fold at
@@ -1225,16 +1254,22 @@ __device__ __forceinline__ void run_body(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4],
     fold_rows<true>(c, pl, r, folded, nrows, bv, bi, ev);
 }
 
+template <uint32_t F>
 __device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const GemvCtx &c, cplan_t *pl,
                                              const Run &r, const ActView &x, float &bv, int32_t &bi,
                                              const EpiPre &ev) {
-    switch (r.type) {
-    case SINTER_Q4_K: run_body<SINTER_Q4_K>(pf, sh, c, pl, r, x, bv, bi, ev); break;
-    case SINTER_Q6_K: run_body<SINTER_Q6_K>(pf, sh, c, pl, r, x, bv, bi, ev); break;
-    case SINTER_Q8_0: run_body<SINTER_Q8_0>(pf, sh, c, pl, r, x, bv, bi, ev); break;
-    case SINTER_BF16: run_body<SINTER_BF16>(pf, sh, c, pl, r, x, bv, bi, ev); break;
-    default: run_body<SINTER_F32>(pf, sh, c, pl, r, x, bv, bi, ev); break;
-    }
+    with_wtype<F>(r.type, [&](auto Tc) { run_body<decltype(Tc)::value>(pf, sh, c, pl, r, x, bv, bi, ev); });
+}
+
+// Whether the interpreter compiled for F runs the planned GEMV: its
+// activation type and every segment's weight type are in F (the host picks
+// a kernel whose set covers the program, so this only guards against a
+// mismatch: a run read with another type's item size would stream past its
+// matrix).
+template <uint32_t F>
+__device__ __forceinline__ bool plan_in_set(cplan_t *pl) {
+    if constexpr (F == FEAT_ALL) return true;
+    else return (pl->feat & ~F) == 0;
 }
 
 // ------------------------------------------------------------ the op
@@ -1243,6 +1278,7 @@ __device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)
 // at a pass end).
 // ts (thread 0, or null): wall clock stamps [1] after the barrier wait,
 // [2] after the prologue.
+template <uint32_t F>
 __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
                                        unsigned *err, GridCross *gx, uint64_t *ts) {
     if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
@@ -1250,7 +1286,8 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     cplan_t *pl = (cplan_t *)plan;
     cu32_t *cu = (cu32_t *)cuts;
     const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
-    const bool ok = pl->ok != 0;
+    // (a plan outside this interpreter's feature set raises UNWIRED_KIND)
+    const bool planned = pl->ok != 0, ok = planned && plan_in_set<F>(pl);
     const uint32_t wv = rel * WAVES + uni(wave_id());
     const uint32_t row_lo = ok ? cu[wv] : 0u, row_hi = ok ? cu[wv + 1] : 0u;
     Run run = make_run(pl, 0, row_lo, row_hi);
@@ -1258,16 +1295,17 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     uint32_t sh[4] = {0, 0, 0, 0};
     if (gx) {
         // (the arrival publishes g_args too)
-        if (!cross_barrier(*gx, [&] { issue_pre(pf, sh, run, (uint64_t)plan); })) return false;
+        if (!cross_barrier(*gx, [&] { issue_pre<F>(pf, sh, run, (uint64_t)plan); })) return false;
     } else {
-        issue_pre(pf, sh, run, (uint64_t)plan);
+        issue_pre<F>(pf, sh, run, (uint64_t)plan);
         __syncthreads();
     }
     if (ts) ts[1] = wall_clock64();
     EpiPre ev;
     epi_preload(pl, run, ev);
     if (!ok) {
-        if (rel == 0 && threadIdx.x == 0) raise_error(err, SINTER_E_BAD_SHAPE, ins.dbg_node);
+        if (rel == 0 && threadIdx.x == 0)
+            raise_error(err, planned ? SINTER_E_UNWIRED_KIND : SINTER_E_BAD_SHAPE, ins.dbg_node);
         settle_vmem();
         __syncthreads();
         return true;
@@ -1278,7 +1316,7 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     const bool write_x = (a.pro == SINTER_PRO_EMBED) && rel == 0 && a.x_out != nullptr;
     // the remaining weight slots stream during the prologue (issued after
     // its activation DMAs, which the prologue then waits for)
-    gemv_prologue(a, vt, write_x, g_red, err, [&] { issue_post<true>(pf, sh, run, (uint64_t)plan); });
+    gemv_prologue<F>(a, vt, write_x, g_red, err, [&] { issue_post<F, true>(pf, sh, run, (uint64_t)plan); });
     if (ts) ts[2] = wall_clock64();
     const ActView x = act_view(g_qbuf, K, vt);
 
@@ -1300,11 +1338,11 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
     float bv = -INFINITY;
     int32_t bi = 0x7fffffff;
     while (run.ok) {
-        run_dispatch(pf, sh, c, pl, run, x, bv, bi, ev);
+        run_dispatch<F>(pf, sh, c, pl, run, x, bv, bi, ev);
         run = make_run(pl, run.s, run.g1, row_hi);
         if (!run.ok) break;
-        issue_pre(pf, sh, run, (uint64_t)plan);
-        issue_post<false>(pf, sh, run, (uint64_t)plan);
+        issue_pre<F>(pf, sh, run, (uint64_t)plan);
+        issue_post<F, false>(pf, sh, run, (uint64_t)plan);
         epi_preload(pl, run, ev);
     }
 

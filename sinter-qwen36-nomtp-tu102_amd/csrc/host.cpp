@@ -198,6 +198,7 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
     p.n_seg = a.n_seg;
     p.ipr = a.K / item_elems(a.seg[0].type);
     p.vt = (uint32_t)vdot(a.seg[0].type);
+    p.feat = feat_x(p.vt);
     bool any_swig = false;
     uint32_t base = 0;
     for (int s = 0; s < a.n_seg; s++) {
@@ -209,6 +210,7 @@ void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint
         q.rows = g.rows;
         q.base = base;
         q.type = g.type;
+        p.feat |= feat_w(g.type);
         q.swig = sw ? 1u : 0u;
         q.ib = item_bytes(g.type);
         q.y = reinterpret_cast<uint64_t>(g.y);
@@ -559,6 +561,7 @@ struct sinter_host {
     GemvPlan *d_plans = nullptr;          // [n_instr]
     uint32_t *d_cuts = nullptr;           // [n_instr][PLAN_CUTS]
     uint32_t n_instr = 0, epoch_stride = 0;
+    uint32_t feat = FEAT_ALL;             // the uploaded program's feature set (isa.h)
     unsigned *d_cells = nullptr;          // [32] err[2] | byte 1024 pass cell |
                                           // byte CELL_GROUPS: grid barrier flags (4 B per workgroup)
     sinter_pass_cell *d_pass = nullptr;
@@ -598,7 +601,8 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     if (!hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream), "barrier flags reset"))
         return SINTER_RUN_ERR;
     if (!hip_ok(hipEventRecord(h->ev0, h->stream), "event")) return SINTER_RUN_ERR;
-    if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream), "cooperative launch")) return SINTER_RUN_ERR;
+    if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream, h->feat), "cooperative launch"))
+        return SINTER_RUN_ERR;
     if (!hip_ok(hipEventRecord(h->ev1, h->stream), "event")) return SINTER_RUN_ERR;
     h->passes_done += n_passes;
     // wait with a watchdog; the kernel's own barrier spin limit bounds it too
@@ -690,12 +694,21 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
     }
     std::vector<GemvPlan> plans(n_instr);
     std::vector<uint32_t> cuts((size_t)n_instr * PLAN_CUTS, 0u);
+    // the feature set the program needs: every GEMV's activation and weight
+    // types, every attention op's KV cache type
+    uint32_t feat = 0;
     for (uint32_t i = 0; i < n_instr; i++) {
         std::memset(&plans[i], 0, sizeof(GemvPlan));
+        if (prog[i].kind == SINTER_OP_ATTN_DECODE) {
+            sinter_attn_args a;
+            std::memcpy(&a, prog[i].payload, sizeof a);
+            feat |= feat_kv(a.kv_type);
+        }
         if (prog[i].kind != SINTER_OP_GEMV) continue;
         sinter_gemv_args a;
         std::memcpy(&a, prog[i].payload, sizeof a);
         build_gemv_plan(a, prog[i].block_hi - prog[i].block_lo, plans[i], cuts.data() + (size_t)i * PLAN_CUTS, nullptr);
+        feat |= plans[i].feat;
     }
     if (h->d_prog) (void)hipFree(h->d_prog);
     if (h->d_plans) (void)hipFree(h->d_plans);
@@ -716,8 +729,13 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
         return SINTER_ERR_HIP;
     h->n_instr = n_instr;
     h->epoch_stride = epoch_stride;
+    h->feat = feat;
     h->prog.assign(prog, prog + n_instr);
     return SINTER_OK;
+}
+
+const char *sinter_host_kernel(const sinter_host *h) {
+    return h && h->n_instr ? interp_kernel_name(h->feat) : nullptr;
 }
 
 int sinter_host_set_gemv_shares(sinter_host *h, uint32_t instr, const float *share, uint32_t n) {

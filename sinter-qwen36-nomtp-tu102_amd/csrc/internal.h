@@ -26,7 +26,11 @@ struct InterpCtl {
 
 hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
                      unsigned *err, hipStream_t s, bool cooperative);
-hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s);
+// the interpreter kernel whose feature set (isa.h) covers feat: the
+// K-quant or bf16 specialisation when one does, else the general one
+hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s,
+                         uint32_t feat);
+const char *interp_kernel_name(uint32_t feat);
 hipError_t interp_max_blocks(int *blocks_per_cu);
 hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_t seed, float a, float b,
                         hipStream_t s);

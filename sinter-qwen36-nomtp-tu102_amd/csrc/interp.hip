@@ -37,8 +37,10 @@ __device__ __forceinline__ bool kind_wired(unsigned k) {
 
 using namespace sinter;
 
-extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
-sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+// The interpreter over feature set F (the GEMV weight / activation types and
+// KV cache types its ops handle; isa.h): one kernel per set below.
+template <uint32_t F>
+__device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ prog, const InterpCtl &ctl) {
     unsigned epoch = 0;
     const uint32_t n = ctl.n_instr;
     const bool timed = ctl.op_cycles && blockIdx.x == 0;
@@ -75,7 +77,7 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
                 uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
                 if (ts) ts[0] = s ? s : wall_clock64();
-                if (!gemv_op(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
+                if (!gemv_op<F>(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
                 if (ts) ts[3] = wall_clock64();
             } else if (fused_gdn) {
                 // the GDN step loads its state slice across the barrier; the
@@ -132,18 +134,31 @@ sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
             if (kind == SINTER_OP_GEMV) {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
-                (void)gemv_op(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
+                (void)gemv_op<F>(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
             } else {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
                 if (kind == SINTER_OP_GDN_STEP) (void)op_gdn_step(ins, ctl.err, ts, nullptr);
-                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode(ins, ctl.err, ts, ctl.spin_limit, pass);
+                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode<F>(ins, ctl.err, ts, ctl.spin_limit, pass);
             }
             if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
             stamp(i, 3, wall_clock64());
         }
         i += 1;
     }
+}
+
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_interp(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+    interp_main<FEAT_ALL>(prog, ctl);
+}
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_interp_kquant(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+    interp_main<FEAT_KQUANT>(prog, ctl);
+}
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_interp_bf16(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+    interp_main<FEAT_BF16SET>(prog, ctl);
 }
 
 // One instruction over the whole (non-cooperative) grid: the standalone op
@@ -155,11 +170,11 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
                  const uint32_t *__restrict__ cuts, unsigned *err) {
     // the host sets block_lo = 0, block_hi = gridDim.x
     switch (ins->kind) {
-    case SINTER_OP_GEMV: (void)gemv_op(*ins, plan, cuts, err, nullptr, nullptr); break;
+    case SINTER_OP_GEMV: (void)gemv_op<FEAT_ALL>(*ins, plan, cuts, err, nullptr, nullptr); break;
     case SINTER_OP_GDN_STEP: (void)op_gdn_step(*ins, err, nullptr, nullptr); break;
     // (attention launches cooperatively: its chunks of one kv head wait for
     // each other, bounded by a 2 s spin limit at 100 MHz)
-    case SINTER_OP_ATTN_DECODE: op_attn_decode(*ins, err, nullptr, 200000000ull, ATT_NO_CACHE); break;
+    case SINTER_OP_ATTN_DECODE: op_attn_decode<FEAT_ALL>(*ins, err, nullptr, 200000000ull, ATT_NO_CACHE); break;
     default: break;
     }
 }
@@ -185,7 +200,7 @@ extern "C" __global__ void sinter_clear_u32(unsigned *p, uint32_t n) {
 // The attention op with its instruction passed by value (nothing staged in
 // device memory for it).
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS) sinter_op_noalloc_kernel(sinter_instr ins, unsigned *err) {
-    op_attn_decode(ins, err, nullptr, 200000000ull, ATT_NO_CACHE);
+    op_attn_decode<FEAT_ALL>(ins, err, nullptr, 200000000ull, ATT_NO_CACHE);
 }
 
 // ---------------------------------------------------------------- barrier litmus
@@ -297,16 +312,40 @@ hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const ui
     return hipGetLastError();
 }
 
-hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s) {
+// the smallest interpreter whose feature set covers `feat`
+static const void *interp_kernel(uint32_t feat) {
+    if ((feat & ~(uint32_t)FEAT_KQUANT) == 0) return (const void *)sinter_interp_kquant;
+    if ((feat & ~(uint32_t)FEAT_BF16SET) == 0) return (const void *)sinter_interp_bf16;
+    return (const void *)sinter_interp;
+}
+
+const char *interp_kernel_name(uint32_t feat) {
+    const void *k = interp_kernel(feat);
+    return k == (const void *)sinter_interp_kquant ? "sinter_interp_kquant"
+         : k == (const void *)sinter_interp_bf16   ? "sinter_interp_bf16"
+                                                   : "sinter_interp";
+}
+
+hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s,
+                         uint32_t feat) {
     InterpCtl c = ctl;
     const sinter_instr *p = prog;
     void *args[] = {(void *)&p, (void *)&c};
-    return hipLaunchCooperativeKernel((const void *)sinter_interp, dim3(blocks), dim3(BLOCK_THREADS), args, 0, s);
+    return hipLaunchCooperativeKernel(interp_kernel(feat), dim3(blocks), dim3(BLOCK_THREADS), args, 0, s);
 }
 
+// workgroups per CU every interpreter kernel can hold (the least of them)
 hipError_t interp_max_blocks(int *blocks_per_cu) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (const void *)sinter_interp,
-                                                        BLOCK_THREADS, 0);
+    int least = 1 << 30;
+    for (const void *k : {(const void *)sinter_interp, (const void *)sinter_interp_kquant,
+                          (const void *)sinter_interp_bf16}) {
+        int n = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, BLOCK_THREADS, 0);
+        if (e != hipSuccess) return e;
+        least = n < least ? n : least;
+    }
+    *blocks_per_cu = least;
+    return hipSuccess;
 }
 
 // Device address of `scratch` on the current device, looked up once per

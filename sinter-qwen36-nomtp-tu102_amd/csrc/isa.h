@@ -20,6 +20,36 @@ namespace sinter {
 constexpr unsigned BLOCK_THREADS = 256;
 constexpr unsigned WAVES = BLOCK_THREADS / 64u;
 
+// Interpreter specialisations.  One interpreter kernel is compiled per set of
+// GEMV weight types, GEMV activation (vec_dot) types and KV cache types; the
+// code of the ops' cases outside the set is left out of it.  At upload the
+// host computes the set a program uses and launches the smallest kernel
+// that covers it (the persistent kernel's code is fetched anew by every
+// phase, and the specialised kernel decodes the 27B Q4_K_M model ~2 %
+// faster than the general one).
+enum : uint32_t {
+    FEAT_W_Q4K = 1u << 0, FEAT_W_Q6K = 1u << 1, FEAT_W_Q80 = 1u << 2, FEAT_W_BF16 = 1u << 3, FEAT_W_F32 = 1u << 4,
+    FEAT_X_Q8K = 1u << 5, FEAT_X_Q80 = 1u << 6, FEAT_X_BF16 = 1u << 7, FEAT_X_F32 = 1u << 8,
+    FEAT_KV_F16 = 1u << 9, FEAT_KV_Q80 = 1u << 10,
+    FEAT_ALL = (1u << 11) - 1u,
+    // K-quant weights, Q8_K activations, f16 KV cache (the Q4_K_M decode)
+    FEAT_KQUANT = FEAT_W_Q4K | FEAT_W_Q6K | FEAT_X_Q8K | FEAT_KV_F16,
+    // bf16 weights and activations, f16 KV cache
+    FEAT_BF16SET = FEAT_W_BF16 | FEAT_X_BF16 | FEAT_KV_F16,
+};
+// the feature bit of a GEMV weight type / activation type (0 for a type no
+// op handles) / KV cache type
+__host__ __device__ constexpr uint32_t feat_w(uint32_t t) {
+    return t == SINTER_Q4_K ? FEAT_W_Q4K : t == SINTER_Q6_K ? FEAT_W_Q6K : t == SINTER_Q8_0 ? FEAT_W_Q80
+         : t == SINTER_BF16 ? FEAT_W_BF16 : t == SINTER_F32 ? FEAT_W_F32 : 0u;
+}
+__host__ __device__ constexpr uint32_t feat_x(uint32_t vt) {
+    return vt == SINTER_Q8_K ? FEAT_X_Q8K : vt == SINTER_Q8_0 ? FEAT_X_Q80 : vt == SINTER_BF16 ? FEAT_X_BF16
+         : vt == SINTER_F32 ? FEAT_X_F32 : 0u;
+}
+// (kv_type 0 is the f16 cache, as SINTER_F16)
+__host__ __device__ constexpr uint32_t feat_kv(uint32_t t) { return t == SINTER_Q8_0 ? FEAT_KV_Q80 : FEAT_KV_F16; }
+
 // LDS: the quantised GEMV activation, and one 96 KiB scratch region shared by
 // the ops: the GEMV's activation staging (prologue) and then its per-wave
 // item-term rings; attention's tiles; the GDN step's vectors.
@@ -103,6 +133,7 @@ struct GemvSegPlan {
 };
 struct GemvPlan {
     uint32_t ok;                        // passed validation (otherwise the op raises BAD_SHAPE)
+    uint32_t feat;                      // feature bits of its activation and weight types
     uint32_t n_seg, ipr, vt, any_argmax, total_rows;
     uint32_t mipr;                      // floor((2^32-1) / ipr)
     // the term ring of a wave: R rows of P terms (per matrix); mR = floor((2^32-1) / R)

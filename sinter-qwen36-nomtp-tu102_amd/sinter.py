@@ -162,6 +162,7 @@ def lib():
         "sinter_host_history": (vp, [vp, C.POINTER(U32)]),
         "sinter_host_error": (I, [vp, C.POINTER(U32), C.POINTER(U32)]),
         "sinter_host_grid": (I, [vp, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32)]),
+        "sinter_host_kernel": (C.c_char_p, [vp]),
         "sinter_host_set_pos": (I, [vp, C.c_int32]),
         "sinter_host_set_grid": (I, [vp, U32]),
         "sinter_host_set_gemv_shares": (I, [vp, U32, C.POINTER(C.c_float), U32]),
@@ -326,7 +327,9 @@ class Model:
     def info(self):
         wb, ni, nb, bl = C.c_uint64(), C.c_uint32(), C.c_uint32(), C.c_uint32()
         check(lib().sinter_model_info(self.h, C.byref(wb), C.byref(ni), C.byref(nb), C.byref(bl)), "info")
-        return {"weight_bytes": wb.value, "n_instr": ni.value, "n_boundaries": nb.value, "blocks": bl.value}
+        k = lib().sinter_host_kernel(self.host())
+        return {"weight_bytes": wb.value, "n_instr": ni.value, "n_boundaries": nb.value, "blocks": bl.value,
+                "kernel": k.decode() if k else None}
 
     def synth_context(self, n_past, seed):
         check(lib().sinter_model_synth_context(self.h, n_past, seed), "synth_context")

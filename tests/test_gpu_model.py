@@ -39,6 +39,8 @@ def test_small_model_decode_matches_oracle(sn, orc, torch_gpu, quant):
         mirror = orc.ModelMirror(m)
         info = m.info()
         assert info["n_boundaries"] == 5 * cfg.n_layer + 1
+        # the interpreter specialised for the program's types runs it
+        assert info["kernel"] == {"q4_k_m": "sinter_interp_kquant", "bf16": "sinter_interp_bf16"}[quant]
         tok, pos = 17, 40
         for step in range(6):
             logits = np.zeros(cfg.n_vocab, np.float32)
