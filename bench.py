@@ -51,7 +51,7 @@ def bytes_per_token(cfg, m, n_attended):
             "total": weights + gdn_state + conv_state + kv_row * n_attended + kv_row + logits}
 
 
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_e2e_q4km_ctx4096.md")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_kquant_e2e_q4km_ctx4096.md")
 
 
 def measured_traffic(passes_per_launch, quant, ctx):

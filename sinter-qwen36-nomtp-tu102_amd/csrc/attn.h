@@ -487,7 +487,8 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
             double ws = row16_sum_f64(wgt);
             ws += __shfl_xor(ws, 16, 64);
             sc[hh * ATT_TILE + r] = wgt;
-            const double cf = (mo == -INFINITY) ? 0.0 : exp(mo - mn);
+            // (an unchanged max: exp(0) = 1 exactly, so the call is skipped)
+            const double cf = (mo == -INFINITY) ? 0.0 : (mo == mn ? 1.0 : exp(mo - mn));
             lrun = lrun * cf + ws;
             mrun = mn;
             if (r == 0) corr[hh] = cf;
