@@ -54,21 +54,41 @@ def bytes_per_token(cfg, m, n_attended):
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_kquant_e2e_q4km_ctx4096.md")
 
 
+def kernel_source_digest():
+    """sha256 of the kernel sources (csrc/*.h, *.hip, sorted by name): the
+    traffic summary records the digest of the sources it was measured on."""
+    import hashlib
+    d = os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd", "csrc")
+    h = hashlib.sha256()
+    for fn in sorted(os.listdir(d)):
+        if fn.endswith((".h", ".hip")):
+            h.update(fn.encode())
+            with open(os.path.join(d, fn), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()
+
+
 def measured_traffic(passes_per_launch, quant, ctx):
-    """HBM bytes per launch of the interpreter, from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE per pass, scaled against a copy kernel of
-    known size), or None when no summary exists or the run is not the
-    summarised workload (q4_k_m weights, 4096-token context)."""
+    """(HBM bytes per launch of the interpreter, the commit it was measured
+    at) from the committed counter summary (FETCH_SIZE + WRITE_SIZE per pass,
+    scaled against a copy kernel of known size); (None, None) when no summary
+    exists, when it was measured on other kernel sources than these (a stale
+    figure), or when the run is not the summarised workload (q4_k_m weights,
+    4096-token context)."""
     if quant != "q4_k_m" or ctx != 4096:
-        return None
+        return None, None
+    fields = {}
     try:
         with open(TRAFFIC_SUMMARY) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_pass:"):
-                    return round(float(line.split(":", 1)[1]) * passes_per_launch)
+                for key in ("traffic_bytes_per_pass", "kernel_sources_sha256", "measured_at_commit"):
+                    if line.startswith(key + ":"):
+                        fields[key] = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    if "traffic_bytes_per_pass" not in fields or fields.get("kernel_sources_sha256") != kernel_source_digest():
+        return None, None
+    return round(float(fields["traffic_bytes_per_pass"]) * passes_per_launch), fields.get("measured_at_commit")
 
 
 CPU_LABEL = "ggml-semantics CPU restatement (oracle/oracle.c: ggml's quantisers and block dots, OpenMP over rows"
@@ -438,6 +458,7 @@ def main():
     sp_ms, _ = single_pass_latency(m, toks[-1], pos0 + args.steps + args.profile_ops)
     mean_attended = pos0 + (args.steps + 1) / 2.0
     bpt = bytes_per_token(cfg, m, mean_attended)
+    traffic, traffic_commit = measured_traffic(ppl, args.quant, args.ctx)
     tok_s = args.steps / wall
     achieved = bpt["total"] * args.steps / (kernel_ms * 1e-3) / 1e9
     line = {
@@ -453,7 +474,8 @@ def main():
                    "gemv_balance": f"{args.balance[0]} updates, {n_bal} traced passes (untimed)",
                    "bytes_per_token": bpt["total"], "bytes_breakdown": bpt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": measured_traffic(ppl, args.quant, args.ctx),
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_measured_at": traffic_commit,
                      "kernel": m.info()["kernel"], "passes_per_launch": ppl,
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
