@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -729,7 +730,10 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
         return SINTER_ERR_HIP;
     h->n_instr = n_instr;
     h->epoch_stride = epoch_stride;
-    h->feat = feat;
+    // SINTER_INTERP=general (a diagnostic): launch the general interpreter
+    // whatever the program's types
+    const char *force = std::getenv("SINTER_INTERP");
+    h->feat = (force && std::strcmp(force, "general") == 0) ? (uint32_t)FEAT_ALL : feat;
     h->prog.assign(prog, prog + n_instr);
     return SINTER_OK;
 }

@@ -59,43 +59,35 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
     };
     while (pass < ctl.n_passes) {
         const unsigned kind = i < n ? prog[i].kind : (unsigned)SINTER_OP_BOUNDARY;
-        // The op this iteration runs: after a boundary the GEMV / GDN step it
-        // is fused with (crossing the barrier inside the op), otherwise the
-        // instruction itself.  One call site per op kind below, so each op's
-        // code is in the kernel once.
-        uint32_t oi = i;                 // the op's instruction
-        unsigned okind = kind;
-        bool run = false;
-        GridCross gx;
-        GridCross *gxp = nullptr;        // non-null: the op crosses this boundary first
-        uint64_t *ts = nullptr;          // the op's trace record (thread 0 of pass 0)
-        const uint64_t s = timed ? wall_clock64() : 0;
-        bool pass_end = false, took_next = false;
         if (kind == SINTER_OP_BOUNDARY) {
-            pass_end = i == n;
+            const bool pass_end = i == n;
             const uint32_t nx = pass_end ? 0u : i + 1;
             const bool more = nx < n && (pass + (pass_end ? 1u : 0u)) < ctl.n_passes;
             const bool in_nx = more && blockIdx.x >= prog[nx].block_lo && blockIdx.x < prog[nx].block_hi;
-            took_next = in_nx && (prog[nx].kind == SINTER_OP_GEMV || prog[nx].kind == SINTER_OP_GDN_STEP);
+            const bool fused = in_nx && prog[nx].kind == SINTER_OP_GEMV;
+            const bool fused_gdn = in_nx && prog[nx].kind == SINTER_OP_GDN_STEP;
+            const uint64_t s = timed ? wall_clock64() : 0;
+            GridCross gx;
             gx.flags = ctl.flags; gx.err = ctl.err; gx.epoch = &epoch;
             gx.spin_limit = ctl.spin_limit; gx.pass_end = pass_end; gx.t0 = t0; gx.t_wait_end = 0;
             gx.pass_slot = (pass_end && blockIdx.x == 0 && ctl.pass_cycles && ctl.pass_cycles_cap)
                                ? ctl.pass_cycles + (ctl.pass_base + pass) % ctl.pass_cycles_cap
                                : nullptr;
-            if (took_next) {
-                oi = nx;
-                okind = prog[nx].kind;
-                run = true;
-                gxp = &gx;
-                ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
-                         ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
-                // a fused GEMV's record keeps the arrival; a fused GDN step's
-                // the wait's end, the boundary's record the arrival
-                if (okind == SINTER_OP_GEMV) {
-                    if (ts) ts[0] = s ? s : wall_clock64();
-                } else {
-                    stamp(i, 0, wall_clock64());
-                }
+            if (fused) {
+                uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
+                if (ts) ts[0] = s ? s : wall_clock64();
+                if (!gemv_op<F>(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
+                if (ts) ts[3] = wall_clock64();
+            } else if (fused_gdn) {
+                // the GDN step loads its state slice across the barrier; the
+                // boundary's record keeps the arrival and the wait's end
+                uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
+                stamp(i, 0, wall_clock64());
+                if (!op_gdn_step(prog[nx], ctl.err, ts, &gx)) return;
+                stamp(i, 1, gx.t_wait_end);
+                if (ts) { ts[0] = gx.t_wait_end; ts[3] = wall_clock64(); }
             } else {
                 stamp(i, 0, wall_clock64());
                 grid_arrive(ctl.flags, epoch);
@@ -113,47 +105,13 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
                 }
                 stamp(i, 1, gx.t_wait_end);
             }
-        } else {
-            if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
-                if (blockIdx.x == 0 && threadIdx.x == 0)
-                    raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
-                settle_vmem();
-                return;
-            }
-            run = blockIdx.x >= prog[i].block_lo && blockIdx.x < prog[i].block_hi;
-            if (run) {
-                ts = (traced && pass == 0 && threadIdx.x == 0)
-                         ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
-                stamp(i, 0, wall_clock64());
-            }
-        }
-        if (run) {
-            bool go_on = true;
-            if (okind == SINTER_OP_GEMV)
-                go_on = gemv_op<F>(prog[oi], ctl.plans + oi, ctl.cuts + (size_t)oi * PLAN_CUTS, ctl.err, gxp, ts);
-            else if (okind == SINTER_OP_GDN_STEP)
-                go_on = op_gdn_step(prog[oi], ctl.err, ts, gxp);
-            else if (okind == SINTER_OP_ATTN_DECODE)
-                op_attn_decode<F>(prog[oi], ctl.err, ts, ctl.spin_limit, pass);
-            if (!go_on) return;
-            const uint64_t e = wall_clock64();
-            if (gxp) {
-                if (okind == SINTER_OP_GDN_STEP) {
-                    stamp(i, 1, gx.t_wait_end);
-                    if (ts) ts[0] = gx.t_wait_end;
-                }
-                if (ts) ts[3] = e;
-            } else {
-                stamp(i, 3, e);
-            }
-            if (timed && threadIdx.x == 0 && !gxp) ctl.op_cycles[okind] += (long long)(e - s);
-        }
-        if (kind == SINTER_OP_BOUNDARY) {
             if (timed && threadIdx.x == 0) {
                 const uint64_t e = wall_clock64();
                 ctl.op_cycles[SINTER_OP_BOUNDARY] += (long long)(gx.t_wait_end - s);
-                if (took_next) ctl.op_cycles[okind] += (long long)(e - gx.t_wait_end);
+                if (fused) ctl.op_cycles[SINTER_OP_GEMV] += (long long)(e - gx.t_wait_end);
+                if (fused_gdn) ctl.op_cycles[SINTER_OP_GDN_STEP] += (long long)(e - gx.t_wait_end);
             }
+            const bool took_next = fused || fused_gdn;
             if (pass_end) {
                 pass += 1;
                 t0 = gx.t_wait_end;
@@ -161,9 +119,32 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
             } else {
                 i += took_next ? 2u : 1u;
             }
-        } else {
-            i += 1;
+            continue;
         }
+        const sinter_instr &ins = prog[i];
+        if (kind >= SINTER_OP_KIND_COUNT || !kind_wired(kind)) {
+            if (blockIdx.x == 0 && threadIdx.x == 0)
+                raise_error(ctl.err, kind >= SINTER_OP_KIND_COUNT ? SINTER_E_BAD_KIND : SINTER_E_UNWIRED_KIND, i);
+            settle_vmem();
+            return;
+        }
+        if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
+            const uint64_t s = timed ? wall_clock64() : 0;
+            stamp(i, 0, wall_clock64());
+            if (kind == SINTER_OP_GEMV) {
+                uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
+                (void)gemv_op<F>(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
+            } else {
+                uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
+                                   ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
+                if (kind == SINTER_OP_GDN_STEP) (void)op_gdn_step(ins, ctl.err, ts, nullptr);
+                else if (kind == SINTER_OP_ATTN_DECODE) op_attn_decode<F>(ins, ctl.err, ts, ctl.spin_limit, pass);
+            }
+            if (timed && threadIdx.x == 0) ctl.op_cycles[kind] += (long long)(wall_clock64() - s);
+            stamp(i, 3, wall_clock64());
+        }
+        i += 1;
     }
 }
 

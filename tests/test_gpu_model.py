@@ -207,3 +207,25 @@ def test_error_cell_path_bad_kind(sn, torch_gpu):
         assert L.sinter_host_shutdown(h, 1000.0) == 0
     finally:
         L.sinter_host_destroy(h)
+
+
+def test_specialised_interpreter_equals_general(sn, torch_gpu, monkeypatch):
+    """The K-quant interpreter (the cases of other types compiled out) and the
+    general one decode bit-identically: same tokens, same logits."""
+    cfg = small_config(sn, n_layer=8, n_ctx=256)
+    runs = {}
+    for name in ("sinter_interp_kquant", "sinter_interp"):
+        if name == "sinter_interp":
+            monkeypatch.setenv("SINTER_INTERP", "general")
+        m = sn.Model(cfg, seed=71)
+        try:
+            assert m.info()["kernel"] == name
+            m.synth_context(50, seed=72)
+            toks = m.greedy(11, 50, 12)
+            runs[name] = (toks, m.logits().copy())
+            print(f"{name}: {toks}", flush=True)
+        finally:
+            m.close()
+    (ta, la), (tb, lb) = runs.values()
+    assert ta == tb
+    assert np.array_equal(la, lb)
