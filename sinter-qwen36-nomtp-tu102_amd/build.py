@@ -22,11 +22,13 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsinter.so")
 REPORT = os.path.join(HERE, "resource_usage.txt")
 SOURCES = ["interp.hip", "host.cpp", "model.cpp", "gguf.cpp"]
-# -O2: the interpreter kernels come out with the same registers as at -O3
-# and decode the 27B Q4_K_M model ~1 % faster (6.07 -> 6.01 ms per token,
-# alternating runs on one box; -O1 6.07, -O3 with the max-ILP scheduler 6.08)
+# -Os: the 27B Q4_K_M decode per token (alternating runs on one box) is
+# 6.07 ms at -O3, 6.00 at -O2, 5.94 at -Os (fewer spilled registers in the
+# K-quant interpreter), 6.08 at -Oz; -O1 6.07; the max-ILP scheduler and
+# -fno-slp-vectorize on top of -Os are slower.  No floating-point effect:
+# contraction is off and no fast-math flag is set at any level.
 FLAGS = [
-    "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-Os", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
