@@ -55,16 +55,18 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_kquant_e
 
 
 def kernel_source_digest():
-    """sha256 of the kernel sources (csrc/*.h, *.hip, sorted by name): the
-    traffic summary records the digest of the sources it was measured on."""
+    """sha256 of the kernel sources (csrc/*.h, *.hip, sorted by name) and of
+    the build recipe (build.py: its compiler flags): the traffic summary
+    records the digest of the build it was measured on."""
     import hashlib
-    d = os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd", "csrc")
+    pkg = os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd")
+    d = os.path.join(pkg, "csrc")
     h = hashlib.sha256()
-    for fn in sorted(os.listdir(d)):
-        if fn.endswith((".h", ".hip")):
-            h.update(fn.encode())
-            with open(os.path.join(d, fn), "rb") as f:
-                h.update(f.read())
+    files = [os.path.join(d, fn) for fn in sorted(os.listdir(d)) if fn.endswith((".h", ".hip"))]
+    for path in files + [os.path.join(pkg, "build.py")]:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
     return h.hexdigest()
 
 
