@@ -209,12 +209,13 @@ def test_error_cell_path_bad_kind(sn, torch_gpu):
         L.sinter_host_destroy(h)
 
 
-def test_specialised_interpreter_equals_general(sn, torch_gpu, monkeypatch):
-    """The K-quant interpreter (the cases of other types compiled out) and the
-    general one decode bit-identically: same tokens, same logits."""
-    cfg = small_config(sn, n_layer=8, n_ctx=256)
+@pytest.mark.parametrize("quant,special", [("q4_k_m", "sinter_interp_kquant"), ("bf16", "sinter_interp_bf16")])
+def test_specialised_interpreter_equals_general(sn, torch_gpu, monkeypatch, quant, special):
+    """A specialised interpreter (the cases of other types compiled out) and
+    the general one decode bit-identically: same tokens, same logits."""
+    cfg = small_config(sn, n_layer=8, n_ctx=256, quant=quant)
     runs = {}
-    for name in ("sinter_interp_kquant", "sinter_interp"):
+    for name in (special, "sinter_interp"):
         if name == "sinter_interp":
             monkeypatch.setenv("SINTER_INTERP", "general")
         m = sn.Model(cfg, seed=71)
