@@ -253,7 +253,8 @@ int  sinter_host_error(sinter_host *h, uint32_t *code, uint32_t *aux);
 int  sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32_t *lds_bytes);
 /* The interpreter kernel the uploaded program launches (null before an
  * upload): "sinter_interp_kquant" when every GEMV reads Q4_K / Q6_K weights
- * with Q8_K activations and every KV cache is f16, "sinter_interp_bf16" for
+ * with Q8_K activations and every KV cache is f16, "sinter_interp_kquant_q8kv"
+ * for the same over Q8_0 KV caches, "sinter_interp_bf16" for
  * bf16 weights and activations over f16 caches, else the general
  * "sinter_interp".  No counterpart in the reference (one kernel there,
  * core/interp.cu:148-150): the specialised kernels leave out the code of the

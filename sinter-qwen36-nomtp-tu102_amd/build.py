@@ -35,7 +35,7 @@ FLAGS = [
     "-Rpass-analysis=kernel-resource-usage",
 ]
 # kernels that run as one resident workgroup per CU (cooperative grids)
-PERSISTENT = {"sinter_interp", "sinter_interp_kquant", "sinter_interp_bf16", "sinter_op_kernel", "sinter_op_noalloc_kernel", "sinter_litmus_kernel"}
+PERSISTENT = {"sinter_interp", "sinter_interp_kquant", "sinter_interp_kquant_q8kv", "sinter_interp_bf16", "sinter_op_kernel", "sinter_op_noalloc_kernel", "sinter_litmus_kernel"}
 LDS_LIMIT = 160 * 1024
 
 _FIELDS = {

@@ -157,6 +157,10 @@ sinter_interp_kquant(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     interp_main<FEAT_KQUANT>(prog, ctl);
 }
 extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
+sinter_interp_kquant_q8kv(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
+    interp_main<FEAT_KQUANT_Q8KV>(prog, ctl);
+}
+extern "C" __global__ void __launch_bounds__(BLOCK_THREADS)
 sinter_interp_bf16(const sinter_instr *__restrict__ prog, InterpCtl ctl) {
     interp_main<FEAT_BF16SET>(prog, ctl);
 }
@@ -315,15 +319,17 @@ hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const ui
 // the smallest interpreter whose feature set covers `feat`
 static const void *interp_kernel(uint32_t feat) {
     if ((feat & ~(uint32_t)FEAT_KQUANT) == 0) return (const void *)sinter_interp_kquant;
+    if ((feat & ~(uint32_t)FEAT_KQUANT_Q8KV) == 0) return (const void *)sinter_interp_kquant_q8kv;
     if ((feat & ~(uint32_t)FEAT_BF16SET) == 0) return (const void *)sinter_interp_bf16;
     return (const void *)sinter_interp;
 }
 
 const char *interp_kernel_name(uint32_t feat) {
     const void *k = interp_kernel(feat);
-    return k == (const void *)sinter_interp_kquant ? "sinter_interp_kquant"
-         : k == (const void *)sinter_interp_bf16   ? "sinter_interp_bf16"
-                                                   : "sinter_interp";
+    return k == (const void *)sinter_interp_kquant      ? "sinter_interp_kquant"
+         : k == (const void *)sinter_interp_kquant_q8kv ? "sinter_interp_kquant_q8kv"
+         : k == (const void *)sinter_interp_bf16        ? "sinter_interp_bf16"
+                                                        : "sinter_interp";
 }
 
 hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_t blocks, hipStream_t s,
@@ -338,7 +344,7 @@ hipError_t launch_interp(const sinter_instr *prog, const InterpCtl &ctl, uint32_
 hipError_t interp_max_blocks(int *blocks_per_cu) {
     int least = 1 << 30;
     for (const void *k : {(const void *)sinter_interp, (const void *)sinter_interp_kquant,
-                          (const void *)sinter_interp_bf16}) {
+                          (const void *)sinter_interp_kquant_q8kv, (const void *)sinter_interp_bf16}) {
         int n = 0;
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, BLOCK_THREADS, 0);
         if (e != hipSuccess) return e;

@@ -34,6 +34,8 @@ enum : uint32_t {
     FEAT_ALL = (1u << 11) - 1u,
     // K-quant weights, Q8_K activations, f16 KV cache (the Q4_K_M decode)
     FEAT_KQUANT = FEAT_W_Q4K | FEAT_W_Q6K | FEAT_X_Q8K | FEAT_KV_F16,
+    // the same over a Q8_0 KV cache
+    FEAT_KQUANT_Q8KV = FEAT_W_Q4K | FEAT_W_Q6K | FEAT_X_Q8K | FEAT_KV_Q80,
     // bf16 weights and activations, f16 KV cache
     FEAT_BF16SET = FEAT_W_BF16 | FEAT_X_BF16 | FEAT_KV_F16,
 };

@@ -106,7 +106,7 @@ def test_small_model_q8_cache_decode_matches_oracle(sn, orc, torch_gpu):
     try:
         m.synth_context(60, seed=52)
         mirror = orc.ModelMirror(m)
-        assert m.info()["kernel"] == "sinter_interp"     # a Q8_0 cache: the general interpreter
+        assert m.info()["kernel"] == "sinter_interp_kquant_q8kv"
         tok, pos = 9, 60
         for step in range(5):
             logits = np.zeros(cfg.n_vocab, np.float32)
