@@ -170,3 +170,52 @@ def test_config_refuses_irregular_attention_pattern(sn, tmp_path):
     with sn.Gguf(str(q)) as g:
         cfg = sn.ModelConfig()
         assert sn.lib().sinter_model_config_from_gguf(g.h, 256, C.byref(cfg)) == sn.ERR_ARG
+
+
+def test_mutated_files_open_or_are_refused(sn, tmp_path):
+    """Seeded byte mutations of a valid file (header, metadata, tensor table
+    and data regions; single-byte flips, 4-byte overwrites with extreme
+    values, truncations): every file either opens with a self-consistent
+    table -- each tensor's data inside the file -- or is refused with
+    SINTER_ERR_ARG; the parser never reads outside the file."""
+    data = np.arange(1024, dtype=np.float32)
+    w = Writer()
+    w.add_kv("general.architecture", K_STRING, "qwen35")
+    w.add_kv("qwen35.block_count", K_U32, 4)
+    w.add_kv("some.array", K_ARRAY, [1, 2, 3, 4], K_I32)
+    w.add_tensor("a", [256, 2], 0, data[:512])
+    w.add_tensor("b.weight", [256, 2], 0, data[512:])
+    raw = bytearray(_write(tmp_path, "base.gguf", w).read_bytes())
+    header_len = len(w.header(w.offsets()))
+    rng = np.random.default_rng(2027)
+    path = tmp_path / "mut.gguf"
+    opened = refused = 0
+    for it in range(300):
+        b = bytearray(raw)
+        kind = it % 3
+        if kind == 0:
+            pos = int(rng.integers(0, header_len))
+            b[pos] ^= 1 << int(rng.integers(0, 8))
+        elif kind == 1:
+            pos = int(rng.integers(0, header_len - 4))
+            b[pos:pos + 4] = struct.pack("<I", int(rng.choice([0, 1, 0x7fffffff, 0xffffffff, 255, 65536])))
+        else:
+            b = b[:int(rng.integers(0, len(b)))]
+        path.write_bytes(bytes(b))
+        h = C.c_void_p()
+        rc = sn.lib().sinter_gguf_open(str(path).encode(), C.byref(h))
+        if rc != sn.OK:
+            assert rc == sn.ERR_ARG, (it, rc)
+            refused += 1
+            continue
+        opened += 1
+        g = sn.Gguf.__new__(sn.Gguf)      # (the handle just opened)
+        g.h = h
+        try:
+            info = g.info()
+            for i in range(info["n_tensors"]):
+                t = g.tensor(i)
+                assert t.nbytes <= len(b)
+        finally:
+            g.close()
+    assert opened and refused
