@@ -55,18 +55,25 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_kquant_e
 
 
 def kernel_source_digest():
-    """sha256 of the kernel sources (csrc/*.h, *.hip, sorted by name) and of
-    the build recipe (build.py: its compiler flags): the traffic summary
-    records the digest of the build it was measured on."""
+    """sha256 of the interpreter's sources (interp.hip and the csrc/*.h
+    headers, sorted by name) and of the compiler flags it is built with
+    (build.py FLAGS): the traffic summary records the digest of the build it
+    was measured on.  Other translation units of the library (the batched
+    GEMV) do not enter it: they are separate code objects."""
     import hashlib
+    import importlib.util
     pkg = os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd")
     d = os.path.join(pkg, "csrc")
     h = hashlib.sha256()
-    files = [os.path.join(d, fn) for fn in sorted(os.listdir(d)) if fn.endswith((".h", ".hip"))]
-    for path in files + [os.path.join(pkg, "build.py")]:
+    files = [os.path.join(d, fn) for fn in sorted(os.listdir(d)) if fn.endswith(".h") or fn == "interp.hip"]
+    for path in files:
         h.update(os.path.basename(path).encode())
         with open(path, "rb") as f:
             h.update(f.read())
+    spec = importlib.util.spec_from_file_location("sinter_build_flags", os.path.join(pkg, "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    h.update(("FLAGS:" + "\x00".join(mod.FLAGS)).encode())
     return h.hexdigest()
 
 

@@ -282,6 +282,19 @@ float sinter_host_last_launch_ms(sinter_host *h);
 int sinter_op_gemv(const sinter_gemv_args *a, uint32_t blocks, void *stream);
 int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream);
 int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stream);
+/* Batched GEMV over a ubatch of tokens, the trunk GEMM of a batched prefill
+ * (replaces the fork's MMQ prefill GEMM, docs/PREFILL-SEMANTICS.md:286-313:
+ * quantised weights times quantised activations on int8 matrix cores).
+ * y[t * rows + r] = row r of w (rows x k, SINTER_Q4_K or SINTER_Q6_K, k a
+ * multiple of 256) dotted with token t's Q8_K activation (xq + t * (k / 256)
+ * blocks of 292 bytes), for t < n_tokens: the single-token GEMV's fp64 item
+ * terms folded in item order, so each y[t] is bit-identical to
+ * sinter_op_gemv on token t alone.  Weights are read once per 64 tokens.
+ * Alignment: w 16 bytes (Q4_K) / 4 bytes (Q6_K), xq and y 4 bytes.
+ * n_tokens == 0 is a no-op.  SINTER_ERR_ARG on a bad type, shape or
+ * alignment (nothing launched). */
+int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, const void *xq,
+                          uint32_t n_tokens, float *y, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

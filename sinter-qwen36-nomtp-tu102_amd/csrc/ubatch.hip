@@ -1,0 +1,348 @@
+// Batched GEMV over a ubatch of tokens: the trunk GEMM of a batched prefill
+// (docs/PREFILL-SEMANTICS.md:286-313 in the reference: the fork's prefill
+// multiplies quantised weights by quantised activations on int8 tensor
+// cores, MMQ, instead of running the single-token GEMV once per token).
+//
+//   y[t][r] = (float) sum_i term(W[r] item i, X[t] item i),  t < n_tokens
+//
+// W: rows x K of ggml Q4_K or Q6_K super-blocks (the GGUF layout as-is);
+// X: n_tokens Q8_K activations (ggml block_q8_K {f32 d; i8 qs[256];
+// i16 bsums[16]}, K/256 blocks per token).  The item terms and their fold
+// are the single-token GEMV's (gemv.h: one fp64 term per 256-element
+// super-block, summed in item order), so every output is bit-identical to
+// the decode GEMV of the same token; only the integer dot products move to
+// MFMA.
+//
+// A workgroup of four waves owns 64 rows (16 per wave) and up to 64 tokens
+// (four 16-token tiles), so each weight byte is read from HBM once per 64
+// tokens.  Item by item the workgroup stages the 64 tokens' Q8_K blocks in
+// LDS (double-buffered: the next item's are loaded while this one is
+// computed) and every wave streams its own rows' weights.  Per item
+// and token tile it runs v_mfma_i32_16x16x32_i8 with the tokens' codes as A
+// (16 x 32, lane l: token l%16, elements 8(l/16)..+7 of the 32) and the rows'
+// codes as B (32 x 16, lane l: row l%16, the same elements); D (16 x 16
+// int32, lane l: row l%16, tokens 4(l/16)+v) holds one exact 32-element dot
+// per (token, row).  A Q4_K sub-block is 32 elements (one MFMA); a Q6_K
+// sub-block is 16, so a 32-element chunk runs two MFMAs, each with the other
+// sub-block's half of B zeroed.  Q4_K's min term sum_s m_s * (sum of the
+// sub-block's activation codes) is one more MFMA per sub-block, against B =
+// m_s in every byte, accumulated across the sub-blocks in D.  Each lane then
+// forms the fp64 term of its four (token, row) pairs from its own row's
+// scales and folds it into its accumulators.
+#include "internal.h"
+
+namespace sinter {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t UB_ROWS = 16;     // rows per wave: the MFMA's N
+constexpr uint32_t UB_TOK = 16;      // tokens per tile: the MFMA's M
+constexpr uint32_t UB_TILES = 4;     // token tiles per wave
+constexpr uint32_t UB_TOKENS = UB_TOK * UB_TILES;
+constexpr uint32_t UB_THREADS = 256;  // four waves: 64 rows of the workgroup's row tile
+constexpr uint32_t UB_WG_ROWS = UB_ROWS * (UB_THREADS / 64u);
+constexpr uint32_t UB_XSTRIDE = 68;   // LDS dwords per staged token (65 used)
+constexpr uint64_t UB_MIN_WGS = 256;  // one per CU
+constexpr uint32_t Q8K_BYTES = 292;  // block_q8_K
+constexpr uint32_t Q4K_BYTES = 144, Q6K_BYTES = 210;
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
+__device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) {
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// 8 bytes at block byte o of a 2-aligned block whose 4-aligned base is
+// base4 = block - sh (sh = 0 or 2): the third dword is read only when the
+// bytes straddle it, so no read leaves the block's own 4-aligned span
+__device__ __forceinline__ void ld8u(const uint8_t *base4, uint32_t o, uint32_t sh, uint32_t &lo, uint32_t &hi) {
+    const uint32_t *p = (const uint32_t *)(base4 + o);
+    const uint32_t d0 = p[0], d1 = p[1];
+    const uint32_t d2 = sh ? p[2] : 0u;
+    // v_alignbyte_b32: ({d1, d0} >> 8 * sh)[31:0] -- the shift counts bytes
+    lo = __builtin_amdgcn_alignbyte(d1, d0, sh);
+    hi = __builtin_amdgcn_alignbyte(d2, d1, sh);
+}
+// bytewise x - 32 for bytes 0..63 (no borrow crosses a byte)
+__device__ __forceinline__ uint32_t sub32b(uint32_t x) { return ((x | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
+
+template <int WT>
+struct WItem;
+
+// Q4_K: the lane's row header (d, dmin, 12 scale bytes) and its four 8-byte
+// slices of qs (bytes 32p + 8g..+7: sub-block 2p in the low nibbles, 2p + 1
+// in the high ones)
+template <>
+struct WItem<SINTER_Q4_K> {
+    uint32_t h[4];
+    uint32_t q[8];
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t i, uint32_t g) {
+        const uint8_t *b = row + (size_t)i * Q4K_BYTES;
+        const uint4 hv = *(const uint4 *)b;
+        h[0] = hv.x; h[1] = hv.y; h[2] = hv.z; h[3] = hv.w;
+#pragma unroll
+        for (uint32_t p = 0; p < 4; p++) {
+            const uint2 v = *(const uint2 *)(b + 16u + 32u * p + 8u * g);
+            q[2 * p] = v.x; q[2 * p + 1] = v.y;
+        }
+    }
+};
+
+// Q6_K: the lane's slices of ql (bytes 64n + 8g and 64n + 32 + 8g), qh
+// (bytes 32n + 8g) for both halves n, the 16 int8 scales and d
+template <>
+struct WItem<SINTER_Q6_K> {
+    uint32_t l0[4], l1[4], hh[4];   // [2n], [2n + 1]: lo / hi dwords of half n
+    uint32_t sc[4];
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, uint32_t i, uint32_t g) {
+        const uint8_t *b = row + (size_t)i * Q6K_BYTES;
+        const uint32_t sh = (uint32_t)((uintptr_t)b & 3u);
+        const uint8_t *b4 = b - sh;
+#pragma unroll
+        for (uint32_t n = 0; n < 2; n++) {
+            ld8u(b4, 64u * n + 8u * g, sh, l0[2 * n], l0[2 * n + 1]);
+            ld8u(b4, 64u * n + 32u + 8u * g, sh, l1[2 * n], l1[2 * n + 1]);
+            ld8u(b4, 128u + 32u * n + 8u * g, sh, hh[2 * n], hh[2 * n + 1]);
+        }
+        ld8u(b4, 192u, sh, sc[0], sc[1]);
+        ld8u(b4, 200u, sh, sc[2], sc[3]);
+        d = *(const uint16_t *)(b + 208);
+    }
+};
+
+// Stage item i of the workgroup's tokens in LDS: token j's Q8_K block i (its
+// 256 codes at dwords 0..63 of LDS row j, its d at dword 64).  Wave w stages
+// token tile w, four lanes per token, each lane 16 code dwords (and the
+// first of the four, d), so the per-item work is one address update and
+// loads at immediate offsets.  Tokens past the last repeat it (never
+// stored).  ld: into registers; st: registers to LDS buffer xs.
+struct ActStage {
+    uint32_t v[16], d;
+    const uint8_t *blk0;   // the lane's token's block 0
+    uint32_t part, row;    // 16-dword quarter of the codes; LDS row (token within the group)
+    __device__ __forceinline__ void init(const uint8_t *xq, uint32_t nb, uint32_t tok0, uint32_t n_tok) {
+        const uint32_t lane = threadIdx.x & 63u;
+        row = UB_TOK * (threadIdx.x >> 6) + (lane >> 2);
+        part = lane & 3u;
+        const uint32_t tok = min(tok0 + row, n_tok - 1u);
+        blk0 = xq + (size_t)tok * nb * Q8K_BYTES;
+    }
+    __device__ __forceinline__ void ld(uint32_t i) {
+        const uint8_t *b = blk0 + (size_t)i * Q8K_BYTES;
+        const uint32_t *c = (const uint32_t *)(b + 4u + 64u * part);
+#pragma unroll
+        for (uint32_t k = 0; k < 16; k++) v[k] = c[k];
+        if (part == 0) d = *(const uint32_t *)b;
+    }
+    __device__ __forceinline__ void st(uint32_t *xs) const {
+        uint32_t *r = xs + row * UB_XSTRIDE;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++)
+            *(uint4 *)(r + 16u * part + 4u * k) = make_uint4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        if (part == 0) r[64] = d;
+    }
+};
+static_assert(UB_THREADS / 64u == UB_TILES, "one staging wave per token tile");
+static_assert(UB_XSTRIDE % 4u == 0, "16-byte LDS row alignment");
+
+template <int WT>
+__global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *__restrict__ w, uint32_t rows,
+                                                                uint32_t nb, const uint8_t *__restrict__ xq,
+                                                                uint32_t n_tok, float *__restrict__ y, uint32_t n_tg,
+                                                                uint32_t tpw) {
+    __shared__ uint32_t xs[2][UB_TOKENS * UB_XSTRIDE];
+    const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, r = lane & 15u, g = lane >> 4;
+    // adjacent workgroups share a row tile (their token groups): its weight
+    // bytes come from HBM once and from the memory-side cache after
+    const uint32_t rt = blockIdx.x / n_tg, tg = blockIdx.x % n_tg;
+    const uint32_t row = rt * UB_WG_ROWS + wv * UB_ROWS + r;
+    const uint32_t rowc = row < rows ? row : rows - 1u;
+    const uint32_t tok0 = tg * UB_TOK * tpw;
+    const uint32_t ntiles = min(tpw, (n_tok - tok0 + UB_TOK - 1u) / UB_TOK);   // block-uniform, 1..4
+    const size_t row_bytes = (size_t)nb * (WT == SINTER_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    const uint8_t *wrow = w + (size_t)rowc * row_bytes;
+
+    double acc[UB_TILES][4];
+#pragma unroll
+    for (uint32_t t = 0; t < UB_TILES; t++)
+#pragma unroll
+        for (uint32_t v = 0; v < 4; v++) acc[t][v] = 0.0;
+
+    ActStage stage;
+    // wave w stages token tile w, when the group has it (wave-uniform)
+    const bool stager = (threadIdx.x >> 6) < ntiles;
+    stage.init(xq, nb, tok0, n_tok);
+    if (stager) stage.ld(0);
+    WItem<WT> cur, nxt;
+    cur.load(wrow, 0, g);
+    if (stager) stage.st(xs[0]);
+    __syncthreads();
+    for (uint32_t i = 0; i < nb; i++) {
+        if (i + 1u < nb) {
+            // activations first: vector loads complete in order, so the
+            // staging store at the end of this item then waits for these
+            // cache hits and not for the weights behind them
+            if (stager) stage.ld(i + 1u);
+            nxt.load(wrow, i + 1u, g);
+        }
+        const uint32_t *xb = xs[i & 1u];
+
+        // B operands and the per-sub-block integer scales of the lane's row
+        long b[8];       // Q4_K: codes x the scale's low 3 bits; Q6_K: codes
+        long bh[8];      // Q4_K: codes x the scale's high 3 bits
+        long bm[8];      // Q4_K: the min in every byte
+        int scl[16];     // Q6_K: the 16 sub-block scales
+        float dw, dmin = 0.0f;
+        if constexpr (WT == SINTER_Q4_K) {
+            // ggml get_scale_min_k4 for sub-blocks 0..7, four at a time
+            const uint32_t s0 = cur.h[1], s1 = cur.h[2], s2 = cur.h[3];
+            const uint32_t dlo = s0 & 0x3F3F3F3Fu, mlo = s1 & 0x3F3F3F3Fu;
+            const uint32_t dhi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+            const uint32_t mhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+#pragma unroll
+            for (uint32_t s = 0; s < 8; s++) {
+                const uint32_t sd = ((s < 4 ? dlo : dhi) >> (8u * (s & 3u))) & 0xFFu;
+                const uint32_t sm = ((s < 4 ? mlo : mhi) >> (8u * (s & 3u))) & 0xFFu;
+                const uint32_t mm = sm * 0x01010101u;
+                bm[s] = pack64(mm, mm);
+                const uint32_t p = s >> 1, sh = 4u * (s & 1u);
+                const uint32_t q0 = (cur.q[2 * p] >> sh) & 0x0F0F0F0Fu, q1 = (cur.q[2 * p + 1] >> sh) & 0x0F0F0F0Fu;
+                // scale = 8 hi + lo (hi, lo <= 7): a code (<= 15) times either
+                // fits a byte (<= 105), so one 32-bit multiply scales four
+                // codes with no carry between them, and the products are
+                // int8 operands
+                const uint32_t lo = sd & 7u, hi = sd >> 3;
+                b[s] = pack64(q0 * lo, q1 * lo);
+                bh[s] = pack64(q0 * hi, q1 * hi);
+            }
+            dw = f16_bits_to_f32(cur.h[0] & 0xFFFFu);
+            dmin = f16_bits_to_f32(cur.h[0] >> 16);
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < 8; c++) {
+                const uint32_t n = c >> 2, q = c & 3u;
+                const uint32_t *L = (q & 1u) ? cur.l1 : cur.l0;
+                const uint32_t ls = 4u * (q >> 1), hs = 2u * q;
+                uint32_t lo = ((L[2 * n] >> ls) & 0x0F0F0F0Fu) | (((cur.hh[2 * n] >> hs) & 0x03030303u) << 4);
+                uint32_t hi = ((L[2 * n + 1] >> ls) & 0x0F0F0F0Fu) | (((cur.hh[2 * n + 1] >> hs) & 0x03030303u) << 4);
+                b[c] = pack64(sub32b(lo), sub32b(hi));
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 16; j++) scl[j] = (int)(int8_t)((cur.sc[j >> 2] >> (8u * (j & 3u))) & 0xFFu);
+            dw = f16_bits_to_f32(cur.d);
+        }
+
+#pragma unroll
+        for (uint32_t t = 0; t < UB_TILES; t++) {
+            if (t < ntiles) {
+                // A: token 16t + r, elements 32c + 8g..+7 (row stride 68 dwords: the
+                // 32 lanes of a half-wave read 32 distinct bank pairs)
+                const uint32_t *xa = xb + (UB_TOK * t + r) * UB_XSTRIDE + 2u * g;
+                long a[8];
+#pragma unroll
+                for (uint32_t c = 0; c < 8; c++) {
+                    const uint2 v2 = *(const uint2 *)(xa + 8u * c);
+                    a[c] = pack64(v2.x, v2.y);
+                }
+                float dx[4];
+#pragma unroll
+                for (uint32_t v = 0; v < 4; v++)
+                    dx[v] = __builtin_bit_cast(float, xb[(UB_TOK * t + 4u * g + v) * UB_XSTRIDE + 64u]);
+                const v4i z = {0, 0, 0, 0};
+                int isum[4] = {0, 0, 0, 0};
+                if constexpr (WT == SINTER_Q4_K) {
+                    // sum_s scale_s dot_s = 8 sum_s hi_s dot_s + sum_s lo_s dot_s, all
+                    // exact in int32 (|each| <= 256 * 105 * 128)
+                    v4i cm = z, ch = z, cl = z;
+#pragma unroll
+                    for (uint32_t s = 0; s < 8; s++) {
+                        cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], b[s], cl, 0, 0, 0);
+                        ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], bh[s], ch, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], bm[s], cm, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (uint32_t v = 0; v < 4; v++) {
+                        isum[v] = 8 * ch[v] + cl[v];
+                        const double dxd = (double)dx[v];
+                        const double t1 = ((double)dw * dxd) * (double)isum[v];
+                        const double t2 = ((double)dmin * dxd) * (double)cm[v];
+                        acc[t][v] += t1 - t2;
+                    }
+                } else {
+                    const bool lo_half = g < 2u;
+#pragma unroll
+                    for (uint32_t c = 0; c < 8; c++) {
+                        const long b0 = lo_half ? b[c] : 0l, b1 = lo_half ? 0l : b[c];
+                        const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[c], b0, z, 0, 0, 0);
+                        const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[c], b1, z, 0, 0, 0);
+                        // |scale| <= 128, |dot| <= 16 * 32 * 128: 24-bit products
+#pragma unroll
+                        for (uint32_t v = 0; v < 4; v++)
+                            isum[v] += __mul24(scl[2 * c], c0[v]) + __mul24(scl[2 * c + 1], c1[v]);
+                    }
+#pragma unroll
+                    for (uint32_t v = 0; v < 4; v++) acc[t][v] += ((double)dw * (double)dx[v]) * (double)isum[v];
+                }
+            }
+        }
+        if (i + 1u < nb) {
+            cur = nxt;
+            // buffer (i + 1) & 1 was last read for item i - 1, before the
+            // barrier that ended that item
+            if (stager) stage.st(xs[(i + 1u) & 1u]);
+        }
+        __syncthreads();
+    }
+
+    if (row < rows) {
+#pragma unroll
+        for (uint32_t t = 0; t < UB_TILES; t++)
+#pragma unroll
+            for (uint32_t v = 0; v < 4; v++) {
+                const uint32_t tok = tok0 + t * UB_TOK + 4u * g + v;
+                if (t < ntiles && tok < n_tok) y[(size_t)tok * rows + row] = (float)acc[t][v];
+            }
+    }
+}
+
+}  // namespace
+}  // namespace sinter
+
+using namespace sinter;
+
+extern "C" int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, const void *xq,
+                                     uint32_t n_tokens, float *y, void *stream) {
+    if (type != SINTER_Q4_K && type != SINTER_Q6_K)
+        return set_error(SINTER_ERR_ARG, "gemv_ubatch: weight type %d (Q4_K or Q6_K)", type);
+    if (rows <= 0 || rows > (int64_t)UINT32_MAX - UB_ROWS || k <= 0 || k % 256 != 0 || k / 256 > (int64_t)UINT32_MAX)
+        return set_error(SINTER_ERR_ARG, "gemv_ubatch: rows %lld / k %lld (k a positive multiple of 256)",
+                         (long long)rows, (long long)k);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!w || !xq || !y) return set_error(SINTER_ERR_ARG, "gemv_ubatch: null pointer");
+    const uintptr_t wa = type == SINTER_Q4_K ? 16u : 4u;
+    if ((uintptr_t)w % wa || (uintptr_t)xq % 4u || (uintptr_t)y % 4u)
+        return set_error(SINTER_ERR_ARG, "gemv_ubatch: alignment (weights %u B, activations and output 4 B)",
+                         (unsigned)wa);
+    const uint64_t n_rt = ((uint64_t)rows + UB_WG_ROWS - 1) / UB_WG_ROWS;
+    // token tiles per workgroup: 4 (weights read once per 64 tokens) unless
+    // that leaves fewer workgroups than CUs; then fewer, the row
+    // tile's token groups running side by side so its weights come from the
+    // memory-side cache after the first
+    uint32_t tpw = UB_TILES;
+    while (tpw > 1 && n_rt * (((uint64_t)n_tokens + UB_TOK * tpw - 1) / (UB_TOK * tpw)) < UB_MIN_WGS) tpw /= 2;
+    const uint64_t n_tg = ((uint64_t)n_tokens + UB_TOK * tpw - 1) / (UB_TOK * tpw);
+    if (n_rt * n_tg > (uint64_t)INT32_MAX) return set_error(SINTER_ERR_ARG, "gemv_ubatch: grid too large");
+    const uint32_t nb = (uint32_t)(k / 256);
+    const dim3 grid((uint32_t)(n_rt * n_tg)), block(UB_THREADS);
+    hipStream_t s = (hipStream_t)stream;
+    if (type == SINTER_Q4_K)
+        hipLaunchKernelGGL(ubatch_gemv_kernel<SINTER_Q4_K>, grid, block, 0, s, (const uint8_t *)w, (uint32_t)rows, nb,
+                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw);
+    else
+        hipLaunchKernelGGL(ubatch_gemv_kernel<SINTER_Q6_K>, grid, block, 0, s, (const uint8_t *)w, (uint32_t)rows, nb,
+                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw);
+    return hip_ok(hipGetLastError(), "gemv_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}

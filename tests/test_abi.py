@@ -94,6 +94,25 @@ def test_gemv_argument_validation_rejects_before_launch(sn):
     assert b"nkv * n_chunks" in L.sinter_last_error()
 
 
+def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
+    """The batched GEMV refuses unsupported types, shapes and alignments on
+    the host (SINTER_ERR_ARG, nothing launched); zero tokens is a no-op."""
+    L = sn.lib()
+    f = L.sinter_op_gemv_ubatch
+    W, X, Y = C.c_void_p(4096), C.c_void_p(8192), C.c_void_p(16384)
+    assert f(sn.Q8_0, W, 16, 256, X, 4, Y, None) == sn.ERR_ARG
+    assert b"Q4_K or Q6_K" in L.sinter_last_error()
+    assert f(sn.Q4_K, W, 16, 300, X, 4, Y, None) == sn.ERR_ARG
+    assert b"multiple of 256" in L.sinter_last_error()
+    assert f(sn.Q4_K, W, 0, 256, X, 4, Y, None) == sn.ERR_ARG
+    assert f(sn.Q4_K, W, 16, 256, X, 0, Y, None) == sn.OK
+    assert f(sn.Q4_K, None, 16, 256, X, 4, Y, None) == sn.ERR_ARG
+    assert f(sn.Q4_K, C.c_void_p(4100), 16, 256, X, 4, Y, None) == sn.ERR_ARG      # Q4_K: 16-byte weights
+    assert b"alignment" in L.sinter_last_error()
+    assert f(sn.Q6_K, W, 16, 256, C.c_void_p(8194), 4, Y, None) == sn.ERR_ARG      # activations: 4 bytes
+    assert f(sn.Q6_K, C.c_void_p(4098), 16, 256, X, 4, Y, None) == sn.ERR_ARG      # Q6_K: 4-byte weights
+
+
 def test_model_config_validation(sn):
     L = sn.lib()
     cfg = sn.qwen36_27b_config()

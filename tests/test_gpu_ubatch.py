@@ -1,0 +1,78 @@
+"""GPU parity of the batched GEMV over a ubatch of tokens
+(sinter_op_gemv_ubatch, the trunk GEMM of a batched prefill) against the CPU
+oracle.  Each token's outputs must equal the oracle's single-token GEMV of
+that token bit for bit: the kernel computes the integer dot products on
+int8 MFMA, but the fp64 item terms and their fold in item order are the
+oracle's (oracle/oracle.c or_block_term / or_gemv_q), and the single-token
+device GEMV is bit-exact against the same oracle (test_gpu_ops.py).
+
+Shapes cover one token, token counts that are not a multiple of the 16-token
+tile or of the 64-token weight pass, row counts that are not a multiple of
+the 16-row tile, odd block counts per row (Q6_K's 210-byte blocks then start
+on both 4-byte phases), K up to 17408, zero activations and activations over
+six decades of scale.  A second test fills the weight blocks with random
+bytes (every scale, min and code pattern, Q6_K's -128 scale included) with
+finite f16 block scales.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from test_gpu_ops import dev, empty_f32, host, stream, synth_w, xvec
+
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K = 12, 14
+
+
+def activations(k, n_tok, seed):
+    xs = []
+    for j in range(n_tok):
+        if j % 11 == 5:
+            xs.append(np.zeros(k, np.float32))          # d = 0: every term is 0
+        else:
+            x = xvec(k, seed + j, zero_block=(j % 3 == 0))
+            xs.append((x * np.float32(10.0 ** ((j % 7) - 3))).astype(np.float32))
+    return xs
+
+
+def run_ubatch(sn, orc, torch, t, w, rows, k, xs):
+    n_tok = len(xs)
+    xq = np.concatenate([orc.quantize(t, x) for x in xs])
+    dw, dxq, dy = dev(torch, w), dev(torch, xq), empty_f32(torch, n_tok * rows)
+    print(f"gemv_ubatch type={t} rows={rows} k={k} tokens={n_tok}", flush=True)
+    rc = sn.lib().sinter_op_gemv_ubatch(t, C.c_void_p(dw.data_ptr()), rows, k, C.c_void_p(dxq.data_ptr()),
+                                        n_tok, C.c_void_p(dy.data_ptr()), C.c_void_p(stream(torch)))
+    sn.check(rc, "gemv_ubatch")
+    torch.cuda.synchronize()
+    return host(dy).reshape(n_tok, rows)
+
+
+@pytest.mark.parametrize("t,rows,k,n_tok", [
+    (Q4_K, 48, 256, 1), (Q4_K, 100, 5120, 5), (Q4_K, 1024, 5120, 64), (Q4_K, 300, 6144, 70),
+    (Q4_K, 33, 17408, 17),
+    (Q6_K, 48, 5120, 1), (Q6_K, 37, 768, 33), (Q6_K, 256, 17408, 16), (Q6_K, 130, 1280, 129)])
+def test_gemv_ubatch_matches_per_token_gemv(sn, orc, torch_gpu, t, rows, k, n_tok):
+    w = synth_w(sn, t, rows, k, 500 + t + k + rows)
+    xs = activations(k, n_tok, 1000 + rows)
+    got = run_ubatch(sn, orc, torch_gpu, t, w, rows, k, xs)
+    for j, x in enumerate(xs):
+        assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x)), j
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_gemv_ubatch_random_block_bytes(sn, orc, torch_gpu, t):
+    rows, k, n_tok = 80, 2304, 23           # 9 blocks per row
+    rng = np.random.default_rng(77 + t)
+    w = rng.integers(0, 256, sn.row_bytes(t, k) * rows, dtype=np.uint8)
+    blocks = w.reshape(rows * (k // 256), sn.BLOCK_BYTES[t])
+    d = rng.standard_normal((blocks.shape[0], 2)).astype(np.float16)
+    if t == Q4_K:
+        blocks[:, 0:4] = d.view(np.uint8)            # d, dmin
+    else:
+        blocks[:, 208:210] = d[:, :1].view(np.uint8)  # d
+    xs = activations(k, n_tok, 3000 + t)
+    got = run_ubatch(sn, orc, torch_gpu, t, w, rows, k, xs)
+    for j, x in enumerate(xs):
+        assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x)), j
