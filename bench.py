@@ -231,6 +231,132 @@ def op_bench(args):
     print(json.dumps(line), flush=True)
 
 
+UBATCH_MATS = (  # one gated-DeltaNet layer's trunk matrices in the Q4_K_M mix: (name, type, rows, k)
+    ("ssm_qkv", 12, 8192, 5120), ("ssm_z", 12, 4096, 5120), ("ssm_beta", 12, 32, 5120),
+    ("ssm_alpha", 12, 32, 5120), ("ssm_out", 12, 5120, 4096), ("ffn_gate", 12, 17408, 5120),
+    ("ffn_up", 12, 17408, 5120), ("ffn_down", 14, 5120, 17408))
+MFMA_INT8_PEAK_TOPS = 5000.0
+
+
+def ubatch_bench(args):
+    """The batched GEMV of a batched prefill (sinter_op_gemv_ubatch) over one
+    gated-DeltaNet layer's trunk matrices (qkv, z, beta, alpha, out, gate,
+    up, down: 220.8 MB at Q4_K / Q6_K) for a ubatch of --ubatch tokens.  A
+    step is the eight launches over one of >= 4 rotated weight copies (past
+    the 256 MB memory-side cache).  Weights are synthetic (seeded, on the
+    device), activations seeded Q8_K blocks; results are bit-identical per
+    token to the single-token GEMV (tests/test_gpu_ubatch.py).  The roofline
+    is int8 MFMA: the integer multiply-adds of the step over its time."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    import sinter
+    L = sinter.lib()
+    T = args.ubatch
+    s = torch.cuda.current_stream()
+    sp = C.c_void_p(s.cuda_stream)
+    layer_bytes = sum(sinter.row_bytes(t, k) * r for _, t, r, k in UBATCH_MATS)
+    n_copy = max(4, int(np.ceil(1.0e9 / layer_bytes)))
+    copies = []
+    for c in range(n_copy):
+        mats = []
+        for j, (_, t, r, k) in enumerate(UBATCH_MATS):
+            w = torch.empty(sinter.row_bytes(t, k) * r, dtype=torch.uint8, device="cuda")
+            sinter.check(L.sinter_synth(1, C.c_void_p(w.data_ptr()), 0, t, r, k, args.seed + 97 * c + j, 0, 0, sp),
+                         "synth")
+            mats.append(w)
+        copies.append(mats)
+    rng = np.random.default_rng(args.seed)
+    xq = {}
+    for k in sorted({k for _, _, _, k in UBATCH_MATS}):
+        nb = k // 256
+        blk = np.zeros((T * nb, 292), np.uint8)
+        blk[:, 0:4] = (np.abs(rng.standard_normal((T * nb, 1))) * 0.01 + 1e-3).astype(np.float32).view(np.uint8)
+        blk[:, 4:260] = rng.integers(-127, 128, (T * nb, 256)).astype(np.int8).view(np.uint8)
+        xq[k] = torch.from_numpy(blk.reshape(-1)).cuda()
+    ys = [torch.empty(T * r, dtype=torch.float32, device="cuda") for _, _, r, _ in UBATCH_MATS]
+
+    def launch(c, j):
+        _, t, r, k = UBATCH_MATS[j]
+        sinter.check(L.sinter_op_gemv_ubatch(t, C.c_void_p(copies[c][j].data_ptr()), r, k,
+                                             C.c_void_p(xq[k].data_ptr()), T, C.c_void_p(ys[j].data_ptr()), sp),
+                     "gemv_ubatch")
+
+    for i in range(args.warmup):
+        for j in range(len(UBATCH_MATS)):
+            launch(i % n_copy, j)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(args.steps):
+        for j in range(len(UBATCH_MATS)):
+            launch(i % n_copy, j)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    # per-matrix launch time (events around each launch, a second timed run)
+    per = []
+    for j, (name, t, r, k) in enumerate(UBATCH_MATS):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(s)
+        for i in range(args.steps):
+            launch(i % n_copy, j)
+        ev[1].record(s)
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) / args.steps * 1e3
+        per.append({"matrix": name, "type": "Q4_K" if t == 12 else "Q6_K", "rows": r, "k": k, "us": round(us, 2),
+                    "tops": round(2.0 * r * k * T / (us * 1e-6) / 1e12, 1)})
+    macs = sum(r * k for _, _, r, k in UBATCH_MATS)
+    tops = 2.0 * macs * T / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "prefill trunk GEMM: tokens/s through one gated-DeltaNet layer's matrices (batched GEMV, "
+                  "sinter_op_gemv_ubatch)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 (fp64 item terms)",
+        "data": "synthetic (seeded random-init Q4_K / Q6_K weights, seeded Q8_K activations)",
+        "config": {"workload": f"ubatch of {T} tokens x one GDN layer's trunk (Qwen3.6-27B shapes, Q4_K_M mix)",
+                   "ubatch": T, "weight_bytes_per_step": layer_bytes, "weight_copies_rotated": n_copy,
+                   "per_matrix": per},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "ubatch_gemv_kernel",
+                     "weights_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = ubatch_cpu_baseline(args)
+    print(json.dumps(line), flush=True)
+
+
+def ubatch_cpu_baseline(args):
+    """The same layer trunk on the CPU oracle (or_gemv, one token at a time):
+    tokens/s over 2 tokens after a warmup token."""
+    import numpy as np
+    import oracle
+    import sinter
+    mats = []
+    for j, (_, t, r, k) in enumerate(UBATCH_MATS):
+        w = np.zeros(sinter.row_bytes(t, k) * r, np.uint8)
+        sinter.check(sinter.lib().sinter_synth(0, w.ctypes.data, 0, t, r, k, args.seed + j, 0, 0, None), "synth")
+        mats.append(w)
+    xs = {k: np.random.default_rng(args.seed + k).standard_normal(k).astype(np.float32)
+          for k in {k for _, _, _, k in UBATCH_MATS}}
+
+    def one():
+        for j, (_, t, r, k) in enumerate(UBATCH_MATS):
+            oracle.gemv(t, mats[j], r, k, xs[k])
+
+    one()
+    t0 = time.perf_counter()
+    for _ in range(2):
+        one()
+    sec = (time.perf_counter() - t0) / 2
+    threads = cpu_threads()
+    return {"value": round(1.0 / sec, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{CPU_LABEL}, {cpu_isa()}, {threads} threads): or_gemv over the eight matrices per token "
+                      f"(Q8_K quantise + rows), 1 warmup + 2 timed tokens, mean {sec * 1e3:.1f} ms/token"}
+
+
 def op_cpu_baseline(m, c, pos):
     """The same op group on the CPU oracle (layer 0's weights and state),
     median of 5 after a warmup."""
@@ -359,6 +485,9 @@ def main():
                     help="only check parity: from a fresh synthetic context, N greedy decode steps on the GPU "
                          "and on the CPU oracle (same weights and state); token ids must be identical, logits "
                          "within rel L2 1e-2; prints one JSON line and exits")
+    ap.add_argument("--ubatch", type=int, default=0, metavar="T",
+                    help="measure the batched GEMV of a batched prefill: T tokens through one GDN layer's "
+                         "trunk matrices (sinter_op_gemv_ubatch) instead of the decode")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 3 times (the HIP runtime's copy kernel) and exit: the "
                          "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -393,6 +522,9 @@ def main():
         print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
         return
 
+    if args.ubatch:
+        ubatch_bench(args)
+        return
     if args.config in (1, 2, 3):
         op_bench(args)
         return
