@@ -295,6 +295,14 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
  * alignment (nothing launched). */
 int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, const void *xq,
                           uint32_t n_tokens, float *y, void *stream);
+/* The activation side of the same GEMM: x (n_tokens x k f32, row-major,
+ * 16-byte aligned, finite) to n_tokens Q8_K activations at xq (k / 256
+ * blocks of 292 bytes each, 4-byte aligned), ggml's quantize_row_q8_K_ref
+ * (the fork's prefill quantises its activations the same way for MMQ,
+ * docs/PREFILL-SEMANTICS.md:303, there to q8_1), bit-identical to the
+ * single-token GEMV's Q8_K quantiser.  n_tokens == 0 is a no-op;
+ * SINTER_ERR_ARG on a bad shape or alignment. */
+int sinter_quant_q8k_ubatch(const float *x, int64_t k, uint32_t n_tokens, void *xq, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

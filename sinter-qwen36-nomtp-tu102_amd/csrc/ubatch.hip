@@ -308,6 +308,53 @@ __global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *
     }
 }
 
+// ggml quantize_row_q8_K_ref over a ubatch (the oracle's or_quant_q8_K):
+// one wave per 256-element block, lane l holding elements 4l..4l+3.  The
+// block's scale comes from its first element of largest |x| (sequentially:
+// `if (|x| > amax)`, so a tie keeps the lower index -- the wave reduction
+// breaks ties by index), iscale = -127 / that element, codes
+// min(127, rint(iscale * x)) (ggml's nearest_int: round half to even), d =
+// 1 / iscale, bsums the 16-element sums of the codes; an all-zero block is
+// all zeros.  Inputs are finite.
+__global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__ x, uint8_t *__restrict__ xq) {
+    const uint32_t lane = threadIdx.x;
+    const size_t blk = blockIdx.x;   // token * (k / 256) + block: x and xq in the same order
+    const float4 v = ((const float4 *)(x + blk * 256u))[lane];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    float amax = 0.0f, mx = 0.0f;
+    uint32_t idx = 0xFFFFFFFFu;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; j++) {
+        const float ax = fabsf(e[j]);
+        if (ax > amax) { amax = ax; mx = e[j]; idx = 4u * lane + j; }
+    }
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const float a2 = __shfl_xor(amax, o), m2 = __shfl_xor(mx, o);
+        const uint32_t i2 = __shfl_xor(idx, o);
+        if (a2 > amax || (a2 == amax && i2 < idx)) { amax = a2; mx = m2; idx = i2; }
+    }
+    uint8_t *ob = xq + blk * Q8K_BYTES;
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (amax != 0.0f) {
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const int t = (int)rintf(iscale * e[j]);
+            q[j] = t < 127 ? t : 127;
+        }
+        d = 1.0f / iscale;
+    }
+    *(uint32_t *)(ob + 4u + 4u * lane) =
+        (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)q[3] << 24);
+    int bs = q[0] + q[1] + q[2] + q[3];
+    bs += __shfl_xor(bs, 1);
+    bs += __shfl_xor(bs, 2);
+    if ((lane & 3u) == 0) *(int16_t *)(ob + 260u + 2u * (lane >> 2)) = (int16_t)bs;
+    if (lane == 0) *(float *)ob = d;
+}
+
 }  // namespace
 }  // namespace sinter
 
@@ -345,4 +392,17 @@ extern "C" int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int6
         hipLaunchKernelGGL(ubatch_gemv_kernel<SINTER_Q6_K>, grid, block, 0, s, (const uint8_t *)w, (uint32_t)rows, nb,
                            (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw);
     return hip_ok(hipGetLastError(), "gemv_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+extern "C" int sinter_quant_q8k_ubatch(const float *x, int64_t k, uint32_t n_tokens, void *xq, void *stream) {
+    if (k <= 0 || k % 256 != 0) return set_error(SINTER_ERR_ARG, "quant_q8k_ubatch: k %lld (a positive multiple of 256)",
+                                                 (long long)k);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!x || !xq) return set_error(SINTER_ERR_ARG, "quant_q8k_ubatch: null pointer");
+    if ((uintptr_t)x % 16u || (uintptr_t)xq % 4u)
+        return set_error(SINTER_ERR_ARG, "quant_q8k_ubatch: alignment (x 16 bytes, xq 4 bytes)");
+    const uint64_t n_blk = (uint64_t)n_tokens * (uint64_t)(k / 256);
+    if (n_blk > (uint64_t)INT32_MAX) return set_error(SINTER_ERR_ARG, "quant_q8k_ubatch: too many blocks");
+    hipLaunchKernelGGL(quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, x, (uint8_t *)xq);
+    return hip_ok(hipGetLastError(), "quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }

@@ -95,8 +95,9 @@ def test_gemv_argument_validation_rejects_before_launch(sn):
 
 
 def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
-    """The batched GEMV refuses unsupported types, shapes and alignments on
-    the host (SINTER_ERR_ARG, nothing launched); zero tokens is a no-op."""
+    """The batched GEMV and its Q8_K quantiser refuse unsupported types,
+    shapes and alignments on the host (SINTER_ERR_ARG, nothing launched);
+    zero tokens is a no-op."""
     L = sn.lib()
     f = L.sinter_op_gemv_ubatch
     W, X, Y = C.c_void_p(4096), C.c_void_p(8192), C.c_void_p(16384)
@@ -111,6 +112,13 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     assert b"alignment" in L.sinter_last_error()
     assert f(sn.Q6_K, W, 16, 256, C.c_void_p(8194), 4, Y, None) == sn.ERR_ARG      # activations: 4 bytes
     assert f(sn.Q6_K, C.c_void_p(4098), 16, 256, X, 4, Y, None) == sn.ERR_ARG      # Q6_K: 4-byte weights
+    q = L.sinter_quant_q8k_ubatch
+    assert q(X, 300, 4, Y, None) == sn.ERR_ARG
+    assert b"multiple of 256" in L.sinter_last_error()
+    assert q(X, 256, 0, Y, None) == sn.OK
+    assert q(C.c_void_p(8196), 256, 4, Y, None) == sn.ERR_ARG                        # x: 16 bytes
+    assert q(X, 256, 4, C.c_void_p(16386), None) == sn.ERR_ARG                       # xq: 4 bytes
+    assert q(None, 256, 4, Y, None) == sn.ERR_ARG
 
 
 def test_model_config_validation(sn):

@@ -13,6 +13,12 @@ on both 4-byte phases), K up to 17408, zero activations and activations over
 six decades of scale.  A second test fills the weight blocks with random
 bytes (every scale, min and code pattern, Q6_K's -128 scale included) with
 finite f16 block scales.
+
+The ubatch Q8_K quantiser (sinter_quant_q8k_ubatch) is compared byte for
+byte with the oracle's (or_quant_q8_K: ggml quantize_row_q8_K_ref), over an
+all-zero block, a block of tied |x| whose first largest element sets the
+sign, and magnitudes from 1e-4 to 1e4; chained with the batched GEMV it must
+reproduce the oracle's f32 GEMV of every token.
 """
 import ctypes as C
 
@@ -76,3 +82,52 @@ def test_gemv_ubatch_random_block_bytes(sn, orc, torch_gpu, t):
     got = run_ubatch(sn, orc, torch_gpu, t, w, rows, k, xs)
     for j, x in enumerate(xs):
         assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x)), j
+
+
+def quant_inputs(k, n_tok, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n_tok, k)).astype(np.float32)
+    x[0, :256] = 0.0                                    # an all-zero block
+    if k >= 512:
+        x[0, 256:512] = 0.5 * np.sign(x[0, 256:512])       # every |x| tied: the first element sets the sign
+        x[0, 300] = -3.0                                 # a tie between the first and a later larger |x|
+        x[0, 400] = 3.0
+    for t in range(1, n_tok):
+        x[t] *= np.float32(10.0 ** ((t % 9) - 4))         # 1e-4 .. 1e4
+    return x
+
+
+@pytest.mark.parametrize("k,n_tok", [(256, 1), (5120, 7), (17408, 33)])
+def test_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, k, n_tok):
+    torch = torch_gpu
+    x = quant_inputs(k, n_tok, 40 + k)
+    dx = dev(torch, x.reshape(-1))
+    dq = torch.zeros(n_tok * sn.row_bytes(sn.Q8_K, k), dtype=torch.uint8, device="cuda")
+    print(f"quant_q8k_ubatch k={k} tokens={n_tok}", flush=True)
+    sn.check(sn.lib().sinter_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()), k, n_tok, C.c_void_p(dq.data_ptr()),
+                                              C.c_void_p(stream(torch))), "quant_q8k_ubatch")
+    torch.cuda.synchronize()
+    got = host(dq).reshape(n_tok, -1)
+    for t in range(n_tok):
+        assert np.array_equal(got[t], orc.quantize(Q4_K, x[t])), t
+
+
+@pytest.mark.parametrize("t,rows,k,n_tok", [(Q4_K, 200, 5120, 40), (Q6_K, 96, 17408, 20)])
+def test_device_quantised_ubatch_equals_oracle_gemv(sn, orc, torch_gpu, t, rows, k, n_tok):
+    """f32 activations quantised on the device, then the batched GEMV: each
+    token's outputs equal the oracle's GEMV of that f32 vector."""
+    torch = torch_gpu
+    w = synth_w(sn, t, rows, k, 900 + t)
+    x = quant_inputs(k, n_tok, 60 + t)
+    dw, dx, dy = dev(torch, w), dev(torch, x.reshape(-1)), empty_f32(torch, n_tok * rows)
+    dq = torch.zeros(n_tok * sn.row_bytes(sn.Q8_K, k), dtype=torch.uint8, device="cuda")
+    s = C.c_void_p(stream(torch))
+    print(f"quant + gemv_ubatch type={t} rows={rows} k={k} tokens={n_tok}", flush=True)
+    sn.check(sn.lib().sinter_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()), k, n_tok, C.c_void_p(dq.data_ptr()), s),
+             "quant")
+    sn.check(sn.lib().sinter_op_gemv_ubatch(t, C.c_void_p(dw.data_ptr()), rows, k, C.c_void_p(dq.data_ptr()), n_tok,
+                                            C.c_void_p(dy.data_ptr()), s), "gemv_ubatch")
+    torch.cuda.synchronize()
+    got = host(dy).reshape(n_tok, rows)
+    for j in range(n_tok):
+        assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x[j])), j
