@@ -303,6 +303,14 @@ int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, cons
  * single-token GEMV's Q8_K quantiser.  n_tokens == 0 is a no-op;
  * SINTER_ERR_ARG on a bad shape or alignment. */
 int sinter_quant_q8k_ubatch(const float *x, int64_t k, uint32_t n_tokens, void *xq, void *stream);
+/* RMSNorm fused ahead of the same quantiser (op_rmsnorm + the activation
+ * quantiser, k0/ops/glue.cuh:56-152 and gemv.cuh:213-237, over a ubatch):
+ * token t's row x[t] (k f32) is normalised as the single-token GEMV's
+ * RMSNORM prologue does (fp32 squares summed in fp64, mean rounded to fp32,
+ * scale = 1 / sqrtf(mean + eps), y = (x * scale) * w; w may be NULL for no
+ * weight), then quantised to Q8_K at xq.  x and w 16-byte aligned, xq 4. */
+int sinter_rmsnorm_quant_q8k_ubatch(const float *x, const float *w, float eps, int64_t k, uint32_t n_tokens,
+                                    void *xq, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -316,11 +316,7 @@ __global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *
 // min(127, rint(iscale * x)) (ggml's nearest_int: round half to even), d =
 // 1 / iscale, bsums the 16-element sums of the codes; an all-zero block is
 // all zeros.  Inputs are finite.
-__global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__ x, uint8_t *__restrict__ xq) {
-    const uint32_t lane = threadIdx.x;
-    const size_t blk = blockIdx.x;   // token * (k / 256) + block: x and xq in the same order
-    const float4 v = ((const float4 *)(x + blk * 256u))[lane];
-    const float e[4] = {v.x, v.y, v.z, v.w};
+__device__ __forceinline__ void quant_block_q8k(const float e[4], uint32_t lane, uint8_t *ob) {
     float amax = 0.0f, mx = 0.0f;
     uint32_t idx = 0xFFFFFFFFu;
 #pragma unroll
@@ -334,7 +330,6 @@ __global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__
         const uint32_t i2 = __shfl_xor(idx, o);
         if (a2 > amax || (a2 == amax && i2 < idx)) { amax = a2; mx = m2; idx = i2; }
     }
-    uint8_t *ob = xq + blk * Q8K_BYTES;
     int q[4] = {0, 0, 0, 0};
     float d = 0.0f;
     if (amax != 0.0f) {
@@ -353,6 +348,53 @@ __global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__
     bs += __shfl_xor(bs, 2);
     if ((lane & 3u) == 0) *(int16_t *)(ob + 260u + 2u * (lane >> 2)) = (int16_t)bs;
     if (lane == 0) *(float *)ob = d;
+}
+
+__global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__ x, uint8_t *__restrict__ xq) {
+    const uint32_t lane = threadIdx.x;
+    const size_t blk = blockIdx.x;   // token * (k / 256) + block: x and xq in the same order
+    const float4 v = ((const float4 *)(x + blk * 256u))[lane];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
+}
+
+// RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
+// single-token GEMV's SINTER_PRO_RMSNORM prologue and of the oracle's
+// or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded to fp32,
+// scale = 1 / sqrtf(mean + eps), y = (x * scale) * w).  The fp64 sum is a
+// fixed tree: each thread's float4 groups in order, then the wave (xor
+// shuffles), then the four waves in order.  Then wave v quantises blocks
+// v, v + 4, ... of the normalised row.
+__global__ __launch_bounds__(256) void rmsnorm_quant_q8k_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                               float eps, uint32_t k, uint8_t *__restrict__ xq) {
+    __shared__ double red[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    const float *xr = x + (size_t)blockIdx.x * k;
+    double s = 0.0;
+    for (uint32_t j = tid; j < k / 4u; j += 256u) {
+        const float4 v = ((const float4 *)xr)[j];
+        s += (double)(v.x * v.x);
+        s += (double)(v.y * v.y);
+        s += (double)(v.z * v.z);
+        s += (double)(v.w * v.w);
+    }
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    s = ((red[0] + red[1]) + red[2]) + red[3];
+    const float mean = (float)(s / (double)k);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    uint8_t *orow = xq + (size_t)blockIdx.x * (k / 256u) * Q8K_BYTES;
+    for (uint32_t b = wv; b < k / 256u; b += 4u) {
+        const float4 v = ((const float4 *)(xr + 256u * b))[lane];
+        float e[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+        if (w) {
+            const float4 g = ((const float4 *)(w + 256u * b))[lane];
+            e[0] = e[0] * g.x; e[1] = e[1] * g.y; e[2] = e[2] * g.z; e[3] = e[3] * g.w;
+        }
+        quant_block_q8k(e, lane, orow + (size_t)b * Q8K_BYTES);
+    }
 }
 
 }  // namespace
@@ -405,4 +447,18 @@ extern "C" int sinter_quant_q8k_ubatch(const float *x, int64_t k, uint32_t n_tok
     if (n_blk > (uint64_t)INT32_MAX) return set_error(SINTER_ERR_ARG, "quant_q8k_ubatch: too many blocks");
     hipLaunchKernelGGL(quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, x, (uint8_t *)xq);
     return hip_ok(hipGetLastError(), "quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+extern "C" int sinter_rmsnorm_quant_q8k_ubatch(const float *x, const float *w, float eps, int64_t k, uint32_t n_tokens,
+                                               void *xq, void *stream) {
+    if (k <= 0 || k % 256 != 0 || k > (int64_t)UINT32_MAX)
+        return set_error(SINTER_ERR_ARG, "rmsnorm_quant_q8k_ubatch: k %lld (a positive multiple of 256)", (long long)k);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!x || !xq) return set_error(SINTER_ERR_ARG, "rmsnorm_quant_q8k_ubatch: null pointer");
+    if ((uintptr_t)x % 16u || (uintptr_t)w % 16u || (uintptr_t)xq % 4u)
+        return set_error(SINTER_ERR_ARG, "rmsnorm_quant_q8k_ubatch: alignment (x, w 16 bytes, xq 4 bytes)");
+    if (!(eps >= 0.0f)) return set_error(SINTER_ERR_ARG, "rmsnorm_quant_q8k_ubatch: eps must be >= 0");
+    hipLaunchKernelGGL(rmsnorm_quant_q8k_kernel, dim3(n_tokens), dim3(256), 0, (hipStream_t)stream, x, w, eps,
+                       (uint32_t)k, (uint8_t *)xq);
+    return hip_ok(hipGetLastError(), "rmsnorm_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }

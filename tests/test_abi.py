@@ -119,6 +119,11 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     assert q(C.c_void_p(8196), 256, 4, Y, None) == sn.ERR_ARG                        # x: 16 bytes
     assert q(X, 256, 4, C.c_void_p(16386), None) == sn.ERR_ARG                       # xq: 4 bytes
     assert q(None, 256, 4, Y, None) == sn.ERR_ARG
+    n = L.sinter_rmsnorm_quant_q8k_ubatch
+    assert n(X, None, C.c_float(1e-6), 300, 4, Y, None) == sn.ERR_ARG
+    assert n(X, None, C.c_float(1e-6), 256, 0, Y, None) == sn.OK
+    assert n(X, C.c_void_p(8196), C.c_float(1e-6), 256, 4, Y, None) == sn.ERR_ARG   # w: 16 bytes
+    assert n(X, None, C.c_float(-1.0), 256, 4, Y, None) == sn.ERR_ARG
 
 
 def test_model_config_validation(sn):

@@ -131,3 +131,26 @@ def test_device_quantised_ubatch_equals_oracle_gemv(sn, orc, torch_gpu, t, rows,
     got = host(dy).reshape(n_tok, rows)
     for j in range(n_tok):
         assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x[j])), j
+
+
+@pytest.mark.parametrize("k,n_tok,weighted", [(5120, 9, True), (17408, 5, False), (6144, 3, True)])
+def test_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, k, n_tok, weighted):
+    """RMSNorm (the single-token GEMV's RMSNORM prologue) then Q8_K over a
+    ubatch: byte for byte the oracle's or_rmsnorm then or_quant_q8_K."""
+    torch = torch_gpu
+    x = quant_inputs(k, n_tok, 80 + k)
+    x[0, :256] = 0.0
+    w = (1.0 + 0.1 * np.random.default_rng(k).standard_normal(k)).astype(np.float32) if weighted else None
+    eps = 1e-6
+    dx = dev(torch, x.reshape(-1))
+    dwt = dev(torch, w) if weighted else None
+    dq = torch.zeros(n_tok * sn.row_bytes(sn.Q8_K, k), dtype=torch.uint8, device="cuda")
+    print(f"rmsnorm_quant_q8k_ubatch k={k} tokens={n_tok} weighted={weighted}", flush=True)
+    sn.check(sn.lib().sinter_rmsnorm_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()),
+                                                      C.c_void_p(dwt.data_ptr()) if weighted else None, eps, k, n_tok,
+                                                      C.c_void_p(dq.data_ptr()), C.c_void_p(stream(torch))),
+             "rmsnorm_quant")
+    torch.cuda.synchronize()
+    got = host(dq).reshape(n_tok, -1)
+    for t in range(n_tok):
+        assert np.array_equal(got[t], orc.quantize(Q4_K, orc.rmsnorm(x[t], w, eps))), t
