@@ -279,7 +279,7 @@ def ubatch_bench(args):
     def launch(c, j):
         _, t, r, k = UBATCH_MATS[j]
         sinter.check(L.sinter_op_gemv_ubatch(t, C.c_void_p(copies[c][j].data_ptr()), r, k,
-                                             C.c_void_p(xq[k].data_ptr()), T, C.c_void_p(ys[j].data_ptr()), sp),
+                                             C.c_void_p(xq[k].data_ptr()), T, C.c_void_p(ys[j].data_ptr()), 0, sp),
                      "gemv_ubatch")
 
     for i in range(args.warmup):

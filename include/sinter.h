@@ -289,12 +289,14 @@ int sinter_op_attn_decode(const sinter_attn_args *a, uint32_t blocks, void *stre
  * multiple of 256) dotted with token t's Q8_K activation (xq + t * (k / 256)
  * blocks of 292 bytes), for t < n_tokens: the single-token GEMV's fp64 item
  * terms folded in item order, so each y[t] is bit-identical to
- * sinter_op_gemv on token t alone.  Weights are read once per 64 tokens.
+ * sinter_op_gemv on token t alone.  accumulate != 0: y[t * rows + r] +=
+ * the result instead (the RESID epilogue's residual add).  Weights are read
+ * once per 64 tokens.
  * Alignment: w 16 bytes (Q4_K) / 4 bytes (Q6_K), xq and y 4 bytes.
  * n_tokens == 0 is a no-op.  SINTER_ERR_ARG on a bad type, shape or
  * alignment (nothing launched). */
 int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, const void *xq,
-                          uint32_t n_tokens, float *y, void *stream);
+                          uint32_t n_tokens, float *y, int accumulate, void *stream);
 /* The activation side of the same GEMM: x (n_tokens x k f32, row-major,
  * 16-byte aligned, finite) to n_tokens Q8_K activations at xq (k / 256
  * blocks of 292 bytes each, 4-byte aligned), ggml's quantize_row_q8_K_ref
@@ -311,6 +313,13 @@ int sinter_quant_q8k_ubatch(const float *x, int64_t k, uint32_t n_tokens, void *
  * weight), then quantised to Q8_K at xq.  x and w 16-byte aligned, xq 4. */
 int sinter_rmsnorm_quant_q8k_ubatch(const float *x, const float *w, float eps, int64_t k, uint32_t n_tokens,
                                     void *xq, void *stream);
+/* SwiGLU fused ahead of the same quantiser (the fused gate/up epilogue,
+ * k0/ops/gemv.cuh:327-347, over a ubatch): f = silu(gate) * up elementwise
+ * (silu(x) = x / (1 + exp(-x)), the exponential in fp64 as in the
+ * single-token GEMV's SWIGLU epilogue), gate and up n_tokens x k f32
+ * (16-byte aligned), then quantised to Q8_K at xq for the down projection. */
+int sinter_swiglu_quant_q8k_ubatch(const float *gate, const float *up, int64_t k, uint32_t n_tokens, void *xq,
+                                   void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

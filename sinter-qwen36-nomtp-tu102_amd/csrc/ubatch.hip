@@ -30,6 +30,7 @@
 // forms the fp64 term of its four (token, row) pairs from its own row's
 // scales and folds it into its accumulators.
 #include "internal.h"
+#include "dev_common.h"
 
 namespace sinter {
 namespace {
@@ -152,7 +153,7 @@ template <int WT>
 __global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *__restrict__ w, uint32_t rows,
                                                                 uint32_t nb, const uint8_t *__restrict__ xq,
                                                                 uint32_t n_tok, float *__restrict__ y, uint32_t n_tg,
-                                                                uint32_t tpw) {
+                                                                uint32_t tpw, uint32_t accumulate) {
     __shared__ uint32_t xs[2][UB_TOKENS * UB_XSTRIDE];
     const uint32_t lane = threadIdx.x & 63u, wv = threadIdx.x >> 6, r = lane & 15u, g = lane >> 4;
     // adjacent workgroups share a row tile (their token groups): its weight
@@ -303,7 +304,12 @@ __global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *
 #pragma unroll
             for (uint32_t v = 0; v < 4; v++) {
                 const uint32_t tok = tok0 + t * UB_TOK + 4u * g + v;
-                if (t < ntiles && tok < n_tok) y[(size_t)tok * rows + row] = (float)acc[t][v];
+                if (t < ntiles && tok < n_tok) {
+                    // accumulate: the residual add of the single-token GEMV's
+                    // RESID epilogue (y = y + result, one fp32 add)
+                    float *yp = y + (size_t)tok * rows + row;
+                    *yp = accumulate ? *yp + (float)acc[t][v] : (float)acc[t][v];
+                }
             }
     }
 }
@@ -358,6 +364,19 @@ __global__ __launch_bounds__(64) void quant_q8k_kernel(const float *__restrict__
     quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
 }
 
+// SwiGLU then the Q8_K quantiser over a ubatch: f = silu(gate) * up (the
+// single-token GEMV's SWIGLU epilogue and the oracle's or_ffn: silu(x) =
+// x / (1 + (float)exp(-(double)x))), quantised for the down projection.
+__global__ __launch_bounds__(64) void swiglu_quant_q8k_kernel(const float *__restrict__ gate,
+                                                             const float *__restrict__ up, uint8_t *__restrict__ xq) {
+    const uint32_t lane = threadIdx.x;
+    const size_t blk = blockIdx.x;
+    const float4 g = ((const float4 *)(gate + blk * 256u))[lane];
+    const float4 u = ((const float4 *)(up + blk * 256u))[lane];
+    const float e[4] = {dev_silu(g.x) * u.x, dev_silu(g.y) * u.y, dev_silu(g.z) * u.z, dev_silu(g.w) * u.w};
+    quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
+}
+
 // RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
 // single-token GEMV's SINTER_PRO_RMSNORM prologue and of the oracle's
 // or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded to fp32,
@@ -403,7 +422,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_q8k_kernel(const float *__r
 using namespace sinter;
 
 extern "C" int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int64_t k, const void *xq,
-                                     uint32_t n_tokens, float *y, void *stream) {
+                                     uint32_t n_tokens, float *y, int accumulate, void *stream) {
     if (type != SINTER_Q4_K && type != SINTER_Q6_K)
         return set_error(SINTER_ERR_ARG, "gemv_ubatch: weight type %d (Q4_K or Q6_K)", type);
     if (rows <= 0 || rows > (int64_t)UINT32_MAX - UB_ROWS || k <= 0 || k % 256 != 0 || k / 256 > (int64_t)UINT32_MAX)
@@ -429,10 +448,12 @@ extern "C" int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int6
     hipStream_t s = (hipStream_t)stream;
     if (type == SINTER_Q4_K)
         hipLaunchKernelGGL(ubatch_gemv_kernel<SINTER_Q4_K>, grid, block, 0, s, (const uint8_t *)w, (uint32_t)rows, nb,
-                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw);
+                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw,
+                           (uint32_t)(accumulate != 0));
     else
         hipLaunchKernelGGL(ubatch_gemv_kernel<SINTER_Q6_K>, grid, block, 0, s, (const uint8_t *)w, (uint32_t)rows, nb,
-                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw);
+                           (const uint8_t *)xq, n_tokens, y, (uint32_t)n_tg, tpw,
+                           (uint32_t)(accumulate != 0));
     return hip_ok(hipGetLastError(), "gemv_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }
 
@@ -461,4 +482,19 @@ extern "C" int sinter_rmsnorm_quant_q8k_ubatch(const float *x, const float *w, f
     hipLaunchKernelGGL(rmsnorm_quant_q8k_kernel, dim3(n_tokens), dim3(256), 0, (hipStream_t)stream, x, w, eps,
                        (uint32_t)k, (uint8_t *)xq);
     return hip_ok(hipGetLastError(), "rmsnorm_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+extern "C" int sinter_swiglu_quant_q8k_ubatch(const float *gate, const float *up, int64_t k, uint32_t n_tokens, void *xq,
+                                              void *stream) {
+    if (k <= 0 || k % 256 != 0)
+        return set_error(SINTER_ERR_ARG, "swiglu_quant_q8k_ubatch: k %lld (a positive multiple of 256)", (long long)k);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!gate || !up || !xq) return set_error(SINTER_ERR_ARG, "swiglu_quant_q8k_ubatch: null pointer");
+    if ((uintptr_t)gate % 16u || (uintptr_t)up % 16u || (uintptr_t)xq % 4u)
+        return set_error(SINTER_ERR_ARG, "swiglu_quant_q8k_ubatch: alignment (gate, up 16 bytes, xq 4 bytes)");
+    const uint64_t n_blk = (uint64_t)n_tokens * (uint64_t)(k / 256);
+    if (n_blk > (uint64_t)INT32_MAX) return set_error(SINTER_ERR_ARG, "swiglu_quant_q8k_ubatch: too many blocks");
+    hipLaunchKernelGGL(swiglu_quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, gate, up,
+                       (uint8_t *)xq);
+    return hip_ok(hipGetLastError(), "swiglu_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }

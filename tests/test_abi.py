@@ -101,17 +101,17 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     L = sn.lib()
     f = L.sinter_op_gemv_ubatch
     W, X, Y = C.c_void_p(4096), C.c_void_p(8192), C.c_void_p(16384)
-    assert f(sn.Q8_0, W, 16, 256, X, 4, Y, None) == sn.ERR_ARG
+    assert f(sn.Q8_0, W, 16, 256, X, 4, Y, 0, None) == sn.ERR_ARG
     assert b"Q4_K or Q6_K" in L.sinter_last_error()
-    assert f(sn.Q4_K, W, 16, 300, X, 4, Y, None) == sn.ERR_ARG
+    assert f(sn.Q4_K, W, 16, 300, X, 4, Y, 0, None) == sn.ERR_ARG
     assert b"multiple of 256" in L.sinter_last_error()
-    assert f(sn.Q4_K, W, 0, 256, X, 4, Y, None) == sn.ERR_ARG
-    assert f(sn.Q4_K, W, 16, 256, X, 0, Y, None) == sn.OK
-    assert f(sn.Q4_K, None, 16, 256, X, 4, Y, None) == sn.ERR_ARG
-    assert f(sn.Q4_K, C.c_void_p(4100), 16, 256, X, 4, Y, None) == sn.ERR_ARG      # Q4_K: 16-byte weights
+    assert f(sn.Q4_K, W, 0, 256, X, 4, Y, 0, None) == sn.ERR_ARG
+    assert f(sn.Q4_K, W, 16, 256, X, 0, Y, 0, None) == sn.OK
+    assert f(sn.Q4_K, None, 16, 256, X, 4, Y, 0, None) == sn.ERR_ARG
+    assert f(sn.Q4_K, C.c_void_p(4100), 16, 256, X, 4, Y, 0, None) == sn.ERR_ARG      # Q4_K: 16-byte weights
     assert b"alignment" in L.sinter_last_error()
-    assert f(sn.Q6_K, W, 16, 256, C.c_void_p(8194), 4, Y, None) == sn.ERR_ARG      # activations: 4 bytes
-    assert f(sn.Q6_K, C.c_void_p(4098), 16, 256, X, 4, Y, None) == sn.ERR_ARG      # Q6_K: 4-byte weights
+    assert f(sn.Q6_K, W, 16, 256, C.c_void_p(8194), 4, Y, 0, None) == sn.ERR_ARG      # activations: 4 bytes
+    assert f(sn.Q6_K, C.c_void_p(4098), 16, 256, X, 4, Y, 0, None) == sn.ERR_ARG      # Q6_K: 4-byte weights
     q = L.sinter_quant_q8k_ubatch
     assert q(X, 300, 4, Y, None) == sn.ERR_ARG
     assert b"multiple of 256" in L.sinter_last_error()
@@ -124,6 +124,10 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     assert n(X, None, C.c_float(1e-6), 256, 0, Y, None) == sn.OK
     assert n(X, C.c_void_p(8196), C.c_float(1e-6), 256, 4, Y, None) == sn.ERR_ARG   # w: 16 bytes
     assert n(X, None, C.c_float(-1.0), 256, 4, Y, None) == sn.ERR_ARG
+    g = L.sinter_swiglu_quant_q8k_ubatch
+    assert g(X, X, 300, 4, Y, None) == sn.ERR_ARG
+    assert g(X, X, 256, 0, Y, None) == sn.OK
+    assert g(X, C.c_void_p(8200), 256, 4, Y, None) == sn.ERR_ARG                     # up: 16 bytes
 
 
 def test_model_config_validation(sn):

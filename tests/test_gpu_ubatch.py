@@ -49,7 +49,7 @@ def run_ubatch(sn, orc, torch, t, w, rows, k, xs):
     dw, dxq, dy = dev(torch, w), dev(torch, xq), empty_f32(torch, n_tok * rows)
     print(f"gemv_ubatch type={t} rows={rows} k={k} tokens={n_tok}", flush=True)
     rc = sn.lib().sinter_op_gemv_ubatch(t, C.c_void_p(dw.data_ptr()), rows, k, C.c_void_p(dxq.data_ptr()),
-                                        n_tok, C.c_void_p(dy.data_ptr()), C.c_void_p(stream(torch)))
+                                        n_tok, C.c_void_p(dy.data_ptr()), 0, C.c_void_p(stream(torch)))
     sn.check(rc, "gemv_ubatch")
     torch.cuda.synchronize()
     return host(dy).reshape(n_tok, rows)
@@ -126,7 +126,7 @@ def test_device_quantised_ubatch_equals_oracle_gemv(sn, orc, torch_gpu, t, rows,
     sn.check(sn.lib().sinter_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()), k, n_tok, C.c_void_p(dq.data_ptr()), s),
              "quant")
     sn.check(sn.lib().sinter_op_gemv_ubatch(t, C.c_void_p(dw.data_ptr()), rows, k, C.c_void_p(dq.data_ptr()), n_tok,
-                                            C.c_void_p(dy.data_ptr()), s), "gemv_ubatch")
+                                            C.c_void_p(dy.data_ptr()), 0, s), "gemv_ubatch")
     torch.cuda.synchronize()
     got = host(dy).reshape(n_tok, rows)
     for j in range(n_tok):
@@ -154,3 +154,41 @@ def test_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, k, n_tok, w
     got = host(dq).reshape(n_tok, -1)
     for t in range(n_tok):
         assert np.array_equal(got[t], orc.quantize(Q4_K, orc.rmsnorm(x[t], w, eps))), t
+
+
+def test_batched_ffn_block_matches_oracle(sn, orc, torch_gpu):
+    """The FFN sub-layer over a ubatch from the batched pieces -- RMSNorm +
+    Q8_K, the gate and up GEMVs, SwiGLU + Q8_K, the down GEMV accumulated
+    into the residual -- equals, token by token, the oracle's
+    x + or_ffn(or_rmsnorm(x, post_norm)) (oracle/oracle.c or_ffn)."""
+    torch = torch_gpu
+    E, F, T, eps = 1024, 2048, 21, 1e-6
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((T, E)).astype(np.float32)
+    wn = (1.0 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    wg, wu = synth_w(sn, Q4_K, F, E, 1201), synth_w(sn, Q4_K, F, E, 1202)
+    wd = synth_w(sn, Q6_K, E, F, 1203)
+    d = {n: dev(torch, a) for n, a in (("x", x.reshape(-1)), ("wn", wn), ("wg", wg), ("wu", wu), ("wd", wd))}
+    g, u = empty_f32(torch, T * F), empty_f32(torch, T * F)
+    xq = torch.zeros(T * sn.row_bytes(sn.Q8_K, E), dtype=torch.uint8, device="cuda")
+    fq = torch.zeros(T * sn.row_bytes(sn.Q8_K, F), dtype=torch.uint8, device="cuda")
+    L, s = sn.lib(), C.c_void_p(stream(torch))
+    ptr = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    print(f"batched ffn E={E} F={F} tokens={T}", flush=True)
+    sn.check(L.sinter_rmsnorm_quant_q8k_ubatch(ptr(d["x"]), ptr(d["wn"]), eps, E, T, ptr(xq), s), "norm")
+    sn.check(L.sinter_op_gemv_ubatch(Q4_K, ptr(d["wg"]), F, E, ptr(xq), T, ptr(g), 0, s), "gate")
+    sn.check(L.sinter_op_gemv_ubatch(Q4_K, ptr(d["wu"]), F, E, ptr(xq), T, ptr(u), 0, s), "up")
+    sn.check(L.sinter_swiglu_quant_q8k_ubatch(ptr(g), ptr(u), F, T, ptr(fq), s), "swiglu")
+    sn.check(L.sinter_op_gemv_ubatch(Q6_K, ptr(d["wd"]), E, F, ptr(fq), T, ptr(d["x"]), 1, s), "down + residual")
+    torch.cuda.synchronize()
+    got = host(d["x"]).reshape(T, E)
+
+    cfg = orc.Cfg()
+    cfg.n_embd, cfg.n_ff, cfg.t_default, cfg.t_ffn_down = E, F, Q4_K, Q6_K
+    slots = (C.c_void_p * orc.NSLOT)()
+    slots[2], slots[3], slots[4] = wg.ctypes.data, wu.ctypes.data, wd.ctypes.data   # FFN gate, up, down
+    for t in range(T):
+        xn = orc.rmsnorm(x[t], wn, eps)
+        a = np.zeros(E, np.float32)
+        orc.lib().or_ffn(C.byref(cfg), slots, orc.P(xn), orc.P(a))
+        assert np.array_equal(got[t], x[t] + a), t
