@@ -320,6 +320,14 @@ int sinter_rmsnorm_quant_q8k_ubatch(const float *x, const float *w, float eps, i
  * (16-byte aligned), then quantised to Q8_K at xq for the down projection. */
 int sinter_swiglu_quant_q8k_ubatch(const float *gate, const float *up, int64_t k, uint32_t n_tokens, void *xq,
                                    void *stream);
+/* The gated RMSNorm of a gated-DeltaNet layer's output (op_gated_rmsnorm,
+ * k0/ops/gdn.cuh:356-383, over a ubatch) fused ahead of the same quantiser:
+ * per head of head_dim elements (a power of two, 4..256) y = ((x * scale) *
+ * w[i]) * silu(z), scale from the head's fp32 squares summed in fp64 (the
+ * single-token GEMV's GATED prologue); x and z n_tokens x k f32 (16-byte
+ * aligned), w head_dim f32 shared by the heads; Q8_K out at xq. */
+int sinter_gated_rmsnorm_quant_q8k_ubatch(const float *x, const float *z, const float *w, uint32_t head_dim,
+                                          float eps, int64_t k, uint32_t n_tokens, void *xq, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

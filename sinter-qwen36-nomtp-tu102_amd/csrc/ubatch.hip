@@ -377,6 +377,34 @@ __global__ __launch_bounds__(64) void swiglu_quant_q8k_kernel(const float *__res
     quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
 }
 
+// Gated RMSNorm per head then the Q8_K quantiser over a ubatch (the input of
+// a gated-DeltaNet layer's ssm_out): for each head of d elements (d a power
+// of two, 4..256), y = ((x * scale) * w[i]) * silu(z) with scale = 1 /
+// sqrtf(mean + eps) from the head's fp32 squares summed in fp64 -- the
+// single-token GEMV's GATED prologue and the oracle's or_gated_rmsnorm.  One
+// wave per 256-element block: the d / 4 lanes of a head reduce its sum by xor
+// shuffles (a fixed tree; the mean divides by a power of two, exactly).
+__global__ __launch_bounds__(64) void gated_norm_quant_q8k_kernel(const float *__restrict__ x,
+                                                                 const float *__restrict__ z,
+                                                                 const float *__restrict__ w, uint32_t log2d,
+                                                                 float eps, uint8_t *__restrict__ xq) {
+    const uint32_t lane = threadIdx.x;
+    const size_t blk = blockIdx.x;
+    const float4 v = ((const float4 *)(x + blk * 256u))[lane];
+    const float4 g = ((const float4 *)(z + blk * 256u))[lane];
+    const uint32_t d = 1u << log2d, i0 = (4u * lane) & (d - 1u);   // element of the head
+    double sq = (double)(v.x * v.x);
+    sq += (double)(v.y * v.y);
+    sq += (double)(v.z * v.z);
+    sq += (double)(v.w * v.w);
+    for (uint32_t o = 1; o < d / 4u; o <<= 1) sq += __shfl_xor(sq, o);
+    const double inv_d = 1.0 / (double)d;   // a power of two: exact
+    const float scale = 1.0f / sqrtf((float)(sq * inv_d) + eps);
+    const float e[4] = {((v.x * scale) * w[i0]) * dev_silu(g.x), ((v.y * scale) * w[i0 + 1]) * dev_silu(g.y),
+                        ((v.z * scale) * w[i0 + 2]) * dev_silu(g.z), ((v.w * scale) * w[i0 + 3]) * dev_silu(g.w)};
+    quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
+}
+
 // RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
 // single-token GEMV's SINTER_PRO_RMSNORM prologue and of the oracle's
 // or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded to fp32,
@@ -497,4 +525,24 @@ extern "C" int sinter_swiglu_quant_q8k_ubatch(const float *gate, const float *up
     hipLaunchKernelGGL(swiglu_quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, gate, up,
                        (uint8_t *)xq);
     return hip_ok(hipGetLastError(), "swiglu_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+extern "C" int sinter_gated_rmsnorm_quant_q8k_ubatch(const float *x, const float *z, const float *w, uint32_t head_dim,
+                                                     float eps, int64_t k, uint32_t n_tokens, void *xq, void *stream) {
+    if (k <= 0 || k % 256 != 0)
+        return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: k %lld (a positive multiple of 256)",
+                         (long long)k);
+    if (head_dim < 4 || head_dim > 256 || (head_dim & (head_dim - 1)))
+        return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: head_dim %u (a power of two, 4..256)",
+                         head_dim);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!x || !z || !w || !xq) return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: null pointer");
+    if ((uintptr_t)x % 16u || (uintptr_t)z % 16u || (uintptr_t)w % 4u || (uintptr_t)xq % 4u)
+        return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: alignment (x, z 16 bytes, w, xq 4 bytes)");
+    if (!(eps >= 0.0f)) return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: eps must be >= 0");
+    const uint64_t n_blk = (uint64_t)n_tokens * (uint64_t)(k / 256);
+    if (n_blk > (uint64_t)INT32_MAX) return set_error(SINTER_ERR_ARG, "gated_rmsnorm_quant_q8k_ubatch: too many blocks");
+    hipLaunchKernelGGL(gated_norm_quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, x, z, w,
+                       (uint32_t)__builtin_ctz(head_dim), eps, (uint8_t *)xq);
+    return hip_ok(hipGetLastError(), "gated_rmsnorm_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }

@@ -128,6 +128,12 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     assert g(X, X, 300, 4, Y, None) == sn.ERR_ARG
     assert g(X, X, 256, 0, Y, None) == sn.OK
     assert g(X, C.c_void_p(8200), 256, 4, Y, None) == sn.ERR_ARG                     # up: 16 bytes
+    gn = L.sinter_gated_rmsnorm_quant_q8k_ubatch
+    assert gn(X, X, X, 128, C.c_float(1e-6), 300, 4, Y, None) == sn.ERR_ARG
+    assert gn(X, X, X, 96, C.c_float(1e-6), 256, 4, Y, None) == sn.ERR_ARG          # head_dim: a power of two
+    assert b"head_dim" in L.sinter_last_error()
+    assert gn(X, X, X, 512, C.c_float(1e-6), 512, 4, Y, None) == sn.ERR_ARG
+    assert gn(X, X, X, 128, C.c_float(1e-6), 256, 0, Y, None) == sn.OK
 
 
 def test_model_config_validation(sn):

@@ -192,3 +192,29 @@ def test_batched_ffn_block_matches_oracle(sn, orc, torch_gpu):
         a = np.zeros(E, np.float32)
         orc.lib().or_ffn(C.byref(cfg), slots, orc.P(xn), orc.P(a))
         assert np.array_equal(got[t], x[t] + a), t
+
+
+@pytest.mark.parametrize("d,k,n_tok", [(128, 4096, 6), (64, 768, 3), (256, 1024, 2)])
+def test_gated_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, d, k, n_tok):
+    """Per-head gated RMSNorm then Q8_K over a ubatch: byte for byte the
+    oracle's or_gated_rmsnorm then or_quant_q8_K."""
+    torch = torch_gpu
+    rng = np.random.default_rng(d + k)
+    x = quant_inputs(k, n_tok, 90 + d)
+    x[0, :d] = 0.0                                       # an all-zero head
+    z = (2.0 * rng.standard_normal((n_tok, k))).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    eps = 1e-6
+    dx, dz, dw = dev(torch, x.reshape(-1)), dev(torch, z.reshape(-1)), dev(torch, w)
+    dq = torch.zeros(n_tok * sn.row_bytes(sn.Q8_K, k), dtype=torch.uint8, device="cuda")
+    print(f"gated_rmsnorm_quant_q8k_ubatch d={d} k={k} tokens={n_tok}", flush=True)
+    sn.check(sn.lib().sinter_gated_rmsnorm_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()), C.c_void_p(dz.data_ptr()),
+                                                            C.c_void_p(dw.data_ptr()), d, eps, k, n_tok,
+                                                            C.c_void_p(dq.data_ptr()), C.c_void_p(stream(torch))),
+             "gated_rmsnorm_quant")
+    torch.cuda.synchronize()
+    got = host(dq).reshape(n_tok, -1)
+    for t in range(n_tok):
+        y = np.zeros(k, np.float32)
+        orc.lib().or_gated_rmsnorm(orc.P(x[t]), orc.P(z[t]), orc.P(w), orc.P(y), k // d, d, eps)
+        assert np.array_equal(got[t], orc.quantize(Q4_K, y)), t
