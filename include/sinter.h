@@ -328,6 +328,14 @@ int sinter_swiglu_quant_q8k_ubatch(const float *gate, const float *up, int64_t k
  * aligned), w head_dim f32 shared by the heads; Q8_K out at xq. */
 int sinter_gated_rmsnorm_quant_q8k_ubatch(const float *x, const float *z, const float *w, uint32_t head_dim,
                                           float eps, int64_t k, uint32_t n_tokens, void *xq, void *stream);
+/* The causal conv + silu of a gated-DeltaNet layer's qkv channels over a
+ * ubatch (k0/ops/gdn.cuh:106-171, token after token): x and y n_tokens x
+ * channels f32; state channels x (dconv - 1) f32, read and left holding the
+ * last dconv - 1 inputs; conv_w channels x dconv f32 (tap-contiguous);
+ * dconv 1..8.  Token t's row equals the single-token GEMV's CONV epilogue
+ * after tokens 0..t-1. */
+int sinter_conv_silu_ubatch(const float *x, float *state, const float *conv_w, float *y, int64_t channels,
+                            uint32_t dconv, uint32_t n_tokens, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -45,6 +45,7 @@ constexpr uint32_t UB_THREADS = 256;  // four waves: 64 rows of the workgroup's 
 constexpr uint32_t UB_WG_ROWS = UB_ROWS * (UB_THREADS / 64u);
 constexpr uint32_t UB_XSTRIDE = 68;   // LDS dwords per staged token (65 used)
 constexpr uint64_t UB_MIN_WGS = 256;  // one per CU
+constexpr uint32_t UB_CONV_MAX = 8;    // conv taps
 constexpr uint32_t Q8K_BYTES = 292;  // block_q8_K
 constexpr uint32_t Q4K_BYTES = 144, Q6K_BYTES = 210;
 
@@ -405,6 +406,41 @@ __global__ __launch_bounds__(64) void gated_norm_quant_q8k_kernel(const float *_
     quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
 }
 
+// The causal conv + silu of a gated-DeltaNet layer's qkv rows over a ubatch,
+// token after token (the single-token GEMV's CONV epilogue and the oracle's
+// or_conv_silu): one thread per channel c keeps its window {state[c][0..nh-1],
+// x[t][c]} in registers, y[t][c] = silu(sum_j win[j] * w[c][j]) with the sum
+// in fp64 in tap order rounded once, then shifts the window; the state holds
+// the last nh = dconv - 1 inputs when the ubatch ends.
+__global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict__ x, float *__restrict__ st,
+                                                       const float *__restrict__ cw, float *__restrict__ y,
+                                                       uint32_t channels, uint32_t dconv, uint32_t n_tok) {
+    const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+    if (c >= channels) return;
+    const uint32_t nh = dconv - 1u;
+    float win[UB_CONV_MAX];
+    float wt[UB_CONV_MAX];
+#pragma unroll
+    for (uint32_t j = 0; j < UB_CONV_MAX; j++) {
+        win[j] = j < nh ? st[(size_t)c * nh + j] : 0.0f;
+        wt[j] = j < dconv ? cw[(size_t)c * dconv + j] : 0.0f;
+    }
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const float xn = x[(size_t)t * channels + c];
+        double acc = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < UB_CONV_MAX; j++)
+            if (j < dconv) acc += (double)(j < nh ? win[j] : xn) * (double)wt[j];
+        y[(size_t)t * channels + c] = dev_silu((float)acc);
+#pragma unroll
+        for (uint32_t j = 0; j + 1 < UB_CONV_MAX; j++)
+            if (j < nh) win[j] = (j + 1 < nh) ? win[j + 1] : xn;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < UB_CONV_MAX; j++)
+        if (j < nh) st[(size_t)c * nh + j] = win[j];
+}
+
 // RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
 // single-token GEMV's SINTER_PRO_RMSNORM prologue and of the oracle's
 // or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded to fp32,
@@ -545,4 +581,19 @@ extern "C" int sinter_gated_rmsnorm_quant_q8k_ubatch(const float *x, const float
     hipLaunchKernelGGL(gated_norm_quant_q8k_kernel, dim3((uint32_t)n_blk), dim3(64), 0, (hipStream_t)stream, x, z, w,
                        (uint32_t)__builtin_ctz(head_dim), eps, (uint8_t *)xq);
     return hip_ok(hipGetLastError(), "gated_rmsnorm_quant_q8k_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
+}
+
+extern "C" int sinter_conv_silu_ubatch(const float *x, float *state, const float *conv_w, float *y, int64_t channels,
+                                       uint32_t dconv, uint32_t n_tokens, void *stream) {
+    if (channels <= 0 || channels > (int64_t)INT32_MAX || dconv < 1 || dconv > UB_CONV_MAX)
+        return set_error(SINTER_ERR_ARG, "conv_silu_ubatch: channels %lld / dconv %u (1..%u)", (long long)channels,
+                         dconv, UB_CONV_MAX);
+    if (n_tokens == 0) return SINTER_OK;
+    if (!x || !conv_w || !y || (dconv > 1 && !state)) return set_error(SINTER_ERR_ARG, "conv_silu_ubatch: null pointer");
+    if ((uintptr_t)x % 4u || (uintptr_t)state % 4u || (uintptr_t)conv_w % 4u || (uintptr_t)y % 4u)
+        return set_error(SINTER_ERR_ARG, "conv_silu_ubatch: alignment (4 bytes)");
+    const uint32_t nblk = (uint32_t)((channels + 255) / 256);
+    hipLaunchKernelGGL(conv_silu_kernel, dim3(nblk), dim3(256), 0, (hipStream_t)stream, x, state, conv_w, y,
+                       (uint32_t)channels, dconv, n_tokens);
+    return hip_ok(hipGetLastError(), "conv_silu_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }

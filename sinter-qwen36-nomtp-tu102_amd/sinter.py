@@ -144,6 +144,7 @@ def lib():
         "sinter_rmsnorm_quant_q8k_ubatch": (I, [vp, vp, C.c_float, I64, U32, vp, vp]),
         "sinter_swiglu_quant_q8k_ubatch": (I, [vp, vp, I64, U32, vp, vp]),
         "sinter_gated_rmsnorm_quant_q8k_ubatch": (I, [vp, vp, vp, U32, C.c_float, I64, U32, vp, vp]),
+        "sinter_conv_silu_ubatch": (I, [vp, vp, vp, vp, I64, U32, U32, vp]),
         "sinter_op_attn_decode_noalloc": (I, [C.POINTER(AttnArgs), U32, vp]),
         "sinter_litmus_barrier": (I, [U32, U32, I, C.POINTER(C.c_uint64)]),
         "sinter_copy_calibration": (I, [I, C.c_size_t, I]),

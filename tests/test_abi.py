@@ -134,6 +134,11 @@ def test_gemv_ubatch_argument_validation_rejects_before_launch(sn):
     assert b"head_dim" in L.sinter_last_error()
     assert gn(X, X, X, 512, C.c_float(1e-6), 512, 4, Y, None) == sn.ERR_ARG
     assert gn(X, X, X, 128, C.c_float(1e-6), 256, 0, Y, None) == sn.OK
+    cv = L.sinter_conv_silu_ubatch
+    assert cv(X, X, X, Y, 64, 9, 4, None) == sn.ERR_ARG                              # dconv 1..8
+    assert cv(X, X, X, Y, 0, 4, 4, None) == sn.ERR_ARG
+    assert cv(X, X, X, Y, 64, 4, 0, None) == sn.OK
+    assert cv(X, None, X, Y, 64, 4, 4, None) == sn.ERR_ARG
 
 
 def test_model_config_validation(sn):

@@ -218,3 +218,31 @@ def test_gated_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, d, k,
         y = np.zeros(k, np.float32)
         orc.lib().or_gated_rmsnorm(orc.P(x[t]), orc.P(z[t]), orc.P(w), orc.P(y), k // d, d, eps)
         assert np.array_equal(got[t], orc.quantize(Q4_K, y)), t
+
+
+@pytest.mark.parametrize("channels,dconv,n_tok", [(8192, 4, 37), (300, 2, 5), (64, 1, 3)])
+def test_conv_silu_ubatch_matches_oracle_token_loop(sn, orc, torch_gpu, channels, dconv, n_tok):
+    """The causal conv + silu over a ubatch equals the oracle's or_conv_silu
+    applied token after token: every output row and the final state, bit for
+    bit."""
+    torch = torch_gpu
+    rng = np.random.default_rng(channels + dconv)
+    x = rng.standard_normal((n_tok, channels)).astype(np.float32)
+    st = (0.5 * rng.standard_normal(channels * max(dconv - 1, 1))).astype(np.float32)[:channels * (dconv - 1)]
+    cw = (0.3 * rng.standard_normal(channels * dconv)).astype(np.float32)
+    dx, dcw, dy = dev(torch, x.reshape(-1)), dev(torch, cw), empty_f32(torch, n_tok * channels)
+    dst = dev(torch, st) if dconv > 1 else None
+    print(f"conv_silu_ubatch channels={channels} dconv={dconv} tokens={n_tok}", flush=True)
+    sn.check(sn.lib().sinter_conv_silu_ubatch(C.c_void_p(dx.data_ptr()), C.c_void_p(dst.data_ptr()) if dst is not None
+                                              else None, C.c_void_p(dcw.data_ptr()), C.c_void_p(dy.data_ptr()),
+                                              channels, dconv, n_tok, C.c_void_p(stream(torch))), "conv_silu")
+    torch.cuda.synchronize()
+    got = host(dy).reshape(n_tok, channels)
+    ref_st = st.copy()
+    for t in range(n_tok):
+        out = np.zeros(channels, np.float32)
+        orc.lib().or_conv_silu(orc.P(x[t]), orc.P(ref_st) if dconv > 1 else None, orc.P(cw), orc.P(out), channels,
+                               dconv)
+        assert np.array_equal(got[t], out), t
+    if dconv > 1:
+        assert np.array_equal(host(dst), ref_st)
