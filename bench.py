@@ -180,6 +180,7 @@ def op_bench(args):
     cfg = sinter.qwen36_27b_config(n_ctx=max(ctx, 64), quant="q4_k_m", n_layer=n_inst)
     cfg.n_vocab = 512
     cfg.attn_every = 1 if c == 3 else 0
+    cfg.attn_chunk_min = args.attn_chunk_min
     if c == 1:
         cfg.t_default = sinter.Q8_0
     t0 = time.perf_counter()
@@ -477,6 +478,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--attn-chunk-min", type=int, default=0, metavar="N",
+                    help="split-K attention: positions per chunk at least (0: the library default)")
     ap.add_argument("--passes-per-launch", type=int, default=16,
                     help="greedy passes per cooperative launch (the warmup is one launch)")
     ap.add_argument("--profile-ops", type=int, default=0,
@@ -531,6 +534,7 @@ def main():
     n_bal = (args.balance[0] + 1) * args.balance[1] if args.balance[1] else 0
     n_ctx = args.ctx + n_bal + args.warmup + max(args.steps, args.parity_steps) + args.profile_ops + 24
     cfg = sinter.qwen36_27b_config(n_ctx=n_ctx, quant=args.quant)
+    cfg.attn_chunk_min = args.attn_chunk_min
     t0 = time.perf_counter()
     m = sinter.Model(cfg, seed=args.seed)
     setup_s = time.perf_counter() - t0

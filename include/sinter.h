@@ -196,7 +196,8 @@ typedef struct sinter_attn_args {
     const float *k_norm;    /* [HD] */
     void *kc;               /* K cache [n_ctx][NKV heads]: f16 [HD] or Q8_0 [HD/32 blocks] per head */
     void *vc;               /* V cache, the same layout */
-    double *part;           /* partials: [NKV][n_chunks][NQ/NKV][HD+2] fp64; sinter_attn_part_len */
+    float *part;            /* partials: [NKV][n_chunks][NQ/NKV][HD+4] fp32 (acc[HD], max, sum, pad);
+                               sinter_attn_part_len */
     uint32_t *count;        /* per-(kv head, chunk) generation flags, sinter_attn_count_len words,
                                0 before first use; each call adds 1 to each of the NKV*n_chunks */
     float *out;             /* [NQ*HD] gated attention output */
@@ -204,9 +205,11 @@ typedef struct sinter_attn_args {
     uint32_t nq, nkv, hd, rope_dims, n_ctx, n_chunks;
     float theta_scale, eps, scale;
     uint32_t kv_type;       /* SINTER_F16 (also 0) or SINTER_Q8_0 (ggml's f32 -> q8_0 block quantiser on append) */
+    uint32_t chunk_min;     /* depth-adaptive split: each chunk spans >= chunk_min positions (whole 32-position
+                               tiles), so fewer than n_chunks run at shallow depth; 0 = one tile */
 } sinter_attn_args;
 
-/* Buffer sizes for sinter_attn_args (n_chunks <= 64): part in doubles,
+/* Buffer sizes for sinter_attn_args (n_chunks <= 64): part in floats,
  * count in 32-bit words.  No counterpart in the reference (its merge reads a
  * fixed 72-way partial array).  The op runs one (kv head, chunk) item per
  * workgroup (blocks >= nkv * n_chunks, all resident: sinter_op_attn_decode
@@ -340,8 +343,8 @@ int sinter_conv_silu_ubatch(const float *x, float *state, const float *conv_w, f
  * counterpart in the reference; for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid allocation).  As sinter_op_attn_decode, except that a->part and
- * a->count must be NULL: the split-K partials (at most 4 MiB,
- * sinter_attn_part_len(...) * 8 bytes) and the generation flags (at most
+ * a->count must be NULL: the split-K partials (at most 2 MiB,
+ * sinter_attn_part_len(...) * 4 bytes) and the generation flags (at most
  * 1024, sinter_attn_count_len(...)) live in a fixed device array the library
  * holds on each GPU it runs on until the process ends; larger shapes are
  * refused with SINTER_ERR_ARG.  Every call on a GPU shares that array (its
@@ -401,6 +404,10 @@ int sinter_synth(int dev, void *dst, int kind, int type, int64_t rows, int64_t k
 uint64_t sinter_seed(uint64_t config_id, const char *tensor_name, int64_t layer);
 
 /* ------------------------------------------------------------------ model */
+/* default of sinter_model_config.attn_chunk_min: the split-K attention gives
+ * each chunk at least this many KV positions */
+#define SINTER_ATTN_CHUNK_MIN 128
+
 typedef struct sinter_model_config {
     int32_t n_layer, attn_every, n_embd, n_ff, n_vocab;
     int32_t gdn_hk, gdn_hv, gdn_d, conv_k;
@@ -409,6 +416,8 @@ typedef struct sinter_model_config {
     int32_t n_ctx;
     int32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
     int32_t t_kv;           /* KV cache type: SINTER_F16 (also when 0) or SINTER_Q8_0 */
+    int32_t attn_chunks;    /* split-K chunks per kv head at most (1..64; 0: min(64, workgroups / attn_nkv)) */
+    int32_t attn_chunk_min; /* positions per chunk at least (depth-adaptive split; 0: SINTER_ATTN_CHUNK_MIN) */
 } sinter_model_config;
 
 typedef struct sinter_model sinter_model;

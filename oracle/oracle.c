@@ -586,6 +586,163 @@ void or_attn_decode_kv(const float *q, const void *kc, const void *vc, int kv_ty
     }
 }
 
+/* Split-K decode attention in fp32, the folds the GPU's attention op declares
+ * (sinter attention op; the reference's fp32 FATTN fold discipline,
+ * k0/ops/attn.cuh:33-42, restated for 64-wide waves):
+ *   chunks: T = ceil(n_kv/32) tiles, tpc = max(ceil(T/C), ceil(chunk_min/32))
+ *           tiles per chunk, ceil(T/tpc) chunks;
+ *   score:  32 lane partials, lane p chaining fmaf over dims 8p..8p+7,
+ *           added by the tree of lane masks 16, 15, 7, 2, 1, times scale;
+ *   groups: a tile's rows split by row mod 8; each group runs its own online
+ *           softmax per q head over its rows of the chunk's tiles:
+ *           m' = max(m, the group's tile max); w = exp(s - m'), corr =
+ *           exp(m - m') (0 before the group's first row, 1 if m is unchanged)
+ *           in fp64 rounded to fp32; sum = (w0 + w1) + (w2 + w3) over the
+ *           group's 4 tile rows (0 past n_kv); l = l*corr + sum;
+ *           acc = acc*corr, then fmaf(w, v, acc) over the group's rows ascending;
+ *   chunk:  M = max m_g, e_g = exp(m_g - M) (0 for an empty group), L and O
+ *           fmaf chains over the groups ascending;
+ *   merge:  M = max m_c, e_c = exp(m_c - M); L, O fmaf chains over chunks
+ *           ascending; out = O / L (the un-gated attention).
+ * Rows past n_kv contribute nothing. */
+static float or_tree32(const float *v, const int masks[5]) {
+    float a[32], b[32];
+    memcpy(a, v, sizeof a);
+    for (int lv = 0; lv < 5; lv++) {
+        for (int p = 0; p < 32; p++) b[p] = a[p] + a[p ^ masks[lv]];
+        memcpy(a, b, sizeof a);
+    }
+    return a[0];
+}
+
+static const int OR_ATT_SCORE_MASKS[5] = {16, 15, 7, 2, 1};
+
+static float or_attn_exp(float x) { return (float)exp((double)x); }
+
+/* one (kv head, chunk) item: acc[gqa][hd], m[gqa], l[gqa] */
+static inline __attribute__((always_inline)) void or_attn_chunk_body(
+        const float *q, const void *kc, const void *vc, int kv_type, int g, int gqa, int nkv, int hd,
+        int kv0, int kv1, float scale, float *acc, float *mo, float *lo) {
+    const size_t rw = (size_t)nkv * hd;
+    float accr[8][8][256];
+    float mrun[8][8], lrun[8][8];
+    float kr[32][256], vr[32][256];
+    for (int gr = 0; gr < 8; gr++)
+        for (int s = 0; s < gqa; s++) { mrun[gr][s] = -INFINITY; lrun[gr][s] = 0.0f; }
+    memset(accr, 0, sizeof accr);
+    for (int t0 = kv0; t0 < kv1; t0 += 32) {
+        const int nr = kv1 - t0 < 32 ? kv1 - t0 : 32;
+        for (int r = 0; r < nr; r++)
+            for (int d = 0; d < hd; d++) {
+                kr[r][d] = kv_elem(kc, kv_type, rw, t0 + r, (size_t)g * hd + d);
+                vr[r][d] = kv_elem(vc, kv_type, rw, t0 + r, (size_t)g * hd + d);
+            }
+        for (int s = 0; s < gqa; s++) {
+            const float *qs = q + (size_t)(g * gqa + s) * hd;
+            float sc[32];
+            for (int r = 0; r < nr; r++) {
+                float part[32];
+                for (int p = 0; p < 32; p++) {
+                    float a = 0.0f;
+                    for (int d = 8 * p; d < 8 * p + 8; d++) a = fmaf(qs[d], kr[r][d], a);
+                    part[p] = a;
+                }
+                sc[r] = or_tree32(part, OR_ATT_SCORE_MASKS) * scale;
+            }
+            for (int gr = 0; gr < 8; gr++) {
+                float mt = -INFINITY, w[4];
+                for (int i = 0; i < 4; i++)
+                    if (gr + 8 * i < nr) mt = fmaxf(mt, sc[gr + 8 * i]);
+                const float m0 = mrun[gr][s], mn = fmaxf(m0, mt);
+                for (int i = 0; i < 4; i++) w[i] = gr + 8 * i < nr ? or_attn_exp(sc[gr + 8 * i] - mn) : 0.0f;
+                const float ws = (w[0] + w[1]) + (w[2] + w[3]);
+                const float cf = m0 == -INFINITY ? 0.0f : (m0 == mn ? 1.0f : or_attn_exp(m0 - mn));
+                const float lc = lrun[gr][s] * cf;
+                lrun[gr][s] = lc + ws;
+                mrun[gr][s] = mn;
+                for (int d = 0; d < hd; d++) accr[gr][s][d] = accr[gr][s][d] * cf;
+                for (int i = 0; i < 4; i++)
+                    if (gr + 8 * i < nr)
+                        for (int d = 0; d < hd; d++) accr[gr][s][d] = fmaf(w[i], vr[gr + 8 * i][d], accr[gr][s][d]);
+            }
+        }
+    }
+    for (int s = 0; s < gqa; s++) {
+        float M = -INFINITY, e[8], L = 0.0f;
+        for (int gr = 0; gr < 8; gr++) M = fmaxf(M, mrun[gr][s]);
+        for (int gr = 0; gr < 8; gr++) {
+            e[gr] = mrun[gr][s] == -INFINITY ? 0.0f : or_attn_exp(mrun[gr][s] - M);
+            L = fmaf(e[gr], lrun[gr][s], L);
+        }
+        for (int d = 0; d < hd; d++) {
+            float o = 0.0f;
+            for (int gr = 0; gr < 8; gr++) o = fmaf(e[gr], accr[gr][s][d], o);
+            acc[(size_t)s * hd + d] = o;
+        }
+        mo[s] = M;
+        lo[s] = L;
+    }
+}
+
+__attribute__((target("avx2,fma"))) static void or_attn_chunk_fma(
+        const float *q, const void *kc, const void *vc, int kv_type, int g, int gqa, int nkv, int hd,
+        int kv0, int kv1, float scale, float *acc, float *mo, float *lo) {
+    or_attn_chunk_body(q, kc, vc, kv_type, g, gqa, nkv, hd, kv0, kv1, scale, acc, mo, lo);
+}
+static void or_attn_chunk_base(
+        const float *q, const void *kc, const void *vc, int kv_type, int g, int gqa, int nkv, int hd,
+        int kv0, int kv1, float scale, float *acc, float *mo, float *lo) {
+    or_attn_chunk_body(q, kc, vc, kv_type, g, gqa, nkv, hd, kv0, kv1, scale, acc, mo, lo);
+}
+
+void or_attn_geom(int n_kv, int n_chunks, int chunk_min, int *tiles, int *tpc, int *nch) {
+    const int T = (n_kv + 31) / 32;
+    const int a = (T + n_chunks - 1) / n_chunks, b = (chunk_min + 31) / 32;
+    int t = a > b ? a : b;
+    if (t < 1) t = 1;
+    *tiles = T;
+    *tpc = t;
+    *nch = (T + t - 1) / t;
+}
+
+void or_attn_split(const float *q, const void *kc, const void *vc, int kv_type, int n_kv, int nq, int nkv,
+                   int hd, float scale, int n_chunks, int chunk_min, float *out) {
+    const int gqa = nq / nkv;
+    int T, tpc, NC;
+    or_attn_geom(n_kv, n_chunks, chunk_min, &T, &tpc, &NC);
+    (void)T;
+    float *acc = (float *)malloc(sizeof(float) * (size_t)nkv * NC * gqa * hd);
+    float *m = (float *)malloc(sizeof(float) * (size_t)nkv * NC * gqa);
+    float *l = (float *)malloc(sizeof(float) * (size_t)nkv * NC * gqa);
+    const int fma_ok = __builtin_cpu_supports("fma");
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int it = 0; it < nkv * NC; it++) {
+        const int g = it / NC, c = it % NC;
+        const int kv0 = c * tpc * 32, kv1 = kv0 + tpc * 32 < n_kv ? kv0 + tpc * 32 : n_kv;
+        float *a = acc + (size_t)it * gqa * hd;
+        if (fma_ok) or_attn_chunk_fma(q, kc, vc, kv_type, g, gqa, nkv, hd, kv0, kv1, scale, a, m + (size_t)it * gqa, l + (size_t)it * gqa);
+        else or_attn_chunk_base(q, kc, vc, kv_type, g, gqa, nkv, hd, kv0, kv1, scale, a, m + (size_t)it * gqa, l + (size_t)it * gqa);
+    }
+    for (int g = 0; g < nkv; g++)
+        for (int s = 0; s < gqa; s++) {
+            float M = -INFINITY;
+            for (int c = 0; c < NC; c++) M = fmaxf(M, m[((size_t)g * NC + c) * gqa + s]);
+            float e[64], L = 0.0f;
+            for (int c = 0; c < NC; c++) {
+                e[c] = or_attn_exp(m[((size_t)g * NC + c) * gqa + s] - M);
+                L = fmaf(e[c], l[((size_t)g * NC + c) * gqa + s], L);
+            }
+            for (int d = 0; d < hd; d++) {
+                float O = 0.0f;
+                for (int c = 0; c < NC; c++) O = fmaf(e[c], acc[(((size_t)g * NC + c) * gqa + s) * hd + d], O);
+                out[(size_t)(g * gqa + s) * hd + d] = O / L;
+            }
+        }
+    free(acc);
+    free(m);
+    free(l);
+}
+
 /* ------------------------------------------------------------ layers */
 
 int or_is_attn_layer(const or_cfg *c, int il) {
@@ -636,6 +793,15 @@ void or_gdn_mixer(const or_cfg *c, const void *const *w, void *const *st,
     free(qkv); free(z); free(al); free(br); free(cv); free(g); free(be); free(o); free(on);
 }
 
+/* the split-K geometry of a configuration (0: the library defaults for a
+ * 256-workgroup grid over attn_nkv kv heads, and SINTER_ATTN_CHUNK_MIN) */
+static int or_chunks(const or_cfg *c) {
+    if (c->attn_chunks > 0) return c->attn_chunks;
+    const int n = 256 / c->attn_nkv;
+    return n > 64 ? 64 : n < 1 ? 1 : n;
+}
+static int or_chunk_min(const or_cfg *c) { return c->attn_chunk_min > 0 ? c->attn_chunk_min : 128; }
+
 /* dbg (nullable): qg[NQ*2*HD] | k[NKV*HD] | v[NKV*HD] | qr[NQ*HD] | kr[NKV*HD]
  * | att[NQ*HD] | gated[NQ*HD] */
 void or_attn_mixer(const or_cfg *c, const void *const *w, void *const *st,
@@ -666,14 +832,14 @@ void or_attn_mixer(const or_cfg *c, const void *const *w, void *const *st,
         blk_q8_0 *K = (blk_q8_0 *)st[OR_ST_K], *V = (blk_q8_0 *)st[OR_ST_V];
         or_quant_q8_0_ref(kr, K + (size_t)pos * (RW / 32), RW);
         or_quant_q8_0_ref(vv, V + (size_t)pos * (RW / 32), RW);
-        or_attn_decode_kv(qr, K, V, OR_Q8_0, pos + 1, NQ, NKV, HD, 1.0f / sqrtf((float)HD), att);
+        or_attn_split(qr, K, V, OR_Q8_0, pos + 1, NQ, NKV, HD, 1.0f / sqrtf((float)HD), or_chunks(c), or_chunk_min(c), att);
     } else {
         uint16_t *K = (uint16_t *)st[OR_ST_K], *V = (uint16_t *)st[OR_ST_V];
         for (int i = 0; i < RW; i++) {
             K[(size_t)pos * RW + i] = or_f32_to_f16(kr[i]);
             V[(size_t)pos * RW + i] = or_f32_to_f16(vv[i]);
         }
-        or_attn_decode(qr, K, V, pos + 1, NQ, NKV, HD, RW, 1.0f / sqrtf((float)HD), att);
+        or_attn_split(qr, K, V, OR_F16, pos + 1, NQ, NKV, HD, 1.0f / sqrtf((float)HD), or_chunks(c), or_chunk_min(c), att);
     }
     for (int h = 0; h < NQ; h++)
         for (int d = 0; d < HD; d++) {

@@ -93,6 +93,14 @@ void  or_attn_decode(const float *q, const uint16_t *kc, const uint16_t *vc,
 void  or_attn_decode_kv(const float *q, const void *kc, const void *vc, int kv_type,
                         int n_kv, int nq, int nkv, int hd, float scale, float *out);
 
+/* the fp32 split-K attention of the GPU op (declared folds, see oracle.c):
+ * out[nq][hd] = the un-gated attention over n_kv positions in at most
+ * n_chunks chunks of >= chunk_min positions; or_attn_geom gives the tiles,
+ * tiles per chunk and chunk count */
+void  or_attn_geom(int n_kv, int n_chunks, int chunk_min, int *tiles, int *tpc, int *nch);
+void  or_attn_split(const float *q, const void *kc, const void *vc, int kv_type, int n_kv, int nq,
+                    int nkv, int hd, float scale, int n_chunks, int chunk_min, float *out);
+
 /* model configuration (mirrors sinter_model_config in include/sinter.h) */
 typedef struct {
     int32_t n_layer, attn_every, n_embd, n_ff, n_vocab;
@@ -102,6 +110,7 @@ typedef struct {
     int32_t n_ctx;
     int32_t t_default, t_attn_v, t_ffn_down, t_output, t_embd;
     int32_t t_kv;   /* KV cache: OR_F16 (also 0) or OR_Q8_0 */
+    int32_t attn_chunks, attn_chunk_min;   /* split-K attention geometry (or_attn_split) */
 } or_cfg;
 
 /* per-layer weight slots (NSLOT pointers per layer) */

@@ -22,7 +22,8 @@ class Cfg(C.Structure):
                                          "gdn_hv", "gdn_d", "conv_k", "attn_nq", "attn_nkv", "head_dim",
                                          "rope_dims")] + \
                [("rope_base", C.c_float), ("eps", C.c_float), ("n_ctx", C.c_int32)] + \
-               [(n, C.c_int32) for n in ("t_default", "t_attn_v", "t_ffn_down", "t_output", "t_embd", "t_kv")]
+               [(n, C.c_int32) for n in ("t_default", "t_attn_v", "t_ffn_down", "t_output", "t_embd", "t_kv",
+                                         "attn_chunks", "attn_chunk_min")]
 
 
 def build():
@@ -60,6 +61,8 @@ def lib():
             "or_rope_theta_scale": (f, [f, i]), "or_rope_neox": (None, [p, i, i, i, f]),
             "or_attn_decode": (None, [p, p, p, i, i, i, i, i, f, p]),
             "or_attn_decode_kv": (None, [p, p, p, i, i, i, i, i, f, p]),
+            "or_attn_split": (None, [p, p, p, i, i, i, i, i, f, i, i, p]),
+            "or_attn_geom": (None, [i, i, i, C.POINTER(i), C.POINTER(i), C.POINTER(i)]),
             "or_is_attn_layer": (i, [C.POINTER(Cfg), i]),
             "or_gdn_mixer": (None, [C.POINTER(Cfg), p, p, p, p, p]),
             "or_row_isa": (i, []),

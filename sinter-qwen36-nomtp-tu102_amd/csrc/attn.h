@@ -5,21 +5,43 @@
 //   KV append at row pos, f16 (attn.cuh:184-211) or Q8_0 blocks (ggml's
 //   f32 -> q8_0 block quantiser)
 //   split-K online-softmax partials            (attn.cuh:244-401)
-//   max/LSE merge by the last-arriving block   (attn.cuh:403-458)
+//   max/LSE merge by the chunks themselves     (attn.cuh:403-458)
 //   sigmoid output gate                        (attn.cuh:460-488)
 // Work item = (kv head g, chunk c).  An item serves all NQ/NKV q heads of
 // its group from one read of its K/V rows (GQA sharing).  The item whose
 // chunk holds `pos` also appends the new K/V row and uses it directly.  Each
-// item publishes an fp64 partial {acc[HD], max, sum} per q head; the block
-// that arrives last for kv head g merges that head group and applies the
-// gate, so the reference's separate FATTN_REDUCE / ATTN_GATE windows (and
-// their barriers) disappear.
+// item publishes an fp32 partial {acc[HD], max, sum} per q head, then the
+// kv head's chunks wait for each other and each merges a slice of the head
+// group's outputs and applies the gate, so the reference's separate
+// FATTN_REDUCE / ATTN_GATE windows (and their barriers) disappear.
 //
-// Declared numerics (oracle/oracle.c or_attn_decode_kv): q/k norms and RoPE
-// in fp32 as ggml; scores are fp64 sums of exact products times the fp32
-// scale; softmax and the V sum in fp64; the merged output rounded to fp32
-// once.  A Q8_0 cache element is dequantised exactly (int8 code times the
-// block's f16 scale, exact in fp32) before it enters the same arithmetic.
+// Declared numerics (fp32 folds in the reference's manner, attn.cuh:33-42;
+// oracle/oracle.c or_attn_split computes the same values):
+//   chunks   whole 32-position tiles: T = ceil(n_kv/32) tiles, tpc =
+//            max(ceil(T/C), ceil(chunk_min/32)) tiles per chunk, ceil(T/tpc)
+//            chunks (att_geom) -- fewer, longer chunks at shallow depth;
+//   scores   q (fp32, normalised and rotated) . k: lane p of 32 holds dims
+//            8p..8p+7 and chains fmaf over them in ascending order; the 32
+//            lane sums are added by the tree of lane xor-masks 16, 15, 7, 2, 1
+//            (level by level); times the fp32 scale; rows past n_kv -> -inf;
+//   groups   the rows of a tile split into 8 row groups (row mod 8), each
+//            with its own online softmax per q head over its rows of the
+//            chunk's tiles (ascending):
+//   softmax  per tile: m' = max(m, max of the group's scores in the tile);
+//            w = exp(s - m') and the correction exp(m - m') (0 before the
+//            group's first row, 1 when m is unchanged) evaluated in fp64 and
+//            rounded to fp32; the tile's (<= 4) w of the group added as
+//            (w0 + w1) + (w2 + w3); l = l*corr + sum;
+//   V sums   per (q head, dim): acc = acc*corr per tile, then fmaf(w, v, acc)
+//            over the group's rows of the tile ascending;
+//   chunk    the 8 groups merged per q head: M = max m_g, e_g = exp(m_g - M)
+//            (0 for a group without rows), L and O fmaf chains over the groups
+//            ascending -- the chunk's partial {O, M, L};
+//   merge    M = max over chunks of m; e_c = exp(m_c - M) (fp64, rounded);
+//            L and O are fmaf chains over the chunks ascending; out = O / L,
+//            then times sigmoid(gate).
+// A Q8_0 cache element is its int8 code times its block's f16 scale, exact in
+// fp32; an f16 element converts exactly.
 #pragma once
 #include "dev_common.h"
 
@@ -28,38 +50,42 @@ namespace sinter {
 constexpr int ATT_TILE = 32;   // KV positions per LDS tile
 constexpr int ATT_MAXG = 8;    // max q heads per kv head
 constexpr uint32_t ATT_Q8_HEAD = 272;   // one head's 256 elements as eight 34-byte Q8_0 blocks
-// Q8_0 tile LDS map (in the f16 tiles' 64 KiB): raw K tiles at 0 and
-// ATT_Q8_RAWB, raw V tiles at 2 * ATT_Q8_RAWB (+ ATT_Q8_RAWB), then the
-// current tile split into codes [32][256] K and V, and scales [32][8] K and V
+// Tiles in flight: tile j lands in buffer j % ATT_NBUF of the scratch region
+// (g_big); tile j + 2 is issued once every wave is past tile j - 1.
+constexpr uint32_t ATT_NBUF = 3;
+constexpr uint32_t ATT_F16_BUF = 2 * ATT_TILE * 512;   // f16: K rows [32][512 B], then V rows
+static_assert(ATT_NBUF * ATT_F16_BUF <= BIG_BYTES, "f16 tiles fit the scratch region");
+// Q8_0 tile LDS map: raw K and V tiles of buffer b at 2 b ATT_Q8_RAWB (+
+// ATT_Q8_RAWB), then the current tile split into codes [32][256] K and V,
+// and scales [32][8] K and V
 constexpr uint32_t ATT_Q8_RAWB = 9600;  // 32 rows x 272 B, plus the third DMA's overrun (56 chunks)
-constexpr uint32_t ATT_Q8_KC = 4 * ATT_Q8_RAWB, ATT_Q8_VC = ATT_Q8_KC + 32 * 256;
+constexpr uint32_t ATT_Q8_KC = 2 * ATT_NBUF * ATT_Q8_RAWB, ATT_Q8_VC = ATT_Q8_KC + 32 * 256;
 constexpr uint32_t ATT_Q8_KS = ATT_Q8_VC + 32 * 256, ATT_Q8_VS = ATT_Q8_KS + 32 * 8 * 4;
-static_assert(ATT_Q8_VS + 32 * 8 * 4 <= 4 * ATT_TILE * 512, "Q8_0 tiles fit the f16 tile region");
+static_assert(ATT_Q8_VS + 32 * 8 * 4 <= BIG_BYTES, "Q8_0 tiles fit the scratch region");
 static_assert(ATT_Q8_RAWB % 16 == 0 && 4 * 136 * 16 + 56 * 16 <= ATT_Q8_RAWB, "raw tile plus overrun");
 
-// The 8 elements [8p, 8p+8) of a 256-element head row, as exact doubles.
+// The 8 elements [8p, 8p+8) of a 256-element head row as fp32 (exact).
 // f16: the row's 512 bytes (16-aligned).  Q8_0: the row split in LDS into
 // its 256 int8 codes (row) and the eight block scales, sc being the scale of
-// block p/4; a code times its scale is exact in fp64.
+// block p/4; a code times its scale is exact in fp32.
 template <bool Q8>
-__device__ __forceinline__ void att_row8(const LDS unsigned char *row, uint32_t p, float sc, double out[8]) {
+__device__ __forceinline__ void att_row8(const LDS unsigned char *row, uint32_t p, float sc, float out[8]) {
     if constexpr (!Q8) {
         (void)sc;
         const u32x4 u = *reinterpret_cast<const LDS u32x4 *>(row + 16 * p);
         const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (uint32_t k = 0; k < 4; k++) {
-            out[2 * k] = (double)h2f((uint16_t)(uw[k] & 0xffff));
-            out[2 * k + 1] = (double)h2f((uint16_t)(uw[k] >> 16));
+            out[2 * k] = h2f((uint16_t)(uw[k] & 0xffff));
+            out[2 * k + 1] = h2f((uint16_t)(uw[k] >> 16));
         }
     } else {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         const u32x2 c = *reinterpret_cast<const LDS u32x2 *>(row + 8 * p);
-        const double d = (double)sc;
 #pragma unroll
         for (uint32_t k = 0; k < 8; k++) {
             const uint32_t w = k < 4 ? c.x : c.y;
-            out[k] = (double)(int)(int8_t)((w >> (8 * (k & 3))) & 0xffu) * d;
+            out[k] = (float)(int)(int8_t)((w >> (8 * (k & 3))) & 0xffu) * sc;
         }
     }
 }
@@ -168,15 +194,12 @@ __device__ __forceinline__ void att_prep(uint32_t nq, uint32_t nh, float eps, in
     __syncthreads();
 }
 
-// Tile-loop thread roles: t = 64 rg + 32 hg + p.  Thread t covers tile rows
-// [8 rg, 8 rg + 8), q head slots [4 hg, 4 hg + 4) and dims [8 p, 8 p + 8):
-// for the scores it holds the slots' q (fp64) for its dims and forms the
-// 8 x 4 partial dot products over them; for V it accumulates the same
-// rows x slots x dims.  Every K/V element of a tile is converted by two
-// threads (the two slot groups), every product appears once.
-constexpr uint32_t ATT_RG = 8, ATT_HG = 4, ATT_DP = 8;
-
-// Reduce-scatter of 32 fp64 partials over the 32 lanes of a half-wave
+// Tile-loop thread roles: t = 32 rr + p.  For the scores thread t covers the
+// tile rows rr + 8i (i < 4), all ATT_MAXG q head slots and dims [8p, 8p+8):
+// it holds the slots' q for its dims and forms the 4 x 8 partial dot
+// products over them; for the V sums it accumulates the same rows, slots and
+// dims.  Every product appears once.
+// Reduce-scatter of 32 fp32 partials over the 32 lanes of a half-wave
 // without selects: lane p keeps its partials permuted, physical slot k
 // holding logical index k ^ att_perm(p), where att_perm is the GF(2)-linear
 // map taking the lane bits (1, 2, 4, 8, 16) to (1, 2, 7, 12, 16).  Every step
@@ -184,19 +207,38 @@ constexpr uint32_t ATT_RG = 8, ATT_HG = 4, ATT_DP = 8;
 // half being folded -- xor 16 (a shuffle), the row mirror (p ^ 15 within the
 // row, whose image differs by 8), the half-row mirror (p ^ 7: by 4), xor 2,
 // xor 1 -- so all lanes add the partner's upper half to their lower half:
-// v[k] += partner's v[k + N].  Lane p ends with logical index att_perm(p).
+// v[k] += partner's v[k + N].  Lane p ends with logical index att_perm(p),
+// the sum over the lanes by the tree of masks 16, 15, 7, 2, 1.
 __device__ __forceinline__ uint32_t att_perm(uint32_t p) {
     return (p & 16u) | ((p & 1u) ? 1u : 0u) ^ ((p & 2u) ? 2u : 0u) ^ ((p & 4u) ? 7u : 0u) ^ ((p & 8u) ? 12u : 0u);
 }
 template <int CTRL, int N>
-__device__ __forceinline__ void att_rs_step(double v[]) {
+__device__ __forceinline__ void att_rs_step(float v[]) {
 #pragma unroll
-    for (int k = 0; k < N; k++) v[k] = v[k] + dpp_d<CTRL>(v[k + N]);
+    for (int k = 0; k < N; k++) v[k] = v[k] + dpp_f<CTRL>(v[k + N]);
 }
-__device__ __forceinline__ void att_rs_step_x16(double v[]) {
+__device__ __forceinline__ void att_rs_step_x16(float v[]) {
 #pragma unroll
     for (int k = 0; k < 16; k++) v[k] = v[k] + __shfl_xor(v[k + 16], 16, 64);
 }
+// Max / sum over the 32 lanes of a half-wave, lane masks 1, 2, 7, 15, 16 in
+// this order (every lane gets the result)
+__device__ __forceinline__ float att_max32(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ float att_sum32(float v) {
+    v = v + dpp_f<DPP_XOR1>(v);
+    v = v + dpp_f<DPP_XOR2>(v);
+    v = v + dpp_f<DPP_HALF_MIRROR>(v);
+    v = v + dpp_f<DPP_MIRROR>(v);
+    return v + __shfl_xor(v, 16, 64);
+}
+// fp64-evaluated exponential rounded to fp32 (the declared transcendental rule)
+__device__ __forceinline__ float att_exp(float x) { return (float)exp((double)x); }
 
 // Wave 0: wait until each of the n (<= 64) generation flags at f holds at
 // least target (wrap-safe); lane l polls flag l, one round trip per round.
@@ -250,27 +292,26 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     // this chunk's generation flag (written only by this item, once per call)
     const uint32_t gen = ld_coh(a.count + rel);
     const uint32_t t = tid();
-    const uint32_t PS = HD + 2;
+    const uint32_t PS = att_rec(HD);
     // cache row: all kv heads of a position; one head HB bytes
     const uint32_t HB = q8 ? ATT_Q8_HEAD : HD * 2u, RWB = NKV * HB;
     const uint32_t n_kv = (uint32_t)pos + 1;
-    const uint32_t clen = (n_kv + C - 1) / C;
+    const AttGeom geo = att_geom(n_kv, C, a.chunk_min);
 
-    // LDS map (the scratch region): K and V tiles double-buffered by LDS-DMA,
-    // q heads (and the new k row), prep scratch, scores -> weights, softmax
-    // corrections; after the tiles the K/V area holds the row-group sums,
-    // then the merge's weights.
+    // LDS map: K and V tiles (ATT_NBUF buffers by LDS-DMA) in the scratch
+    // region; in the GEMV activation buffer (unused by this op): q heads (and
+    // the new k row), prep scratch, the tile weights of each half-wave, the
+    // new K/V rows, the merge's chunk weights.
     lds_char *L = (lds_char *)g_big;
     LDS unsigned char *Lu = reinterpret_cast<LDS unsigned char *>(L);
-    LDS uint16_t *kb = reinterpret_cast<LDS uint16_t *>(L);                          // [2][32][256]
-    LDS uint16_t *vb = reinterpret_cast<LDS uint16_t *>(L + 2 * ATT_TILE * 512);     // [2][32][256]
-    LDS float *qf = reinterpret_cast<LDS float *>(L + 4 * ATT_TILE * 512);           // [gqa][256] q, then the new k row
+    lds_char *Q = (lds_char *)g_qbuf;
+    LDS float *qf = reinterpret_cast<LDS float *>(Q);                                // [gqa][256] q, then the new k row
     LDS float *qn = qf + (ATT_MAXG + 1) * 256;    // [ATT_MAXG+4][256] raw q / k / v rows (then prep scratch), q_norm, k_norm
     LDS float *rot = (LDS float *)g_att_rot;                                         // [2][128] rope cos | sin
-    LDS double *pred = reinterpret_cast<LDS double *>(qn + (ATT_MAXG + 4) * 256);    // [5][ATT_MAXG+1]
-    LDS double *sc = pred + 5 * (ATT_MAXG + 1);                                      // [ATT_MAXG][32] scores -> weights
-    LDS double *corr = sc + ATT_MAXG * ATT_TILE;                                     // [ATT_MAXG]
-    LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(corr + ATT_MAXG);          // [256]
+    LDS float *wl = qn + (ATT_MAXG + 4) * 256;    // [8 row groups][4 rows x 8 slots weights | 8 corr], then m, l [2][8][8]
+    LDS float *me = wl + 8 * 5 * ATT_MAXG + 2 * 8 * ATT_MAXG;                        // merge: [64][ATT_MAXG] chunk weights
+    LDS float *mL = me + 64 * ATT_MAXG;                                              //        [ATT_MAXG] L per slot
+    LDS uint16_t *knew = reinterpret_cast<LDS uint16_t *>(mL + ATT_MAXG);            // [256]
     LDS uint16_t *vnew = knew + 256;                                                 // [256]
     LDS unsigned *flag = reinterpret_cast<LDS unsigned *>(vnew + 256);
     // Q8_0: the appended K / V head rows (16-aligned)
@@ -278,54 +319,50 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
         ((uint32_t)(uintptr_t)(flag + 1) + 15u) & ~15u);
     LDS unsigned char *vnew8 = knew8 + ATT_Q8_HEAD;
 
-    LDS double *comb = reinterpret_cast<LDS double *>(L);       // after the tiles: [4 rg][16][64 lanes]
-    LDS double *mw = reinterpret_cast<LDS double *>(L);         // merge: [C][gqa] m, then weights e
-    LDS double *mlv = mw + 64 * ATT_MAXG;                       //        [C][gqa] l
-    LDS double *mM = mlv + 64 * ATT_MAXG;                       //        [ATT_MAXG + gqa]: L at ATT_MAXG + h
-    LDS double *msum = mM + 2 * ATT_MAXG;                       //        [256] per-thread element partials
     const uint32_t w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63u;
-    const uint32_t kbase = (uint32_t)(uintptr_t)kb, vbase = (uint32_t)(uintptr_t)vb;
+    const uint32_t kbase = (uint32_t)(uintptr_t)L;
 
     const uint32_t g = rel / C, c = rel % C;
-    const uint32_t kv0 = min(c * clen, n_kv), kv1 = min(kv0 + clen, n_kv);
+    if (c >= geo.n) {
+        // no positions for this chunk at this depth: its generation flag
+        // still advances, so every flag of the kv head moves in step
+        if (t == 0) st_coh(a.count + rel, gen + 1u);
+        return;
+    }
+    const uint32_t kv0 = c * geo.tpc * ATT_TILE, kv1 = min(kv0 + geo.tpc * ATT_TILE, n_kv);
     const bool owner = kv0 <= (uint32_t)pos && (uint32_t)pos < kv1;
     const uint32_t ntile = (kv1 - kv0 + ATT_TILE - 1) / ATT_TILE;
     // Tile j (32 rows of this kv head: HB bytes of K and of V each) into
-    // buffer j % 2 (16 KiB apart), rows back to back.  f16: each wave DMAs
+    // buffer j % ATT_NBUF, rows back to back.  f16: each wave DMAs
     // rows 2k, 2k+1 for k = w, w+4, w+8, w+12 of K and of V (lane l: row
     // 2k + l/32, bytes 16 (l%32) ..) -- 8 DMAs per wave.  Q8_0: the tile's
-    // 32 x 17 16-byte chunks into raw buffer j % 2 (ATT_Q8_RAWB apart),
+    // 32 x 17 16-byte chunks into raw buffer j % ATT_NBUF (K, then V),
     // wave w chunks [136w, 136w + 192) in three whole-wave DMAs per matrix --
     // 6 per wave; the last 56 chunks of a wave are the next wave's first (the
     // same bytes written twice), past the tile (wave 3) they land in the
     // buffer's overrun.  Rows past kv1 re-read row kv1-1 (masked in the
     // scores).
     auto issue_tile = [&](uint32_t j) {
-        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
+        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j % ATT_NBUF) * ATT_F16_BUF;
         if (!q8) {
 #pragma unroll
             for (uint32_t kk = 0; kk < 4; kk++) {
                 const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), kv1 - 1);
                 const uint32_t voff = row * RWB + g * HB + (lane & 31) * 16;
                 lds_dma16<true>((uintptr_t)a.kc, voff, kbase + bo + k * 1024);
-                lds_dma16<true>((uintptr_t)a.vc, voff, vbase + bo + k * 1024);
+                lds_dma16<true>((uintptr_t)a.vc, voff, kbase + bo + ATT_TILE * 512 + k * 1024);
             }
             return;
         }
-        const uint32_t rb = (j & 1) * ATT_Q8_RAWB;
+        const uint32_t rb = (j % ATT_NBUF) * 2 * ATT_Q8_RAWB;
 #pragma unroll
         for (uint32_t kk = 0; kk < 3; kk++) {
             const uint32_t c0 = 136u * w + 64u * kk, ci = c0 + lane;
             const uint32_t row = min(t0 + ci / 17u, kv1 - 1), voff = row * RWB + g * HB + (ci % 17u) * 16u;
             lds_dma16<true>((uintptr_t)a.kc, voff, kbase + rb + c0 * 16u);
-            lds_dma16<true>((uintptr_t)a.vc, voff, kbase + 2 * ATT_Q8_RAWB + rb + c0 * 16u);
+            lds_dma16<true>((uintptr_t)a.vc, voff, kbase + rb + ATT_Q8_RAWB + c0 * 16u);
         }
-    };
-    const uint32_t rg = t >> 6, hg = (t >> 5) & 1, p = t & 31, mp = att_perm(p);
-    double qd[ATT_HG][ATT_DP];      // q slots 4hg + (j ^ mp%4), dims 8p.. (fp64)
-    double acc[ATT_HG][ATT_DP];     // V sums over this thread's rows
-    double mrun = -INFINITY, lrun = 0.0;   // softmax state of slot t/32 (every lane of the half-wave)
-    {
+    };    {
         // The raw q heads g*gqa .. (and, for the owner, the new k and v
         // rows) by LDS-DMA into qn rows 0..gqa+1, the q and k norm weights
         // into rows ATT_MAXG+2, +3, one 1 KiB row per wave instruction; then
@@ -397,274 +434,258 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
             st_coh(reinterpret_cast<uint64_t *>(dst) + 1, (uint64_t)u.z | ((uint64_t)u.w << 32));
         }
     }
+    // Thread roles in the tile loop: t = 32 rr + p.  Row group rr (one
+    // half-wave) takes the tile rows rr + 8i (i < 4); lane p the dims
+    // 8p..8p+7.  A lane holds every head slot's q for its dims (register slot
+    // s holding head slot s ^ (mp & 7), permuted for the reduce-scatter) and
+    // the V sums of every slot for its dims.  Each row group keeps its own
+    // online softmax per slot (the group's rows of a slot sit in 4 lanes), so
+    // a tile needs one workgroup barrier; the eight groups are merged at the
+    // chunk's end.
+    const uint32_t rr = t >> 5, p = t & 31, mp = att_perm(p);
+    float qv[ATT_MAXG][8], acc[ATT_MAXG][8];
 #pragma unroll
-    for (uint32_t j = 0; j < ATT_HG; j++) {
-        const uint32_t hh = ATT_HG * hg + (j ^ (mp & 3));
-        const f32x4 q0 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p);
-        const f32x4 q1 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + ATT_DP * p + 4);
-        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    for (uint32_t s = 0; s < ATT_MAXG; s++) {
+        const uint32_t hh = s ^ (mp & 7u);
+        const f32x4 q0 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + 8 * p);
+        const f32x4 q1 = *reinterpret_cast<const LDS f32x4 *>(qf + hh * 256 + 8 * p + 4);
+        const float q8v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-        for (uint32_t d = 0; d < ATT_DP; d++) {
-            qd[j][d] = hh < gqa ? (double)qv[d] : 0.0;
-            acc[j][d] = 0.0;
+        for (uint32_t d = 0; d < 8; d++) {
+            qv[s][d] = hh < gqa ? q8v[d] : 0.0f;
+            acc[s][d] = 0.0f;
         }
     }
+    // softmax state of (row group rr, slot mp % 8): the same in the group's 4 lanes of that slot
+    float mrun = -INFINITY, lrun = 0.0f;
+    const uint32_t my_s = mp & 7u, my_i = mp >> 3;
+    LDS float *wgr = wl + rr * (4 * ATT_MAXG + ATT_MAXG);   // this group's weights [4 rows][8 slots], then corr [8]
     if (ts) ts[1] = wall_clock64();
 
     for (uint32_t j = 0; j < ntile; j++) {
-        const uint32_t t0 = kv0 + j * ATT_TILE, bo = (j & 1) * ATT_TILE * 512;
-        if (j == 0) {
-            dma_wait();   // (also the owner's cache stores)
+        const uint32_t t0 = kv0 + j * ATT_TILE, b = j % ATT_NBUF;
+        if (j == 0 || j + 1 >= ntile) {
+            dma_wait();   // (the first: also the owner's cache stores)
         } else {
-            // tile j landed; tile j+1 (issued last step) may still fly
-            if (j + 1 < ntile) {
-                if (q8) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-                else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-            } else {
-                dma_wait();
-            }
+            // tile j landed; tile j+1 may still fly
+            if (q8) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         }
-        __syncthreads();
+        __syncthreads();   // tile j landed for every wave; every wave is past tile j - 1
+        if (j + 2 < ntile) issue_tile(j + 2);   // into the buffer tile j - 1 used
+        const LDS unsigned char *kt = Lu + b * ATT_F16_BUF, *vt = kt + ATT_TILE * 512;
         if constexpr (Q8) {
             // thread t splits block t % 8 of row t / 8 of the K and the V tile
-            const uint32_t rr = t >> 3, bb = t & 7u, rb = (j & 1) * ATT_Q8_RAWB;
-            const LDS unsigned char *raw = Lu + rb + rr * ATT_Q8_HEAD + 34u * bb;
-            att_q8_split(raw, Lu + ATT_Q8_KC + rr * 256 + 32u * bb, reinterpret_cast<LDS float *>(Lu + ATT_Q8_KS) + t);
+            const uint32_t rq = t >> 3, bb = t & 7u, rb = b * 2 * ATT_Q8_RAWB;
+            const LDS unsigned char *raw = Lu + rb + rq * ATT_Q8_HEAD + 34u * bb;
+            att_q8_split(raw, Lu + ATT_Q8_KC + rq * 256 + 32u * bb, reinterpret_cast<LDS float *>(Lu + ATT_Q8_KS) + t);
             sched_fence();   // one block's words live at a time
-            att_q8_split(raw + 2 * ATT_Q8_RAWB, Lu + ATT_Q8_VC + rr * 256 + 32u * bb,
+            att_q8_split(raw + ATT_Q8_RAWB, Lu + ATT_Q8_VC + rq * 256 + 32u * bb,
                          reinterpret_cast<LDS float *>(Lu + ATT_Q8_VS) + t);
             __syncthreads();
+            kt = Lu + ATT_Q8_KC;
+            vt = Lu + ATT_Q8_VC;
         }
-        // scores: partial dots over dims 8p..8p+7 (ascending) of rows
-        // 8rg + (i ^ mp/4) and slots 4hg + (jj ^ mp%4) in slot i*4 + jj (the
-        // permuted order above), then the reduce-scatter over the 32 lanes of
-        // the half-wave leaves lane p with row 8rg + mp/4, slot 4hg + mp%4
-        {
-            double part[ATT_RG * ATT_HG];
+        // scores: partial dots over dims 8p..8p+7 (ascending fmaf) of rows
+        // rr + 8 (i ^ mp/8) and slots s ^ mp%8 in slot 8i + s; the
+        // reduce-scatter over the half-wave leaves lane p with row rr + 8 (mp/8),
+        // slot mp%8
+        float part[4 * ATT_MAXG];
 #pragma unroll
-            for (uint32_t i = 0; i < ATT_RG; i++) {
-                const uint32_t r = ATT_RG * rg + (i ^ (mp >> 2));
-                const bool nr = owner && t0 + r == (uint32_t)pos;
-                const LDS unsigned char *kr = nr ? reinterpret_cast<const LDS unsigned char *>(knew)
-                                            : q8 ? Lu + ATT_Q8_KC + r * 256
-                                                 : reinterpret_cast<const LDS unsigned char *>(kb) + bo + r * 512;
-                const float ks = !q8 ? 0.0f
-                                : nr ? reinterpret_cast<const LDS float *>(kr + 256)[p >> 2]
-                                     : reinterpret_cast<const LDS float *>(Lu + ATT_Q8_KS)[r * 8 + (p >> 2)];
-                double kd[ATT_DP];
-                att_row8<Q8>(kr, p, ks, kd);
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t r = rr + 8 * (i ^ (mp >> 3));
+            const bool nr = owner && t0 + r == (uint32_t)pos;
+            const LDS unsigned char *kr = nr ? reinterpret_cast<const LDS unsigned char *>(knew)
+                                             : kt + r * (q8 ? 256u : 512u);
+            const float ks = !q8 ? 0.0f
+                            : nr ? reinterpret_cast<const LDS float *>(kr + 256)[p >> 2]
+                                 : reinterpret_cast<const LDS float *>(Lu + ATT_Q8_KS)[r * 8 + (p >> 2)];
+            float kd[8];
+            att_row8<Q8>(kr, p, ks, kd);
 #pragma unroll
-                for (uint32_t jj = 0; jj < ATT_HG; jj++) {
-                    double d = 0.0;
+            for (uint32_t s = 0; s < ATT_MAXG; s++) {
+                float d = 0.0f;
 #pragma unroll
-                    for (uint32_t dd = 0; dd < ATT_DP; dd++) d = fma(qd[jj][dd], kd[dd], d);
-                    part[i * ATT_HG + jj] = d;
-                }
+                for (uint32_t dd = 0; dd < 8; dd++) d = fmaf(qv[s][dd], kd[dd], d);
+                part[i * ATT_MAXG + s] = d;
             }
-            att_rs_step_x16(part);
-            att_rs_step<DPP_MIRROR, 8>(part);
-            att_rs_step<DPP_HALF_MIRROR, 4>(part);
-            att_rs_step<DPP_XOR2, 2>(part);
-            att_rs_step<DPP_XOR1, 1>(part);
-            const uint32_t r = ATT_RG * rg + (mp >> 2), hh = ATT_HG * hg + (mp & 3);
-            sc[hh * ATT_TILE + r] = (t0 + r < kv1) ? part[0] * (double)a.scale : -INFINITY;
         }
-        __syncthreads();
-        // online softmax: head slot hh = t/32 over its 32 rows (lane r);
-        // max and sum over the 32 lanes with DPP plus one cross-row step
+        att_rs_step_x16(part);
+        att_rs_step<DPP_MIRROR, 8>(part);
+        att_rs_step<DPP_HALF_MIRROR, 4>(part);
+        att_rs_step<DPP_XOR2, 2>(part);
+        att_rs_step<DPP_XOR1, 1>(part);
+        // the group's online softmax of slot my_s over its (<= 4) rows of the
+        // tile: the lanes of one slot differ by the lane masks 15 (row i ^ 1)
+        // and 16 (row i ^ 2)
         {
-            const uint32_t hh = t / ATT_TILE, r = t % ATT_TILE;
-            const double s = sc[hh * ATT_TILE + r];
-            double mt = s;
-            mt = fmax(mt, dpp_d<DPP_XOR1>(mt));
-            mt = fmax(mt, dpp_d<DPP_XOR2>(mt));
-            mt = fmax(mt, dpp_d<DPP_HALF_MIRROR>(mt));
-            mt = fmax(mt, dpp_d<DPP_MIRROR>(mt));
-            mt = fmax(mt, __shfl_xor(mt, 16, 64));
-            const double mo = mrun;
-            const double mn = fmax(mo, mt);
-            const double wgt = (s == -INFINITY || hh >= gqa) ? 0.0 : exp(s - mn);
-            double ws = row16_sum_f64(wgt);
-            ws += __shfl_xor(ws, 16, 64);
-            sc[hh * ATT_TILE + r] = wgt;
-            // (an unchanged max: exp(0) = 1 exactly, so the call is skipped)
-            const double cf = (mo == -INFINITY) ? 0.0 : (mo == mn ? 1.0 : exp(mo - mn));
-            lrun = lrun * cf + ws;
+            const uint32_t r = rr + 8 * my_i;
+            const bool valid = my_s < gqa && t0 + r < kv1;
+            const float sv = valid ? part[0] * a.scale : -INFINITY;
+            float mt = fmaxf(sv, dpp_f<DPP_MIRROR>(sv));
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            const float mn = fmaxf(mrun, mt);
+            const float wgt = valid ? att_exp(sv - mn) : 0.0f;
+            float ws = wgt + dpp_f<DPP_MIRROR>(wgt);
+            ws = ws + __shfl_xor(ws, 16, 64);
+            const float cf = mrun == -INFINITY ? 0.0f : (mrun == mn ? 1.0f : att_exp(mrun - mn));
+            const float lc = lrun * cf;
+            lrun = lc + ws;
             mrun = mn;
-            if (r == 0) corr[hh] = cf;
+            wgr[my_i * ATT_MAXG + my_s] = wgt;
+            if (my_i == 0) wgr[4 * ATT_MAXG + my_s] = cf;
         }
-        __syncthreads();
-        // V: rows 8rg+i, slots 4hg+jj, dims 8p.. (the weights are broadcast reads)
+        // (read back by this wave only: LDS accesses of a wave complete in order)
         {
+            const f32x4 c0 = *reinterpret_cast<const LDS f32x4 *>(wgr + 4 * ATT_MAXG);
+            const f32x4 c1 = *reinterpret_cast<const LDS f32x4 *>(wgr + 4 * ATT_MAXG + 4);
+            const float cfv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-            for (uint32_t jj = 0; jj < ATT_HG; jj++) {
-                const double cf = corr[ATT_HG * hg + jj];
+            for (uint32_t s = 0; s < ATT_MAXG; s++)
 #pragma unroll
-                for (uint32_t dd = 0; dd < ATT_DP; dd++) acc[jj][dd] = acc[jj][dd] * cf;
-            }
+                for (uint32_t dd = 0; dd < 8; dd++) acc[s][dd] = acc[s][dd] * cfv[s];
+        }
+        // V: the group's rows ascending, every slot, dims 8p..
 #pragma unroll
-            for (uint32_t i = 0; i < ATT_RG; i++) {
-                const uint32_t r = ATT_RG * rg + i;
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t r = rr + 8 * i;
+            if (t0 + r < kv1) {
                 const bool nr = owner && t0 + r == (uint32_t)pos;
                 const LDS unsigned char *vr = nr ? reinterpret_cast<const LDS unsigned char *>(vnew)
-                                            : q8 ? Lu + ATT_Q8_VC + r * 256
-                                                 : reinterpret_cast<const LDS unsigned char *>(vb) + bo + r * 512;
+                                                 : vt + r * (q8 ? 256u : 512u);
                 const float vs = !q8 ? 0.0f
                                 : nr ? reinterpret_cast<const LDS float *>(vr + 256)[p >> 2]
                                      : reinterpret_cast<const LDS float *>(Lu + ATT_Q8_VS)[r * 8 + (p >> 2)];
-                double wt[ATT_HG];
-#pragma unroll
-                for (uint32_t jj = 0; jj < ATT_HG; jj++) wt[jj] = sc[(ATT_HG * hg + jj) * ATT_TILE + r];
-                double vd[ATT_DP];
+                float vd[8];
                 att_row8<Q8>(vr, p, vs, vd);
+                const f32x4 w0 = *reinterpret_cast<const LDS f32x4 *>(wgr + i * ATT_MAXG);
+                const f32x4 w1 = *reinterpret_cast<const LDS f32x4 *>(wgr + i * ATT_MAXG + 4);
+                const float w8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-                for (uint32_t jj = 0; jj < ATT_HG; jj++)
+                for (uint32_t s = 0; s < 6; s++)
 #pragma unroll
-                    for (uint32_t dd = 0; dd < ATT_DP; dd++) acc[jj][dd] = fma(wt[jj], vd[dd], acc[jj][dd]);
+                    for (uint32_t dd = 0; dd < 8; dd++) acc[s][dd] = fmaf(w8[s], vd[dd], acc[s][dd]);
+                if (gqa > 6) {
+#pragma unroll
+                    for (uint32_t s = 6; s < ATT_MAXG; s++)
+#pragma unroll
+                        for (uint32_t dd = 0; dd < 8; dd++) acc[s][dd] = fmaf(w8[s], vd[dd], acc[s][dd]);
+                }
             }
         }
-        __syncthreads();
-        // the tile after next into the buffer just freed
-        if (j + 2 < ntile) issue_tile(j + 2);
     }
     if (ts) ts[2] = wall_clock64();
 
-    // the chunk's partial: the four row groups' V sums added in order (two
-    // rounds of four dims each through LDS), published with m and l
-    double *pbase = a.part + ((size_t)g * C + c) * gqa * PS;
+    // the chunk's partial: the eight row groups merged per slot (through LDS,
+    // in the tile region): M = max m_g, e_g = exp(m_g - M) (0 for a group
+    // without rows), L and O fmaf chains over the groups ascending
+    float *pbase = a.part + ((size_t)g * C + c) * gqa * PS;
+    LDS float *comb = reinterpret_cast<LDS float *>(L);   // [8 rr][ATT_MAXG][256]
+    LDS float *gm = wl + 8 * (4 * ATT_MAXG + ATT_MAXG);   // [8 rr][ATT_MAXG] m, then l
+    __syncthreads();   // every wave done with the last tile's buffers
+#pragma unroll
+    for (uint32_t s = 0; s < ATT_MAXG; s++) {
+        LDS float *d = comb + (rr * ATT_MAXG + s) * 256 + 8 * p;
+        const f32x4 v0 = {acc[s][0], acc[s][1], acc[s][2], acc[s][3]};
+        const f32x4 v1 = {acc[s][4], acc[s][5], acc[s][6], acc[s][7]};
+        *reinterpret_cast<LDS f32x4 *>(d) = v0;
+        *reinterpret_cast<LDS f32x4 *>(d + 4) = v1;
+    }
+    if (my_i == 0) {
+        gm[rr * ATT_MAXG + my_s] = mrun;
+        gm[8 * ATT_MAXG + rr * ATT_MAXG + my_s] = lrun;
+    }
+    __syncthreads();
     {
-        const uint32_t hh = t >> 5, pp = t & 31;   // output: slot hh, dims 8pp + 4k + 0..3
+        const uint32_t s = t >> 5, po = t & 31;
+        float M = -INFINITY;
 #pragma unroll
-        for (uint32_t k = 0; k < 2; k++) {
-            // value (jj, dd) of lane l of row group rg at comb[(rg*16 + jj*4 + dd)*64 + l]:
-            // every write and read instruction touches 64 consecutive doubles
+        for (uint32_t g2 = 0; g2 < 8; g2++) M = fmaxf(M, gm[g2 * ATT_MAXG + s]);
+        float Lc = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (uint32_t jj = 0; jj < ATT_HG; jj++)
+        for (uint32_t g2 = 0; g2 < 8; g2++) {
+            const float mg = gm[g2 * ATT_MAXG + s];
+            const float e = (s < gqa && mg != -INFINITY) ? att_exp(mg - M) : 0.0f;
+            Lc = fmaf(e, gm[8 * ATT_MAXG + g2 * ATT_MAXG + s], Lc);
+            const f32x4 c0 = *reinterpret_cast<const LDS f32x4 *>(comb + (g2 * ATT_MAXG + s) * 256 + 8 * po);
+            const f32x4 c1 = *reinterpret_cast<const LDS f32x4 *>(comb + (g2 * ATT_MAXG + s) * 256 + 8 * po + 4);
+            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-                for (uint32_t dd = 0; dd < 4; dd++) comb[(rg * 16 + jj * 4 + dd) * 64 + (t & 63)] = acc[jj][4 * k + dd];
-            __syncthreads();
-            // thread (hh, pp) sums row groups 0..3 of wave lane (hh/4)*32 + pp
-            const uint32_t src_lane = (hh / ATT_HG) * 32 + pp, jj = hh % ATT_HG;
-            double o[4];
-#pragma unroll
-            for (uint32_t dd = 0; dd < 4; dd++) {
-                double sum = 0.0;
-#pragma unroll
-                for (uint32_t r4 = 0; r4 < 4; r4++) sum += comb[(r4 * 16 + jj * 4 + dd) * 64 + src_lane];
-                o[dd] = sum;
-            }
-            if (hh < gqa) {
-                double *d = pbase + hh * PS + ATT_DP * pp + 4 * k;
-                st_coh(d, o[0]); st_coh(d + 1, o[1]); st_coh(d + 2, o[2]); st_coh(d + 3, o[3]);
-            }
-            __syncthreads();
+            for (uint32_t dd = 0; dd < 8; dd++) o[dd] = fmaf(e, cv[dd], o[dd]);
         }
-        if ((t & 31) == 0 && hh < gqa) {
-            st_coh(pbase + hh * PS + HD, mrun);
-            st_coh(pbase + hh * PS + HD + 1, lrun);
+        if (s < gqa) {
+            float *d = pbase + s * PS + 8 * po;
+            st_coh4(d, make_float4(o[0], o[1], o[2], o[3]));
+            st_coh4(d + 4, make_float4(o[4], o[5], o[6], o[7]));
+            if (po == 0) {
+                st_coh(pbase + s * PS + HD, M);
+                st_coh(pbase + s * PS + HD + 1, Lc);
+            }
         }
     }
 
     // the merge's element mapping: this workgroup finalises elements
-    // [c*ne, ...) of the head group's gqa*HD outputs, tpe threads per element
-    const uint32_t E = gqa * HD, ne = (E + C - 1) / C, e0 = c * ne, e1 = min(e0 + ne, E);
-    uint32_t tpe = 1;                           // a power of two <= C
-    while (tpe * 2 <= C && tpe * 2 * ne <= BLOCK_THREADS) tpe *= 2;
-    const uint32_t cpt = (C + tpe - 1) / tpe;   // chunks per thread
-    const uint32_t ept = BLOCK_THREADS / tpe;   // elements per pass
+    // [c*ne, ...) of the head group's gqa*HD outputs, one thread each
+    const uint32_t E = gqa * HD, NC = geo.n, ne = (E + NC - 1) / NC, e0 = c * ne, e1 = min(e0 + ne, E);
 
-    // wait for the kv head's C chunks: each publishes generation gen + 1 in
+    // wait for the kv head's NC chunks: each publishes generation gen + 1 in
     // its own flag (one store, after its partial's stores completed) and
-    // waits for all C flags of the head; the merge's gates are loaded while
-    // the flags are polled (a load before the settle would be waited for)
+    // waits for all NC flags of the head
     settle_vmem();
     __syncthreads();
     if (t == 0) st_coh(a.count + rel, gen + 1u);
-    float gate0 = 0.0f;
-    {
-        const uint32_t el = min(e0 + t / tpe, E - 1);
-        gate0 = ld_coh(a.qg + (size_t)(g * gqa + el / HD) * 2 * HD + HD + el % HD);
-    }
     if (t < 64) {
-        const bool okw = att_wait_flags(a.count + g * C, C, gen + 1u, spin_limit, err, ins.dbg_node);
+        const bool okw = att_wait_flags(a.count + g * C, NC, gen + 1u, spin_limit, err, ins.dbg_node);
         if (t == 0) *flag = okw ? 1u : 0u;
     }
     __syncthreads();
     if (*flag == 0) return;
 
-    // merge: M = max m_i, acc = sum_i e_i acc_i, l = sum_i e_i l_i with
-    // e_i = exp(m_i - M), chunks ascending (runs of cpt chunks per thread,
-    // the runs then ascending); out = acc/l * sigmoid(gate).  Every load of
-    // the first pass is issued at once: m and l of each (chunk, slot) and
-    // this thread's first eight chunk values.
-    {
-        const __amdgpu_buffer_rsrc_t r = coh_rsrc(a.part + (size_t)g * C * gqa * PS, C * gqa * PS * 8);
-        double vpre[8];
-        {
-            const uint32_t el = min(e0 + t / tpe, e1 - 1), hh = el / HD, dd = el % HD, i0 = (t % tpe) * cpt;
+    // merge: M = max_c m_c, e_c = exp(m_c - M), L = sum_c e_c l_c and
+    // O = sum_c e_c acc_c as fmaf chains over the chunks ascending;
+    // out = O / L * sigmoid(gate).  One load round trip: every value this
+    // thread folds, its gate and its wave's m / l are loaded before any is used.
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(a.part + (size_t)g * C * gqa * PS, NC * gqa * PS * 4);
+    auto merge = [&](auto nmax) {
+        constexpr uint32_t NM = decltype(nmax)::value;
+        for (uint32_t eb = e0; eb < e1; eb += BLOCK_THREADS) {
+            const uint32_t el = eb + t, elc = min(el, e1 - 1), s = elc / HD, d = elc % HD;
+            float v[NM];
 #pragma unroll
-            for (uint32_t k = 0; k < 8; k++) {
-                const uint32_t i = min(i0 + k, C - 1);
-                vpre[k] = ld_coh8(r, (((size_t)i * gqa + hh) * PS + dd) * 8);
-            }
-        }
-        {
-            // (C*gqa <= 512: two per thread)
-            const uint32_t n = C * gqa, i0 = t, i1 = t + BLOCK_THREADS;
-            const uint32_t j0 = min(i0, n - 1), j1 = min(i1, n - 1);
-            const double m0 = ld_coh8(r, ((size_t)j0 * PS + HD) * 8), l0 = ld_coh8(r, ((size_t)j0 * PS + HD + 1) * 8);
-            const double m1 = ld_coh8(r, ((size_t)j1 * PS + HD) * 8), l1 = ld_coh8(r, ((size_t)j1 * PS + HD + 1) * 8);
-            if (i0 < n) { mw[i0] = m0; mlv[i0] = l0; }
-            if (i1 < n) { mw[i1] = m1; mlv[i1] = l1; }
-        }
-        __syncthreads();
-        // slot h on wave h % 4, chunk i on lane i: M by a wave max, then the
-        // weights e_i and L = sum_i e_i l_i (a wave sum)
-        for (uint32_t h = w; h < gqa; h += WAVES) {
-            const double m = lane < C ? mw[lane * gqa + h] : -INFINITY;
-            double M = m;
+            for (uint32_t k = 0; k < NM; k++) v[k] = ld_coh4b(r, ((min(k, NC - 1) * gqa + s) * PS + d) * 4);
+            const uint32_t h = g * gqa + s;
+            const float gate = ld_coh(a.qg + (size_t)h * 2 * HD + HD + d);
+            if (eb == e0) {
+                // slot sl on wave sl % 4, chunk i on lane i
+                for (uint32_t sl = w; sl < gqa; sl += WAVES) {
+                    const uint32_t ci = min(lane, NC - 1);
+                    const float m = ld_coh4b(r, ((ci * gqa + sl) * PS + HD) * 4);
+                    const float l = ld_coh4b(r, ((ci * gqa + sl) * PS + HD + 1) * 4);
+                    float M = lane < NC ? m : -INFINITY;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) M = fmax(M, __shfl_xor(M, o, 64));
-            const double e = (m == -INFINITY) ? 0.0 : exp(m - M);
-            const double le = (lane < C && e != 0.0) ? e * mlv[lane * gqa + h] : 0.0;
-            const double Ls = wave_sum_f64(le);
-            if (lane < C) mw[lane * gqa + h] = e;
-            if (lane == 0) mM[ATT_MAXG + h] = Ls;
-        }
-        __syncthreads();
-        for (uint32_t eb = e0; eb < e1; eb += ept) {
-            const uint32_t el = eb + t / tpe, sub = t % tpe;
-            const uint32_t elc = min(el, e1 - 1), hh = elc / HD, dd = elc % HD;
-            const uint32_t i0 = sub * cpt, i1 = min(i0 + cpt, C);
-            double O = 0.0;
-            // eight chunks' values per batch, all loads issued first (the
-            // first batch of the first pass is already in flight)
-            for (uint32_t ib = i0; ib < i1; ib += 8) {
-                double v[8];
-#pragma unroll
-                for (uint32_t k = 0; k < 8; k++) {
-                    const uint32_t i = min(ib + k, C - 1);
-                    v[k] = (eb == e0 && ib == i0) ? vpre[k] : ld_coh8(r, (((size_t)i * gqa + hh) * PS + dd) * 8);
+                    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+                    const float e = lane < NC ? att_exp(m - M) : 0.0f;
+                    float Ls = 0.0f;
+                    for (uint32_t k = 0; k < NC; k++) {
+                        const float ek = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), (int)k));
+                        const float lk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), (int)k));
+                        Ls = fmaf(ek, lk, Ls);
+                    }
+                    if (lane < NC) me[lane * ATT_MAXG + sl] = e;
+                    if (lane == 0) mL[sl] = Ls;
                 }
+                __syncthreads();
+            }
+            float O = 0.0f;
 #pragma unroll
-                for (uint32_t k = 0; k < 8; k++) {
-                    const double e = ib + k < i1 ? mw[(ib + k) * gqa + hh] : 0.0;
-                    if (e != 0.0) O = fma(e, v[k], O);
-                }
-            }
-            msum[t] = O;
-            __syncthreads();
-            if (el < e1 && sub == 0) {
-                double tot = 0.0;
-                for (uint32_t s2 = 0; s2 < tpe; s2++) tot += msum[t + s2];
-                const uint32_t h = g * gqa + hh;
-                const float att = (float)(tot / mM[ATT_MAXG + hh]);
-                const float gate = eb == e0 ? gate0 : ld_coh(a.qg + (size_t)h * 2 * HD + HD + dd);
-                st_coh(a.out + (size_t)h * HD + dd, att * dev_sigmoid(gate));
-            }
-            __syncthreads();
+            for (uint32_t k = 0; k < NM; k++)
+                if (k < NC) O = fmaf(me[k * ATT_MAXG + s], v[k], O);
+            if (el < e1) st_coh(a.out + (size_t)h * HD + d, (O / mL[s]) * dev_sigmoid(gate));
         }
-    }
+    };
+    if (NC <= 16) merge(std::integral_constant<uint32_t, 16>{});
+    else if (NC <= 32) merge(std::integral_constant<uint32_t, 32>{});
+    else merge(std::integral_constant<uint32_t, 64>{});
     settle_vmem();
 }
 

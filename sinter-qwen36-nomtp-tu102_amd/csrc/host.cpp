@@ -383,7 +383,7 @@ int sinter_op_gdn_step(const sinter_gdn_args *a, uint32_t blocks, void *stream) 
 
 size_t sinter_attn_part_len(uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t n_chunks) {
     if (!nkv || !n_chunks) return 0;
-    return (size_t)nkv * (n_chunks + (n_chunks + 7) / 8) * (nq / nkv) * (hd + 2);
+    return (size_t)nkv * n_chunks * (nq / nkv) * att_rec(hd);
 }
 
 uint32_t sinter_attn_count_len(uint32_t nkv, uint32_t n_chunks) {

@@ -191,7 +191,7 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
 // Every call on a device shares the array; calls that overlap on one
 // device race.
 constexpr size_t NOALLOC_FLAG_WORDS = 1024;
-constexpr size_t NOALLOC_PART_BYTES = 4u << 20;
+constexpr size_t NOALLOC_PART_BYTES = 2u << 20;
 constexpr size_t NOALLOC_FLAG_OFF = 256, NOALLOC_PART_OFF = NOALLOC_FLAG_OFF + NOALLOC_FLAG_WORDS * 4;
 static __device__ __align__(256) unsigned char scratch[NOALLOC_PART_OFF + NOALLOC_PART_BYTES];
 
@@ -381,7 +381,7 @@ unsigned *noalloc_err_cell() {
 }
 
 int attn_noalloc(const sinter_attn_args &args, uint32_t blocks, hipStream_t s) {
-    const size_t part_bytes = sinter_attn_part_len(args.nq, args.nkv, args.hd, args.n_chunks) * 8;
+    const size_t part_bytes = sinter_attn_part_len(args.nq, args.nkv, args.hd, args.n_chunks) * 4;
     const uint32_t flags = sinter_attn_count_len(args.nkv, args.n_chunks);
     if (part_bytes > NOALLOC_PART_BYTES || flags > NOALLOC_FLAG_WORDS)
         return set_error(SINTER_ERR_ARG,
@@ -395,7 +395,7 @@ int attn_noalloc(const sinter_attn_args &args, uint32_t blocks, hipStream_t s) {
     ins.block_lo = 0;
     ins.block_hi = (uint16_t)blocks;
     sinter_attn_args a = args;
-    a.part = reinterpret_cast<double *>(p + NOALLOC_PART_OFF);
+    a.part = reinterpret_cast<float *>(p + NOALLOC_PART_OFF);
     a.count = reinterpret_cast<uint32_t *>(p + NOALLOC_FLAG_OFF);
     std::memcpy(ins.payload, &a, sizeof a);
     // every chunk starts the call at generation 0 (an earlier call may have

@@ -110,6 +110,23 @@ __host__ __device__ inline size_t sinter_row_bytes_dev(int t, int64_t k) {
     }
 }
 
+// Split-K geometry of decode attention over n_kv >= 1 positions and at most
+// C >= 1 chunks of whole 32-position tiles, each at least chunk_min
+// positions long: T tiles, tpc tiles per chunk, n (1 <= n <= C) non-empty
+// chunks; chunk c covers tiles [c*tpc, min((c+1)*tpc, T)).
+struct AttGeom { uint32_t tiles, tpc, n; };
+__host__ __device__ inline AttGeom att_geom(uint32_t n_kv, uint32_t C, uint32_t chunk_min) {
+    AttGeom g;
+    g.tiles = (n_kv + 31u) / 32u;
+    const uint32_t a = (g.tiles + C - 1u) / C, b = (chunk_min + 31u) / 32u;
+    g.tpc = a > b ? a : b;
+    if (g.tpc == 0) g.tpc = 1;
+    g.n = (g.tiles + g.tpc - 1u) / g.tpc;
+    return g;
+}
+// fp32 elements of one partial record (acc[hd], max, sum; 16-byte aligned)
+__host__ __device__ inline uint32_t att_rec(uint32_t hd) { return hd + 4u; }
+
 // GEMV items: one 256-element group for the quantised types (one Q4_K /
 // Q6_K block, eight Q8_0 blocks), 64 elements for BF16 / F32.
 __host__ __device__ inline uint32_t item_elems(int t) { return (t == SINTER_BF16 || t == SINTER_F32) ? 64u : 256u; }

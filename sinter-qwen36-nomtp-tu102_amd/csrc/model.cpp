@@ -60,8 +60,8 @@ bool is_attn(const sinter_model_config &c, int il) {
 
 }  // namespace
 
-// split-K chunks per kv head: one (kv head, chunk) item per workgroup, at
-// most 64 (the merge tree's two levels of fan-in 8)
+// split-K chunks per kv head at most: one (kv head, chunk) item per
+// workgroup, at most 64 (one merge lane per chunk)
 static uint32_t attn_chunks(uint32_t blocks, uint32_t nkv) {
     return std::min(64u, std::max(1u, blocks / nkv));
 }
@@ -77,7 +77,7 @@ struct sinter_model {
     std::vector<std::array<Tensor, 2>> S;
     float *X = nullptr, *H = nullptr, *qkv = nullptr, *z = nullptr, *al = nullptr, *be = nullptr, *o = nullptr;
     float *ffn = nullptr, *qg = nullptr, *kk = nullptr, *vv = nullptr, *att = nullptr, *logits = nullptr;
-    double *part = nullptr;
+    float *part = nullptr;
     unsigned *count = nullptr;
     sinter_argmax_ws *ws = nullptr;
     std::vector<sinter_instr> prog;
@@ -320,7 +320,8 @@ void push_mixer(sinter_model *m, int il, bool embed) {
         a.hd = (uint32_t)HD;
         a.rope_dims = (uint32_t)c.rope_dims;
         a.n_ctx = (uint32_t)c.n_ctx;
-        a.n_chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
+        a.n_chunks = (uint32_t)c.attn_chunks;
+        a.chunk_min = (uint32_t)c.attn_chunk_min;
         a.theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
         a.eps = c.eps;
         a.scale = 1.0f / std::sqrt((float)HD);
@@ -436,6 +437,8 @@ int check_config(const sinter_model_config &c) {
         return set_error(SINTER_ERR_ARG, "config: attention shape");
     if (!(c.t_kv == 0 || c.t_kv == SINTER_F16 || c.t_kv == SINTER_Q8_0))
         return set_error(SINTER_ERR_ARG, "config: KV cache type must be F16 or Q8_0");
+    if (c.attn_chunks < 0 || c.attn_chunks > 64 || c.attn_chunk_min < 0)
+        return set_error(SINTER_ERR_ARG, "config: attn_chunks must be 0..64, attn_chunk_min >= 0");
     return SINTER_OK;
 }
 
@@ -476,6 +479,12 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
     sinter_host_grid(m->host, &hb, nullptr, nullptr);
     m->blocks = blocks ? std::min(blocks, hb) : hb;
     if ((rc = sinter_host_set_grid(m->host, m->blocks)) != SINTER_OK) return fail(rc);
+    // the split-K attention geometry (at most one chunk per workgroup and kv head)
+    {
+        const uint32_t cmax = attn_chunks(m->blocks, (uint32_t)m->cfg.attn_nkv);
+        m->cfg.attn_chunks = m->cfg.attn_chunks ? (int32_t)std::min((uint32_t)m->cfg.attn_chunks, cmax) : (int32_t)cmax;
+        if (m->cfg.attn_chunk_min == 0) m->cfg.attn_chunk_min = SINTER_ATTN_CHUNK_MIN;
+    }
     if (!hip_ok(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "model stream")) return fail(SINTER_ERR_HIP);
     const sinter_model_config &c = m->cfg;
     const int E = c.n_embd, F = c.n_ff, D = c.gdn_d, HK = c.gdn_hk, HV = c.gdn_hv;
@@ -530,8 +539,8 @@ static int model_create(const sinter_model_config *cfg, int device, uint64_t see
          (m->be = fa(HV)) && (m->o = fa(VD)) && (m->ffn = fa(F)) && (m->qg = fa((size_t)NQ * 2 * HD)) &&
          (m->kk = fa(RW)) && (m->vv = fa(RW)) && (m->att = fa((size_t)NQ * HD)) &&
          (m->logits = ext && ext->logits ? ext->logits : fa(c.n_vocab));
-    const uint32_t chunks = attn_chunks(m->blocks, NKV);
-    ok = ok && (m->part = (double *)dalloc(m, sinter_attn_part_len(NQ, NKV, HD, chunks) * 8));
+    const uint32_t chunks = (uint32_t)c.attn_chunks;
+    ok = ok && (m->part = (float *)dalloc(m, sinter_attn_part_len(NQ, NKV, HD, chunks) * 4));
     ok = ok && (m->count = (unsigned *)dalloc(m, (size_t)sinter_attn_count_len(NKV, chunks) * 4));
     if (!ok) {
         if (gg && std::strncmp(sinter_last_error(), "gguf", 4) == 0) return fail(SINTER_ERR_ARG);
@@ -847,13 +856,13 @@ int sinter_model_buffer(sinter_model *m, const char *name, void **dev_ptr, size_
     const sinter_model_config &c = m->cfg;
     const size_t E = (size_t)c.n_embd, VD = (size_t)c.gdn_hv * c.gdn_d, NQHD = (size_t)c.attn_nq * c.head_dim;
     const size_t C = (size_t)(2 * c.gdn_hk + c.gdn_hv) * c.gdn_d, RW = (size_t)c.attn_nkv * c.head_dim;
-    const uint32_t chunks = attn_chunks(m->blocks, (uint32_t)c.attn_nkv);
+    const uint32_t chunks = (uint32_t)c.attn_chunks;
     struct B { const char *n; void *p; size_t b; } tab[] = {
         {"X", m->X, E * 4}, {"H", m->H, E * 4}, {"qkv", m->qkv, C * 4}, {"z", m->z, VD * 4},
         {"alpha", m->al, (size_t)c.gdn_hv * 4}, {"beta", m->be, (size_t)c.gdn_hv * 4}, {"o", m->o, VD * 4},
         {"ffn", m->ffn, (size_t)c.n_ff * 4}, {"qg", m->qg, NQHD * 2 * 4}, {"k", m->kk, RW * 4}, {"v", m->vv, RW * 4},
         {"att", m->att, NQHD * 4}, {"logits", m->logits, (size_t)c.n_vocab * 4},
-        {"attn_part", m->part, sinter_attn_part_len(c.attn_nq, c.attn_nkv, c.head_dim, chunks) * 8},
+        {"attn_part", m->part, sinter_attn_part_len(c.attn_nq, c.attn_nkv, c.head_dim, chunks) * 4},
         {"attn_count", m->count, (size_t)sinter_attn_count_len(c.attn_nkv, chunks) * 4},
         {"argmax_ws", m->ws, sizeof(sinter_argmax_ws)}};
     for (const B &b : tab)

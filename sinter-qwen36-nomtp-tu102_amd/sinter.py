@@ -62,7 +62,7 @@ class AttnArgs(C.Structure):
                 ("part", vp), ("count", vp), ("out", vp), ("pass_cell", vp),
                 ("nq", C.c_uint32), ("nkv", C.c_uint32), ("hd", C.c_uint32), ("rope_dims", C.c_uint32),
                 ("n_ctx", C.c_uint32), ("n_chunks", C.c_uint32), ("theta_scale", C.c_float),
-                ("eps", C.c_float), ("scale", C.c_float), ("kv_type", C.c_uint32)]
+                ("eps", C.c_float), ("scale", C.c_float), ("kv_type", C.c_uint32), ("chunk_min", C.c_uint32)]
 
 
 class ModelBindings(C.Structure):
@@ -85,11 +85,12 @@ class ModelConfig(C.Structure):
                 ("conv_k", C.c_int32), ("attn_nq", C.c_int32), ("attn_nkv", C.c_int32),
                 ("head_dim", C.c_int32), ("rope_dims", C.c_int32), ("rope_base", C.c_float),
                 ("eps", C.c_float), ("n_ctx", C.c_int32), ("t_default", C.c_int32), ("t_attn_v", C.c_int32),
-                ("t_ffn_down", C.c_int32), ("t_output", C.c_int32), ("t_embd", C.c_int32), ("t_kv", C.c_int32)]
+                ("t_ffn_down", C.c_int32), ("t_output", C.c_int32), ("t_embd", C.c_int32), ("t_kv", C.c_int32),
+                ("attn_chunks", C.c_int32), ("attn_chunk_min", C.c_int32)]
 
 
 assert C.sizeof(Instr) == 256 and C.sizeof(GemvSeg) == 40
-assert C.sizeof(GemvArgs) == 224 and C.sizeof(GdnArgs) == 80 and C.sizeof(AttnArgs) == 128
+assert C.sizeof(GemvArgs) == 224 and C.sizeof(GdnArgs) == 80 and C.sizeof(AttnArgs) == 136
 
 
 def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64, kv="f16"):
@@ -316,6 +317,9 @@ class Model:
             check(lib().sinter_model_get_config(h, C.byref(cfg)), "get_config")
         else:
             check(lib().sinter_model_create(C.byref(cfg), device, seed, blocks, C.byref(h)), "model_create")
+        # the configuration as the model resolved it (defaults filled in)
+        cfg = ModelConfig()
+        check(lib().sinter_model_get_config(h, C.byref(cfg)), "get_config")
         self.cfg = cfg
         self.h = h
 

@@ -110,8 +110,12 @@ class GraphExec:
     QWeight; `alias` maps a node/leaf reference to another one (to splice
     sections of the graph together)."""
 
-    def __init__(self, nodes, leaves, orc, bind, alias=None):
+    def __init__(self, nodes, leaves, orc, bind, alias=None, attn_split=(64, 128)):
+        """attn_split: (chunks, chunk_min) of the split-K attention whose
+        declared fp32 folds FLASH_ATTN_EXT is evaluated with (or_attn_split,
+        the attention the product runs)."""
         self.nodes, self.leaves, self.orc = nodes, leaves, orc
+        self.attn_split = attn_split
         self.vals = {}
         self.bind = bind
         self.alias = alias or {}
@@ -326,8 +330,8 @@ class GraphExec:
             kc = np.ascontiguousarray(k.buf[k.off:k.off + n_kv * NKV * HD])
             vc = np.ascontiguousarray(v.buf[v.off:v.off + n_kv * NKV * HD])
             out = np.zeros(NQ * HD, np.float32)
-            self.L.or_attn_decode(qf.ctypes.data, kc.ctypes.data, vc.ctypes.data, n_att, NQ, NKV, HD, NKV * HD,
-                                  scale, out.ctypes.data)
+            self.L.or_attn_split(qf.ctypes.data, kc.ctypes.data, vc.ctypes.data, self.orc.F16, n_att, NQ, NKV, HD,
+                                 scale, self.attn_split[0], self.attn_split[1], out.ctypes.data)
             del kb
             return T(out, ne)
         raise NotImplementedError("op %s (n%d)" % (op, i))

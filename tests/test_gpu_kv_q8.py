@@ -27,10 +27,10 @@ def q8_rows(orc, x):
     return out
 
 
-@pytest.mark.parametrize("pos,n_ctx,chunks", [(0, 64, 64), (5, 4096, 64), (1000, 4096, 64), (4095, 4096, 7),
-                                              (300, 4096, 1), (2000, 4096, 9), (3000, 4096, 17),
-                                              (32767, 32768, 64)])
-def test_attn_decode_q8_cache_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
+@pytest.mark.parametrize("pos,n_ctx,chunks,cmin", [(0, 64, 64, 0), (5, 4096, 64, 0), (1000, 4096, 64, 128),
+                                                   (4095, 4096, 7, 0), (300, 4096, 1, 0), (2000, 4096, 9, 256),
+                                                   (3000, 4096, 17, 0), (32767, 32768, 64, 128)])
+def test_attn_decode_q8_cache_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks, cmin):
     torch = torch_gpu
     NQ, NKV, HD = 24, 4, 256
     RW = NKV * HD
@@ -48,12 +48,12 @@ def test_attn_decode_q8_cache_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chu
     ts = orc.lib().or_rope_theta_scale(1e7, 64)
     dK, dV = dev(torch, K), dev(torch, V)
     dqg, dk, dv_, dqn, dkn = dev(torch, qg), dev(torch, k), dev(torch, v), dev(torch, qn), dev(torch, kn)
-    part = torch.zeros(sn.lib().sinter_attn_part_len(NQ, NKV, HD, chunks), dtype=torch.float64, device="cuda")
+    part = torch.zeros(sn.lib().sinter_attn_part_len(NQ, NKV, HD, chunks), dtype=torch.float32, device="cuda")
     cnt = torch.zeros(sn.lib().sinter_attn_count_len(NKV, chunks), dtype=torch.int32, device="cuda")
     out = empty_f32(torch, NQ * HD)
     cell = dev(torch, np.array([0, pos, 0, 0], np.int32))
     a = sn.AttnArgs(nq=NQ, nkv=NKV, hd=HD, rope_dims=64, n_ctx=n_ctx, n_chunks=chunks, theta_scale=ts, eps=1e-6,
-                    scale=0.0625, kv_type=Q8_0)
+                    scale=0.0625, kv_type=Q8_0, chunk_min=cmin)
     a.qg, a.k, a.v, a.q_norm, a.k_norm = dqg.data_ptr(), dk.data_ptr(), dv_.data_ptr(), dqn.data_ptr(), dkn.data_ptr()
     a.kc, a.vc, a.part, a.count, a.out, a.pass_cell = (dK.data_ptr(), dV.data_ptr(), part.data_ptr(),
                                                        cnt.data_ptr(), out.data_ptr(), cell.data_ptr())
@@ -76,15 +76,18 @@ def test_attn_decode_q8_cache_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chu
     assert np.array_equal(host(dK)[pos], K[pos])
     assert np.array_equal(host(dV)[pos], V[pos])
     att = np.zeros((NQ, HD), np.float32)
-    L.or_attn_decode_kv(qr.ctypes.data, K.ctypes.data, V.ctypes.data, Q8_0, pos + 1, NQ, NKV, HD, 0.0625,
-                        att.ctypes.data)
+    L.or_attn_split(qr.ctypes.data, K.ctypes.data, V.ctypes.data, Q8_0, pos + 1, NQ, NKV, HD, 0.0625, chunks, cmin,
+                    att.ctypes.data)
     gate = qg.reshape(NQ, 2, HD)[:, 1]
-    ref = np.array([[np.float32(att[h, i]) * np.float32(L.or_sigmoid(float(gate[h, i]))) for i in range(HD)]
-                    for h in range(NQ)], np.float32)
+    sig = np.array([[L.or_sigmoid(float(gate[h, i])) for i in range(HD)] for h in range(NQ)], np.float32)
+    ref = (att * sig).astype(np.float32)
     got = host(out).reshape(NQ, HD)
-    ulp = np.abs(np.spacing(ref))
-    assert np.all(np.abs(got - ref) <= ulp), np.abs(got - ref).max()
-    assert np.mean(got == ref) > 0.999
+    assert np.array_equal(got, ref), (np.abs(got - ref).max(), np.mean(got == ref))
+    # the pin: exact fp64 attention over the dequantised cache within rel L2 1e-5
+    ex = np.zeros((NQ, HD), np.float32)
+    L.or_attn_decode_kv(qr.ctypes.data, K.ctypes.data, V.ctypes.data, Q8_0, pos + 1, NQ, NKV, HD, 0.0625,
+                        ex.ctypes.data)
+    assert np.linalg.norm(got - ex * sig) <= 1e-5 * np.linalg.norm(ex * sig)
 
 
 def test_device_q8_0_synth_equals_host(sn, torch_gpu):

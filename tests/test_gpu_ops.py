@@ -354,13 +354,18 @@ def test_gdn_step_matches_oracle(sn, orc, torch_gpu, cols, blocks):
     assert np.array_equal(host(do), o)
 
 
-@pytest.mark.parametrize("pos,n_ctx,chunks", [(0, 64, 64), (5, 4096, 64), (1000, 4096, 64), (4095, 4096, 64),
-                                              (4095, 4096, 7), (40000, 40960, 64), (300, 4096, 1),
-                                              (2000, 4096, 9), (3000, 4096, 17), (32767, 32768, 64),
-                                              (131071, 131072, 64)])
-def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
+@pytest.mark.parametrize("pos,n_ctx,chunks,cmin,nq,nkv", [
+    (0, 64, 64, 0, 24, 4), (5, 4096, 64, 0, 24, 4), (1000, 4096, 64, 0, 24, 4), (4095, 4096, 64, 0, 24, 4),
+    (4095, 4096, 64, 128, 24, 4), (4100, 4352, 64, 256, 24, 4), (4095, 4096, 7, 0, 24, 4),
+    (40000, 40960, 64, 128, 24, 4), (300, 4096, 1, 0, 24, 4), (2000, 4096, 9, 0, 24, 4),
+    (3000, 4096, 17, 1000, 24, 4), (32767, 32768, 64, 128, 24, 4), (131071, 131072, 64, 128, 24, 4),
+    (777, 1024, 32, 64, 16, 2), (777, 1024, 32, 0, 8, 8), (95, 128, 64, 0, 12, 4)])
+def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks, cmin, nq, nkv):
+    """The fp32 split-K attention op (norms, rope, append, chunks, merge,
+    gate) bit-identical to the oracle's restatement of its declared folds
+    (or_attn_split), and within rel L2 1e-5 of the exact fp64 attention."""
     torch = torch_gpu
-    NQ, NKV, HD = 24, 4, 256
+    NQ, NKV, HD = nq, nkv, 256
     RW = NKV * HD
     rng = np.random.default_rng(20 + pos)
     qg = (rng.standard_normal(NQ * 2 * HD) * 2).astype(np.float32)
@@ -375,16 +380,17 @@ def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     ts = orc.lib().or_rope_theta_scale(1e7, 64)
     dK, dV = dev(torch, K.view(np.uint16)), dev(torch, V.view(np.uint16))
     dqg, dk, dv_, dqn, dkn = dev(torch, qg), dev(torch, k), dev(torch, v), dev(torch, qn), dev(torch, kn)
-    part = torch.zeros(sn.lib().sinter_attn_part_len(NQ, NKV, HD, chunks), dtype=torch.float64, device="cuda")
+    part = torch.zeros(sn.lib().sinter_attn_part_len(NQ, NKV, HD, chunks), dtype=torch.float32, device="cuda")
     cnt = torch.zeros(sn.lib().sinter_attn_count_len(NKV, chunks), dtype=torch.int32, device="cuda")
     out = empty_f32(torch, NQ * HD)
     cell = dev(torch, np.array([0, pos, 0, 0], np.int32))
     a = sn.AttnArgs(nq=NQ, nkv=NKV, hd=HD, rope_dims=64, n_ctx=n_ctx, n_chunks=chunks, theta_scale=ts, eps=1e-6,
-                    scale=0.0625)
+                    scale=0.0625, chunk_min=cmin)
     a.qg, a.k, a.v, a.q_norm, a.k_norm = dqg.data_ptr(), dk.data_ptr(), dv_.data_ptr(), dqn.data_ptr(), dkn.data_ptr()
     a.kc, a.vc, a.part, a.count, a.out, a.pass_cell = (dK.data_ptr(), dV.data_ptr(), part.data_ptr(),
                                                        cnt.data_ptr(), out.data_ptr(), cell.data_ptr())
-    print(f"attn_decode pos={pos} n_ctx={n_ctx} chunks={chunks} blocks=256", flush=True)
+    print(f"attn_decode pos={pos} n_ctx={n_ctx} chunks={chunks} chunk_min={cmin} nq={nq} nkv={nkv} blocks=256",
+          flush=True)
     sn.check(sn.lib().sinter_op_attn_decode(C.byref(a), 256, C.c_void_p(stream(torch))), "attn")
     torch.cuda.synchronize()
     assert sn.op_error()[0] == 0
@@ -413,16 +419,18 @@ def test_attn_decode_matches_oracle(sn, orc, torch_gpu, pos, n_ctx, chunks):
     assert np.array_equal(host(dK)[pos], K[pos].view(np.uint16))
     assert np.array_equal(host(dV)[pos], V[pos].view(np.uint16))
     att = np.zeros((NQ, HD), np.float32)
-    L.or_attn_decode(qr.ctypes.data, K.ctypes.data, V.ctypes.data, pos + 1, NQ, NKV, HD, RW, 0.0625, att.ctypes.data)
+    L.or_attn_split(qr.ctypes.data, K.ctypes.data, V.ctypes.data, orc.F16, pos + 1, NQ, NKV, HD, 0.0625, chunks, cmin,
+                    att.ctypes.data)
     gate = qg.reshape(NQ, 2, HD)[:, 1]
-    ref = np.array([[np.float32(att[h, i]) * np.float32(L.or_sigmoid(float(gate[h, i]))) for i in range(HD)]
-                    for h in range(NQ)], np.float32)
+    sig = np.array([[L.or_sigmoid(float(gate[h, i])) for i in range(HD)] for h in range(NQ)], np.float32)
+    ref = (att * sig).astype(np.float32)
     got = host(out).reshape(NQ, HD)
-    # fp64 softmax folded in a different (split) order: equal after the fp32
-    # rounding except with ~1e-8 probability per element; allow 1 ulp
-    ulp = np.abs(np.spacing(ref))
-    assert np.all(np.abs(got - ref) <= ulp), np.abs(got - ref).max()
-    assert np.mean(got == ref) > 0.999
+    assert np.array_equal(got, ref), (np.abs(got - ref).max(), np.mean(got == ref))
+    # the pin: exact fp64 attention (or_attn_decode) within rel L2 1e-5
+    ex = np.zeros((NQ, HD), np.float32)
+    L.or_attn_decode(qr.ctypes.data, K.ctypes.data, V.ctypes.data, pos + 1, NQ, NKV, HD, RW, 0.0625, ex.ctypes.data)
+    exg = ex * sig
+    assert np.linalg.norm(got - exg) <= 1e-5 * np.linalg.norm(exg)
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, BF16])

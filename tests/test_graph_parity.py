@@ -56,7 +56,7 @@ def test_captured_graph_matches_oracle_decode(sn, orc, graph):
     cfg = orc.Cfg(n_layer=4, attn_every=4, n_embd=E, n_ff=F, n_vocab=VOCAB, gdn_hk=HK, gdn_hv=HV, gdn_d=D,
                   conv_k=DCONV, attn_nq=NQ, attn_nkv=NKV, head_dim=HD, rope_dims=64, rope_base=1e7, eps=1e-6,
                   n_ctx=NCTX, t_default=orc.Q4_K, t_attn_v=orc.Q6_K, t_ffn_down=orc.Q6_K, t_output=orc.Q6_K,
-                  t_embd=orc.Q4_K)
+                  t_embd=orc.Q4_K, attn_chunks=64, attn_chunk_min=128)
     W, Y = sn.SYN_WEIGHT, sn.SYN_NORMAL
     seed = 777
     w = {}   # (layer, slot) -> (type, array, k, rows)
@@ -163,7 +163,8 @@ def test_captured_graph_matches_oracle_decode(sn, orc, graph):
     blocks = {b: sorted(i for i, n in nodes.items() if n["block"] == b) for b in ("pre", "0", "1", "2", "3", "post")}
     last3 = blocks["3"][-1]
     post_src = [r for r in nodes[blocks["post"][0]]["src"] if r.startswith("n")][0]
-    ex = GraphExec(nodes, leaves, orc, bind, alias={"l%d" % trunk_root[0]: "n0", post_src: "n%d" % last3})
+    ex = GraphExec(nodes, leaves, orc, bind, alias={"l%d" % trunk_root[0]: "n0", post_src: "n%d" % last3},
+                   attn_split=(cfg.attn_chunks, cfg.attn_chunk_min))
     order = sorted(blocks["pre"] + blocks["0"] + blocks["1"] + blocks["2"] + blocks["3"]) + blocks["post"]
     vals = ex.run(order)
 

@@ -414,3 +414,74 @@ def test_argmax_first_max_wins(orc):
     assert orc.lib().or_argmax_first(P(x), 6) == 1
     x = np.array([-np.inf, -2, -2], np.float32)
     assert orc.lib().or_argmax_first(P(x), 3) == 1
+
+
+# ---------------------------------------------------------------- split-K attention (fp32 declared folds)
+
+def _attn_case(rng, n, nq, nkv, hd=256):
+    q = rng.standard_normal((nq, hd)).astype(np.float32)
+    K = rng.standard_normal((n, nkv * hd)).astype(np.float16)
+    V = rng.standard_normal((n, nkv * hd)).astype(np.float16)
+    return q, K, V
+
+
+@pytest.mark.parametrize("n,nq,nkv,chunks,cmin", [(1, 24, 4, 64, 0), (33, 24, 4, 64, 0), (100, 8, 2, 3, 0),
+                                                  (4097, 24, 4, 64, 128), (4097, 24, 4, 64, 256),
+                                                  (777, 16, 2, 32, 1000), (64, 4, 4, 1, 0), (300, 12, 4, 9, 64)])
+def test_attn_split_near_exact_attention(orc, n, nq, nkv, chunks, cmin):
+    """or_attn_split (fp32 folds) within rel L2 1e-5 of the exact fp64
+    attention, and its geometry covers [0, n) with at most `chunks`
+    non-empty chunks of whole tiles, each at least chunk_min long (but the
+    last)."""
+    rng = np.random.default_rng(n + nq)
+    q, K, V = _attn_case(rng, n, nq, nkv)
+    out = np.zeros((nq, 256), np.float32)
+    ex = np.zeros((nq, 256), np.float32)
+    L = orc.lib()
+    L.or_attn_split(P(q), P(K), P(V), 1, n, nq, nkv, 256, 0.0625, chunks, cmin, P(out))
+    L.or_attn_decode(P(q), P(K.view(np.uint16)), P(V.view(np.uint16)), n, nq, nkv, 256, nkv * 256, 0.0625, P(ex))
+    assert np.linalg.norm(out - ex) <= 1e-5 * np.linalg.norm(ex)
+    T, tpc, nch = C.c_int(), C.c_int(), C.c_int()
+    L.or_attn_geom(n, chunks, cmin, C.byref(T), C.byref(tpc), C.byref(nch))
+    assert T.value == -(-n // 32) and 1 <= nch.value <= chunks
+    assert (nch.value - 1) * tpc.value < T.value <= nch.value * tpc.value      # every chunk non-empty, all covered
+    assert tpc.value * 32 >= cmin and tpc.value >= -(-T.value // chunks)
+
+
+def test_attn_split_closed_forms(orc):
+    """One position: the output is the V row exactly (weight exp(0) = 1, one
+    chunk).  Identical keys: every weight is 1, so the output is the mean of
+    the V rows (to fp32 rounding).  A shifted score (q scaled so all scores
+    move together) leaves the softmax unchanged."""
+    rng = np.random.default_rng(5)
+    L = orc.lib()
+    q, K, V = _attn_case(rng, 1, 8, 2)
+    out = np.zeros((8, 256), np.float32)
+    L.or_attn_split(P(q), P(K), P(V), 1, 1, 8, 2, 256, 0.0625, 64, 0, P(out))
+    assert np.array_equal(out, np.repeat(V.astype(np.float32).reshape(2, 256), 4, axis=0))
+    n = 200
+    q, K, V = _attn_case(rng, n, 8, 2)
+    K[:] = K[0]
+    L.or_attn_split(P(q), P(K), P(V), 1, n, 8, 2, 256, 0.0625, 7, 0, P(out))
+    mean = V.astype(np.float64).reshape(n, 2, 256).mean(axis=0)
+    assert np.allclose(out.reshape(2, 4, 256), mean[:, None, :], rtol=2e-6, atol=2e-6)
+
+
+def test_attn_split_planted_mistakes_are_caught(orc):
+    """The fp64 pin separates the fold from plausible mistakes: attention with
+    the wrong scale, or with the last position dropped, is far outside the
+    1e-5 band the correct fold meets."""
+    rng = np.random.default_rng(9)
+    L = orc.lib()
+    n, nq, nkv = 300, 8, 2
+    q, K, V = _attn_case(rng, n, nq, nkv)
+    q *= 8
+    ex = np.zeros((nq, 256), np.float32)
+    L.or_attn_decode(P(q), P(K.view(np.uint16)), P(V.view(np.uint16)), n, nq, nkv, 256, nkv * 256, 0.0625, P(ex))
+    good = np.zeros((nq, 256), np.float32)
+    L.or_attn_split(P(q), P(K), P(V), 1, n, nq, nkv, 256, 0.0625, 9, 0, P(good))
+    assert np.linalg.norm(good - ex) <= 1e-6 * np.linalg.norm(ex)
+    for args in ((n, 0.125), (n - 1, 0.0625)):
+        bad = np.zeros((nq, 256), np.float32)
+        L.or_attn_split(P(q), P(K), P(V), 1, args[0], nq, nkv, 256, args[1], 9, 0, P(bad))
+        assert np.linalg.norm(bad - ex) > 1e-5 * np.linalg.norm(ex)

@@ -50,7 +50,7 @@ def run_pair(sn, orc, torch, nq, nkv, pos, n_ctx, chunks, seed):
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     L = sn.lib()
     # the existing entry point on caller workspace
-    part = torch.zeros(L.sinter_attn_part_len(nq, nkv, 256, chunks), dtype=torch.float64, device="cuda")
+    part = torch.zeros(L.sinter_attn_part_len(nq, nkv, 256, chunks), dtype=torch.float32, device="cuda")
     cnt = torch.zeros(L.sinter_attn_count_len(nkv, chunks), dtype=torch.int32, device="cuda")
     a.kc, a.vc, a.out = bufs[0]["K"].data_ptr(), bufs[0]["V"].data_ptr(), bufs[0]["out"].data_ptr()
     a.part, a.count = part.data_ptr(), cnt.data_ptr()
@@ -82,13 +82,13 @@ def test_noalloc_attention_equals_workspace_entry_point(sn, orc, torch_gpu):
 def test_noalloc_attention_refuses_what_it_cannot_hold(sn, orc, torch_gpu):
     torch = torch_gpu
     L = sn.lib()
-    a, keep, bufs = make_case(sn, orc, torch, 48, 6, 100, 256, 40, 3)   # 6*45*8*258*8 B > 4 MiB of partials
+    a, keep, bufs = make_case(sn, orc, torch, 64, 8, 100, 256, 32, 3)   # 8*32*8*260*4 B > 2 MiB of partials
     a.kc, a.vc, a.out = bufs[0]["K"].data_ptr(), bufs[0]["V"].data_ptr(), bufs[0]["out"].data_ptr()
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert L.sinter_op_attn_decode_noalloc(C.byref(a), 256, st) == sn.ERR_ARG
     assert b"scratch maximum" in L.sinter_last_error()
     a.n_chunks = 8
-    dummy = torch.zeros(16, dtype=torch.float64, device="cuda")
+    dummy = torch.zeros(16, dtype=torch.float32, device="cuda")
     a.part = dummy.data_ptr()                  # workspace is the library's: refused
     assert L.sinter_op_attn_decode_noalloc(C.byref(a), 256, st) == sn.ERR_ARG
     torch.cuda.synchronize()
