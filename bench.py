@@ -54,6 +54,29 @@ def bytes_per_token(cfg, m, n_attended):
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_sinter_interp_kquant_e2e_q4km_ctx4096.md")
 
 
+HBM_PEAK_BYTES, HBM_PEAK_REPS = 2 << 30, 5
+
+
+def measured_peak():
+    """The box's measured HBM bandwidth (sinter_hbm_peak: a library read
+    stream and a copy over a 2 GiB buffer, far past the 256 MB memory-side
+    cache, 5 timed passes each): {"read": GB/s, "copy": GB/s}."""
+    import ctypes as C
+    import sinter
+    r, c = C.c_double(), C.c_double()
+    sinter.check(sinter.lib().sinter_hbm_peak(HBM_PEAK_BYTES, HBM_PEAK_REPS, C.byref(r), C.byref(c)), "hbm_peak")
+    return {"read": round(r.value, 1), "copy": round(c.value, 1)}
+
+
+def roofline_peaks(achieved):
+    """roofline fields for the measured peak (the decode reads ~97 % of its
+    bytes, so the read stream is its practical ceiling)"""
+    pk = measured_peak()
+    return {"peak_measured": pk["read"], "frac_measured": round(achieved / pk["read"], 4),
+            "peak_measured_how": f"sinter_hbm_peak read stream, {HBM_PEAK_BYTES >> 30} GiB x {HBM_PEAK_REPS} "
+                                 f"(copy: {pk['copy']} GB/s read+written)"}
+
+
 def kernel_source_digest():
     """sha256 of the interpreter's sources (interp.hip and the csrc/*.h
     headers, sorted by name) and of the compiler flags it is built with
@@ -226,6 +249,7 @@ def op_bench(args):
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": m.info()["kernel"],
                      "roofline_us": round(nbytes / (PEAK_GBS * 1e9) * 1e6, 3)},
     }
+    line["roofline"].update(roofline_peaks(achieved))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = op_cpu_baseline(m, c, pos)
     m.close()
@@ -513,11 +537,14 @@ def main():
               "(the 27B model fits one MI355X; no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
 
-    # Only libsinter's HIP runtime is loaded (no torch here): torch bundles its
-    # own HIP and HSA runtimes, and two of each in one process do not tear
-    # down cleanly at exit under rocprofv3.  Every model call below returns
-    # after its device work has finished.
+    # The decode, op and calibration runs need no torch: they load libsinter on
+    # the system ROCm runtime, the one rocprofv3 belongs to (torch would bring
+    # its own bundled HIP/HSA runtime into the process).  Every model call
+    # below returns after its device work has finished.  The batched-GEMV run
+    # uses torch for its buffers, so torch's runtime is loaded there.
     import sinter
+    if not args.ubatch:
+        sinter.use_system_runtime()
 
     if args.copy_calibration:
         n = args.copy_calibration << 20
@@ -628,6 +655,7 @@ def main():
         "single_pass": {"ms_per_token": round(sp_ms, 4), "calls": 8,
                         "path": "sinter_model_decode: one cooperative launch per token, token read back"},
     }
+    line["roofline"].update(roofline_peaks(achieved))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(m, args.ctx, args.cpu_seconds)
     m.close()

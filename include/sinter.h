@@ -356,6 +356,15 @@ int sinter_op_attn_decode_noalloc(const sinter_attn_args *a, uint32_t blocks, vo
  * copy kernel, so that FETCH_SIZE / WRITE_SIZE of a copy of known size can
  * scale the same counters read on the interpreter. */
 int sinter_copy_calibration(int device, size_t bytes, int reps);
+
+/* Measured HBM bandwidth on the current device (a diagnostic, no counterpart
+ * in the reference, which quotes its practical peak from a copy benchmark,
+ * k0/ops/NOTES-gemv.md:58-72): `bytes` (>= 64 MiB, rounded down to 16 MiB)
+ * of device memory read by a streaming kernel `reps` times, and copied half
+ * to half `reps` times, after one untimed pass of each.  read_gbs = bytes
+ * read / time; copy_gbs = bytes read + written / time (1e9 B/s).  Buffers
+ * well past the 256 MB memory-side cache measure HBM. */
+int sinter_hbm_peak(uint64_t bytes, uint32_t reps, double *read_gbs, double *copy_gbs);
 /* Grid-barrier litmus on the current device (mirrors tests/litmus_boundary.cu:1-18
  * and docs/SYNC-FINDINGS.md:9-32 of the reference; a diagnostic, not a decode
  * entry point).  `blocks` co-resident workgroups cross the interpreter's grid

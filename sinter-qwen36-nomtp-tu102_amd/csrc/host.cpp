@@ -583,6 +583,28 @@ struct sinter_host {
     std::vector<sinter_instr> prog;       // host copy of the uploaded program
 };
 
+// Wait until the work queued on s has finished, or timeout_ms passed
+// (SINTER_ERR_TIMEOUT; SINTER_ERR_HIP on a device error).  A launch runs for
+// milliseconds and the caller needs its result at once, so the stream is
+// polled without sleeping (yielding the core between queries) for the first
+// WAIT_SPIN_MS -- a sleeping poll adds its sleep quantum plus the scheduler's
+// wake-up latency to every pass -- and with 100 us sleeps after that.
+static constexpr double WAIT_SPIN_MS = 2000.0;
+static int wait_stream(hipStream_t s, double timeout_ms, const char *what) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const auto deadline = t0 + std::chrono::duration<double, std::milli>(timeout_ms);
+    const auto spin_end = t0 + std::chrono::duration<double, std::milli>(WAIT_SPIN_MS);
+    for (;;) {
+        const hipError_t q = hipStreamQuery(s);
+        if (q == hipSuccess) return SINTER_OK;
+        if (q != hipErrorNotReady) return hip_ok(q, what) ? SINTER_OK : SINTER_ERR_HIP;
+        const auto now = std::chrono::steady_clock::now();
+        if (now > deadline) return SINTER_ERR_TIMEOUT;
+        if (now < spin_end) std::this_thread::yield();
+        else std::this_thread::sleep_for(std::chrono::microseconds(100));
+    }
+}
+
 static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     InterpCtl ctl;
     std::memset(&ctl, 0, sizeof ctl);
@@ -607,20 +629,12 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     if (!hip_ok(hipEventRecord(h->ev1, h->stream), "event")) return SINTER_RUN_ERR;
     h->passes_done += n_passes;
     // wait with a watchdog; the kernel's own barrier spin limit bounds it too
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double, std::milli>(timeout_ms);
-    for (;;) {
-        const hipError_t q = hipStreamQuery(h->stream);
-        if (q == hipSuccess) break;
-        if (q != hipErrorNotReady) {
-            hip_ok(q, "interpreter");
-            return SINTER_RUN_ERR;
-        }
-        if (std::chrono::steady_clock::now() > deadline) {
-            set_error(SINTER_ERR_TIMEOUT, "watchdog: pass did not finish in %.1f ms", timeout_ms);
-            return SINTER_RUN_TIMEOUT;
-        }
-        std::this_thread::sleep_for(std::chrono::microseconds(50));
+    const int ws = wait_stream(h->stream, timeout_ms, "interpreter");
+    if (ws == SINTER_ERR_TIMEOUT) {
+        set_error(SINTER_ERR_TIMEOUT, "watchdog: pass did not finish in %.1f ms", timeout_ms);
+        return SINTER_RUN_TIMEOUT;
     }
+    if (ws != SINTER_OK) return SINTER_RUN_ERR;
     (void)hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1);
     unsigned e[2] = {0, 0};
     if (!hip_ok(hipMemcpy(e, h->d_cells + 32, 8, hipMemcpyDeviceToHost), "error cell")) return SINTER_RUN_ERR;
@@ -783,17 +797,15 @@ int sinter_host_launch(sinter_host *h) {
 
 int sinter_host_run_pass(sinter_host *h, int32_t token, double timeout_ms) {
     if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_pass before launch"), SINTER_RUN_ERR;
-    if (!hip_ok(hipMemcpyAsync(&h->d_pass->token, &token, 4, hipMemcpyHostToDevice, h->stream), "token write"))
-        return SINTER_RUN_ERR;
+    if (!hip_ok(hipMemsetD32Async(&h->d_pass->token, token, 1, h->stream), "token write")) return SINTER_RUN_ERR;
     return run_launch(h, 1, timeout_ms);
 }
 
 int sinter_host_run_passes(sinter_host *h, int32_t token, uint32_t n_passes, int32_t *tokens_out, double timeout_ms) {
     if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_passes before launch"), SINTER_RUN_ERR;
     if (n_passes == 0 || n_passes > h->history_cap) return set_error(SINTER_ERR_ARG, "n_passes"), SINTER_RUN_ERR;
-    int32_t cell[2] = {token, 0};
-    if (!hip_ok(hipMemcpyAsync(&h->d_pass->token, &cell[0], 4, hipMemcpyHostToDevice, h->stream), "token write") ||
-        !hip_ok(hipMemcpyAsync(&h->d_pass->steps, &cell[1], 4, hipMemcpyHostToDevice, h->stream), "steps reset"))
+    if (!hip_ok(hipMemsetD32Async(&h->d_pass->token, token, 1, h->stream), "token write") ||
+        !hip_ok(hipMemsetD32Async(&h->d_pass->steps, 0, 1, h->stream), "steps reset"))
         return SINTER_RUN_ERR;
     const int rs = run_launch(h, n_passes, timeout_ms);
     if (rs != SINTER_RUN_OK) return rs;
@@ -806,14 +818,9 @@ int sinter_host_run_passes(sinter_host *h, int32_t token, uint32_t n_passes, int
 int sinter_host_shutdown(sinter_host *h, double timeout_ms) {
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
     if (!h->launched) return SINTER_OK;
-    const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double, std::milli>(timeout_ms);
-    for (;;) {
-        const hipError_t q = hipStreamQuery(h->stream);
-        if (q == hipSuccess) break;
-        if (q != hipErrorNotReady) return hip_ok(q, "shutdown") ? SINTER_OK : SINTER_ERR_HIP;
-        if (std::chrono::steady_clock::now() > deadline) return set_error(SINTER_ERR_TIMEOUT, "shutdown watchdog");
-        std::this_thread::sleep_for(std::chrono::microseconds(100));
-    }
+    const int ws = wait_stream(h->stream, timeout_ms, "shutdown");
+    if (ws == SINTER_ERR_TIMEOUT) return set_error(SINTER_ERR_TIMEOUT, "shutdown watchdog");
+    if (ws != SINTER_OK) return ws;
     h->launched = false;
     return SINTER_OK;
 }
@@ -905,10 +912,9 @@ int sinter_host_set_grid(sinter_host *h, uint32_t blocks) {
 
 int sinter_host_set_pos(sinter_host *h, int32_t pos) {
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
-    return hip_ok(hipMemcpyAsync(&h->d_pass->pos, &pos, 4, hipMemcpyHostToDevice, h->stream), "pos write") &&
-                   hip_ok(hipStreamSynchronize(h->stream), "pos sync")
-               ? SINTER_OK
-               : SINTER_ERR_HIP;
+    // a 32-bit fill carries the value in the command itself: no host buffer
+    // to stage, no wait (the stream orders it before the next launch)
+    return hip_ok(hipMemsetD32Async(&h->d_pass->pos, pos, 1, h->stream), "pos write") ? SINTER_OK : SINTER_ERR_HIP;
 }
 
 }  // extern "C"

@@ -6,6 +6,7 @@ and nothing here falls back to a CPU path.
 """
 import ctypes as C
 import os
+import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsinter.so")
@@ -112,6 +113,21 @@ def qwen36_27b_config(n_ctx=4352, quant="q4_k_m", n_layer=64, kv="f16"):
 _lib = None
 
 
+_system_runtime = False
+
+
+def use_system_runtime():
+    """Make this process load libsinter on the system ROCm runtime (the one
+    the image's tools, rocprofv3 among them, belong to) instead of torch's
+    bundled copy.  Call it before the first lib() in a process that will not
+    import torch: once the system libamdhip64.so.7 is loaded, torch imported
+    later would bind to it and not run."""
+    global _system_runtime
+    if _lib is not None or "torch" in sys.modules:
+        raise RuntimeError("use_system_runtime() must come before lib() and before any torch import")
+    _system_runtime = True
+
+
 def lib():
     """Load libsinter.so; raise if it has not been built."""
     global _lib
@@ -123,11 +139,13 @@ def lib():
     # One HIP runtime per process: torch ships its own libamdhip64.so.7, and
     # whichever copy is loaded first satisfies the other's dependency.  torch
     # does not run on the system copy, while libsinter runs on either, so
-    # let torch (when installed) load its runtime first.
-    try:
-        import torch  # noqa: F401
-    except ImportError:
-        pass
+    # unless the process chose the system runtime (use_system_runtime), let
+    # torch (when installed) load its runtime first.
+    if not _system_runtime:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
     L = C.CDLL(LIB_PATH)
     I, U32, I64, U64 = C.c_int, C.c_uint32, C.c_int64, C.c_uint64
     sig = {
@@ -149,6 +167,7 @@ def lib():
         "sinter_op_attn_decode_noalloc": (I, [C.POINTER(AttnArgs), U32, vp]),
         "sinter_litmus_barrier": (I, [U32, U32, I, C.POINTER(C.c_uint64)]),
         "sinter_copy_calibration": (I, [I, C.c_size_t, I]),
+        "sinter_hbm_peak": (I, [C.c_uint64, U32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
         "sinter_op_error": (I, [C.POINTER(U32), C.POINTER(U32)]),
         "sinter_argmax_ws_create": (I, [U32, vp, vp, U32, C.POINTER(vp)]),
         "sinter_argmax_ws_destroy": (None, [vp]),
