@@ -127,6 +127,23 @@ def build(verbose=False):
 
 GGML_SHIM_SRC = os.path.join(HERE, "ggml_backend", "sinter_ggml.cpp")
 GGML_SHIM_LIB = os.path.join(HERE, "ggml_backend", "libsinter_ggml.so")
+GGML_RULES_SRC = os.path.join(HERE, "ggml_backend", "graph_rules.cpp")
+GGML_RULES_LIB = os.path.join(HERE, "ggml_backend", "libsinter_ggml_rules.so")
+
+
+def build_ggml_rules(verbose=False):
+    """The ggml shim's decision rules (ggml_backend/graph_rules.cpp: which
+    graph is a decode graph, what it binds to, when to rebind), built on
+    their own with g++ -- no ggml tree and no GPU needed -- so that the CPU
+    tests exercise them (tests/test_shim_rules.py)."""
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", GGML_RULES_SRC, "-o", GGML_RULES_LIB + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("ggml rules build failed:\n" + r.stdout + r.stderr)
+    os.replace(GGML_RULES_LIB + ".tmp", GGML_RULES_LIB)
+    return GGML_RULES_LIB
 
 
 def build_ggml_shim(verbose=False):
@@ -141,7 +158,7 @@ def build_ggml_shim(verbose=False):
     if not os.path.exists(os.path.join(inc, "ggml-backend-impl.h")):
         raise RuntimeError(f"SINTER_GGML_INCLUDE={inc} has no ggml-backend-impl.h")
     cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-I", inc,
-           "-I", os.path.join(os.path.dirname(HERE), "include"), GGML_SHIM_SRC, "-o", GGML_SHIM_LIB,
+           "-I", os.path.join(os.path.dirname(HERE), "include"), GGML_SHIM_SRC, GGML_RULES_SRC, "-o", GGML_SHIM_LIB,
            "-L", HERE, "-lsinter", "-Wl,-rpath," + HERE]
     if libdir:
         cmd += ["-L", libdir, "-lggml-base", "-Wl,-rpath," + libdir]
@@ -155,4 +172,5 @@ def build_ggml_shim(verbose=False):
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_ggml_rules(verbose="-v" in sys.argv))
     print(build_ggml_shim(verbose="-v" in sys.argv) or "ggml shim: skipped (SINTER_GGML_INCLUDE not set)")

@@ -20,6 +20,9 @@
 //     result_output; prefill (GDN node suffix __fgdn_ch__, or ne[2] > 1:
 //     docs/PREFILL-SEMANTICS.md:344-377), batch > 1, a KV row other than the
 //     position, or any shape the model does not match is delegated unchanged.
+// The decisions themselves (which graph is a decode graph, what it binds to,
+// when to rebind, which pass inputs run) are graph_rules.cpp's, over a
+// ggml-free description of the graph, so they are tested without ggml.
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -30,26 +33,12 @@
 #include "ggml-backend-impl.h"
 #include "ggml-backend.h"
 #include "ggml.h"
+#include "graph_rules.h"
 #include "sinter.h"
 
 namespace {
 
-// ------------------------------------------------------------------ names
-
-// A tensor's name without the scheduler's copy decoration "<backend>#<name>#<c>".
-std::string base_name(const ggml_tensor *t) {
-    std::string n = t->name;
-    const size_t a = n.find('#');
-    if (a == std::string::npos) return n;
-    const size_t b = n.rfind('#');
-    return b > a ? n.substr(a + 1, b - a - 1) : n.substr(a + 1);
-}
-
-// The tensor a view reads from (the cache tensors appear through views).
-const ggml_tensor *view_root(const ggml_tensor *t) {
-    while (t && t->view_src) t = t->view_src;
-    return t;
-}
+using namespace sinter_ggml;
 
 // ggml type -> sinter_type (the numbering is ggml's; only what the kernels read)
 int sinter_type_of(ggml_type t) {
@@ -64,172 +53,64 @@ int sinter_type_of(ggml_type t) {
     }
 }
 
-// ------------------------------------------------------------------ fingerprint
-
-// What one received graph is, as far as the decode path cares.
-struct Shape {
-    bool decode = false;              // a batch-1 decode graph of a Qwen3.6-style hybrid
-    std::string why;                  // the reason it is not (logged once per reason)
-    std::map<std::string, ggml_tensor *> named;   // every node and leaf by base name
-    int n_layer = 0, n_gdn = 0, n_attn = 0;
-    ggml_tensor *logits = nullptr, *tokens = nullptr, *embd = nullptr, *pos = nullptr;
-};
-
-Shape inspect(ggml_cgraph *g) {
-    Shape s;
-    auto note = [&](ggml_tensor *t) {
-        if (t && t->name[0]) s.named.emplace(base_name(t), t);
-    };
-    const int n = ggml_graph_n_nodes(g);
-    for (int i = 0; i < n; i++) {
-        ggml_tensor *t = ggml_graph_node(g, i);
-        note(t);
-        for (int j = 0; j < GGML_MAX_SRC; j++) note(t->src[j]);
-        if (t->op == GGML_OP_GATED_DELTA_NET) {
-            const std::string nm = t->name;
-            if (nm.find("__fgdn_ch__") != std::string::npos) { s.why = "prefill (chunked GDN node)"; return s; }
-            if (nm.find("__fgdn_ar__") == std::string::npos) { s.why = "GDN node without the decode suffix"; return s; }
-            // ne[2] of q is the token count of the ubatch
-            if (t->src[0] && t->src[0]->ne[2] != 1) { s.why = "GDN over more than one token"; return s; }
-            s.n_gdn++;
-        } else if (t->op == GGML_OP_FLASH_ATTN_EXT) {
-            if (t->src[0] && t->src[0]->ne[1] != 1) { s.why = "attention over more than one query"; return s; }
-            s.n_attn++;
-        }
+int32_t op_of(ggml_op op) {
+    switch (op) {
+    case GGML_OP_RMS_NORM: return G_RMS_NORM;
+    case GGML_OP_ROPE: return G_ROPE;
+    case GGML_OP_GATED_DELTA_NET: return G_GDN;
+    case GGML_OP_FLASH_ATTN_EXT: return G_FATTN;
+    default: return G_OTHER;
     }
-    s.logits = s.named.count("result_output") ? s.named["result_output"] : nullptr;
-    s.tokens = s.named.count("inp_tokens") ? s.named["inp_tokens"] : nullptr;
-    s.embd = s.named.count("inp_embd") ? s.named["inp_embd"] : nullptr;
-    s.pos = s.named.count("inp_pos") ? s.named["inp_pos"] : nullptr;
-    s.n_layer = s.n_gdn + s.n_attn;
-    if (!s.logits || s.logits->ne[1] != 1) { s.why = "no single-row result_output"; return s; }
-    if (!s.pos || ggml_nelements(s.pos) != 1) { s.why = "no single position"; return s; }
-    if (!s.tokens && !s.embd) { s.why = "neither token ids nor an embedded row as input"; return s; }
-    if (s.n_gdn == 0 || s.n_attn == 0) { s.why = "not the hybrid decode graph"; return s; }
-    s.decode = true;
-    return s;
 }
 
-// ------------------------------------------------------------------ binding
-
-// Per-layer weight names in the slot numbering of sinter_model_tensor_info
-// (the same table as schedule.py's packer).
-const char *const kCommon[5] = {"attn_norm.weight", "post_attention_norm.weight", "ffn_gate.weight",
-                                "ffn_up.weight", "ffn_down.weight"};
-const char *const kGdn[9] = {"attn_qkv.weight", "attn_gate.weight", "ssm_alpha.weight", "ssm_beta.weight",
-                             "ssm_out.weight", "ssm_conv1d.weight", "ssm_dt.bias", "ssm_a", "ssm_norm.weight"};
-const char *const kAttn[6] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
-                              "attn_q_norm.weight", "attn_k_norm.weight"};
-
-struct Bound {
-    sinter_model *m = nullptr;
-    std::vector<void *> tensors, states;
-    std::vector<int32_t> types;
-    const void *key_logits = nullptr;   // the graph instance the model was bound to
-    bool embed_outside = false;
-    float *x = nullptr;                 // the model's X buffer (embed_outside)
+// The ggml-free description of a received graph (graph_rules.h): every node,
+// its operands and the tensors views read from.
+struct Described {
+    GraphDesc g;
+    std::map<const ggml_tensor *, int32_t> index;
+    std::vector<const ggml_tensor *> ptr;
 };
 
-// Resolve the decode graph's tensors into bindings and a config; false (with
-// the reason) when anything the model needs is missing or mis-shaped.
-bool bind_graph(const Shape &s, ggml_backend_t stock, sinter_model_config &c, Bound &b, std::string &why) {
-    auto get = [&](const std::string &n) -> ggml_tensor * {
-        auto it = s.named.find(n);
-        return it == s.named.end() ? nullptr : it->second;
-    };
-    ggml_tensor *embd_w = get("token_embd.weight"), *out_w = get("output.weight"), *onorm = get("output_norm.weight");
-    if (!onorm) { why = "no output_norm.weight"; return false; }
-    if (!out_w) out_w = embd_w;                    // tied head
-    if (!out_w) { why = "no head weight"; return false; }
-    std::memset(&c, 0, sizeof c);
-    c.n_layer = s.n_layer;
-    c.n_embd = (int32_t)out_w->ne[0];
-    c.n_vocab = (int32_t)out_w->ne[1];
-    // scalars no weight carries, from the ops that use them: the RMS-norm
-    // epsilon (op_params[0]), the rope's rotated dims ([1]) and base ([5])
-    c.eps = 1e-6f;
-    c.rope_base = 1e7f;
-    c.rope_dims = 64;
-    for (const auto &kv : s.named) {
-        const ggml_tensor *t = kv.second;
-        if (t->op == GGML_OP_RMS_NORM) std::memcpy(&c.eps, t->op_params, sizeof(float));
-        if (t->op == GGML_OP_ROPE) {
-            c.rope_dims = t->op_params[1];
-            std::memcpy(&c.rope_base, t->op_params + 5, sizeof(float));
-        }
-    }
-    c.t_kv = SINTER_F16;
-    int first_attn = -1;
-    for (int il = 0; il < c.n_layer && first_attn < 0; il++)
-        if (get("blk." + std::to_string(il) + ".attn_q.weight")) first_attn = il;
-    if (first_attn < 0) { why = "no attention layer"; return false; }
-    c.attn_every = first_attn + 1;
-    const std::string l0 = "blk." + std::to_string(first_attn) + ".";
-    ggml_tensor *wq = get(l0 + "attn_q.weight"), *wk = get(l0 + "attn_k.weight"), *qn = get(l0 + "attn_q_norm.weight");
-    ggml_tensor *up = get("blk.0.ffn_up.weight"), *qkv = get("blk.0.attn_qkv.weight"), *sa = get("blk.0.ssm_a");
-    ggml_tensor *sn = get("blk.0.ssm_norm.weight");
-    if (!wq || !wk || !qn || !up || !qkv || !sa || !sn) { why = "layer 0 / first attention layer incomplete"; return false; }
-    ggml_tensor *cw = get("blk.0.ssm_conv1d.weight");
-    if (!cw) { why = "no ssm_conv1d.weight"; return false; }
-    c.conv_k = (int32_t)cw->ne[0];
-    c.head_dim = (int32_t)qn->ne[0];
-    c.attn_nq = (int32_t)(wq->ne[1] / (2 * c.head_dim));
-    c.attn_nkv = (int32_t)(wk->ne[1] / c.head_dim);
-    c.n_ff = (int32_t)up->ne[1];
-    c.gdn_d = (int32_t)sn->ne[0];
-    c.gdn_hv = (int32_t)ggml_nelements(sa);
-    c.gdn_hk = (int32_t)((qkv->ne[1] / c.gdn_d - c.gdn_hv) / 2);
-    // the KV cache tensors (views of cache_k_l<il> / cache_v_l<il>)
-    ggml_tensor *kc0 = get("cache_k_l" + std::to_string(first_attn));
-    if (!kc0) { why = "no KV cache tensor"; return false; }
-    const ggml_tensor *kr = view_root(kc0);
-    c.n_ctx = (int32_t)(ggml_nelements(kr) / ((int64_t)c.attn_nkv * c.head_dim));
-    if (kr->type == GGML_TYPE_Q8_0) c.t_kv = SINTER_Q8_0;
-    else if (kr->type != GGML_TYPE_F16) { why = "KV cache neither f16 nor q8_0"; return false; }
-    c.t_default = sinter_type_of(qkv->type);
-    c.t_attn_v = c.t_ffn_down = c.t_output = c.t_embd = c.t_default;
+int32_t add(Described &d, const ggml_tensor *t) {
+    if (!t) return -1;
+    auto it = d.index.find(t);
+    if (it != d.index.end()) return it->second;
+    const int32_t i = (int32_t)d.g.t.size();
+    d.index.emplace(t, i);
+    d.g.t.emplace_back();
+    d.ptr.push_back(t);
+    const int32_t root = add(d, t->view_src), src0 = add(d, t->src[0]);
+    GTensor &g = d.g.t[(size_t)i];   // (after the recursive adds: the vector may have grown)
+    g.name = t->name;
+    g.op = op_of(t->op);
+    g.type = sinter_type_of(t->type);
+    for (int k = 0; k < 4; k++) g.ne[k] = t->ne[k];
+    g.data = t->data;
+    g.root = root;
+    g.src0 = src0;
+    std::memcpy(g.op_params, t->op_params, sizeof g.op_params);
+    return i;
+}
 
-    const size_t nt = (size_t)c.n_layer * 16 + 3;
-    b.tensors.assign(nt, nullptr);
-    b.types.assign(nt, SINTER_F32);
-    b.states.assign((size_t)c.n_layer * 2, nullptr);
-    auto put = [&](size_t i, ggml_tensor *t) -> bool {
-        if (!t) return false;
-        const int st = sinter_type_of(t->type);
-        if (st < 0) return false;
-        b.tensors[i] = t->data;
-        b.types[i] = st;
-        return true;
-    };
-    for (int il = 0; il < c.n_layer; il++) {
-        const std::string p = "blk." + std::to_string(il) + ".";
-        const bool at = il % c.attn_every == c.attn_every - 1;
-        for (int k = 0; k < 5; k++)
-            if (!put((size_t)il * 16 + k, get(p + kCommon[k]))) { why = p + kCommon[k]; return false; }
-        const int nk = at ? 6 : 9;
-        for (int k = 0; k < nk; k++) {
-            const char *nm = at ? kAttn[k] : kGdn[k];
-            if (!put((size_t)il * 16 + 5 + k, get(p + nm))) { why = p + nm; return false; }
-        }
-        const std::string sfx = std::to_string(il);
-        ggml_tensor *s0 = get((at ? "cache_k_l" : "cache_r_l") + sfx), *s1 = get((at ? "cache_v_l" : "cache_s_l") + sfx);
-        if (!s0 || !s1) { why = "state of layer " + sfx; return false; }
-        b.states[(size_t)il * 2] = view_root(s0)->data;
-        b.states[(size_t)il * 2 + 1] = view_root(s1)->data;
+Described describe(ggml_cgraph *graph) {
+    Described d;
+    const int n = ggml_graph_n_nodes(graph);
+    for (int i = 0; i < n; i++) {
+        ggml_tensor *t = ggml_graph_node(graph, i);
+        add(d, t);
+        for (int j = 0; j < GGML_MAX_SRC; j++) add(d, t->src[j]);
     }
-    b.embed_outside = s.tokens == nullptr;
-    const size_t g0 = (size_t)c.n_layer * 16;
-    if (!b.embed_outside && !put(g0, embd_w)) { why = "token_embd.weight not on the GPU"; return false; }
-    if (!put(g0 + 1, onorm) || !put(g0 + 2, out_w)) { why = "head tensors"; return false; }
-    (void)stock;
-    return true;
+    return d;
 }
 
 // ------------------------------------------------------------------ backend
 
 struct Ctx {
     ggml_backend_t stock = nullptr;    // the HIP backend every miss goes to
-    Bound bound;
+    sinter_model *m = nullptr;         // bound to `bound`
+    Binding bound;
+    std::vector<void *> tensors, states;   // sinter_model_bindings' arrays of `bound`
+    float *x = nullptr;                // the model's X buffer (embed_outside)
     std::map<std::string, int> misses; // reasons already logged
 };
 
@@ -237,7 +118,7 @@ const char *be_name(ggml_backend_t) { return "SINTER"; }
 
 void be_free(ggml_backend_t be) {
     Ctx *c = static_cast<Ctx *>(be->context);
-    if (c->bound.m) sinter_model_destroy(c->bound.m);
+    if (c->m) sinter_model_destroy(c->m);
     if (c->stock) ggml_backend_free(c->stock);
     delete c;
     delete be;
@@ -250,54 +131,71 @@ enum ggml_status delegate(Ctx *c, ggml_cgraph *g, const std::string &why) {
     return ggml_backend_graph_compute(c->stock, g);
 }
 
+// (Re)build the bound model over `now` -- whenever any bound pointer or type
+// differs from the model's, not only the logits buffer.
+bool rebind(Ctx *c, const Binding &now, std::string &why) {
+    if (c->m) sinter_model_destroy(c->m);
+    c->m = nullptr;
+    c->x = nullptr;
+    c->bound = now;
+    c->tensors.assign(now.tensors.size(), nullptr);
+    c->states.assign(now.states.size(), nullptr);
+    for (size_t i = 0; i < now.tensors.size(); i++) c->tensors[i] = const_cast<void *>(now.tensors[i]);
+    for (size_t i = 0; i < now.states.size(); i++) c->states[i] = const_cast<void *>(now.states[i]);
+    sinter_model_bindings mb;
+    std::memset(&mb, 0, sizeof mb);
+    mb.tensors = c->tensors.data();
+    mb.types = c->bound.types.data();
+    mb.states = c->states.data();
+    mb.logits = static_cast<float *>(const_cast<void *>(now.logits));
+    mb.embed_outside = now.embed_outside ? 1u : 0u;
+    if (sinter_model_create_bound(&c->bound.cfg, 0, 0, &mb, &c->m) != SINTER_OK) {
+        why = std::string("bound model refused: ") + sinter_last_error();
+        c->m = nullptr;
+        return false;
+    }
+    if (now.embed_outside) {
+        void *x = nullptr;
+        size_t xb = 0;
+        if (sinter_model_buffer(c->m, "X", &x, &xb) != SINTER_OK) { why = "no X buffer"; return false; }
+        c->x = static_cast<float *>(x);
+    }
+    return true;
+}
+
 enum ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
     Ctx *c = static_cast<Ctx *>(be->context);
-    Shape s = inspect(g);
-    if (!s.decode) return delegate(c, g, s.why);
-    Bound &b = c->bound;
-    // (re)bind when the graph's buffers are not the ones the model holds
-    if (!b.m || b.key_logits != s.logits->data) {
-        if (b.m) sinter_model_destroy(b.m);
-        b = Bound();
-        sinter_model_config cfg;
-        std::string why;
-        if (!bind_graph(s, c->stock, cfg, b, why)) return delegate(c, g, "unbindable decode graph: " + why);
-        sinter_model_bindings mb;
-        std::memset(&mb, 0, sizeof mb);
-        mb.tensors = b.tensors.data();
-        mb.types = b.types.data();
-        mb.states = b.states.data();
-        mb.logits = static_cast<float *>(s.logits->data);
-        mb.embed_outside = b.embed_outside ? 1u : 0u;
-        if (sinter_model_create_bound(&cfg, 0, 0, &mb, &b.m) != SINTER_OK)
-            return delegate(c, g, std::string("bound model refused: ") + sinter_last_error());
-        b.key_logits = s.logits->data;
-        if (b.embed_outside) {
-            void *x = nullptr;
-            size_t xb = 0;
-            if (sinter_model_buffer(b.m, "X", &x, &xb) != SINTER_OK) return delegate(c, g, "no X buffer");
-            b.x = static_cast<float *>(x);
-        }
+    const Described d = describe(g);
+    const Classified cl = classify(d.g);
+    if (!cl.decode) return delegate(c, g, cl.why);
+    Binding now;
+    std::string why;
+    if (!bind(d.g, cl, now, why)) return delegate(c, g, "unbindable decode graph: " + why);
+    // this pass's inputs: position (1 or 4 M-RoPE ids), the KV row the graph
+    // writes, the token (or the embedded row)
+    const ggml_tensor *pt = d.ptr[(size_t)cl.pos];
+    int32_t ids[4] = {0, 0, 0, 0}, pos = 0, tok = 0;
+    const int n_ids = (int)ggml_nelements(pt);
+    ggml_backend_tensor_get(const_cast<ggml_tensor *>(pt), ids, 0, (size_t)n_ids * sizeof(int32_t));
+    int64_t row = -1;
+    const bool have_row = cl.k_idxs >= 0;
+    if (have_row) {
+        const ggml_tensor *ki = d.ptr[(size_t)cl.k_idxs];
+        if (ki->type != GGML_TYPE_I64) return delegate(c, g, "k_idxs not i64");
+        ggml_backend_tensor_get(const_cast<ggml_tensor *>(ki), &row, 0, sizeof row);
     }
-    // this pass's inputs: position, token (or the embedded row)
-    int32_t pos = 0, tok = 0;
-    ggml_backend_tensor_get(s.pos, &pos, 0, sizeof pos);
-    if (s.tokens) ggml_backend_tensor_get(s.tokens, &tok, 0, sizeof tok);
-    if (b.embed_outside) {
+    if (!pass_inputs(ids, n_ids, have_row, row, pos, why)) return delegate(c, g, why);
+    if (!c->m || !same_binding(c->bound, now))
+        if (!rebind(c, now, why)) return delegate(c, g, why);
+    if (cl.tokens >= 0) ggml_backend_tensor_get(const_cast<ggml_tensor *>(d.ptr[(size_t)cl.tokens]), &tok, 0, sizeof tok);
+    if (now.embed_outside) {
         // the embedded row, device to device into the model's X
-        const size_t bytes = (size_t)ggml_nelements(s.embd) * sizeof(float);
-        if (s.embd->type != GGML_TYPE_F32 || sinter_model_copy(b.m, b.x, s.embd->data, bytes, 2) != SINTER_OK)
+        const ggml_tensor *e = d.ptr[(size_t)cl.embd];
+        const size_t bytes = (size_t)ggml_nelements(e) * sizeof(float);
+        if (e->type != GGML_TYPE_F32 || sinter_model_copy(c->m, c->x, e->data, bytes, 2) != SINTER_OK)
             return delegate(c, g, "embedded row copy failed");
     }
-    // the KV row the stock graph would write must be the position (one
-    // sequence, no holes): the kernel attends over rows [0, pos]
-    if (s.named.count("k_idxs")) {
-        int64_t row = -1;
-        ggml_tensor *ki = s.named["k_idxs"];
-        if (ki->type == GGML_TYPE_I64) ggml_backend_tensor_get(ki, &row, 0, sizeof row);
-        if (row != pos) return delegate(c, g, "KV row is not the position");
-    }
-    if (sinter_model_decode(b.m, tok, pos, nullptr, nullptr) != SINTER_OK) {
+    if (sinter_model_decode(c->m, tok, pos, nullptr, nullptr) != SINTER_OK) {
         std::fprintf(stderr, "sinter: decode pass failed: %s\n", sinter_last_error());
         return GGML_STATUS_FAILED;
     }
