@@ -331,6 +331,22 @@ def ubatch_bench(args):
         us = ev[0].elapsed_time(ev[1]) / args.steps * 1e3
         per.append({"matrix": name, "type": "Q4_K" if t == 12 else "Q6_K", "rows": r, "k": k, "us": round(us, 2),
                     "tops": round(2.0 * r * k * T / (us * 1e-6) / 1e12, 1)})
+    # spot check: ssm_out's outputs of token 0 against the oracle's GEMV over
+    # the same quantised activation
+    check = None
+    try:
+        import oracle
+        j = 4
+        _, t, r, k = UBATCH_MATS[j]
+        launch(0, j)
+        torch.cuda.synchronize()
+        wh = copies[0][j].cpu().numpy()
+        xh = xq[k].cpu().numpy()[:sinter.row_bytes(sinter.Q8_K, k)]
+        ref = np.zeros(r, np.float32)
+        oracle.lib().or_gemv_q(t, oracle.P(wh), r, k, oracle.P(xh), oracle.P(ref))
+        check = {"matrix": UBATCH_MATS[j][0], "token": 0, "bit_exact": bool(np.array_equal(ys[j].cpu().numpy()[:r], ref))}
+    except ImportError:
+        pass
     macs = sum(r * k for _, _, r, k in UBATCH_MATS)
     tops = 2.0 * macs * T / (ms * 1e-3) / 1e12
     line = {
@@ -342,7 +358,7 @@ def ubatch_bench(args):
         "data": "synthetic (seeded random-init Q4_K / Q6_K weights, seeded Q8_K activations)",
         "config": {"workload": f"ubatch of {T} tokens x one GDN layer's trunk (Qwen3.6-27B shapes, Q4_K_M mix)",
                    "ubatch": T, "weight_bytes_per_step": layer_bytes, "weight_copies_rotated": n_copy,
-                   "per_matrix": per},
+                   "per_matrix": per, "oracle_spot_check": check},
         "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": MFMA_INT8_PEAK_TOPS, "unit": "TOP/s",
                      "frac": round(tops / MFMA_INT8_PEAK_TOPS, 4), "traffic": None,
                      "kernel": "ubatch_gemv_kernel",

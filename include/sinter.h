@@ -341,8 +341,10 @@ int sinter_conv_silu_ubatch(const float *x, float *state, const float *conv_w, f
                             uint32_t dconv, uint32_t n_tokens, void *stream);
 /* The attention op without caller workspace, allocating nothing: no
  * counterpart in the reference; for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid allocation).  As sinter_op_attn_decode, except that a->part and
+ * memory (tight serving loops, harnesses that forbid allocation; it launches
+ * cooperatively and takes the array's address on its first call per device,
+ * so it is not offered for HIP graph capture).  As sinter_op_attn_decode,
+ * except that a->part and
  * a->count must be NULL: the split-K partials (at most 2 MiB,
  * sinter_attn_part_len(...) * 4 bytes) and the generation flags (at most
  * 1024, sinter_attn_count_len(...)) live in a fixed device array the library

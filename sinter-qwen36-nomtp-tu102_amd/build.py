@@ -7,9 +7,11 @@ exactly as written, matching the CPU oracle) and no packed-fp32 instructions.
 
 Resource gate: the compiler's kernel-resource-usage remarks are parsed for
 every kernel.  The build fails if any kernel uses scratch (private memory:
-register spills to memory or stack arrays), has a dynamic stack, or if a
+register spills to memory or stack arrays), has a dynamic stack, if a
 persistent-grid kernel cannot keep one 256-thread workgroup per CU (LDS over
-160 KiB or occupancy below one wave per SIMD).  The figures are written to
+160 KiB or occupancy below one wave per SIMD), or if a persistent kernel
+spills more registers (VGPRs into AGPRs, SGPRs into VGPR lanes) than its
+committed budget (SPILL_BUDGET).  The figures are written to
 resource_usage.txt beside the library.
 """
 import os
@@ -37,6 +39,19 @@ FLAGS = [
 # kernels that run as one resident workgroup per CU (cooperative grids)
 PERSISTENT = {"sinter_interp", "sinter_interp_kquant", "sinter_interp_kquant_q8kv", "sinter_interp_bf16", "sinter_op_kernel", "sinter_op_noalloc_kernel", "sinter_litmus_kernel"}
 LDS_LIMIT = 160 * 1024
+# Register budget of the persistent kernels: the most VGPRs spilled into
+# AGPRs and SGPRs spilled into VGPR lanes the build accepts (the figures of
+# the committed build; a change that spills more fails until it is measured
+# and the budget raised on purpose).  Spills to memory (scratch) are never
+# accepted.
+SPILL_BUDGET = {
+    "sinter_interp": (20, 593),
+    "sinter_interp_kquant": (12, 406),
+    "sinter_interp_kquant_q8kv": (18, 405),
+    "sinter_interp_bf16": (12, 455),
+    "sinter_op_kernel": (0, 211),
+    "sinter_op_noalloc_kernel": (0, 171),
+}
 
 _FIELDS = {
     "TotalSGPRs": "sgprs", "VGPRs": "vgprs", "AGPRs": "agprs",
@@ -87,6 +102,13 @@ def gate(kernels):
     for name in PERSISTENT:
         if kernels and name not in kernels:
             bad.append(f"{name}: no resource remarks")
+    for name, (vmax, smax) in SPILL_BUDGET.items():
+        k = kernels.get(name)
+        if k is None:
+            continue
+        if k.get("vgpr_spill", 0) > vmax or k.get("sgpr_spill", 0) > smax:
+            bad.append(f"{name}: {k.get('vgpr_spill')} VGPR / {k.get('sgpr_spill')} SGPR spills over the budget "
+                       f"({vmax} / {smax})")
     return bad
 
 

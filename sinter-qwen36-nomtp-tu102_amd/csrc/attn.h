@@ -650,9 +650,17 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
         constexpr uint32_t NM = decltype(nmax)::value;
         for (uint32_t eb = e0; eb < e1; eb += BLOCK_THREADS) {
             const uint32_t el = eb + t, elc = min(el, e1 - 1), s = elc / HD, d = elc % HD;
+            // chunk k's value at off + k * stride: the offset advances in a
+            // vector register (no per-chunk scalar), and loads past chunk NC - 1
+            // fall outside the buffer resource, which returns 0
             float v[NM];
+            const uint32_t stride = gqa * PS * 4;
+            uint32_t off = (s * PS + d) * 4;
 #pragma unroll
-            for (uint32_t k = 0; k < NM; k++) v[k] = ld_coh4b(r, ((min(k, NC - 1) * gqa + s) * PS + d) * 4);
+            for (uint32_t k = 0; k < NM; k++) {
+                v[k] = ld_coh4b(r, off);
+                off += stride;
+            }
             const uint32_t h = g * gqa + s;
             const float gate = ld_coh(a.qg + (size_t)h * 2 * HD + HD + d);
             if (eb == e0) {
@@ -683,9 +691,7 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
             if (el < e1) st_coh(a.out + (size_t)h * HD + d, (O / mL[s]) * dev_sigmoid(gate));
         }
     };
-    if (NC <= 16) merge(std::integral_constant<uint32_t, 16>{});
-    else if (NC <= 32) merge(std::integral_constant<uint32_t, 32>{});
-    else merge(std::integral_constant<uint32_t, 64>{});
+    merge(std::integral_constant<uint32_t, 64>{});   // (loads past NC re-read chunk NC - 1: cache hits)
     settle_vmem();
 }
 

@@ -172,14 +172,27 @@ struct sinter_gguf {
             for (int d = 0; d < 4; d++) ti.ne[d] = 1;
             for (uint32_t d = 0; d < ti.n_dims; d++)
                 if (!rd(ti.ne[d])) return false;
+            // as ggml's reader: every dimension at least 1 and at most INT64_MAX
+            for (int d = 0; d < 4; d++)
+                if (ti.ne[d] == 0 || ti.ne[d] > (uint64_t)INT64_MAX) {
+                    err = "tensor " + names[t] + ": dimension " + std::to_string(d) + " is 0 or exceeds INT64_MAX";
+                    return false;
+                }
             if (!rd(ti.type) || !rd(ti.offset)) return false;
             const TypeSize ts = type_size(ti.type);
             if (!ts.elems) { err = "tensor " + names[t] + ": unknown type id " + std::to_string(ti.type); return false; }
             if (ti.ne[0] % ts.elems) { err = "tensor " + names[t] + ": row not a whole number of blocks"; return false; }
-            // nbytes = ne0/elems*bytes * ne1*ne2*ne3, refusing overflow
+            // nbytes = ne0/elems*bytes * ne1*ne2*ne3, refused as soon as a
+            // partial product exceeds the file (each factor is below 2^63, so
+            // a partial product of at most the file size times one factor
+            // fits the 128-bit accumulator and cannot wrap)
             unsigned __int128 nb = (unsigned __int128)(ti.ne[0] / ts.elems) * ts.bytes;
-            for (int d = 1; d < 4; d++) nb *= ti.ne[d];
-            if (nb > size) { err = "tensor " + names[t] + ": larger than the file"; return false; }
+            bool fits = nb <= size;
+            for (int d = 1; d < 4 && fits; d++) {
+                nb *= ti.ne[d];
+                fits = nb <= size;
+            }
+            if (!fits) { err = "tensor " + names[t] + ": larger than the file"; return false; }
             ti.nbytes = (uint64_t)nb;
             if (by_name.count(names[t])) { err = "duplicate tensor name " + names[t]; return false; }
             by_name[names[t]] = t;

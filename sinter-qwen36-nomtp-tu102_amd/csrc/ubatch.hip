@@ -442,27 +442,38 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict_
 }
 
 // RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
-// single-token GEMV's SINTER_PRO_RMSNORM prologue and of the oracle's
-// or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded to fp32,
-// scale = 1 / sqrtf(mean + eps), y = (x * scale) * w).  The fp64 sum is a
-// fixed tree: each thread's float4 groups in order, then the wave (xor
-// shuffles), then the four waves in order.  Then wave v quantises blocks
-// v, v + 4, ... of the normalised row.
+// single-token GEMV's SINTER_PRO_RMSNORM prologue (gemv.h) and of the
+// oracle's or_rmsnorm (ggml: fp32 squares summed in fp64, the mean rounded
+// to fp32, scale = 1 / sqrtf(mean + eps), y = (x * scale) * w).  The fp64 sum
+// is the prologue's tree exactly, so prefill and decode normalise a row to
+// the same bits: row g = t / 16 (16 lanes) owns the 256-element chunks g,
+// g + 16, ..., lane r = t % 16 elements 16r..16r+15 of each; the lane keeps
+// four partial sums (element i into sum i / 4) over its chunks g + 32,
+// g + 48, ... and then g and g + 16; the row adds them as
+// (s0 + s1) + (s2 + s3) and by its DPP butterfly, the wave its four rows in
+// order, the workgroup its four waves in order.  Then wave v quantises
+// blocks v, v + 4, ... of the normalised row.
+__device__ __forceinline__ void ub_add_sq(const float *xr, uint32_t c, uint32_t r, double s4[4]) {
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float4 v = ((const float4 *)(xr + 256u * c + 16u * r))[q];
+        s4[q] += (double)(v.x * v.x);
+        s4[q] += (double)(v.y * v.y);
+        s4[q] += (double)(v.z * v.z);
+        s4[q] += (double)(v.w * v.w);
+    }
+}
 __global__ __launch_bounds__(256) void rmsnorm_quant_q8k_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                                float eps, uint32_t k, uint8_t *__restrict__ xq) {
     __shared__ double red[4];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6, r = tid & 15u, g = tid >> 4, nchunk = k / 256u;
     const float *xr = x + (size_t)blockIdx.x * k;
-    double s = 0.0;
-    for (uint32_t j = tid; j < k / 4u; j += 256u) {
-        const float4 v = ((const float4 *)xr)[j];
-        s += (double)(v.x * v.x);
-        s += (double)(v.y * v.y);
-        s += (double)(v.z * v.z);
-        s += (double)(v.w * v.w);
-    }
-#pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+    double s4[4] = {0.0, 0.0, 0.0, 0.0};
+    for (uint32_t c = g + 32u; c < nchunk; c += 16u) ub_add_sq(xr, c, r, s4);
+    if (g < nchunk) ub_add_sq(xr, g, r, s4);
+    if (g + 16u < nchunk) ub_add_sq(xr, g + 16u, r, s4);
+    double s = row16_sum_f64((s4[0] + s4[1]) + (s4[2] + s4[3]));
+    s = ((readlane_f64(s, 0) + readlane_f64(s, 16)) + readlane_f64(s, 32)) + readlane_f64(s, 48);
     if (lane == 0) red[wv] = s;
     __syncthreads();
     s = ((red[0] + red[1]) + red[2]) + red[3];

@@ -197,3 +197,36 @@ def test_cfg1_q8_0_synth_matches_config(sn, orc):
     q = blk[:, 2:].view(np.int8).astype(np.int64)
     assert d.min() >= 0 and abs(d.mean() - 0.02 * np.sqrt(2 / np.pi)) < 0.002
     assert q.min() == -127 and q.max() == 127 and abs(q.mean()) < 0.5
+
+
+def test_build_gate_enforces_the_spill_budget():
+    """The resource gate fails a build whose persistent kernel spills more
+    registers than its committed budget, or uses scratch; the committed
+    build's own figures pass."""
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd"))
+    import build
+    base = {n: {"vgpr_spill": v, "sgpr_spill": s_, "scratch": 0, "lds": 1024, "occupancy": 1}
+            for n, (v, s_) in build.SPILL_BUDGET.items()}
+    for n in build.PERSISTENT:
+        base.setdefault(n, {"vgpr_spill": 0, "sgpr_spill": 0, "scratch": 0, "lds": 1024, "occupancy": 1})
+    assert build.gate(base) == []
+    over = {n: dict(k) for n, k in base.items()}
+    over["sinter_interp_kquant"]["sgpr_spill"] += 1
+    assert any("over the budget" in b for b in build.gate(over))
+    scratch = {n: dict(k) for n, k in base.items()}
+    scratch["sinter_interp_bf16"]["scratch"] = 16
+    assert any("scratch" in b for b in build.gate(scratch))
+    # the committed build's report is within the budget
+    rep = os.path.join(ROOT, "sinter-qwen36-nomtp-tu102_amd", "resource_usage.txt")
+    if os.path.exists(rep):
+        lines = open(rep).read().split("\n")
+        cols = lines[0].split()[1:]
+        figs = {}
+        for ln in lines[1:]:
+            if ln.strip():
+                f = ln.split()
+                figs[f[0]] = {c: int(v) if v.lstrip("-").isdigit() else v for c, v in zip(cols, f[1:])}
+        for n, (vmax, smax) in build.SPILL_BUDGET.items():
+            if n in figs:
+                assert figs[n]["vgpr_spill"] <= vmax and figs[n]["sgpr_spill"] <= smax, n

@@ -153,6 +153,13 @@ def test_malformed_files_are_refused(sn, tmp_path):
     w.add_tensor("a", [8], 0, np.zeros(8, np.float32))
     w.add_tensor("a", [8], 0, np.zeros(8, np.float32))
     assert "duplicate" in _expect_refused(sn, _write(tmp_path, "dup.gguf", w), "duplicate")
+    # dimensions whose byte count wraps 128 bits (2^62 * 2^62 * 4 * 4 B = 2^128),
+    # a zero dimension, and one past INT64_MAX
+    for ne, what in (([1 << 62, 1 << 62, 4], "larger than the file"), ([8, 0], "is 0"),
+                     ([8, (1 << 63) + 8], "INT64_MAX")):
+        w = Writer()
+        w.add_tensor("a", ne, 0, np.zeros(8, np.float32))
+        assert what in _expect_refused(sn, _write(tmp_path, "dims.gguf", w), str(ne))
     assert sn.lib().sinter_gguf_open(str(tmp_path / "missing.gguf").encode(), C.byref(C.c_void_p())) == sn.ERR_ARG
 
 

@@ -67,6 +67,22 @@ def test_gemv_ubatch_matches_per_token_gemv(sn, orc, torch_gpu, t, rows, k, n_to
         assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x)), j
 
 
+@pytest.mark.parametrize("t,rows,k,n_tok", [
+    (Q4_K, 16384, 512, 100),    # 256 row tiles: four token tiles per workgroup, the last group three
+    (Q4_K, 8192, 512, 64),      # 128 row tiles: two token tiles per workgroup
+    (Q6_K, 16384, 512, 100),
+    (Q6_K, 8192, 768, 40)])     # two token tiles per workgroup, the last group one
+def test_gemv_ubatch_multi_tile_workgroups(sn, orc, torch_gpu, t, rows, k, n_tok):
+    """Shapes with enough row tiles that a workgroup takes several 16-token
+    tiles (its waves staging tiles 1-3, a partial last token group): the
+    production shapes of a batched prefill run this path."""
+    w = synth_w(sn, t, rows, k, 700 + t + k + rows)
+    xs = activations(k, n_tok, 2000 + rows)
+    got = run_ubatch(sn, orc, torch_gpu, t, w, rows, k, xs)
+    for j, x in enumerate(xs):
+        assert np.array_equal(got[j], orc.gemv(t, w, rows, k, x)), j
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
 def test_gemv_ubatch_random_block_bytes(sn, orc, torch_gpu, t):
     rows, k, n_tok = 80, 2304, 23           # 9 blocks per row
@@ -154,6 +170,40 @@ def test_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, k, n_tok, w
     got = host(dq).reshape(n_tok, -1)
     for t in range(n_tok):
         assert np.array_equal(got[t], orc.quantize(Q4_K, orc.rmsnorm(x[t], w, eps))), t
+
+
+@pytest.mark.parametrize("k", [5120, 17408])
+def test_rmsnorm_ubatch_equals_single_token_prologue_wide_range(sn, orc, torch_gpu, k):
+    """RMSNorm + Q8_K over a ubatch then the batched GEMV gives, token by
+    token, the single-token GEMV with the RMSNORM prologue bit for bit, also
+    on rows whose values span 1e-6 .. 1e3 (where an fp64 sum of squares in
+    another order can round differently): both sum in the same fixed tree."""
+    from test_gpu_ops import run_gemv
+    torch = torch_gpu
+    rows, T, eps = 700, 6, 1e-6
+    rng = np.random.default_rng(k + 3)
+    x = rng.standard_normal((T, k)).astype(np.float32)
+    x *= (10.0 ** rng.uniform(-6, 3, (T, k))).astype(np.float32)     # nine decades in one row
+    wn = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    w = synth_w(sn, Q4_K, rows, k, 909 + k)
+    dx, dwn, dw = dev(torch, x.reshape(-1)), dev(torch, wn), dev(torch, w)
+    dq = torch.zeros(T * sn.row_bytes(sn.Q8_K, k), dtype=torch.uint8, device="cuda")
+    dy = empty_f32(torch, T * rows)
+    s = C.c_void_p(stream(torch))
+    print(f"rmsnorm ubatch vs prologue k={k} tokens={T}", flush=True)
+    sn.check(sn.lib().sinter_rmsnorm_quant_q8k_ubatch(C.c_void_p(dx.data_ptr()), C.c_void_p(dwn.data_ptr()), eps, k, T,
+                                                      C.c_void_p(dq.data_ptr()), s), "rmsnorm_quant")
+    sn.check(sn.lib().sinter_op_gemv_ubatch(Q4_K, C.c_void_p(dw.data_ptr()), rows, k, C.c_void_p(dq.data_ptr()), T,
+                                            C.c_void_p(dy.data_ptr()), 0, s), "gemv_ubatch")
+    torch.cuda.synchronize()
+    got = host(dy).reshape(T, rows)
+    for t in range(T):
+        dxt, dyt = dev(torch, x[t]), empty_f32(torch, rows)
+        a = sn.GemvArgs(K=k, pro=sn.PRO_RMSNORM, n_seg=1, eps=eps)
+        a.x, a.norm_w = dxt.data_ptr(), dwn.data_ptr()
+        a.seg[0] = sn.GemvSeg(w=dw.data_ptr(), y=dyt.data_ptr(), rows=rows, type=Q4_K, epi=sn.EPI_STORE)
+        run_gemv(sn, torch, a, 256)
+        assert np.array_equal(got[t], host(dyt)), t
 
 
 def test_batched_ffn_block_matches_oracle(sn, orc, torch_gpu):
