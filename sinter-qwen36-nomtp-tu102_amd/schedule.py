@@ -463,7 +463,10 @@ def pack(model, prog):
             for f in ("qg", "k", "v", "q_norm", "k_norm", "kc", "vc", "part", "count", "out", "pass_cell"):
                 setattr(a, f, ptr(ins[f]))
             a.nq, a.nkv, a.hd, a.rope_dims, a.n_ctx = cfg.attn_nq, cfg.attn_nkv, cfg.head_dim, cfg.rope_dims, cfg.n_ctx
-            a.n_chunks = min(64, max(1, blocks // cfg.attn_nkv))
+            # the split-K geometry the model resolved (its config), else the
+            # library default for this grid
+            a.n_chunks = cfg.attn_chunks or min(64, max(1, blocks // cfg.attn_nkv))
+            a.chunk_min = cfg.attn_chunk_min or sinter.ATTN_CHUNK_MIN
             a.theta_scale = float(np.float32(math.pow(float(np.float32(cfg.rope_base)), -2.0 / cfg.rope_dims)))
             a.eps = cfg.eps
             a.scale = float(np.float32(1.0) / np.sqrt(np.float32(cfg.head_dim)))

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libsinter.so")
 
 # sinter_type
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 8, 12, 14, 15, 30
+ATTN_CHUNK_MIN = 128   # SINTER_ATTN_CHUNK_MIN: default positions per split-K attention chunk
 # ops
 OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range(6)
 BENCH_GEMV, BENCH_GDN, BENCH_ATTN = 1, 2, 3

@@ -172,7 +172,7 @@ def test_rmsnorm_quant_q8k_ubatch_matches_oracle(sn, orc, torch_gpu, k, n_tok, w
         assert np.array_equal(got[t], orc.quantize(Q4_K, orc.rmsnorm(x[t], w, eps))), t
 
 
-@pytest.mark.parametrize("k", [5120, 17408])
+@pytest.mark.parametrize("k", [5120, 2048])
 def test_rmsnorm_ubatch_equals_single_token_prologue_wide_range(sn, orc, torch_gpu, k):
     """RMSNorm + Q8_K over a ubatch then the batched GEMV gives, token by
     token, the single-token GEMV with the RMSNORM prologue bit for bit, also
