@@ -591,7 +591,7 @@ def main():
         tok = m.prefill(prompt, 0)
         ps = time.perf_counter() - t1
         prefill_info = {"tokens": args.ctx, "seconds": round(ps, 3), "tok_s": round(args.ctx / ps, 2),
-                        "path": "sinter_model_prefill: decode passes on the GPU with the prompt's tokens forced",
+                        "path": "sinter_model_prefill: batched (ubatches of 256 tokens, each layer once per ubatch)",
                         "prompt": f"random.Random({args.seed + 1}) token ids"}
         print(f"# prefilled {args.ctx} tokens on the GPU in {ps:.1f} s; next token {tok}", file=sys.stderr, flush=True)
     else:

@@ -463,12 +463,33 @@ typedef struct sinter_model_bindings {
 } sinter_model_bindings;
 int  sinter_model_create_bound(const sinter_model_config *cfg, int device, uint32_t blocks,
                                const sinter_model_bindings *b, sinter_model **out);
-/* Prefill on the GPU: tokens[0..n) at positions pos0.. through the decode
- * passes (KV rows and recurrent state written exactly as decoding them one by
- * one would), the greedy continuation of the last one in *next_token (may be
- * null).  Launches run up to the history capacity's passes each. */
+/* Prefill on the GPU: tokens[0..n) at positions pos0.., the greedy
+ * continuation of the last one in *next_token (may be null), its logits in
+ * the model's logits buffer (sinter_model_logits).  The KV rows, the
+ * recurrent and conv states and the logits are bit-identical to decoding the
+ * tokens one by one.  Batched (sinter_model_prefill_batched with
+ * SINTER_PREFILL_UBATCH tokens per ubatch) when every matrix of the model is
+ * Q4_K or Q6_K, else the decode passes (sinter_model_prefill_tokenwise).
+ * Replaces the prompt stage of the reference's server
+ * (docs/PREFILL-SEMANTICS.md:23-57, 379-426). */
 int  sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0,
                           int32_t *next_token);
+/* The decode program over the prompt: one pass per token with each pass's
+ * next token forced to the prompt's (the reference's "(b)" token loop for
+ * every layer); launches run up to the history capacity's passes each. */
+int  sinter_model_prefill_tokenwise(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0,
+                                    int32_t *next_token);
+/* The batched prefill: ubatches of up to `ubatch` tokens (1..SINTER_PREFILL_UBATCH_MAX),
+ * each layer once per ubatch -- RMSNorm + Q8_K, the trunk GEMMs on int8 MFMA
+ * (sinter_op_gemv_ubatch), the conv and the gated-DeltaNet recurrence token
+ * after token in one launch per layer, q/k norm + RoPE + the KV append, and
+ * causal attention split per query as the decode splits it -- then the head
+ * on the last token.  SINTER_ERR_ARG for a model with a matrix of another
+ * type (Q8_0, BF16, F32) or embedded outside. */
+#define SINTER_PREFILL_UBATCH 256
+#define SINTER_PREFILL_UBATCH_MAX 1024
+int  sinter_model_prefill_batched(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0,
+                                  uint32_t ubatch, int32_t *next_token);
 /* the logits of the last pass (n_vocab floats to host): the result_output
  * cell of k0/program.json, read after run_pass / greedy */
 int  sinter_model_logits(sinter_model *m, float *logits_host);

@@ -23,7 +23,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsinter.so")
 REPORT = os.path.join(HERE, "resource_usage.txt")
-SOURCES = ["interp.hip", "ubatch.hip", "hbm.hip", "host.cpp", "model.cpp", "gguf.cpp"]
+SOURCES = ["interp.hip", "ubatch.hip", "prefill.hip", "hbm.hip", "host.cpp", "model.cpp", "gguf.cpp"]
 # -Os: the 27B Q4_K_M decode per token (alternating runs on one box) is
 # 6.07 ms at -O3, 6.00 at -O2, 5.94 at -Os (fewer spilled registers in the
 # K-quant interpreter), 6.08 at -Oz; -O1 6.07; the max-ILP scheduler and

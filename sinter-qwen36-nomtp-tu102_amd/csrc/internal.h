@@ -51,3 +51,27 @@ int validate_gemv(const sinter_gemv_args &a, const char **why);
 void build_gemv_plan(const sinter_gemv_args &a, uint32_t nblk, GemvPlan &p, uint32_t *cuts, const uint32_t *bw);
 
 }  // namespace sinter
+
+namespace sinter {
+
+// the batched prefill's own kernels (prefill.hip), launched on s
+hipError_t launch_embed_ubatch(const void *embd, int type, uint32_t E, const int32_t *tokens, uint32_t n_tok, float *x,
+                               hipStream_t s);
+// the GDN step over n_tok tokens; work: gdn_ubatch_work(...) floats
+hipError_t launch_gdn_ubatch(const float *qkv, const float *alpha, const float *beta, const float *dt_bias,
+                             const float *ssm_a, float *state, float *o, float *work, uint32_t hk, uint32_t hv,
+                             uint32_t d, uint32_t n_tok, float eps, float scale, hipStream_t s);
+size_t gdn_ubatch_work(uint32_t hk, uint32_t hv, uint32_t d, uint32_t n_tok);
+hipError_t launch_attn_prep_ubatch(const float *qg, const float *k, const float *v, const float *q_norm,
+                                   const float *k_norm, void *kc, void *vc, uint32_t kv_type, int32_t pos0,
+                                   uint32_t n_tok, uint32_t nq, uint32_t nkv, uint32_t hd, uint32_t rope_dims,
+                                   float theta_scale, float eps, float *qr, hipStream_t s);
+// causal attention of n_tok queries at positions pos0.. over the cache, split
+// per query as the decode splits it; part: attn_prefill_part(...) floats
+hipError_t launch_attn_prefill(const float *qr, const float *qg, const void *kc, const void *vc, uint32_t kv_type,
+                               int32_t pos0, uint32_t n_tok, uint32_t nq, uint32_t nkv, uint32_t hd,
+                               uint32_t n_chunks, uint32_t chunk_min, float scale, float *part, float *out,
+                               hipStream_t s);
+size_t attn_prefill_part(uint32_t n_tok, uint32_t nq, uint32_t hd, uint32_t n_chunks);
+
+}  // namespace sinter

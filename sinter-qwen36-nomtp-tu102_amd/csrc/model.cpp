@@ -88,6 +88,16 @@ struct sinter_model {
     sinter_gguf *gg = nullptr;   // weights come from this file when set (else synthesised)
     const sinter_model_bindings *ext = nullptr;   // caller-owned weights and state (creation only)
     bool embed_outside = false;  // the caller writes the embedded row into X before each pass
+    // batched prefill buffers for ubatches of up to pf_cap tokens (allocated
+    // at the first batched prefill, kept until the model is destroyed)
+    struct Prefill {
+        uint32_t cap = 0;
+        int32_t *tok = nullptr;
+        float *x = nullptr, *qkv = nullptr, *conv = nullptr, *z = nullptr, *al = nullptr, *be = nullptr;
+        float *o = nullptr, *work = nullptr, *qg = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr;
+        float *att = nullptr, *gate = nullptr, *up = nullptr, *part = nullptr;
+        void *xq = nullptr;
+    } pf;
 };
 
 namespace {
@@ -739,6 +749,199 @@ int sinter_model_bench_program(sinter_model *m, int kind, uint64_t seed) {
     return sinter_host_launch(m->host);
 }
 
+// the argument checks every prefill entry shares
+static int prefill_args(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0) {
+    if (!m || !tokens || n == 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.n_ctx)
+        return set_error(SINTER_ERR_ARG, "prefill: tokens / n / pos0 out of range");
+    if (m->embed_outside) return set_error(SINTER_ERR_STATE, "prefill: the caller embeds each token");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.n_vocab) return set_error(SINTER_ERR_ARG, "prefill: token %u out of range", i);
+    return SINTER_OK;
+}
+
+// Whether the batched prefill runs this model: every matrix a type the
+// batched GEMV reads (Q4_K, Q6_K); why (if not) names the first that is not.
+static bool prefill_batched_ok(const sinter_model *m, std::string &why) {
+    const sinter_model_config &c = m->cfg;
+    auto kq = [](const Tensor &t) { return t.type == SINTER_Q4_K || t.type == SINTER_Q6_K; };
+    for (int il = 0; il < c.n_layer; il++) {
+        const auto &w = m->W[il];
+        const bool at = is_attn(c, il);
+        const int mats_gdn[] = {S_QKV, S_Z, S_ALPHA, S_BETA, S_SSM_OUT, S_FFN_GATE, S_FFN_UP, S_FFN_DOWN};
+        const int mats_att[] = {S_WQ, S_WK, S_WV, S_WO, S_FFN_GATE, S_FFN_UP, S_FFN_DOWN};
+        const int *ms = at ? mats_att : mats_gdn;
+        const int nm = at ? 7 : 8;
+        for (int i = 0; i < nm; i++)
+            if (!kq(w[ms[i]])) {
+                why = "layer " + std::to_string(il) + " matrix slot " + std::to_string(ms[i]) + " has type " +
+                      std::to_string(w[ms[i]].type);
+                return false;
+            }
+    }
+    if (!kq(m->output)) {
+        why = "the output matrix has type " + std::to_string(m->output.type);
+        return false;
+    }
+    if (c.conv_k > 8) {
+        why = "conv kernel longer than 8 taps";
+        return false;
+    }
+    return true;
+}
+
+// The batched prefill's buffers for ubatches of up to cap tokens.
+static int prefill_buffers(sinter_model *m, uint32_t cap) {
+    if (m->pf.cap >= cap) return SINTER_OK;
+    const sinter_model_config &c = m->cfg;
+    const size_t E = (size_t)c.n_embd, F = (size_t)c.n_ff, D = (size_t)c.gdn_d, HD = (size_t)c.head_dim;
+    const size_t C = (size_t)(2 * c.gdn_hk + c.gdn_hv) * D, VD = (size_t)c.gdn_hv * D;
+    const size_t NQ = (size_t)c.attn_nq, RW = (size_t)c.attn_nkv * HD;
+    const size_t kmax = std::max({E, F, VD, NQ * HD});
+    // (buffers of an earlier, smaller cap stay in the model's allocation list)
+    auto f = [&](size_t n) { return static_cast<float *>(dalloc(m, n * 4)); };
+    m->pf.tok = static_cast<int32_t *>(dalloc(m, (size_t)cap * 4));
+    m->pf.x = f(cap * E);
+    m->pf.qkv = f(cap * C);
+    m->pf.conv = f(cap * C);
+    m->pf.z = f(cap * VD);
+    m->pf.al = f(cap * (size_t)c.gdn_hv);
+    m->pf.be = f(cap * (size_t)c.gdn_hv);
+    m->pf.o = f(cap * VD);
+    m->pf.work = f(gdn_ubatch_work((uint32_t)c.gdn_hk, (uint32_t)c.gdn_hv, (uint32_t)D, cap));
+    m->pf.qg = f(cap * NQ * 2 * HD);
+    m->pf.k = f(cap * RW);
+    m->pf.v = f(cap * RW);
+    m->pf.qr = f(cap * NQ * HD);
+    m->pf.att = f(cap * NQ * HD);
+    m->pf.gate = f(cap * F);
+    m->pf.up = f(cap * F);
+    m->pf.part = f(attn_prefill_part(cap, (uint32_t)NQ, (uint32_t)HD, (uint32_t)c.attn_chunks));
+    m->pf.xq = dalloc(m, (size_t)cap * (kmax / 256) * 292);
+    const bool ok = m->pf.tok && m->pf.x && m->pf.qkv && m->pf.conv && m->pf.z && m->pf.al && m->pf.be && m->pf.o &&
+                    m->pf.work && m->pf.qg && m->pf.k && m->pf.v && m->pf.qr && m->pf.att && m->pf.gate &&
+                    m->pf.up && m->pf.part && m->pf.xq;
+    if (!ok) {
+        m->pf.cap = 0;
+        return set_error(SINTER_ERR_HIP, "prefill: buffers for a ubatch of %u tokens", cap);
+    }
+    m->pf.cap = cap;
+    return SINTER_OK;
+}
+
+// One ubatch of T tokens at positions pos.. through every layer (the
+// tokens already in pf.tok); on the last ubatch, the head on its last token.
+static int prefill_ubatch(sinter_model *m, uint32_t T, int32_t pos, bool last) {
+    const sinter_model_config &c = m->cfg;
+    const hipStream_t s = m->stream;
+    void *sv = (void *)s;
+    const uint32_t E = (uint32_t)c.n_embd, F = (uint32_t)c.n_ff, D = (uint32_t)c.gdn_d, HD = (uint32_t)c.head_dim;
+    const uint32_t HK = (uint32_t)c.gdn_hk, HV = (uint32_t)c.gdn_hv, C = (2 * HK + HV) * D, VD = HV * D;
+    const uint32_t NQ = (uint32_t)c.attn_nq, NKV = (uint32_t)c.attn_nkv, RW = NKV * HD;
+    auto &p = m->pf;
+    int rc = SINTER_OK;
+    auto gemv = [&](const Tensor &w, uint32_t k, float *y, int acc) {
+        if (rc == SINTER_OK) rc = sinter_op_gemv_ubatch(w.type, w.d, w.rows, k, p.xq, T, y, acc, sv);
+    };
+    auto hip = [&](hipError_t e, const char *what) {
+        if (rc == SINTER_OK && !hip_ok(e, what)) rc = SINTER_ERR_HIP;
+    };
+    hip(launch_embed_ubatch(m->embd.d, m->embd.type, E, p.tok, T, p.x, s), "prefill: embed");
+    const float theta_scale = (float)std::pow((double)c.rope_base, -2.0 / (double)c.rope_dims);
+    for (int il = 0; il < c.n_layer && rc == SINTER_OK; il++) {
+        const auto &w = m->W[il];
+        rc = sinter_rmsnorm_quant_q8k_ubatch(p.x, (const float *)w[S_ATTN_NORM].d, c.eps, E, T, p.xq, sv);
+        if (is_attn(c, il)) {
+            gemv(w[S_WQ], E, p.qg, 0);
+            gemv(w[S_WK], E, p.k, 0);
+            gemv(w[S_WV], E, p.v, 0);
+            hip(launch_attn_prep_ubatch(p.qg, p.k, p.v, (const float *)w[S_Q_NORM].d, (const float *)w[S_K_NORM].d,
+                                        m->S[il][0].d, m->S[il][1].d, (uint32_t)c.t_kv, pos, T, NQ, NKV, HD,
+                                        (uint32_t)c.rope_dims, theta_scale, c.eps, p.qr, s),
+                "prefill: attention prep");
+            hip(launch_attn_prefill(p.qr, p.qg, m->S[il][0].d, m->S[il][1].d, (uint32_t)c.t_kv, pos, T, NQ, NKV, HD,
+                                    (uint32_t)c.attn_chunks, (uint32_t)c.attn_chunk_min,
+                                    1.0f / std::sqrt((float)HD), p.part, p.att, s),
+                "prefill: attention");
+            if (rc == SINTER_OK) rc = sinter_quant_q8k_ubatch(p.att, (int64_t)NQ * HD, T, p.xq, sv);
+            gemv(w[S_WO], NQ * HD, p.x, 1);
+        } else {
+            gemv(w[S_QKV], E, p.qkv, 0);
+            gemv(w[S_Z], E, p.z, 0);
+            gemv(w[S_ALPHA], E, p.al, 0);
+            gemv(w[S_BETA], E, p.be, 0);
+            if (rc == SINTER_OK)
+                rc = sinter_conv_silu_ubatch(p.qkv, (float *)m->S[il][0].d, (const float *)w[S_CONV_W].d, p.conv, C,
+                                             (uint32_t)c.conv_k, T, sv);
+            hip(launch_gdn_ubatch(p.conv, p.al, p.be, (const float *)w[S_DT_BIAS].d, (const float *)w[S_SSM_A].d,
+                                  (float *)m->S[il][1].d, p.o, p.work, HK, HV, D, T, c.eps,
+                                  1.0f / std::sqrt((float)D), s),
+                "prefill: gated DeltaNet");
+            if (rc == SINTER_OK)
+                rc = sinter_gated_rmsnorm_quant_q8k_ubatch(p.o, p.z, (const float *)w[S_SSM_NORM].d, D, c.eps, VD, T,
+                                                           p.xq, sv);
+            gemv(w[S_SSM_OUT], VD, p.x, 1);
+        }
+        if (rc == SINTER_OK)
+            rc = sinter_rmsnorm_quant_q8k_ubatch(p.x, (const float *)w[S_POST_NORM].d, c.eps, E, T, p.xq, sv);
+        gemv(w[S_FFN_GATE], E, p.gate, 0);
+        gemv(w[S_FFN_UP], E, p.up, 0);
+        if (rc == SINTER_OK) rc = sinter_swiglu_quant_q8k_ubatch(p.gate, p.up, F, T, p.xq, sv);
+        gemv(w[S_FFN_DOWN], F, p.x, 1);
+    }
+    (void)RW;
+    if (rc == SINTER_OK && last) {
+        // the head on the last token: output norm + Q8_K, logits
+        rc = sinter_rmsnorm_quant_q8k_ubatch(p.x + (size_t)(T - 1) * E, (const float *)m->onorm.d, c.eps, E, 1, p.xq,
+                                             sv);
+        if (rc == SINTER_OK)
+            rc = sinter_op_gemv_ubatch(m->output.type, m->output.d, m->output.rows, E, p.xq, 1, m->logits, 0, sv);
+    }
+    return rc;
+}
+
+int sinter_model_prefill_batched(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0, uint32_t ubatch,
+                                 int32_t *next_token) {
+    if (int rc = prefill_args(m, tokens, n, pos0)) return rc;
+    if (ubatch < 1 || ubatch > SINTER_PREFILL_UBATCH_MAX)
+        return set_error(SINTER_ERR_ARG, "prefill: ubatch %u (1..%u)", ubatch, (unsigned)SINTER_PREFILL_UBATCH_MAX);
+    std::string why;
+    if (!prefill_batched_ok(m, why)) return set_error(SINTER_ERR_ARG, "prefill: not batched: %s", why.c_str());
+    const uint32_t cap = std::min(ubatch, n);
+    if (int rc = prefill_buffers(m, cap)) return rc;
+    int rc = SINTER_OK;
+    for (uint32_t b = 0; rc == SINTER_OK && b < n; b += cap) {
+        const uint32_t T = std::min(cap, n - b);
+        if (!hip_ok(hipMemcpyAsync(m->pf.tok, tokens + b, (size_t)T * 4, hipMemcpyHostToDevice, m->stream),
+                    "prefill: tokens"))
+            return SINTER_ERR_HIP;
+        rc = prefill_ubatch(m, T, pos0 + (int32_t)b, b + T == n);
+        // (the token copy of the next ubatch reads host memory the caller
+        // owns: the stream is drained before it is queued)
+        if (rc == SINTER_OK && !hip_ok(hipStreamSynchronize(m->stream), "prefill: ubatch")) rc = SINTER_ERR_HIP;
+    }
+    if (rc != SINTER_OK) return rc;
+    // the greedy continuation: the first maximum of the logits (the decode
+    // head's argmax), also left in the pass cell as a decode pass leaves it
+    std::vector<float> lg((size_t)m->cfg.n_vocab);
+    if (!hip_ok(hipMemcpy(lg.data(), m->logits, lg.size() * 4, hipMemcpyDeviceToHost), "prefill: logits"))
+        return SINTER_ERR_HIP;
+    int32_t best = 0;
+    for (int32_t i = 1; i < m->cfg.n_vocab; i++)
+        if (lg[(size_t)i] > lg[(size_t)best]) best = i;
+    if (!hip_ok(hipMemcpy(&sinter_host_pass_cell(m->host)->token, &best, 4, hipMemcpyHostToDevice), "prefill: token"))
+        return SINTER_ERR_HIP;
+    if (next_token) *next_token = best;
+    return SINTER_OK;
+}
+
+int sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0, int32_t *next_token) {
+    if (int rc = prefill_args(m, tokens, n, pos0)) return rc;
+    std::string why;
+    if (prefill_batched_ok(m, why))
+        return sinter_model_prefill_batched(m, tokens, n, pos0, SINTER_PREFILL_UBATCH, next_token);
+    return sinter_model_prefill_tokenwise(m, tokens, n, pos0, next_token);
+}
+
 int sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logits_host, int32_t *next_token) {
     if (!m || pos < 0 || pos >= m->cfg.n_ctx || token < 0 || token >= m->cfg.n_vocab)
         return set_error(SINTER_ERR_ARG, "decode: token/pos out of range");
@@ -767,12 +970,9 @@ int sinter_model_greedy(sinter_model *m, int32_t token, int32_t pos, uint32_t n,
     return SINTER_OK;
 }
 
-int sinter_model_prefill(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0, int32_t *next_token) {
-    if (!m || !tokens || n == 0 || pos0 < 0 || (int64_t)pos0 + n > m->cfg.n_ctx)
-        return set_error(SINTER_ERR_ARG, "prefill: tokens / n / pos0 out of range");
-    if (m->embed_outside) return set_error(SINTER_ERR_STATE, "prefill: the caller embeds each token");
-    for (uint32_t i = 0; i < n; i++)
-        if (tokens[i] < 0 || tokens[i] >= m->cfg.n_vocab) return set_error(SINTER_ERR_ARG, "prefill: token %u out of range", i);
+int sinter_model_prefill_tokenwise(sinter_model *m, const int32_t *tokens, uint32_t n, int32_t pos0,
+                                   int32_t *next_token) {
+    if (int rc = prefill_args(m, tokens, n, pos0)) return rc;
     uint32_t cap = 0;
     (void)sinter_host_history(m->host, &cap);
     cap = std::max(1u, std::min(cap, 1024u));

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libsinter.so")
 # sinter_type
 F32, F16, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 0, 1, 8, 12, 14, 15, 30
 ATTN_CHUNK_MIN = 128   # SINTER_ATTN_CHUNK_MIN: default positions per split-K attention chunk
+PREFILL_UBATCH = 256   # SINTER_PREFILL_UBATCH: tokens per ubatch of the batched prefill
 # ops
 OP_NOP, OP_BOUNDARY, OP_GEMV, OP_GDN_STEP, OP_ATTN_DECODE, OP_KIND_COUNT = range(6)
 BENCH_GEMV, BENCH_GDN, BENCH_ATTN = 1, 2, 3
@@ -199,6 +200,9 @@ def lib():
         "sinter_model_decode": (I, [vp, C.c_int32, C.c_int32, vp, C.POINTER(C.c_int32)]),
         "sinter_model_greedy": (I, [vp, C.c_int32, C.c_int32, U32, C.POINTER(C.c_int32)]),
         "sinter_model_prefill": (I, [vp, C.POINTER(C.c_int32), U32, C.c_int32, C.POINTER(C.c_int32)]),
+        "sinter_model_prefill_tokenwise": (I, [vp, C.POINTER(C.c_int32), U32, C.c_int32, C.POINTER(C.c_int32)]),
+        "sinter_model_prefill_batched": (I, [vp, C.POINTER(C.c_int32), U32, C.c_int32, U32,
+                                             C.POINTER(C.c_int32)]),
         "sinter_model_create_bound": (I, [C.POINTER(ModelConfig), I, U32, C.POINTER(ModelBindings), C.POINTER(vp)]),
         "sinter_model_synth_context": (I, [vp, C.c_int32, U64]),
         "sinter_model_logits": (I, [vp, vp]),
@@ -375,12 +379,22 @@ class Model:
         check(lib().sinter_model_greedy(self.h, token, pos, n, out), "greedy")
         return list(out)
 
-    def prefill(self, tokens, pos0=0):
-        """Prefill tokens at positions pos0.. on the GPU (decode passes with
-        the prompt's tokens forced); returns the greedy next token."""
+    def prefill(self, tokens, pos0=0, mode="auto", ubatch=PREFILL_UBATCH):
+        """Prefill tokens at positions pos0.. on the GPU; returns the greedy
+        next token.  mode "auto": batched when the model's matrices allow it,
+        else the decode passes; "batched" (ubatches of `ubatch` tokens) or
+        "tokenwise" (the decode passes with the prompt's tokens forced)."""
         arr = (C.c_int32 * len(tokens))(*tokens)
         nxt = C.c_int32()
-        check(lib().sinter_model_prefill(self.h, arr, len(tokens), pos0, C.byref(nxt)), "prefill")
+        if mode == "auto":
+            rc = lib().sinter_model_prefill(self.h, arr, len(tokens), pos0, C.byref(nxt))
+        elif mode == "batched":
+            rc = lib().sinter_model_prefill_batched(self.h, arr, len(tokens), pos0, ubatch, C.byref(nxt))
+        elif mode == "tokenwise":
+            rc = lib().sinter_model_prefill_tokenwise(self.h, arr, len(tokens), pos0, C.byref(nxt))
+        else:
+            raise ValueError(f"prefill mode {mode!r}")
+        check(rc, "prefill")
         return nxt.value
 
     def logits(self, out=None):
