@@ -495,6 +495,65 @@ def parity(m, cfg, args):
                       "pass": mism == 0 and done == args.parity_steps and worst_rel <= 1e-2}), flush=True)
 
 
+def prefill_only(m, cfg, args):
+    """--prefill-check / --prefill-reps: the batched prefill of a --ctx-token
+    prompt alone, optionally checked bit for bit against the decode program
+    over the same prompt on a second model of the same weights."""
+    import random
+
+    import numpy as np
+    import sinter
+    rng = random.Random(args.seed + 1)
+    prompt = [rng.randrange(cfg.n_vocab) for _ in range(args.ctx)]
+    times = []
+    tok = None
+    for r in range(max(1, args.prefill_reps)):
+        t1 = time.perf_counter()
+        tok = m.prefill(prompt, 0, mode="batched")
+        times.append(time.perf_counter() - t1)
+        print(f"# batched prefill {r}: {args.ctx} tokens in {times[-1]:.3f} s; next token {tok}",
+              file=sys.stderr, flush=True)
+    best = min(times)
+    line = {"metric": "prefill tok/s, 27B-shaped Q4_K (batched prefill, ubatch 256)", "value": round(args.ctx / best, 2),
+            "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "tokens": args.ctx,
+            "seconds": [round(t, 4) for t in times], "next_token": tok,
+            "config": {"workload": f"{args.ctx}-token prompt from position 0, Qwen3.6-27B-shaped hybrid, "
+                                   f"{args.quant} weights", "ubatch": sinter.PREFILL_UBATCH},
+            "data": f"synthetic (seeded random-init weights; random.Random({args.seed + 1}) token ids)"}
+    if args.prefill_check:
+        ref = sinter.Model(cfg, seed=args.seed)
+        try:
+            t1 = time.perf_counter()
+            rtok = ref.prefill(prompt, 0, mode="tokenwise")
+            ts = time.perf_counter() - t1
+            print(f"# tokenwise prefill: {args.ctx} tokens in {ts:.1f} s; next token {rtok}", file=sys.stderr,
+                  flush=True)
+            same = {"next_token": tok == rtok, "logits": bool(np.array_equal(m.logits(), ref.logits()))}
+            n_diff = 0
+            for il in range(cfg.n_layer):
+                for sl in range(2):
+                    da, na = m.state(il, sl)
+                    db, nb = ref.state(il, sl)
+                    a = np.empty(na, np.uint8)
+                    b = np.empty(nb, np.uint8)
+                    m.d2h(a, da, na)
+                    ref.d2h(b, db, nb)
+                    if na != nb or not np.array_equal(a, b):
+                        n_diff += 1
+            same["states"] = n_diff == 0
+            line["check"] = {"against": "sinter_model_prefill_tokenwise (the decode program over the prompt), "
+                                        "a second model of the same weights",
+                             "tokenwise_seconds": round(ts, 3), "tokenwise_tok_s": round(args.ctx / ts, 2),
+                             "bit_identical": same, "state_buffers_differing": n_diff,
+                             "compared": "next token, logits, K and V caches of every attention layer, conv and "
+                                         "recurrent state of every GDN layer (whole buffers, byte for byte)"}
+        finally:
+            ref.close()
+    print(json.dumps(line), flush=True)
+    if args.prefill_check and not all(line["check"]["bit_identical"].values()):
+        sys.exit(1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -512,8 +571,8 @@ def main():
     ap.add_argument("--quant", default="q4_k_m", choices=["q4_k_m", "bf16"])
     ap.add_argument("--context", choices=["prefill", "synth"], default=None,
                     help="how the context is made: prefill (default for config 4, as BASELINE specifies it): "
-                         "seeded random prompt tokens through sinter_model_prefill on the GPU (decode passes with "
-                         "the prompt's tokens forced); synth (default for config 5, whose 131072-token prefill "
+                         "seeded random prompt tokens through sinter_model_prefill on the GPU (the batched "
+                         "prefill); synth (default for config 5, whose 131072-token prefill "
                          "would take ~35 min, and for --parity-steps): seeded synthetic KV and recurrent state")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -531,6 +590,14 @@ def main():
     ap.add_argument("--ubatch", type=int, default=0, metavar="T",
                     help="measure the batched GEMV of a batched prefill: T tokens through one GDN layer's "
                          "trunk matrices (sinter_op_gemv_ubatch) instead of the decode")
+    ap.add_argument("--prefill-check", action="store_true",
+                    help="only the prefill: the --ctx-token prompt through the batched prefill (timed), then a "
+                         "second model of the same weights through the decode program over the prompt (timed); "
+                         "the next token, logits, KV caches and recurrent / conv states must be bit-identical; "
+                         "prints one JSON line and exits")
+    ap.add_argument("--prefill-reps", type=int, default=0, metavar="N",
+                    help="only the batched prefill: N timed prefills of the --ctx-token prompt at position 0 "
+                         "(each from the state the last left: the same work); prints one JSON line and exits")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 3 times (the HIP runtime's copy kernel) and exit: the "
                          "known-size reference the FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -583,6 +650,10 @@ def main():
     setup_s = time.perf_counter() - t0
     print(f"# model ready in {setup_s:.1f} s: {m.info()}", file=sys.stderr, flush=True)
     tok, prefill_info = 1, None
+    if args.prefill_check or args.prefill_reps:
+        prefill_only(m, cfg, args)
+        m.close()
+        return
     if args.context == "prefill" and args.ctx > 0:
         import random
         rng = random.Random(args.seed + 1)

@@ -90,15 +90,22 @@ __global__ __launch_bounds__(256) void gdn_prep_ubatch_kernel(GdnUb a) {
 // thread layout and folds -- kv and o as fp64 sums over the thread's RPT rows
 // then lanes_sum_f64 over the column's threads, delta and the update in the
 // same fp32 expressions.  The state slice stays in registers from the first
-// token to the last; each token's inputs (precomputed by
-// gdn_prep_ubatch_kernel) are loaded one token ahead, and no token needs a
-// workgroup barrier.
+// token to the last.  The per-token inputs (precomputed by
+// gdn_prep_ubatch_kernel) move through LDS in stages of GDN_STAGE tokens,
+// double-buffered: stage s + 1 is loaded into registers while stage s is
+// computed, so a token waits on no memory and the workgroup meets at one
+// barrier per stage.
+constexpr uint32_t GDN_STAGE = 16;
 template <uint32_t RPT>
 __global__ __launch_bounds__(256) void gdn_scan_ubatch_kernel(GdnUb a) {
+    // per buffer: k | q [GDN_STAGE][2][D], v [GDN_STAGE][cols], g [GDN_STAGE], beta [GDN_STAGE]
+    constexpr uint32_t BUF = GDN_STAGE * (2 * 256 + 32 + 2);
+    __shared__ __attribute__((aligned(16))) float lds[2 * BUF];
     const uint32_t D = a.d, HK = a.hk, HV = a.hv, cols = a.cols, tpc = 256u / cols;
-    const uint32_t slices = D / cols, item = blockIdx.x;
+    const uint32_t slices = D / cols, item = blockIdx.x, tid = threadIdx.x;
     const uint32_t h = item / slices, c0 = (item % slices) * cols, hk = h % HK;
-    const uint32_t col = c0 + threadIdx.x / tpc, i0 = (threadIdx.x % tpc) * RPT;
+    const uint32_t col = c0 + tid / tpc, i0 = (tid % tpc) * RPT;
+    const uint32_t kq_f = GDN_STAGE * 2 * D, v_off = kq_f, g_off = v_off + GDN_STAGE * cols, b_off = g_off + GDN_STAGE;
     float *srow = a.state + ((size_t)h * D + col) * D + i0;
     float s[RPT];
 #pragma unroll
@@ -106,44 +113,104 @@ __global__ __launch_bounds__(256) void gdn_scan_ubatch_kernel(GdnUb a) {
         const f32x4 t = *reinterpret_cast<const f32x4 *>(srow + r);
         s[r] = t.x; s[r + 1] = t.y; s[r + 2] = t.z; s[r + 3] = t.w;
     }
-    struct In {
-        float k[RPT], q[RPT], v, g, b;
+    // stage loads into registers: thread tid takes float4 j = tid + 256 i of
+    // the k|q block (token j / (D / 2), half (j / (D / 4)) % 2, element
+    // 4 (j % (D / 4))); threads below GDN_STAGE cols / 4 one float4 of v;
+    // threads 128 .. 128 + 2 GDN_STAGE one g or beta
+    constexpr uint32_t KQ4 = GDN_STAGE * 2 * 256 / 4 / 256;   // float4 per thread at D = 256
+    const uint32_t n_kq4 = kq_f / 4, n_v4 = GDN_STAGE * cols / 4;
+    f32x4 rkq[KQ4];
+    f32x4 rv = {0.0f, 0.0f, 0.0f, 0.0f};
+    float rg = 0.0f;
+    const uint32_t nst = (a.n_tok + GDN_STAGE - 1) / GDN_STAGE;
+    auto issue = [&](uint32_t st) {
+        const uint32_t tb = st * GDN_STAGE;
+#pragma unroll
+        for (uint32_t i = 0; i < KQ4; i++) {
+            const uint32_t j = tid + 256u * i;
+            if (j < n_kq4) {
+                const uint32_t tk = j / (D / 2), half = (j / (D / 4)) & 1u, e = 4u * (j % (D / 4));
+                const uint32_t t = min(tb + tk, a.n_tok - 1);
+                const float *src = (half ? a.qn : a.kn) + ((size_t)t * HK + hk) * D + e;
+                rkq[i] = *reinterpret_cast<const f32x4 *>(src);
+            }
+        }
+        if (tid < n_v4) {
+            const uint32_t tk = tid / (cols / 4), e = 4u * (tid % (cols / 4));
+            const uint32_t t = min(tb + tk, a.n_tok - 1);
+            rv = *reinterpret_cast<const f32x4 *>(a.qkv + (size_t)t * a.c_stride + (size_t)2 * HK * D +
+                                                  (size_t)h * D + c0 + e);
+        }
+        if (tid >= 128 && tid < 128 + 2 * GDN_STAGE) {
+            const uint32_t tk = (tid - 128) % GDN_STAGE, t = min(tb + tk, a.n_tok - 1);
+            rg = tid < 128 + GDN_STAGE ? a.gate[(size_t)t * HV + h] : a.bgate[(size_t)t * HV + h];
+        }
     };
-    auto load = [&](uint32_t t, In &in) {
-        const float *kr = a.kn + ((size_t)t * HK + hk) * D + i0, *qr = a.qn + ((size_t)t * HK + hk) * D + i0;
+    auto park = [&](uint32_t st) {
+        float *L = lds + (st & 1u) * BUF;
+#pragma unroll
+        for (uint32_t i = 0; i < KQ4; i++) {
+            const uint32_t j = tid + 256u * i;
+            if (j < n_kq4) *reinterpret_cast<f32x4 *>(L + 4 * j) = rkq[i];
+        }
+        if (tid < n_v4) *reinterpret_cast<f32x4 *>(L + v_off + 4 * tid) = rv;
+        if (tid >= 128 && tid < 128 + 2 * GDN_STAGE) L[g_off + (tid - 128)] = rg;
+    };
+    issue(0);
+    park(0);
+    if (nst > 1) issue(1);
+    __syncthreads();
+    // Each fp64 sum adds exact products (two fp32 values multiply exactly in
+    // fp64), so fma(s, k, acc) rounds exactly as acc + s * k.  Token t's o
+    // sum and token t + 1's kv sum take the same updated state and run in one
+    // loop, two independent chains; the kv sum of a stage's first token runs
+    // alone after the stage barrier.
+    auto load8 = [&](const float *p, float (&d)[RPT]) {
 #pragma unroll
         for (uint32_t r = 0; r < RPT; r += 4) {
-            const f32x4 kv = *reinterpret_cast<const f32x4 *>(kr + r), qv = *reinterpret_cast<const f32x4 *>(qr + r);
-            in.k[r] = kv.x; in.k[r + 1] = kv.y; in.k[r + 2] = kv.z; in.k[r + 3] = kv.w;
-            in.q[r] = qv.x; in.q[r + 1] = qv.y; in.q[r + 2] = qv.z; in.q[r + 3] = qv.w;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(p + r);
+            d[r] = v.x; d[r + 1] = v.y; d[r + 2] = v.z; d[r + 3] = v.w;
         }
-        in.v = a.qkv[(size_t)t * a.c_stride + (size_t)2 * HK * D + (size_t)h * D + col];
-        in.g = a.gate[(size_t)t * HV + h];
-        in.b = a.bgate[(size_t)t * HV + h];
     };
-    In cur, nxt;
-    load(0, cur);
-    for (uint32_t t = 0; t < a.n_tok; t++) {
-        load(min(t + 1, a.n_tok - 1), nxt);
+    for (uint32_t st = 0; st < nst; st++) {
+        const float *L = lds + (st & 1u) * BUF;
+        const uint32_t tb = st * GDN_STAGE, te = min(GDN_STAGE, a.n_tok - tb);
+        float kk[RPT], qq[RPT], kn[RPT];
+        load8(L + i0, kk);
         double dkv = 0.0;
 #pragma unroll
-        for (uint32_t r = 0; r < RPT; r++) dkv += (double)s[r] * (double)cur.k[r];
+        for (uint32_t r = 0; r < RPT; r++) dkv = fma((double)s[r], (double)kk[r], dkv);
         dkv = lanes_sum_f64(dkv, tpc);
-        const float kvf = (float)dkv;
-        const float t1 = cur.g * kvf;
-        const float t2 = cur.v - t1;
-        const float delta = t2 * cur.b;
-        double dout = 0.0;
+        for (uint32_t tk = 0; tk < te; tk++) {
+            const uint32_t tn = tk + 1 < te ? tk + 1 : tk;   // (the last token's "next" sum is dropped)
+            load8(L + tk * 2 * D + D + i0, qq);
+            load8(L + tn * 2 * D + i0, kn);
+            const float vcol = L[v_off + tk * cols + (col - c0)];
+            const float g = L[g_off + tk], beta = L[b_off + tk];
+            const float kvf = (float)dkv;
+            const float t1 = g * kvf;
+            const float t2 = vcol - t1;
+            const float delta = t2 * beta;
+            double dout = 0.0, dkn = 0.0;
 #pragma unroll
-        for (uint32_t r = 0; r < RPT; r++) {
-            const float u1 = cur.g * s[r];
-            const float u2 = cur.k[r] * delta;
-            s[r] = u1 + u2;
-            dout += (double)s[r] * (double)cur.q[r];
+            for (uint32_t r = 0; r < RPT; r++) {
+                const float u1 = g * s[r];
+                const float u2 = kk[r] * delta;
+                s[r] = u1 + u2;
+                dout = fma((double)s[r], (double)qq[r], dout);
+                dkn = fma((double)s[r], (double)kn[r], dkn);
+            }
+            dout = lanes_sum_f64(dout, tpc);
+            dkv = lanes_sum_f64(dkn, tpc);
+            if ((tid % tpc) == 0) a.o[(size_t)(tb + tk) * HV * D + (size_t)h * D + col] = (float)dout * a.scale;
+#pragma unroll
+            for (uint32_t r = 0; r < RPT; r++) kk[r] = kn[r];
         }
-        dout = lanes_sum_f64(dout, tpc);
-        if ((threadIdx.x % tpc) == 0) a.o[(size_t)t * HV * D + (size_t)h * D + col] = (float)dout * a.scale;
-        cur = nxt;
+        if (st + 1 < nst) {
+            park(st + 1);   // (its buffer was last read in stage st - 1, before the last barrier)
+            if (st + 2 < nst) issue(st + 2);
+        }
+        __syncthreads();
     }
 #pragma unroll
     for (uint32_t r = 0; r < RPT; r += 4) {
@@ -268,6 +335,17 @@ struct AttnPrefill {
 };
 
 constexpr uint32_t PF_SLOTS = 8;   // queries per work item
+// K/V tile buffers of the prefill attention: with PF_NBUF = 2 (tile j + 1
+// loads while tile j is computed) the workgroup's LDS fits two workgroups
+// per CU; 3 keeps two tiles in flight as the decode does.
+#ifndef PF_NBUF
+#define PF_NBUF 2
+#endif
+constexpr uint32_t PF_Q8_KC = 2 * PF_NBUF * ATT_Q8_RAWB, PF_Q8_VC = PF_Q8_KC + 32 * 256;
+constexpr uint32_t PF_Q8_KS = PF_Q8_VC + 32 * 256, PF_Q8_VS = PF_Q8_KS + 32 * 8 * 4;
+constexpr uint32_t PF_TILES = PF_NBUF * ATT_F16_BUF > 8u * PF_SLOTS * 256u * 4u ? PF_NBUF * ATT_F16_BUF
+                                                                               : 8u * PF_SLOTS * 256u * 4u;
+static_assert(PF_Q8_VS + 32 * 8 * 4 <= PF_TILES, "Q8_0 tiles fit the tile region");
 
 // Work item = (kv head g, split chunk c, q head hh of g's group, block of 8
 // consecutive queries), the block index running over the query blocks
@@ -284,7 +362,7 @@ constexpr uint32_t PF_SLOTS = 8;   // queries per work item
 // -- the 8 row groups merged, O, M, L -- is the decode's, bit for bit.
 template <bool Q8>
 __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, uint32_t cmax) {
-    __shared__ __attribute__((aligned(16))) unsigned char tiles[ATT_NBUF * ATT_F16_BUF];
+    __shared__ __attribute__((aligned(16))) unsigned char tiles[PF_TILES];
     __shared__ __attribute__((aligned(16))) float wl[8 * (4 * PF_SLOTS + PF_SLOTS)];
     __shared__ __attribute__((aligned(16))) float gm[2 * 8 * PF_SLOTS];
     const uint32_t t = threadIdx.x, HD = a.hd, NQ = a.nq, NKV = a.nkv, gqa = NQ / NKV, C = a.n_chunks;
@@ -319,12 +397,12 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
     const uint32_t w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63u;
     LDS unsigned char *Lu = (LDS unsigned char *)tiles;
     const uint32_t kbase = (uint32_t)(uintptr_t)Lu;
-    // tile j (rows U0 + 32 j ..) into buffer j % ATT_NBUF, as the decode's
+    // tile j (rows U0 + 32 j ..) into buffer j % PF_NBUF, as the decode's
     // issue_tile; rows past U1 re-read row U1 - 1
     auto issue_tile = [&](uint32_t j) {
         const uint32_t t0 = U0 + j * ATT_TILE;
         if constexpr (!Q8) {
-            const uint32_t bo = (j % ATT_NBUF) * ATT_F16_BUF;
+            const uint32_t bo = (j % PF_NBUF) * ATT_F16_BUF;
 #pragma unroll
             for (uint32_t kk = 0; kk < 4; kk++) {
                 const uint32_t k = w + 4 * kk, row = min(t0 + 2 * k + (lane >> 5), U1 - 1);
@@ -333,7 +411,7 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
                 lds_dma16<false>((uintptr_t)a.vc, voff, kbase + bo + ATT_TILE * 512 + k * 1024);
             }
         } else {
-            const uint32_t rb = (j % ATT_NBUF) * 2 * ATT_Q8_RAWB;
+            const uint32_t rb = (j % PF_NBUF) * 2 * ATT_Q8_RAWB;
 #pragma unroll
             for (uint32_t kk = 0; kk < 3; kk++) {
                 const uint32_t c0 = 136u * w + 64u * kk, ci = c0 + lane;
@@ -344,7 +422,7 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
         }
     };
     issue_tile(0);
-    if (ntile > 1) issue_tile(1);
+    if (PF_NBUF > 2 && ntile > 1) issue_tile(1);
     const uint32_t rr = t >> 5, p = t & 31, mp = att_perm(p);
     // register slot s holds query q0 + (s ^ (mp & 7)) of head `head` (zero past the ubatch)
     float qv[PF_SLOTS][8], acc[PF_SLOTS][8];
@@ -370,8 +448,8 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
     LDS float *gml = (LDS float *)gm;
 
     for (uint32_t j = 0; j < ntile; j++) {
-        const uint32_t t0 = U0 + j * ATT_TILE, b = j % ATT_NBUF;
-        if (j + 1 < ntile) {
+        const uint32_t t0 = U0 + j * ATT_TILE, b = j % PF_NBUF;
+        if (PF_NBUF > 2 && j + 1 < ntile) {
             // tile j landed; tile j+1 may still fly
             if (Q8) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
             else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
@@ -379,25 +457,25 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
             dma_wait();
         }
         __syncthreads();   // tile j landed for every wave; every wave is past tile j - 1
-        if (j + 2 < ntile) issue_tile(j + 2);
+        if (j + PF_NBUF - 1 < ntile) issue_tile(j + PF_NBUF - 1);   // into the buffer tile j - 1 used
         const LDS unsigned char *kt = Lu + b * ATT_F16_BUF, *vt = kt + ATT_TILE * 512;
         if constexpr (Q8) {
             const uint32_t rq = t >> 3, bb = t & 7u, rb = b * 2 * ATT_Q8_RAWB;
             const LDS unsigned char *raw = Lu + rb + rq * ATT_Q8_HEAD + 34u * bb;
-            att_q8_split(raw, Lu + ATT_Q8_KC + rq * 256 + 32u * bb, reinterpret_cast<LDS float *>(Lu + ATT_Q8_KS) + t);
+            att_q8_split(raw, Lu + PF_Q8_KC + rq * 256 + 32u * bb, reinterpret_cast<LDS float *>(Lu + PF_Q8_KS) + t);
             sched_fence();
-            att_q8_split(raw + ATT_Q8_RAWB, Lu + ATT_Q8_VC + rq * 256 + 32u * bb,
-                         reinterpret_cast<LDS float *>(Lu + ATT_Q8_VS) + t);
+            att_q8_split(raw + ATT_Q8_RAWB, Lu + PF_Q8_VC + rq * 256 + 32u * bb,
+                         reinterpret_cast<LDS float *>(Lu + PF_Q8_VS) + t);
             __syncthreads();
-            kt = Lu + ATT_Q8_KC;
-            vt = Lu + ATT_Q8_VC;
+            kt = Lu + PF_Q8_KC;
+            vt = Lu + PF_Q8_VC;
         }
         float part[4 * PF_SLOTS];
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             const uint32_t r = rr + 8 * (i ^ (mp >> 3));
             const LDS unsigned char *kr = kt + r * (Q8 ? 256u : 512u);
-            const float ks = Q8 ? reinterpret_cast<const LDS float *>(Lu + ATT_Q8_KS)[r * 8 + (p >> 2)] : 0.0f;
+            const float ks = Q8 ? reinterpret_cast<const LDS float *>(Lu + PF_Q8_KS)[r * 8 + (p >> 2)] : 0.0f;
             float kd[8];
             att_row8<Q8>(kr, p, ks, kd);
 #pragma unroll
@@ -445,7 +523,7 @@ __global__ __launch_bounds__(256) void attn_prefill_split_kernel(AttnPrefill a, 
             const uint32_t r = rr + 8 * i;
             if (t0 + r < U1) {
                 const LDS unsigned char *vr = vt + r * (Q8 ? 256u : 512u);
-                const float vs = Q8 ? reinterpret_cast<const LDS float *>(Lu + ATT_Q8_VS)[r * 8 + (p >> 2)] : 0.0f;
+                const float vs = Q8 ? reinterpret_cast<const LDS float *>(Lu + PF_Q8_VS)[r * 8 + (p >> 2)] : 0.0f;
                 float vd[8];
                 att_row8<Q8>(vr, p, vs, vd);
                 const f32x4 w0 = *reinterpret_cast<const LDS f32x4 *>(wgr + i * PF_SLOTS);

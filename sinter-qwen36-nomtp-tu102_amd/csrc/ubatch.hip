@@ -406,26 +406,31 @@ __global__ __launch_bounds__(64) void gated_norm_quant_q8k_kernel(const float *_
     quant_block_q8k(e, lane, xq + blk * Q8K_BYTES);
 }
 
-// The causal conv + silu of a gated-DeltaNet layer's qkv rows over a ubatch,
-// token after token (the single-token GEMV's CONV epilogue and the oracle's
-// or_conv_silu): one thread per channel c keeps its window {state[c][0..nh-1],
-// x[t][c]} in registers, y[t][c] = silu(sum_j win[j] * w[c][j]) with the sum
-// in fp64 in tap order rounded once, then shifts the window; the state holds
-// the last nh = dconv - 1 inputs when the ubatch ends.
-__global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict__ x, float *__restrict__ st,
+// The causal conv + silu of a gated-DeltaNet layer's qkv rows over a ubatch
+// (the single-token GEMV's CONV epilogue and the oracle's or_conv_silu, token
+// after token): with input(tau) = x[tau][c] for tau >= 0 and the conv state
+// st[c][nh + tau] for -nh <= tau < 0 (nh = dconv - 1, oldest first),
+// y[t][c] = silu(sum_j input(t - nh + j) * w[c][j]), the sum in fp64 in tap
+// order rounded once.  Outputs do not depend on each other, so a thread
+// takes channel c over UB_CONV_TOK consecutive tokens (blockIdx.y), its
+// window in registers; the state moves on in conv_state_kernel, launched
+// after this one.
+constexpr uint32_t UB_CONV_TOK = 8;
+__global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict__ x, const float *__restrict__ st,
                                                        const float *__restrict__ cw, float *__restrict__ y,
                                                        uint32_t channels, uint32_t dconv, uint32_t n_tok) {
     const uint32_t c = blockIdx.x * 256u + threadIdx.x;
     if (c >= channels) return;
-    const uint32_t nh = dconv - 1u;
+    const uint32_t nh = dconv - 1u, t0 = blockIdx.y * UB_CONV_TOK, t1 = min(t0 + UB_CONV_TOK, n_tok);
     float win[UB_CONV_MAX];
     float wt[UB_CONV_MAX];
 #pragma unroll
     for (uint32_t j = 0; j < UB_CONV_MAX; j++) {
-        win[j] = j < nh ? st[(size_t)c * nh + j] : 0.0f;
+        const int tau = (int)t0 - (int)nh + (int)j;
+        win[j] = j >= nh ? 0.0f : tau >= 0 ? x[(size_t)tau * channels + c] : st[(size_t)c * nh + (uint32_t)(tau + (int)nh)];
         wt[j] = j < dconv ? cw[(size_t)c * dconv + j] : 0.0f;
     }
-    for (uint32_t t = 0; t < n_tok; t++) {
+    for (uint32_t t = t0; t < t1; t++) {
         const float xn = x[(size_t)t * channels + c];
         double acc = 0.0;
 #pragma unroll
@@ -436,9 +441,24 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict_
         for (uint32_t j = 0; j + 1 < UB_CONV_MAX; j++)
             if (j < nh) win[j] = (j + 1 < nh) ? win[j + 1] : xn;
     }
+}
+
+// The conv state after the ubatch: st[c][j] = input(n_tok - nh + j), the last
+// nh inputs (old state entries when the ubatch is shorter than nh).
+__global__ __launch_bounds__(256) void conv_state_kernel(const float *__restrict__ x, float *__restrict__ st,
+                                                        uint32_t channels, uint32_t dconv, uint32_t n_tok) {
+    const uint32_t c = blockIdx.x * 256u + threadIdx.x;
+    if (c >= channels) return;
+    const uint32_t nh = dconv - 1u;
+    float nv[UB_CONV_MAX];
+#pragma unroll
+    for (uint32_t j = 0; j < UB_CONV_MAX; j++) {
+        const int tau = (int)n_tok - (int)nh + (int)j;
+        nv[j] = j >= nh ? 0.0f : tau >= 0 ? x[(size_t)tau * channels + c] : st[(size_t)c * nh + (uint32_t)(tau + (int)nh)];
+    }
 #pragma unroll
     for (uint32_t j = 0; j < UB_CONV_MAX; j++)
-        if (j < nh) st[(size_t)c * nh + j] = win[j];
+        if (j < nh) st[(size_t)c * nh + j] = nv[j];
 }
 
 // RMSNorm then the Q8_K quantiser, one workgroup per token: the norm of the
@@ -604,7 +624,10 @@ extern "C" int sinter_conv_silu_ubatch(const float *x, float *state, const float
     if ((uintptr_t)x % 4u || (uintptr_t)state % 4u || (uintptr_t)conv_w % 4u || (uintptr_t)y % 4u)
         return set_error(SINTER_ERR_ARG, "conv_silu_ubatch: alignment (4 bytes)");
     const uint32_t nblk = (uint32_t)((channels + 255) / 256);
-    hipLaunchKernelGGL(conv_silu_kernel, dim3(nblk), dim3(256), 0, (hipStream_t)stream, x, state, conv_w, y,
-                       (uint32_t)channels, dconv, n_tokens);
+    hipLaunchKernelGGL(conv_silu_kernel, dim3(nblk, (n_tokens + UB_CONV_TOK - 1) / UB_CONV_TOK), dim3(256), 0,
+                       (hipStream_t)stream, x, state, conv_w, y, (uint32_t)channels, dconv, n_tokens);
+    if (dconv > 1)
+        hipLaunchKernelGGL(conv_state_kernel, dim3(nblk), dim3(256), 0, (hipStream_t)stream, x, state,
+                           (uint32_t)channels, dconv, n_tokens);
     return hip_ok(hipGetLastError(), "conv_silu_ubatch: launch") ? SINTER_OK : SINTER_ERR_HIP;
 }
