@@ -434,14 +434,18 @@ def op_cpu_baseline(m, c, pos):
 def single_pass_latency(m, tok, pos, n=8):
     """Per-token latency of one pass per launch (sinter_model_decode: pos and
     token set, one cooperative launch, the next token read back): median wall
-    time of n calls."""
+    time of n calls, and the median of those launches' own kernel time (HIP
+    events on the interpreter's stream)."""
     import numpy as np
-    ts = []
+    import sinter
+    L = sinter.lib()
+    ts, ks = [], []
     for i in range(n):
         s = time.perf_counter()
         tok = m.decode(tok, pos + i)
         ts.append(time.perf_counter() - s)
-    return float(np.median(ts)) * 1e3, tok
+        ks.append(float(L.sinter_host_last_launch_ms(m.host())))
+    return float(np.median(ts)) * 1e3, tok, float(np.median(ks))
 
 
 def parity(m, cfg, args):
@@ -714,7 +718,7 @@ def main():
         rep = {n: round(c / 1e5 / args.profile_ops, 4) for n, c in zip(names, cyc)}
         print(f"# block-0 ms per token by kind: {rep}", file=sys.stderr, flush=True)
     # one pass per launch (the reference's doorbell rhythm): per-token latency
-    sp_ms, _ = single_pass_latency(m, toks[-1], pos0 + args.steps + args.profile_ops)
+    sp_ms, _, sp_kernel_ms = single_pass_latency(m, toks[-1], pos0 + args.steps + args.profile_ops)
     mean_attended = pos0 + (args.steps + 1) / 2.0
     bpt = bytes_per_token(cfg, m, mean_attended)
     traffic, traffic_commit = measured_traffic(ppl, args.quant, args.ctx)
@@ -739,7 +743,7 @@ def main():
                      "kernel_ms_per_launch": round(kernel_ms / len(launch_ms), 4),
                      "kernel_ms_per_token": round(kernel_ms / args.steps, 4)},
         "prefill": prefill_info,
-        "single_pass": {"ms_per_token": round(sp_ms, 4), "calls": 8,
+        "single_pass": {"ms_per_token": round(sp_ms, 4), "calls": 8, "kernel_ms": round(sp_kernel_ms, 4),
                         "path": "sinter_model_decode: one cooperative launch per token, token read back"},
     }
     line["roofline"].update(roofline_peaks(achieved))

@@ -263,6 +263,9 @@ int  sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint3
  * core/interp.cu:148-150): the specialised kernels leave out the code of the
  * cases a program does not use. */
 const char *sinter_host_kernel(const sinter_host *h);
+/* The position of the next run_pass / run_passes: the launch's workgroups
+ * write it into the pass cell before their first barrier, as they write the
+ * token those calls take (no command of its own on the stream). */
 int  sinter_host_set_pos(sinter_host *h, int32_t pos);
 /* cooperative grid size (default: one workgroup per CU); before launch() */
 int  sinter_host_set_grid(sinter_host *h, uint32_t blocks);

@@ -580,6 +580,16 @@ struct sinter_host {
     bool profile_ops = false;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // bracket every interpreter launch
     float last_ms = 0.0f;
+    // launch inputs for the next launch (set_pos), the launch record in
+    // pinned host memory, and the barrier epoch the flags hold after the last
+    // launch (valid only after a launch that ran all its passes)
+    int32_t pend_pos = 0;
+    bool have_pos = false;
+    unsigned *out = nullptr;            // [seq, token, pos, err]
+    uint32_t seq = 0;
+    unsigned epoch = 0;
+    bool epoch_ok = false;
+    uint32_t pass_barriers = 0;         // grid barriers per pass: the program's BOUNDARYs + the pass end
     std::vector<sinter_instr> prog;       // host copy of the uploaded program
 };
 
@@ -605,9 +615,24 @@ static int wait_stream(hipStream_t s, double timeout_ms, const char *what) {
     }
 }
 
-static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
+// One launch of n_passes passes.  cell_set / token: the pass cell fields the
+// kernel writes before its first barrier (bit 0 token, bit 1 pos -- the
+// pending set_pos --, bit 2 steps = 0).  The barrier flags are zeroed only
+// when their epoch is unknown (the first launch, or one that stopped early);
+// otherwise the epochs continue from the last launch's.  The result comes
+// back through the launch record in pinned host memory; the device error
+// cell is read only when the record is missing (a launch that stopped early).
+static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms, uint32_t cell_set = 0,
+                      int32_t token = 0) {
     InterpCtl ctl;
     std::memset(&ctl, 0, sizeof ctl);
+    ctl.cell = h->d_pass;
+    ctl.cell_token = token;
+    ctl.cell_pos = h->pend_pos;
+    ctl.cell_set = cell_set | (h->have_pos ? 2u : 0u);
+    ctl.out = h->out;
+    ctl.seq = ++h->seq;
+    if (ctl.seq == 0) ctl.seq = ++h->seq;   // (0 never marks a record)
     ctl.flags = h->d_cells + CELL_GROUPS / 4;
     ctl.err = h->d_cells + 32;
     ctl.pass_cycles = h->d_pass_cycles;
@@ -621,8 +646,15 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     ctl.cuts = h->d_cuts;
     ctl.n_instr = h->n_instr;
     ctl.n_passes = n_passes;
-    if (!hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream), "barrier flags reset"))
-        return SINTER_RUN_ERR;
+    if (!h->epoch_ok) {
+        if (!hip_ok(hipMemsetAsync(h->d_cells + CELL_GROUPS / 4, 0, CELL_GROUP_BYTES, h->stream),
+                    "barrier flags reset"))
+            return SINTER_RUN_ERR;
+        h->epoch = 0;
+    }
+    ctl.epoch0 = h->epoch;
+    h->epoch_ok = false;   // until this launch is seen to finish every pass
+    h->have_pos = false;
     if (!hip_ok(hipEventRecord(h->ev0, h->stream), "event")) return SINTER_RUN_ERR;
     if (!hip_ok(launch_interp(h->d_prog, ctl, h->blocks, h->stream, h->feat), "cooperative launch"))
         return SINTER_RUN_ERR;
@@ -636,13 +668,21 @@ static int run_launch(sinter_host *h, uint32_t n_passes, double timeout_ms) {
     }
     if (ws != SINTER_OK) return SINTER_RUN_ERR;
     (void)hipEventElapsedTime(&h->last_ms, h->ev0, h->ev1);
+    const volatile unsigned *rec = h->out;
+    if (rec[0] == ctl.seq && rec[3] == 0) {
+        h->epoch = ctl.epoch0 + n_passes * h->pass_barriers;
+        h->epoch_ok = true;
+        return SINTER_RUN_OK;
+    }
+    // stopped early (or an error in the record): the device's error cell
     unsigned e[2] = {0, 0};
     if (!hip_ok(hipMemcpy(e, h->d_cells + 32, 8, hipMemcpyDeviceToHost), "error cell")) return SINTER_RUN_ERR;
     if (e[0]) {
         set_error(SINTER_ERR_DEVICE, "device error %u (aux %u)", e[0], e[1]);
         return SINTER_RUN_ERR;
     }
-    return SINTER_RUN_OK;
+    return set_error(SINTER_ERR_DEVICE, "launch ended without its record (seq %u, record %u)", ctl.seq, rec[0]),
+           SINTER_RUN_ERR;
 }
 
 extern "C" {
@@ -669,7 +709,9 @@ int sinter_host_init(sinter_host **out, int device, unsigned pass_cycles_cap) {
     h->spin_limit = h->clock_khz * 1000ull * 10ull;  // 10 s
     bool ok = hip_ok(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "stream") &&
               hip_ok(hipEventCreate(&h->ev0), "event") && hip_ok(hipEventCreate(&h->ev1), "event") &&
-              hip_ok(hipMalloc(&h->d_cells, CELL_BYTES), "cells") && hip_ok(hipMemset(h->d_cells, 0, CELL_BYTES), "cells clear");
+              hip_ok(hipMalloc(&h->d_cells, CELL_BYTES), "cells") && hip_ok(hipMemset(h->d_cells, 0, CELL_BYTES), "cells clear") &&
+              hip_ok(hipHostMalloc(reinterpret_cast<void **>(&h->out), 64, hipHostMallocCoherent), "launch record");
+    if (ok) std::memset(h->out, 0, 64);
     if (ok) h->d_pass = reinterpret_cast<sinter_pass_cell *>(reinterpret_cast<char *>(h->d_cells) + 1024);
     h->pass_cycles_cap = pass_cycles_cap;
     if (ok && pass_cycles_cap) {
@@ -744,6 +786,9 @@ int sinter_host_upload(sinter_host *h, const sinter_instr *prog, uint32_t n_inst
         return SINTER_ERR_HIP;
     h->n_instr = n_instr;
     h->epoch_stride = epoch_stride;
+    h->pass_barriers = 1;
+    for (uint32_t i = 0; i < n_instr; i++) h->pass_barriers += prog[i].kind == SINTER_OP_BOUNDARY ? 1u : 0u;
+    h->epoch_ok = false;
     // SINTER_INTERP=general (a diagnostic): launch the general interpreter
     // whatever the program's types
     const char *force = std::getenv("SINTER_INTERP");
@@ -797,17 +842,13 @@ int sinter_host_launch(sinter_host *h) {
 
 int sinter_host_run_pass(sinter_host *h, int32_t token, double timeout_ms) {
     if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_pass before launch"), SINTER_RUN_ERR;
-    if (!hip_ok(hipMemsetD32Async(&h->d_pass->token, token, 1, h->stream), "token write")) return SINTER_RUN_ERR;
-    return run_launch(h, 1, timeout_ms);
+    return run_launch(h, 1, timeout_ms, 1u, token);
 }
 
 int sinter_host_run_passes(sinter_host *h, int32_t token, uint32_t n_passes, int32_t *tokens_out, double timeout_ms) {
     if (!h || !h->launched) return set_error(SINTER_ERR_STATE, "run_passes before launch"), SINTER_RUN_ERR;
     if (n_passes == 0 || n_passes > h->history_cap) return set_error(SINTER_ERR_ARG, "n_passes"), SINTER_RUN_ERR;
-    if (!hip_ok(hipMemsetD32Async(&h->d_pass->token, token, 1, h->stream), "token write") ||
-        !hip_ok(hipMemsetD32Async(&h->d_pass->steps, 0, 1, h->stream), "steps reset"))
-        return SINTER_RUN_ERR;
-    const int rs = run_launch(h, n_passes, timeout_ms);
+    const int rs = run_launch(h, n_passes, timeout_ms, 1u | 4u, token);
     if (rs != SINTER_RUN_OK) return rs;
     if (tokens_out &&
         !hip_ok(hipMemcpy(tokens_out, h->d_history, (size_t)n_passes * 4, hipMemcpyDeviceToHost), "history read"))
@@ -835,6 +876,7 @@ void sinter_host_destroy(sinter_host *h) {
     if (h->d_pass_cycles) (void)hipFree(h->d_pass_cycles);
     if (h->d_op_cycles) (void)hipFree(h->d_op_cycles);
     if (h->d_history) (void)hipFree(h->d_history);
+    if (h->out) (void)hipHostFree(h->out);
     if (h->ev0) (void)hipEventDestroy(h->ev0);
     if (h->ev1) (void)hipEventDestroy(h->ev1);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -907,14 +949,23 @@ int sinter_host_set_grid(sinter_host *h, uint32_t blocks) {
         return set_error(SINTER_ERR_ARG, "set_grid: %u blocks exceed the co-resident limit %d", blocks,
                          per_cu * p.multiProcessorCount);
     h->blocks = blocks;
+    h->epoch_ok = false;   // flags of workgroups that have not run yet
     return SINTER_OK;
 }
 
 int sinter_host_set_pos(sinter_host *h, int32_t pos) {
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
-    // a 32-bit fill carries the value in the command itself: no host buffer
-    // to stage, no wait (the stream orders it before the next launch)
-    return hip_ok(hipMemsetD32Async(&h->d_pass->pos, pos, 1, h->stream), "pos write") ? SINTER_OK : SINTER_ERR_HIP;
+    // the next launch's workgroups write it into the pass cell (no command
+    // of its own on the stream)
+    h->pend_pos = pos;
+    h->have_pos = true;
+    return SINTER_OK;
 }
 
 }  // extern "C"
+
+namespace sinter {
+int32_t host_last_token(const sinter_host *h) {
+    return h && h->out ? (int32_t)((const volatile unsigned *)h->out)[1] : -1;
+}
+}  // namespace sinter

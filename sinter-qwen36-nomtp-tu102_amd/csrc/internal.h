@@ -22,6 +22,18 @@ struct InterpCtl {
     uint32_t n_passes;
     uint32_t pass_cycles_cap;
     uint32_t pass_base;
+    // launch inputs: every workgroup writes the fields cell_set names into
+    // the pass cell before its first barrier (bit 0 token, bit 1 pos, bit 2
+    // steps = 0; all write the same values)
+    sinter_pass_cell *cell;
+    int32_t cell_token, cell_pos;
+    uint32_t cell_set;
+    unsigned epoch0;          // barrier epoch the flags hold at the launch (0: zeroed flags)
+    // launch record in host-visible memory, or null: [1] token, [2] pos, [3]
+    // error code of the pass cell after the last pass, then [0] = seq; written
+    // only by a launch that ran all its passes
+    unsigned *out;
+    uint32_t seq;
 };
 
 hipError_t launch_op(const sinter_instr *ins_dev, const GemvPlan *plan, const uint32_t *cuts, uint32_t blocks,
@@ -36,6 +48,8 @@ hipError_t launch_synth(void *dst, int kind, int type, uint64_t n_units, uint64_
                         hipStream_t s);
 
 // host-side helpers (host.cpp)
+// the pass cell's token after the host's last launch (its launch record)
+int32_t host_last_token(const sinter_host *h);
 int set_error(int status, const char *fmt, ...);
 bool hip_ok(hipError_t e, const char *what);
 unsigned *op_err_cell();  // per-device error cell of the standalone op launches

@@ -41,7 +41,7 @@ using namespace sinter;
 // KV cache types its ops handle; isa.h): one kernel per set below.
 template <uint32_t F>
 __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ prog, const InterpCtl &ctl) {
-    unsigned epoch = 0;
+    unsigned epoch = ctl.epoch0;
     const uint32_t n = ctl.n_instr;
     const bool timed = ctl.op_cycles && blockIdx.x == 0;
     // i in [0, n]: i == n is the pass-end barrier.  A barrier followed by a
@@ -51,7 +51,16 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
     // next pass's first instruction.  One copy of each op's code.
     uint32_t pass = 0, i = 0;
     uint64_t t0 = wall_clock64();
-    if (threadIdx.x == 0) g_att_key[0] = ATT_NO_CACHE;   // no attention cache from an earlier launch
+    if (threadIdx.x == 0) {
+        g_att_key[0] = ATT_NO_CACHE;   // no attention cache from an earlier launch
+        // the launch's inputs into the pass cell: every workgroup stores the
+        // same values and waits for its stores, so its own reads below see
+        // them, and each workgroup's stores precede its first arrival
+        if (ctl.cell_set & 1u) st_coh(&ctl.cell->token, ctl.cell_token);
+        if (ctl.cell_set & 2u) st_coh(&ctl.cell->pos, ctl.cell_pos);
+        if (ctl.cell_set & 4u) st_coh(&ctl.cell->steps, 0);
+        settle_vmem();
+    }
     __syncthreads();
     const bool traced = ctl.trace != nullptr;
     auto stamp = [&](uint32_t ii, uint32_t k, uint64_t v) {
@@ -145,6 +154,17 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
             stamp(i, 3, wall_clock64());
         }
         i += 1;
+    }
+    // every pass ran: the launch record (the last pass-end barrier put every
+    // workgroup's cell and error stores before this)
+    if (ctl.out && blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned e = __hip_atomic_load(ctl.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int tok = ld_coh(&ctl.cell->token), pos = ld_coh(&ctl.cell->pos);
+        __hip_atomic_store(ctl.out + 1, (unsigned)tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ctl.out + 2, (unsigned)pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ctl.out + 3, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ctl.out, ctl.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        settle_vmem();
     }
 }
 

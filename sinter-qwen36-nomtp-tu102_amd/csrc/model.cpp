@@ -952,9 +952,7 @@ int sinter_model_decode(sinter_model *m, int32_t token, int32_t pos, float *logi
     if (logits_host &&
         !hip_ok(hipMemcpy(logits_host, m->logits, (size_t)m->cfg.n_vocab * 4, hipMemcpyDeviceToHost), "logits"))
         return SINTER_ERR_HIP;
-    if (next_token &&
-        !hip_ok(hipMemcpy(next_token, &sinter_host_pass_cell(m->host)->token, 4, hipMemcpyDeviceToHost), "token"))
-        return SINTER_ERR_HIP;
+    if (next_token) *next_token = host_last_token(m->host);   // (the launch record: no device read)
     return SINTER_OK;
 }
 
@@ -998,9 +996,7 @@ int sinter_model_prefill_tokenwise(sinter_model *m, const int32_t *tokens, uint3
     }
     if (!set_forced(nullptr, 0) && rc == SINTER_OK) rc = SINTER_ERR_HIP;
     (void)hipFree(d_tok);
-    if (rc == SINTER_OK && next_token &&
-        !hip_ok(hipMemcpy(next_token, &sinter_host_pass_cell(m->host)->token, 4, hipMemcpyDeviceToHost), "prefill: token"))
-        rc = SINTER_ERR_HIP;
+    if (rc == SINTER_OK && next_token) *next_token = host_last_token(m->host);
     return rc;
 }
 
