@@ -443,35 +443,68 @@ void or_gdn_gates(const float *alpha, const float *beta_raw, const float *dt_bia
     }
 }
 
-/* k0/ops/gdn.cuh:248-337 (delta rule, modulo head map hk = h % HK):
- *   kv    = sum_i S[i][col] k[i]                       (fp64, rounded once)
- *   delta = (v[col] - g*kv) * beta                     (fp32 ops)
- *   S'    = g*S + k*delta                              (fp32: mul, mul, add)
- *   o     = (sum_i S'[i][col] q[i]) * scale            (fp64 sum, then fp32 mul) */
+/* k0/ops/gdn.cuh:248-337 (delta rule, modulo head map hk = h % HK), with
+ * the declared fp32 folds of k0/ops/gdn.cuh:19-28 over the kernel's thread
+ * layout (csrc/gdn.h): a state column's D rows split over tpc = 256 / cols
+ * threads, thread t holding rows [t rpt, (t + 1) rpt), rpt = D / tpc:
+ *   kv    = tree_t (sum_r S[t rpt + r][col] k[t rpt + r])   per-thread sums
+ *           sequential fp32 (a rounded product, then a rounded add), closed
+ *           by the butterfly a[t] += a[t ^ m], m = 1, 2, 4, ... (or_lanes_tree)
+ *   delta = (v[col] - g*kv) * beta                            (fp32 ops)
+ *   S'    = g*S + k*delta                                     (fp32: mul, mul, add)
+ *   o     = tree_t (sum_r S'[..][col] q[..]) * scale          (same fold, scale last) */
+static float or_lanes_tree(float *a, int n) {
+    for (int m = 1; m < n; m <<= 1) {
+        float b[64];
+        for (int t = 0; t < n; t++) b[t] = a[t] + a[t ^ m];
+        memcpy(a, b, sizeof(float) * (size_t)n);
+    }
+    return a[0];
+}
+
 void or_gdn_step(const float *q, const float *k, const float *v, const float *g,
                  const float *beta, float *state, float *o, int hv, int hk, int d,
-                 float scale) {
+                 float scale, int cols) {
+    const int tpc = 256 / cols, rpt = d / tpc;
     for (int h = 0; h < hv; h++) {
         const int kh = h % hk;
         const float *qh = q + (size_t)kh * d, *kk = k + (size_t)kh * d;
         const float gv = g[h], bv = beta[h];
         for (int col = 0; col < d; col++) {
             float *s = state + ((size_t)h * d + col) * d;
-            double kv = 0.0;
-            for (int i = 0; i < d; i++) kv += (double)s[i] * (double)kk[i];
-            const float kvf = (float)kv;
-            const float delta = (v[(size_t)h * d + col] - gv * kvf) * bv;
-            double acc = 0.0;
+            float part[64];
+            for (int t = 0; t < tpc; t++) {
+                float acc = 0.0f;
+                for (int r = 0; r < rpt; r++) {
+                    const float pr = s[t * rpt + r] * kk[t * rpt + r];
+                    acc = acc + pr;
+                }
+                part[t] = acc;
+            }
+            const float kvf = or_lanes_tree(part, tpc);
+            const float t1 = gv * kvf;
+            const float t2 = v[(size_t)h * d + col] - t1;
+            const float delta = t2 * bv;
             for (int i = 0; i < d; i++) {
                 const float a = gv * s[i];
                 const float b = kk[i] * delta;
                 s[i] = a + b;
-                acc += (double)s[i] * (double)qh[i];
             }
-            o[(size_t)h * d + col] = (float)acc * scale;
+            for (int t = 0; t < tpc; t++) {
+                float acc = 0.0f;
+                for (int r = 0; r < rpt; r++) {
+                    const float pr = s[t * rpt + r] * qh[t * rpt + r];
+                    acc = acc + pr;
+                }
+                part[t] = acc;
+            }
+            o[(size_t)h * d + col] = or_lanes_tree(part, tpc) * scale;
         }
     }
 }
+
+/* the GDN step's columns per workgroup item for a head size (csrc/model.cpp) */
+int or_gdn_cols(int d) { return d >= 128 ? 32 : 16; }
 
 /* k0/ops/gdn.cuh:339-383: per head rms_norm(x)*w, then * silu(z). */
 void or_gated_rmsnorm(const float *x, const float *z, const float *w, float *y,
@@ -775,7 +808,7 @@ void or_gdn_mixer(const or_cfg *c, const void *const *w, void *const *st,
     or_gdn_gates(al, br, (const float *)w[OR_SLOT_DT_BIAS], (const float *)w[OR_SLOT_SSM_A], g, be, HV);
     const float scale = 1.0f / sqrtf((float)D);
     or_gdn_step(cv, cv + (size_t)HK * D, cv + (size_t)2 * HK * D, g, be, (float *)st[OR_ST_SSM], o,
-                HV, HK, D, scale);
+                HV, HK, D, scale, or_gdn_cols(D));
     or_gated_rmsnorm(o, z, (const float *)w[OR_SLOT_SSM_NORM], on, HV, D, c->eps);
     or_gemv(t, w[OR_SLOT_SSM_OUT], E, VD, on, out);
     if (dbg) {

@@ -75,10 +75,12 @@ void or_conv_silu(const float *xnew, float *conv_state, const float *conv_w,
                   float *out, int64_t channels, int dconv);
 void or_gdn_gates(const float *alpha, const float *beta_raw, const float *dt_bias,
                   const float *ssm_a, float *g, float *beta, int nh);
-/* state M[h][col][i] = S[i][col], updated in place; o[h*dv + col] */
+/* state M[h][col][i] = S[i][col], updated in place; o[h*dv + col]; the fp32
+ * folds follow the kernel's layout of cols columns per 256-thread item */
 void or_gdn_step(const float *q, const float *k, const float *v, const float *g,
                  const float *beta, float *state, float *o, int hv, int hk, int d,
-                 float scale);
+                 float scale, int cols);
+int or_gdn_cols(int d);
 void or_gated_rmsnorm(const float *x, const float *z, const float *w, float *y,
                       int nh, int d, float eps);
 

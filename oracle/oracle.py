@@ -56,7 +56,8 @@ def lib():
             "or_silu": (f, [f]), "or_sigmoid": (f, [f]), "or_softplus": (f, [f]),
             "or_conv_silu": (None, [p, p, p, p, i64, i]),
             "or_gdn_gates": (None, [p, p, p, p, p, p, i]),
-            "or_gdn_step": (None, [p, p, p, p, p, p, p, i, i, i, f]),
+            "or_gdn_step": (None, [p, p, p, p, p, p, p, i, i, i, f, i]),
+            "or_gdn_cols": (i, [i]),
             "or_gated_rmsnorm": (None, [p, p, p, p, i, i, f]),
             "or_rope_theta_scale": (f, [f, i]), "or_rope_neox": (None, [p, i, i, i, f]),
             "or_attn_decode": (None, [p, p, p, i, i, i, i, i, f, p]),

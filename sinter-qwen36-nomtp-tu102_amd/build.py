@@ -44,10 +44,14 @@ LDS_LIMIT = 160 * 1024
 # the committed build; a change that spills more fails until it is measured
 # and the budget raised on purpose).  Spills to memory (scratch) are never
 # accepted.
+# Raised once on purpose: the fp32 GDN-step folds moved the K-quant kernels
+# from (12, 406) / (18, 405) to (22, 475) / (22, 492) spills, with the
+# 27B-shaped decode unchanged (A/B, three alternating runs each: 5.924 vs
+# 5.932 ms per token).
 SPILL_BUDGET = {
-    "sinter_interp": (20, 593),
-    "sinter_interp_kquant": (12, 406),
-    "sinter_interp_kquant_q8kv": (18, 405),
+    "sinter_interp": (20, 596),
+    "sinter_interp_kquant": (22, 475),
+    "sinter_interp_kquant_q8kv": (22, 492),
     "sinter_interp_bf16": (12, 455),
     "sinter_op_kernel": (0, 211),
     "sinter_op_noalloc_kernel": (0, 171),

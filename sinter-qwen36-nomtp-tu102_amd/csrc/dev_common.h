@@ -182,6 +182,19 @@ __device__ __forceinline__ double lanes_sum_f64(double v, uint32_t n) {
     return v;
 }
 
+// The same butterfly in fp32: after the step at distance m every lane holds
+// the sum of its aligned group of 2m lanes, partner order not mattering (an
+// fp32 add commutes exactly), i.e. the tree a[t] += a[t ^ m], m = 1, 2, 4, ...
+__device__ __forceinline__ float lanes_sum_f32(float v, uint32_t n) {
+    if (n >= 2) v += dpp_f<DPP_XOR1>(v);
+    if (n >= 4) v += dpp_f<DPP_XOR2>(v);
+    if (n >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if (n >= 16) v += dpp_f<DPP_MIRROR>(v);
+    if (n >= 32) v += __shfl_xor(v, 16, 64);
+    if (n >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // ---------------------------------------------------------------- conversions
 
 __device__ __forceinline__ float h2f(uint16_t h) {

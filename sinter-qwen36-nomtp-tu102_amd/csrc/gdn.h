@@ -13,9 +13,13 @@
 // D/cols workgroups; each streams its cols*D*4 bytes of state once in and
 // once out (in place).  The k-head of v-head h is h % HK (gdn.cuh:257-259).
 //
-// Declared numerics (oracle/oracle.c or_gdn_step): kv and o are fp64 sums of
-// exact fp32 products rounded to fp32 once; delta and the state update are
-// the reference's fp32 expressions (mul, mul, add; no contraction).
+// Declared numerics (oracle/oracle.c or_gdn_step), fp32 folds in the style
+// of k0/ops/gdn.cuh:19-28: kv and o are per-thread sequential fp32 sums over
+// the thread's RPT rows ascending (acc = acc + s*x, a rounded product then a
+// rounded add, never contracted), closed by the butterfly a[t] += a[t ^ m],
+// m = 1, 2, 4, ... over the column's tpc = 256 / cols threads
+// (lanes_sum_f32); delta = (v - g*kv) * beta and the state update g*S + k*delta
+// are the reference's fp32 expressions (mul, mul, add); o is scaled last.
 #pragma once
 #include <type_traits>
 
@@ -107,29 +111,32 @@ __device__ __forceinline__ bool op_gdn_step(const sinter_instr &ins, unsigned *e
         __syncthreads();
         if (ts && item == rel) ts[1] = wall_clock64();
 
-        double dkv = 0.0;
+        float dkv = 0.0f;
 #pragma unroll
-        for (uint32_t r = 0; r < RPT; r++) dkv += (double)s[r] * (double)ks[i0 + r];
-        dkv = lanes_sum_f64(dkv, tpc);
-        const float kvf = (float)dkv;
+        for (uint32_t r = 0; r < RPT; r++) {
+            const float pr = s[r] * ks[i0 + r];
+            dkv = dkv + pr;
+        }
+        const float kvf = lanes_sum_f32(dkv, tpc);
         const float t1 = g * kvf;
         const float t2 = vcol - t1;
         const float delta = t2 * beta;
-        double dout = 0.0;
+        float dout = 0.0f;
 #pragma unroll
         for (uint32_t r = 0; r < RPT; r++) {
             const float u1 = g * s[r];
             const float u2 = ks[i0 + r] * delta;
             s[r] = u1 + u2;
-            dout += (double)s[r] * (double)qs[i0 + r];
+            const float pr = s[r] * qs[i0 + r];
+            dout = dout + pr;
         }
-        dout = lanes_sum_f64(dout, tpc);
+        dout = lanes_sum_f32(dout, tpc);
 #pragma unroll
         for (uint32_t r = 0; r < RPT; r += 4) {
             const f32x4 v = {s[r], s[r + 1], s[r + 2], s[r + 3]};
             *reinterpret_cast<GLB f32x4 *>(srow + r) = v;
         }
-        if ((threadIdx.x % tpc) == 0) st_coh(a.o + (size_t)h * D + col, (float)dout * a.scale);
+        if ((threadIdx.x % tpc) == 0) st_coh(a.o + (size_t)h * D + col, dout * a.scale);
         if (ts && item == rel) ts[2] = wall_clock64();
         __syncthreads();  // qs/ks reused by the next item
     }

@@ -87,9 +87,9 @@ __global__ __launch_bounds__(256) void gdn_prep_ubatch_kernel(GdnUb a) {
 
 // The delta rule over the ubatch: one (v-head, slice of `cols` state
 // columns) item per workgroup, the decode op_gdn_step's item (gdn.h) with its
-// thread layout and folds -- kv and o as fp64 sums over the thread's RPT rows
-// then lanes_sum_f64 over the column's threads, delta and the update in the
-// same fp32 expressions.  The state slice stays in registers from the first
+// thread layout and folds -- kv and o as sequential fp32 sums over the
+// thread's RPT rows then lanes_sum_f32 over the column's threads, delta and
+// the update in the same fp32 expressions.  The state slice stays in registers from the first
 // token to the last.  The per-token inputs (precomputed by
 // gdn_prep_ubatch_kernel) move through LDS in stages of GDN_STAGE tokens,
 // double-buffered: stage s + 1 is loaded into registers while stage s is
@@ -160,11 +160,9 @@ __global__ __launch_bounds__(256) void gdn_scan_ubatch_kernel(GdnUb a) {
     park(0);
     if (nst > 1) issue(1);
     __syncthreads();
-    // Each fp64 sum adds exact products (two fp32 values multiply exactly in
-    // fp64), so fma(s, k, acc) rounds exactly as acc + s * k.  Token t's o
-    // sum and token t + 1's kv sum take the same updated state and run in one
-    // loop, two independent chains; the kv sum of a stage's first token runs
-    // alone after the stage barrier.
+    // Token t's o sum and token t + 1's kv sum take the same updated state
+    // and run in one loop, two independent chains; the kv sum of a stage's
+    // first token runs alone after the stage barrier.
     auto load8 = [&](const float *p, float (&d)[RPT]) {
 #pragma unroll
         for (uint32_t r = 0; r < RPT; r += 4) {
@@ -177,32 +175,36 @@ __global__ __launch_bounds__(256) void gdn_scan_ubatch_kernel(GdnUb a) {
         const uint32_t tb = st * GDN_STAGE, te = min(GDN_STAGE, a.n_tok - tb);
         float kk[RPT], qq[RPT], kn[RPT];
         load8(L + i0, kk);
-        double dkv = 0.0;
+        float dkv = 0.0f;
 #pragma unroll
-        for (uint32_t r = 0; r < RPT; r++) dkv = fma((double)s[r], (double)kk[r], dkv);
-        dkv = lanes_sum_f64(dkv, tpc);
+        for (uint32_t r = 0; r < RPT; r++) {
+            const float pr = s[r] * kk[r];
+            dkv = dkv + pr;
+        }
+        dkv = lanes_sum_f32(dkv, tpc);
         for (uint32_t tk = 0; tk < te; tk++) {
             const uint32_t tn = tk + 1 < te ? tk + 1 : tk;   // (the last token's "next" sum is dropped)
             load8(L + tk * 2 * D + D + i0, qq);
             load8(L + tn * 2 * D + i0, kn);
             const float vcol = L[v_off + tk * cols + (col - c0)];
             const float g = L[g_off + tk], beta = L[b_off + tk];
-            const float kvf = (float)dkv;
+            const float kvf = dkv;
             const float t1 = g * kvf;
             const float t2 = vcol - t1;
             const float delta = t2 * beta;
-            double dout = 0.0, dkn = 0.0;
+            float dout = 0.0f, dkn = 0.0f;
 #pragma unroll
             for (uint32_t r = 0; r < RPT; r++) {
                 const float u1 = g * s[r];
                 const float u2 = kk[r] * delta;
                 s[r] = u1 + u2;
-                dout = fma((double)s[r], (double)qq[r], dout);
-                dkn = fma((double)s[r], (double)kn[r], dkn);
+                const float po = s[r] * qq[r], pn = s[r] * kn[r];
+                dout = dout + po;
+                dkn = dkn + pn;
             }
-            dout = lanes_sum_f64(dout, tpc);
-            dkv = lanes_sum_f64(dkn, tpc);
-            if ((tid % tpc) == 0) a.o[(size_t)(tb + tk) * HV * D + (size_t)h * D + col] = (float)dout * a.scale;
+            dout = lanes_sum_f32(dout, tpc);
+            dkv = lanes_sum_f32(dkn, tpc);
+            if ((tid % tpc) == 0) a.o[(size_t)(tb + tk) * HV * D + (size_t)h * D + col] = dout * a.scale;
 #pragma unroll
             for (uint32_t r = 0; r < RPT; r++) kk[r] = kn[r];
         }

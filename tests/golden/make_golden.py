@@ -9,8 +9,8 @@ Each fixture is an .npz (no pickles) of inputs and the oracle's outputs:
   q80_rows.npz   3 rows x K=512 Q8_0, per-block distinct f16 scales; same
   q8k_quant.npz  Q8_K quantisation of x with edge chunks (all zero; +/-max
                  tie, first index wins; half-way codes)
-  gdn_step.npz   one GDN step, HK=2 HV=4 D=64: raw qkv / gates / state in,
-                 output and updated state out
+  gdn_step.npz   one GDN step, HK=2 HV=4 D=64 (16 state columns per item):
+                 raw qkv / gates / state in, output and updated state out
   attn.npz       one attention decode step, NQ=4 NKV=2 HD=256 at pos 37
 The tests recompute every output with the oracle (tests/test_golden.py) and
 run the GPU ops on the same inputs (tests/test_gpu_golden.py).
@@ -138,9 +138,10 @@ def gdn(rng):
     o = np.zeros(HV * D, np.float32)
     st = M.copy()
     v = qkv[2 * HK * D:].copy()
+    cols = 16
     L.or_gdn_step(q.ctypes.data, k.ctypes.data, v.ctypes.data, g.ctypes.data, bt.ctypes.data, st.ctypes.data,
-                  o.ctypes.data, HV, HK, D, scale)
-    return dict(hk=HK, hv=HV, d=D, scale=scale, qkv=qkv, alpha=al, beta_raw=be, dt_bias=dt, ssm_a=A, state_in=M,
+                  o.ctypes.data, HV, HK, D, scale, cols)
+    return dict(hk=HK, hv=HV, d=D, cols=cols, scale=scale, qkv=qkv, alpha=al, beta_raw=be, dt_bias=dt, ssm_a=A, state_in=M,
                 o=o, state_out=st)
 
 

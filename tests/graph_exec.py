@@ -281,7 +281,7 @@ class GraphExec:
             o = np.zeros(HV * D, np.float32)
             scale = np.float32(1.0) / np.sqrt(np.float32(D))
             self.L.or_gdn_step(qf.ctypes.data, kf.ctypes.data, vf.ctypes.data, ge.ctypes.data, bf.ctypes.data,
-                               state.ctypes.data, o.ctypes.data, HV, HK, D, float(scale))
+                               state.ctypes.data, o.ctypes.data, HV, HK, D, float(scale), self.L.or_gdn_cols(D))
             out = np.concatenate([o, state])
             assert out.size == math.prod(ne)
             return T(out, ne)

@@ -94,7 +94,7 @@ def test_gdn_fixture_recomputes(orc):
                    f["ssm_a"].ctypes.data, g.ctypes.data, bt.ctypes.data, HV)
     st, o = f["state_in"].copy(), np.zeros(HV * D, np.float32)
     L.or_gdn_step(q.ctypes.data, k.ctypes.data, v.ctypes.data, g.ctypes.data, bt.ctypes.data, st.ctypes.data,
-                  o.ctypes.data, HV, HK, D, float(f["scale"]))
+                  o.ctypes.data, HV, HK, D, float(f["scale"]), int(f["cols"]))
     assert np.array_equal(st, f["state_out"]) and np.array_equal(o, f["o"])
     # float64 restatement of the delta rule on the same normalised inputs
     o64, M64 = R.gdn_step64(q.reshape(HK, D), k.reshape(HK, D), v.reshape(HV, D), g, bt, f["state_in"], HK)

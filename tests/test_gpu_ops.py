@@ -349,7 +349,7 @@ def test_gdn_step_matches_oracle(sn, orc, torch_gpu, cols, blocks):
     st = M.copy()
     v = qkv[2 * HK * D:].copy()
     L.or_gdn_step(q.ctypes.data, k.ctypes.data, v.ctypes.data, g.ctypes.data, bt.ctypes.data, st.ctypes.data,
-                  o.ctypes.data, HV, HK, D, a.scale)
+                  o.ctypes.data, HV, HK, D, a.scale, cols)
     assert np.array_equal(host(d["M"]), st)
     assert np.array_equal(host(do), o)
 

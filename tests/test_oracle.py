@@ -296,12 +296,12 @@ def _gdn_inputs(seed, HK=2, HV=4, D=128):
     return q, k, v, g, beta, M
 
 
-def _or_gdn(orc, q, k, v, g, beta, M):
+def _or_gdn(orc, q, k, v, g, beta, M, cols=32):
     HV, D, _ = M.shape
     o = np.zeros((HV, D), np.float32)
     st = M.copy()
     orc.lib().or_gdn_step(P(q), P(k), P(v), P(g), P(beta), P(st), P(o), HV, q.shape[0], D,
-                          np.float32(1) / np.sqrt(np.float32(D)))
+                          np.float32(1) / np.sqrt(np.float32(D)), cols)
     return o, st
 
 
@@ -311,6 +311,29 @@ def test_gdn_step_reference(orc):
     o64, M64 = R.gdn_step64(q, k, v, g, beta, M, q.shape[0])
     assert np.allclose(st, M64, rtol=1e-5, atol=1e-6)
     assert np.allclose(o, o64, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("cols", [16, 32])
+def test_gdn_step_exact_dyadic(orc, cols):
+    """Inputs on dyadic grids, so that kv, delta and the updated state are
+    exact in fp32 whatever the fold order: the oracle's S' must equal the
+    exact fp64 delta rule bit for bit -- a dropped or misindexed term, a
+    transposed state or a wrong head map fails it -- and o must be within
+    fp32 rounding of it."""
+    rng = np.random.default_rng(31 + cols)
+    HK, HV, D = 2, 4, 128
+    q = (rng.integers(-8, 9, (HK, D)) / 64).astype(np.float32)
+    k = (rng.integers(-8, 9, (HK, D)) / 64).astype(np.float32)
+    v = (rng.integers(-8, 9, (HV, D)) / 8).astype(np.float32)
+    g = np.array([0.5, 1.0, 0.25, 0.75], np.float32)
+    beta = np.array([0.5, 0.25, 1.0, 0.125], np.float32)
+    M = (rng.integers(-8, 9, (HV, D, D)) / 16).astype(np.float32)
+    o, st = _or_gdn(orc, q, k, v, g, beta, M, cols)
+    o64, M64 = R.gdn_step64(q, k, v, g, beta, M, HK)
+    # kv, delta and S' stay on a 2^-21 grid below 2: exact in fp32
+    assert np.array_equal(st.astype(np.float64), M64)
+    # the o sums need more than 24 bits: within fp32 rounding of the exact value
+    assert np.allclose(o, o64, rtol=2e-6, atol=1e-7)
 
 
 def test_gdn_step_closed_forms(orc):
