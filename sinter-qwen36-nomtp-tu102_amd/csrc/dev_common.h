@@ -167,24 +167,13 @@ __device__ __forceinline__ void block_sum2_f64(double &a, double &b, P red) {
 }
 
 // Sum over aligned groups of n lanes (n a power of two, 1..64), every lane of
-// a group getting the group's sum: the butterfly over lane distances 1, 2,
-// 4, ..., n/2.  Within a 16-lane row the steps at distance 4 and 8 use the
-// half-row and row mirrors (the partner holds the same partial sum as the
+// a group getting the group's sum: the butterfly a[t] += a[t ^ m], m = 1, 2,
+// 4, ..., n/2 (after the step at distance m every lane holds the sum of its
+// aligned group of 2m lanes; the partner order does not matter, an fp32 add
+// commutes exactly).  Within a 16-lane row the steps at distance 4 and 8 use
+// the half-row and row mirrors (the partner holds the same partial sum as the
 // lane at distance 4 / 8 once the smaller steps are done, so the sums are
 // bit-identical); wider steps use cross-lane shuffles.
-__device__ __forceinline__ double lanes_sum_f64(double v, uint32_t n) {
-    if (n >= 2) v += dpp_d<DPP_XOR1>(v);
-    if (n >= 4) v += dpp_d<DPP_XOR2>(v);
-    if (n >= 8) v += dpp_d<DPP_HALF_MIRROR>(v);
-    if (n >= 16) v += dpp_d<DPP_MIRROR>(v);
-    if (n >= 32) v += __shfl_xor(v, 16, 64);
-    if (n >= 64) v += __shfl_xor(v, 32, 64);
-    return v;
-}
-
-// The same butterfly in fp32: after the step at distance m every lane holds
-// the sum of its aligned group of 2m lanes, partner order not mattering (an
-// fp32 add commutes exactly), i.e. the tree a[t] += a[t ^ m], m = 1, 2, 4, ...
 __device__ __forceinline__ float lanes_sum_f32(float v, uint32_t n) {
     if (n >= 2) v += dpp_f<DPP_XOR1>(v);
     if (n >= 4) v += dpp_f<DPP_XOR2>(v);

@@ -207,7 +207,7 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
 // sinter_op_attn_decode_noalloc: the standalone attention op with its split-K
 // partials, per-chunk generation flags and error cell in this file-scope
 // device array instead of caller-allocated workspace.  Layout: error cell
-// [0, 256) | flags [256, 256 + 4 * NOALLOC_FLAG_WORDS) | partials (fp64).
+// [0, 256) | flags [256, 256 + 4 * NOALLOC_FLAG_WORDS) | partials (fp32).
 // Every call on a device shares the array; calls that overlap on one
 // device race.
 constexpr size_t NOALLOC_FLAG_WORDS = 1024;
