@@ -165,3 +165,23 @@ def test_batched_prefill_refuses_other_weight_types(sn, torch_gpu):
         assert L.sinter_model_prefill_batched(m.h, arr, 4, 62, 16, C.byref(nxt)) == sn.ERR_ARG   # past n_ctx
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("d,hk,hv", [(64, 2, 4), (256, 1, 2)])
+def test_batched_prefill_gdn_head_sizes(sn, torch_gpu, d, hk, hv):
+    """The GDN scan's other layouts (head size 64: 16 columns per item, 4 rows
+    per thread; 256: 32 rows per thread) against the decode program."""
+    cfg = small_config(sn, n_layer=4, n_ctx=256)
+    cfg.gdn_d, cfg.gdn_hk, cfg.gdn_hv = d, hk, hv
+    toks = [int(t) for t in np.random.default_rng(d).integers(0, cfg.n_vocab, 70)]
+    a, b = sn.Model(cfg, seed=51), sn.Model(cfg, seed=51)
+    try:
+        print(f"batched prefill gdn_d={d} hk={hk} hv={hv}", flush=True)
+        nxt_a = a.prefill(toks, 0, mode="batched", ubatch=32)
+        nxt_b = b.prefill(toks, 0, mode="tokenwise")
+        assert nxt_a == nxt_b
+        assert np.array_equal(a.logits(), b.logits())
+        same_state(a, b, cfg)
+    finally:
+        a.close()
+        b.close()
