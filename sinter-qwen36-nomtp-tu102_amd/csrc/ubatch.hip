@@ -22,11 +22,13 @@
 // (16 x 32, lane l: token l%16, elements 8(l/16)..+7 of the 32) and the rows'
 // codes as B (32 x 16, lane l: row l%16, the same elements); D (16 x 16
 // int32, lane l: row l%16, tokens 4(l/16)+v) holds one exact 32-element dot
-// per (token, row).  A Q4_K sub-block is 32 elements (one MFMA); a Q6_K
-// sub-block is 16, so a 32-element chunk runs two MFMAs, each with the other
+// per (token, row).  A Q4_K sub-block is 32 elements, and two of them go
+// through one 64-deep v_mfma_i32_16x16x64_i8 (the pair's 8-byte operands side
+// by side: the sums accumulate over all sub-blocks anyway); a Q6_K sub-block
+// is 16, so a 32-element chunk runs two 32-deep MFMAs, each with the other
 // sub-block's half of B zeroed.  Q4_K's min term sum_s m_s * (sum of the
-// sub-block's activation codes) is one more MFMA per sub-block, against B =
-// m_s in every byte, accumulated across the sub-blocks in D.  Each lane then
+// sub-block's activation codes) is one more MFMA per sub-block pair, against
+// B = m_s in every byte, accumulated across the sub-blocks in D.  Each lane then
 // forms the fp64 term of its four (token, row) pairs from its own row's
 // scales and folds it into its accumulators.
 #include "internal.h"
@@ -52,6 +54,12 @@ constexpr uint32_t Q4K_BYTES = 144, Q6K_BYTES = 210;
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
 __device__ __forceinline__ long pack64(uint32_t lo, uint32_t hi) {
     return (long)(((unsigned long)hi << 32) | lo);
+}
+// two 8-byte MFMA operands as one 16-byte operand (x in bytes 0-7)
+__device__ __forceinline__ v4i pack128(long x, long y) {
+    const v4i r = {(int)(uint32_t)x, (int)(uint32_t)((unsigned long)x >> 32), (int)(uint32_t)y,
+                   (int)(uint32_t)((unsigned long)y >> 32)};
+    return r;
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -257,13 +265,18 @@ __global__ __launch_bounds__(UB_THREADS) void ubatch_gemv_kernel(const uint8_t *
                 int isum[4] = {0, 0, 0, 0};
                 if constexpr (WT == SINTER_Q4_K) {
                     // sum_s scale_s dot_s = 8 sum_s hi_s dot_s + sum_s lo_s dot_s, all
-                    // exact in int32 (|each| <= 256 * 105 * 128)
+                    // exact in int32 (|each| <= 256 * 105 * 128).  Sub-blocks s and
+                    // s + 1 go through one 64-deep MFMA: A and B carry sub-block s in
+                    // bytes 0-7 of each lane and s + 1 in bytes 8-15 (the MFMA pairs
+                    // A and B bytes by the same lane-group / byte k index, so any
+                    // common placement gives the same exact sums)
                     v4i cm = z, ch = z, cl = z;
 #pragma unroll
-                    for (uint32_t s = 0; s < 8; s++) {
-                        cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], b[s], cl, 0, 0, 0);
-                        ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], bh[s], ch, 0, 0, 0);
-                        cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[s], bm[s], cm, 0, 0, 0);
+                    for (uint32_t s = 0; s < 8; s += 2) {
+                        const v4i a2 = pack128(a[s], a[s + 1]);
+                        cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, pack128(b[s], b[s + 1]), cl, 0, 0, 0);
+                        ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, pack128(bh[s], bh[s + 1]), ch, 0, 0, 0);
+                        cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, pack128(bm[s], bm[s + 1]), cm, 0, 0, 0);
                     }
 #pragma unroll
                     for (uint32_t v = 0; v < 4; v++) {
