@@ -58,8 +58,11 @@ def test_full_shape_decode_matches_oracle(sn, orc, torch_gpu):
     """The benchmark configuration itself (64 layers, Qwen3.6-27B shapes,
     Q4_K_M mix, 4096-token synthetic context), single-pass path: two greedy
     steps on the GPU and on the CPU oracle from the same weights and state;
-    identical token ids, logits within rel L2 1e-5 (the pass bar is 1e-2)."""
-    cfg = sn.qwen36_27b_config(n_ctx=4096 + 8, quant="q4_k_m")
+    identical token ids, logits within rel L2 1e-5 (the pass bar is 1e-2).
+    Then a 20-token batched prefill (ubatches of 8, 8 and 4 tokens) against
+    the oracle stepping the same tokens: the same next token and logits
+    within rel L2 1e-5."""
+    cfg = sn.qwen36_27b_config(n_ctx=4096 + 32, quant="q4_k_m")
     print("full shape: create", flush=True)
     m = sn.Model(cfg, seed=2026)
     try:
@@ -76,6 +79,15 @@ def test_full_shape_decode_matches_oracle(sn, orc, torch_gpu):
             assert nxt == rtok == int(np.argmax(rlog))
             assert rel < 1e-5, rel
             tok, pos = nxt, pos + 1
+        prompt = [int(t) for t in np.random.default_rng(2028).integers(0, cfg.n_vocab, 20)]
+        print(f"full shape: batched prefill of {len(prompt)} tokens at {pos}", flush=True)
+        nxt = m.prefill(prompt, pos, mode="batched", ubatch=8)
+        for i, t in enumerate(prompt):
+            rtok, rlog = mirror.step(t, pos + i)
+        rel = np.linalg.norm(m.logits() - rlog) / np.linalg.norm(rlog)
+        print(f"full shape prefill: gpu {nxt} oracle {rtok} rel {rel:.2e}", flush=True)
+        assert nxt == rtok
+        assert rel < 1e-5, rel
     finally:
         m.close()
 
