@@ -46,7 +46,12 @@ constexpr uint32_t UB_TOKENS = UB_TOK * UB_TILES;
 constexpr uint32_t UB_THREADS = 256;  // four waves: 64 rows of the workgroup's row tile
 constexpr uint32_t UB_WG_ROWS = UB_ROWS * (UB_THREADS / 64u);
 constexpr uint32_t UB_XSTRIDE = 68;   // LDS dwords per staged token (65 used)
-constexpr uint64_t UB_MIN_WGS = 256;  // one per CU
+// fewest workgroups a launch splits its token groups to reach: two per CU, so
+// each SIMD holds two waves to hide the latency of its MFMA / fp64 chains
+// (4096-token prefill: 1.076 s at one per CU, 1.021 s at 384 or 512, 1.153 s
+// at 768 or 1024, where the 5120-row matrices drop to one token tile per
+// workgroup and read their weights four times)
+constexpr uint64_t UB_MIN_WGS = 512;
 constexpr uint32_t UB_CONV_MAX = 8;    // conv taps
 constexpr uint32_t Q8K_BYTES = 292;  // block_q8_K
 constexpr uint32_t Q4K_BYTES = 144, Q6K_BYTES = 210;
@@ -544,7 +549,7 @@ extern "C" int sinter_op_gemv_ubatch(int type, const void *w, int64_t rows, int6
                          (unsigned)wa);
     const uint64_t n_rt = ((uint64_t)rows + UB_WG_ROWS - 1) / UB_WG_ROWS;
     // token tiles per workgroup: 4 (weights read once per 64 tokens) unless
-    // that leaves fewer workgroups than CUs; then fewer, the row
+    // that leaves fewer than UB_MIN_WGS workgroups; then fewer, the row
     // tile's token groups running side by side so its weights come from the
     // memory-side cache after the first
     uint32_t tpw = UB_TILES;
