@@ -596,16 +596,26 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
         gm[8 * ATT_MAXG + rr * ATT_MAXG + my_s] = lrun;
     }
     __syncthreads();
-    {
-        const uint32_t s = t >> 5, po = t & 31;
+    // each (row group, slot) weight e_g once: lane 8 g + s of wave 0 (in the
+    // merge's weight array, unused until the merge); the slot's M at [64 + s]
+    LDS float *ew = me;
+    if (t < 64) {
+        const uint32_t g2 = t >> 3, s = t & 7u;
         float M = -INFINITY;
 #pragma unroll
-        for (uint32_t g2 = 0; g2 < 8; g2++) M = fmaxf(M, gm[g2 * ATT_MAXG + s]);
+        for (uint32_t k = 0; k < 8; k++) M = fmaxf(M, gm[k * ATT_MAXG + s]);
+        const float mg = gm[g2 * ATT_MAXG + s];
+        ew[g2 * ATT_MAXG + s] = (s < gqa && mg != -INFINITY) ? att_exp(mg - M) : 0.0f;
+        if (g2 == 0) ew[64 + s] = M;
+    }
+    __syncthreads();
+    {
+        const uint32_t s = t >> 5, po = t & 31;
+        const float M = ew[64 + s];
         float Lc = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t g2 = 0; g2 < 8; g2++) {
-            const float mg = gm[g2 * ATT_MAXG + s];
-            const float e = (s < gqa && mg != -INFINITY) ? att_exp(mg - M) : 0.0f;
+            const float e = ew[g2 * ATT_MAXG + s];
             Lc = fmaf(e, gm[8 * ATT_MAXG + g2 * ATT_MAXG + s], Lc);
             const f32x4 c0 = *reinterpret_cast<const LDS f32x4 *>(comb + (g2 * ATT_MAXG + s) * 256 + 8 * po);
             const f32x4 c1 = *reinterpret_cast<const LDS f32x4 *>(comb + (g2 * ATT_MAXG + s) * 256 + 8 * po + 4);
@@ -625,7 +635,7 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     }
 
     // the merge's element mapping: this workgroup finalises elements
-    // [c*ne, ...) of the head group's gqa*HD outputs, one thread each
+    // [e0, e1) of the head group's gqa*HD outputs (slots s_lo .. s_hi)
     const uint32_t E = gqa * HD, NC = geo.n, ne = (E + NC - 1) / NC, e0 = c * ne, e1 = min(e0 + ne, E);
 
     // wait for the kv head's NC chunks: each publishes generation gen + 1 in
@@ -640,58 +650,82 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     }
     __syncthreads();
     if (*flag == 0) return;
+    if (e0 >= e1) { settle_vmem(); return; }
 
     // merge: M = max_c m_c, e_c = exp(m_c - M), L = sum_c e_c l_c and
     // O = sum_c e_c acc_c as fmaf chains over the chunks ascending;
-    // out = O / L * sigmoid(gate).  One load round trip: every value this
-    // thread folds, its gate and its wave's m / l are loaded before any is used.
-    const __amdgpu_buffer_rsrc_t r = coh_rsrc(a.part + (size_t)g * C * gqa * PS, NC * gqa * PS * 4);
-    auto merge = [&](auto nmax) {
-        constexpr uint32_t NM = decltype(nmax)::value;
-        for (uint32_t eb = e0; eb < e1; eb += BLOCK_THREADS) {
-            const uint32_t el = eb + t, elc = min(el, e1 - 1), s = elc / HD, d = elc % HD;
-            // chunk k's value at off + k * stride: the offset advances in a
-            // vector register (no per-chunk scalar), and loads past chunk NC - 1
-            // fall outside the buffer resource, which returns 0
-            float v[NM];
-            const uint32_t stride = gqa * PS * 4;
-            uint32_t off = (s * PS + d) * 4;
+    // out = O / L * sigmoid(gate).  One load round trip: every value of the
+    // workgroup's elements in every chunk (pair q = t, t + 256, .. of the
+    // chunk-major (chunk, element) pairs), the m / l of every chunk for its
+    // slots and the gates are loaded before any is used, then staged in LDS
+    // (the tile region).
+    const uint32_t nel = e1 - e0, s_lo = e0 / HD, nsl = (e1 - 1) / HD - s_lo + 1, npair = NC * nel;
+    LDS float *mv = reinterpret_cast<LDS float *>(L);   // [NC][nel] values
+    LDS float *mm = mv + npair;                         // [nsl][NC] m, then [nsl][NC] l
+    LDS float *mw = mm + 2 * nsl * NC;                  // [nsl][NC] e_c, then [nsl] L
+    const uint32_t pbytes = NC * gqa * PS * 4;   // (an offset of pbytes lies outside: loads 0, no access)
+    const __amdgpu_buffer_rsrc_t r = coh_rsrc(a.part + (size_t)g * C * gqa * PS, pbytes);
+    constexpr uint32_t MAXV = (ATT_MAXG * 256 + 64 + BLOCK_THREADS - 1) / BLOCK_THREADS;   // pairs per thread
+    constexpr uint32_t MAXG = (ATT_MAXG * 256 + BLOCK_THREADS - 1) / BLOCK_THREADS;        // elements per thread
+    float v[MAXV], ml[4], gt[MAXG];
 #pragma unroll
-            for (uint32_t k = 0; k < NM; k++) {
-                v[k] = ld_coh4b(r, off);
-                off += stride;
-            }
-            const uint32_t h = g * gqa + s;
-            const float gate = ld_coh(a.qg + (size_t)h * 2 * HD + HD + d);
-            if (eb == e0) {
-                // slot sl on wave sl % 4, chunk i on lane i
-                for (uint32_t sl = w; sl < gqa; sl += WAVES) {
-                    const uint32_t ci = min(lane, NC - 1);
-                    const float m = ld_coh4b(r, ((ci * gqa + sl) * PS + HD) * 4);
-                    const float l = ld_coh4b(r, ((ci * gqa + sl) * PS + HD + 1) * 4);
-                    float M = lane < NC ? m : -INFINITY;
+    for (uint32_t k = 0; k < MAXV; k++) {
+        const uint32_t q = t + k * BLOCK_THREADS, cq = q / nel, el = e0 + q % nel;
+        const uint32_t off = q < npair ? ((cq * gqa + el / HD) * PS + el % HD) * 4 : pbytes;
+        v[k] = ld_coh4b(r, off);
+    }
 #pragma unroll
-                    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-                    const float e = lane < NC ? att_exp(m - M) : 0.0f;
-                    float Ls = 0.0f;
-                    for (uint32_t k = 0; k < NC; k++) {
-                        const float ek = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), (int)k));
-                        const float lk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), (int)k));
-                        Ls = fmaf(ek, lk, Ls);
-                    }
-                    if (lane < NC) me[lane * ATT_MAXG + sl] = e;
-                    if (lane == 0) mL[sl] = Ls;
-                }
-                __syncthreads();
-            }
-            float O = 0.0f;
+    for (uint32_t k = 0; k < 2; k++) {
+        const uint32_t q = t + k * BLOCK_THREADS, sl = q / NC, cq = q % NC;
+        const uint32_t off = sl < nsl ? ((cq * gqa + s_lo + sl) * PS + HD) * 4 : pbytes;
+        ml[2 * k] = ld_coh4b(r, off);
+        ml[2 * k + 1] = ld_coh4b(r, off + 4);
+    }
 #pragma unroll
-            for (uint32_t k = 0; k < NM; k++)
-                if (k < NC) O = fmaf(me[k * ATT_MAXG + s], v[k], O);
-            if (el < e1) st_coh(a.out + (size_t)h * HD + d, (O / mL[s]) * dev_sigmoid(gate));
+    for (uint32_t k = 0; k < MAXG; k++) {
+        const uint32_t j = t + k * BLOCK_THREADS, el = e0 + min(j, nel - 1), h = g * gqa + el / HD;
+        gt[k] = j < nel ? ld_coh(a.qg + (size_t)h * 2 * HD + HD + el % HD) : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < MAXV; k++) {
+        const uint32_t q = t + k * BLOCK_THREADS;
+        if (q < npair) mv[q] = v[k];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < 2; k++) {
+        const uint32_t q = t + k * BLOCK_THREADS;
+        if (q < nsl * NC) { mm[q] = ml[2 * k]; mm[nsl * NC + q] = ml[2 * k + 1]; }
+    }
+    __syncthreads();
+    // per slot (wave sl % 4), lane k = chunk k: M, e_k, then the L chain
+    for (uint32_t sl = w; sl < nsl; sl += WAVES) {
+        const float m = lane < NC ? mm[sl * NC + lane] : -INFINITY;
+        const float l = lane < NC ? mm[nsl * NC + sl * NC + lane] : 0.0f;
+        float M = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float e = lane < NC ? att_exp(m - M) : 0.0f;
+        float Ls = 0.0f;
+        for (uint32_t k = 0; k < NC; k++) {
+            const float ek = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), (int)k));
+            const float lk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), (int)k));
+            Ls = fmaf(ek, lk, Ls);
         }
-    };
-    merge(std::integral_constant<uint32_t, 64>{});   // (loads past NC re-read chunk NC - 1: cache hits)
+        if (lane < NC) mw[sl * NC + lane] = e;
+        if (lane == 0) mw[nsl * NC + sl] = Ls;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < MAXG; k++) {
+        const uint32_t j = t + k * BLOCK_THREADS;
+        if (j < nel) {
+            const uint32_t el = e0 + j, sl = el / HD - s_lo, h = g * gqa + el / HD;
+            const LDS float *ec = mw + sl * NC;
+            float O = 0.0f;
+            for (uint32_t cq = 0; cq < NC; cq++) O = fmaf(ec[cq], mv[cq * nel + j], O);
+            st_coh(a.out + (size_t)h * HD + el % HD, (O / mw[nsl * NC + sl]) * dev_sigmoid(gt[k]));
+        }
+    }
     settle_vmem();
 }
 
