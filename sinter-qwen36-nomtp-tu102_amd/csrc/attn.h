@@ -272,7 +272,8 @@ __device__ __forceinline__ void op_attn_decode_t(const sinter_instr &ins, unsign
     // and the partials, which the compiler cannot tell apart from the payload
     // (every field would be reloaded from memory after each such store)
     const sinter_attn_args a = *reinterpret_cast<const sinter_attn_args *>(ins.payload);
-    const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
+    const uint64_t hdr = ins_hdr(ins);
+    const uint32_t rel = blockIdx.x - hdr_lo(hdr), nblk = hdr_hi(hdr) - hdr_lo(hdr);
     const uint32_t NQ = a.nq, NKV = a.nkv, HD = a.hd, C = a.n_chunks;
     const uint32_t pc_lo = (uint32_t)(uintptr_t)a.pass_cell, pc_hi = (uint32_t)((uintptr_t)a.pass_cell >> 32);
     const bool cached = pass_id != ATT_NO_CACHE && g_att_key[0] == pass_id && g_att_key[4] == pc_lo &&

@@ -129,8 +129,10 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// Block-wide fp64 sum (blockDim.x a multiple of 64, <= 1024, every thread
-// active); every thread gets the same total.  `red` is LDS scratch of >= 16
+// Block-wide fp64 sum over a 256-thread workgroup (every thread active;
+// the wave count is the constant WAVES, not blockDim.x, whose read is a
+// vector load from the dispatch's implicit arguments); every thread gets the
+// same total.  `red` is LDS scratch of >= 16
 // doubles.  Rows are reduced with DPP, the four row sums of a wave and then
 // the wave sums are added in a fixed order; the result is order-dependent
 // only at fp64 rounding level (callers round to fp32).
@@ -138,7 +140,7 @@ template <class P>
 __device__ __forceinline__ double block_sum_f64(double v, P red) {
     v = row16_sum_f64(v);
     const double w = ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
-    const int nw = blockDim.x >> 6;
+    constexpr int nw = (int)WAVES;
     __syncthreads();
     if (lane_id() == 0) red[wave_id()] = w;
     __syncthreads();
@@ -155,7 +157,7 @@ __device__ __forceinline__ void block_sum2_f64(double &a, double &b, P red) {
     b = row16_sum_f64(b);
     const double wa = ((readlane_f64(a, 0) + readlane_f64(a, 16)) + readlane_f64(a, 32)) + readlane_f64(a, 48);
     const double wb = ((readlane_f64(b, 0) + readlane_f64(b, 16)) + readlane_f64(b, 32)) + readlane_f64(b, 48);
-    const int nw = blockDim.x >> 6;
+    constexpr int nw = (int)WAVES;
     __syncthreads();
     if (lane_id() == 0) { red[2 * wave_id()] = wa; red[2 * wave_id() + 1] = wb; }
     __syncthreads();
@@ -422,6 +424,22 @@ __device__ __forceinline__ bool cross_barrier(GridCross &gx, Pre &&pre) {
     }
     return true;
 }
+
+// ---------------------------------------------------------------- instruction header
+
+// An instruction's header {kind, block_lo, block_hi, flags} as one 64-bit
+// scalar load (constant address space: a program does not change while a
+// launch runs).  Its 16-bit fields read one by one from global memory are
+// vector loads, each waited for with a vmcnt(0) that also waits for every
+// vector load and store of the wave still in flight.
+typedef const __attribute__((address_space(4))) uint64_t chdr_t;
+__device__ __forceinline__ uint64_t ins_hdr(const sinter_instr &ins) { return *(chdr_t *)&ins; }
+__device__ __forceinline__ uint32_t hdr_kind(uint64_t h) { return (uint32_t)h & 0xffffu; }
+__device__ __forceinline__ uint32_t hdr_lo(uint64_t h) { return (uint32_t)(h >> 16) & 0xffffu; }
+__device__ __forceinline__ uint32_t hdr_hi(uint64_t h) { return (uint32_t)(h >> 32) & 0xffffu; }
+static_assert(offsetof(sinter_instr, kind) == 0 && offsetof(sinter_instr, block_lo) == 2 &&
+                  offsetof(sinter_instr, block_hi) == 4,
+              "instruction header layout");
 
 // ---------------------------------------------------------------- block formats
 

@@ -35,7 +35,8 @@ namespace sinter {
 __device__ __forceinline__ bool op_gdn_step(const sinter_instr &ins, unsigned *err, uint64_t *ts, GridCross *gx) {
     lds_char *lds = (lds_char *)g_big;
     const sinter_gdn_args &a = *reinterpret_cast<const sinter_gdn_args *>(ins.payload);
-    const uint32_t rel = blockIdx.x - ins.block_lo, nblk = ins.block_hi - ins.block_lo;
+    const uint64_t hdr = ins_hdr(ins);
+    const uint32_t rel = blockIdx.x - hdr_lo(hdr), nblk = hdr_hi(hdr) - hdr_lo(hdr);
     const uint32_t D = a.d, HK = a.hk, HV = a.hv, cols = a.cols;
     // supported envelope: D in {64,128,256}, cols divides D, 256 threads
     // split evenly over cols columns with >= 4 rows per thread

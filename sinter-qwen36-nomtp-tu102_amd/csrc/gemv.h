@@ -1285,7 +1285,8 @@ __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan 
         reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
     cplan_t *pl = (cplan_t *)plan;
     cu32_t *cu = (cu32_t *)cuts;
-    const uint32_t rel = uni(blockIdx.x - ins.block_lo), nblk = uni(ins.block_hi - ins.block_lo);
+    const uint64_t hdr = ins_hdr(ins);
+    const uint32_t rel = uni(blockIdx.x - hdr_lo(hdr)), nblk = uni(hdr_hi(hdr) - hdr_lo(hdr));
     // (a plan outside this interpreter's feature set raises UNWIRED_KIND)
     const bool planned = pl->ok != 0, ok = planned && plan_in_set<F>(pl);
     const uint32_t wv = rel * WAVES + uni(wave_id());

@@ -67,14 +67,16 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
         if (traced && pass == 0 && threadIdx.x == 0) ctl.trace[((size_t)ii * gridDim.x + blockIdx.x) * 4 + k] = v;
     };
     while (pass < ctl.n_passes) {
-        const unsigned kind = i < n ? prog[i].kind : (unsigned)SINTER_OP_BOUNDARY;
+        const uint64_t hdr = i < n ? ins_hdr(prog[i]) : 0u;
+        const unsigned kind = i < n ? hdr_kind(hdr) : (unsigned)SINTER_OP_BOUNDARY;
         if (kind == SINTER_OP_BOUNDARY) {
             const bool pass_end = i == n;
             const uint32_t nx = pass_end ? 0u : i + 1;
             const bool more = nx < n && (pass + (pass_end ? 1u : 0u)) < ctl.n_passes;
-            const bool in_nx = more && blockIdx.x >= prog[nx].block_lo && blockIdx.x < prog[nx].block_hi;
-            const bool fused = in_nx && prog[nx].kind == SINTER_OP_GEMV;
-            const bool fused_gdn = in_nx && prog[nx].kind == SINTER_OP_GDN_STEP;
+            const uint64_t hnx = more ? ins_hdr(prog[nx]) : 0u;
+            const bool in_nx = more && blockIdx.x >= hdr_lo(hnx) && blockIdx.x < hdr_hi(hnx);
+            const bool fused = in_nx && hdr_kind(hnx) == SINTER_OP_GEMV;
+            const bool fused_gdn = in_nx && hdr_kind(hnx) == SINTER_OP_GDN_STEP;
             const uint64_t s = timed ? wall_clock64() : 0;
             GridCross gx;
             gx.flags = ctl.flags; gx.err = ctl.err; gx.epoch = &epoch;
@@ -137,7 +139,7 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
             settle_vmem();
             return;
         }
-        if (blockIdx.x >= ins.block_lo && blockIdx.x < ins.block_hi) {
+        if (blockIdx.x >= hdr_lo(hdr) && blockIdx.x < hdr_hi(hdr)) {
             const uint64_t s = timed ? wall_clock64() : 0;
             stamp(i, 0, wall_clock64());
             if (kind == SINTER_OP_GEMV) {
