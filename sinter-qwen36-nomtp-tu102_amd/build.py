@@ -51,12 +51,12 @@ LDS_LIMIT = 160 * 1024
 # every kernel's SGPR spills down (K-quant 475 -> 335) and gave the
 # standalone op kernel one VGPR kept in an AGPR; reading instruction headers
 # with one scalar load brought them to 278 and moved 2 VGPRs of the Q8_0-cache
-# kernel into AGPRs.
+# kernel into AGPRs; the header table in LDS moved them by a few either way.
 SPILL_BUDGET = {
-    "sinter_interp": (20, 324),
-    "sinter_interp_kquant": (22, 278),
-    "sinter_interp_kquant_q8kv": (24, 305),
-    "sinter_interp_bf16": (12, 279),
+    "sinter_interp": (20, 337),
+    "sinter_interp_kquant": (22, 274),
+    "sinter_interp_kquant_q8kv": (22, 307),
+    "sinter_interp_bf16": (12, 286),
     "sinter_op_kernel": (1, 18),
     "sinter_op_noalloc_kernel": (0, 0),
 }

@@ -934,7 +934,7 @@ int sinter_host_grid(sinter_host *h, uint32_t *blocks, uint32_t *threads, uint32
     if (!h) return set_error(SINTER_ERR_ARG, "null host");
     if (blocks) *blocks = h->blocks;
     if (threads) *threads = BLOCK_THREADS;
-    if (lds_bytes) *lds_bytes = BIG_BYTES + QBUF_BYTES + 512;
+    if (lds_bytes) *lds_bytes = BIG_BYTES + QBUF_BYTES + HDR_CAP * 8 + 512;
     return SINTER_OK;
 }
 

@@ -37,6 +37,13 @@ __device__ __forceinline__ bool kind_wired(unsigned k) {
 
 using namespace sinter;
 
+// The program's instruction headers, copied into LDS at launch (the first
+// HDR_CAP; a longer program reads the rest with scalar loads): the program
+// (256 B per instruction) is far larger than the scalar cache, so a header
+// read from memory is an L2 round trip on the way to every op and barrier.
+// (HDR_CAP is in isa.h)
+__shared__ uint64_t g_hdr[HDR_CAP];
+
 // The interpreter over feature set F (the GEMV weight / activation types and
 // KV cache types its ops handle; isa.h): one kernel per set below.
 template <uint32_t F>
@@ -51,6 +58,9 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
     // next pass's first instruction.  One copy of each op's code.
     uint32_t pass = 0, i = 0;
     uint64_t t0 = wall_clock64();
+    for (uint32_t k = threadIdx.x; k < min(n, HDR_CAP); k += BLOCK_THREADS)
+        g_hdr[k] = *(const GLB uint64_t *)&prog[k];
+    auto hdr_at = [&](uint32_t k) -> uint64_t { return k < HDR_CAP ? g_hdr[k] : ins_hdr(prog[k]); };
     if (threadIdx.x == 0) {
         g_att_key[0] = ATT_NO_CACHE;   // no attention cache from an earlier launch
         // the launch's inputs into the pass cell: every workgroup stores the
@@ -67,13 +77,13 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
         if (traced && pass == 0 && threadIdx.x == 0) ctl.trace[((size_t)ii * gridDim.x + blockIdx.x) * 4 + k] = v;
     };
     while (pass < ctl.n_passes) {
-        const uint64_t hdr = i < n ? ins_hdr(prog[i]) : 0u;
+        const uint64_t hdr = i < n ? hdr_at(i) : 0u;
         const unsigned kind = i < n ? hdr_kind(hdr) : (unsigned)SINTER_OP_BOUNDARY;
         if (kind == SINTER_OP_BOUNDARY) {
             const bool pass_end = i == n;
             const uint32_t nx = pass_end ? 0u : i + 1;
             const bool more = nx < n && (pass + (pass_end ? 1u : 0u)) < ctl.n_passes;
-            const uint64_t hnx = more ? ins_hdr(prog[nx]) : 0u;
+            const uint64_t hnx = more ? hdr_at(nx) : 0u;
             const bool in_nx = more && blockIdx.x >= hdr_lo(hnx) && blockIdx.x < hdr_hi(hnx);
             const bool fused = in_nx && hdr_kind(hnx) == SINTER_OP_GEMV;
             const bool fused_gdn = in_nx && hdr_kind(hnx) == SINTER_OP_GDN_STEP;

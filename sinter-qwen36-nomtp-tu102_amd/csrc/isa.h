@@ -52,6 +52,9 @@ __host__ __device__ constexpr uint32_t feat_x(uint32_t vt) {
 // (kv_type 0 is the f16 cache, as SINTER_F16)
 __host__ __device__ constexpr uint32_t feat_kv(uint32_t t) { return t == SINTER_Q8_0 ? FEAT_KV_Q80 : FEAT_KV_F16; }
 
+// The interpreter's LDS table of instruction headers (interp.hip): entries.
+constexpr uint32_t HDR_CAP = 1024;
+
 // LDS: the quantised GEMV activation, and one 96 KiB scratch region shared by
 // the ops: the GEMV's activation staging (prologue) and then its per-wave
 // item-term rings; attention's tiles; the GDN step's vectors.
