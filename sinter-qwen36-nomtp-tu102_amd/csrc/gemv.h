@@ -1277,28 +1277,42 @@ __device__ __forceinline__ bool plan_in_set(cplan_t *pl) {
 // Returns false when the kernel must stop (barrier timeout, or an error seen
 // at a pass end).
 // ts (thread 0, or null): wall clock stamps [1] after the barrier wait,
-// [2] after the prologue.
+// [2] after the prologue.  hdr: the instruction's header (ins_hdr).
 template <uint32_t F>
 __device__ __forceinline__ bool gemv_op(const sinter_instr &ins, const GemvPlan *plan, const uint32_t *cuts,
-                                       unsigned *err, GridCross *gx, uint64_t *ts) {
-    if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
-        reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] = reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
+                                       unsigned *err, GridCross *gx, uint64_t *ts, uint64_t hdr) {
     cplan_t *pl = (cplan_t *)plan;
     cu32_t *cu = (cu32_t *)cuts;
-    const uint64_t hdr = ins_hdr(ins);
     const uint32_t rel = uni(blockIdx.x - hdr_lo(hdr)), nblk = uni(hdr_hi(hdr) - hdr_lo(hdr));
-    // (a plan outside this interpreter's feature set raises UNWIRED_KIND)
-    const bool planned = pl->ok != 0, ok = planned && plan_in_set<F>(pl);
-    const uint32_t wv = rel * WAVES + uni(wave_id());
-    const uint32_t row_lo = ok ? cu[wv] : 0u, row_hi = ok ? cu[wv + 1] : 0u;
-    Run run = make_run(pl, 0, row_lo, row_hi);
+    bool planned = false, ok = false;
+    uint32_t row_hi = 0;
+    Run run;
     u32x4 pf[PF_MAX];
     uint32_t sh[4] = {0, 0, 0, 0};
-    if (gx) {
-        // (the arrival publishes g_args too)
-        if (!cross_barrier(*gx, [&] { issue_pre<F>(pf, sh, run, (uint64_t)plan); })) return false;
-    } else {
+    // The op's reads of its payload and plan are memory round trips (the
+    // program and the plans are far larger than the scalar cache): they run
+    // between the barrier's arrival and its wait, so the last workgroup to
+    // arrive does not wait for them before it arrives.  The payload goes to
+    // LDS first (its wait then covers no weight load); then the plan, this
+    // wave's run and the first weight slots.
+    auto setup = [&] {
+        if (threadIdx.x < sizeof(sinter_gemv_args) / 4)
+            reinterpret_cast<uint32_t *>(g_args)[threadIdx.x] =
+                reinterpret_cast<const uint32_t *>(ins.payload)[threadIdx.x];
+        // (a plan outside this interpreter's feature set raises UNWIRED_KIND)
+        planned = pl->ok != 0;
+        ok = planned && plan_in_set<F>(pl);
+        const uint32_t wv = rel * WAVES + uni(wave_id());
+        const uint32_t row_lo = ok ? cu[wv] : 0u;
+        row_hi = ok ? cu[wv + 1] : 0u;
+        run = make_run(pl, 0, row_lo, row_hi);
         issue_pre<F>(pf, sh, run, (uint64_t)plan);
+    };
+    if (gx) {
+        // (the wait's workgroup barrier publishes g_args)
+        if (!cross_barrier(*gx, setup)) return false;
+    } else {
+        setup();
         __syncthreads();
     }
     if (ts) ts[1] = wall_clock64();

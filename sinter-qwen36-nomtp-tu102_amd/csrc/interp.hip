@@ -98,7 +98,8 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
                 uint64_t *ts = (traced && pass + (pass_end ? 1u : 0u) == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)nx * gridDim.x + blockIdx.x) * 4 : nullptr;
                 if (ts) ts[0] = s ? s : wall_clock64();
-                if (!gemv_op<F>(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts)) return;
+                if (!gemv_op<F>(prog[nx], ctl.plans + nx, ctl.cuts + (size_t)nx * PLAN_CUTS, ctl.err, &gx, ts, hnx))
+                    return;
                 if (ts) ts[3] = wall_clock64();
             } else if (fused_gdn) {
                 // the GDN step loads its state slice across the barrier; the
@@ -155,7 +156,7 @@ __device__ __forceinline__ void interp_main(const sinter_instr *__restrict__ pro
             if (kind == SINTER_OP_GEMV) {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
-                (void)gemv_op<F>(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts);
+                (void)gemv_op<F>(ins, ctl.plans + i, ctl.cuts + (size_t)i * PLAN_CUTS, ctl.err, nullptr, ts, hdr);
             } else {
                 uint64_t *ts = (traced && pass == 0 && threadIdx.x == 0)
                                    ? (uint64_t *)ctl.trace + ((size_t)i * gridDim.x + blockIdx.x) * 4 : nullptr;
@@ -206,7 +207,7 @@ sinter_op_kernel(const sinter_instr *__restrict__ ins, const GemvPlan *__restric
                  const uint32_t *__restrict__ cuts, unsigned *err) {
     // the host sets block_lo = 0, block_hi = gridDim.x
     switch (ins->kind) {
-    case SINTER_OP_GEMV: (void)gemv_op<FEAT_ALL>(*ins, plan, cuts, err, nullptr, nullptr); break;
+    case SINTER_OP_GEMV: (void)gemv_op<FEAT_ALL>(*ins, plan, cuts, err, nullptr, nullptr, ins_hdr(*ins)); break;
     case SINTER_OP_GDN_STEP: (void)op_gdn_step(*ins, err, nullptr, nullptr); break;
     // (attention launches cooperatively: its chunks of one kv head wait for
     // each other, bounded by a 2 s spin limit at 100 MHz)
