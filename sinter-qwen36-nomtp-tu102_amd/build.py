@@ -57,7 +57,7 @@ SPILL_BUDGET = {
     "sinter_interp": (20, 337),
     "sinter_interp_kquant": (22, 288),
     "sinter_interp_kquant_q8kv": (22, 307),
-    "sinter_interp_bf16": (12, 286),
+    "sinter_interp_bf16": (12, 289),
     "sinter_op_kernel": (1, 18),
     "sinter_op_noalloc_kernel": (0, 0),
 }
