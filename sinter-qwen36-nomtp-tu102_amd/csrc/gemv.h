@@ -926,17 +926,21 @@ __device__ __forceinline__ Run make_run(cplan_t *pl, uint32_t s, uint32_t lo, ui
 // lane.  The first DPRE slots are loaded across the grid barrier, slots up
 // to DPRO during the prologue (issued behind its activation DMAs), the rest
 // when the body starts -- at most PF_PRE registers of 16 B stay live through
-// the prologue.  Measured on the 27B decode: one more Q4_K slot in the body
-// (D = 4) is 1 % faster, a third Q6_K slot 0.4 %; a fourth Q4_K slot across
-// the barrier (DPRE = 4) is 0.6 % slower; moving a slot from across the barrier to the
-// prologue (DPRE < DPRO), or more slots live through the prologue (which
-// then spill), is slower -- loads issued behind the activation DMAs delay
-// the activation reads of the workgroups released later.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
+// the prologue.  Measured on the 27B decode: Q4_K with D = 3 is 0.4 % faster
+// than with a fourth slot in the body and 0.6 % faster than D = 2 (a lane's
+// item is nine 16-byte loads 144 B apart, so each load instruction of a wave
+// touches ~64 cache lines: a stream probe of that pattern reads 5.4 TB/s with
+// two items in flight per lane and 4.5 with four); a third Q6_K slot is 1 %
+// faster than two, a fourth 3.8 % slower; a fourth Q4_K slot across the
+// barrier (DPRE = 4) was 0.6 % slower; moving a slot from across the barrier
+// to the prologue (DPRE < DPRO), or more slots live through the prologue
+// (which then spill), is slower -- loads issued behind the activation DMAs
+// delay the activation reads of the workgroups released later.  A Q6_K block (210 B, 2-aligned) is read as 13 x 16 B + 4 B from the
 // 4-aligned address at or below it: every byte read lies in
 // [block - 2, block + 210), never past the end of the weights.
 constexpr int PF_MAX = 42, PF_PRE = 28;
 template <int T> struct TypeCfg;
-template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 4, DPRE = 3, DPRO = 3; };
+template <> struct TypeCfg<SINTER_Q4_K> { static constexpr int NI = 9, IB = 144, D = 3, DPRE = 3, DPRO = 3; };
 template <> struct TypeCfg<SINTER_Q6_K> { static constexpr int NI = 14, IB = 210, D = 3, DPRE = 2, DPRO = 2; };
 template <> struct TypeCfg<SINTER_Q8_0> { static constexpr int NI = 17, IB = 272, D = 2, DPRE = 1, DPRO = 1; };
 template <> struct TypeCfg<SINTER_BF16> { static constexpr int NI = 8, IB = 128, D = 4, DPRE = 3, DPRO = 3; };
