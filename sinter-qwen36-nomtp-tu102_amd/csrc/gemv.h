@@ -1267,14 +1267,15 @@ __device__ __forceinline__ uint32_t run_body(u32x4 (&pf)[PF_MAX], uint32_t (&sh)
     return folded;
 }
 
-// (measured: the shared final fold is 1 % faster in the K-quant decode and
-// 1.4 % slower in the bf16 one, whose interpreter has one weight type)
+// (measured: the shared final fold is 1 % faster in the K-quant decode, and
+// 4.5 % slower for the general interpreter's Q8_0 GEMV -- that interpreter
+// and the bf16 one keep the fold in each type's body)
 template <uint32_t F>
 __device__ __forceinline__ void run_dispatch(u32x4 (&pf)[PF_MAX], uint32_t (&sh)[4], const GemvCtx &c, cplan_t *pl,
                                              const Run &r, const ActView &x, float &bv, int32_t &bi,
                                              const EpiPre &ev) {
     constexpr uint32_t FW = F & (FEAT_W_Q4K | FEAT_W_Q6K | FEAT_W_Q80 | FEAT_W_BF16 | FEAT_W_F32);
-    constexpr bool shared = (FW & (FW - 1)) != 0;   // more than one weight type
+    constexpr bool shared = FW == (FEAT_W_Q4K | FEAT_W_Q6K);   // the K-quant interpreters
     if constexpr (shared) {
         uint32_t folded = 0;
         with_wtype<F>(r.type, [&](auto Tc) {
